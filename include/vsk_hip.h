@@ -1,0 +1,228 @@
+/*
+ * vsk_hip.h -- C ABI of the MI355X (gfx950) search hot path of
+ * VectorStoreKit: flat k-NN (L2, L2^2, cosine, dot, Manhattan) with fused
+ * top-k, IVF-Flat (coarse probe + inverted-list scan), int8 scalar-quantized
+ * scan and product-quantized ADC scan with exact re-rank.
+ *
+ * Reference paths are relative to Sources/VectorStoreKit/ of
+ * gifton/VectorStoreKit.  Each entry point names the reference interface it
+ * replaces.
+ *
+ * Conventions
+ *  - Every function returns vsk_status (0 = OK, negative = error);
+ *    vsk_last_error(ctx) returns the message of the last failure on ctx.
+ *  - Pointer arguments may point to host memory or to device memory of the
+ *    context's GPU (hipMalloc / torch tensors); the library inspects each
+ *    pointer and stages host buffers through device memory itself.
+ *  - One context owns one HIP stream.  Calls on one context are serialised
+ *    by the caller (the reference makes every engine/index an actor); calls
+ *    on distinct contexts may run concurrently.  Every call returns after
+ *    its results are in the caller's buffers.
+ *  - Results are ordered ascending by (distance, tie key); the tie key is
+ *    the row id (flat, SQ, PQ), the centroid index (IVF probe) or the
+ *    position of the row in the probe-ordered candidate list (IVF search),
+ *    which is the order the reference's stable sort + prefix(k) produces
+ *    (Indexes/IVFIndex.swift:175-176).  Missing results (k larger than the
+ *    number of candidates) are reported as distance +inf and id -1.
+ *  - Row ids are int64 in the outputs; a database handle holds at most
+ *    2^31 - 1 rows.
+ */
+#ifndef VSK_HIP_H
+#define VSK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t vsk_status;
+
+/* Status codes.  They map 1:1 onto the reference's Swift errors:
+ * MetalComputeError (Acceleration/Metal/MetalErrors.swift:10-39),
+ * AcceleratorError (API/Strategies/AcceleratorStrategies.swift:504-510),
+ * IVFError (Indexes/IVFIndex.swift:619-623) and QuantizationError
+ * (Quantization/ProductQuantizerTypes.swift:33-39). */
+#define VSK_OK 0
+#define VSK_ERR_DEVICE_NOT_AVAILABLE (-1) /* .deviceNotAvailable / .noDevice  */
+#define VSK_ERR_INVALID_ARGUMENT (-2)     /* .invalidInputData / .invalidParameter */
+#define VSK_ERR_EMPTY_INPUT (-3)          /* .emptyInput                      */
+#define VSK_ERR_DIMENSION_MISMATCH (-4)   /* .dimensionMismatch               */
+#define VSK_ERR_OUT_OF_MEMORY (-5)        /* .bufferAllocationFailed / .deviceOutOfMemory */
+#define VSK_ERR_EXECUTION_FAILED (-6)     /* .commandBufferExecutionFailed    */
+#define VSK_ERR_NOT_TRAINED (-7)          /* IVFError/QuantizationError.notTrained */
+#define VSK_ERR_UNSUPPORTED (-8)          /* .unsupportedOperation            */
+#define VSK_ERR_INVALID_BUFFER_SIZE (-9)  /* .invalidBufferSize (k or size over a limit) */
+
+/* Distance metrics: DistanceMetric raw values "euclidean", "cosine",
+ * "dotProduct", "manhattan" (Core/SearchTypes.swift:105-110) plus the
+ * squared-L2 and pre-normalised cosine forms the reference's kernels use
+ * (Acceleration/Metal/Shaders/DistanceShaders.metal:620-654, 815-845). */
+#define VSK_METRIC_L2SQ 0              /* sum (q-x)^2                        */
+#define VSK_METRIC_L2 1                /* sqrt(sum (q-x)^2)     "euclidean"  */
+#define VSK_METRIC_COSINE 2            /* 1 - q.x/(|q||x|+1e-8) "cosine"     */
+#define VSK_METRIC_COSINE_NORMALIZED 3 /* 1 - q.x (unit-norm rows/queries)  */
+#define VSK_METRIC_DOT 4               /* -q.x                  "dotProduct" */
+#define VSK_METRIC_L1 5                /* sum |q-x|             "manhattan"  */
+
+#define VSK_MAX_K 1024 /* largest k of any top-k call */
+
+/* vsk_db_upload_f32 flags */
+#define VSK_DB_NORMALIZE 1 /* L2-normalise each row on the device, x/(|x|+1e-8)
+                              (normalizeVectors, DistanceShaders.metal:403-429) */
+
+typedef struct vsk_ctx vsk_ctx;
+typedef struct vsk_db vsk_db;
+typedef struct vsk_ivf vsk_ivf;
+typedef struct vsk_sq8 vsk_sq8;
+typedef struct vsk_pq vsk_pq;
+
+/* Device description; backs ComputeAccelerator.capabilities()
+ * (Core/Protocols.swift:11-20). */
+typedef struct {
+  char name[96];
+  char arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t device;
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int32_t lds_bytes_per_block;
+  int64_t global_mem_bytes;
+  int32_t clock_khz;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width_bits;
+} vsk_caps;
+
+/* Per-kernel timing collected with HIP events on the context's stream. */
+typedef struct {
+  char name[64];
+  int64_t launches;
+  double total_ms;
+} vsk_kernel_stat;
+
+/* ---- context --------------------------------------------------------------
+ * Replaces ComputeAccelerator.initialize() -> DeviceType
+ * (Core/Protocols.swift:18; Metal: API/Strategies/AcceleratorStrategies.swift:
+ * 20-214) and the MetalAccelerationEngine initialiser
+ * (Acceleration/MetalAccelerationEngine.swift:40-70). */
+vsk_status vsk_create(int32_t device, vsk_ctx **out);
+vsk_status vsk_destroy(vsk_ctx *ctx);
+/* ComputeAccelerator.capabilities() (Core/Protocols.swift:19) */
+vsk_status vsk_device_info(vsk_ctx *ctx, vsk_caps *caps);
+const char *vsk_last_error(const vsk_ctx *ctx);
+/* HIP stream the context launches on (a hipStream_t), for interop. */
+void *vsk_stream(vsk_ctx *ctx);
+/* Wall time of the last API call's device work, from HIP events; replaces
+ * MetalProfiler.recordOperation (Acceleration/Metal/MetalProfiler.swift:
+ * 74-110). */
+float vsk_last_kernel_ms(const vsk_ctx *ctx);
+/* Per-kernel event timing (off by default). */
+vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on);
+vsk_status vsk_profile_reset(vsk_ctx *ctx);
+int32_t vsk_profile_count(const vsk_ctx *ctx);
+vsk_status vsk_profile_get(const vsk_ctx *ctx, int32_t i, vsk_kernel_stat *out);
+
+/* ---- flat database -------------------------------------------------------
+ * Replaces the per-call candidate upload of
+ * MetalAccelerationEngine.batchComputeDistancesGPU
+ * (Acceleration/MetalAccelerationEngine.swift:393-405): rows are uploaded
+ * once and stay resident in HBM.  x: n x d fp32 row-major. */
+vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                             int32_t flags, vsk_db **out);
+vsk_status vsk_db_free(vsk_ctx *ctx, vsk_db *db);
+vsk_status vsk_db_info(const vsk_db *db, int64_t *n, int32_t *d);
+/* Copy rows [row0, row0+count) back (after VSK_DB_NORMALIZE: normalised). */
+vsk_status vsk_db_read_f32(vsk_ctx *ctx, const vsk_db *db, int64_t row0,
+                           int64_t count, float *out);
+
+/* ---- flat search ---------------------------------------------------------
+ * MetalAccelerationEngine.batchComputeDistances(queries:candidates:metric:
+ * topK:) (Acceleration/MetalAccelerationEngine.swift:139-204) with the top-k
+ * fused on the device and ids returned (the reference returns distances
+ * only, after a CPU sort of the full matrix, :457-477).  Also the exact
+ * path of VectorIndex.search (Core/Protocols.swift:116-121).
+ * q: nq x d fp32; out_dist: nq x k fp32; out_ids: nq x k int64. */
+vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                           int64_t nq, int32_t k, int32_t metric,
+                           float *out_dist, int64_t *out_ids);
+/* Full distance matrix out[i*n + j] = dist(q_i, x_j): computeDistances
+ * (:76-136, nq = 1) and batchComputeDistances(topK: nil) (:139-204). */
+vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                         int64_t nq, int32_t metric, float *out);
+
+/* ---- IVF-Flat ------------------------------------------------------------
+ * IVFIndex (Indexes/IVFIndex.swift).  The coarse centroids come from
+ * training (IVFIndex.train, :397-446); vsk_ivf_create takes them as given. */
+vsk_status vsk_ivf_create(vsk_ctx *ctx, const float *centroids, int32_t nlist,
+                          int32_t d, vsk_ivf **out);
+vsk_status vsk_ivf_free(vsk_ctx *ctx, vsk_ivf *ivf);
+/* IVFIndex.insert (:80-122): each row goes to its nearest centroid
+ * (findNearestCentroid, :514-527, strict '<'), appended in call order.
+ * ids may be NULL (then ids are the running row count). */
+vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
+                       const int64_t *ids, int64_t n);
+/* findNearestCentroid for each row (:514-527): out_list[n] */
+vsk_status vsk_ivf_assign(vsk_ctx *ctx, const vsk_ivf *ivf, const float *x,
+                          int64_t n, int32_t *out_list);
+/* findNearestCentroids (:529-540): out_lists[nq x nprobe] */
+vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                         int64_t nq, int32_t nprobe, int32_t *out_lists);
+/* IVFIndex.search (:124-202): probe nprobe lists, exact L2 (sqrt) over
+ * their union, top k.  nprobe >= nlist is the .exact strategy (:551-554). */
+vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                          int64_t nq, int32_t nprobe, int32_t k,
+                          float *out_dist, int64_t *out_ids);
+/* sizes[nlist] = rows per inverted list; total = sum */
+vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
+                              int64_t *sizes);
+
+/* ---- int8 scalar quantization ---------------------------------------------
+ * ScalarQuantizer (Quantization/ScalarQuantizer.swift).  per_dim = 0 is the
+ * reference's global min/max (:389-451); per_dim = 1 applies the same
+ * formulas per dimension.  scale/offset: d floats (per_dim) or 1. */
+vsk_status vsk_sq8_train(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                         int32_t per_dim, float *scale, float *offset);
+/* quantizeToInt8 (:251-270): code = clamp(trunc(x*scale + offset)) */
+vsk_status vsk_sq8_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                          int32_t per_dim, const float *scale,
+                          const float *offset, int8_t *codes);
+/* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81). */
+vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
+                          int32_t d, vsk_sq8 **out);
+vsk_status vsk_sq8_free(vsk_ctx *ctx, vsk_sq8 *db);
+/* Top k by score = sum_j qcode_j * code_j (int32, exact), i.e. ascending
+ * distance -score.  out_score: nq x k int32 (INT32_MIN where missing). */
+vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
+                          const int8_t *qcodes, int64_t nq, int32_t k,
+                          int32_t *out_score, int64_t *out_ids);
+
+/* ---- product quantization -------------------------------------------------
+ * ProductQuantizer (Quantization/ProductQuantizer.swift): M segments of
+ * dsub dims, ksub codewords each (ksub <= 256, codes uint8).
+ * codebooks: M x ksub x dsub fp32. */
+vsk_status vsk_pq_create(vsk_ctx *ctx, const float *codebooks, int32_t M,
+                         int32_t ksub, int32_t dsub, vsk_pq **out);
+vsk_status vsk_pq_free(vsk_ctx *ctx, vsk_pq *pq);
+/* encode (:68-112) via Codebook.encode (ProductQuantizerCodebook.swift:12-30):
+ * codes n x M uint8 */
+vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,
+                         int64_t n, uint8_t *codes);
+/* Append n x M codes to the resident code database. */
+vsk_status vsk_pq_add_codes(vsk_ctx *ctx, vsk_pq *pq, const uint8_t *codes,
+                            int64_t n);
+/* precomputeDistanceTables (:209-233): lut nq x M x ksub fp32 */
+vsk_status vsk_pq_lut(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                      int64_t nq, float *lut);
+/* ADC scan (DistanceTables.computeDistance, ProductQuantizerTypes.swift:
+ * 14-20) over all resident codes -> top k_adc by ADC sum, then, when
+ * rerank_db != NULL and rerank_metric >= 0, exact re-rank of those
+ * candidates with rerank_metric on rerank_db's rows -> top k.  Without
+ * re-rank the first k ADC results are returned as sqrt(sum). */
+vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                         int64_t nq, int32_t k_adc, int32_t k,
+                         int32_t rerank_metric, const vsk_db *rerank_db,
+                         float *out_dist, int64_t *out_ids);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VSK_HIP_H */

@@ -1,0 +1,242 @@
+"""numpy front end of the CPU oracle (oracle/libvsk_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
+the checker and by bench.py's cpu_baseline leg.  The product library never
+imports it.  The C code restates the reference's CPU algorithms; each
+function there cites the reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import c_float, c_int32, c_int64, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libvsk_oracle.so")
+
+L2SQ, L2, COSINE, COSINE_NORMALIZED, DOT, L1 = range(6)
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        P = c_void_p
+        sig = {
+            "vsko_l2sq": (c_float, [P, P, c_int32]),
+            "vsko_dot": (c_float, [P, P, c_int32]),
+            "vsko_l1": (c_float, [P, P, c_int32]),
+            "vsko_distance": (c_float, [P, P, c_int32, c_int32]),
+            "vsko_distances": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, c_int32]),
+            "vsko_search_flat": (None, [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P, P,
+                                        c_int32, c_int32]),
+            "vsko_topk": (None, [P, c_int64, c_int32, P, P]),
+            "vsko_ivf_assign": (None, [P, c_int64, P, c_int32, c_int32, P, c_int32]),
+            "vsko_ivf_probe": (None, [P, c_int64, P, c_int32, c_int32, c_int32, P, c_int32]),
+            "vsko_ivf_search": (None, [P, c_int64, P, P, P, c_int64, c_int32, P, c_int32,
+                                       c_int32, c_int32, P, P, c_int32]),
+            "vsko_sq8_train": (None, [P, c_int64, c_int32, c_int32, P, P]),
+            "vsko_sq8_encode": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
+            "vsko_sq8_decode": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
+            "vsko_sq8_dot": (c_int32, [P, P, c_int32]),
+            "vsko_sq8_search": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, P, c_int32]),
+            "vsko_pq_lut": (None, [P, P, c_int32, c_int32, c_int32, P]),
+            "vsko_pq_encode": (None, [P, c_int64, P, c_int32, c_int32, c_int32, P, c_int32]),
+            "vsko_pq_decode": (None, [P, c_int64, P, c_int32, c_int32, c_int32, P]),
+            "vsko_pq_adc_sum": (c_float, [P, P, c_int32, c_int32]),
+            "vsko_pq_adc_scan": (None, [P, P, c_int64, c_int32, c_int32, P]),
+            "vsko_pq_search": (None, [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32,
+                                      c_int32, c_int32, P, c_int32, P, P, c_int32]),
+            "vsko_kmeans": (None, [P, c_int64, c_int32, c_int32, c_int32, c_uint64, P, c_int32]),
+            "vsko_num_threads": (c_int32, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data
+
+
+def num_threads() -> int:
+    return int(lib().vsko_num_threads())
+
+
+def distance(q, x, metric) -> float:
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    return float(lib().vsko_distance(qp, xp, q.shape[-1], metric))
+
+
+def distances(q, x, metric, threads=0):
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    out = np.empty((q.shape[0], x.shape[0]), np.float32)
+    lib().vsko_distances(qp, q.shape[0], xp, x.shape[0], q.shape[1], metric,
+                         out.ctypes.data, threads)
+    return out
+
+
+def search_flat(q, x, k, metric, threads=0, fast=False):
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    nq = q.shape[0]
+    od = np.empty((nq, k), np.float32)
+    oi = np.empty((nq, k), np.int64)
+    lib().vsko_search_flat(qp, nq, xp, x.shape[0], x.shape[1], k, metric, od.ctypes.data,
+                           oi.ctypes.data, threads, 1 if fast else 0)
+    return od, oi
+
+
+def topk(dist, k):
+    d, dp = _c(dist, np.float32)
+    od = np.empty(k, np.float32)
+    oi = np.empty(k, np.int64)
+    lib().vsko_topk(dp, d.shape[0], k, od.ctypes.data, oi.ctypes.data)
+    return od, oi
+
+
+def ivf_assign(x, centroids, threads=0):
+    x, xp = _c(x, np.float32)
+    c, cp = _c(centroids, np.float32)
+    out = np.empty(x.shape[0], np.int32)
+    lib().vsko_ivf_assign(xp, x.shape[0], cp, c.shape[0], x.shape[1], out.ctypes.data, threads)
+    return out
+
+
+def ivf_probe(q, centroids, nprobe, threads=0):
+    q, qp = _c(q, np.float32)
+    c, cp = _c(centroids, np.float32)
+    out = np.empty((q.shape[0], nprobe), np.int32)
+    lib().vsko_ivf_probe(qp, q.shape[0], cp, c.shape[0], q.shape[1], nprobe, out.ctypes.data,
+                         threads)
+    return out
+
+
+def ivf_search(q, x, ids, list_of, centroids, nprobe, k, threads=0):
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    ids, ip = _c(ids, np.int64)
+    lo, lp = _c(list_of, np.int32)
+    c, cp = _c(centroids, np.float32)
+    nq = q.shape[0]
+    od = np.empty((nq, k), np.float32)
+    oi = np.empty((nq, k), np.int64)
+    lib().vsko_ivf_search(qp, nq, xp, ip, lp, x.shape[0], x.shape[1], cp, c.shape[0], nprobe, k,
+                          od.ctypes.data, oi.ctypes.data, threads)
+    return od, oi
+
+
+def sq8_train(x, per_dim=True):
+    x, xp = _c(x, np.float32)
+    d = x.shape[1]
+    s = np.empty(d if per_dim else 1, np.float32)
+    o = np.empty(d if per_dim else 1, np.float32)
+    lib().vsko_sq8_train(xp, x.shape[0], d, 1 if per_dim else 0, s.ctypes.data, o.ctypes.data)
+    return s, o
+
+
+def sq8_encode(x, scale, offset):
+    x, xp = _c(x, np.float32)
+    s, sp = _c(scale, np.float32)
+    o, op = _c(offset, np.float32)
+    per_dim = 1 if s.shape[0] > 1 or x.shape[1] == 1 else 0
+    out = np.empty(x.shape, np.int8)
+    lib().vsko_sq8_encode(xp, x.shape[0], x.shape[1], per_dim, sp, op, out.ctypes.data)
+    return out
+
+
+def sq8_decode(codes, scale, offset):
+    c, cp = _c(codes, np.int8)
+    s, sp = _c(scale, np.float32)
+    o, op = _c(offset, np.float32)
+    per_dim = 1 if s.shape[0] > 1 or c.shape[1] == 1 else 0
+    out = np.empty(c.shape, np.float32)
+    lib().vsko_sq8_decode(cp, c.shape[0], c.shape[1], per_dim, sp, op, out.ctypes.data)
+    return out
+
+
+def sq8_search(qcodes, codes, k, threads=0):
+    q, qp = _c(qcodes, np.int8)
+    c, cp = _c(codes, np.int8)
+    nq = q.shape[0]
+    os_ = np.empty((nq, k), np.int32)
+    oi = np.empty((nq, k), np.int64)
+    lib().vsko_sq8_search(qp, nq, cp, c.shape[0], c.shape[1], k, os_.ctypes.data,
+                          oi.ctypes.data, threads)
+    return os_, oi
+
+
+def pq_lut(q, codebooks):
+    q, qp = _c(q, np.float32)
+    cb, cbp = _c(codebooks, np.float32)
+    M, ksub, dsub = cb.shape
+    out = np.empty((M, ksub), np.float32)
+    lib().vsko_pq_lut(qp, cbp, M, ksub, dsub, out.ctypes.data)
+    return out
+
+
+def pq_encode(x, codebooks, threads=0):
+    x, xp = _c(x, np.float32)
+    cb, cbp = _c(codebooks, np.float32)
+    M, ksub, dsub = cb.shape
+    out = np.empty((x.shape[0], M), np.uint8)
+    lib().vsko_pq_encode(xp, x.shape[0], cbp, M, ksub, dsub, out.ctypes.data, threads)
+    return out
+
+
+def pq_decode(codes, codebooks):
+    c, cp = _c(codes, np.uint8)
+    cb, cbp = _c(codebooks, np.float32)
+    M, ksub, dsub = cb.shape
+    out = np.empty((c.shape[0], M * dsub), np.float32)
+    lib().vsko_pq_decode(cp, c.shape[0], cbp, M, ksub, dsub, out.ctypes.data)
+    return out
+
+
+def pq_adc_scan(lut, codes):
+    l, lp = _c(lut, np.float32)
+    c, cp = _c(codes, np.uint8)
+    out = np.empty(c.shape[0], np.float32)
+    lib().vsko_pq_adc_scan(lp, cp, c.shape[0], c.shape[1], l.shape[1], out.ctypes.data)
+    return out
+
+
+def pq_search(q, codebooks, codes, k_adc, k, x=None, rerank_metric=-1, threads=0):
+    q, qp = _c(q, np.float32)
+    cb, cbp = _c(codebooks, np.float32)
+    c, cp = _c(codes, np.uint8)
+    M, ksub, dsub = cb.shape
+    xp = 0
+    if x is not None:
+        x, xp = _c(x, np.float32)
+    nq = q.shape[0]
+    od = np.empty((nq, k), np.float32)
+    oi = np.empty((nq, k), np.int64)
+    lib().vsko_pq_search(qp, nq, cbp, cp, c.shape[0], M, ksub, dsub, k_adc, k,
+                         xp if x is not None else None, rerank_metric, od.ctypes.data,
+                         oi.ctypes.data, threads)
+    return od, oi
+
+
+def kmeans(x, k, iters=10, seed=0, threads=0):
+    x, xp = _c(x, np.float32)
+    out = np.empty((k, x.shape[1]), np.float32)
+    lib().vsko_kmeans(xp, x.shape[0], x.shape[1], k, iters, seed, out.ctypes.data, threads)
+    return out

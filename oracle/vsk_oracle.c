@@ -1,0 +1,770 @@
+/*
+ * vsk_oracle.c -- CPU restatement of VectorStoreKit's search hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker and CPU-baseline timing).  The
+ * shipped HIP library never links or calls it.  Build: oracle/Makefile
+ * (gcc -O3 -ffp-contract=off; no -ffast-math, so the fp32 order written
+ * here is the order executed).
+ *
+ * Reference paths below are relative to Sources/VectorStoreKit/ of
+ * gifton/VectorStoreKit.
+ */
+#include "vsk_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------------ */
+/* threading: a static split of [0, n) over nthreads pthreads                 */
+/* ------------------------------------------------------------------------ */
+typedef void (*range_fn)(void *ctx, int64_t lo, int64_t hi);
+typedef struct {
+  range_fn fn;
+  void *ctx;
+  int64_t lo, hi;
+} range_job;
+
+static void *range_trampoline(void *p) {
+  range_job *j = (range_job *)p;
+  j->fn(j->ctx, j->lo, j->hi);
+  return NULL;
+}
+
+int32_t vsko_num_threads(void) {
+  long c = sysconf(_SC_NPROCESSORS_ONLN);
+  return c > 0 ? (int32_t)c : 1;
+}
+
+static void parallel_for(int64_t n, int32_t nthreads, range_fn fn, void *ctx) {
+  if (nthreads <= 0) nthreads = vsko_num_threads();
+  if (nthreads > n) nthreads = (int32_t)(n > 0 ? n : 1);
+  if (nthreads <= 1) {
+    fn(ctx, 0, n);
+    return;
+  }
+  pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * nthreads);
+  range_job *jobs = (range_job *)malloc(sizeof(range_job) * nthreads);
+  for (int32_t t = 0; t < nthreads; ++t) {
+    jobs[t].fn = fn;
+    jobs[t].ctx = ctx;
+    jobs[t].lo = n * t / nthreads;
+    jobs[t].hi = n * (t + 1) / nthreads;
+    pthread_create(&th[t], NULL, range_trampoline, &jobs[t]);
+  }
+  for (int32_t t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+  free(th);
+  free(jobs);
+}
+
+/* ------------------------------------------------------------------------ */
+/* distances                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* sum (a_i - b_i)^2, i ascending, no FMA.
+ * Indexes/IVFIndex.swift:542-549 (computeDistance, before its sqrt);
+ * Quantization/ProductQuantizer.swift:362-369 (euclideanDistanceSquared). */
+float vsko_l2sq(const float *a, const float *b, int32_t d) {
+  float s = 0.0f;
+  for (int32_t i = 0; i < d; ++i) {
+    float diff = a[i] - b[i];
+    s += diff * diff;
+  }
+  return s;
+}
+
+/* sum a_i * b_i, i ascending (vDSP_dotpr in
+ * Acceleration/AccelerateOptimizer.swift:301-307,371-377; the order inside
+ * vDSP is not published, sequential order is this restatement's choice). */
+float vsko_dot(const float *a, const float *b, int32_t d) {
+  float s = 0.0f;
+  for (int32_t i = 0; i < d; ++i) s += a[i] * b[i];
+  return s;
+}
+
+/* sum |a_i - b_i|  (Acceleration/AccelerateOptimizer.swift:322-360:
+ * vDSP_vsub, vDSP_vabs, vDSP_sve). */
+float vsko_l1(const float *a, const float *b, int32_t d) {
+  float s = 0.0f;
+  for (int32_t i = 0; i < d; ++i) s += fabsf(a[i] - b[i]);
+  return s;
+}
+
+/* Acceleration/AccelerateOptimizer.swift:251-383 (euclidean: sqrt of the
+ * sum of squares; cosine: 1 - dot/(|q||x| + 1e-8) with magnitudes from
+ * vDSP_svesq + sqrt; dotProduct: -dot; manhattan: sum |q-x|) and
+ * Acceleration/Metal/Shaders/DistanceShaders.metal:815-845 (normalized
+ * cosine: 1 - dot). */
+float vsko_distance(const float *q, const float *x, int32_t d,
+                    int32_t metric) {
+  switch (metric) {
+  case VSKO_L2SQ:
+    return vsko_l2sq(q, x, d);
+  case VSKO_L2:
+    return sqrtf(vsko_l2sq(q, x, d));
+  case VSKO_COSINE: {
+    float qn = sqrtf(vsko_dot(q, q, d));
+    float xn = sqrtf(vsko_dot(x, x, d));
+    float dp = vsko_dot(q, x, d);
+    return 1.0f - dp / (qn * xn + 1e-8f);
+  }
+  case VSKO_COSINE_NORMALIZED:
+    return 1.0f - vsko_dot(q, x, d);
+  case VSKO_DOT:
+    return -vsko_dot(q, x, d);
+  case VSKO_L1:
+    return vsko_l1(q, x, d);
+  default:
+    return NAN;
+  }
+}
+
+/* 16 independent accumulators: what a SIMD library loop does.  Used only by
+ * the CPU-baseline timing (fast != 0), never by parity checks. */
+static float dot16(const float *a, const float *b, int32_t d) {
+  float acc[16] = {0};
+  int32_t i = 0;
+  for (; i + 16 <= d; i += 16)
+    for (int j = 0; j < 16; ++j) acc[j] += a[i + j] * b[i + j];
+  float s = 0.0f;
+  for (int j = 0; j < 16; ++j) s += acc[j];
+  for (; i < d; ++i) s += a[i] * b[i];
+  return s;
+}
+static float l2sq16(const float *a, const float *b, int32_t d) {
+  float acc[16] = {0};
+  int32_t i = 0;
+  for (; i + 16 <= d; i += 16)
+    for (int j = 0; j < 16; ++j) {
+      float t = a[i + j] - b[i + j];
+      acc[j] += t * t;
+    }
+  float s = 0.0f;
+  for (int j = 0; j < 16; ++j) s += acc[j];
+  for (; i < d; ++i) {
+    float t = a[i] - b[i];
+    s += t * t;
+  }
+  return s;
+}
+static float l116(const float *a, const float *b, int32_t d) {
+  float acc[16] = {0};
+  int32_t i = 0;
+  for (; i + 16 <= d; i += 16)
+    for (int j = 0; j < 16; ++j) acc[j] += fabsf(a[i + j] - b[i + j]);
+  float s = 0.0f;
+  for (int j = 0; j < 16; ++j) s += acc[j];
+  for (; i < d; ++i) s += fabsf(a[i] - b[i]);
+  return s;
+}
+static float distance_fast(const float *q, const float *x, int32_t d,
+                           int32_t metric, float qnorm) {
+  switch (metric) {
+  case VSKO_L2SQ:
+    return l2sq16(q, x, d);
+  case VSKO_L2:
+    return sqrtf(l2sq16(q, x, d));
+  case VSKO_COSINE: {
+    float xn = sqrtf(dot16(x, x, d));
+    return 1.0f - dot16(q, x, d) / (qnorm * xn + 1e-8f);
+  }
+  case VSKO_COSINE_NORMALIZED:
+    return 1.0f - dot16(q, x, d);
+  case VSKO_DOT:
+    return -dot16(q, x, d);
+  case VSKO_L1:
+    return l116(q, x, d);
+  default:
+    return NAN;
+  }
+}
+
+typedef struct {
+  const float *q, *x;
+  int64_t n;
+  int32_t d, metric;
+  float *out;
+} dist_ctx;
+static void dist_range(void *p, int64_t lo, int64_t hi) {
+  dist_ctx *c = (dist_ctx *)p;
+  for (int64_t i = lo; i < hi; ++i)
+    for (int64_t j = 0; j < c->n; ++j)
+      c->out[i * c->n + j] =
+          vsko_distance(c->q + i * c->d, c->x + j * c->d, c->d, c->metric);
+}
+void vsko_distances(const float *q, int64_t nq, const float *x, int64_t n,
+                    int32_t d, int32_t metric, float *out, int32_t nthreads) {
+  dist_ctx c = {q, x, n, d, metric, out};
+  parallel_for(nq, nthreads, dist_range, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* top-k: k smallest by (value, tie) ascending                                */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  float v;
+  int64_t t; /* tie key */
+} pair_t;
+
+static int pair_less(pair_t a, pair_t b) {
+  return a.v < b.v || (a.v == b.v && a.t < b.t);
+}
+
+/* max-heap of size k on (v, t): root = current worst kept element */
+static void heap_sift_down(pair_t *h, int32_t n, int32_t i) {
+  for (;;) {
+    int32_t l = 2 * i + 1, r = l + 1, m = i;
+    if (l < n && pair_less(h[m], h[l])) m = l;
+    if (r < n && pair_less(h[m], h[r])) m = r;
+    if (m == i) return;
+    pair_t t = h[i];
+    h[i] = h[m];
+    h[m] = t;
+    i = m;
+  }
+}
+static void heap_sift_up(pair_t *h, int32_t i) {
+  while (i > 0) {
+    int32_t p = (i - 1) / 2;
+    if (!pair_less(h[p], h[i])) return;
+    pair_t t = h[i];
+    h[i] = h[p];
+    h[p] = t;
+    i = p;
+  }
+}
+typedef struct {
+  pair_t *h;
+  int32_t n, k;
+} topk_t;
+static void topk_push(topk_t *s, float v, int64_t t) {
+  pair_t p = {v, t};
+  if (s->n < s->k) {
+    s->h[s->n] = p;
+    heap_sift_up(s->h, s->n);
+    s->n++;
+  } else if (s->k > 0 && pair_less(p, s->h[0])) {
+    s->h[0] = p;
+    heap_sift_down(s->h, s->n, 0);
+  }
+}
+static int pair_cmp(const void *a, const void *b) {
+  pair_t x = *(const pair_t *)a, y = *(const pair_t *)b;
+  if (pair_less(x, y)) return -1;
+  if (pair_less(y, x)) return 1;
+  return 0;
+}
+/* sorted ascending into out; slots past the kept count get (inf, -1) */
+static void topk_finish(topk_t *s, float *out_v, int64_t *out_t) {
+  qsort(s->h, (size_t)s->n, sizeof(pair_t), pair_cmp);
+  for (int32_t i = 0; i < s->k; ++i) {
+    if (i < s->n) {
+      out_v[i] = s->h[i].v;
+      out_t[i] = s->h[i].t;
+    } else {
+      out_v[i] = INFINITY;
+      out_t[i] = -1;
+    }
+  }
+}
+
+/* The selection the reference's stable sort + prefix(k) performs
+ * (Indexes/IVFIndex.swift:175-176), with ties broken by index; it does NOT
+ * reproduce AccelerateOptimizer.selectTopK's k>=10 heap branch
+ * (Acceleration/AccelerateOptimizer.swift:136-148), which keeps a min-heap
+ * and so returns the wrong elements. */
+void vsko_topk(const float *dist, int64_t n, int32_t k, float *out_dist,
+               int64_t *out_idx) {
+  topk_t s = {(pair_t *)malloc(sizeof(pair_t) * (k > 0 ? k : 1)), 0, k};
+  for (int64_t i = 0; i < n; ++i) topk_push(&s, dist[i], i);
+  topk_finish(&s, out_dist, out_idx);
+  free(s.h);
+}
+
+/* ------------------------------------------------------------------------ */
+/* flat exact search                                                          */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const float *q, *x;
+  int64_t n;
+  int32_t d, k, metric, fast;
+  float *od;
+  int64_t *oi;
+} flat_ctx;
+
+/* per query: distance to every row (Acceleration/AccelerateOptimizer.swift:
+ * 96-121 batchComputeDistances -> computeDistances), then the k smallest. */
+static void flat_range(void *p, int64_t lo, int64_t hi) {
+  flat_ctx *c = (flat_ctx *)p;
+  topk_t s = {(pair_t *)malloc(sizeof(pair_t) * (c->k > 0 ? c->k : 1)), 0,
+              c->k};
+  for (int64_t i = lo; i < hi; ++i) {
+    const float *qi = c->q + i * c->d;
+    float qn = sqrtf(dot16(qi, qi, c->d));
+    s.n = 0;
+    for (int64_t j = 0; j < c->n; ++j) {
+      const float *xj = c->x + j * c->d;
+      float v = c->fast ? distance_fast(qi, xj, c->d, c->metric, qn)
+                        : vsko_distance(qi, xj, c->d, c->metric);
+      topk_push(&s, v, j);
+    }
+    topk_finish(&s, c->od + i * c->k, c->oi + i * c->k);
+  }
+  free(s.h);
+}
+void vsko_search_flat(const float *q, int64_t nq, const float *x, int64_t n,
+                      int32_t d, int32_t k, int32_t metric, float *out_dist,
+                      int64_t *out_ids, int32_t nthreads, int32_t fast) {
+  flat_ctx c = {q, x, n, d, k, metric, fast, out_dist, out_ids};
+  parallel_for(nq, nthreads, flat_range, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* IVF-Flat                                                                   */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const float *x, *c;
+  int32_t nlist, d;
+  int32_t *out;
+} assign_ctx;
+/* Indexes/IVFIndex.swift:514-527 findNearestCentroid: distance =
+ * sqrt(sum diff^2) (:542-549), strict '<' so the first minimum wins. */
+static void assign_range(void *p, int64_t lo, int64_t hi) {
+  assign_ctx *a = (assign_ctx *)p;
+  for (int64_t i = lo; i < hi; ++i) {
+    float best = INFINITY;
+    int32_t bi = 0;
+    for (int32_t c = 0; c < a->nlist; ++c) {
+      float v = sqrtf(vsko_l2sq(a->x + i * a->d, a->c + (int64_t)c * a->d,
+                                a->d));
+      if (v < best) {
+        best = v;
+        bi = c;
+      }
+    }
+    a->out[i] = bi;
+  }
+}
+void vsko_ivf_assign(const float *x, int64_t n, const float *centroids,
+                     int32_t nlist, int32_t d, int32_t *out_list,
+                     int32_t nthreads) {
+  assign_ctx a = {x, centroids, nlist, d, out_list};
+  parallel_for(n, nthreads, assign_range, &a);
+}
+
+/* Indexes/IVFIndex.swift:529-540 findNearestCentroids: sqrt-L2 to every
+ * centroid, stable sort ascending, first `count` indices. */
+static void probe_one(const float *q, const float *centroids, int32_t nlist,
+                      int32_t d, int32_t nprobe, int32_t *out, pair_t *buf) {
+  topk_t s = {buf, 0, nprobe};
+  for (int32_t c = 0; c < nlist; ++c)
+    topk_push(&s, sqrtf(vsko_l2sq(q, centroids + (int64_t)c * d, d)), c);
+  qsort(s.h, (size_t)s.n, sizeof(pair_t), pair_cmp);
+  for (int32_t i = 0; i < nprobe; ++i)
+    out[i] = i < s.n ? (int32_t)s.h[i].t : -1;
+}
+typedef struct {
+  const float *q, *c;
+  int32_t nlist, d, nprobe;
+  int32_t *out;
+} probe_ctx;
+static void probe_range(void *p, int64_t lo, int64_t hi) {
+  probe_ctx *a = (probe_ctx *)p;
+  pair_t *buf = (pair_t *)malloc(sizeof(pair_t) * (a->nprobe + 1));
+  for (int64_t i = lo; i < hi; ++i)
+    probe_one(a->q + i * a->d, a->c, a->nlist, a->d, a->nprobe,
+              a->out + i * a->nprobe, buf);
+  free(buf);
+}
+void vsko_ivf_probe(const float *q, int64_t nq, const float *centroids,
+                    int32_t nlist, int32_t d, int32_t nprobe,
+                    int32_t *out_lists, int32_t nthreads) {
+  probe_ctx a = {q, centroids, nlist, d, nprobe, out_lists};
+  parallel_for(nq, nthreads, probe_range, &a);
+}
+
+typedef struct {
+  const float *q, *x, *c;
+  const int64_t *ids;
+  const int64_t *list_start; /* [nlist+1] offsets into rows_by_list */
+  const int64_t *rows_by_list;
+  int32_t d, nlist, nprobe, k;
+  float *od;
+  int64_t *oi;
+} ivf_ctx;
+
+/* Indexes/IVFIndex.swift:124-176: probe (:147-148), concatenate the probed
+ * lists in probe order (:151-157), exact sqrt-L2 per candidate (:167-172),
+ * stable sort + prefix(k) (:175-176).  The tie key is the position in the
+ * concatenation, which is what a stable sort keeps. */
+static void ivf_range(void *p, int64_t lo, int64_t hi) {
+  ivf_ctx *a = (ivf_ctx *)p;
+  int32_t *probes = (int32_t *)malloc(sizeof(int32_t) * a->nprobe);
+  pair_t *pbuf = (pair_t *)malloc(sizeof(pair_t) * (a->nprobe + 1));
+  pair_t *kbuf = (pair_t *)malloc(sizeof(pair_t) * (a->k > 0 ? a->k : 1));
+  int64_t *pos_row = NULL;
+  int64_t cap = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const float *qi = a->q + i * a->d;
+    probe_one(qi, a->c, a->nlist, a->d, a->nprobe, probes, pbuf);
+    topk_t s = {kbuf, 0, a->k};
+    int64_t pos = 0;
+    for (int32_t pi = 0; pi < a->nprobe; ++pi) {
+      int32_t l = probes[pi];
+      if (l < 0) continue;
+      int64_t b = a->list_start[l], e = a->list_start[l + 1];
+      if (pos + (e - b) > cap) {
+        cap = (pos + (e - b)) * 2;
+        pos_row = (int64_t *)realloc(pos_row, sizeof(int64_t) * cap);
+      }
+      for (int64_t r = b; r < e; ++r) {
+        int64_t row = a->rows_by_list[r];
+        float v = sqrtf(vsko_l2sq(qi, a->x + row * a->d, a->d));
+        pos_row[pos] = row;
+        topk_push(&s, v, pos);
+        ++pos;
+      }
+    }
+    topk_finish(&s, a->od + i * a->k, a->oi + i * a->k);
+    for (int32_t j = 0; j < a->k; ++j) {
+      int64_t ps = a->oi[i * a->k + j];
+      a->oi[i * a->k + j] = ps >= 0 ? a->ids[pos_row[ps]] : -1;
+    }
+  }
+  free(pos_row);
+  free(kbuf);
+  free(pbuf);
+  free(probes);
+}
+
+void vsko_ivf_search(const float *q, int64_t nq, const float *x,
+                     const int64_t *ids, const int32_t *list_of, int64_t n,
+                     int32_t d, const float *centroids, int32_t nlist,
+                     int32_t nprobe, int32_t k, float *out_dist,
+                     int64_t *out_ids, int32_t nthreads) {
+  /* inverted lists keep insertion order (Indexes/IVFIndex.swift:80-122
+   * appends to invertedLists[nearest]) */
+  int64_t *start = (int64_t *)calloc((size_t)nlist + 1, sizeof(int64_t));
+  int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * (n > 0 ? n : 1));
+  for (int64_t i = 0; i < n; ++i) start[list_of[i] + 1]++;
+  for (int32_t l = 0; l < nlist; ++l) start[l + 1] += start[l];
+  int64_t *fill = (int64_t *)malloc(sizeof(int64_t) * (nlist + 1));
+  memcpy(fill, start, sizeof(int64_t) * (nlist + 1));
+  for (int64_t i = 0; i < n; ++i) rows[fill[list_of[i]]++] = i;
+  free(fill);
+  ivf_ctx a = {q,     x,     centroids, ids,      start,   rows,
+               d,     nlist, nprobe,    k,        out_dist, out_ids};
+  parallel_for(nq, nthreads, ivf_range, &a);
+  free(rows);
+  free(start);
+}
+
+/* ------------------------------------------------------------------------ */
+/* scalar quantization, int8                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Quantization/ScalarQuantizer.swift:389-418 (min/max over the values) and
+ * :420-451 (.int8: scale = 255/(max-min), offset = -min*scale - 128).  The
+ * reference uses the global min/max; per_dim applies the same formulas per
+ * column.  A zero range would give an infinite scale in the reference; here
+ * scale = 1 is used so every value maps to -128. */
+static void sq8_params(float mn, float mx, float *s, float *o) {
+  float range = mx - mn;
+  float scale = range > 0.0f ? 255.0f / range : 1.0f;
+  *s = scale;
+  *o = -mn * scale - 128.0f;
+}
+void vsko_sq8_train(const float *x, int64_t n, int32_t d, int32_t per_dim,
+                    float *scale, float *offset) {
+  if (per_dim) {
+    for (int32_t j = 0; j < d; ++j) {
+      float mn = INFINITY, mx = -INFINITY;
+      for (int64_t i = 0; i < n; ++i) {
+        float v = x[i * d + j];
+        if (v < mn) mn = v;
+        if (v > mx) mx = v;
+      }
+      sq8_params(mn, mx, &scale[j], &offset[j]);
+    }
+  } else {
+    float mn = INFINITY, mx = -INFINITY;
+    for (int64_t i = 0; i < n * d; ++i) {
+      if (x[i] < mn) mn = x[i];
+      if (x[i] > mx) mx = x[i];
+    }
+    sq8_params(mn, mx, &scale[0], &offset[0]);
+  }
+}
+
+/* Quantization/ScalarQuantizer.swift:251-270 quantizeToInt8:
+ * vDSP_vsmsa (t = x*scale + offset) then vDSP_vfix8 (conversion toward
+ * zero).  Out-of-range values are clamped to [-128, 127] here (vDSP_vfix8's
+ * out-of-range behaviour is not published). */
+static int8_t sq8_code(float v, float s, float o) {
+  float t = v * s;
+  t = t + o;
+  if (!(t > -128.0f)) return -128; /* also NaN */
+  if (t >= 127.0f) return 127;
+  return (int8_t)(int32_t)t; /* C conversion truncates toward zero */
+}
+void vsko_sq8_encode(const float *x, int64_t n, int32_t d, int32_t per_dim,
+                     const float *scale, const float *offset, int8_t *codes) {
+  for (int64_t i = 0; i < n; ++i)
+    for (int32_t j = 0; j < d; ++j) {
+      float s = per_dim ? scale[j] : scale[0];
+      float o = per_dim ? offset[j] : offset[0];
+      codes[i * d + j] = sq8_code(x[i * d + j], s, o);
+    }
+}
+/* Quantization/ScalarQuantizer.swift:568-580 dequantizeFromInt8:
+ * (code - offset) / scale */
+void vsko_sq8_decode(const int8_t *codes, int64_t n, int32_t d,
+                     int32_t per_dim, const float *scale, const float *offset,
+                     float *out) {
+  for (int64_t i = 0; i < n; ++i)
+    for (int32_t j = 0; j < d; ++j) {
+      float s = per_dim ? scale[j] : scale[0];
+      float o = per_dim ? offset[j] : offset[0];
+      out[i * d + j] = ((float)codes[i * d + j] - o) / s;
+    }
+}
+/* exact integer dot of two code vectors (the int32-accumulated score the
+ * scan ranks by; the reference has no int8 distance, so this is the
+ * documented build rule: distance = -score). */
+int32_t vsko_sq8_dot(const int8_t *a, const int8_t *b, int32_t d) {
+  int32_t s = 0;
+  for (int32_t i = 0; i < d; ++i) s += (int32_t)a[i] * (int32_t)b[i];
+  return s;
+}
+typedef struct {
+  const int8_t *q, *x;
+  int64_t n;
+  int32_t d, k;
+  int32_t *os;
+  int64_t *oi;
+} sq8_ctx;
+static void sq8_range(void *p, int64_t lo, int64_t hi) {
+  sq8_ctx *c = (sq8_ctx *)p;
+  pair_t *buf = (pair_t *)malloc(sizeof(pair_t) * (c->k > 0 ? c->k : 1));
+  float *tmpd = (float *)malloc(sizeof(float) * (c->k > 0 ? c->k : 1));
+  for (int64_t i = lo; i < hi; ++i) {
+    topk_t s = {buf, 0, c->k};
+    for (int64_t j = 0; j < c->n; ++j)
+      topk_push(&s, (float)(-vsko_sq8_dot(c->q + i * c->d, c->x + j * c->d,
+                                          c->d)),
+                j);
+    topk_finish(&s, tmpd, c->oi + i * c->k);
+    for (int32_t t = 0; t < c->k; ++t)
+      c->os[i * c->k + t] =
+          c->oi[i * c->k + t] >= 0 ? (int32_t)(-tmpd[t]) : INT32_MIN;
+  }
+  free(tmpd);
+  free(buf);
+}
+/* |score| <= 128*128*d < 2^24 for d <= 1024, so the float key is exact. */
+void vsko_sq8_search(const int8_t *qcodes, int64_t nq, const int8_t *codes,
+                     int64_t n, int32_t d, int32_t k, int32_t *out_score,
+                     int64_t *out_ids, int32_t nthreads) {
+  sq8_ctx c = {qcodes, codes, n, d, k, out_score, out_ids};
+  parallel_for(nq, nthreads, sq8_range, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* product quantization                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Quantization/ProductQuantizer.swift:209-233 precomputeDistanceTables:
+ * table[m][c] = euclideanDistanceSquared(q segment m, codeword c)
+ * (:362-369, sequential, no FMA). */
+void vsko_pq_lut(const float *q, const float *codebooks, int32_t M,
+                 int32_t ksub, int32_t dsub, float *lut) {
+  for (int32_t m = 0; m < M; ++m)
+    for (int32_t c = 0; c < ksub; ++c)
+      lut[m * ksub + c] = vsko_l2sq(
+          q + m * dsub, codebooks + ((int64_t)m * ksub + c) * dsub, dsub);
+}
+
+/* Quantization/ProductQuantizerCodebook.swift:12-30 Codebook.encode:
+ * argmin over codewords of the squared distance, strict '<'. */
+typedef struct {
+  const float *x, *cb;
+  int32_t M, ksub, dsub;
+  uint8_t *codes;
+} pqenc_ctx;
+static void pqenc_range(void *p, int64_t lo, int64_t hi) {
+  pqenc_ctx *a = (pqenc_ctx *)p;
+  int32_t d = a->M * a->dsub;
+  for (int64_t i = lo; i < hi; ++i)
+    for (int32_t m = 0; m < a->M; ++m) {
+      float best = INFINITY;
+      int32_t bc = 0;
+      for (int32_t c = 0; c < a->ksub; ++c) {
+        float v = vsko_l2sq(a->x + i * d + m * a->dsub,
+                            a->cb + ((int64_t)m * a->ksub + c) * a->dsub,
+                            a->dsub);
+        if (v < best) {
+          best = v;
+          bc = c;
+        }
+      }
+      a->codes[i * a->M + m] = (uint8_t)bc;
+    }
+}
+void vsko_pq_encode(const float *x, int64_t n, const float *codebooks,
+                    int32_t M, int32_t ksub, int32_t dsub, uint8_t *codes,
+                    int32_t nthreads) {
+  pqenc_ctx a = {x, codebooks, M, ksub, dsub, codes};
+  parallel_for(n, nthreads, pqenc_range, &a);
+}
+/* Quantization/ProductQuantizerCodebook.swift:32-34 decode (codeword copy) */
+void vsko_pq_decode(const uint8_t *codes, int64_t n, const float *codebooks,
+                    int32_t M, int32_t ksub, int32_t dsub, float *out) {
+  for (int64_t i = 0; i < n; ++i)
+    for (int32_t m = 0; m < M; ++m)
+      memcpy(out + i * M * dsub + m * dsub,
+             codebooks + ((int64_t)m * ksub + codes[i * M + m]) * dsub,
+             sizeof(float) * dsub);
+}
+
+/* Quantization/ProductQuantizerTypes.swift:14-20 DistanceTables.computeDistance
+ * before its sqrt: sum over segments in ascending order, starting at 0. */
+float vsko_pq_adc_sum(const float *lut, const uint8_t *code, int32_t M,
+                      int32_t ksub) {
+  float s = 0.0f;
+  for (int32_t m = 0; m < M; ++m) s += lut[m * ksub + code[m]];
+  return s;
+}
+void vsko_pq_adc_scan(const float *lut, const uint8_t *codes, int64_t n,
+                      int32_t M, int32_t ksub, float *out_sum) {
+  for (int64_t i = 0; i < n; ++i)
+    out_sum[i] = vsko_pq_adc_sum(lut, codes + i * M, M, ksub);
+}
+
+typedef struct {
+  const float *q, *cb, *x;
+  const uint8_t *codes;
+  int64_t n;
+  int32_t M, ksub, dsub, k_adc, k, rerank;
+  float *od;
+  int64_t *oi;
+} pqs_ctx;
+static void pqs_range(void *p, int64_t lo, int64_t hi) {
+  pqs_ctx *a = (pqs_ctx *)p;
+  int32_t d = a->M * a->dsub;
+  float *lut = (float *)malloc(sizeof(float) * a->M * a->ksub);
+  pair_t *buf = (pair_t *)malloc(sizeof(pair_t) * (a->k_adc > 0 ? a->k_adc : 1));
+  pair_t *buf2 = (pair_t *)malloc(sizeof(pair_t) * (a->k > 0 ? a->k : 1));
+  float *cd = (float *)malloc(sizeof(float) * (a->k_adc > 0 ? a->k_adc : 1));
+  int64_t *ci = (int64_t *)malloc(sizeof(int64_t) * (a->k_adc > 0 ? a->k_adc : 1));
+  for (int64_t i = lo; i < hi; ++i) {
+    const float *qi = a->q + i * d;
+    vsko_pq_lut(qi, a->cb, a->M, a->ksub, a->dsub, lut);
+    topk_t s = {buf, 0, a->k_adc};
+    for (int64_t j = 0; j < a->n; ++j)
+      topk_push(&s, vsko_pq_adc_sum(lut, a->codes + j * a->M, a->M, a->ksub),
+                j);
+    topk_finish(&s, cd, ci);
+    if (a->x && a->rerank >= 0) {
+      topk_t s2 = {buf2, 0, a->k};
+      for (int32_t t = 0; t < a->k_adc; ++t)
+        if (ci[t] >= 0)
+          topk_push(&s2, vsko_distance(qi, a->x + ci[t] * d, d, a->rerank),
+                    ci[t]);
+      topk_finish(&s2, a->od + i * a->k, a->oi + i * a->k);
+    } else {
+      for (int32_t t = 0; t < a->k; ++t) {
+        a->od[i * a->k + t] =
+            t < a->k_adc && ci[t] >= 0 ? sqrtf(cd[t]) : INFINITY;
+        a->oi[i * a->k + t] = t < a->k_adc ? ci[t] : -1;
+      }
+    }
+  }
+  free(ci);
+  free(cd);
+  free(buf2);
+  free(buf);
+  free(lut);
+}
+void vsko_pq_search(const float *q, int64_t nq, const float *codebooks,
+                    const uint8_t *codes, int64_t n, int32_t M, int32_t ksub,
+                    int32_t dsub, int32_t k_adc, int32_t k, const float *x,
+                    int32_t rerank_metric, float *out_dist, int64_t *out_ids,
+                    int32_t nthreads) {
+  pqs_ctx a = {q,    codebooks, x,     codes, n,        M,       ksub,
+               dsub, k_adc,     k,     rerank_metric, out_dist, out_ids};
+  parallel_for(nq, nthreads, pqs_range, &a);
+}
+
+/* ------------------------------------------------------------------------ */
+/* k-means (used only to make test fixtures: PQ codebooks)                    */
+/* ------------------------------------------------------------------------ */
+static uint64_t splitmix64(uint64_t *s) {
+  uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+typedef struct {
+  const float *x, *c;
+  int32_t d, k;
+  int32_t *assign;
+} km_ctx;
+static void km_assign_range(void *p, int64_t lo, int64_t hi) {
+  km_ctx *a = (km_ctx *)p;
+  for (int64_t i = lo; i < hi; ++i) {
+    float best = INFINITY;
+    int32_t bi = 0;
+    for (int32_t c = 0; c < a->k; ++c) {
+      float v = vsko_l2sq(a->x + i * a->d, a->c + (int64_t)c * a->d, a->d);
+      if (v < best) {
+        best = v;
+        bi = c;
+      }
+    }
+    a->assign[i] = bi;
+  }
+}
+/* Clustering/KMeansClustering.swift:48-113 (Lloyd loop), :271-295
+ * (assignment with strict '<'), :342-380 (mean update).  Initialisation
+ * here is a seeded sample of k distinct rows, not k-means++. */
+void vsko_kmeans(const float *x, int64_t n, int32_t d, int32_t k,
+                 int32_t iters, uint64_t seed, float *centroids,
+                 int32_t nthreads) {
+  int64_t *perm = (int64_t *)malloc(sizeof(int64_t) * n);
+  for (int64_t i = 0; i < n; ++i) perm[i] = i;
+  uint64_t st = seed;
+  for (int64_t i = 0; i < k && i < n; ++i) {
+    int64_t j = i + (int64_t)(splitmix64(&st) % (uint64_t)(n - i));
+    int64_t t = perm[i];
+    perm[i] = perm[j];
+    perm[j] = t;
+  }
+  for (int32_t c = 0; c < k; ++c)
+    memcpy(centroids + (int64_t)c * d, x + perm[c % n] * d,
+           sizeof(float) * d);
+  free(perm);
+  int32_t *assign = (int32_t *)malloc(sizeof(int32_t) * n);
+  double *sum = (double *)malloc(sizeof(double) * (size_t)k * d);
+  int64_t *cnt = (int64_t *)malloc(sizeof(int64_t) * k);
+  for (int32_t it = 0; it < iters; ++it) {
+    km_ctx a = {x, centroids, d, k, assign};
+    parallel_for(n, nthreads, km_assign_range, &a);
+    memset(sum, 0, sizeof(double) * (size_t)k * d);
+    memset(cnt, 0, sizeof(int64_t) * k);
+    for (int64_t i = 0; i < n; ++i) {
+      cnt[assign[i]]++;
+      for (int32_t j = 0; j < d; ++j)
+        sum[(int64_t)assign[i] * d + j] += x[i * d + j];
+    }
+    for (int32_t c = 0; c < k; ++c)
+      if (cnt[c] > 0)
+        for (int32_t j = 0; j < d; ++j)
+          centroids[(int64_t)c * d + j] =
+              (float)(sum[(int64_t)c * d + j] / (double)cnt[c]);
+  }
+  free(cnt);
+  free(sum);
+  free(assign);
+}

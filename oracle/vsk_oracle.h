@@ -1,0 +1,123 @@
+/*
+ * vsk_oracle.h -- CPU restatement of VectorStoreKit's search hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the shipped library links, loads or
+ * calls this code.  It is used by tests/ (as the parity checker), by
+ * __graft_entry__.smoke() (as the checker of one small GPU call) and by
+ * bench.py's cpu_baseline leg (timed on the host, never as the GPU result).
+ *
+ * All arithmetic is plain fp32 in the reference's order (sequential, index
+ * ascending, no FMA contraction: built with -ffp-contract=off), int32 for
+ * int8 codes.  Every function names the reference file:line it restates
+ * (paths relative to Sources/VectorStoreKit/ of gifton/VectorStoreKit).
+ *
+ * Ordering rule used everywhere: ascending (distance, tie key) where the tie
+ * key is the row id for flat/SQ/PQ search, the centroid index for IVF
+ * probing and the position in the probe-ordered candidate concatenation for
+ * IVF search.  That is what the reference's stable `sort` + `prefix(k)`
+ * produces (Indexes/IVFIndex.swift:175-176, :538-539).
+ */
+#ifndef VSK_ORACLE_H
+#define VSK_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* metric codes (same values as the VSK_METRIC_* codes of the C ABI) */
+enum {
+  VSKO_L2SQ = 0,              /* sum (q-x)^2                                 */
+  VSKO_L2 = 1,                /* sqrt(sum (q-x)^2)                           */
+  VSKO_COSINE = 2,            /* 1 - q.x / (|q||x| + 1e-8)                   */
+  VSKO_COSINE_NORMALIZED = 3, /* 1 - q.x (unit-norm inputs)                  */
+  VSKO_DOT = 4,               /* -q.x                                        */
+  VSKO_L1 = 5                 /* sum |q-x|                                   */
+};
+
+/* ---- distances ---------------------------------------------------------- */
+float vsko_l2sq(const float *a, const float *b, int32_t d);
+float vsko_dot(const float *a, const float *b, int32_t d);
+float vsko_l1(const float *a, const float *b, int32_t d);
+float vsko_distance(const float *q, const float *x, int32_t d, int32_t metric);
+/* out[i*n + j] = distance(q_i, x_j) */
+void vsko_distances(const float *q, int64_t nq, const float *x, int64_t n,
+                    int32_t d, int32_t metric, float *out, int32_t nthreads);
+
+/* ---- exact flat k-NN ---------------------------------------------------- */
+/* fast != 0 uses a 16-accumulator dot/L2 (timing only; different fp order). */
+void vsko_search_flat(const float *q, int64_t nq, const float *x, int64_t n,
+                      int32_t d, int32_t k, int32_t metric, float *out_dist,
+                      int64_t *out_ids, int32_t nthreads, int32_t fast);
+/* k smallest of dist[0..n) by (dist, index); missing slots get (inf, -1). */
+void vsko_topk(const float *dist, int64_t n, int32_t k, float *out_dist,
+               int64_t *out_idx);
+
+/* ---- IVF-Flat ----------------------------------------------------------- */
+void vsko_ivf_assign(const float *x, int64_t n, const float *centroids,
+                     int32_t nlist, int32_t d, int32_t *out_list,
+                     int32_t nthreads);
+void vsko_ivf_probe(const float *q, int64_t nq, const float *centroids,
+                    int32_t nlist, int32_t d, int32_t nprobe,
+                    int32_t *out_lists, int32_t nthreads);
+/* list_of[i] = inverted list of row i (rows keep insertion order inside a
+ * list); ids[i] = user id of row i.  Output distances are L2 (sqrt). */
+void vsko_ivf_search(const float *q, int64_t nq, const float *x,
+                     const int64_t *ids, const int32_t *list_of, int64_t n,
+                     int32_t d, const float *centroids, int32_t nlist,
+                     int32_t nprobe, int32_t k, float *out_dist,
+                     int64_t *out_ids, int32_t nthreads);
+
+/* ---- scalar quantization (int8) ----------------------------------------- */
+/* per_dim != 0: scale[d], offset[d] from per-column min/max;
+ * per_dim == 0: scale[0], offset[0] from the global min/max. */
+void vsko_sq8_train(const float *x, int64_t n, int32_t d, int32_t per_dim,
+                    float *scale, float *offset);
+void vsko_sq8_encode(const float *x, int64_t n, int32_t d, int32_t per_dim,
+                     const float *scale, const float *offset, int8_t *codes);
+void vsko_sq8_decode(const int8_t *codes, int64_t n, int32_t d,
+                     int32_t per_dim, const float *scale, const float *offset,
+                     float *out);
+int32_t vsko_sq8_dot(const int8_t *a, const int8_t *b, int32_t d);
+/* top-k by (-score, id); out_score = score (int32) */
+void vsko_sq8_search(const int8_t *qcodes, int64_t nq, const int8_t *codes,
+                     int64_t n, int32_t d, int32_t k, int32_t *out_score,
+                     int64_t *out_ids, int32_t nthreads);
+
+/* ---- product quantization ----------------------------------------------- */
+/* codebooks: [M][ksub][dsub] fp32; lut: [M][ksub] */
+void vsko_pq_lut(const float *q, const float *codebooks, int32_t M,
+                 int32_t ksub, int32_t dsub, float *lut);
+void vsko_pq_encode(const float *x, int64_t n, const float *codebooks,
+                    int32_t M, int32_t ksub, int32_t dsub, uint8_t *codes,
+                    int32_t nthreads);
+void vsko_pq_decode(const uint8_t *codes, int64_t n, const float *codebooks,
+                    int32_t M, int32_t ksub, int32_t dsub, float *out);
+float vsko_pq_adc_sum(const float *lut, const uint8_t *code, int32_t M,
+                      int32_t ksub);
+/* ADC top-k_adc by (sum, id).  If x != NULL and rerank_metric >= 0 the
+ * k_adc candidates are re-scored with the exact metric on x and the top k
+ * by (exact, id) are returned; otherwise the first k ADC results are
+ * returned with distance sqrt(sum). */
+void vsko_pq_search(const float *q, int64_t nq, const float *codebooks,
+                    const uint8_t *codes, int64_t n, int32_t M, int32_t ksub,
+                    int32_t dsub, int32_t k_adc, int32_t k, const float *x,
+                    int32_t rerank_metric, float *out_dist, int64_t *out_ids,
+                    int32_t nthreads);
+/* ADC sums only: out_sum[i] = sum_m lut[m][codes[i][m]] */
+void vsko_pq_adc_scan(const float *lut, const uint8_t *codes, int64_t n,
+                      int32_t M, int32_t ksub, float *out_sum);
+
+/* ---- k-means (fixture generation only) ---------------------------------- */
+/* Lloyd iterations from the first k rows of a seeded permutation; strict '<'
+ * assignment, empty clusters keep their previous centre. */
+void vsko_kmeans(const float *x, int64_t n, int32_t d, int32_t k,
+                 int32_t iters, uint64_t seed, float *centroids,
+                 int32_t nthreads);
+
+int32_t vsko_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

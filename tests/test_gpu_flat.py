@@ -1,0 +1,189 @@
+"""Flat k-NN on the GPU (libvsk_hip.so) against the CPU oracle.
+
+Float bar: distances within 1e-4 relative, id sets equal except for ties
+within that tolerance.  Manhattan is summed in the oracle's order on the GPU
+too, so its distances and ids must be bit-identical.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from parity import assert_sorted_unique, assert_topk_match, recall
+from vectorstorekit_amd import VSKError, VectorDatabase
+from vectorstorekit_amd._lib import (METRIC_COSINE, METRIC_COSINE_NORMALIZED, METRIC_DOT,
+                                     METRIC_L1, METRIC_L2, METRIC_L2SQ)
+
+pytestmark = pytest.mark.gpu
+
+ALL = [METRIC_L2SQ, METRIC_L2, METRIC_COSINE, METRIC_COSINE_NORMALIZED, METRIC_DOT, METRIC_L1]
+
+
+def _data(seed, n, nq, d, normalize=False):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    if normalize:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+    return x, q
+
+
+def _check(ctx, x, q, k, metric, exact=False):
+    db = VectorDatabase(ctx, x)
+    gd, gi = db.search(q, k, metric)
+    od, oi = O.search_flat(q, x, k, metric)
+    assert_sorted_unique(gd, gi)
+    if exact:
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gd, od)
+    else:
+        assert_topk_match(gd, gi, od, oi,
+                          lambda qi, ids: O.distances(q[qi:qi + 1], x[ids], metric)[0])
+    return gd, gi
+
+
+def test_config1_l2sq_full(ctx):
+    """10,000 x 128 N(0,1), 100 queries, L2^2, k=10."""
+    x, q = _data(1, 10_000, 100, 128)
+    print("config1 L2SQ 10000x128 q100 k10", flush=True)
+    _check(ctx, x, q, 10, METRIC_L2SQ)
+
+
+@pytest.mark.parametrize("metric", ALL)
+@pytest.mark.parametrize("shape", [(1000, 100, 33, 7), (5000, 70, 128, 100), (300, 3, 5, 1)])
+def test_metrics_shapes(ctx, metric, shape):
+    n, nq, d, k = shape
+    x, q = _data(100 + metric, n, nq, d, normalize=metric == METRIC_COSINE_NORMALIZED)
+    print(f"flat metric={metric} n={n} nq={nq} d={d} k={k}", flush=True)
+    _check(ctx, x, q, k, metric, exact=metric == METRIC_L1)
+
+
+def test_chunked_path_large_n(ctx):
+    """n well above the first chunk: exercises the filtered, atomic-append
+    pass and the running thresholds."""
+    x, q = _data(7, 200_000, 130, 64)
+    print("flat chunked n=200000 nq=130 d=64 k=100", flush=True)
+    _check(ctx, x, q, 100, METRIC_L2SQ)
+    _check(ctx, x, q, 32, METRIC_L1, exact=True)
+
+
+def test_overflow_fallback(ctx):
+    """Rows get strictly closer with growing id, so every filtered chunk
+    keeps everything and overflows; the sub-chunk re-scan must still give
+    the exact answer."""
+    n = 120_000
+    x = np.zeros((n, 4), np.float32)
+    x[:, 0] = np.arange(n, dtype=np.float32) / n
+    q = np.array([[2.0, 0, 0, 0], [-1.0, 0, 0, 0]], np.float32)
+    print("flat overflow n=120000", flush=True)
+    db = VectorDatabase(ctx, x)
+    gd, gi = db.search(q, 10, METRIC_L2SQ)
+    od, oi = O.search_flat(q, x, 10, METRIC_L2SQ)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_allclose(gd, od, rtol=1e-4)
+
+
+def test_ties_by_id(ctx):
+    x, q = _data(11, 2000, 5, 16)
+    x[100:110] = x[5]  # 11 identical rows
+    q[:] = x[5]
+    db = VectorDatabase(ctx, x)
+    for metric in (METRIC_L2SQ, METRIC_L1):
+        gd, gi = db.search(q, 11, metric)
+        np.testing.assert_array_equal(gi[0], [5] + list(range(100, 110)))
+
+
+def test_k_larger_than_n_pads(ctx):
+    x, q = _data(12, 50, 4, 8)
+    db = VectorDatabase(ctx, x)
+    gd, gi = db.search(q, 64, METRIC_L2)
+    od, oi = O.search_flat(q, x, 64, METRIC_L2)
+    assert (gi[:, 50:] == -1).all() and np.isinf(gd[:, 50:]).all()
+    assert_topk_match(gd, gi, od, oi, lambda qi, ids: O.distances(q[qi:qi + 1], x[ids], METRIC_L2)[0])
+
+
+def test_distance_matrix(ctx):
+    x, q = _data(13, 777, 9, 40)
+    db = VectorDatabase(ctx, x)
+    for metric in ALL:
+        g = db.distances(q, metric)
+        o = O.distances(q, x, metric)
+        if metric == METRIC_L1:
+            np.testing.assert_array_equal(g, o)
+        else:
+            np.testing.assert_allclose(g, o, rtol=1e-4, atol=2e-4)
+
+
+def test_kat_constant_rows(ctx):
+    """MetalDistance512Tests.swift:50-66 / Vector512Tests.swift:174-204:
+    query 0 vs rows filled with i -> sqrt(512 i^2)."""
+    x = np.stack([np.full(512, i, np.float32) for i in range(100)])
+    db = VectorDatabase(ctx, x)
+    g = db.distances(np.zeros((1, 512), np.float32), METRIC_L2)[0]
+    np.testing.assert_allclose(g, np.sqrt(512.0) * np.arange(100), rtol=1e-5, atol=1e-3)
+    g1 = db.distances(np.zeros((1, 512), np.float32), METRIC_L1)[0]
+    np.testing.assert_array_equal(g1, 512.0 * np.arange(100))
+
+
+def test_errors(ctx):
+    x, q = _data(14, 100, 3, 8)
+    db = VectorDatabase(ctx, x)
+    with pytest.raises(VSKError) as e:
+        db.search(q, 2000, METRIC_L2)
+    assert e.value.kind == "invalidBufferSize"
+    with pytest.raises(VSKError) as e:
+        db.search(q, 5, 42)
+    assert e.value.kind == "invalidArgument"
+    with pytest.raises(VSKError) as e:
+        db.search(q[:0], 5, METRIC_L2)
+    assert e.value.kind == "emptyInput"
+    with pytest.raises(VSKError) as e:
+        VectorDatabase(ctx, x[:0])
+    assert e.value.kind == "emptyInput"
+
+
+def test_device_tensors(ctx):
+    """Inputs/outputs as torch device tensors take the zero-copy path."""
+    import torch
+
+    x, q = _data(15, 3000, 17, 64)
+    xt, qt = torch.from_numpy(x).cuda(), torch.from_numpy(q).cuda()
+    db = VectorDatabase(ctx, xt)
+    gd, gi = db.search(qt, 20, METRIC_COSINE)
+    assert gd.is_cuda and gi.is_cuda
+    hd, hi = VectorDatabase(ctx, x).search(q, 20, METRIC_COSINE)
+    np.testing.assert_array_equal(gi.cpu().numpy(), hi)
+    np.testing.assert_array_equal(gd.cpu().numpy(), hd)
+
+
+def test_config2_cosine_full_size(ctx):
+    """BASELINE config 2 at full size: 1,000,000 x 768 unit-norm rows; parity
+    of 24 queries against the oracle, recall@100 of 200 queries equal to
+    the oracle's, and size-independent properties over all 10,000."""
+    import torch
+
+    n, d, nq, k = 1_000_000, 768, 10_000, 100
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    x = torch.randn(n, d, generator=g, device="cuda")
+    x /= x.norm(dim=1, keepdim=True)
+    g.manual_seed(2)
+    q = torch.randn(nq, d, generator=g, device="cuda")
+    q /= q.norm(dim=1, keepdim=True)
+    print("config2 cosine 1Mx768 q10000 k100", flush=True)
+    db = VectorDatabase(ctx, x)
+    gd, gi = db.search(q, k, METRIC_COSINE_NORMALIZED)
+    gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
+    assert_sorted_unique(gd, gi)
+    assert (gi >= 0).all() and (gi < n).all()
+    xh, qh = x.cpu().numpy(), q.cpu().numpy()
+    sub = 24
+    od, oi = O.search_flat(qh[:sub], xh, k, METRIC_COSINE_NORMALIZED)
+    assert_topk_match(gd[:sub], gi[:sub], od, oi,
+                      lambda qi, ids: O.distances(qh[qi:qi + 1], xh[ids], METRIC_COSINE_NORMALIZED)[0])
+    assert recall(gi[:sub], oi) == pytest.approx(1.0, abs=1e-3)
+    # the GPU's distances are the oracle's distances of the returned ids
+    some = np.random.default_rng(0).choice(nq, 8, replace=False)
+    for qi in some:
+        ref = O.distances(qh[qi:qi + 1], xh[gi[qi]], METRIC_COSINE_NORMALIZED)[0]
+        np.testing.assert_allclose(gd[qi], ref, rtol=1e-4, atol=1e-4)

@@ -1,0 +1,438 @@
+// core.hip -- context, staging of caller buffers, event profiling, small
+// utility kernels (fills, row norms, key decoding) and the flat database.
+#include <cstring>
+
+#include "vsk_api.hpp"
+#include "vsk_core.hpp"
+
+namespace vsk {
+
+[[noreturn]] void fail(vsk_status code, const std::string &msg) {
+  throw Error{code, msg};
+}
+
+void check_hip(hipError_t e, const char *what, const char *file, int line) {
+  if (e == hipSuccess) return;
+  char buf[512];
+  snprintf(buf, sizeof buf, "%s failed: %s (%s:%d)", what, hipGetErrorString(e),
+           file, line);
+  vsk_status code = VSK_ERR_EXECUTION_FAILED;
+  if (e == hipErrorOutOfMemory) code = VSK_ERR_OUT_OF_MEMORY;
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+    code = VSK_ERR_DEVICE_NOT_AVAILABLE;
+  fail(code, buf);
+}
+
+DevBuf::~DevBuf() { release(); }
+void DevBuf::release() {
+  if (p) (void)hipFree(p);
+  p = nullptr;
+  bytes = 0;
+}
+void DevBuf::reserve(size_t b) {
+  if (b <= bytes && p) return;
+  release();
+  size_t want = b ? b : 1;
+  hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    p = nullptr;
+    fail(VSK_ERR_OUT_OF_MEMORY,
+         "device allocation of " + std::to_string(want) + " bytes failed");
+  }
+  bytes = want;
+}
+
+bool is_device_ptr(const void *p) {
+  if (!p) return false;
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice;
+}
+
+CallScope::CallScope(vsk_ctx *c) : ctx(c) {
+  VSK_HIP(hipEventRecord(ctx->call_begin, ctx->stream));
+}
+void CallScope::finish() {
+  VSK_HIP(hipEventRecord(ctx->call_end, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  float ms = 0.f;
+  VSK_HIP(hipEventElapsedTime(&ms, ctx->call_begin, ctx->call_end));
+  ctx->last_ms = ms;
+  ctx->resolve_pending();
+}
+
+KernelTimer::KernelTimer(vsk_ctx *c, const char *name) : ctx(c) {
+  if (!ctx->profile) return;
+  auto it = ctx->stat_index.find(name);
+  if (it == ctx->stat_index.end()) {
+    vsk_kernel_stat s;
+    memset(&s, 0, sizeof s);
+    snprintf(s.name, sizeof s.name, "%s", name);
+    ctx->stats.push_back(s);
+    it = ctx->stat_index.emplace(name, (int)ctx->stats.size() - 1).first;
+  }
+  stat = it->second;
+  a = ctx->take_event();
+  VSK_HIP(hipEventRecord(a, ctx->stream));
+}
+KernelTimer::~KernelTimer() {
+  if (stat < 0) return;
+  hipEvent_t b = ctx->take_event();
+  if (hipEventRecord(b, ctx->stream) == hipSuccess)
+    ctx->pending.push_back({stat, a, b});
+}
+
+void check_launch(const char *name) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    fail(VSK_ERR_EXECUTION_FAILED,
+         std::string("launch of ") + name + " failed: " + hipGetErrorString(e));
+}
+
+const void *input_to_device(vsk_ctx *ctx, const void *p, size_t bytes,
+                            const std::string &slot) {
+  if (bytes == 0 || is_device_ptr(p)) return p;
+  void *d = ctx->scratch_ptr(slot, bytes);
+  VSK_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, ctx->stream));
+  return d;
+}
+
+OutputStage::OutputStage(vsk_ctx *c, void *user_ptr, size_t nbytes,
+                         const std::string &slot)
+    : ctx(c), user(user_ptr), bytes(nbytes) {
+  host = !is_device_ptr(user_ptr);
+  dev = host ? ctx->scratch_ptr(slot, nbytes) : user_ptr;
+}
+void OutputStage::copy_back() {
+  if (host && bytes)
+    VSK_HIP(hipMemcpyAsync(user, dev, bytes, hipMemcpyDeviceToHost,
+                           ctx->stream));
+}
+
+const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
+                                   int32_t d, int32_t ld,
+                                   const std::string &slot) {
+  if (rows == 0) return nullptr;
+  bool dev = is_device_ptr(p);
+  if (dev && ld == d) return p;
+  float *out = static_cast<float *>(
+      ctx->scratch_ptr(slot, sizeof(float) * (size_t)rows * ld));
+  if (ld != d)
+    fill_i32(ctx, reinterpret_cast<int32_t *>(out), rows * (int64_t)ld, 0);
+  VSK_HIP(hipMemcpy2DAsync(out, sizeof(float) * ld, p, sizeof(float) * d,
+                           sizeof(float) * d, rows,
+                           dev ? hipMemcpyDeviceToDevice
+                               : hipMemcpyHostToDevice,
+                           ctx->stream));
+  return out;
+}
+
+bool metric_valid(int32_t m) {
+  return m >= VSK_METRIC_L2SQ && m <= VSK_METRIC_L1;
+}
+
+// ---------------------------------------------------------------------------
+// utility kernels
+// ---------------------------------------------------------------------------
+__global__ void k_fill_u64(uint64_t *p, int64_t n, uint64_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+__global__ void k_fill_i32(int32_t *p, int64_t n, int32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+static unsigned fill_grid(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 4096 ? (g > 0 ? g : 1) : 4096);
+}
+void fill_u64(vsk_ctx *ctx, uint64_t *p, int64_t n, uint64_t v) {
+  if (n <= 0) return;
+  k_fill_u64<<<fill_grid(n), 256, 0, ctx->stream>>>(p, n, v);
+  check_launch("fill_u64");
+}
+void fill_i32(vsk_ctx *ctx, int32_t *p, int64_t n, int32_t v) {
+  if (n <= 0) return;
+  k_fill_i32<<<fill_grid(n), 256, 0, ctx->stream>>>(p, n, v);
+  check_launch("fill_i32");
+}
+
+// one wave per row: lane-strided partial sums, then a butterfly reduction
+__global__ __launch_bounds__(256) void k_row_norms(const float *x, int64_t n,
+                                                   int32_t d, int32_t ld,
+                                                   float *sq, float *nrm) {
+  const int lane = threadIdx.x & 63;
+  int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const float *r = x + row * ld;
+  float s = 0.f;
+  for (int j = lane; j < d; j += 64) s += r[j] * r[j];
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) {
+    if (sq) sq[row] = s;
+    if (nrm) nrm[row] = sqrtf(s);
+  }
+}
+void row_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
+               float *sq, float *nrm) {
+  if (n <= 0) return;
+  k_row_norms<<<(unsigned)ceil_div(n, 4), 256, 0, ctx->stream>>>(x, n, d, ld,
+                                                                   sq, nrm);
+  check_launch("row_norms");
+}
+
+// x <- x / (|x| + 1e-8), as normalizeVectors
+// (Acceleration/Metal/Shaders/DistanceShaders.metal:403-429)
+__global__ __launch_bounds__(256) void k_normalize_rows(float *x, int64_t n,
+                                                       int32_t d, int32_t ld) {
+  const int lane = threadIdx.x & 63;
+  int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  float *r = x + row * ld;
+  float s = 0.f;
+  for (int j = lane; j < d; j += 64) s += r[j] * r[j];
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  float inv = 1.0f / (sqrtf(s) + 1e-8f);
+  for (int j = lane; j < d; j += 64) r[j] = r[j] * inv;
+}
+
+// decode composite keys into (distance, id) outputs
+__global__ void k_decode_f32(const uint64_t *best, int64_t total, int32_t mode,
+                             const int64_t *id_map, float *out_dist,
+                             int64_t *out_ids) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    uint64_t key = best[i];
+    if (key == VSK_KEY_NONE) {
+      out_dist[i] = __int_as_float(0x7f800000);
+      out_ids[i] = -1;
+      continue;
+    }
+    float dist = vsk_ord2f((uint32_t)(key >> 32));
+    if (mode == 1) dist = __fsqrt_rn(fmaxf(dist, 0.f));
+    uint32_t tie = (uint32_t)key;
+    out_dist[i] = dist;
+    out_ids[i] = id_map ? id_map[tie] : (int64_t)tie;
+  }
+}
+void decode_keys(vsk_ctx *ctx, const uint64_t *best, int64_t total,
+                 bool sqrt_out, const int64_t *id_map, float *out_dist,
+                 int64_t *out_ids) {
+  if (total <= 0) return;
+  KernelTimer t(ctx, "decode_keys");
+  k_decode_f32<<<fill_grid(total), 256, 0, ctx->stream>>>(
+      best, total, sqrt_out ? 1 : 0, id_map, out_dist, out_ids);
+  check_launch("decode_keys");
+}
+
+}  // namespace vsk
+
+// ---------------------------------------------------------------------------
+// vsk_ctx members
+// ---------------------------------------------------------------------------
+void *vsk_ctx::scratch_ptr(const std::string &key, size_t bytes) {
+  auto &b = scratch[key];
+  if (!b) b.reset(new vsk::DevBuf());
+  if (b->bytes < bytes || !b->p) {
+    // a buffer in use by queued work must not be freed under it
+    VSK_HIP(hipStreamSynchronize(stream));
+    b->reserve(bytes + bytes / 8);
+  }
+  return b->p;
+}
+hipEvent_t vsk_ctx::take_event() {
+  if (!event_pool.empty()) {
+    hipEvent_t e = event_pool.back();
+    event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  VSK_HIP(hipEventCreate(&e));
+  return e;
+}
+void vsk_ctx::resolve_pending() {
+  for (auto &p : pending) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      stats[p.stat].launches += 1;
+      stats[p.stat].total_ms += ms;
+    }
+    event_pool.push_back(p.a);
+    event_pool.push_back(p.b);
+  }
+  pending.clear();
+}
+
+// ---------------------------------------------------------------------------
+// C ABI: context, profiling, flat database
+// ---------------------------------------------------------------------------
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_create(int32_t device, vsk_ctx **out) {
+  if (!out) return VSK_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    (void)hipGetLastError();
+    return VSK_ERR_DEVICE_NOT_AVAILABLE;
+  }
+  if (device < 0 || device >= count) return VSK_ERR_DEVICE_NOT_AVAILABLE;
+  if (hipSetDevice(device) != hipSuccess) return VSK_ERR_DEVICE_NOT_AVAILABLE;
+  vsk_ctx *c = new vsk_ctx();
+  c->device = device;
+  // a blocking stream: it orders itself after work on the null stream, so
+  // device buffers produced there (e.g. by torch) are complete when read
+  if (hipStreamCreate(&c->stream) != hipSuccess ||
+      hipEventCreate(&c->call_begin) != hipSuccess ||
+      hipEventCreate(&c->call_end) != hipSuccess) {
+    delete c;
+    return VSK_ERR_DEVICE_NOT_AVAILABLE;
+  }
+  *out = c;
+  return VSK_OK;
+}
+
+vsk_status vsk_destroy(vsk_ctx *ctx) {
+  if (!ctx) return VSK_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  ctx->resolve_pending();
+  for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
+  ctx->scratch.clear();
+  (void)hipEventDestroy(ctx->call_begin);
+  (void)hipEventDestroy(ctx->call_end);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return VSK_OK;
+}
+
+const char *vsk_last_error(const vsk_ctx *ctx) {
+  return ctx ? ctx->last_error.c_str() : "null context";
+}
+void *vsk_stream(vsk_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+float vsk_last_kernel_ms(const vsk_ctx *ctx) { return ctx ? ctx->last_ms : 0.f; }
+
+vsk_status vsk_device_info(vsk_ctx *ctx, vsk_caps *caps) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(caps, VSK_ERR_INVALID_ARGUMENT, "caps is null");
+  hipDeviceProp_t p;
+  VSK_HIP(hipGetDeviceProperties(&p, ctx->device));
+  memset(caps, 0, sizeof *caps);
+  snprintf(caps->name, sizeof caps->name, "%s", p.name);
+  snprintf(caps->arch, sizeof caps->arch, "%s", p.gcnArchName);
+  caps->device = ctx->device;
+  caps->compute_units = p.multiProcessorCount;
+  caps->wavefront_size = p.warpSize;
+  caps->lds_bytes_per_block = (int32_t)p.sharedMemPerBlock;
+  caps->global_mem_bytes = (int64_t)p.totalGlobalMem;
+  caps->clock_khz = p.clockRate;
+  caps->memory_clock_khz = p.memoryClockRate;
+  caps->memory_bus_width_bits = p.memoryBusWidth;
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on) {
+  if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
+  ctx->profile = on != 0;
+  return VSK_OK;
+}
+vsk_status vsk_profile_reset(vsk_ctx *ctx) {
+  if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
+  ctx->stats.clear();
+  ctx->stat_index.clear();
+  return VSK_OK;
+}
+int32_t vsk_profile_count(const vsk_ctx *ctx) {
+  return ctx ? (int32_t)ctx->stats.size() : 0;
+}
+vsk_status vsk_profile_get(const vsk_ctx *ctx, int32_t i,
+                           vsk_kernel_stat *out) {
+  if (!ctx || !out || i < 0 || i >= (int32_t)ctx->stats.size())
+    return VSK_ERR_INVALID_ARGUMENT;
+  *out = ctx->stats[i];
+  return VSK_OK;
+}
+
+vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                             int32_t flags, vsk_db **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "database has no rows");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(x, VSK_ERR_INVALID_ARGUMENT, "x is null");
+  VSK_REQUIRE(n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "a database holds at most 2^31-1 rows");
+  VSK_REQUIRE((flags & ~VSK_DB_NORMALIZE) == 0, VSK_ERR_INVALID_ARGUMENT,
+              "unknown flags");
+  std::unique_ptr<vsk_db> db(new vsk_db());
+  db->n = n;
+  db->d = d;
+  db->ld = padded_ld(d);
+  CallScope cs(ctx);
+  db->x.reserve(sizeof(float) * (size_t)n * db->ld);
+  if (db->ld != d)
+    fill_i32(ctx, db->x.as<int32_t>(), n * (int64_t)db->ld, 0);
+  bool dev = is_device_ptr(x);
+  VSK_HIP(hipMemcpy2DAsync(db->x.p, sizeof(float) * db->ld, x,
+                           sizeof(float) * d, sizeof(float) * d, n,
+                           dev ? hipMemcpyDeviceToDevice
+                               : hipMemcpyHostToDevice,
+                           ctx->stream));
+  if (flags & VSK_DB_NORMALIZE) {
+    k_normalize_rows<<<(unsigned)ceil_div(n, 4), 256, 0, ctx->stream>>>(
+        db->x.as<float>(), n, d, db->ld);
+    check_launch("normalize_rows");
+  }
+  db->sqnorm.reserve(sizeof(float) * n);
+  db->norm.reserve(sizeof(float) * n);
+  row_norms(ctx, db->x.as<float>(), n, d, db->ld, db->sqnorm.as<float>(),
+            db->norm.as<float>());
+  cs.finish();
+  *out = db.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_db_free(vsk_ctx *ctx, vsk_db *db) {
+  if (ctx) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+  }
+  delete db;
+  return VSK_OK;
+}
+
+vsk_status vsk_db_info(const vsk_db *db, int64_t *n, int32_t *d) {
+  if (!db) return VSK_ERR_INVALID_ARGUMENT;
+  if (n) *n = db->n;
+  if (d) *d = db->d;
+  return VSK_OK;
+}
+
+vsk_status vsk_db_read_f32(vsk_ctx *ctx, const vsk_db *db, int64_t row0,
+                           int64_t count, float *out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db && out, VSK_ERR_INVALID_ARGUMENT, "null argument");
+  VSK_REQUIRE(row0 >= 0 && count >= 0 && row0 + count <= db->n,
+              VSK_ERR_INVALID_ARGUMENT, "row range out of bounds");
+  if (count == 0) return VSK_OK;
+  CallScope cs(ctx);
+  bool dev = is_device_ptr(out);
+  VSK_HIP(hipMemcpy2DAsync(
+      out, sizeof(float) * db->d, db->x.as<float>() + row0 * db->ld,
+      sizeof(float) * db->ld, sizeof(float) * db->d, count,
+      dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, ctx->stream));
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

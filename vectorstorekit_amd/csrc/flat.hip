@@ -1,0 +1,449 @@
+// flat.hip -- flat (brute-force) k-NN: query x row distances on fp32 MFMA
+// (L2^2 / L2 / cosine / normalised cosine / dot) or on the VALU (Manhattan),
+// fused with the filter/append stage of the progressive top-k, so no
+// query x row distance matrix is written to HBM.
+//
+// Reference: the batched distance kernels batchEuclideanDistance /
+// batchCosineDistance / batchManhattanDistance / batchDotProduct
+// (Acceleration/Metal/Shaders/DistanceShaders.metal:248-379, one thread per
+// (query, row) pair) and their host side
+// MetalAccelerationEngine.batchComputeDistancesGPU
+// (Acceleration/MetalAccelerationEngine.swift:377-478), which reads back the
+// full matrix and sorts each row on the CPU.
+//
+// MFMA kernel: a workgroup owns 64 queries and a contiguous slice of rows,
+// walks the slice in tiles of 128 rows; each of its 4 waves computes a
+// 32-row x 64-query block as 2x4 v_mfma_f32_16x16x4f32 tiles, with both
+// operands staged through LDS in 32-dim stages.  Distances follow from the
+// dot product and precomputed norms:
+//   L2^2 = |q|^2 + |x|^2 - 2 q.x       cosine = 1 - q.x / (|q||x| + 1e-8)
+//   normalised cosine = 1 - q.x        dot = -q.x
+#include "vsk_api.hpp"
+
+namespace vsk {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int FB_N = 128;  // rows per tile
+constexpr int FB_Q = 64;   // queries per workgroup
+constexpr int FB_K = 32;   // dims per LDS stage
+constexpr int FS = FB_K + 2;  // LDS row stride (floats): conflict-free MFMA reads
+
+enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2 };
+
+struct FlatArgs {
+  const float *X;
+  int64_t ldx;
+  const float *Q;
+  int64_t ldq;
+  const float *xaux;  // |x|^2 (L2), |x| (cosine), else null
+  const float *qaux;  // same for queries
+  int32_t kdim;       // padded dimension (multiple of 4)
+  int32_t nq;
+  int64_t r0, r1;
+  int64_t rows_per_split;
+  int32_t metric;
+  const uint64_t *thresh;
+  const uint8_t *active;
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+  float *mat;  // MODE_MATRIX output, row-major nq x ldm
+  int64_t ldm;
+};
+
+__device__ inline float metric_from_dot(int metric, float dot, float qa,
+                                        float xa) {
+  switch (metric) {
+  case VSK_METRIC_L2SQ:
+  case VSK_METRIC_L2:
+    return fmaxf(qa + xa - 2.0f * dot, 0.0f);
+  case VSK_METRIC_COSINE:
+    return 1.0f - dot / (qa * xa + 1e-8f);
+  case VSK_METRIC_COSINE_NORMALIZED:
+    return 1.0f - dot;
+  default:  // VSK_METRIC_DOT
+    return -dot;
+  }
+}
+
+// one (query, row, distance) result of a tile
+template <int MODE>
+__device__ inline void emit(const FlatArgs &a, int64_t qi, int64_t row,
+                            float dist, uint64_t th) {
+  if (MODE == MODE_MATRIX) {
+    a.mat[qi * a.ldm + row] =
+        a.metric == VSK_METRIC_L2 ? __fsqrt_rn(dist) : dist;
+  } else {
+    uint64_t key = vsk_key(dist, (uint32_t)row);
+    if (MODE == MODE_DENSE) {
+      a.cand[qi * a.cap + (row - a.r0)] = key;
+    } else if (key <= th) {
+      int slot = atomicAdd(&a.counts[qi], 1);
+      if (slot < a.cap) a.cand[qi * a.cap + slot] = key;
+    }
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
+  __shared__ float xs[FB_N * FS];
+  __shared__ float qs[FB_Q * FS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t q0 = (int64_t)blockIdx.x * FB_Q;
+  const int64_t s0 = a.r0 + (int64_t)blockIdx.y * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+
+  // the 4 queries this lane's accumulators belong to
+  int64_t qi[4];
+  bool qok[4];
+  uint64_t th[4];
+  float qa[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    qi[j] = q0 + j * 16 + (lane & 15);
+    qok[j] = qi[j] < a.nq && (!a.active || a.active[qi[j]]);
+    th[j] = (MODE == MODE_FILTER && qok[j]) ? a.thresh[qi[j]] : 0;
+    qa[j] = (a.qaux && qi[j] < a.nq) ? a.qaux[qi[j]] : 0.f;
+  }
+  // global->LDS copy assignment: 8 threads per 32-float row segment
+  const int crow = tid >> 3, ccol = (tid & 7) * 4;
+
+  for (int64_t t0 = s0; t0 < s1; t0 += FB_N) {
+    f4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    f4 xr[4], qr[2];
+    auto gload = [&](int k0) {
+      const bool kin = k0 + ccol < a.kdim;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int64_t grow = t0 + u * 32 + crow;
+        xr[u] = (kin && grow < s1)
+                    ? *reinterpret_cast<const f4 *>(a.X + grow * a.ldx + k0 +
+                                                    ccol)
+                    : f4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        int64_t gq = q0 + u * 32 + crow;
+        qr[u] = (kin && gq < a.nq)
+                    ? *reinterpret_cast<const f4 *>(a.Q + gq * a.ldq + k0 +
+                                                    ccol)
+                    : f4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    gload(0);
+    for (int k0 = 0; k0 < a.kdim; k0 += FB_K) {
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float *p = xs + (u * 32 + crow) * FS + ccol;
+        p[0] = xr[u].x;
+        p[1] = xr[u].y;
+        p[2] = xr[u].z;
+        p[3] = xr[u].w;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float *p = qs + (u * 32 + crow) * FS + ccol;
+        p[0] = qr[u].x;
+        p[1] = qr[u].y;
+        p[2] = qr[u].z;
+        p[3] = qr[u].w;
+      }
+      __syncthreads();
+      if (k0 + FB_K < a.kdim) gload(k0 + FB_K);
+#pragma unroll
+      for (int kk = 0; kk < FB_K; kk += 4) {
+        float af[2], bf[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          af[i] = xs[(w * 32 + i * 16 + (lane & 15)) * FS + kk + (lane >> 4)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bf[j] = qs[(j * 16 + (lane & 15)) * FS + kk + (lane >> 4)];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j],
+                                                             acc[i][j], 0, 0,
+                                                             0);
+      }
+    }
+    // epilogue: D[row = 4*(lane/16) + r][query = lane%16] of each tile
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = t0 + w * 32 + i * 16 + 4 * (lane >> 4) + r;
+        if (row >= s1) continue;
+        const float xa = a.xaux ? a.xaux[row] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!qok[j]) continue;
+          float dist = metric_from_dot(a.metric, acc[i][j][r], qa[j], xa);
+          emit<MODE>(a, qi[j], row, dist, th[j]);
+        }
+      }
+    }
+  }
+}
+
+// Manhattan on the VALU.  Thread (tid) owns rows (tid%32)+32u, u<4, and
+// queries (tid/32)+8v, v<8; every |q-x| term is added in dimension order,
+// the order of the reference's per-candidate vDSP loop
+// (Acceleration/AccelerateOptimizer.swift:322-360).
+constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_flat_l1(FlatArgs a) {
+  __shared__ float xs[FB_N * LS];
+  __shared__ float qs[FB_Q * LS];
+  const int tid = threadIdx.x;
+  const int64_t q0 = (int64_t)blockIdx.x * FB_Q;
+  const int64_t s0 = a.r0 + (int64_t)blockIdx.y * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+  const int rsub = tid & 31, qsub = tid >> 5;
+  int64_t qi[8];
+  bool qok[8];
+  uint64_t th[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    qi[v] = q0 + qsub + 8 * v;
+    qok[v] = qi[v] < a.nq && (!a.active || a.active[qi[v]]);
+    th[v] = (MODE == MODE_FILTER && qok[v]) ? a.thresh[qi[v]] : 0;
+  }
+  const int crow = tid >> 3, ccol = (tid & 7) * 4;
+  for (int64_t t0 = s0; t0 < s1; t0 += FB_N) {
+    float acc[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) acc[u][v] = 0.f;
+    for (int k0 = 0; k0 < a.kdim; k0 += FB_K) {
+      const bool kin = k0 + ccol < a.kdim;
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int64_t grow = t0 + u * 32 + crow;
+        f4 v = (kin && grow < s1)
+                   ? *reinterpret_cast<const f4 *>(a.X + grow * a.ldx + k0 +
+                                                   ccol)
+                   : f4{0.f, 0.f, 0.f, 0.f};
+        float *p = xs + (u * 32 + crow) * LS + ccol;
+        p[0] = v.x;
+        p[1] = v.y;
+        p[2] = v.z;
+        p[3] = v.w;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        int64_t gq = q0 + u * 32 + crow;
+        f4 v = (kin && gq < a.nq)
+                   ? *reinterpret_cast<const f4 *>(a.Q + gq * a.ldq + k0 +
+                                                   ccol)
+                   : f4{0.f, 0.f, 0.f, 0.f};
+        float *p = qs + (u * 32 + crow) * LS + ccol;
+        p[0] = v.x;
+        p[1] = v.y;
+        p[2] = v.z;
+        p[3] = v.w;
+      }
+      __syncthreads();
+      const int kend = a.kdim - k0 < FB_K ? a.kdim - k0 : FB_K;
+      for (int kk = 0; kk < kend; ++kk) {
+        float xv[4], qv[8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xv[u] = xs[(rsub + 32 * u) * LS + kk];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) qv[v] = qs[(qsub + 8 * v) * LS + kk];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 8; ++v) acc[u][v] += fabsf(qv[v] - xv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t row = t0 + rsub + 32 * u;
+      if (row >= s1) continue;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        if (!qok[v]) continue;
+        emit<MODE>(a, qi[v], row, acc[u][v], th[v]);
+      }
+    }
+  }
+}
+
+// grid: query tiles x row splits, enough workgroups to fill 256 CUs
+static void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode) {
+  const int64_t rows = a.r1 - a.r0;
+  if (rows <= 0 || a.nq <= 0) return;
+  const int64_t qt = ceil_div(a.nq, FB_Q);
+  int64_t splits = ceil_div(4096, qt);
+  const int64_t max_splits = ceil_div(rows, FB_N);
+  if (splits > max_splits) splits = max_splits;
+  if (splits > 65535) splits = 65535;
+  if (splits < 1) splits = 1;
+  a.rows_per_split = ceil_div(ceil_div(rows, splits), FB_N) * FB_N;
+  splits = ceil_div(rows, a.rows_per_split);
+  dim3 grid((unsigned)qt, (unsigned)splits);
+  const bool l1 = a.metric == VSK_METRIC_L1;
+  const char *name = l1 ? (mode == MODE_MATRIX ? "flat_l1_matrix"
+                                               : "flat_l1_scan")
+                        : (mode == MODE_MATRIX ? "flat_mfma_matrix"
+                                               : "flat_mfma_scan");
+  KernelTimer t(ctx, name);
+  if (l1) {
+    if (mode == MODE_DENSE)
+      k_flat_l1<MODE_DENSE><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (mode == MODE_FILTER)
+      k_flat_l1<MODE_FILTER><<<grid, 256, 0, ctx->stream>>>(a);
+    else
+      k_flat_l1<MODE_MATRIX><<<grid, 256, 0, ctx->stream>>>(a);
+  } else {
+    if (mode == MODE_DENSE)
+      k_flat_mfma<MODE_DENSE><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (mode == MODE_FILTER)
+      k_flat_mfma<MODE_FILTER><<<grid, 256, 0, ctx->stream>>>(a);
+    else
+      k_flat_mfma<MODE_MATRIX><<<grid, 256, 0, ctx->stream>>>(a);
+  }
+  check_launch(name);
+}
+
+static const float *x_aux(const vsk_db *db, int32_t metric) {
+  if (metric == VSK_METRIC_L2SQ || metric == VSK_METRIC_L2)
+    return db->sqnorm.as<float>();
+  if (metric == VSK_METRIC_COSINE) return db->norm.as<float>();
+  return nullptr;
+}
+
+static float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                    int32_t ld, int32_t metric) {
+  if (metric != VSK_METRIC_L2SQ && metric != VSK_METRIC_L2 &&
+      metric != VSK_METRIC_COSINE)
+    return nullptr;
+  float *aux = static_cast<float *>(ctx->scratch_ptr("flat.qaux", 4 * nq));
+  if (metric == VSK_METRIC_COSINE)
+    row_norms(ctx, dq, nq, d, ld, nullptr, aux);
+  else
+    row_norms(ctx, dq, nq, d, ld, aux, nullptr);
+  return aux;
+}
+
+// top-k over a resident database for queries already on the device
+void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+                      int64_t nq, int32_t k, int32_t metric, uint64_t *best) {
+  const int64_t cap = default_cap(k);
+  const int64_t qb = query_batch(nq, cap);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    const float *qbat = dq + b0 * db->ld;
+    float *qa = q_aux(ctx, qbat, nb, db->d, db->ld, metric);
+    FlatArgs base{};
+    base.X = db->x.as<float>();
+    base.ldx = db->ld;
+    base.Q = qbat;
+    base.ldq = db->ld;
+    base.xaux = x_aux(db, metric);
+    base.qaux = qa;
+    base.kdim = db->ld;
+    base.nq = (int32_t)nb;
+    base.metric = metric;
+    ScanFn scan = [&](const ScanRequest &r) {
+      FlatArgs a = base;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER);
+    };
+    progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k,
+                     "flat_select");
+  }
+}
+
+}  // namespace vsk
+
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                           int64_t nq, int32_t k, int32_t metric,
+                           float *out_dist, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db, VSK_ERR_INVALID_ARGUMENT, "db is null");
+  VSK_REQUIRE(metric_valid(metric), VSK_ERR_INVALID_ARGUMENT,
+              "unknown metric");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE,
+              "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "too many queries");
+  CallScope cs(ctx);
+  const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("flat.best", sizeof(uint64_t) * (size_t)nq * k));
+  flat_topk_device(ctx, db, dq, nq, k, metric, best);
+  OutputStage od(ctx, out_dist, sizeof(float) * (size_t)nq * k, "out.dist");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * (size_t)nq * k, "out.ids");
+  decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2, nullptr,
+              od.ptr<float>(), oi.ptr<int64_t>());
+  od.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                         int64_t nq, int32_t metric, float *out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db, VSK_ERR_INVALID_ARGUMENT, "db is null");
+  VSK_REQUIRE(metric_valid(metric), VSK_ERR_INVALID_ARGUMENT,
+              "unknown metric");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && out, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "too many queries");
+  CallScope cs(ctx);
+  const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
+  OutputStage om(ctx, out, sizeof(float) * (size_t)nq * db->n, "out.matrix");
+  FlatArgs a{};
+  a.X = db->x.as<float>();
+  a.ldx = db->ld;
+  a.Q = dq;
+  a.ldq = db->ld;
+  a.xaux = x_aux(db, metric);
+  a.qaux = q_aux(ctx, dq, nq, db->d, db->ld, metric);
+  a.kdim = db->ld;
+  a.nq = (int32_t)nq;
+  a.r0 = 0;
+  a.r1 = db->n;
+  a.metric = metric;
+  a.mat = om.ptr<float>();
+  a.ldm = db->n;
+  launch_flat(ctx, a, MODE_MATRIX);
+  om.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

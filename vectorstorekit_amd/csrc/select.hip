@@ -1,0 +1,255 @@
+// select.hip -- exact k-smallest selection over composite (distance, tie)
+// keys, one workgroup per query, and the progressive chunked driver that
+// keeps the full query x row distance matrix out of HBM.
+//
+// The reference selects on the CPU after reading back the whole distance
+// matrix (Acceleration/MetalAccelerationEngine.swift:457-477) with a stable
+// sort + prefix(k) (Indexes/IVFIndex.swift:175-176).  Here every distance
+// carries its tie key in the low 32 bits, so all keys of a query are
+// distinct and "the k smallest keys" is exactly the stable-sort prefix.
+//
+// Selection is a most-significant-digit radix select: 8 passes of 8-bit
+// digits at most, each a 256-bin LDS histogram of the keys that still match
+// the resolved prefix; it stops early as soon as the bucket holding the
+// k-th key is taken whole.  The <= k winners are gathered into LDS and
+// bitonic-sorted (at most 1024 of them).
+#include "vsk_api.hpp"
+
+namespace vsk {
+
+constexpr int SEL_THREADS = 256;
+
+__device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np,
+                                    const uint64_t *C, int64_t i) {
+  return i < np ? P[i] : C[i - np];
+}
+
+__global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  if (a.active && !a.active[q]) return;
+
+  const int32_t k = a.k;
+  const uint64_t *P = a.prev ? a.prev + q * (int64_t)k : nullptr;
+  const int64_t np = P ? k : 0;
+  int64_t base = a.seg_off ? a.seg_off[q] : q * a.cap;
+  int64_t cnt = a.counts ? (int64_t)a.counts[q]
+                         : (a.seg_off ? a.seg_off[q + 1] - base : a.cap);
+  bool overflow = false;
+  if (a.counts && !a.seg_off && cnt > a.cap) {
+    overflow = true;
+    cnt = a.cap;
+  }
+  if (overflow) {
+    if (tid == 0) {
+      if (a.overflow_mask) a.overflow_mask[q] = 1;
+      if (a.overflow_count) atomicAdd(a.overflow_count, 1);
+    }
+    return;
+  }
+  const uint64_t *C = a.cand + base;
+  const int64_t total = np + cnt;
+
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t sel[VSK_MAX_K];
+  __shared__ int sh_bucket, sh_take_all;
+  __shared__ uint32_t sh_before, sh_bcount;
+  __shared__ int sel_count;
+
+  uint64_t prefix = 0, mask = 0, T = VSK_KEY_NONE;
+  int64_t need = k;
+  bool take_all = false;
+
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += SEL_THREADS) hist[i] = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < total; i += SEL_THREADS) {
+      uint64_t key = sel_elem(P, np, C, i);
+      if (key != VSK_KEY_NONE && (key & mask) == prefix)
+        atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1],
+               h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+      uint32_t s = h0 + h1 + h2 + h3;
+      uint32_t incl = s;
+      for (int o = 1; o < 64; o <<= 1) {
+        uint32_t v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      uint32_t all = __shfl(incl, 63);
+      uint32_t excl = incl - s;
+      if (shift == 56 && all <= (uint32_t)k) {
+        if (lane == 0) sh_take_all = 1;
+      } else {
+        if (lane == 0) sh_take_all = 0;
+        bool here = excl < (uint64_t)need && (uint64_t)need <= incl;
+        if (here) {
+          uint32_t hs[4] = {h0, h1, h2, h3};
+          uint32_t before = excl;
+          int j = 0;
+          while (before + hs[j] < (uint64_t)need) {
+            before += hs[j];
+            ++j;
+          }
+          sh_bucket = 4 * lane + j;
+          sh_before = before;
+          sh_bcount = hs[j];
+        }
+      }
+    }
+    __syncthreads();
+    if (sh_take_all) {
+      take_all = true;
+      break;
+    }
+    const uint32_t b = (uint32_t)sh_bucket;
+    need -= sh_before;
+    prefix |= (uint64_t)b << shift;
+    mask |= 0xFFull << shift;
+    const bool full = (uint64_t)sh_bcount == (uint64_t)need;
+    __syncthreads();  // everyone has read the sh_* values
+    if (full || shift == 0) {
+      T = prefix | ~mask;
+      break;
+    }
+  }
+
+  if (tid == 0) sel_count = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < total; i += SEL_THREADS) {
+    uint64_t key = sel_elem(P, np, C, i);
+    if (key != VSK_KEY_NONE && (take_all || key <= T)) {
+      int pos = atomicAdd(&sel_count, 1);
+      if (pos < VSK_MAX_K) sel[pos] = key;
+    }
+  }
+  __syncthreads();
+  int m = sel_count;
+  if (m > k) m = k;  // cannot happen with distinct keys; keeps LDS in range
+  int P2 = 1;
+  while (P2 < m) P2 <<= 1;
+  for (int i = m + tid; i < P2; i += SEL_THREADS) sel[i] = VSK_KEY_NONE;
+  __syncthreads();
+  for (int size = 2; size <= P2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (P2 >> 1); i += SEL_THREADS) {
+        int lo = 2 * i - (i & (stride - 1));
+        int hi = lo + stride;
+        bool up = (lo & size) == 0;
+        uint64_t x = sel[lo], y = sel[hi];
+        if ((x > y) == up) {
+          sel[lo] = y;
+          sel[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  uint64_t *out = a.best_out + q * (int64_t)k;
+  for (int i = tid; i < k; i += SEL_THREADS)
+    out[i] = i < m ? sel[i] : VSK_KEY_NONE;
+  if (tid == 0 && a.thresh) a.thresh[q] = (m >= k) ? sel[k - 1] : VSK_KEY_NONE;
+}
+
+void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
+  if (a.nq <= 0) return;
+  if (a.k < 1 || a.k > VSK_MAX_K)
+    fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
+  KernelTimer t(ctx, name);
+  k_select<<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  check_launch(name);
+}
+
+int64_t default_cap(int32_t k) {
+  int64_t c = 16384;
+  while (c < 16ll * k) c <<= 1;
+  return c;
+}
+
+int64_t query_batch(int64_t nq, int64_t cap) {
+  // candidate buffers of one batch stay under ~2 GiB of HBM
+  const int64_t budget = 2ll << 30;
+  int64_t b = budget / (cap * (int64_t)sizeof(uint64_t));
+  if (b < 64) b = 64;
+  return nq < b ? nq : b;
+}
+
+void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
+                      int64_t cap, const ScanFn &scan, uint64_t *best,
+                      const char *select_name) {
+  if (nq <= 0) return;
+  fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
+  if (n <= 0) return;
+  uint64_t *thresh =
+      static_cast<uint64_t *>(ctx->scratch_ptr("topk.thresh", 8 * nq));
+  uint64_t *cand = static_cast<uint64_t *>(
+      ctx->scratch_ptr("topk.cand", sizeof(uint64_t) * (size_t)nq * cap));
+  int32_t *counts =
+      static_cast<int32_t *>(ctx->scratch_ptr("topk.counts", 4 * nq));
+  uint8_t *ovf_mask =
+      static_cast<uint8_t *>(ctx->scratch_ptr("topk.ovfmask", nq + 64));
+  int32_t *ovf_count =
+      static_cast<int32_t *>(ctx->scratch_ptr("topk.ovfcount", 64));
+  fill_u64(ctx, thresh, nq, VSK_KEY_NONE);
+
+  int64_t r0 = 0;
+  bool first = true;
+  while (r0 < n) {
+    int64_t c;
+    if (first) {
+      c = n < cap ? n : cap;
+    } else {
+      // expected survivors of a chunk of c rows after r0 rows are about
+      // k*c/r0; keep that near cap/2
+      int64_t grow = r0 * (cap / (2 * (int64_t)k));
+      c = grow > cap ? grow : cap;
+      if (c > n - r0) c = n - r0;
+    }
+    const bool dense = first;
+    fill_i32(ctx, counts, nq, dense ? (int32_t)c : 0);
+    scan(ScanRequest{r0, r0 + c, thresh, nullptr, cand, cap, counts, dense});
+    SelectArgs sa;
+    sa.nq = nq;
+    sa.k = k;
+    sa.prev = best;
+    sa.cand = cand;
+    sa.cap = cap;
+    sa.counts = counts;
+    sa.best_out = best;
+    sa.thresh = thresh;
+    if (!dense) {
+      fill_i32(ctx, ovf_count, 1, 0);
+      fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
+      sa.overflow_mask = ovf_mask;
+      sa.overflow_count = ovf_count;
+    }
+    launch_select(ctx, sa, select_name);
+    if (!dense) {
+      int32_t h_ovf = 0;
+      VSK_HIP(hipMemcpyAsync(&h_ovf, ovf_count, 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+      VSK_HIP(hipStreamSynchronize(ctx->stream));
+      if (h_ovf > 0) {
+        // queries whose survivors did not fit re-scan this chunk in
+        // sub-chunks of cap rows, each kept whole
+        for (int64_t s0 = r0; s0 < r0 + c; s0 += cap) {
+          int64_t s1 = s0 + cap < r0 + c ? s0 + cap : r0 + c;
+          fill_i32(ctx, counts, nq, (int32_t)(s1 - s0));
+          scan(ScanRequest{s0, s1, thresh, ovf_mask, cand, cap, counts, true});
+          SelectArgs sb = sa;
+          sb.active = ovf_mask;
+          sb.overflow_mask = nullptr;
+          sb.overflow_count = nullptr;
+          launch_select(ctx, sb, select_name);
+        }
+      }
+    }
+    r0 += c;
+    first = false;
+  }
+}
+
+}  // namespace vsk

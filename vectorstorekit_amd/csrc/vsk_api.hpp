@@ -1,0 +1,98 @@
+// vsk_api.hpp -- entry-point boilerplate and the shared top-k machinery.
+#pragma once
+
+#include <functional>
+
+#include "vsk_core.hpp"
+
+// Every C entry point runs its body inside VSK_API_BEGIN / VSK_API_END: the
+// context's device is made current and internal errors become status codes.
+#define VSK_API_BEGIN(ctx)                                                    \
+  if (!(ctx)) return VSK_ERR_INVALID_ARGUMENT;                                \
+  try {                                                                       \
+    (ctx)->last_error.clear();                                                \
+    VSK_HIP(hipSetDevice((ctx)->device));
+
+#define VSK_API_END(ctx)                                                      \
+  }                                                                           \
+  catch (const ::vsk::Error &e) {                                             \
+    (ctx)->last_error = e.msg;                                                \
+    (void)hipStreamSynchronize((ctx)->stream);                                \
+    (void)hipGetLastError();                                                  \
+    return e.code;                                                            \
+  }                                                                           \
+  catch (const std::exception &e) {                                           \
+    (ctx)->last_error = e.what();                                             \
+    return VSK_ERR_EXECUTION_FAILED;                                          \
+  }                                                                           \
+  return VSK_OK;
+
+namespace vsk {
+
+// ---------------------------------------------------------------------------
+// top-k selection over composite keys (select.hip)
+// ---------------------------------------------------------------------------
+// Segment q holds, in this order, prev[q*k .. q*k+k) (VSK_KEY_NONE entries
+// are ignored; prev may be null) and the candidates
+//   cand[base .. base+count)   base = seg_off ? seg_off[q] : q*cap
+//                              count = counts ? counts[q]
+//                                      : seg_off ? seg_off[q+1]-seg_off[q]
+//                                      : cap
+// All keys of a segment must be distinct.  The k smallest are written
+// sorted to best_out[q*k ..] (VSK_KEY_NONE-padded; may alias prev) and
+// thresh[q] (optional) receives the k-th key (VSK_KEY_NONE if fewer).
+// If counts[q] > cap (only with uniform stride) the segment overflowed: its
+// outputs are left untouched, overflow_mask[q] = 1 and *overflow_count is
+// incremented.  Segments with active && !active[q] are skipped.
+struct SelectArgs {
+  int64_t nq = 0;
+  int32_t k = 0;
+  const uint64_t *prev = nullptr;
+  const uint64_t *cand = nullptr;
+  int64_t cap = 0;
+  const int64_t *seg_off = nullptr;
+  const int32_t *counts = nullptr;
+  uint64_t *best_out = nullptr;
+  uint64_t *thresh = nullptr;
+  const uint8_t *active = nullptr;
+  uint8_t *overflow_mask = nullptr;
+  int32_t *overflow_count = nullptr;
+};
+void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name);
+
+// A scan kernel over database rows [r0, r1) that, for each active query q,
+// either writes the key of every row to cand[q*cap + (row - r0)] (dense) or
+// appends the keys <= thresh[q] to cand[q*cap + atomicAdd(&counts[q], 1)]
+// (keys past cap are dropped, counts keeps counting).
+struct ScanRequest {
+  int64_t r0, r1;
+  const uint64_t *thresh;
+  const uint8_t *active;  // null: all queries active
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+  bool dense;
+};
+using ScanFn = std::function<void(const ScanRequest &)>;
+
+// Exact top-k over n rows for nq queries by streaming the rows in growing
+// chunks: the first chunk is kept whole, later chunks only keep rows that
+// beat the running k-th key of their query; a query whose survivors
+// overflow cap re-scans the chunk in whole sub-chunks.  best: nq*k keys
+// (device), sorted ascending per query on return.
+void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
+                      int64_t cap, const ScanFn &scan, uint64_t *best,
+                      const char *select_name);
+
+// candidate buffer capacity per query used by the progressive scans
+int64_t default_cap(int32_t k);
+// largest query batch whose candidate buffers fit the scratch budget
+int64_t query_batch(int64_t nq, int64_t cap);
+
+// decode keys: dist = float of the key (sqrt when sqrt_out), id =
+// id_map ? id_map[tie] : tie; VSK_KEY_NONE -> (+inf, -1)
+void decode_keys(vsk_ctx *ctx, const uint64_t *best, int64_t total,
+                 bool sqrt_out, const int64_t *id_map, float *out_dist,
+                 int64_t *out_ids);
+
+}  // namespace vsk

@@ -1,0 +1,186 @@
+// vsk_core.hpp -- context, errors, device buffers and the composite
+// (distance, tie) key shared by every kernel of the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "vsk_hip.h"
+
+namespace vsk {
+
+// ---------------------------------------------------------------------------
+// errors: every internal failure throws Error; the C entry points catch it,
+// store the message on the context and return the code.
+// ---------------------------------------------------------------------------
+struct Error {
+  vsk_status code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(vsk_status code, const std::string &msg);
+void check_hip(hipError_t e, const char *what, const char *file, int line);
+#define VSK_HIP(expr) ::vsk::check_hip((expr), #expr, __FILE__, __LINE__)
+#define VSK_REQUIRE(cond, code, msg)                                          \
+  do {                                                                        \
+    if (!(cond)) ::vsk::fail((code), (msg));                                   \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// device memory
+// ---------------------------------------------------------------------------
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf();
+  void reserve(size_t b);  // grow (contents not kept)
+  void release();
+  template <class T> T *as() const { return static_cast<T *>(p); }
+};
+
+bool is_device_ptr(const void *p);
+
+}  // namespace vsk
+
+// ---------------------------------------------------------------------------
+// context (one HIP stream; per-call scratch slots; event profiling)
+// ---------------------------------------------------------------------------
+struct vsk_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  float last_ms = 0.f;
+  hipEvent_t call_begin = nullptr, call_end = nullptr;
+
+  // scratch buffers, reused across calls, keyed by purpose
+  std::map<std::string, std::unique_ptr<vsk::DevBuf>> scratch;
+  void *scratch_ptr(const std::string &key, size_t bytes);
+
+  // profiling
+  bool profile = false;
+  struct Pending {
+    int stat;
+    hipEvent_t a, b;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::vector<vsk_kernel_stat> stats;
+  std::map<std::string, int> stat_index;
+  hipEvent_t take_event();
+  void resolve_pending();
+};
+
+struct vsk_db {
+  int64_t n = 0;
+  int32_t d = 0;
+  int32_t ld = 0;  // row stride in floats (multiple of 4, >= d; zero padded)
+  vsk::DevBuf x;       // n x ld fp32
+  vsk::DevBuf sqnorm;  // n: sum x^2 (fp32)
+  vsk::DevBuf norm;    // n: sqrt(sum x^2)
+};
+
+namespace vsk {
+
+// RAII marker for one API call: records the call's begin/end events,
+// synchronises the stream at the end and resolves profiling events.
+struct CallScope {
+  vsk_ctx *ctx;
+  explicit CallScope(vsk_ctx *c);
+  void finish();  // sync + timing; call before returning results
+};
+
+// Times one kernel launch when profiling is on.
+struct KernelTimer {
+  vsk_ctx *ctx;
+  int stat = -1;
+  hipEvent_t a = nullptr;
+  KernelTimer(vsk_ctx *c, const char *name);
+  ~KernelTimer();
+};
+
+// check the last launch on the stream
+void check_launch(const char *name);
+
+// staging of caller buffers: a device pointer is used as is, a host
+// pointer is copied through a scratch slot.
+const void *input_to_device(vsk_ctx *ctx, const void *p, size_t bytes,
+                            const std::string &slot);
+struct OutputStage {
+  vsk_ctx *ctx;
+  void *user;
+  void *dev;
+  size_t bytes;
+  bool host;
+  OutputStage(vsk_ctx *c, void *user_ptr, size_t nbytes,
+              const std::string &slot);
+  template <class T> T *ptr() const { return static_cast<T *>(dev); }
+  void copy_back();  // enqueue device->host copy when user is host memory
+};
+
+// pad rows of a (rows x d) fp32 matrix to stride ld on the device
+const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
+                                   int32_t d, int32_t ld,
+                                   const std::string &slot);
+
+inline int32_t padded_ld(int32_t d) { return (d + 3) & ~3; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool metric_valid(int32_t m);
+
+// fill kernels (used instead of hipMemsetAsync so callers may capture the
+// stream into a graph)
+void fill_u64(vsk_ctx *ctx, uint64_t *p, int64_t n, uint64_t v);
+void fill_i32(vsk_ctx *ctx, int32_t *p, int64_t n, int32_t v);
+
+// row norms of an (n x ld) matrix over its first d columns:
+// sq[i] = sum x^2 (fp32), nrm[i] = sqrt(sq[i]); either may be null.
+void row_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
+               float *sq, float *nrm);
+
+}  // namespace vsk
+
+// ---------------------------------------------------------------------------
+// composite sort key: (distance, tie) packed in a uint64 whose unsigned order
+// equals ascending distance then ascending tie key.  The distance's fp32
+// bits are mapped to an order-preserving uint32 (negatives flipped, -0
+// folded onto +0, NaN sorted after +inf).
+// ---------------------------------------------------------------------------
+#define VSK_KEY_NONE 0xFFFFFFFFFFFFFFFFull
+
+__host__ __device__ inline uint32_t vsk_f2ord(float f) {
+  if (f == 0.0f) f = 0.0f;          // -0 -> +0
+  if (f != f) return 0xFFFFFFFFu;   // NaN last
+  uint32_t u;
+#ifdef __HIP_DEVICE_COMPILE__
+  u = __float_as_uint(f);
+#else
+  __builtin_memcpy(&u, &f, 4);
+#endif
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__host__ __device__ inline float vsk_ord2f(uint32_t o) {
+  uint32_t u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+  float f;
+#ifdef __HIP_DEVICE_COMPILE__
+  f = __uint_as_float(u);
+#else
+  __builtin_memcpy(&f, &u, 4);
+#endif
+  return f;
+}
+__host__ __device__ inline uint64_t vsk_key(float dist, uint32_t tie) {
+  return ((uint64_t)vsk_f2ord(dist) << 32) | (uint64_t)tie;
+}
+// int32 distance (SQ8: -score) keyed the same way
+__host__ __device__ inline uint64_t vsk_key_i32(int32_t dist, uint32_t tie) {
+  return ((uint64_t)((uint32_t)dist ^ 0x80000000u) << 32) | (uint64_t)tie;
+}

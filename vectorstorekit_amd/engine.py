@@ -1,0 +1,254 @@
+"""Host-side mirror of VectorStoreKit's accelerator surface over the C ABI.
+
+* ``HIPAcceleratorStrategy`` -- the ``ComputeAccelerator`` slot
+  (Core/Protocols.swift:11-20; Metal versions in
+  API/Strategies/AcceleratorStrategies.swift:20-214): ``identifier``,
+  ``requirements``, ``initialize()``, ``capabilities()``.
+* ``HIPAccelerationEngine`` -- ``MetalAccelerationEngine``'s distance API
+  (Acceleration/MetalAccelerationEngine.swift:76-204):
+  ``computeDistances(query, candidates, metric)`` and
+  ``batchComputeDistances(queries, candidates, metric, topK)``, plus
+  ``search`` which also returns the ids (the reference returns distances
+  only).
+* ``VectorDatabase`` -- rows resident in HBM (``vsk_db``).
+
+Paths in citations are relative to Sources/VectorStoreKit/ of
+gifton/VectorStoreKit.  Every call goes through libvsk_hip.so; there is no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import VSKError, as_buffer, check, load_library, out_buffer
+
+
+class DistanceMetric(str, enum.Enum):
+    """``DistanceMetric`` raw values (Core/SearchTypes.swift:105-110) for the
+    four hot-path metrics, plus the squared-L2 and pre-normalised cosine
+    forms of the reference's kernels."""
+
+    euclidean = "euclidean"
+    cosine = "cosine"
+    dotProduct = "dotProduct"
+    manhattan = "manhattan"
+    euclideanSquared = "euclideanSquared"
+    cosineNormalized = "cosineNormalized"
+
+    @property
+    def code(self) -> int:
+        return _METRIC_CODES[self]
+
+
+_METRIC_CODES = {
+    DistanceMetric.euclideanSquared: _lib.METRIC_L2SQ,
+    DistanceMetric.euclidean: _lib.METRIC_L2,
+    DistanceMetric.cosine: _lib.METRIC_COSINE,
+    DistanceMetric.cosineNormalized: _lib.METRIC_COSINE_NORMALIZED,
+    DistanceMetric.dotProduct: _lib.METRIC_DOT,
+    DistanceMetric.manhattan: _lib.METRIC_L1,
+}
+
+
+def metric_code(metric) -> int:
+    if isinstance(metric, int):
+        return metric
+    return DistanceMetric(metric).code
+
+
+class Context:
+    """One ``vsk_ctx``: a device and the HIP stream every call runs on."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        st = self.lib.vsk_create(device, ctypes.byref(h))
+        if st != 0:
+            raise VSKError(st, f"cannot open HIP device {device}")
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.vsk_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, status):
+        check(self.handle, status)
+
+    @property
+    def stream(self) -> int:
+        return self.lib.vsk_stream(self.handle) or 0
+
+    @property
+    def last_kernel_ms(self) -> float:
+        return float(self.lib.vsk_last_kernel_ms(self.handle))
+
+    def capabilities(self) -> dict:
+        caps = _lib.vsk_caps()
+        self.check(self.lib.vsk_device_info(self.handle, ctypes.byref(caps)))
+        return {
+            "name": caps.name.decode(),
+            "arch": caps.arch.decode(),
+            "device": caps.device,
+            "compute_units": caps.compute_units,
+            "wavefront_size": caps.wavefront_size,
+            "lds_bytes_per_block": caps.lds_bytes_per_block,
+            "global_mem_bytes": caps.global_mem_bytes,
+            "clock_khz": caps.clock_khz,
+            "memory_clock_khz": caps.memory_clock_khz,
+            "memory_bus_width_bits": caps.memory_bus_width_bits,
+        }
+
+    # per-kernel HIP-event timing
+    def profile(self, on: bool = True):
+        self.check(self.lib.vsk_profile_enable(self.handle, 1 if on else 0))
+
+    def profile_reset(self):
+        self.check(self.lib.vsk_profile_reset(self.handle))
+
+    def profile_stats(self) -> dict:
+        out = {}
+        for i in range(self.lib.vsk_profile_count(self.handle)):
+            s = _lib.vsk_kernel_stat()
+            self.check(self.lib.vsk_profile_get(self.handle, i, ctypes.byref(s)))
+            out[s.name.decode()] = (int(s.launches), float(s.total_ms))
+        return out
+
+
+class VectorDatabase:
+    """Database rows resident in HBM (``vsk_db_upload_f32``).  ``vectors``
+    is an (n, d) float32 numpy array or torch tensor (host or device)."""
+
+    def __init__(self, ctx: Context, vectors, normalize: bool = False):
+        self.ctx = ctx
+        shape = tuple(vectors.shape)
+        if len(shape) != 2:
+            raise VSKError(-4, "vectors must be 2-D (n, d)")
+        self.n, self.d = int(shape[0]), int(shape[1])
+        ptr, keep = as_buffer(vectors, np.float32)
+        h = ctypes.c_void_p()
+        ctx.check(ctx.lib.vsk_db_upload_f32(ctx.handle, ptr, self.n, self.d,
+                                            _lib.DB_NORMALIZE if normalize else 0,
+                                            ctypes.byref(h)))
+        del keep
+        self.handle = h
+
+    def free(self):
+        if getattr(self, "handle", None):
+            self.ctx.lib.vsk_db_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def read(self, row0: int = 0, count: int | None = None) -> np.ndarray:
+        count = self.n - row0 if count is None else count
+        out = np.empty((count, self.d), np.float32)
+        self.ctx.check(self.ctx.lib.vsk_db_read_f32(self.ctx.handle, self.handle, row0,
+                                                    count, out.ctypes.data))
+        return out
+
+    def search(self, queries, k: int, metric="euclidean"):
+        """Exact top-k: (distances [nq, k] float32, ids [nq, k] int64),
+        ascending (distance, id).  Outputs are torch tensors on the device
+        when ``queries`` is a CUDA tensor, else numpy arrays."""
+        nq = int(queries.shape[0])
+        qp, qk = as_buffer(queries, np.float32, (nq, self.d))
+        dp, dist = out_buffer((nq, k), np.float32, queries)
+        ip, ids = out_buffer((nq, k), np.int64, queries)
+        self.ctx.check(self.ctx.lib.vsk_search_flat(self.ctx.handle, self.handle, qp, nq,
+                                                    k, metric_code(metric), dp, ip))
+        del qk
+        return dist, ids
+
+    def distances(self, queries, metric="euclidean"):
+        """Full distance matrix [nq, n]."""
+        nq = int(queries.shape[0])
+        qp, qk = as_buffer(queries, np.float32, (nq, self.d))
+        mp, mat = out_buffer((nq, self.n), np.float32, queries)
+        self.ctx.check(self.ctx.lib.vsk_distances(self.ctx.handle, self.handle, qp, nq,
+                                                  metric_code(metric), mp))
+        del qk
+        return mat
+
+
+@dataclass(frozen=True)
+class HardwareRequirements:
+    """``HardwareRequirements`` of the accelerator slot."""
+
+    minimumMemory: int = 0
+    requiredComputeUnits: int = 1
+    requiredFeatures: tuple = ("gfx950",)
+
+
+class HIPAcceleratorStrategy:
+    """``ComputeAccelerator`` conformance for HIP (Core/Protocols.swift:11-20):
+    ``initialize()`` returns the device context, ``capabilities()`` its
+    description.  This is what ``accelerate(using:)`` receives."""
+
+    identifier = "hip-gfx950"
+    requirements = HardwareRequirements()
+
+    def __init__(self, device: int = 0):
+        self.device = device
+        self._ctx: Context | None = None
+
+    def initialize(self) -> Context:
+        if self._ctx is None:
+            self._ctx = Context(self.device)
+        return self._ctx
+
+    def capabilities(self) -> dict:
+        return self.initialize().capabilities()
+
+
+class HIPAccelerationEngine:
+    """``MetalAccelerationEngine``'s distance API on the HIP library
+    (Acceleration/MetalAccelerationEngine.swift:76-204).  Candidates may be
+    a ``VectorDatabase`` (resident) or an array uploaded for the call."""
+
+    def __init__(self, device: int | Context = 0):
+        self.ctx = device if isinstance(device, Context) else Context(device)
+
+    def _db(self, candidates, metric):
+        if isinstance(candidates, VectorDatabase):
+            return candidates
+        if len(candidates) == 0:
+            raise VSKError(-3, "candidates is empty")
+        return VectorDatabase(self.ctx, np.asarray(candidates, np.float32)
+                              if not _lib._is_torch(candidates) else candidates)
+
+    def computeDistances(self, query, candidates, metric="euclidean"):
+        """Distances from one query to every candidate (:76-136)."""
+        q = np.asarray(query, np.float32).reshape(1, -1) if not _lib._is_torch(query) \
+            else query.reshape(1, -1)
+        return self._db(candidates, metric).distances(q, metric)[0]
+
+    def batchComputeDistances(self, queries, candidates, metric="euclidean", topK=None):
+        """Per query: all distances (topK None) or the topK smallest,
+        ascending (:139-204)."""
+        db = self._db(candidates, metric)
+        if topK is None:
+            return db.distances(queries, metric)
+        k = min(int(topK), db.n)
+        dist, _ = db.search(queries, k, metric)
+        return dist
+
+    def search(self, queries, candidates, k: int, metric="euclidean"):
+        """Top-k distances and ids."""
+        return self._db(candidates, metric).search(queries, k, metric)
