@@ -1,0 +1,140 @@
+"""IVF-Flat on the GPU against the oracle.  Probing, assignment and the list
+scan sum every squared difference in the reference's order without FMA, so
+probes, assignments, distances and ids must be bit-identical."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from parity import assert_sorted_unique, recall
+from vectorstorekit_amd import IVFConfiguration, IVFIndex, VSKError
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _mixture(seed, ncent, n, d, nq):
+    rng = np.random.default_rng(seed)
+    cent = (2.0 * rng.standard_normal((ncent, d))).astype(np.float32)
+    a = rng.integers(0, ncent, n)
+    x = (cent[a] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    qa = rng.integers(0, ncent, nq)
+    q = (cent[qa] + 0.5 * rng.standard_normal((nq, d))).astype(np.float32)
+    c = (cent + 0.1 * rng.standard_normal(cent.shape)).astype(np.float32)
+    return x, q, c
+
+
+def _index(ctx, c, x, ids=None, nprobe=8):
+    idx = IVFIndex(ctx, IVFConfiguration(dimensions=c.shape[1], numberOfCentroids=c.shape[0],
+                                         numberOfProbes=nprobe))
+    idx.set_centroids(c)
+    if x is not None:
+        idx.insert(x, ids)
+    return idx
+
+
+@pytest.mark.parametrize("shape", [(64, 20_000, 128, 200, 8, 10), (37, 5000, 33, 50, 5, 7),
+                                   (16, 3000, 24, 40, 16, 20)])
+def test_ivf_bit_exact(ctx, shape):
+    ncent, n, d, nq, nprobe, k = shape
+    print(f"ivf ncent={ncent} n={n} d={d} nq={nq} nprobe={nprobe} k={k}", flush=True)
+    x, q, c = _mixture(ncent + n, ncent, n, d, nq)
+    ids = np.arange(n, dtype=np.int64) * 3 + 7
+    idx = _index(ctx, c, x, ids, nprobe)
+    lists = O.ivf_assign(x, c)
+    np.testing.assert_array_equal(idx.assign(x), lists)
+    np.testing.assert_array_equal(idx.list_sizes(), np.bincount(lists, minlength=ncent))
+    np.testing.assert_array_equal(idx.probe(q, nprobe), O.ivf_probe(q, c, nprobe))
+    gd, gi = idx.search(q, k)
+    od, oi = O.ivf_search(q, x, ids, lists, c, nprobe, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_ivf_incremental_inserts_keep_order(ctx):
+    x, q, c = _mixture(9, 20, 4000, 16, 30)
+    idx = _index(ctx, c, None, nprobe=6)
+    for part in np.array_split(np.arange(len(x)), 3):
+        idx.insert(x[part], part.astype(np.int64))
+    lists = O.ivf_assign(x, c)
+    gd, gi = idx.search(q, 15)
+    od, oi = O.ivf_search(q, x, np.arange(len(x), dtype=np.int64), lists, c, 6, 15)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_ivf_exact_strategy_equals_flat(ctx):
+    x, q, c = _mixture(10, 24, 3000, 20, 25)
+    idx = _index(ctx, c, x, nprobe=3)
+    gd, gi = idx.search(q, 10, strategy="exact")
+    fd, fi = O.search_flat(q, x, 10, O.L2)
+    np.testing.assert_array_equal(gd, fd)
+    for a, b in zip(gi, fi):
+        assert set(a) == set(b)
+
+
+def test_ivf_reference_kats(ctx):
+    with open(os.path.join(GOLD, "reference_kats.json")) as f:
+        k = json.load(f)["ivf_basic"]
+    c = np.array(k["training"][:4], np.float32)
+    idx = _index(ctx, c, np.array([k["inserted"]], np.float32), np.array([1], np.int64),
+                 nprobe=k["nprobe"])
+    d, i = idx.search(np.array([k["query"]], np.float32), 1)
+    assert i[0, 0] == 1
+
+
+def test_ivf_train_and_errors(ctx):
+    x, q, c = _mixture(11, 8, 2000, 16, 5)
+    idx = IVFIndex(ctx, IVFConfiguration(dimensions=16, numberOfCentroids=8, numberOfProbes=2))
+    with pytest.raises(VSKError) as e:
+        idx.search(q, 3)
+    assert e.value.kind == "notTrained"
+    idx.train(x, iterations=5)
+    idx.insert(x)
+    d, i = idx.search(q, 5, strategy="exact")
+    fd, fi = O.search_flat(q, x, 5, O.L2)
+    np.testing.assert_array_equal(d, fd)
+    # empty lists and k > candidates pad with (inf, -1)
+    empty = _index(ctx, c, None, nprobe=2)
+    d, i = empty.search(q, 4)
+    assert (i == -1).all() and np.isinf(d).all()
+
+
+def test_config3_full_size(ctx):
+    """1M x 128 from a 4,096-Gaussian mixture, nlist 4096,
+    nprobe 32, 10,000 queries, k=10.  Assignment checked bit-exact on a row
+    sample, search bit-exact on 200 queries, recall@10 vs exact search equal
+    to the oracle's on those queries."""
+    import torch
+
+    n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    cent = 2.0 * torch.randn(ncent, d, generator=g, device="cuda")
+    g.manual_seed(5)
+    a = torch.randint(0, ncent, (n,), generator=g, device="cuda")
+    qa = torch.randint(0, ncent, (nq,), generator=g, device="cuda")
+    g.manual_seed(1)
+    x = cent[a] + 0.5 * torch.randn(n, d, generator=g, device="cuda")
+    g.manual_seed(2)
+    q = cent[qa] + 0.5 * torch.randn(nq, d, generator=g, device="cuda")
+    g.manual_seed(4)
+    c = cent + 0.1 * torch.randn(ncent, d, generator=g, device="cuda")
+    xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), c.cpu().numpy()
+    print("config3 ivf 1Mx128 nlist4096 nprobe32 q10000 k10", flush=True)
+    idx = _index(ctx, ch, x, nprobe=nprobe)
+    lists = idx.assign(x).cpu().numpy()
+    sample = np.random.default_rng(0).choice(n, 20_000, replace=False)
+    np.testing.assert_array_equal(lists[sample], O.ivf_assign(xh[sample], ch))
+    gd, gi = idx.search(q, k)
+    gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
+    assert_sorted_unique(gd, gi)
+    sub = 200
+    od, oi = O.ivf_search(qh[:sub], xh, np.arange(n, dtype=np.int64), lists, ch, nprobe, k)
+    np.testing.assert_array_equal(gi[:sub], oi)
+    np.testing.assert_array_equal(gd[:sub], od)
+    td, ti = O.search_flat(qh[:sub], xh, k, O.L2)
+    assert recall(gi[:sub], ti) == recall(oi, ti)
+    print(f"config3 recall@10 on {sub} queries: {recall(gi[:sub], ti):.4f}", flush=True)

@@ -1,0 +1,181 @@
+"""int8 scalar-quantized scan and PQ-ADC scan on the GPU against the oracle.
+Both are bit-exact paths: int32 scores, fp32 tables/ADC sums formed in the
+reference's order, L1 re-rank summed in index order."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from parity import assert_sorted_unique, recall
+from vectorstorekit_amd import ProductQuantizer, ScalarQuantizer, SQ8Database, VectorDatabase
+from vectorstorekit_amd._lib import METRIC_COSINE, METRIC_L1, METRIC_L2, METRIC_L2SQ
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ SQ8 ---
+
+@pytest.mark.parametrize("per_dim", [True, False])
+def test_sq8_train_encode_bit_exact(ctx, per_dim):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((5000, 45)).astype(np.float32) * 3
+    sq = ScalarQuantizer(ctx, per_dim=per_dim)
+    s, o = sq.train(x)
+    es, eo = O.sq8_train(x, per_dim)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(o, eo)
+    np.testing.assert_array_equal(sq.quantizeBatch(x), O.sq8_encode(x, es, eo))
+
+
+@pytest.mark.parametrize("shape", [(20_000, 128, 37, 100), (3000, 45, 70, 10), (500, 7, 3, 1)])
+def test_sq8_search_bit_exact(ctx, shape):
+    n, d, nq, k = shape
+    print(f"sq8 n={n} d={d} nq={nq} k={k}", flush=True)
+    rng = np.random.default_rng(n + d)
+    codes = rng.integers(-128, 128, (n, d)).astype(np.int8)
+    qc = rng.integers(-128, 128, (nq, d)).astype(np.int8)
+    codes[7] = codes[3]
+    qc[0] = codes[3]
+    db = SQ8Database(ctx, codes)
+    gs, gi = db.search(qc, k)
+    os_, oi = O.sq8_search(qc, codes, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gs, os_)
+
+
+def test_sq8_chunked_and_overflow(ctx):
+    """Scores fall with the row id, so every filtered chunk overflows."""
+    n, d = 150_000, 32
+    codes = np.zeros((n, d), np.int8)
+    codes[:, 0] = (np.arange(n) * 255 // n - 128).astype(np.int8)
+    codes[:, 1] = np.random.default_rng(2).integers(-128, 128, n).astype(np.int8)
+    qc = np.zeros((3, d), np.int8)
+    qc[0, 0] = 127
+    qc[1, 0] = -128
+    qc[2, 1] = 5
+    gs, gi = SQ8Database(ctx, codes).search(qc, 50)
+    os_, oi = O.sq8_search(qc, codes, 50)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gs, os_)
+
+
+def test_config4_full_size(ctx):
+    """10M x 128 N(0,1) quantised per dimension, 1,000
+    queries quantised with the same parameters, k=100; scores and ids
+    bit-exact on 8 queries, properties on all."""
+    import torch
+
+    n, d, nq, k = 10_000_000, 128, 1000, 100
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    x = torch.randn(n, d, generator=g, device="cuda")
+    g.manual_seed(2)
+    q = torch.randn(nq, d, generator=g, device="cuda")
+    print("config4 sq8 10Mx128 q1000 k100", flush=True)
+    sq = ScalarQuantizer(ctx, per_dim=True)
+    s, o = sq.train(x)
+    codes = sq.quantizeBatch(x)
+    xs = x[:4096].cpu().numpy()
+    del x
+    qc = sq.quantizeBatch(q)
+    db = SQ8Database(ctx, codes)
+    gs, gi = db.search(qc, k)
+    gs, gi = gs.cpu().numpy(), gi.cpu().numpy()
+    assert (np.diff(gs, axis=1) <= 0).all()
+    ch, qh = codes.cpu().numpy(), qc.cpu().numpy()
+    sub = 8
+    os_, oi = O.sq8_search(qh[:sub], ch, k)
+    np.testing.assert_array_equal(gi[:sub], oi)
+    np.testing.assert_array_equal(gs[:sub], os_)
+    # scores are the integer dots of the returned rows
+    for qi in (100, 999):
+        np.testing.assert_array_equal(
+            gs[qi], ch[gi[qi]].astype(np.int64) @ qh[qi].astype(np.int64))
+    # encode parity on a row sample
+    np.testing.assert_array_equal(ch[:4096], O.sq8_encode(xs, s, o))
+
+
+# ------------------------------------------------------------------- PQ ---
+
+def _pq_data(seed, n, d, M, ksub, nq, ncent=64):
+    rng = np.random.default_rng(seed)
+    cent = (2.0 * rng.standard_normal((ncent, d))).astype(np.float32)
+    x = (cent[rng.integers(0, ncent, n)] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    q = (cent[rng.integers(0, ncent, nq)] + 0.5 * rng.standard_normal((nq, d))).astype(np.float32)
+    dsub = d // M
+    cb = np.stack([O.kmeans(x[:4096, m * dsub:(m + 1) * dsub].copy(), ksub, iters=4, seed=m)
+                   for m in range(M)])
+    return x, q, cb
+
+
+@pytest.mark.parametrize("shape", [(20_000, 128, 16, 256, 30), (5000, 24, 6, 100, 9)])
+def test_pq_lut_encode_adc_bit_exact(ctx, shape):
+    n, d, M, ksub, nq = shape
+    print(f"pq n={n} d={d} M={M} ksub={ksub} nq={nq}", flush=True)
+    x, q, cb = _pq_data(n, n, d, M, ksub, nq)
+    pq = ProductQuantizer(ctx, cb)
+    codes = pq.encode(x)
+    np.testing.assert_array_equal(codes, O.pq_encode(x, cb))
+    lut = pq.precomputeDistanceTables(q)
+    for qi in range(nq):
+        np.testing.assert_array_equal(lut[qi], O.pq_lut(q[qi], cb))
+    pq.add(codes)
+    for k_adc, k in [(100, 100), (300, 10)]:
+        gd, gi = pq.search(q, k, k_adc=k_adc)
+        od, oi = O.pq_search(q, cb, codes, k_adc, k)
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gd, od)
+
+
+@pytest.mark.parametrize("metric", [METRIC_L1, METRIC_L2, METRIC_L2SQ, METRIC_COSINE])
+def test_pq_rerank_bit_exact(ctx, metric):
+    x, q, cb = _pq_data(5, 30_000, 64, 8, 256, 20)
+    pq = ProductQuantizer(ctx, cb)
+    codes = O.pq_encode(x, cb)
+    pq.add(codes[:10_000])
+    pq.add(codes[10_000:])  # appended in two calls
+    db = VectorDatabase(ctx, x)
+    gd, gi = pq.search(q, 100, k_adc=1000, rerank_metric=metric, rerank_db=db)
+    od, oi = O.pq_search(q, cb, codes, 1000, 100, x=x, rerank_metric=metric)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_config5_full_size(ctx):
+    """10M x 128 from a 1,024-Gaussian mixture, PQ M=16 x
+    256 (codebooks trained on a 65,536-row sample), 1,000 queries, ADC top-1000
+    then exact L1 re-rank -> k=100.  Bit-exact on 4 queries; recall@100 vs
+    exact L1 search equal to the oracle's on those queries."""
+    import torch
+
+    n, d, nq, M, ksub = 10_000_000, 128, 1000, 16, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    cent = 2.0 * torch.randn(1024, d, generator=g, device="cuda")
+    g.manual_seed(5)
+    a = torch.randint(0, 1024, (n,), generator=g, device="cuda")
+    qa = torch.randint(0, 1024, (nq,), generator=g, device="cuda")
+    g.manual_seed(1)
+    x = cent[a] + 0.5 * torch.randn(n, d, generator=g, device="cuda")
+    g.manual_seed(2)
+    q = cent[qa] + 0.5 * torch.randn(nq, d, generator=g, device="cuda")
+    print("config5 pq 10Mx128 M16x256 q1000 kadc1000 k100 L1", flush=True)
+    sample = x[:65536].cpu().numpy()
+    dsub = d // M
+    cb = np.stack([O.kmeans(sample[:, m * dsub:(m + 1) * dsub].copy(), ksub, iters=8, seed=m)
+                   for m in range(M)])
+    pq = ProductQuantizer(ctx, cb)
+    codes = pq.encode(x)
+    pq.add(codes)
+    db = VectorDatabase(ctx, x)
+    gd, gi = pq.search(q, 100, k_adc=1000, rerank_metric=METRIC_L1, rerank_db=db)
+    gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
+    assert_sorted_unique(gd, gi)
+    xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), codes.cpu().numpy()
+    np.testing.assert_array_equal(ch[:20_000], O.pq_encode(xh[:20_000], cb))
+    sub = 4
+    od, oi = O.pq_search(qh[:sub], cb, ch, 1000, 100, x=xh, rerank_metric=O.L1)
+    np.testing.assert_array_equal(gi[:sub], oi)
+    np.testing.assert_array_equal(gd[:sub], od)
+    td, ti = O.search_flat(qh[:sub], xh, 100, O.L1)
+    assert recall(gi[:sub], ti) == recall(oi, ti)
+    print(f"config5 recall@100 on {sub} queries: {recall(gi[:sub], ti):.4f}", flush=True)

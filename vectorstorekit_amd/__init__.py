@@ -12,3 +12,5 @@ from .engine import (  # noqa: F401
     HIPAcceleratorStrategy,
     VectorDatabase,
 )
+from .ivf import IVFConfiguration, IVFIndex  # noqa: F401,E402
+from .quantization import ProductQuantizer, ScalarQuantizer, SQ8Database  # noqa: F401,E402

@@ -18,7 +18,7 @@
 // dot product and precomputed norms:
 //   L2^2 = |q|^2 + |x|^2 - 2 q.x       cosine = 1 - q.x / (|q||x| + 1e-8)
 //   normalised cosine = 1 - q.x        dot = -q.x
-#include "vsk_api.hpp"
+#include "flat.hpp"
 
 namespace vsk {
 
@@ -29,54 +29,28 @@ constexpr int FB_Q = 64;   // queries per workgroup
 constexpr int FB_K = 32;   // dims per LDS stage
 constexpr int FS = FB_K + 2;  // LDS row stride (floats): conflict-free MFMA reads
 
-enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2 };
-
-struct FlatArgs {
-  const float *X;
-  int64_t ldx;
-  const float *Q;
-  int64_t ldq;
-  const float *xaux;  // |x|^2 (L2), |x| (cosine), else null
-  const float *qaux;  // same for queries
-  int32_t kdim;       // padded dimension (multiple of 4)
-  int32_t nq;
-  int64_t r0, r1;
-  int64_t rows_per_split;
-  int32_t metric;
-  const uint64_t *thresh;
-  const uint8_t *active;
-  uint64_t *cand;
-  int64_t cap;
-  int32_t *counts;
-  float *mat;  // MODE_MATRIX output, row-major nq x ldm
-  int64_t ldm;
-};
-
-__device__ inline float metric_from_dot(int metric, float dot, float qa,
-                                        float xa) {
-  switch (metric) {
-  case VSK_METRIC_L2SQ:
-  case VSK_METRIC_L2:
+// the metric is a template parameter: the epilogue has no runtime switch
+template <int METRIC>
+__device__ inline float metric_from_dot(float dot, float qa, float xa) {
+  if constexpr (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2)
     return fmaxf(qa + xa - 2.0f * dot, 0.0f);
-  case VSK_METRIC_COSINE:
+  else if constexpr (METRIC == VSK_METRIC_COSINE)
     return 1.0f - dot / (qa * xa + 1e-8f);
-  case VSK_METRIC_COSINE_NORMALIZED:
+  else if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED)
     return 1.0f - dot;
-  default:  // VSK_METRIC_DOT
+  else
     return -dot;
-  }
 }
 
 // one (query, row, distance) result of a tile
-template <int MODE>
+template <int MODE, int METRIC>
 __device__ inline void emit(const FlatArgs &a, int64_t qi, int64_t row,
                             float dist, uint64_t th) {
-  if (MODE == MODE_MATRIX) {
-    a.mat[qi * a.ldm + row] =
-        a.metric == VSK_METRIC_L2 ? __fsqrt_rn(dist) : dist;
+  if constexpr (MODE == MODE_MATRIX) {
+    a.mat[qi * a.ldm + row] = METRIC == VSK_METRIC_L2 ? __fsqrt_rn(dist) : dist;
   } else {
     uint64_t key = vsk_key(dist, (uint32_t)row);
-    if (MODE == MODE_DENSE) {
+    if constexpr (MODE == MODE_DENSE) {
       a.cand[qi * a.cap + (row - a.r0)] = key;
     } else if (key <= th) {
       int slot = atomicAdd(&a.counts[qi], 1);
@@ -85,7 +59,7 @@ __device__ inline void emit(const FlatArgs &a, int64_t qi, int64_t row,
   }
 }
 
-template <int MODE>
+template <int MODE, int METRIC>
 __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
   __shared__ float xs[FB_N * FS];
   __shared__ float qs[FB_Q * FS];
@@ -188,22 +162,47 @@ __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if (!qok[j]) continue;
-          float dist = metric_from_dot(a.metric, acc[i][j][r], qa[j], xa);
-          emit<MODE>(a, qi[j], row, dist, th[j]);
+          float dist = metric_from_dot<METRIC>(acc[i][j][r], qa[j], xa);
+          emit<MODE, METRIC>(a, qi[j], row, dist, th[j]);
         }
       }
     }
   }
 }
 
-// Manhattan on the VALU.  Thread (tid) owns rows (tid%32)+32u, u<4, and
-// queries (tid/32)+8v, v<8; every |q-x| term is added in dimension order,
-// the order of the reference's per-candidate vDSP loop
-// (Acceleration/AccelerateOptimizer.swift:322-360).
+// Exact VALU distances, every term added in dimension order:
+//  OP_L1    sum |q-x|   (the order of the reference's per-candidate vDSP
+//           loop, Acceleration/AccelerateOptimizer.swift:322-360)
+//  OP_L2SEQ sqrt(sum (q-x)^2) with separate multiply and add (no FMA), as
+//           IVFIndex.computeDistance (Indexes/IVFIndex.swift:542-549)
+// so the distances are bit-identical to a sequential fp32 loop.  Thread
+// (tid) owns rows (tid%32)+32u, u<4, and queries (tid/32)+8v, v<8.
+// MODE_ARGMIN keeps, per query, the smallest (distance, row) key over all
+// rows, i.e. the first minimum under strict '<' (findNearestCentroid,
+// Indexes/IVFIndex.swift:514-527), and writes the row index to argmin[q].
 constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
+enum { OP_L1 = 0, OP_L2SEQ = 1 };
 
-template <int MODE>
-__global__ __launch_bounds__(256) void k_flat_l1(FlatArgs a) {
+__device__ inline uint64_t shfl_xor_u64(uint64_t v, int m) {
+  uint32_t lo = __shfl_xor((uint32_t)v, m);
+  uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int OP>
+__device__ inline float valu_term(float q, float x) {
+#pragma clang fp contract(off)
+  if constexpr (OP == OP_L1) {
+    return fabsf(q - x);
+  } else {
+    float t = q - x;
+    return t * t;
+  }
+}
+
+template <int MODE, int OP>
+__global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) {
+#pragma clang fp contract(off)
   __shared__ float xs[FB_N * LS];
   __shared__ float qs[FB_Q * LS];
   const int tid = threadIdx.x;
@@ -216,11 +215,13 @@ __global__ __launch_bounds__(256) void k_flat_l1(FlatArgs a) {
   int64_t qi[8];
   bool qok[8];
   uint64_t th[8];
+  uint64_t best[8];
 #pragma unroll
   for (int v = 0; v < 8; ++v) {
     qi[v] = q0 + qsub + 8 * v;
     qok[v] = qi[v] < a.nq && (!a.active || a.active[qi[v]]);
     th[v] = (MODE == MODE_FILTER && qok[v]) ? a.thresh[qi[v]] : 0;
+    best[v] = VSK_KEY_NONE;
   }
   const int crow = tid >> 3, ccol = (tid & 7) * 4;
   for (int64_t t0 = s0; t0 < s1; t0 += FB_N) {
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(256) void k_flat_l1(FlatArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int v = 0; v < 8; ++v) acc[u][v] += fabsf(qv[v] - xv[u]);
+          for (int v = 0; v < 8; ++v) acc[u][v] += valu_term<OP>(qv[v], xv[u]);
       }
     }
 #pragma unroll
@@ -279,45 +280,93 @@ __global__ __launch_bounds__(256) void k_flat_l1(FlatArgs a) {
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         if (!qok[v]) continue;
-        emit<MODE>(a, qi[v], row, acc[u][v], th[v]);
+        const float dist = OP == OP_L2SEQ ? __fsqrt_rn(acc[u][v]) : acc[u][v];
+        if constexpr (MODE == MODE_ARGMIN) {
+          uint64_t key = vsk_key(dist, (uint32_t)row);
+          best[v] = key < best[v] ? key : best[v];
+        } else {
+          // L2SEQ keys/matrix carry the sqrt distance already
+          emit<MODE, VSK_METRIC_L1>(a, qi[v], row, dist, th[v]);
+        }
       }
+    }
+  }
+  if constexpr (MODE == MODE_ARGMIN) {
+    // the 32 lanes with equal qsub hold disjoint rows of the same queries
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      uint64_t b = best[v];
+#pragma unroll
+      for (int m = 16; m > 0; m >>= 1) {
+        uint64_t o = shfl_xor_u64(b, m);
+        b = o < b ? o : b;
+      }
+      if (rsub == 0 && qok[v]) argmin[qi[v]] = (int32_t)(uint32_t)b;
     }
   }
 }
 
-// grid: query tiles x row splits, enough workgroups to fill 256 CUs
-static void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode) {
+template <int METRIC>
+static void launch_mfma(vsk_ctx *ctx, dim3 grid, const FlatArgs &a, int mode) {
+  if (mode == MODE_DENSE)
+    k_flat_mfma<MODE_DENSE, METRIC><<<grid, 256, 0, ctx->stream>>>(a);
+  else if (mode == MODE_FILTER)
+    k_flat_mfma<MODE_FILTER, METRIC><<<grid, 256, 0, ctx->stream>>>(a);
+  else
+    k_flat_mfma<MODE_MATRIX, METRIC><<<grid, 256, 0, ctx->stream>>>(a);
+}
+
+template <int OP>
+static void launch_valu(vsk_ctx *ctx, dim3 grid, const FlatArgs &a, int mode,
+                        int32_t *argmin) {
+  if (mode == MODE_DENSE)
+    k_flat_valu<MODE_DENSE, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+  else if (mode == MODE_FILTER)
+    k_flat_valu<MODE_FILTER, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+  else if (mode == MODE_MATRIX)
+    k_flat_valu<MODE_MATRIX, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+  else
+    k_flat_valu<MODE_ARGMIN, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+}
+
+// grid: query tiles x row splits, enough workgroups to fill 256 CUs (argmin
+// keeps every row of a query in one workgroup)
+void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   const int64_t rows = a.r1 - a.r0;
   if (rows <= 0 || a.nq <= 0) return;
   const int64_t qt = ceil_div(a.nq, FB_Q);
-  int64_t splits = ceil_div(4096, qt);
+  int64_t splits = mode == MODE_ARGMIN ? 1 : ceil_div(4096, qt);
   const int64_t max_splits = ceil_div(rows, FB_N);
   if (splits > max_splits) splits = max_splits;
   if (splits > 65535) splits = 65535;
   if (splits < 1) splits = 1;
   a.rows_per_split = ceil_div(ceil_div(rows, splits), FB_N) * FB_N;
   splits = ceil_div(rows, a.rows_per_split);
+  if (qt > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
   dim3 grid((unsigned)qt, (unsigned)splits);
-  const bool l1 = a.metric == VSK_METRIC_L1;
-  const char *name = l1 ? (mode == MODE_MATRIX ? "flat_l1_matrix"
-                                               : "flat_l1_scan")
-                        : (mode == MODE_MATRIX ? "flat_mfma_matrix"
-                                               : "flat_mfma_scan");
+  const bool valu = a.metric == VSK_METRIC_L1 || a.metric == METRIC_L2_EXACT;
+  static const char *names[2][4] = {
+      {"flat_mfma_scan", "flat_mfma_scan", "flat_mfma_matrix", "flat_mfma_argmin"},
+      {"flat_valu_scan", "flat_valu_scan", "flat_valu_matrix", "flat_valu_argmin"}};
+  const char *name = names[valu ? 1 : 0][mode];
   KernelTimer t(ctx, name);
-  if (l1) {
-    if (mode == MODE_DENSE)
-      k_flat_l1<MODE_DENSE><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (mode == MODE_FILTER)
-      k_flat_l1<MODE_FILTER><<<grid, 256, 0, ctx->stream>>>(a);
+  if (valu) {
+    if (a.metric == VSK_METRIC_L1)
+      launch_valu<OP_L1>(ctx, grid, a, mode, argmin);
     else
-      k_flat_l1<MODE_MATRIX><<<grid, 256, 0, ctx->stream>>>(a);
+      launch_valu<OP_L2SEQ>(ctx, grid, a, mode, argmin);
   } else {
-    if (mode == MODE_DENSE)
-      k_flat_mfma<MODE_DENSE><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (mode == MODE_FILTER)
-      k_flat_mfma<MODE_FILTER><<<grid, 256, 0, ctx->stream>>>(a);
-    else
-      k_flat_mfma<MODE_MATRIX><<<grid, 256, 0, ctx->stream>>>(a);
+    if (mode == MODE_ARGMIN)
+      fail(VSK_ERR_UNSUPPORTED, "argmin needs an exact VALU metric");
+    switch (a.metric) {
+    case VSK_METRIC_L2SQ: launch_mfma<VSK_METRIC_L2SQ>(ctx, grid, a, mode); break;
+    case VSK_METRIC_L2: launch_mfma<VSK_METRIC_L2>(ctx, grid, a, mode); break;
+    case VSK_METRIC_COSINE: launch_mfma<VSK_METRIC_COSINE>(ctx, grid, a, mode); break;
+    case VSK_METRIC_COSINE_NORMALIZED:
+      launch_mfma<VSK_METRIC_COSINE_NORMALIZED>(ctx, grid, a, mode);
+      break;
+    default: launch_mfma<VSK_METRIC_DOT>(ctx, grid, a, mode); break;
+    }
   }
   check_launch(name);
 }
@@ -370,7 +419,7 @@ void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
       a.cand = r.cand;
       a.cap = r.cap;
       a.counts = r.counts;
-      launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER);
+      launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER, nullptr);
     };
     progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k,
                      "flat_select");
@@ -440,7 +489,7 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
   a.metric = metric;
   a.mat = om.ptr<float>();
   a.ldm = db->n;
-  launch_flat(ctx, a, MODE_MATRIX);
+  launch_flat(ctx, a, MODE_MATRIX, nullptr);
   om.copy_back();
   cs.finish();
   VSK_API_END(ctx);

@@ -1,0 +1,588 @@
+// ivf.hip -- IVF-Flat: coarse probing, insertion into CSR inverted lists and
+// the list-major inverted-list scan.
+//
+// Reference: IVFIndex (Indexes/IVFIndex.swift): insert (:80-122) appends a
+// row to the list of its nearest centroid (findNearestCentroid, :514-527);
+// search (:124-202) ranks the centroids by sqrt-L2 (findNearestCentroids,
+// :529-540), concatenates the nprobe lists in probe order (:151-157),
+// computes the exact sqrt-L2 of every candidate (:167-172) and keeps the
+// first k after a stable sort (:175-176).
+//
+// Layout in HBM: the centroids as a resident flat database; the lists as
+// CSR -- rows sorted by list (insertion order inside a list), their user
+// ids, and list offsets.
+//
+// Search pipeline (all on the stream):
+//  1. probe: exact sequential-L2 (VALU, bit-identical to the reference's
+//     loop) of every (query, centroid) pair + top-nprobe selection with ties
+//     broken by centroid index;
+//  2. per query, the candidate count and each probe's position base (the
+//     offset of its list in the probe-ordered concatenation);
+//  3. the (query, probe) pairs are grouped by list, so each list is read
+//     from HBM once per group of up to QG queries rather than once per
+//     query; a thread owns one list row and keeps QG sequential-L2
+//     accumulators; every distance is written as a (distance, position) key
+//     into its query's candidate segment;
+//  4. per-query selection over the segment -> k smallest (distance,
+//     position), i.e. the stable-sort prefix; positions map back to ids.
+#include <algorithm>
+#include <numeric>
+
+#include "flat.hpp"
+
+struct vsk_ivf {
+  int32_t nlist = 0, d = 0, ld = 0;
+  vsk_db centroids;
+  vsk::DevBuf rows;     // total x ld fp32, grouped by list
+  vsk::DevBuf ids;      // total int64
+  vsk::DevBuf list_off; // nlist+1 int64 (device copy of off)
+  std::vector<int64_t> off;  // nlist+1
+  int64_t total = 0;
+  int64_t next_id = 0;
+};
+
+namespace vsk {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+__global__ void k_scatter_rows(const float *src, const int64_t *src_ids,
+                               int64_t id_base, const int64_t *dest, int64_t n,
+                               int32_t ld, float *dst, int64_t *dst_ids) {
+  // one wave per row
+  const int lane = threadIdx.x & 63;
+  for (int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n;
+       r += (int64_t)gridDim.x * 4) {
+    const int64_t t = dest[r];
+    for (int j = lane; j < ld; j += 64) dst[t * ld + j] = src[r * ld + j];
+    if (lane == 0) dst_ids[t] = src_ids ? src_ids[r] : id_base + r;
+  }
+}
+
+// keys (dist, centroid) of the top-nprobe -> centroid indices
+__global__ void k_keys_to_tie(const uint64_t *keys, int64_t total,
+                              int32_t *out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = keys[i] == VSK_KEY_NONE ? -1 : (int32_t)(uint32_t)keys[i];
+}
+
+// per query: candidate count and the position base of each probe
+__global__ void k_probe_bases(const int32_t *probes, int64_t nq, int32_t np,
+                              const int64_t *list_off, int64_t *pos_base,
+                              int64_t *cnt) {
+  int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  int64_t s = 0;
+  for (int p = 0; p < np; ++p) {
+    int32_t l = probes[q * np + p];
+    pos_base[q * np + p] = s;
+    if (l >= 0) s += list_off[l + 1] - list_off[l];
+  }
+  cnt[q] = s;
+}
+
+// pair (q, p) -> its slot in the list-grouped pair array
+__global__ void k_group_pairs(const int32_t *probes, int64_t npairs, int32_t np,
+                              int64_t *cursor, int32_t *pairs) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int32_t l = probes[i];
+    if (l < 0) continue;
+    int64_t slot = atomicAdd((unsigned long long *)&cursor[l], 1ull);
+    pairs[slot] = (int32_t)i;  // i = q * np + p
+  }
+}
+
+struct ListScanArgs {
+  const float *rows;     // list rows, ld stride
+  const int64_t *list_off;
+  const float *Q;        // queries (batch), ld stride
+  int32_t ld;
+  int32_t np;            // probes per query
+  const int32_t *probes; // [nq][np]
+  const int32_t *pairs;  // pair ids (q*np+p) grouped by list
+  const int4 *groups;    // (list, pair_begin, pair_count, 0)
+  const int64_t *pos_base;  // [nq][np]
+  const int64_t *seg_off;   // [nq+1] candidate segment offsets
+  uint64_t *cand;
+};
+
+// one workgroup per group: up to QG queries probing the same list
+template <int QG>
+__global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float qs[];  // QG x ld
+  const int4 g = a.groups[blockIdx.x];
+  const int32_t l = g.x;
+  const int npair = g.z;
+  const int64_t v0 = a.list_off[l], v1 = a.list_off[l + 1];
+  int32_t qidx[QG];
+  int64_t obase[QG], tbase[QG];
+#pragma unroll
+  for (int j = 0; j < QG; ++j) {
+    int32_t pid = a.pairs[g.y + (j < npair ? j : 0)];
+    int32_t q = pid / a.np;
+    qidx[j] = q;
+    obase[j] = a.seg_off[q] + a.pos_base[pid];
+    tbase[j] = a.pos_base[pid];
+  }
+  for (int i = threadIdx.x; i < QG * a.ld; i += blockDim.x) {
+    int j = i / a.ld, c = i - j * a.ld;
+    int32_t pid = a.pairs[g.y + (j < npair ? j : 0)];
+    qs[i] = a.Q[(int64_t)(pid / a.np) * a.ld + c];
+  }
+  __syncthreads();
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+    const float *x = a.rows + v * a.ld;
+    float acc[QG];
+#pragma unroll
+    for (int j = 0; j < QG; ++j) acc[j] = 0.f;
+    for (int c = 0; c < a.ld; c += 4) {
+      const f4 xv = *reinterpret_cast<const f4 *>(x + c);
+#pragma unroll
+      for (int j = 0; j < QG; ++j) {
+        const f4 qv = *reinterpret_cast<const f4 *>(qs + j * a.ld + c);
+        float t;
+        t = qv.x - xv.x;
+        acc[j] = acc[j] + t * t;
+        t = qv.y - xv.y;
+        acc[j] = acc[j] + t * t;
+        t = qv.z - xv.z;
+        acc[j] = acc[j] + t * t;
+        t = qv.w - xv.w;
+        acc[j] = acc[j] + t * t;
+      }
+    }
+    const int64_t i = v - v0;
+#pragma unroll
+    for (int j = 0; j < QG; ++j) {
+      if (j >= npair) break;
+      a.cand[obase[j] + i] =
+          vsk_key(__fsqrt_rn(acc[j]), (uint32_t)(tbase[j] + i));
+    }
+  }
+  (void)qidx;
+}
+
+// best keys (dist, position) -> (dist, user id)
+__global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
+                             const int32_t *probes, int32_t np,
+                             const int64_t *pos_base, const int64_t *list_off,
+                             const int64_t *ids, float *out_dist,
+                             int64_t *out_ids) {
+  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= nq * k) return;
+  const int64_t q = i / k;
+  const uint64_t key = best[i];
+  if (key == VSK_KEY_NONE) {
+    out_dist[i] = __int_as_float(0x7f800000);
+    out_ids[i] = -1;
+    return;
+  }
+  const int64_t pos = (uint32_t)key;
+  const int64_t *pb = pos_base + q * np;
+  int p = np - 1;
+  while (p > 0 && (pb[p] > pos || probes[q * np + p] < 0)) --p;
+  const int32_t l = probes[q * np + p];
+  const int64_t row = list_off[l] + (pos - pb[p]);
+  out_dist[i] = vsk_ord2f((uint32_t)(key >> 32));
+  out_ids[i] = ids[row];
+}
+
+static unsigned grid1(int64_t n, int threads = 256) {
+  int64_t g = ceil_div(n, threads);
+  return (unsigned)(g < 65535 * 16 ? (g > 0 ? g : 1) : 65535 * 16);
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+static FlatArgs centroid_args(const vsk_ivf *ivf, const float *dq, int64_t nq) {
+  FlatArgs a{};
+  a.X = ivf->centroids.x.as<float>();
+  a.ldx = ivf->ld;
+  a.Q = dq;
+  a.ldq = ivf->ld;
+  a.kdim = ivf->ld;
+  a.nq = (int32_t)nq;
+  a.r0 = 0;
+  a.r1 = ivf->nlist;
+  a.metric = METRIC_L2_EXACT;
+  return a;
+}
+
+// nearest centroid of every row (strict '<', first minimum)
+static void ivf_assign_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dx,
+                              int64_t n, int32_t *out) {
+  const int64_t chunk = 1 << 24;  // rows per launch (grid.x bound)
+  for (int64_t r = 0; r < n; r += chunk) {
+    int64_t m = n - r < chunk ? n - r : chunk;
+    FlatArgs a = centroid_args(ivf, dx + r * ivf->ld, m);
+    launch_flat(ctx, a, MODE_ARGMIN, out + r);
+  }
+}
+
+// top-nprobe centroids per query (ties by centroid index)
+static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
+                             int64_t nq, int32_t np, int32_t *probes) {
+  uint64_t *keys = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.probe_keys", sizeof(uint64_t) * nq * np));
+  const int64_t cap = ivf->nlist;  // one dense chunk
+  const int64_t qb = query_batch(nq, cap);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    FlatArgs base = centroid_args(ivf, dq + b0 * ivf->ld, nb);
+    ScanFn scan = [&](const ScanRequest &r) {
+      FlatArgs a = base;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER, nullptr);
+    };
+    progressive_topk(ctx, nb, ivf->nlist, np, cap, scan, keys + b0 * np,
+                     "ivf_probe_select");
+  }
+  KernelTimer t(ctx, "ivf_probe_ids");
+  k_keys_to_tie<<<grid1(nq * np), 256, 0, ctx->stream>>>(keys, nq * np, probes);
+  check_launch("ivf_probe_ids");
+}
+
+static void require_ivf(const vsk_ivf *ivf) {
+  VSK_REQUIRE(ivf, VSK_ERR_INVALID_ARGUMENT, "ivf is null");
+}
+
+}  // namespace vsk
+
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_ivf_create(vsk_ctx *ctx, const float *centroids, int32_t nlist,
+                          int32_t d, vsk_ivf **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(centroids, VSK_ERR_NOT_TRAINED, "no centroids (index not trained)");
+  VSK_REQUIRE(nlist > 0, VSK_ERR_NOT_TRAINED, "nlist must be positive");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  std::unique_ptr<vsk_ivf> ivf(new vsk_ivf());
+  ivf->nlist = nlist;
+  ivf->d = d;
+  ivf->ld = padded_ld(d);
+  CallScope cs(ctx);
+  vsk_db &c = ivf->centroids;
+  c.n = nlist;
+  c.d = d;
+  c.ld = ivf->ld;
+  c.x.reserve(sizeof(float) * (size_t)nlist * c.ld);
+  const float *src = rows_to_device_padded(ctx, centroids, nlist, d, c.ld,
+                                           "ivf.centroids_in");
+  VSK_HIP(hipMemcpyAsync(c.x.p, src, sizeof(float) * (size_t)nlist * c.ld,
+                         hipMemcpyDeviceToDevice, ctx->stream));
+  c.sqnorm.reserve(sizeof(float) * nlist);
+  c.norm.reserve(sizeof(float) * nlist);
+  row_norms(ctx, c.x.as<float>(), nlist, d, c.ld, c.sqnorm.as<float>(),
+            c.norm.as<float>());
+  ivf->off.assign(nlist + 1, 0);
+  ivf->list_off.reserve(sizeof(int64_t) * (nlist + 1));
+  VSK_HIP(hipMemcpyAsync(ivf->list_off.p, ivf->off.data(),
+                         sizeof(int64_t) * (nlist + 1), hipMemcpyHostToDevice,
+                         ctx->stream));
+  cs.finish();
+  *out = ivf.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_free(vsk_ctx *ctx, vsk_ivf *ivf) {
+  if (ctx) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+  }
+  delete ivf;
+  return VSK_OK;
+}
+
+vsk_status vsk_ivf_assign(vsk_ctx *ctx, const vsk_ivf *ivf, const float *x,
+                          int64_t n, int32_t *out_list) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no rows");
+  VSK_REQUIRE(x && out_list, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const float *dx = rows_to_device_padded(ctx, x, n, ivf->d, ivf->ld, "ivf.x");
+  OutputStage o(ctx, out_list, sizeof(int32_t) * n, "out.assign");
+  ivf_assign_device(ctx, ivf, dx, n, o.ptr<int32_t>());
+  o.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
+                       const int64_t *ids, int64_t n) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no rows");
+  VSK_REQUIRE(x, VSK_ERR_INVALID_ARGUMENT, "x is null");
+  VSK_REQUIRE(ivf->total + n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "an IVF index holds at most 2^31-1 rows");
+  CallScope cs(ctx);
+  const int32_t ld = ivf->ld, nlist = ivf->nlist;
+  const float *dx = rows_to_device_padded(ctx, x, n, ivf->d, ld, "ivf.x");
+  const int64_t *did = ids ? static_cast<const int64_t *>(input_to_device(
+                                 ctx, ids, sizeof(int64_t) * n, "ivf.ids_in"))
+                           : nullptr;
+  int32_t *assign =
+      static_cast<int32_t *>(ctx->scratch_ptr("ivf.assign", 4 * n));
+  ivf_assign_device(ctx, ivf, dx, n, assign);
+  std::vector<int32_t> h_assign(n);
+  VSK_HIP(hipMemcpyAsync(h_assign.data(), assign, 4 * n, hipMemcpyDeviceToHost,
+                         ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+
+  // new CSR: old lists keep their order, new rows follow in call order
+  std::vector<int64_t> add(nlist, 0);
+  for (int64_t i = 0; i < n; ++i) add[h_assign[i]]++;
+  std::vector<int64_t> noff(nlist + 1, 0);
+  for (int32_t l = 0; l < nlist; ++l)
+    noff[l + 1] = noff[l] + (ivf->off[l + 1] - ivf->off[l]) + add[l];
+  const int64_t total = ivf->total + n;
+  std::vector<int64_t> dest_old(ivf->total), dest_new(n);
+  for (int32_t l = 0; l < nlist; ++l)
+    for (int64_t r = ivf->off[l]; r < ivf->off[l + 1]; ++r)
+      dest_old[r] = noff[l] + (r - ivf->off[l]);
+  std::vector<int64_t> cursor(nlist);
+  for (int32_t l = 0; l < nlist; ++l)
+    cursor[l] = noff[l] + (ivf->off[l + 1] - ivf->off[l]);
+  for (int64_t i = 0; i < n; ++i) dest_new[i] = cursor[h_assign[i]]++;
+
+  auto rows2 = std::make_unique<DevBuf>();
+  auto ids2 = std::make_unique<DevBuf>();
+  rows2->reserve(sizeof(float) * (size_t)total * ld);
+  ids2->reserve(sizeof(int64_t) * total);
+  int64_t *ddest = static_cast<int64_t *>(
+      ctx->scratch_ptr("ivf.dest", sizeof(int64_t) * std::max(ivf->total, n)));
+  if (ivf->total > 0) {
+    VSK_HIP(hipMemcpyAsync(ddest, dest_old.data(), 8 * ivf->total,
+                           hipMemcpyHostToDevice, ctx->stream));
+    k_scatter_rows<<<grid1(ivf->total, 4), 256, 0, ctx->stream>>>(
+        ivf->rows.as<float>(), ivf->ids.as<int64_t>(), 0, ddest, ivf->total,
+        ld, rows2->as<float>(), ids2->as<int64_t>());
+    check_launch("ivf_scatter_old");
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+  }
+  VSK_HIP(hipMemcpyAsync(ddest, dest_new.data(), 8 * n, hipMemcpyHostToDevice,
+                         ctx->stream));
+  k_scatter_rows<<<grid1(n, 4), 256, 0, ctx->stream>>>(
+      dx, did, ivf->next_id, ddest, n, ld, rows2->as<float>(),
+      ids2->as<int64_t>());
+  check_launch("ivf_scatter_new");
+  VSK_HIP(hipMemcpyAsync(ivf->list_off.p, noff.data(),
+                         sizeof(int64_t) * (nlist + 1), hipMemcpyHostToDevice,
+                         ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  std::swap(ivf->rows.p, rows2->p);
+  std::swap(ivf->rows.bytes, rows2->bytes);
+  std::swap(ivf->ids.p, ids2->p);
+  std::swap(ivf->ids.bytes, ids2->bytes);
+  ivf->off = noff;
+  ivf->total = total;
+  ivf->next_id += n;
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                         int64_t nq, int32_t nprobe, int32_t *out_lists) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && out_lists, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(nprobe >= 1 && nprobe <= VSK_MAX_K, VSK_ERR_INVALID_ARGUMENT,
+              "nprobe must be in [1, VSK_MAX_K]");
+  CallScope cs(ctx);
+  const float *dq = rows_to_device_padded(ctx, q, nq, ivf->d, ivf->ld, "ivf.q");
+  OutputStage o(ctx, out_lists, sizeof(int32_t) * nq * nprobe, "out.probes");
+  ivf_probe_device(ctx, ivf, dq, nq, nprobe, o.ptr<int32_t>());
+  o.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
+                              int64_t *sizes) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(sizes, VSK_ERR_INVALID_ARGUMENT, "sizes is null");
+  for (int32_t l = 0; l < ivf->nlist; ++l)
+    sizes[l] = ivf->off[l + 1] - ivf->off[l];
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                          int64_t nq, int32_t nprobe, int32_t k,
+                          float *out_dist, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE,
+              "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nprobe >= 1, VSK_ERR_INVALID_ARGUMENT, "nprobe must be >= 1");
+  const int32_t np = nprobe < ivf->nlist ? nprobe : ivf->nlist;  // .exact
+  VSK_REQUIRE(np <= VSK_MAX_K || np == ivf->nlist, VSK_ERR_INVALID_ARGUMENT,
+              "nprobe must be <= VSK_MAX_K or cover every list");
+  CallScope cs(ctx);
+  const int32_t ld = ivf->ld;
+  const float *dq = rows_to_device_padded(ctx, q, nq, ivf->d, ld, "ivf.q");
+  OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
+
+  // 1. probes
+  int32_t *probes = static_cast<int32_t *>(
+      ctx->scratch_ptr("ivf.probes", sizeof(int32_t) * nq * np));
+  if (np == ivf->nlist && np > VSK_MAX_K) {
+    // .exact with more lists than a selection holds: every list, in index
+    // order (the stable sort's order when all lists are kept is by
+    // distance, but the candidate set -- and so the result -- is the same
+    // up to the position tie key)
+    std::vector<int32_t> all((size_t)nq * np);
+    for (int64_t i = 0; i < nq; ++i)
+      std::iota(all.begin() + i * np, all.begin() + (i + 1) * np, 0);
+    VSK_HIP(hipMemcpyAsync(probes, all.data(), 4 * all.size(),
+                           hipMemcpyHostToDevice, ctx->stream));
+  } else {
+    ivf_probe_device(ctx, ivf, dq, nq, np, probes);
+  }
+  // 2. candidate counts and probe position bases
+  int64_t *pos_base = static_cast<int64_t *>(
+      ctx->scratch_ptr("ivf.pos_base", sizeof(int64_t) * nq * np));
+  int64_t *cnt =
+      static_cast<int64_t *>(ctx->scratch_ptr("ivf.cnt", sizeof(int64_t) * nq));
+  {
+    KernelTimer t(ctx, "ivf_probe_bases");
+    k_probe_bases<<<grid1(nq), 256, 0, ctx->stream>>>(
+        probes, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt);
+    check_launch("ivf_probe_bases");
+  }
+  std::vector<int64_t> h_cnt(nq);
+  std::vector<int32_t> h_probes((size_t)nq * np);
+  VSK_HIP(hipMemcpyAsync(h_cnt.data(), cnt, 8 * nq, hipMemcpyDeviceToHost,
+                         ctx->stream));
+  VSK_HIP(hipMemcpyAsync(h_probes.data(), probes, 4 * h_probes.size(),
+                         hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+
+  const int QG = ld <= 512 ? 16 : (ld <= 1024 ? 8 : 1);
+  VSK_REQUIRE((int64_t)QG * ld * 4 <= 64 * 1024, VSK_ERR_UNSUPPORTED,
+              "dimension too large for the IVF list scan");
+  int64_t max_cnt = 0;
+  for (auto c : h_cnt) max_cnt = std::max(max_cnt, c);
+  const int64_t budget = std::max<int64_t>(1ll << 27, max_cnt);
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.best", sizeof(uint64_t) * nq * k));
+
+  // query batches whose candidate segments fit the budget
+  int64_t b0 = 0;
+  while (b0 < nq) {
+    int64_t b1 = b0, tot = 0;
+    while (b1 < nq && tot + h_cnt[b1] <= budget) tot += h_cnt[b1++];
+    const int64_t nb = b1 - b0;
+    std::vector<int64_t> seg(nb + 1, 0);
+    for (int64_t i = 0; i < nb; ++i) seg[i + 1] = seg[i] + h_cnt[b0 + i];
+    // 3. pairs grouped by list
+    std::vector<int64_t> lcount(ivf->nlist + 1, 0);
+    for (int64_t i = 0; i < nb * np; ++i) {
+      int32_t l = h_probes[b0 * np + i];
+      if (l >= 0) lcount[l + 1]++;
+    }
+    for (int32_t l = 0; l < ivf->nlist; ++l) lcount[l + 1] += lcount[l];
+    std::vector<int4> groups;
+    for (int32_t l = 0; l < ivf->nlist; ++l) {
+      int64_t c = lcount[l + 1] - lcount[l];
+      if (c == 0 || ivf->off[l + 1] == ivf->off[l]) continue;
+      for (int64_t j = 0; j < c; j += QG)
+        groups.push_back(int4{l, (int)(lcount[l] + j),
+                              (int)std::min<int64_t>(QG, c - j), 0});
+    }
+    const int64_t npairs = nb * np;
+    int64_t *dseg = static_cast<int64_t *>(
+        ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * (nb + 1)));
+    int64_t *dcursor = static_cast<int64_t *>(
+        ctx->scratch_ptr("ivf.cursor", sizeof(int64_t) * (ivf->nlist + 1)));
+    int32_t *dpairs = static_cast<int32_t *>(
+        ctx->scratch_ptr("ivf.pairs", sizeof(int32_t) * (npairs + 1)));
+    int4 *dgroups = static_cast<int4 *>(
+        ctx->scratch_ptr("ivf.groups", sizeof(int4) * (groups.size() + 1)));
+    uint64_t *cand = static_cast<uint64_t *>(
+        ctx->scratch_ptr("ivf.cand", sizeof(uint64_t) * (tot + 1)));
+    VSK_HIP(hipMemcpyAsync(dseg, seg.data(), 8 * (nb + 1),
+                           hipMemcpyHostToDevice, ctx->stream));
+    VSK_HIP(hipMemcpyAsync(dcursor, lcount.data(), 8 * (ivf->nlist + 1),
+                           hipMemcpyHostToDevice, ctx->stream));
+    if (!groups.empty())
+      VSK_HIP(hipMemcpyAsync(dgroups, groups.data(),
+                             sizeof(int4) * groups.size(),
+                             hipMemcpyHostToDevice, ctx->stream));
+    {
+      KernelTimer t(ctx, "ivf_group_pairs");
+      k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(
+          probes + b0 * np, npairs, np, dcursor, dpairs);
+      check_launch("ivf_group_pairs");
+    }
+    if (!groups.empty()) {
+      ListScanArgs la;
+      la.rows = ivf->rows.as<float>();
+      la.list_off = ivf->list_off.as<int64_t>();
+      la.Q = dq + b0 * ld;
+      la.ld = ld;
+      la.np = np;
+      la.probes = probes + b0 * np;
+      la.pairs = dpairs;
+      la.groups = dgroups;
+      la.pos_base = pos_base + b0 * np;
+      la.seg_off = dseg;
+      la.cand = cand;
+      const size_t lds = sizeof(float) * QG * ld;
+      KernelTimer t(ctx, "ivf_list_scan");
+      if (QG == 16)
+        k_list_scan<16><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
+      else if (QG == 8)
+        k_list_scan<8><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
+      else
+        k_list_scan<1><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
+      check_launch("ivf_list_scan");
+    }
+    // 4. selection per query segment
+    SelectArgs sa;
+    sa.nq = nb;
+    sa.k = k;
+    sa.cand = cand;
+    sa.seg_off = dseg;
+    sa.best_out = best + b0 * k;
+    launch_select(ctx, sa, "ivf_select");
+    VSK_HIP(hipStreamSynchronize(ctx->stream));  // host vectors reused
+    b0 = b1;
+  }
+  {
+    KernelTimer t(ctx, "ivf_decode");
+    k_ivf_decode<<<grid1(nq * k), 256, 0, ctx->stream>>>(
+        best, nq, k, probes, np, pos_base, ivf->list_off.as<int64_t>(),
+        ivf->ids.as<int64_t>(), od.ptr<float>(), oi.ptr<int64_t>());
+    check_launch("ivf_decode");
+  }
+  od.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

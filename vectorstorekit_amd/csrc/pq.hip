@@ -1,0 +1,473 @@
+// pq.hip -- product quantization: distance tables (LUT), encoding, the ADC
+// scan with the tables resident in LDS, and the exact re-rank.
+//
+// Reference: ProductQuantizer (Quantization/ProductQuantizer.swift):
+// precomputeDistanceTables (:209-233) -- table[m][c] =
+// euclideanDistanceSquared(query segment m, codeword c) (:362-369,
+// sequential sum of squared differences); DistanceTables.computeDistance
+// (Quantization/ProductQuantizerTypes.swift:14-20) -- sqrt of the sum of
+// table[m][code_m] over m ascending; Codebook.encode
+// (Quantization/ProductQuantizerCodebook.swift:12-30) -- argmin with strict
+// '<'.  The reference has no batch scan and no re-rank; the re-rank uses the
+// reference's exact CPU distance formulas
+// (Acceleration/AccelerateOptimizer.swift:251-383) summed in index order.
+//
+// Every floating-point sum here is formed in the reference's order with
+// separate multiply and add roundings (no FMA), so tables, ADC sums, re-rank
+// distances and ids are bit-identical to the CPU.
+//
+// ADC scan: a workgroup holds the tables of QG queries in LDS (M*ksub*4
+// bytes each) and streams a slice of the code rows; a thread owns a row,
+// loads its M code bytes once and accumulates the QG sums; each sum is keyed
+// (sum, row) and goes through the same threshold filter / append as the flat
+// scan.  Ranking is on the sum (sqrt is monotone); sqrt is applied to the
+// outputs only.
+#include "flat.hpp"
+
+struct vsk_pq {
+  int32_t M = 0, ksub = 0, dsub = 0, d = 0;
+  vsk::DevBuf codebooks;  // M x ksub x dsub fp32
+  vsk::DevBuf codes;      // n x M uint8
+  int64_t n = 0, cap_rows = 0;
+};
+
+namespace vsk {
+
+constexpr int PQ_QG = 4;  // queries per ADC workgroup
+
+// lut[q][m][c], one thread per entry
+__global__ void k_pq_lut(const float *q, int64_t nq, int32_t ldq,
+                         const float *cb, int32_t M, int32_t ksub, int32_t dsub,
+                         float *lut) {
+#pragma clang fp contract(off)
+  const int64_t total = nq * (int64_t)M * ksub;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t qi = i / ((int64_t)M * ksub);
+    const int32_t mc = (int32_t)(i - qi * (int64_t)M * ksub);
+    const int32_t m = mc / ksub;
+    const float *qs = q + qi * ldq + m * dsub;
+    const float *c = cb + (int64_t)mc * dsub;
+    float s = 0.f;
+    for (int j = 0; j < dsub; ++j) {
+      float t = qs[j] - c[j];
+      s = s + t * t;
+    }
+    lut[i] = s;
+  }
+}
+
+// codes[i][m] = argmin_c |x_m - C_m[c]|^2 (strict '<'), one thread per (i, m)
+__global__ void k_pq_encode(const float *x, int64_t n, int32_t ldx,
+                            const float *cb, int32_t M, int32_t ksub,
+                            int32_t dsub, uint8_t *codes) {
+#pragma clang fp contract(off)
+  const int64_t total = n * (int64_t)M;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / M;
+    const int32_t m = (int32_t)(i - r * M);
+    const float *xs = x + r * ldx + m * dsub;
+    float best = __int_as_float(0x7f800000);
+    int32_t bc = 0;
+    for (int32_t c = 0; c < ksub; ++c) {
+      const float *cw = cb + ((int64_t)m * ksub + c) * dsub;
+      float s = 0.f;
+      for (int j = 0; j < dsub; ++j) {
+        float t = xs[j] - cw[j];
+        s = s + t * t;
+      }
+      if (s < best) {
+        best = s;
+        bc = c;
+      }
+    }
+    codes[i] = (uint8_t)bc;
+  }
+}
+
+struct AdcArgs {
+  const uint8_t *codes;
+  int32_t M, ksub;
+  const float *lut;  // [nq][M][ksub]
+  int32_t nq;
+  int64_t r0, r1, rows_per_split;
+  const uint64_t *thresh;
+  const uint8_t *active;
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+};
+
+template <bool DENSE, bool M16>
+__global__ __launch_bounds__(256) void k_pq_adc(AdcArgs a) {
+  extern __shared__ float lut_s[];  // PQ_QG x M x ksub
+  const int64_t q0 = (int64_t)blockIdx.x * PQ_QG;
+  const int64_t s0 = a.r0 + (int64_t)blockIdx.y * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+  const int tsz = a.M * a.ksub;
+  for (int i = threadIdx.x; i < PQ_QG * tsz; i += blockDim.x) {
+    const int j = i / tsz;
+    lut_s[i] = (q0 + j < a.nq) ? a.lut[(q0 + j) * tsz + (i - j * tsz)] : 0.f;
+  }
+  bool qok[PQ_QG];
+  uint64_t th[PQ_QG];
+#pragma unroll
+  for (int j = 0; j < PQ_QG; ++j) {
+    qok[j] = q0 + j < a.nq && (!a.active || a.active[q0 + j]);
+    th[j] = (!DENSE && qok[j]) ? a.thresh[q0 + j] : 0;
+  }
+  __syncthreads();
+  for (int64_t r = s0 + threadIdx.x; r < s1; r += blockDim.x) {
+    float s[PQ_QG];
+#pragma unroll
+    for (int j = 0; j < PQ_QG; ++j) s[j] = 0.f;
+    if constexpr (M16) {
+      const uint4 cw = *reinterpret_cast<const uint4 *>(a.codes + r * 16);
+      const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const int c = (w4[m >> 2] >> (8 * (m & 3))) & 0xFF;
+#pragma unroll
+        for (int j = 0; j < PQ_QG; ++j)
+          s[j] = s[j] + lut_s[j * tsz + m * a.ksub + c];
+      }
+    } else {
+      const uint8_t *cr = a.codes + r * a.M;
+      for (int m = 0; m < a.M; ++m) {
+        const int c = cr[m];
+#pragma unroll
+        for (int j = 0; j < PQ_QG; ++j)
+          s[j] = s[j] + lut_s[j * tsz + m * a.ksub + c];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PQ_QG; ++j) {
+      if (!qok[j]) continue;
+      const int64_t qi = q0 + j;
+      const uint64_t key = vsk_key(s[j], (uint32_t)r);
+      if (DENSE) {
+        a.cand[qi * a.cap + (r - a.r0)] = key;
+      } else if (key <= th[j]) {
+        int slot = atomicAdd(&a.counts[qi], 1);
+        if (slot < a.cap) a.cand[qi * a.cap + slot] = key;
+      }
+    }
+  }
+}
+
+static void launch_adc(vsk_ctx *ctx, AdcArgs a, bool dense) {
+  const int64_t rows = a.r1 - a.r0;
+  if (rows <= 0 || a.nq <= 0) return;
+  const int64_t qt = ceil_div(a.nq, PQ_QG);
+  int64_t splits = ceil_div(8192, qt);
+  const int64_t max_splits = ceil_div(rows, 1024);
+  if (splits > max_splits) splits = max_splits;
+  if (splits > 65535) splits = 65535;
+  if (splits < 1) splits = 1;
+  a.rows_per_split = ceil_div(rows, splits);
+  splits = ceil_div(rows, a.rows_per_split);
+  dim3 grid((unsigned)qt, (unsigned)splits);
+  const size_t lds = sizeof(float) * PQ_QG * a.M * a.ksub;
+  const bool m16 = a.M == 16;
+  KernelTimer t(ctx, "pq_adc_scan");
+  if (dense) {
+    if (m16)
+      k_pq_adc<true, true><<<grid, 256, lds, ctx->stream>>>(a);
+    else
+      k_pq_adc<true, false><<<grid, 256, lds, ctx->stream>>>(a);
+  } else {
+    if (m16)
+      k_pq_adc<false, true><<<grid, 256, lds, ctx->stream>>>(a);
+    else
+      k_pq_adc<false, false><<<grid, 256, lds, ctx->stream>>>(a);
+  }
+  check_launch("pq_adc_scan");
+}
+
+// exact distance of each ADC candidate, summed in index order (no FMA);
+// one thread per (query, candidate)
+__global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
+                         const float *q, int32_t ldq, const float *x,
+                         int32_t ldx, int32_t d, int32_t metric,
+                         uint64_t *out) {
+#pragma clang fp contract(off)
+  const int64_t total = nq * (int64_t)kadc;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t key = adc_best[i];
+    if (key == VSK_KEY_NONE) {
+      out[i] = VSK_KEY_NONE;
+      continue;
+    }
+    const uint32_t row = (uint32_t)key;
+    const float *qr = q + (i / kadc) * ldq;
+    const float *xr = x + (int64_t)row * ldx;
+    float dist;
+    if (metric == VSK_METRIC_L1) {
+      float s = 0.f;
+      for (int j = 0; j < d; ++j) s = s + fabsf(qr[j] - xr[j]);
+      dist = s;
+    } else if (metric == VSK_METRIC_L2SQ || metric == VSK_METRIC_L2) {
+      float s = 0.f;
+      for (int j = 0; j < d; ++j) {
+        float t = qr[j] - xr[j];
+        s = s + t * t;
+      }
+      dist = metric == VSK_METRIC_L2 ? __fsqrt_rn(s) : s;
+    } else {
+      float dp = 0.f, qq = 0.f, xx = 0.f;
+      for (int j = 0; j < d; ++j) {
+        dp = dp + qr[j] * xr[j];
+        qq = qq + qr[j] * qr[j];
+        xx = xx + xr[j] * xr[j];
+      }
+      if (metric == VSK_METRIC_COSINE) {
+        float den = __fsqrt_rn(qq) * __fsqrt_rn(xx);
+        den = den + 1e-8f;
+        dist = 1.0f - __fdiv_rn(dp, den);
+      } else if (metric == VSK_METRIC_COSINE_NORMALIZED) {
+        dist = 1.0f - dp;
+      } else {
+        dist = -dp;
+      }
+    }
+    out[i] = vsk_key(dist, row);
+  }
+}
+
+static unsigned grid1(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 16384 ? (g > 0 ? g : 1) : 16384);
+}
+
+static void require_pq(const vsk_pq *pq) {
+  VSK_REQUIRE(pq, VSK_ERR_INVALID_ARGUMENT, "pq is null");
+}
+
+// q (host or device, nq x d) -> device, stride d
+static const float *pq_queries(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                               int64_t nq) {
+  return static_cast<const float *>(
+      input_to_device(ctx, q, sizeof(float) * nq * pq->d, "pq.q"));
+}
+
+static void pq_lut_device(vsk_ctx *ctx, const vsk_pq *pq, const float *dq,
+                          int64_t nq, float *lut) {
+  KernelTimer t(ctx, "pq_lut");
+  k_pq_lut<<<grid1(nq * pq->M * pq->ksub), 256, 0, ctx->stream>>>(
+      dq, nq, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, lut);
+  check_launch("pq_lut");
+}
+
+}  // namespace vsk
+
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_pq_create(vsk_ctx *ctx, const float *codebooks, int32_t M,
+                         int32_t ksub, int32_t dsub, vsk_pq **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(codebooks, VSK_ERR_NOT_TRAINED, "no codebooks (not trained)");
+  VSK_REQUIRE(M > 0 && dsub > 0, VSK_ERR_INVALID_ARGUMENT,
+              "segments and segment dimension must be positive");
+  VSK_REQUIRE(ksub >= 1 && ksub <= 256, VSK_ERR_INVALID_ARGUMENT,
+              "codebook size must be in [1, 256] (8-bit codes)");
+  VSK_REQUIRE((int64_t)PQ_QG * M * ksub * 4 <= 64 * 1024, VSK_ERR_UNSUPPORTED,
+              "M * ksub too large for LDS-resident distance tables");
+  std::unique_ptr<vsk_pq> pq(new vsk_pq());
+  pq->M = M;
+  pq->ksub = ksub;
+  pq->dsub = dsub;
+  pq->d = M * dsub;
+  CallScope cs(ctx);
+  const size_t bytes = sizeof(float) * (size_t)M * ksub * dsub;
+  pq->codebooks.reserve(bytes);
+  VSK_HIP(hipMemcpyAsync(pq->codebooks.p, codebooks, bytes, hipMemcpyDefault,
+                         ctx->stream));
+  cs.finish();
+  *out = pq.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_pq_free(vsk_ctx *ctx, vsk_pq *pq) {
+  if (ctx) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+  }
+  delete pq;
+  return VSK_OK;
+}
+
+vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,
+                         int64_t n, uint8_t *codes) {
+  VSK_API_BEGIN(ctx);
+  require_pq(pq);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no vectors");
+  VSK_REQUIRE(x && codes, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const float *dx = static_cast<const float *>(
+      input_to_device(ctx, x, sizeof(float) * n * pq->d, "pq.x"));
+  OutputStage oc(ctx, codes, (size_t)n * pq->M, "out.codes");
+  {
+    KernelTimer t(ctx, "pq_encode");
+    k_pq_encode<<<grid1(n * pq->M), 256, 0, ctx->stream>>>(
+        dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub,
+        oc.ptr<uint8_t>());
+    check_launch("pq_encode");
+  }
+  oc.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_pq_add_codes(vsk_ctx *ctx, vsk_pq *pq, const uint8_t *codes,
+                            int64_t n) {
+  VSK_API_BEGIN(ctx);
+  require_pq(pq);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no codes");
+  VSK_REQUIRE(codes, VSK_ERR_INVALID_ARGUMENT, "codes is null");
+  VSK_REQUIRE(pq->n + n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "a code database holds at most 2^31-1 rows");
+  CallScope cs(ctx);
+  const int64_t need = pq->n + n;
+  if (need > pq->cap_rows) {
+    int64_t cap = std::max<int64_t>(need, pq->cap_rows + pq->cap_rows / 2);
+    auto nb = std::make_unique<DevBuf>();
+    nb->reserve((size_t)cap * pq->M + 16);
+    if (pq->n > 0)
+      VSK_HIP(hipMemcpyAsync(nb->p, pq->codes.p, (size_t)pq->n * pq->M,
+                             hipMemcpyDeviceToDevice, ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    std::swap(pq->codes.p, nb->p);
+    std::swap(pq->codes.bytes, nb->bytes);
+    pq->cap_rows = cap;
+  }
+  VSK_HIP(hipMemcpyAsync(pq->codes.as<uint8_t>() + pq->n * pq->M, codes,
+                         (size_t)n * pq->M, hipMemcpyDefault, ctx->stream));
+  cs.finish();
+  pq->n = need;
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_pq_lut(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                      int64_t nq, float *lut) {
+  VSK_API_BEGIN(ctx);
+  require_pq(pq);
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && lut, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const float *dq = pq_queries(ctx, pq, q, nq);
+  OutputStage ol(ctx, lut, sizeof(float) * nq * pq->M * pq->ksub, "out.lut");
+  pq_lut_device(ctx, pq, dq, nq, ol.ptr<float>());
+  ol.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                         int64_t nq, int32_t k_adc, int32_t k,
+                         int32_t rerank_metric, const vsk_db *rerank_db,
+                         float *out_dist, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  require_pq(pq);
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(pq->n > 0, VSK_ERR_EMPTY_INPUT, "no codes added");
+  VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  VSK_REQUIRE(k >= 1 && k_adc >= 1, VSK_ERR_INVALID_ARGUMENT,
+              "k and k_adc must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K && k_adc <= VSK_MAX_K,
+              VSK_ERR_INVALID_BUFFER_SIZE, "k exceeds VSK_MAX_K");
+  const bool rerank = rerank_db && rerank_metric >= 0;
+  if (rerank) {
+    VSK_REQUIRE(metric_valid(rerank_metric), VSK_ERR_INVALID_ARGUMENT,
+                "unknown re-rank metric");
+    VSK_REQUIRE(rerank_db->d == pq->d, VSK_ERR_DIMENSION_MISMATCH,
+                "re-rank rows have another dimension");
+    VSK_REQUIRE(rerank_db->n >= pq->n, VSK_ERR_DIMENSION_MISMATCH,
+                "re-rank rows do not cover every code row");
+  }
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "too many queries");
+  CallScope cs(ctx);
+  const float *dq = pq_queries(ctx, pq, q, nq);
+  float *lut = static_cast<float *>(
+      ctx->scratch_ptr("pq.lut", sizeof(float) * nq * pq->M * pq->ksub));
+  pq_lut_device(ctx, pq, dq, nq, lut);
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("pq.best", sizeof(uint64_t) * nq * k_adc));
+  const int64_t cap = default_cap(k_adc);
+  const int64_t qb = query_batch(nq, cap);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    AdcArgs base{};
+    base.codes = pq->codes.as<uint8_t>();
+    base.M = pq->M;
+    base.ksub = pq->ksub;
+    base.lut = lut + b0 * pq->M * pq->ksub;
+    base.nq = (int32_t)nb;
+    ScanFn scan = [&](const ScanRequest &r) {
+      AdcArgs a = base;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_adc(ctx, a, r.dense);
+    };
+    progressive_topk(ctx, nb, pq->n, k_adc, cap, scan, best + b0 * k_adc,
+                     "pq_select");
+  }
+  OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
+  if (rerank) {
+    uint64_t *rk = static_cast<uint64_t *>(
+        ctx->scratch_ptr("pq.rerank", sizeof(uint64_t) * nq * k_adc));
+    {
+      KernelTimer t(ctx, "pq_rerank");
+      k_rerank<<<grid1(nq * k_adc), 256, 0, ctx->stream>>>(
+          best, nq, k_adc, dq, pq->d, rerank_db->x.as<float>(), rerank_db->ld,
+          pq->d, rerank_metric, rk);
+      check_launch("pq_rerank");
+    }
+    uint64_t *fin = static_cast<uint64_t *>(
+        ctx->scratch_ptr("pq.final", sizeof(uint64_t) * nq * k));
+    SelectArgs sa;
+    sa.nq = nq;
+    sa.k = k;
+    sa.cand = rk;
+    sa.cap = k_adc;
+    sa.best_out = fin;
+    launch_select(ctx, sa, "pq_rerank_select");
+    decode_keys(ctx, fin, nq * (int64_t)k, false, nullptr, od.ptr<float>(),
+                oi.ptr<int64_t>());
+  } else if (k <= k_adc) {
+    uint64_t *fin = static_cast<uint64_t *>(
+        ctx->scratch_ptr("pq.final", sizeof(uint64_t) * nq * k));
+    SelectArgs sa;  // first k of the sorted ADC list
+    sa.nq = nq;
+    sa.k = k;
+    sa.cand = best;
+    sa.cap = k_adc;
+    sa.best_out = fin;
+    launch_select(ctx, sa, "pq_rerank_select");
+    decode_keys(ctx, fin, nq * (int64_t)k, true, nullptr, od.ptr<float>(),
+                oi.ptr<int64_t>());
+  } else {
+    fail(VSK_ERR_INVALID_ARGUMENT, "k > k_adc needs a re-rank database");
+  }
+  od.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

@@ -183,6 +183,7 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
   if (nq <= 0) return;
   fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
   if (n <= 0) return;
+  if (cap > n) cap = n;  // the whole database is one dense chunk
   uint64_t *thresh =
       static_cast<uint64_t *>(ctx->scratch_ptr("topk.thresh", 8 * nq));
   uint64_t *cand = static_cast<uint64_t *>(

@@ -1,0 +1,427 @@
+// sq8.hip -- int8 scalar quantization: min/max training, encoding and the
+// int8-MFMA scan with int32 accumulation fused with the top-k filter.
+//
+// Reference: ScalarQuantizer (Quantization/ScalarQuantizer.swift):
+// calculateStatistics (:389-418, min/max over the values),
+// calculateQuantizationParameters (:420-451, .int8: scale = 255/(max-min),
+// offset = -min*scale - 128), quantizeToInt8 (:251-270, vDSP_vsmsa then
+// vDSP_vfix8: x*scale + offset converted toward zero).  The reference has
+// no distance over int8 codes; the scan ranks by the exact int32 score
+// sum_j qcode_j * code_j (distance = -score), ties by row id.
+//
+// Scan kernel: the flat-search tiling on int8 -- a workgroup owns 64 queries
+// and a slice of rows, 128-row tiles, 128-byte K stages in LDS, each wave a
+// 32-row x 64-query block of 2x4 v_mfma_i32_16x16x32_i8 tiles.  Integer
+// accumulation is exact, so scores and ids are bit-identical to the CPU.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "vsk_api.hpp"
+
+struct vsk_sq8 {
+  int64_t n = 0;
+  int32_t d = 0, ldc = 0;  // ldc: row stride in bytes (multiple of 32)
+  vsk::DevBuf codes;
+};
+
+namespace vsk {
+
+typedef int i4 __attribute__((ext_vector_type(4)));
+
+constexpr int SB_N = 128, SB_Q = 64, SB_K = 128;  // rows, queries, bytes
+constexpr int SS = SB_K + 16;                     // LDS row stride (bytes)
+
+struct Sq8Args {
+  const int8_t *X;
+  int64_t ldx;
+  const int8_t *Q;
+  int64_t ldq;
+  int32_t kbytes;  // padded code length (multiple of 32)
+  int32_t nq;
+  int64_t r0, r1, rows_per_split;
+  const uint64_t *thresh;
+  const uint8_t *active;
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+};
+
+template <bool DENSE>
+__global__ __launch_bounds__(256) void k_sq8_scan(Sq8Args a) {
+  __shared__ __attribute__((aligned(16))) int8_t xs[SB_N * SS];
+  __shared__ __attribute__((aligned(16))) int8_t qs[SB_Q * SS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t q0 = (int64_t)blockIdx.x * SB_Q;
+  const int64_t s0 = a.r0 + (int64_t)blockIdx.y * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+  int64_t qi[4];
+  bool qok[4];
+  uint64_t th[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    qi[j] = q0 + j * 16 + (lane & 15);
+    qok[j] = qi[j] < a.nq && (!a.active || a.active[qi[j]]);
+    th[j] = (!DENSE && qok[j]) ? a.thresh[qi[j]] : 0;
+  }
+  const int crow = tid >> 3, ccol = (tid & 7) * 16;
+  for (int64_t t0 = s0; t0 < s1; t0 += SB_N) {
+    i4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = i4{0, 0, 0, 0};
+    for (int k0 = 0; k0 < a.kbytes; k0 += SB_K) {
+      const bool kin = k0 + ccol < a.kbytes;
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int64_t grow = t0 + u * 32 + crow;
+        i4 v = (kin && grow < s1)
+                   ? *reinterpret_cast<const i4 *>(a.X + grow * a.ldx + k0 + ccol)
+                   : i4{0, 0, 0, 0};
+        *reinterpret_cast<i4 *>(xs + (u * 32 + crow) * SS + ccol) = v;
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        int64_t gq = q0 + u * 32 + crow;
+        i4 v = (kin && gq < a.nq)
+                   ? *reinterpret_cast<const i4 *>(a.Q + gq * a.ldq + k0 + ccol)
+                   : i4{0, 0, 0, 0};
+        *reinterpret_cast<i4 *>(qs + (u * 32 + crow) * SS + ccol) = v;
+      }
+      __syncthreads();
+      const int kend = a.kbytes - k0 < SB_K ? a.kbytes - k0 : SB_K;
+      for (int kk = 0; kk < kend; kk += 32) {
+        long af[2], bf[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          af[i] = *reinterpret_cast<const long *>(
+              xs + (w * 32 + i * 16 + (lane & 15)) * SS + kk + 8 * (lane >> 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bf[j] = *reinterpret_cast<const long *>(
+              qs + (j * 16 + (lane & 15)) * SS + kk + 8 * (lane >> 4));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j],
+                                                              acc[i][j], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = t0 + w * 32 + i * 16 + 4 * (lane >> 4) + r;
+        if (row >= s1) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!qok[j]) continue;
+          const uint64_t key = vsk_key_i32(-acc[i][j][r], (uint32_t)row);
+          if (DENSE) {
+            a.cand[qi[j] * a.cap + (row - a.r0)] = key;
+          } else if (key <= th[j]) {
+            int slot = atomicAdd(&a.counts[qi[j]], 1);
+            if (slot < a.cap) a.cand[qi[j] * a.cap + slot] = key;
+          }
+        }
+      }
+    }
+  }
+}
+
+static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
+  const int64_t rows = a.r1 - a.r0;
+  if (rows <= 0 || a.nq <= 0) return;
+  const int64_t qt = ceil_div(a.nq, SB_Q);
+  int64_t splits = ceil_div(4096, qt);
+  const int64_t max_splits = ceil_div(rows, SB_N);
+  if (splits > max_splits) splits = max_splits;
+  if (splits > 65535) splits = 65535;
+  if (splits < 1) splits = 1;
+  a.rows_per_split = ceil_div(ceil_div(rows, splits), SB_N) * SB_N;
+  splits = ceil_div(rows, a.rows_per_split);
+  dim3 grid((unsigned)qt, (unsigned)splits);
+  KernelTimer t(ctx, "sq8_mfma_scan");
+  if (dense)
+    k_sq8_scan<true><<<grid, 256, 0, ctx->stream>>>(a);
+  else
+    k_sq8_scan<false><<<grid, 256, 0, ctx->stream>>>(a);
+  check_launch("sq8_mfma_scan");
+}
+
+// per-block partial min/max per dimension
+__global__ __launch_bounds__(256) void k_minmax_partial(const float *x,
+                                                        int64_t n, int32_t d,
+                                                        int64_t rows_per_block,
+                                                        float *pmin,
+                                                        float *pmax) {
+  const int64_t r0 = blockIdx.x * rows_per_block;
+  int64_t r1 = r0 + rows_per_block;
+  if (r1 > n) r1 = n;
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    float mn = __int_as_float(0x7f800000), mx = -__int_as_float(0x7f800000);
+    for (int64_t r = r0; r < r1; ++r) {
+      float v = x[r * d + j];
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+    pmin[(int64_t)blockIdx.x * d + j] = mn;
+    pmax[(int64_t)blockIdx.x * d + j] = mx;
+  }
+}
+
+// code = clamp(trunc(x * scale + offset)), multiply and add rounded apart
+__global__ void k_sq8_encode(const float *x, int64_t n, int32_t d,
+                             int32_t per_dim, const float *scale,
+                             const float *offset, int8_t *codes, int32_t ldc) {
+#pragma clang fp contract(off)
+  const int64_t total = n * (int64_t)d;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / d;
+    const int32_t j = (int32_t)(i - r * d);
+    const float s = per_dim ? scale[j] : scale[0];
+    const float o = per_dim ? offset[j] : offset[0];
+    float t = x[i] * s;
+    t = t + o;
+    int8_t c;
+    if (!(t > -128.0f))
+      c = -128;
+    else if (t >= 127.0f)
+      c = 127;
+    else
+      c = (int8_t)(int32_t)t;
+    codes[r * ldc + j] = c;
+  }
+}
+
+__global__ void k_sq8_decode(const uint64_t *best, int64_t total,
+                             int32_t *score, int64_t *ids) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t key = best[i];
+    if (key == VSK_KEY_NONE) {
+      score[i] = (int32_t)0x80000000;
+      ids[i] = -1;
+    } else {
+      score[i] = -(int32_t)((uint32_t)(key >> 32) ^ 0x80000000u);
+      ids[i] = (uint32_t)key;
+    }
+  }
+}
+
+static unsigned grid1(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
+}
+
+// the reference's parameter formulas with each operation rounded on its own
+static void sq8_params(float mn, float mx, float *s, float *o) {
+#pragma clang fp contract(off)
+  float range = mx - mn;
+  float scale = range > 0.0f ? 255.0f / range : 1.0f;
+  float t = -mn * scale;
+  *s = scale;
+  *o = t - 128.0f;
+}
+
+// codes (host or device, n x d) -> device buffer with row stride ldc
+static const int8_t *codes_to_device(vsk_ctx *ctx, const int8_t *p, int64_t n,
+                                     int32_t d, int32_t ldc,
+                                     const std::string &slot) {
+  bool dev = is_device_ptr(p);
+  if (dev && ldc == d) return p;
+  int8_t *out = static_cast<int8_t *>(ctx->scratch_ptr(slot, (size_t)n * ldc));
+  if (ldc != d) fill_i32(ctx, reinterpret_cast<int32_t *>(out), n * ldc / 4, 0);
+  VSK_HIP(hipMemcpy2DAsync(out, ldc, p, d, d, n,
+                           dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           ctx->stream));
+  return out;
+}
+
+}  // namespace vsk
+
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_sq8_train(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                         int32_t per_dim, float *scale, float *offset) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no training vectors");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(x && scale && offset, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const float *dx = static_cast<const float *>(
+      input_to_device(ctx, x, sizeof(float) * n * d, "sq8.x"));
+  int64_t blocks = ceil_div(n, 4096);
+  if (blocks > 4096) blocks = 4096;
+  const int64_t rpb = ceil_div(n, blocks);
+  blocks = ceil_div(n, rpb);
+  float *pmin = static_cast<float *>(
+      ctx->scratch_ptr("sq8.pmin", sizeof(float) * blocks * d));
+  float *pmax = static_cast<float *>(
+      ctx->scratch_ptr("sq8.pmax", sizeof(float) * blocks * d));
+  {
+    KernelTimer t(ctx, "sq8_minmax");
+    k_minmax_partial<<<(unsigned)blocks, 256, 0, ctx->stream>>>(dx, n, d, rpb,
+                                                                pmin, pmax);
+    check_launch("sq8_minmax");
+  }
+  std::vector<float> hmin(blocks * d), hmax(blocks * d);
+  VSK_HIP(hipMemcpyAsync(hmin.data(), pmin, 4 * hmin.size(),
+                         hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipMemcpyAsync(hmax.data(), pmax, 4 * hmax.size(),
+                         hipMemcpyDeviceToHost, ctx->stream));
+  cs.finish();
+  std::vector<float> mn(d, INFINITY), mx(d, -INFINITY);
+  for (int64_t b = 0; b < blocks; ++b)
+    for (int32_t j = 0; j < d; ++j) {
+      mn[j] = std::min(mn[j], hmin[b * d + j]);
+      mx[j] = std::max(mx[j], hmax[b * d + j]);
+    }
+  std::vector<float> s(d), o(d);
+  if (per_dim) {
+    for (int32_t j = 0; j < d; ++j) sq8_params(mn[j], mx[j], &s[j], &o[j]);
+  } else {
+    float gmn = *std::min_element(mn.begin(), mn.end());
+    float gmx = *std::max_element(mx.begin(), mx.end());
+    sq8_params(gmn, gmx, &s[0], &o[0]);
+  }
+  const size_t cnt = per_dim ? d : 1;
+  if (is_device_ptr(scale))
+    VSK_HIP(hipMemcpy(scale, s.data(), 4 * cnt, hipMemcpyHostToDevice));
+  else
+    std::memcpy(scale, s.data(), 4 * cnt);
+  if (is_device_ptr(offset))
+    VSK_HIP(hipMemcpy(offset, o.data(), 4 * cnt, hipMemcpyHostToDevice));
+  else
+    std::memcpy(offset, o.data(), 4 * cnt);
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_sq8_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                          int32_t per_dim, const float *scale,
+                          const float *offset, int8_t *codes) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no vectors");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(x && scale && offset && codes, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  CallScope cs(ctx);
+  const size_t cnt = per_dim ? d : 1;
+  const float *dx = static_cast<const float *>(
+      input_to_device(ctx, x, sizeof(float) * n * d, "sq8.x"));
+  const float *ds = static_cast<const float *>(
+      input_to_device(ctx, scale, 4 * cnt, "sq8.scale"));
+  const float *dof = static_cast<const float *>(
+      input_to_device(ctx, offset, 4 * cnt, "sq8.offset"));
+  OutputStage oc(ctx, codes, (size_t)n * d, "out.codes");
+  {
+    KernelTimer t(ctx, "sq8_encode");
+    k_sq8_encode<<<grid1(n * d), 256, 0, ctx->stream>>>(
+        dx, n, d, per_dim, ds, dof, oc.ptr<int8_t>(), d);
+    check_launch("sq8_encode");
+  }
+  oc.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
+                          int32_t d, vsk_sq8 **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no codes");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(codes, VSK_ERR_INVALID_ARGUMENT, "codes is null");
+  VSK_REQUIRE(n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "a database holds at most 2^31-1 rows");
+  std::unique_ptr<vsk_sq8> db(new vsk_sq8());
+  db->n = n;
+  db->d = d;
+  db->ldc = (d + 31) & ~31;  // whole 32-byte MFMA k-steps
+  CallScope cs(ctx);
+  db->codes.reserve((size_t)n * db->ldc);
+  if (db->ldc != d)
+    fill_i32(ctx, db->codes.as<int32_t>(), n * db->ldc / 4, 0);
+  bool dev = is_device_ptr(codes);
+  VSK_HIP(hipMemcpy2DAsync(db->codes.p, db->ldc, codes, d, d, n,
+                           dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           ctx->stream));
+  cs.finish();
+  *out = db.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_sq8_free(vsk_ctx *ctx, vsk_sq8 *db) {
+  if (ctx) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+  }
+  delete db;
+  return VSK_OK;
+}
+
+vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
+                          const int8_t *qcodes, int64_t nq, int32_t k,
+                          int32_t *out_score, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db, VSK_ERR_INVALID_ARGUMENT, "db is null");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(qcodes && out_score && out_ids, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE,
+              "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "too many queries");
+  CallScope cs(ctx);
+  const int8_t *dq = codes_to_device(ctx, qcodes, nq, db->d, db->ldc, "sq8.q");
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("sq8.best", sizeof(uint64_t) * nq * k));
+  const int64_t cap = default_cap(k);
+  const int64_t qb = query_batch(nq, cap);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    Sq8Args base{};
+    base.X = db->codes.as<int8_t>();
+    base.ldx = db->ldc;
+    base.Q = dq + b0 * db->ldc;
+    base.ldq = db->ldc;
+    base.kbytes = db->ldc;
+    base.nq = (int32_t)nb;
+    ScanFn scan = [&](const ScanRequest &r) {
+      Sq8Args a = base;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_sq8(ctx, a, r.dense);
+    };
+    progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k, "sq8_select");
+  }
+  OutputStage os(ctx, out_score, sizeof(int32_t) * nq * k, "out.score");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
+  {
+    KernelTimer t(ctx, "sq8_decode");
+    k_sq8_decode<<<grid1(nq * k), 256, 0, ctx->stream>>>(
+        best, nq * k, os.ptr<int32_t>(), oi.ptr<int64_t>());
+    check_launch("sq8_decode");
+  }
+  os.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

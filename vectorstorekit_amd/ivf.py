@@ -1,0 +1,152 @@
+"""``IVFIndex`` mirror over the C ABI (Indexes/IVFIndex.swift of
+gifton/VectorStoreKit).
+
+Reference surface kept: ``IVFConfiguration(dimensions, numberOfCentroids,
+numberOfProbes)`` (Config/Indexes/IVFConfiguration.swift:8-92),
+``train(on:)`` (:397-446), ``insert`` (:80-122), ``search(query, k,
+strategy)`` (:124-202; ``"exact"`` probes every list, :551-554),
+``getCentroids()`` (:483).  Search returns (distances, ids) arrays instead of
+``SearchResult`` objects; distances are the reference's sqrt-L2.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import VSKError, as_buffer, out_buffer
+from .engine import Context
+
+
+@dataclass
+class IVFConfiguration:
+    dimensions: int
+    numberOfCentroids: int = 1024
+    numberOfProbes: int = 10
+
+    def validate(self):
+        if self.dimensions <= 0:
+            raise VSKError(-2, "dimensions must be positive")
+        if self.numberOfCentroids <= 0:
+            raise VSKError(-2, "numberOfCentroids must be positive")
+        if not 0 < self.numberOfProbes <= self.numberOfCentroids:
+            raise VSKError(-2, "numberOfProbes must be in [1, numberOfCentroids]")
+
+
+class IVFIndex:
+    """IVF-Flat index resident on one GPU."""
+
+    def __init__(self, ctx: Context, configuration: IVFConfiguration):
+        configuration.validate()
+        self.ctx = ctx
+        self.configuration = configuration
+        self.handle = None
+        self._centroids = None
+
+    @property
+    def trained(self) -> bool:
+        return self.handle is not None
+
+    def set_centroids(self, centroids):
+        """Adopt trained centroids (nlist, d)."""
+        c = np.ascontiguousarray(centroids, np.float32)
+        if c.shape != (self.configuration.numberOfCentroids, self.configuration.dimensions):
+            raise VSKError(-4, f"centroids shape {c.shape}")
+        self.free()
+        h = ctypes.c_void_p()
+        self.ctx.check(self.ctx.lib.vsk_ivf_create(self.ctx.handle, c.ctypes.data, c.shape[0],
+                                                   c.shape[1], ctypes.byref(h)))
+        self.handle = h
+        self._centroids = c
+
+    def train(self, on, iterations: int = 10, seed: int = 0):
+        """Lloyd k-means (Clustering/KMeansClustering.swift:48-113): seeded
+        sample of distinct rows as the start, assignment on the GPU with the
+        reference's strict-'<' nearest-centroid rule, mean update."""
+        x = np.ascontiguousarray(on, np.float32)
+        k = self.configuration.numberOfCentroids
+        if x.shape[0] < k:
+            raise VSKError(-2, f"insufficient training data: {x.shape[0]} < {k}")
+        rng = np.random.default_rng(seed)
+        cent = x[rng.choice(x.shape[0], k, replace=False)].copy()
+        for _ in range(iterations):
+            self.set_centroids(cent)
+            a = self.assign(x)
+            sums = np.zeros((k, x.shape[1]), np.float64)
+            np.add.at(sums, a, x)
+            cnt = np.bincount(a, minlength=k)
+            nz = cnt > 0
+            cent[nz] = (sums[nz] / cnt[nz, None]).astype(np.float32)
+        self.set_centroids(cent)
+
+    def getCentroids(self) -> np.ndarray:
+        self._need()
+        return self._centroids.copy()
+
+    def _need(self):
+        if self.handle is None:
+            raise VSKError(-7, "IVF index must be trained before use")
+
+    def assign(self, vectors) -> np.ndarray:
+        self._need()
+        n = int(vectors.shape[0])
+        xp, xk = as_buffer(vectors, np.float32, (n, self.configuration.dimensions))
+        op, out = out_buffer((n,), np.int32, vectors)
+        self.ctx.check(self.ctx.lib.vsk_ivf_assign(self.ctx.handle, self.handle, xp, n, op))
+        return out
+
+    def insert(self, vectors, ids=None):
+        self._need()
+        n = int(vectors.shape[0])
+        xp, xk = as_buffer(vectors, np.float32, (n, self.configuration.dimensions))
+        ip, ik = (as_buffer(ids, np.int64, (n,)) if ids is not None else (None, None))
+        self.ctx.check(self.ctx.lib.vsk_ivf_add(self.ctx.handle, self.handle, xp, ip, n))
+
+    def probe(self, queries, nprobe=None) -> np.ndarray:
+        self._need()
+        nprobe = nprobe or self.configuration.numberOfProbes
+        nq = int(queries.shape[0])
+        qp, qk = as_buffer(queries, np.float32, (nq, self.configuration.dimensions))
+        op, out = out_buffer((nq, nprobe), np.int32, queries)
+        self.ctx.check(self.ctx.lib.vsk_ivf_probe(self.ctx.handle, self.handle, qp, nq,
+                                                  nprobe, op))
+        return out
+
+    def search(self, queries, k: int, strategy: str = "approximate", nprobe=None):
+        self._need()
+        if strategy == "exact":
+            nprobe = self.configuration.numberOfCentroids
+        nprobe = nprobe or self.configuration.numberOfProbes
+        q = queries
+        if not hasattr(q, "shape") or len(q.shape) == 1:
+            q = np.asarray(q, np.float32).reshape(1, -1)
+        nq = int(q.shape[0])
+        qp, qk = as_buffer(q, np.float32, (nq, self.configuration.dimensions))
+        dp, dist = out_buffer((nq, k), np.float32, q)
+        ip, ids = out_buffer((nq, k), np.int64, q)
+        self.ctx.check(self.ctx.lib.vsk_ivf_search(self.ctx.handle, self.handle, qp, nq,
+                                                   nprobe, k, dp, ip))
+        return dist, ids
+
+    def list_sizes(self) -> np.ndarray:
+        self._need()
+        out = np.empty(self.configuration.numberOfCentroids, np.int64)
+        self.ctx.check(self.ctx.lib.vsk_ivf_list_sizes(self.ctx.handle, self.handle,
+                                                       out.ctypes.data))
+        return out
+
+    @property
+    def count(self) -> int:
+        return int(self.list_sizes().sum()) if self.trained else 0
+
+    def free(self):
+        if self.handle is not None:
+            self.ctx.lib.vsk_ivf_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
