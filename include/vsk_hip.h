@@ -92,11 +92,13 @@ typedef struct {
   int32_t memory_bus_width_bits;
 } vsk_caps;
 
-/* Per-kernel timing collected with HIP events on the context's stream. */
+/* Per-kernel timing collected with HIP events on the context's stream.
+ * work = items the launches processed: (query, row) pairs for the scans. */
 typedef struct {
   char name[64];
   int64_t launches;
   double total_ms;
+  double work;
 } vsk_kernel_stat;
 
 /* ---- context --------------------------------------------------------------

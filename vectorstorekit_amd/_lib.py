@@ -66,7 +66,8 @@ class vsk_caps(ctypes.Structure):
 
 
 class vsk_kernel_stat(ctypes.Structure):
-    _fields_ = [("name", c_char * 64), ("launches", c_int64), ("total_ms", c_double)]
+    _fields_ = [("name", c_char * 64), ("launches", c_int64), ("total_ms", c_double),
+                ("work", c_double)]
 
 
 P = c_void_p  # every buffer argument is passed as a raw address

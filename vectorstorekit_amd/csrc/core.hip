@@ -66,7 +66,8 @@ void CallScope::finish() {
   ctx->resolve_pending();
 }
 
-KernelTimer::KernelTimer(vsk_ctx *c, const char *name) : ctx(c) {
+KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items)
+    : ctx(c), work(work_items) {
   if (!ctx->profile) return;
   auto it = ctx->stat_index.find(name);
   if (it == ctx->stat_index.end()) {
@@ -84,7 +85,7 @@ KernelTimer::~KernelTimer() {
   if (stat < 0) return;
   hipEvent_t b = ctx->take_event();
   if (hipEventRecord(b, ctx->stream) == hipSuccess)
-    ctx->pending.push_back({stat, a, b});
+    ctx->pending.push_back({stat, a, b, work});
 }
 
 void check_launch(const char *name) {
@@ -216,7 +217,7 @@ __global__ void k_decode_f32(const uint64_t *best, int64_t total, int32_t mode,
       continue;
     }
     float dist = vsk_ord2f((uint32_t)(key >> 32));
-    if (mode == 1) dist = __fsqrt_rn(fmaxf(dist, 0.f));
+    if (mode == 1) dist = sqrtf(fmaxf(dist, 0.f));
     uint32_t tie = (uint32_t)key;
     out_dist[i] = dist;
     out_ids[i] = id_map ? id_map[tie] : (int64_t)tie;
@@ -263,6 +264,7 @@ void vsk_ctx::resolve_pending() {
     if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
       stats[p.stat].launches += 1;
       stats[p.stat].total_ms += ms;
+      stats[p.stat].work += p.work;
     }
     event_pool.push_back(p.a);
     event_pool.push_back(p.b);

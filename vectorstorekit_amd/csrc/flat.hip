@@ -47,7 +47,7 @@ template <int MODE, int METRIC>
 __device__ inline void emit(const FlatArgs &a, int64_t qi, int64_t row,
                             float dist, uint64_t th) {
   if constexpr (MODE == MODE_MATRIX) {
-    a.mat[qi * a.ldm + row] = METRIC == VSK_METRIC_L2 ? __fsqrt_rn(dist) : dist;
+    a.mat[qi * a.ldm + row] = METRIC == VSK_METRIC_L2 ? sqrtf(dist) : dist;
   } else {
     uint64_t key = vsk_key(dist, (uint32_t)row);
     if constexpr (MODE == MODE_DENSE) {
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         if (!qok[v]) continue;
-        const float dist = OP == OP_L2SEQ ? __fsqrt_rn(acc[u][v]) : acc[u][v];
+        const float dist = OP == OP_L2SEQ ? sqrtf(acc[u][v]) : acc[u][v];
         if constexpr (MODE == MODE_ARGMIN) {
           uint64_t key = vsk_key(dist, (uint32_t)row);
           best[v] = key < best[v] ? key : best[v];
@@ -346,10 +346,10 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   dim3 grid((unsigned)qt, (unsigned)splits);
   const bool valu = a.metric == VSK_METRIC_L1 || a.metric == METRIC_L2_EXACT;
   static const char *names[2][4] = {
-      {"flat_mfma_scan", "flat_mfma_scan", "flat_mfma_matrix", "flat_mfma_argmin"},
-      {"flat_valu_scan", "flat_valu_scan", "flat_valu_matrix", "flat_valu_argmin"}};
+      {"flat_mfma_dense", "flat_mfma_filter", "flat_mfma_matrix", "flat_mfma_argmin"},
+      {"flat_valu_dense", "flat_valu_filter", "flat_valu_matrix", "flat_valu_argmin"}};
   const char *name = names[valu ? 1 : 0][mode];
-  KernelTimer t(ctx, name);
+  KernelTimer t(ctx, name, (double)a.nq * (double)rows);
   if (valu) {
     if (a.metric == VSK_METRIC_L1)
       launch_valu<OP_L1>(ctx, grid, a, mode, argmin);

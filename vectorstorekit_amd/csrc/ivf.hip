@@ -158,11 +158,10 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
     }
     const int64_t i = v - v0;
 #pragma unroll
-    for (int j = 0; j < QG; ++j) {
-      if (j >= npair) break;
-      a.cand[obase[j] + i] =
-          vsk_key(__fsqrt_rn(acc[j]), (uint32_t)(tbase[j] + i));
-    }
+    for (int j = 0; j < QG; ++j)
+      if (j < npair)
+        a.cand[obase[j] + i] =
+            vsk_key(sqrtf(acc[j]), (uint32_t)(tbase[j] + i));
   }
   (void)qidx;
 }
@@ -552,7 +551,7 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
       la.seg_off = dseg;
       la.cand = cand;
       const size_t lds = sizeof(float) * QG * ld;
-      KernelTimer t(ctx, "ivf_list_scan");
+      KernelTimer t(ctx, "ivf_list_scan", (double)tot);
       if (QG == 16)
         k_list_scan<16><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
       else if (QG == 8)

@@ -172,7 +172,8 @@ static void launch_adc(vsk_ctx *ctx, AdcArgs a, bool dense) {
   dim3 grid((unsigned)qt, (unsigned)splits);
   const size_t lds = sizeof(float) * PQ_QG * a.M * a.ksub;
   const bool m16 = a.M == 16;
-  KernelTimer t(ctx, "pq_adc_scan");
+  KernelTimer t(ctx, dense ? "pq_adc_dense" : "pq_adc_filter",
+                (double)a.nq * (double)rows);
   if (dense) {
     if (m16)
       k_pq_adc<true, true><<<grid, 256, lds, ctx->stream>>>(a);
@@ -216,7 +217,7 @@ __global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
         float t = qr[j] - xr[j];
         s = s + t * t;
       }
-      dist = metric == VSK_METRIC_L2 ? __fsqrt_rn(s) : s;
+      dist = metric == VSK_METRIC_L2 ? sqrtf(s) : s;
     } else {
       float dp = 0.f, qq = 0.f, xx = 0.f;
       for (int j = 0; j < d; ++j) {
@@ -225,9 +226,9 @@ __global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
         xx = xx + xr[j] * xr[j];
       }
       if (metric == VSK_METRIC_COSINE) {
-        float den = __fsqrt_rn(qq) * __fsqrt_rn(xx);
+        float den = sqrtf(qq) * sqrtf(xx);
         den = den + 1e-8f;
-        dist = 1.0f - __fdiv_rn(dp, den);
+        dist = 1.0f - dp / den;
       } else if (metric == VSK_METRIC_COSINE_NORMALIZED) {
         dist = 1.0f - dp;
       } else {

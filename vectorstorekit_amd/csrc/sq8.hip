@@ -146,7 +146,8 @@ static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
   a.rows_per_split = ceil_div(ceil_div(rows, splits), SB_N) * SB_N;
   splits = ceil_div(rows, a.rows_per_split);
   dim3 grid((unsigned)qt, (unsigned)splits);
-  KernelTimer t(ctx, "sq8_mfma_scan");
+  KernelTimer t(ctx, dense ? "sq8_mfma_dense" : "sq8_mfma_filter",
+                (double)a.nq * (double)rows);
   if (dense)
     k_sq8_scan<true><<<grid, 256, 0, ctx->stream>>>(a);
   else

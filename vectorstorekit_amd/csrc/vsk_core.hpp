@@ -70,6 +70,7 @@ struct vsk_ctx {
   struct Pending {
     int stat;
     hipEvent_t a, b;
+    double work;
   };
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
@@ -103,7 +104,8 @@ struct KernelTimer {
   vsk_ctx *ctx;
   int stat = -1;
   hipEvent_t a = nullptr;
-  KernelTimer(vsk_ctx *c, const char *name);
+  double work = 0;
+  KernelTimer(vsk_ctx *c, const char *name, double work_items = 0);
   ~KernelTimer();
 };
 

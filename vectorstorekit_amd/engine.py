@@ -123,7 +123,7 @@ class Context:
         for i in range(self.lib.vsk_profile_count(self.handle)):
             s = _lib.vsk_kernel_stat()
             self.check(self.lib.vsk_profile_get(self.handle, i, ctypes.byref(s)))
-            out[s.name.decode()] = (int(s.launches), float(s.total_ms))
+            out[s.name.decode()] = (int(s.launches), float(s.total_ms), float(s.work))
         return out
 
 
