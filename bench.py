@@ -6,8 +6,8 @@ k = 100, distance 1 - q.x.  One step = one vsk_search_flat call over all
 10,000 queries with the database and the queries already in HBM.
 
 Prints one JSON line: QPS (value), the roofline of the dominant kernel
-(fused fp32-MFMA scan: algorithmic FLOP 2*rows*queries*d per launch over its
-HIP-event time), and a CPU baseline (the oracle's flat search on this host's
+(the fused scan: algorithmic FLOP 2*d per (query, row) pair of a launch over
+its HIP-event time), and a CPU baseline (the oracle's flat search on this host's
 cores over the first queries of the same workload).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
@@ -22,6 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, datasheet
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, datasheet
 PEAK_HBM_GBPS = 8000.0
 
 
@@ -37,7 +38,24 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target length of the CPU baseline sample")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB 3 times (the "
+                        "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+def copy_calibration(mib):
+    """A plain copy kernel of known size: reads and writes mib MiB."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_mib": mib, "bytes_read": n * 4, "bytes_written": n * 4}))
 
 
 def cpu_baseline(x_host, q_host, k, gi, metric_code, target_s):
@@ -71,6 +89,9 @@ def cpu_baseline(x_host, q_host, k, gi, metric_code, target_s):
 
 def main():
     a = parse()
+    if a.copy_calibration:
+        copy_calibration(a.copy_calibration)
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding "
                           "is design-only (rows split across GPUs, one merge of k results)",
@@ -118,10 +139,18 @@ def main():
     ctx.profile(False)
 
     qps = a.nq * a.steps / el
-    # dominant kernel: the filtered fp32-MFMA pass (rows after the first,
-    # dense chunk); its algorithmic FLOP = 2 * d * (query, row) pairs it
-    # scanned, which the library counts per launch
-    launches, scan_ms, pairs = stats.get("flat_mfma_filter", (0, 0.0, 0.0))
+    # dominant kernel: the filtered pass of the flat scan (rows after the
+    # first, dense chunk).  Its algorithmic FLOP = 2 * d per (query, row)
+    # pair the library counted for its launches.  The default kernel forms
+    # each fp32 product from 3 bf16 MFMA products (hi/lo split), so its
+    # ceiling in algorithmic FLOP/s is the bf16 dense peak / 3; the fp32
+    # MFMA kernel's ceiling is the fp32 matrix peak.
+    if "flat_bf16x3_filter" in stats:
+        kname, peak = "flat_bf16x3_filter (k_flat_bf16x3<1,3>)", PEAK_BF16_MFMA_TFLOPS / 3
+        launches, scan_ms, pairs = stats["flat_bf16x3_filter"]
+    else:
+        kname, peak = "flat_mfma_filter (k_flat_mfma<1,3>)", PEAK_FP32_MFMA_TFLOPS
+        launches, scan_ms, pairs = stats.get("flat_mfma_filter", (0, 0.0, 0.0))
     flop = 2.0 * a.d * pairs
     achieved = flop / (scan_ms * 1e-3) / 1e12 if scan_ms > 0 else None
     kernels = {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
@@ -145,12 +174,16 @@ def main():
         "distances_per_s": a.nq * a.n * a.steps / el,
         "roofline": {
             "bound": "mfma",
-            "kernel": "flat_mfma_filter (k_flat_mfma<1,3>)",
+            "kernel": kname,
             "flop_per_launch": flop / launches if launches else None,
             "achieved": round(achieved, 2) if achieved else None,
-            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "peak": round(peak, 1),
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4) if achieved else None,
+            "frac": round(achieved / peak, 4) if achieved else None,
+            "peak_basis": ("bf16 dense MFMA 2500 TFLOP/s / 3 products per fp32 product"
+                           if peak != PEAK_FP32_MFMA_TFLOPS else "fp32 dense MFMA"),
+            "frac_of_fp32_mfma_peak": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4)
+            if achieved else None,
             "traffic": None,
             "launches": launches,
             "avg_launch_ms": round(scan_ms / launches, 4) if launches else None,

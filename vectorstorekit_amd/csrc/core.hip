@@ -1,5 +1,6 @@
 // core.hip -- context, staging of caller buffers, event profiling, small
 // utility kernels (fills, row norms, key decoding) and the flat database.
+#include <cstdlib>
 #include <cstring>
 
 #include "vsk_api.hpp"
@@ -291,6 +292,8 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   if (hipSetDevice(device) != hipSuccess) return VSK_ERR_DEVICE_NOT_AVAILABLE;
   vsk_ctx *c = new vsk_ctx();
   c->device = device;
+  const char *fk = getenv("VSK_FLAT_KERNEL");
+  c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
   // a blocking stream: it orders itself after work on the null stream, so
   // device buffers produced there (e.g. by torch) are complete when read
   if (hipStreamCreate(&c->stream) != hipSuccess ||

@@ -391,6 +391,35 @@ static float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
   return aux;
 }
 
+static bool use_bf16x3(const vsk_ctx *ctx, int32_t metric) {
+  return !ctx->flat_fp32 && metric != VSK_METRIC_L1 && metric != METRIC_L2_EXACT;
+}
+
+// hi/lo planes of the database (once) and of a query batch (per call)
+static SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+                            int64_t nq) {
+  const int32_t ldb = (db->d + 31) & ~31;
+  if (!db->split.p) {
+    db->split.reserve(sizeof(uint16_t) * 2 * (size_t)db->n * ldb);
+    db->ldb = ldb;
+    uint16_t *h = db->split.as<uint16_t>();
+    split_bf16(ctx, db->x.as<float>(), db->n, db->d, db->ld, h,
+               h + (size_t)db->n * ldb, ldb);
+  }
+  uint16_t *qs = static_cast<uint16_t *>(
+      ctx->scratch_ptr("flat.qsplit", sizeof(uint16_t) * 2 * (size_t)nq * ldb));
+  split_bf16(ctx, dq, nq, db->d, db->ld, qs, qs + (size_t)nq * ldb, ldb);
+  SplitPtrs s;
+  s.xh = db->split.as<uint16_t>();
+  s.xl = s.xh + (size_t)db->n * ldb;
+  s.qh = qs;
+  s.ql = qs + (size_t)nq * ldb;
+  s.ldxb = ldb;
+  s.ldqb = ldb;
+  s.kb = ldb;
+  return s;
+}
+
 // top-k over a resident database for queries already on the device
 void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                       int64_t nq, int32_t k, int32_t metric, uint64_t *best) {
@@ -410,6 +439,9 @@ void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
     base.kdim = db->ld;
     base.nq = (int32_t)nb;
     base.metric = metric;
+    const bool x3 = use_bf16x3(ctx, metric);
+    SplitPtrs sp{};
+    if (x3) sp = make_split(ctx, db, qbat, nb);
     ScanFn scan = [&](const ScanRequest &r) {
       FlatArgs a = base;
       a.r0 = r.r0;
@@ -419,7 +451,10 @@ void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
       a.cand = r.cand;
       a.cap = r.cap;
       a.counts = r.counts;
-      launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER, nullptr);
+      if (x3)
+        launch_flat_bf16x3(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER);
+      else
+        launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER, nullptr);
     };
     progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k,
                      "flat_select");
@@ -489,7 +524,10 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
   a.metric = metric;
   a.mat = om.ptr<float>();
   a.ldm = db->n;
-  launch_flat(ctx, a, MODE_MATRIX, nullptr);
+  if (use_bf16x3(ctx, metric))
+    launch_flat_bf16x3(ctx, a, make_split(ctx, db, dq, nq), MODE_MATRIX);
+  else
+    launch_flat(ctx, a, MODE_MATRIX, nullptr);
   om.copy_back();
   cs.finish();
   VSK_API_END(ctx);

@@ -31,7 +31,20 @@ struct FlatArgs {
   int32_t *counts;
   float *mat;  // MODE_MATRIX output, row-major nq x ldm
   int64_t ldm;
+  int32_t splits_per_xcd;  // bf16x3 kernel: row splits owned by each XCD
 };
+
+// bf16 hi/lo operand planes of the bf16x3 kernel
+struct SplitPtrs {
+  const uint16_t *xh, *xl;  // row planes, stride ldxb
+  const uint16_t *qh, *ql;  // query planes, stride ldqb
+  int64_t ldxb, ldqb;
+  int32_t kb;               // padded dimension (multiple of 32)
+};
+// hi = bf16(x), lo = bf16(x - hi) of an (n x ld) fp32 matrix, ldb columns
+void split_bf16(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
+                uint16_t *hi, uint16_t *lo, int32_t ldb);
+void launch_flat_bf16x3(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode);
 
 // launch one scan over rows [a.r0, a.r1) of a.X for the a.nq queries of a.Q
 // (mode MODE_*; argmin output only for MODE_ARGMIN).  a.rows_per_split is

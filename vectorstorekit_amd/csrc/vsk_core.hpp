@@ -65,6 +65,10 @@ struct vsk_ctx {
   std::map<std::string, std::unique_ptr<vsk::DevBuf>> scratch;
   void *scratch_ptr(const std::string &key, size_t bytes);
 
+  // flat dot-product kernel: bf16x3 split MFMA (default) or fp32 MFMA
+  // (environment VSK_FLAT_KERNEL=fp32 at context creation)
+  bool flat_fp32 = false;
+
   // profiling
   bool profile = false;
   struct Pending {
@@ -87,6 +91,9 @@ struct vsk_db {
   vsk::DevBuf x;       // n x ld fp32
   vsk::DevBuf sqnorm;  // n: sum x^2 (fp32)
   vsk::DevBuf norm;    // n: sqrt(sum x^2)
+  // bf16 hi/lo planes for the bf16x3 MFMA kernel, built on first use
+  mutable vsk::DevBuf split;
+  mutable int32_t ldb = 0;
 };
 
 namespace vsk {
