@@ -1,16 +1,31 @@
 """Benchmark of the search hot path on one MI355X.
 
-Workload: flat cosine search, 1,000,000 x 768 fp32 rows
-(i.i.d. N(0,1), each L2-normalised), 10,000 queries drawn the same way,
-k = 100, distance 1 - q.x.  One step = one vsk_search_flat call over all
-10,000 queries with the database and the queries already in HBM.
+Default workload (the headline metric): flat cosine search,
+1,000,000 x 768 fp32 rows (i.i.d. N(0,1), each L2-normalised), 10,000
+queries drawn the same way, k = 100, distance 1 - q.x.  One step = one
+vsk_search_flat call over all 10,000 queries with the database and the
+queries already in HBM.
 
-Prints one JSON line: QPS (value), the roofline of the dominant kernel
-(the fused scan: algorithmic FLOP 2*d per (query, row) pair of a launch over
-its HIP-event time), and a CPU baseline (the oracle's flat search on this host's
-cores over the first queries of the same workload).
+The other BASELINE configs are measured with ``--config``:
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+* ``c1`` flat L2^2, 10,000 x 128, 100 queries, k = 10 (latency-bound);
+* ``c3`` IVF-Flat L2, 1M x 128 from a 4,096-Gaussian mixture, nlist 4096,
+  nprobe 32, 10,000 queries, k = 10 (one step = one vsk_ivf_search);
+* ``c4`` int8 SQ scan, 10M x 128 codes, 1,000 queries, k = 100;
+* ``c5`` PQ M=16 x 256 ADC over 10M codes, top-1000, exact L1 re-rank to
+  k = 100 (one step = one vsk_pq_search).
+
+Each prints one JSON line: QPS (value), the roofline of the dominant kernel
+(algorithmic FLOP/OP or bytes per (query, row) pair the library counted for
+that kernel's launches, over its HIP-event time on the library's stream), and
+a CPU baseline (the oracle on this host's cores over the first queries of the
+same workload, plus the agreement of the GPU's ids with the CPU's there).
+``traffic`` is the kernel's HBM bytes per launch read from
+profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes, scaled by
+a plain-copy calibration) when that file holds an entry for this kernel and
+workload, else null.
+
+    python bench.py [--config c2] [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
 import argparse
 import json
@@ -23,25 +38,29 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, datasheet
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, datasheet
-PEAK_HBM_GBPS = 8000.0
+PEAK_INT8_MFMA_TOPS = 5000.0  # MI355X dense int8 matrix, datasheet
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
+
+DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1)}
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=5)
-    p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--n", type=int, default=1_000_000)
-    p.add_argument("--d", type=int, default=768)
-    p.add_argument("--nq", type=int, default=10_000)
-    p.add_argument("--k", type=int, default=100)
+    p.add_argument("--config", default="c2", choices=sorted(DEFAULT_STEPS))
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target length of the CPU baseline sample")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 3 times (the "
                         "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    return p.parse_args()
+    a = p.parse_args()
+    s, w = DEFAULT_STEPS[a.config]
+    a.steps = s if a.steps is None else a.steps
+    a.warmup = w if a.warmup is None else a.warmup
+    return a
 
 
 def copy_calibration(mib):
@@ -58,34 +77,330 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_mib": mib, "bytes_read": n * 4, "bytes_written": n * 4}))
 
 
-def cpu_baseline(x_host, q_host, k, gi, metric_code, target_s):
-    """Time the oracle's flat search (16-accumulator variant, all host
-    threads) on the first queries of the workload; also returns the recall
-    of the GPU's ids against the exact CPU answer on those queries."""
-    import numpy as np
+def host_threads():
+    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
 
-    from oracle import oracle as O
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+def cpu_sample(run, nq_total, target_s, threads):
+    """Times ``run(m)`` (the oracle over the first m queries, all threads):
+    one probe round of ``threads`` queries, then a sample sized to about
+    target_s seconds (the whole set repeated when it is quicker).  Returns
+    (queries/s, m, repeats, seconds, result of the last call)."""
+    m0 = min(nq_total, threads)
     t0 = time.perf_counter()
-    O.search_flat(q_host[:threads], x_host, k, metric_code, threads=threads, fast=True)
-    t1 = time.perf_counter()
-    per_round = t1 - t0  # one query per thread
-    rounds = max(1, int(target_s / max(per_round, 1e-3)))
-    nsamp = min(len(q_host), rounds * threads)
+    run(m0)
+    per = time.perf_counter() - t0
+    rounds = max(1, int(target_s / max(per, 1e-4)))
+    m = min(nq_total, rounds * m0)
+    reps = 1
+    if m == nq_total:  # whole query set is quick: repeat it
+        reps = max(1, int(target_s / max(per * nq_total / m0, 1e-4)))
     t0 = time.perf_counter()
-    od, oi = O.search_flat(q_host[:nsamp], x_host, k, metric_code, threads=threads, fast=True)
+    for _ in range(reps):
+        res = run(m)
     el = time.perf_counter() - t0
-    hits = sum(len(set(a) & set(b)) for a, b in zip(gi[:nsamp].tolist(), oi.tolist()))
-    return {
-        "value": nsamp / el,
-        "unit": "queries/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"first {nsamp} of {len(q_host)} queries against all "
-                  f"{x_host.shape[0]} rows ({el:.1f} s)",
-    }, hits / oi.size
+    return m * reps / el, m, reps, el, res
 
+
+def id_agreement(gi, oi):
+    """Fraction of the CPU's top-k ids that the GPU also returned."""
+    hits = sum(len(set(a) & set(b)) for a, b in zip(gi.tolist(), oi.tolist()))
+    return hits / max(1, oi.size)
+
+
+# ---------------------------------------------------------------- workloads
+
+def gen_flat(n, d, nq, normalise, dev):
+    import torch
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    x = torch.randn(n, d, generator=g, device=dev)
+    g.manual_seed(2)
+    q = torch.randn(nq, d, generator=g, device=dev)
+    if normalise:
+        x /= x.norm(dim=1, keepdim=True)
+        q /= q.norm(dim=1, keepdim=True)
+    return x, q
+
+
+def gen_mixture(n, d, ncent, nq, dev, jitter=True):
+    """centres ~ N(0, 4 I) (seed 3), centre index uniform (seed 5), points =
+    centre + 0.5 N(0, I) (rows seed 1, queries seed 2), centroids = centres +
+    0.1 N(0, I) (seed 4)."""
+    import torch
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    cent = 2.0 * torch.randn(ncent, d, generator=g, device=dev)
+    g.manual_seed(5)
+    a = torch.randint(0, ncent, (n,), generator=g, device=dev)
+    qa = torch.randint(0, ncent, (nq,), generator=g, device=dev)
+    g.manual_seed(1)
+    x = cent[a] + 0.5 * torch.randn(n, d, generator=g, device=dev)
+    del a
+    g.manual_seed(2)
+    q = cent[qa] + 0.5 * torch.randn(nq, d, generator=g, device=dev)
+    c = None
+    if jitter:
+        g.manual_seed(4)
+        c = cent + 0.1 * torch.randn(ncent, d, generator=g, device=dev)
+    return x, q, c
+
+
+def setup(a, ctx, dev):
+    """Builds the resident index for the config; returns (spec, step,
+    cpu_leg) where cpu_leg(target_s) gives (baseline dict, agreement)."""
+    import numpy as np
+    import torch
+
+    from vectorstorekit_amd import _lib as L
+    from vectorstorekit_amd import (IVFConfiguration, IVFIndex, ProductQuantizer,
+                                    ScalarQuantizer, SQ8Database, VectorDatabase)
+
+    lib = ctx.lib
+    c = a.config
+    if c in ("c1", "c2"):
+        n, d, nq, k = (10_000, 128, 100, 10) if c == "c1" else (1_000_000, 768, 10_000, 100)
+        metric = L.METRIC_L2SQ if c == "c1" else L.METRIC_COSINE_NORMALIZED
+        x, q = gen_flat(n, d, nq, c == "c2", dev)
+        db = VectorDatabase(ctx, x)
+        dist = torch.empty(nq, k, device=dev)
+        ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+
+        def step():
+            ctx.check(lib.vsk_search_flat(ctx.handle, db.handle, q.data_ptr(), nq, k, metric,
+                                          dist.data_ptr(), ids.data_ptr()))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            xh, qh = x.cpu().numpy(), q.cpu().numpy()
+            th = host_threads()
+            qps, m, reps, el, (od, oi) = cpu_sample(
+                lambda m: O.search_flat(qh[:m], xh, k, metric, threads=th, fast=True),
+                nq, target_s, th)
+            return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "sample": f"first {m} of {nq} queries against all {n} rows, "
+                               f"{reps} pass(es) ({el:.1f} s)"},
+                    id_agreement(ids.cpu().numpy()[:m], oi))
+
+        spec = {
+            "metric": ("QPS @k=100, 1M x 768 fp32 flat cosine" if c == "c2"
+                       else "QPS @k=10, 10k x 128 fp32 flat L2^2"),
+            "workload": (f"flat-cosine-1Mx768-q10000-k100 (BASELINE config 2)" if c == "c2"
+                         else "flat-l2sq-10000x128-q100-k10 (BASELINE config 1)"),
+            "config": {"n": n, "d": d, "nq": nq, "k": k,
+                       "metric": "1 - q.x" if c == "c2" else "sum (q-x)^2"},
+            "data": ("synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2)"
+                     + (", L2-normalised" if c == "c2" else "")),
+            "dtype": "f32", "nq": nq, "n": n, "d": d,
+            "kernels": [("flat_bf16x3_filter", "k_flat_bf16x3<FILTER>", "mfma"),
+                        ("flat_bf16x3_dense", "k_flat_bf16x3<DENSE>", "mfma"),
+                        ("flat_mfma_filter", "k_flat_mfma<FILTER>", "mfma32"),
+                        ("flat_mfma_dense", "k_flat_mfma<DENSE>", "mfma32")],
+            "keep": (db, x, q, dist, ids),
+        }
+        return spec, step, cpu_leg
+
+    if c == "c3":
+        n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
+        x, q, cent = gen_mixture(n, d, ncent, nq, dev)
+        idx = IVFIndex(ctx, IVFConfiguration(dimensions=d, numberOfCentroids=ncent,
+                                             numberOfProbes=nprobe))
+        idx.set_centroids(cent.cpu().numpy())
+        idx.insert(x)
+        dist = torch.empty(nq, k, device=dev)
+        ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+
+        def step():
+            ctx.check(lib.vsk_ivf_search(ctx.handle, idx.handle, q.data_ptr(), nq, nprobe, k,
+                                         dist.data_ptr(), ids.data_ptr()))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), idx.getCentroids()
+            lists = idx.assign(x).cpu().numpy()
+            rid = np.arange(n, dtype=np.int64)
+            th = host_threads()
+            qps, m, reps, el, (od, oi) = cpu_sample(
+                lambda m: O.ivf_search(qh[:m], xh, rid, lists, ch, nprobe, k, threads=th),
+                nq, target_s, th)
+            return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "sample": f"first {m} of {nq} queries, probe + scan of 32 lists "
+                               f"(index built from the GPU's assignment; list build inside "
+                               f"each oracle call), {reps} pass(es) ({el:.1f} s)"},
+                    id_agreement(ids.cpu().numpy()[:m], oi))
+
+        spec = {
+            "metric": "QPS @k=10, IVF-Flat L2 1M x 128, nlist 4096, nprobe 32",
+            "workload": "ivf-flat-l2-1Mx128-nlist4096-nprobe32-q10000-k10 (BASELINE config 3)",
+            "config": {"n": n, "d": d, "nlist": ncent, "nprobe": nprobe, "nq": nq, "k": k,
+                       "metric": "sqrt(sum (q-x)^2)"},
+            "data": "synthetic: 4,096-Gaussian mixture, centres 2 N(0,I) (seed 3), "
+                    "points centre + 0.5 N(0,I) (seeds 5, 1, 2), centroids centre + "
+                    "0.1 N(0,I) (seed 4); torch Philox",
+            "dtype": "f32", "nq": nq, "n": n, "d": d,
+            "kernels": [("ivf_list_scan", "k_list_scan<16>", "hbm")],
+            "keep": (idx, x, q, dist, ids),
+        }
+        return spec, step, cpu_leg
+
+    if c == "c4":
+        n, d, nq, k = 10_000_000, 128, 1000, 100
+        x, q = gen_flat(n, d, nq, False, dev)
+        sq = ScalarQuantizer(ctx, per_dim=True)
+        sq.train(x)
+        codes = sq.quantizeBatch(x)
+        del x
+        qc = sq.quantizeBatch(q)
+        db = SQ8Database(ctx, codes)
+        score = torch.empty(nq, k, dtype=torch.int32, device=dev)
+        ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+
+        def step():
+            ctx.check(lib.vsk_sq8_search(ctx.handle, db.handle, qc.data_ptr(), nq, k,
+                                         score.data_ptr(), ids.data_ptr()))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            ch, qh = codes.cpu().numpy(), qc.cpu().numpy()
+            th = host_threads()
+            qps, m, reps, el, (os_, oi) = cpu_sample(
+                lambda m: O.sq8_search(qh[:m], ch, k, threads=th), nq, target_s, th)
+            return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "sample": f"first {m} of {nq} queries against all {n} codes, "
+                               f"{reps} pass(es) ({el:.1f} s)"},
+                    id_agreement(ids.cpu().numpy()[:m], oi))
+
+        spec = {
+            "metric": "QPS @k=100, int8 SQ dot scan 10M x 128",
+            "workload": "sq8-dot-10Mx128-q1000-k100 (BASELINE config 4)",
+            "config": {"n": n, "d": d, "nq": nq, "k": k,
+                       "metric": "-sum code_q code_x (int32)", "quantiser": "per-dim min/max"},
+            "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), "
+                    "quantised per dimension",
+            "dtype": "i8 (i32 accumulate)", "nq": nq, "n": n, "d": d,
+            "kernels": [("sq8_mfma_filter", "k_sq8_scan<FILTER>", "int8"),
+                        ("sq8_mfma_dense", "k_sq8_scan<DENSE>", "int8")],
+            "keep": (db, codes, qc, score, ids),
+        }
+        return spec, step, cpu_leg
+
+    # c5
+    n, d, nq, M, ksub, k_adc, k = 10_000_000, 128, 1000, 16, 256, 1000, 100
+    x, q, _ = gen_mixture(n, d, 1024, nq, dev, jitter=False)
+    pq = ProductQuantizer.train(ctx, x[:65536], M, ksub, iterations=8, seed=0)
+    codes = pq.encode(x)
+    pq.add(codes)
+    db = VectorDatabase(ctx, x)
+    dist = torch.empty(nq, k, device=dev)
+    ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+    l1 = L.METRIC_L1
+
+    def step():
+        ctx.check(lib.vsk_pq_search(ctx.handle, pq.handle, q.data_ptr(), nq, k_adc, k, l1,
+                                    db.handle, dist.data_ptr(), ids.data_ptr()))
+
+    def cpu_leg(target_s):
+        from oracle import oracle as O
+        xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), codes.cpu().numpy()
+        th = host_threads()
+        qps, m, reps, el, (od, oi) = cpu_sample(
+            lambda m: O.pq_search(qh[:m], pq.codebooks, ch, k_adc, k, x=xh, rerank_metric=l1,
+                                  threads=th), nq, target_s, th)
+        return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                 "sample": f"first {m} of {nq} queries: ADC over all {n} codes, top-1000, "
+                           f"L1 re-rank, {reps} pass(es) ({el:.1f} s)"},
+                id_agreement(ids.cpu().numpy()[:m], oi))
+
+    spec = {
+        "metric": "QPS @k=100, PQ M16x256 ADC 10M x 128, top-1000 L1 re-rank",
+        "workload": "pq-adc-10Mx128-m16-q1000-kadc1000-l1rerank-k100 (BASELINE config 5)",
+        "config": {"n": n, "d": d, "M": M, "ksub": ksub, "nq": nq, "k_adc": k_adc, "k": k,
+                   "metric": "ADC sum of LUT[m][code_m]; re-rank sum |q-x|"},
+        "data": "synthetic: 1,024-Gaussian mixture, centres 2 N(0,I) (seed 3), points "
+                "centre + 0.5 N(0,I) (seeds 5, 1, 2); codebooks: 8 Lloyd iterations "
+                "per segment on the first 65,536 rows (GPU assignment)",
+        "dtype": "u8 codes, f32 LUT", "nq": nq, "n": n, "d": d, "M": M,
+        "kernels": [("pq_adc_filter", "k_pq_adc<FILTER,M16>", "hbm_pq"),
+                    ("pq_adc_dense", "k_pq_adc<DENSE,M16>", "hbm_pq")],
+        "keep": (pq, db, x, q, codes, dist, ids),
+    }
+    return spec, step, cpu_leg
+
+
+# ----------------------------------------------------------------- roofline
+
+def roofline(spec, stats):
+    """Dominant kernel's roofline from the library's event timers."""
+    d = spec["d"]
+    best = None
+    for key, label, kind in spec["kernels"]:
+        if key in stats and stats[key][1] > 0:
+            if best is None or stats[key][1] > stats[best[0]][1]:
+                best = (key, label, kind)
+    if best is None:
+        return None
+    key, label, kind = best
+    launches, ms, pairs = stats[key]
+    sec = ms * 1e-3
+    r = {"kernel": f"{key} ({label})", "launches": launches,
+         "avg_launch_ms": round(ms / launches, 4) if launches else None,
+         "pairs_per_launch": pairs / launches if launches else None}
+    if kind in ("mfma", "mfma32"):
+        flop = 2.0 * d * pairs
+        peak = PEAK_BF16_MFMA_TFLOPS / 3 if kind == "mfma" else PEAK_FP32_MFMA_TFLOPS
+        ach = flop / sec / 1e12
+        r.update({"bound": "mfma", "achieved": round(ach, 2), "peak": round(peak, 1),
+                  "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                  "algorithmic": "2*d FLOP per (query, row) pair",
+                  "peak_basis": ("bf16 dense MFMA 2500 TFLOP/s / 3 products per fp32 product"
+                                 if kind == "mfma" else "fp32 dense MFMA"),
+                  "frac_of_fp32_mfma_peak": round(ach / PEAK_FP32_MFMA_TFLOPS, 4)})
+    elif kind == "int8":
+        ops = 2.0 * d * pairs
+        ach = ops / sec / 1e12
+        r.update({"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_MFMA_TOPS,
+                  "unit": "TOP/s", "frac": round(ach / PEAK_INT8_MFMA_TOPS, 4),
+                  "algorithmic": "2*d int8 OP per (query, row) pair",
+                  "peak_basis": "int8 dense MFMA 5.0 POP/s"})
+    elif kind == "hbm":
+        by = 4.0 * d * pairs
+        ach = by / sec / 1e9
+        r.update({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                  "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
+                  "algorithmic": "4*d bytes per (query, probed row) pair: every probed "
+                                 "list row read once per query"})
+    else:  # hbm_pq
+        M = spec["M"]
+        by = 1.0 * M * pairs
+        ach = by / sec / 1e9
+        r.update({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                  "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
+                  "algorithmic": "M code bytes per (query, row) pair: all codes read "
+                                 "once per query",
+                  "lds_lookups_per_s": M * pairs / sec})
+    r["traffic"] = traffic_for(key, spec["workload"])
+    return r
+
+
+def traffic_for(kernel_key, workload):
+    """HBM bytes per launch of this kernel on this workload, from the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, else None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rows = json.load(f)["entries"]
+    except (OSError, ValueError, KeyError):
+        return None
+    tag = workload.split(" ")[0]
+    for e in rows:
+        if e.get("kernel") == kernel_key and e.get("workload") == tag:
+            return e.get("traffic_bytes_per_launch")
+    return None
+
+
+# --------------------------------------------------------------------- main
 
 def main():
     a = parse()
@@ -97,32 +412,16 @@ def main():
                           "is design-only (rows split across GPUs, one merge of k results)",
                           "n_gpus": a.gpus}))
         sys.exit(2)
-    import numpy as np
     import torch
 
-    from vectorstorekit_amd import Context, VectorDatabase
-    from vectorstorekit_amd._lib import METRIC_COSINE_NORMALIZED
+    from vectorstorekit_amd import Context
 
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(1)
-    x = torch.randn(a.n, a.d, generator=g, device=dev)
-    x /= x.norm(dim=1, keepdim=True)
-    g.manual_seed(2)
-    q = torch.randn(a.nq, a.d, generator=g, device=dev)
-    q /= q.norm(dim=1, keepdim=True)
-    torch.cuda.synchronize()
-
     ctx = Context(0)
-    db = VectorDatabase(ctx, x)
-    dist = torch.empty(a.nq, a.k, device=dev)
-    ids = torch.empty(a.nq, a.k, dtype=torch.int64, device=dev)
-    lib = ctx.lib
-
-    def step():
-        ctx.check(lib.vsk_search_flat(ctx.handle, db.handle, q.data_ptr(), a.nq, a.k,
-                                      METRIC_COSINE_NORMALIZED, dist.data_ptr(),
-                                      ids.data_ptr()))
+    t0 = time.perf_counter()
+    spec, step, cpu_leg = setup(a, ctx, dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
 
     for _ in range(a.warmup):
         step()
@@ -138,26 +437,10 @@ def main():
     stats = ctx.profile_stats()
     ctx.profile(False)
 
-    qps = a.nq * a.steps / el
-    # dominant kernel: the filtered pass of the flat scan (rows after the
-    # first, dense chunk).  Its algorithmic FLOP = 2 * d per (query, row)
-    # pair the library counted for its launches.  The default kernel forms
-    # each fp32 product from 3 bf16 MFMA products (hi/lo split), so its
-    # ceiling in algorithmic FLOP/s is the bf16 dense peak / 3; the fp32
-    # MFMA kernel's ceiling is the fp32 matrix peak.
-    if "flat_bf16x3_filter" in stats:
-        kname, peak = "flat_bf16x3_filter (k_flat_bf16x3<1,3>)", PEAK_BF16_MFMA_TFLOPS / 3
-        launches, scan_ms, pairs = stats["flat_bf16x3_filter"]
-    else:
-        kname, peak = "flat_mfma_filter (k_flat_mfma<1,3>)", PEAK_FP32_MFMA_TFLOPS
-        launches, scan_ms, pairs = stats.get("flat_mfma_filter", (0, 0.0, 0.0))
-    flop = 2.0 * a.d * pairs
-    achieved = flop / (scan_ms * 1e-3) / 1e12 if scan_ms > 0 else None
-    kernels = {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
-               for k, v in stats.items()}
-
+    nq, n = spec["nq"], spec["n"]
+    qps = nq * a.steps / el
     out = {
-        "metric": "QPS @k=100, 1M x 768 fp32 flat cosine",
+        "metric": spec["metric"],
         "value": round(qps, 1),
         "unit": "queries/s",
         "n_gpus": 1,
@@ -167,40 +450,23 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), L2-normalised",
-        "config": {"workload": "flat-cosine-1Mx768-q10000-k100 (BASELINE config 2)",
-                   "n": a.n, "d": a.d, "nq": a.nq, "k": a.k, "metric": "1 - q.x"},
-        "distances_per_s": a.nq * a.n * a.steps / el,
-        "roofline": {
-            "bound": "mfma",
-            "kernel": kname,
-            "flop_per_launch": flop / launches if launches else None,
-            "achieved": round(achieved, 2) if achieved else None,
-            "peak": round(peak, 1),
-            "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4) if achieved else None,
-            "peak_basis": ("bf16 dense MFMA 2500 TFLOP/s / 3 products per fp32 product"
-                           if peak != PEAK_FP32_MFMA_TFLOPS else "fp32 dense MFMA"),
-            "frac_of_fp32_mfma_peak": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4)
-            if achieved else None,
-            "traffic": None,
-            "launches": launches,
-            "avg_launch_ms": round(scan_ms / launches, 4) if launches else None,
-        },
-        "kernels": kernels,
+        "dtype": spec["dtype"],
+        "data": spec["data"],
+        "config": dict({"workload": spec["workload"]}, **spec["config"]),
+        "distances_per_s": nq * n * a.steps / el,
+        "roofline": roofline(spec, stats),
+        "setup_s": round(build_s, 2),
+        "kernels": {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
+                    for k, v in stats.items()},
     }
     if not a.no_cpu:
-        xh = x.cpu().numpy()
-        qh = q.cpu().numpy()
-        base, rec = cpu_baseline(xh, qh, a.k, ids.cpu().numpy(), METRIC_COSINE_NORMALIZED,
-                                 a.cpu_seconds)
+        base, agree = cpu_leg(a.cpu_seconds)
         out["cpu_baseline"] = base
-        out["recall_vs_cpu"] = round(rec, 5)
+        out["ids_agreement_vs_cpu"] = round(agree, 5)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
-    db.free()
+    del spec
     ctx.close()
 
 

@@ -116,6 +116,58 @@ void OutputStage::copy_back() {
                            ctx->stream));
 }
 
+void copy_rows(vsk_ctx *ctx, void *dst, size_t dst_pitch, const void *src,
+               size_t src_pitch, size_t row_bytes, int64_t rows) {
+  if (rows <= 0 || row_bytes == 0) return;
+  const bool sdev = is_device_ptr(src), ddev = is_device_ptr(dst);
+  const bool dense = src_pitch == row_bytes && dst_pitch == row_bytes;
+  const hipMemcpyKind kind =
+      sdev ? (ddev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost)
+           : (ddev ? hipMemcpyHostToDevice : hipMemcpyHostToHost);
+  if (dense) {
+    VSK_HIP(hipMemcpyAsync(dst, src, row_bytes * (size_t)rows, kind,
+                           ctx->stream));
+    return;
+  }
+  if (sdev && ddev) {
+    VSK_HIP(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, row_bytes,
+                             (size_t)rows, kind, ctx->stream));
+    return;
+  }
+  VSK_REQUIRE(sdev || ddev, VSK_ERR_INVALID_ARGUMENT,
+              "host-to-host row copy is not supported");
+  VSK_REQUIRE(!sdev || dst_pitch == row_bytes, VSK_ERR_INVALID_ARGUMENT,
+              "host destination rows must be packed");
+  // one side is host memory: move whole chunks in one transfer each and do
+  // the pitch change on the device
+  const size_t host_pitch = sdev ? dst_pitch : src_pitch;
+  const size_t chunk_bytes = size_t(64) << 20;
+  int64_t chunk = (int64_t)(chunk_bytes / host_pitch);
+  if (chunk < 1) chunk = 1;
+  if (chunk > rows) chunk = rows;
+  char *stage = static_cast<char *>(
+      ctx->scratch_ptr("stage.rows", host_pitch * (size_t)chunk));
+  for (int64_t r = 0; r < rows; r += chunk) {
+    const int64_t m = rows - r < chunk ? rows - r : chunk;
+    const size_t span = host_pitch * (size_t)(m - 1) + row_bytes;
+    if (!sdev) {
+      VSK_HIP(hipMemcpyAsync(stage, static_cast<const char *>(src) + r * src_pitch,
+                             span, hipMemcpyHostToDevice, ctx->stream));
+      VSK_HIP(hipMemcpy2DAsync(static_cast<char *>(dst) + r * dst_pitch,
+                               dst_pitch, stage, src_pitch, row_bytes,
+                               (size_t)m, hipMemcpyDeviceToDevice,
+                               ctx->stream));
+    } else {
+      VSK_HIP(hipMemcpy2DAsync(stage, dst_pitch,
+                               static_cast<const char *>(src) + r * src_pitch,
+                               src_pitch, row_bytes, (size_t)m,
+                               hipMemcpyDeviceToDevice, ctx->stream));
+      VSK_HIP(hipMemcpyAsync(static_cast<char *>(dst) + r * dst_pitch, stage,
+                             span, hipMemcpyDeviceToHost, ctx->stream));
+    }
+  }
+}
+
 const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
                                    int32_t d, int32_t ld,
                                    const std::string &slot) {
@@ -126,11 +178,8 @@ const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
       ctx->scratch_ptr(slot, sizeof(float) * (size_t)rows * ld));
   if (ld != d)
     fill_i32(ctx, reinterpret_cast<int32_t *>(out), rows * (int64_t)ld, 0);
-  VSK_HIP(hipMemcpy2DAsync(out, sizeof(float) * ld, p, sizeof(float) * d,
-                           sizeof(float) * d, rows,
-                           dev ? hipMemcpyDeviceToDevice
-                               : hipMemcpyHostToDevice,
-                           ctx->stream));
+  copy_rows(ctx, out, sizeof(float) * ld, p, sizeof(float) * d,
+            sizeof(float) * d, rows);
   return out;
 }
 
@@ -387,12 +436,8 @@ vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
   db->x.reserve(sizeof(float) * (size_t)n * db->ld);
   if (db->ld != d)
     fill_i32(ctx, db->x.as<int32_t>(), n * (int64_t)db->ld, 0);
-  bool dev = is_device_ptr(x);
-  VSK_HIP(hipMemcpy2DAsync(db->x.p, sizeof(float) * db->ld, x,
-                           sizeof(float) * d, sizeof(float) * d, n,
-                           dev ? hipMemcpyDeviceToDevice
-                               : hipMemcpyHostToDevice,
-                           ctx->stream));
+  copy_rows(ctx, db->x.p, sizeof(float) * db->ld, x, sizeof(float) * d,
+            sizeof(float) * d, n);
   if (flags & VSK_DB_NORMALIZE) {
     k_normalize_rows<<<(unsigned)ceil_div(n, 4), 256, 0, ctx->stream>>>(
         db->x.as<float>(), n, d, db->ld);
@@ -431,11 +476,8 @@ vsk_status vsk_db_read_f32(vsk_ctx *ctx, const vsk_db *db, int64_t row0,
               VSK_ERR_INVALID_ARGUMENT, "row range out of bounds");
   if (count == 0) return VSK_OK;
   CallScope cs(ctx);
-  bool dev = is_device_ptr(out);
-  VSK_HIP(hipMemcpy2DAsync(
-      out, sizeof(float) * db->d, db->x.as<float>() + row0 * db->ld,
-      sizeof(float) * db->ld, sizeof(float) * db->d, count,
-      dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, ctx->stream));
+  copy_rows(ctx, out, sizeof(float) * db->d, db->x.as<float>() + row0 * db->ld,
+            sizeof(float) * db->ld, sizeof(float) * db->d, count);
   cs.finish();
   VSK_API_END(ctx);
 }

@@ -57,7 +57,64 @@ __global__ void k_pq_lut(const float *q, int64_t nq, int32_t ldq,
   }
 }
 
-// codes[i][m] = argmin_c |x_m - C_m[c]|^2 (strict '<'), one thread per (i, m)
+// codes[i][m] = argmin_c |x_m - C_m[c]|^2 (strict '<': the first minimum
+// wins), each sum over j in ascending order without FMA.  Block (bx, m):
+// codebook m staged in LDS (every lane reads the same codeword, a broadcast),
+// one row per thread with its segment in registers when DS (compile-time
+// dsub) is nonzero.
+template <int DS>
+__global__ __launch_bounds__(256) void k_pq_encode_lds(
+    const float *x, int64_t n, int32_t ldx, const float *cb, int32_t M,
+    int32_t ksub, int32_t dsub, uint8_t *codes) {
+#pragma clang fp contract(off)
+  extern __shared__ float s_cb[];  // ksub x dsub
+  const int32_t m = blockIdx.y;
+  const int32_t ds = DS > 0 ? DS : dsub;
+  const float *cbm = cb + (int64_t)m * ksub * ds;
+  for (int32_t i = threadIdx.x; i < ksub * ds; i += blockDim.x) s_cb[i] = cbm[i];
+  __syncthreads();
+  for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < n;
+       r += (int64_t)gridDim.x * blockDim.x) {
+    const float *xs = x + r * ldx + (int64_t)m * ds;
+    float best = __int_as_float(0x7f800000);
+    int32_t bc = 0;
+    if constexpr (DS > 0) {
+      float xv[DS];
+#pragma unroll
+      for (int j = 0; j < DS; ++j) xv[j] = xs[j];
+      for (int32_t c = 0; c < ksub; ++c) {
+        const float *cw = s_cb + c * DS;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+          float t = xv[j] - cw[j];
+          acc = acc + t * t;
+        }
+        if (acc < best) {
+          best = acc;
+          bc = c;
+        }
+      }
+    } else {
+      for (int32_t c = 0; c < ksub; ++c) {
+        const float *cw = s_cb + c * ds;
+        float acc = 0.f;
+        for (int j = 0; j < ds; ++j) {
+          float t = xs[j] - cw[j];
+          acc = acc + t * t;
+        }
+        if (acc < best) {
+          best = acc;
+          bc = c;
+        }
+      }
+    }
+    codes[r * M + m] = (uint8_t)bc;
+  }
+}
+
+// same result for codebooks too large for LDS: one thread per (row, m),
+// codewords read from global memory
 __global__ void k_pq_encode(const float *x, int64_t n, int32_t ldx,
                             const float *cb, int32_t M, int32_t ksub,
                             int32_t dsub, uint8_t *codes) {
@@ -72,18 +129,55 @@ __global__ void k_pq_encode(const float *x, int64_t n, int32_t ldx,
     int32_t bc = 0;
     for (int32_t c = 0; c < ksub; ++c) {
       const float *cw = cb + ((int64_t)m * ksub + c) * dsub;
-      float s = 0.f;
+      float acc = 0.f;
       for (int j = 0; j < dsub; ++j) {
         float t = xs[j] - cw[j];
-        s = s + t * t;
+        acc = acc + t * t;
       }
-      if (s < best) {
-        best = s;
+      if (acc < best) {
+        best = acc;
         bc = c;
       }
     }
     codes[i] = (uint8_t)bc;
   }
+}
+
+static unsigned grid1(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 16384 ? (g > 0 ? g : 1) : 16384);
+}
+
+static void launch_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *dx,
+                          int64_t n, uint8_t *codes) {
+  const size_t lds = sizeof(float) * (size_t)pq->ksub * pq->dsub;
+  KernelTimer t(ctx, "pq_encode", (double)n * pq->M);
+  if (lds <= 64 * 1024) {
+    int64_t bx = ceil_div(n, 256);
+    if (bx > 2048) bx = 2048;
+    dim3 grid((unsigned)bx, (unsigned)pq->M);
+    switch (pq->dsub) {
+      case 4:
+        k_pq_encode_lds<4><<<grid, 256, lds, ctx->stream>>>(
+            dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, codes);
+        break;
+      case 8:
+        k_pq_encode_lds<8><<<grid, 256, lds, ctx->stream>>>(
+            dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, codes);
+        break;
+      case 16:
+        k_pq_encode_lds<16><<<grid, 256, lds, ctx->stream>>>(
+            dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, codes);
+        break;
+      default:
+        k_pq_encode_lds<0><<<grid, 256, lds, ctx->stream>>>(
+            dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, codes);
+    }
+  } else {
+    k_pq_encode<<<grid1(n * pq->M), 256, 0, ctx->stream>>>(
+        dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, codes);
+  }
+  check_launch("pq_encode");
 }
 
 struct AdcArgs {
@@ -239,11 +333,6 @@ __global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
   }
 }
 
-static unsigned grid1(int64_t n) {
-  int64_t g = ceil_div(n, 256);
-  return (unsigned)(g < 16384 ? (g > 0 ? g : 1) : 16384);
-}
-
 static void require_pq(const vsk_pq *pq) {
   VSK_REQUIRE(pq, VSK_ERR_INVALID_ARGUMENT, "pq is null");
 }
@@ -315,13 +404,7 @@ vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,
   const float *dx = static_cast<const float *>(
       input_to_device(ctx, x, sizeof(float) * n * pq->d, "pq.x"));
   OutputStage oc(ctx, codes, (size_t)n * pq->M, "out.codes");
-  {
-    KernelTimer t(ctx, "pq_encode");
-    k_pq_encode<<<grid1(n * pq->M), 256, 0, ctx->stream>>>(
-        dx, n, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub,
-        oc.ptr<uint8_t>());
-    check_launch("pq_encode");
-  }
+  launch_encode(ctx, pq, dx, n, oc.ptr<uint8_t>());
   oc.copy_back();
   cs.finish();
   VSK_API_END(ctx);

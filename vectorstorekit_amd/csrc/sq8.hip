@@ -239,9 +239,7 @@ static const int8_t *codes_to_device(vsk_ctx *ctx, const int8_t *p, int64_t n,
   if (dev && ldc == d) return p;
   int8_t *out = static_cast<int8_t *>(ctx->scratch_ptr(slot, (size_t)n * ldc));
   if (ldc != d) fill_i32(ctx, reinterpret_cast<int32_t *>(out), n * ldc / 4, 0);
-  VSK_HIP(hipMemcpy2DAsync(out, ldc, p, d, d, n,
-                           dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                           ctx->stream));
+  copy_rows(ctx, out, ldc, p, d, d, n);
   return out;
 }
 
@@ -352,10 +350,7 @@ vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
   db->codes.reserve((size_t)n * db->ldc);
   if (db->ldc != d)
     fill_i32(ctx, db->codes.as<int32_t>(), n * db->ldc / 4, 0);
-  bool dev = is_device_ptr(codes);
-  VSK_HIP(hipMemcpy2DAsync(db->codes.p, db->ldc, codes, d, d, n,
-                           dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                           ctx->stream));
+  copy_rows(ctx, db->codes.p, db->ldc, codes, d, d, n);
   cs.finish();
   *out = db.release();
   VSK_API_END(ctx);

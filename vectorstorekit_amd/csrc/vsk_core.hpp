@@ -135,6 +135,13 @@ struct OutputStage {
   void copy_back();  // enqueue device->host copy when user is host memory
 };
 
+// rows x row_bytes from src (row pitch src_pitch) to dst (dst_pitch) on the
+// context's stream; either side may be host memory.  A host side moves in
+// whole chunks through a device staging slot and the pitch change runs as a
+// device-to-device copy, so narrow rows never become one transfer per row.
+void copy_rows(vsk_ctx *ctx, void *dst, size_t dst_pitch, const void *src,
+               size_t src_pitch, size_t row_bytes, int64_t rows);
+
 // pad rows of a (rows x d) fp32 matrix to stride ld on the device
 const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
                                    int32_t d, int32_t ld,

@@ -72,12 +72,15 @@ class IVFIndex:
         cent = x[rng.choice(x.shape[0], k, replace=False)].copy()
         for _ in range(iterations):
             self.set_centroids(cent)
-            a = self.assign(x)
-            sums = np.zeros((k, x.shape[1]), np.float64)
-            np.add.at(sums, a, x)
+            a = np.asarray(self.assign(x))
+            # per-cluster sums in row order: stable sort by cluster, then one
+            # float64 reduction per contiguous segment
+            order = np.argsort(a, kind="stable")
             cnt = np.bincount(a, minlength=k)
+            start = np.concatenate(([0], np.cumsum(cnt)[:-1]))
             nz = cnt > 0
-            cent[nz] = (sums[nz] / cnt[nz, None]).astype(np.float32)
+            sums = np.add.reduceat(x[order].astype(np.float64), start[nz], axis=0)
+            cent[nz] = (sums / cnt[nz, None]).astype(np.float32)
         self.set_centroids(cent)
 
     def getCentroids(self) -> np.ndarray:

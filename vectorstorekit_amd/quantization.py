@@ -101,6 +101,33 @@ class SQ8Database:
 class ProductQuantizer:
     """PQ with trained codebooks (M, ksub, dsub) and resident codes."""
 
+    @classmethod
+    def train(cls, ctx: Context, vectors, M: int, ksub: int = 256, iterations: int = 10,
+              seed: int = 0) -> "ProductQuantizer":
+        """ProductQuantizer.train (Quantization/ProductQuantizer.swift:34-64):
+        per segment, Lloyd k-means (Clustering/KMeansClustering.swift:48-113)
+        from a seeded sample of distinct rows; nearest-codeword assignment
+        runs on the GPU (strict '<', first minimum), means on the host."""
+        from .ivf import IVFConfiguration, IVFIndex
+
+        x = np.asarray(vectors.cpu().numpy() if _lib._is_torch(vectors) else vectors,
+                       np.float32)
+        n, d = x.shape
+        if d % M:
+            raise VSKError(-2, f"dimension {d} is not a multiple of {M} segments")
+        if n < ksub:
+            raise VSKError(-2, f"insufficient training data: {n} < {ksub}")
+        dsub = d // M
+        books = np.empty((M, ksub, dsub), np.float32)
+        for m in range(M):
+            seg = np.ascontiguousarray(x[:, m * dsub:(m + 1) * dsub])
+            km = IVFIndex(ctx, IVFConfiguration(dimensions=dsub, numberOfCentroids=ksub,
+                                                numberOfProbes=1))
+            km.train(seg, iterations=iterations, seed=seed + m)
+            books[m] = km.getCentroids()
+            km.free()
+        return cls(ctx, books)
+
     def __init__(self, ctx: Context, codebooks):
         self.ctx = ctx
         cb = np.ascontiguousarray(codebooks, np.float32)
