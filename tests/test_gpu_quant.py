@@ -26,8 +26,14 @@ def test_sq8_train_encode_bit_exact(ctx, per_dim):
     np.testing.assert_array_equal(sq.quantizeBatch(x), O.sq8_encode(x, es, eo))
 
 
-@pytest.mark.parametrize("shape", [(20_000, 128, 37, 100), (3000, 45, 70, 10), (500, 7, 3, 1)])
+@pytest.mark.parametrize("shape", [(20_000, 128, 37, 100), (3000, 45, 70, 10), (500, 7, 3, 1),
+                                   (30_000, 200, 130, 50), (20_000, 300, 40, 20),
+                                   (8000, 700, 20, 10), (3000, 1100, 9, 5),
+                                   (40_000, 64, 1100, 10)])
 def test_sq8_search_bit_exact(ctx, shape):
+    """Every scan variant: code lengths of 1, 2, 4, 8 and 16 64-byte k-steps
+    (register-resident kernel) and over 1024 bytes (LDS kernel); several
+    query groups and filtered chunks; a duplicated row for the tie rule."""
     n, d, nq, k = shape
     print(f"sq8 n={n} d={d} nq={nq} k={k}", flush=True)
     rng = np.random.default_rng(n + d)

@@ -179,7 +179,7 @@ int64_t query_batch(int64_t nq, int64_t cap) {
 
 void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
                       int64_t cap, const ScanFn &scan, uint64_t *best,
-                      const char *select_name) {
+                      const char *select_name, int64_t max_growth) {
   if (nq <= 0) return;
   fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
   if (n <= 0) return;
@@ -205,7 +205,9 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     } else {
       // expected survivors of a chunk of c rows after r0 rows are about
       // k*c/r0; keep that near cap/2
-      int64_t grow = r0 * (cap / (2 * (int64_t)k));
+      int64_t factor = cap / (2 * (int64_t)k);
+      if (max_growth > 0 && factor > max_growth) factor = max_growth;
+      int64_t grow = r0 * factor;
       c = grow > cap ? grow : cap;
       if (c > n - r0) c = n - r0;
     }

@@ -134,6 +134,225 @@ __global__ __launch_bounds__(256) void k_sq8_scan(Sq8Args a) {
   }
 }
 
+// Register-resident scan for codes up to 1024 bytes (the common case).
+// Each wave keeps QT query tiles (16 queries each) of KS 64-byte k-steps as
+// v_mfma_i32_16x16x64_i8 B operands in registers for the whole launch and
+// streams 16-row A tiles of the database straight from memory (buffer loads,
+// no LDS); the four waves of a workgroup hold different queries and read the
+// same rows, which they share through L1.  The filter test is one integer
+// compare per score against the query's score floor; the 64-bit key is built
+// only where a score can pass.  Workgroup L runs on XCD L % 8, and the query
+// groups of one row split are consecutive slots of one XCD so they share its
+// L2.
+
+template <int RT, int KS, int QT>
+__device__ __forceinline__ void sq8_mma(const i4 (&ar)[RT][KS],
+                                        const i4 (&bq)[QT][KS],
+                                        i4 (&acc)[RT][QT]) {
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < QT; ++j) acc[i][j] = i4{0, 0, 0, 0};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < QT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ar[i][ks], bq[j][ks],
+                                                          acc[i][j], 0, 0, 0);
+}
+
+// Filtered candidates are staged per wave in LDS (SQ_WBUF entries) and
+// appended to the global per-query lists only when the list fills and at
+// the end, 64 at a time: an atomic that returns a value makes the wave wait
+// for every memory operation it has in flight, row prefetches included.
+constexpr int SQ_WBUF = 512;
+
+__device__ __forceinline__ void sq8_flush(const Sq8Args &a, const uint64_t *lkey,
+                                          const int32_t *lq, int32_t &nbuf,
+                                          int lane) {
+  for (int32_t e = lane; e < nbuf; e += 64) {
+    const int32_t q = lq[e];
+    const int c = atomicAdd(&a.counts[q], 1);
+    if (c < a.cap) a.cand[(int64_t)q * a.cap + c] = lkey[e];
+  }
+  nbuf = 0;
+}
+
+// scores of rows t0 .. t0 + 16*RT - 1 (absolute ids) against the wave's
+// queries: every key of valid rows in the dense chunk, else the keys that
+// pass the query's threshold
+template <int RT, int QT, bool DENSE>
+__device__ __forceinline__ void sq8_epilogue(
+    const Sq8Args &a, const i4 (&acc)[RT][QT], int64_t t0, int64_t s1,
+    int lane, int64_t qw0, const bool (&qok)[QT], const int32_t (&smin)[QT],
+    const uint64_t (&th)[QT], uint64_t *lkey, int32_t *lq, int32_t &nbuf) {
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int64_t rb = t0 + 16 * i + 4 * (lane >> 4);  // + r
+    if (DENSE) {
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        if (!qok[j]) continue;
+        const int64_t q = qw0 + 16 * j + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (rb + r < s1)
+            a.cand[q * a.cap + (rb + r - a.r0)] =
+                vsk_key_i32(-acc[i][j][r], (uint32_t)(rb + r));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        const int32_t m01 = acc[i][j][0] > acc[i][j][1] ? acc[i][j][0] : acc[i][j][1];
+        const int32_t m23 = acc[i][j][2] > acc[i][j][3] ? acc[i][j][2] : acc[i][j][3];
+        const bool hit = (m01 > m23 ? m01 : m23) >= smin[j];
+        if (!__builtin_amdgcn_ballot_w64(hit)) continue;  // the common case
+        // key <= th[j]: a higher score, or the floor score at a row id not
+        // above the threshold's.  Control flow stays wave-uniform so nbuf
+        // stays uniform: passing keys take consecutive slots of the wave's
+        // LDS list in lane order.
+        const uint32_t trow = (uint32_t)th[j];
+        const int32_t q = (int32_t)(qw0 + 16 * j + (lane & 15));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t v = acc[i][j][r];
+          const bool p = rb + r < s1 &&
+                         (v > smin[j] || (v == smin[j] && (uint32_t)(rb + r) <= trow));
+          const uint64_t m = __builtin_amdgcn_ballot_w64(p);
+          if (!m) continue;
+          if (p) {
+            const int32_t pos =
+                nbuf + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                           (uint32_t)(m >> 32),
+                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            lkey[pos] = vsk_key_i32(-v, (uint32_t)(rb + r));
+            lq[pos] = q;
+          }
+          nbuf += __builtin_popcountll(m);
+        }
+        if (nbuf > SQ_WBUF - 256) sq8_flush(a, lkey, lq, nbuf, lane);
+      }
+    }
+  }
+}
+
+template <int RT, int KS, int QT, bool DENSE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_sq8_reg(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
+  const int grp = slot % groups;
+  const int split = (slot / groups) * 8 + xcd;
+  if (split >= 8 * splits_per_xcd) return;
+  const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+  const int64_t qw0 = ((int64_t)grp * 4 + w) * (QT * 16);
+  if (qw0 >= a.nq) return;
+  const int kc = 16 * (lane >> 4);  // this lane's byte chunk of a k-step
+
+  i4 bq[QT][KS];
+  int32_t smin[QT];
+  uint64_t th[QT];
+  bool qok[QT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int64_t q = qw0 + 16 * j + (lane & 15);
+    qok[j] = q < a.nq && (!a.active || a.active[q]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = 64 * ks + kc;
+      bq[j][ks] = (qok[j] && off < a.kbytes)
+                      ? *reinterpret_cast<const i4 *>(a.Q + q * a.ldq + off)
+                      : i4{0, 0, 0, 0};
+    }
+    th[j] = (!DENSE && qok[j]) ? a.thresh[q] : 0;
+    // key <= th needs -score <= the distance half of th: score >= smin
+    smin[j] = qok[j] ? -(int32_t)((uint32_t)(th[j] >> 32) ^ 0x80000000u)
+                     : 0x7FFFFFFF;
+  }
+
+  const int64_t nrows = s1 - s0;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.X + s0 * a.ldx), 0, (int32_t)(nrows * a.ldx), 0x00020000);
+  const int32_t lrow = (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  i4 ar0[RT][KS], ar1[RT][KS];
+#define SR_LOAD(AR, T)                                                       \
+  _Pragma("unroll") for (int i = 0; i < RT; ++i)                          \
+  _Pragma("unroll") for (int ks = 0; ks < KS; ++ks)                          \
+      AR[i][ks] = __builtin_bit_cast(                                        \
+          i4, __builtin_amdgcn_raw_buffer_load_b128(                         \
+                  rx, (int32_t)((T) + 16 * i) * (int32_t)a.ldx + lrow,       \
+                  64 * ks, 0))
+  i4 acc[RT][QT];
+  __shared__ uint64_t s_key[4][DENSE ? 1 : SQ_WBUF];
+  __shared__ int32_t s_q[4][DENSE ? 1 : SQ_WBUF];
+  int32_t nbuf = 0;  // wave-uniform count of staged candidates
+  // two row blocks in flight: a block's buffer is refilled with the block
+  // after next once its multiplies and filter are done.  Loads past the
+  // split read zeros from the buffer descriptor, so they need no condition
+  // (a conditional load would make the compiler wait for every load at the
+  // loop head).
+  constexpr int32_t RB = 16 * RT;
+  const int32_t nr = (int32_t)nrows;
+  // scheduling barriers keep the loads and multiplies in program order:
+  // the first block's loads are issued before the second's (on entry as on
+  // the loop's back edge), so the wait at the loop head covers only them
+  SR_LOAD(ar0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  SR_LOAD(ar1, RB);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int32_t t = 0; t < nr; t += 2 * RB) {
+    sq8_mma<RT, KS, QT>(ar0, bq, acc);
+    sq8_epilogue<RT, QT, DENSE>(a, acc, s0 + t, s1, lane, qw0, qok, smin, th,
+                                s_key[w], s_q[w], nbuf);
+    SR_LOAD(ar0, t + 2 * RB);
+    __builtin_amdgcn_sched_barrier(0);
+    // the second block may lie past the split: it reads zeros and the
+    // epilogue drops its rows (no exit mid-body, which would make the
+    // compiler carry the prefetch registers around the loop by copies)
+    sq8_mma<RT, KS, QT>(ar1, bq, acc);
+    sq8_epilogue<RT, QT, DENSE>(a, acc, s0 + t + RB, s1, lane, qw0, qok, smin,
+                                th, s_key[w], s_q[w], nbuf);
+    SR_LOAD(ar1, t + 3 * RB);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (!DENSE && nbuf > 0) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
+#undef SR_LOAD
+}
+
+template <int RT, int KS, int QT>
+static void launch_reg(vsk_ctx *ctx, const Sq8Args &a, bool dense) {
+  const int64_t rows = a.r1 - a.r0;
+  const int64_t qpg = 4 * QT * 16;  // queries per workgroup
+  const int64_t groups = ceil_div(a.nq, qpg);
+  // row splits: a multiple of 8 (one share per XCD), about 4096 workgroups
+  int64_t splits = ceil_div(4096, groups);
+  const int64_t max_splits = ceil_div(rows, 16 * RT);
+  if (splits > max_splits) splits = max_splits;
+  if (splits < 1) splits = 1;
+  Sq8Args b = a;
+  b.rows_per_split = ceil_div(ceil_div(rows, splits), 16 * RT) * (16 * RT);
+  // buffer offsets (row * ldx, prefetch up to 4 blocks past the end) stay
+  // within int32
+  const int64_t max_rows = 0x7FFFFFFFll / a.ldx - 4 * 16 * RT;
+  if (b.rows_per_split > max_rows)
+    b.rows_per_split = max_rows / (16 * RT) * (16 * RT);
+  splits = ceil_div(ceil_div(rows, b.rows_per_split), 8) * 8;
+  const int64_t spx = splits / 8;
+  const int64_t nblocks = 8 * spx * groups;
+  if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
+  if (dense)
+    k_sq8_reg<RT, KS, QT, true><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(
+        b, (int32_t)groups, (int32_t)spx);
+  else
+    k_sq8_reg<RT, KS, QT, false><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(
+        b, (int32_t)groups, (int32_t)spx);
+}
+
 static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
   const int64_t rows = a.r1 - a.r0;
   if (rows <= 0 || a.nq <= 0) return;
@@ -148,7 +367,18 @@ static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
   dim3 grid((unsigned)qt, (unsigned)splits);
   KernelTimer t(ctx, dense ? "sq8_mfma_dense" : "sq8_mfma_filter",
                 (double)a.nq * (double)rows);
-  if (dense)
+  const int32_t ksteps = (a.kbytes + 63) / 64;
+  if (ksteps <= 1)
+    launch_reg<2, 1, 8>(ctx, a, dense);
+  else if (ksteps <= 2)
+    launch_reg<2, 2, 8>(ctx, a, dense);
+  else if (ksteps <= 4)
+    launch_reg<2, 4, 4>(ctx, a, dense);
+  else if (ksteps <= 8)
+    launch_reg<1, 8, 2>(ctx, a, dense);
+  else if (ksteps <= 16)
+    launch_reg<1, 16, 1>(ctx, a, dense);
+  else if (dense)
     k_sq8_scan<true><<<grid, 256, 0, ctx->stream>>>(a);
   else
     k_sq8_scan<false><<<grid, 256, 0, ctx->stream>>>(a);
@@ -404,7 +634,10 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
       a.counts = r.counts;
       launch_sq8(ctx, a, r.dense);
     };
-    progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k, "sq8_select");
+    // chunks grow at most 8x, so the running threshold is tight before the
+    // bulk of the rows is scanned (the filter epilogue is cheap only when
+    // few scores pass)
+    progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k, "sq8_select", 8);
   }
   OutputStage os(ctx, out_score, sizeof(int32_t) * nq * k, "out.score");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");

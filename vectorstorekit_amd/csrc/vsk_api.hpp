@@ -79,10 +79,12 @@ using ScanFn = std::function<void(const ScanRequest &)>;
 // chunks: the first chunk is kept whole, later chunks only keep rows that
 // beat the running k-th key of their query; a query whose survivors
 // overflow cap re-scans the chunk in whole sub-chunks.  best: nq*k keys
-// (device), sorted ascending per query on return.
+// (device), sorted ascending per query on return.  A chunk after the first
+// holds at most cap/(2k) times the rows already seen, and at most max_growth
+// times when that is positive.
 void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
                       int64_t cap, const ScanFn &scan, uint64_t *best,
-                      const char *select_name);
+                      const char *select_name, int64_t max_growth = 0);
 
 // candidate buffer capacity per query used by the progressive scans
 int64_t default_cap(int32_t k);
