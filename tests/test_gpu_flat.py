@@ -142,6 +142,74 @@ def test_errors(ctx):
     assert e.value.kind == "emptyInput"
 
 
+SCREEN = [METRIC_L2SQ, METRIC_L2, METRIC_COSINE_NORMALIZED, METRIC_DOT]
+
+
+@pytest.mark.parametrize("metric", SCREEN)
+@pytest.mark.parametrize("shape", [(3000, 20, 128, 10), (40_000, 64, 100, 50),
+                                   (20_000, 33, 37, 100), (25_000, 10, 768, 320),
+                                   (6000, 12, 96, 20)])
+def test_screen_bit_exact(ctx, metric, shape):
+    """The screened metrics (one-pass bf16 screen, proven bound, fp32
+    rescore) return the CPU reference's sequential fp32 distances and its
+    (distance, id) order exactly: one dense chunk, filtered chunks, odd d,
+    and the largest k the screen takes."""
+    n, nq, d, k = shape
+    x, q = _data(n + d + metric, n, nq, d, normalize=metric == METRIC_COSINE_NORMALIZED)
+    print(f"screen metric={metric} n={n} nq={nq} d={d} k={k}", flush=True)
+    ctx.profile(True)
+    ctx.profile_reset()
+    gd, gi = VectorDatabase(ctx, x).search(q, k, metric)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    assert "flat_screen_dense" in stats and "screen_rescore" in stats
+    od, oi = O.search_flat(q, x, k, metric)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+@pytest.mark.parametrize("metric", SCREEN)
+def test_screen_fallback_near_ties(ctx, metric):
+    """Rows closer to each other than the screen's error bound: the margin
+    test fails for every query, at the wide second screen too, the exact
+    VALU scan redoes them, and the result is still the reference's, bit for
+    bit."""
+    rng = np.random.default_rng(70 + metric)
+    d = 64
+    base = rng.standard_normal(d).astype(np.float32)
+    x = (base + 1e-4 * rng.standard_normal((20_000, d))).astype(np.float32)
+    q = (base + 1e-4 * rng.standard_normal((8, d))).astype(np.float32)
+    if metric == METRIC_COSINE_NORMALIZED:
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+    print(f"screen fallback metric={metric}", flush=True)
+    ctx.profile(True)
+    ctx.profile_reset()
+    gd, gi = VectorDatabase(ctx, x).search(q, 10, metric)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    assert stats["screen_retry"][2] == 8  # work counter: queries redone
+    assert stats["screen_fallback"][2] == 8
+    od, oi = O.search_flat(q, x, 10, metric)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+def test_screen_normalized_db_and_device_queries(ctx):
+    """Rows normalised on upload and queries already on the device: the
+    rescore reads the stored (normalised) rows."""
+    import torch
+
+    x, q = _data(31, 30_000, 40, 96)
+    db = VectorDatabase(ctx, x, normalize=True)
+    xn = db.read()
+    qn = q / np.linalg.norm(q, axis=1, keepdims=True)
+    gd, gi = db.search(torch.from_numpy(qn).cuda(), 25, METRIC_COSINE_NORMALIZED)
+    od, oi = O.search_flat(qn, xn, 25, METRIC_COSINE_NORMALIZED)
+    np.testing.assert_array_equal(gi.cpu().numpy(), oi)
+    np.testing.assert_array_equal(gd.cpu().numpy(), od)
+
+
 def test_upload_read_roundtrip_padded_chunked(ctx):
     """Host rows with a pitch that needs padding (d=129 -> 132) and more than
     one 64 MB staging chunk: upload and read-back are exact, from host and

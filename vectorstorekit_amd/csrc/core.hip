@@ -173,7 +173,8 @@ const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
                                    const std::string &slot) {
   if (rows == 0) return nullptr;
   bool dev = is_device_ptr(p);
-  if (dev && ld == d) return p;
+  // used in place when already laid out (kernels load 16-byte vectors)
+  if (dev && ld == d && (reinterpret_cast<uintptr_t>(p) & 15) == 0) return p;
   float *out = static_cast<float *>(
       ctx->scratch_ptr(slot, sizeof(float) * (size_t)rows * ld));
   if (ld != d)
@@ -343,6 +344,7 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   c->device = device;
   const char *fk = getenv("VSK_FLAT_KERNEL");
   c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
+  c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
   // a blocking stream: it orders itself after work on the null stream, so
   // device buffers produced there (e.g. by torch) are complete when read
   if (hipStreamCreate(&c->stream) != hipSuccess ||

@@ -18,6 +18,8 @@
 // dot product and precomputed norms:
 //   L2^2 = |q|^2 + |x|^2 - 2 q.x       cosine = 1 - q.x / (|q||x| + 1e-8)
 //   normalised cosine = 1 - q.x        dot = -q.x
+#include <cstring>
+
 #include "flat.hpp"
 
 namespace vsk {
@@ -181,7 +183,9 @@ __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
 // rows, i.e. the first minimum under strict '<' (findNearestCentroid,
 // Indexes/IVFIndex.swift:514-527), and writes the row index to argmin[q].
 constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
-enum { OP_L1 = 0, OP_L2SEQ = 1 };
+// sequential (dimension-order, no FMA) terms and final transforms of the
+// exact VALU kernel, one per metric of the CPU reference
+enum { OP_L1 = 0, OP_L2SEQ = 1, OP_L2SQSEQ = 2, OP_CNSEQ = 3, OP_DOTSEQ = 4 };
 
 __device__ inline uint64_t shfl_xor_u64(uint64_t v, int m) {
   uint32_t lo = __shfl_xor((uint32_t)v, m);
@@ -194,10 +198,20 @@ __device__ inline float valu_term(float q, float x) {
 #pragma clang fp contract(off)
   if constexpr (OP == OP_L1) {
     return fabsf(q - x);
-  } else {
+  } else if constexpr (OP == OP_L2SEQ || OP == OP_L2SQSEQ) {
     float t = q - x;
     return t * t;
+  } else {
+    return q * x;
   }
+}
+
+template <int OP>
+__device__ inline float valu_final(float s) {
+  if constexpr (OP == OP_L2SEQ) return sqrtf(s);
+  else if constexpr (OP == OP_CNSEQ) return 1.0f - s;
+  else if constexpr (OP == OP_DOTSEQ) return -s;
+  else return s;
 }
 
 template <int MODE, int OP>
@@ -280,12 +294,12 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
         if (!qok[v]) continue;
-        const float dist = OP == OP_L2SEQ ? sqrtf(acc[u][v]) : acc[u][v];
+        const float dist = valu_final<OP>(acc[u][v]);
         if constexpr (MODE == MODE_ARGMIN) {
           uint64_t key = vsk_key(dist, (uint32_t)row);
           best[v] = key < best[v] ? key : best[v];
         } else {
-          // L2SEQ keys/matrix carry the sqrt distance already
+          // the keys/matrix carry the final distance already
           emit<MODE, VSK_METRIC_L1>(a, qi[v], row, dist, th[v]);
         }
       }
@@ -344,17 +358,21 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   splits = ceil_div(rows, a.rows_per_split);
   if (qt > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
   dim3 grid((unsigned)qt, (unsigned)splits);
-  const bool valu = a.metric == VSK_METRIC_L1 || a.metric == METRIC_L2_EXACT;
+  const bool valu = a.metric == VSK_METRIC_L1 || a.metric >= METRIC_L2_EXACT;
   static const char *names[2][4] = {
       {"flat_mfma_dense", "flat_mfma_filter", "flat_mfma_matrix", "flat_mfma_argmin"},
       {"flat_valu_dense", "flat_valu_filter", "flat_valu_matrix", "flat_valu_argmin"}};
   const char *name = names[valu ? 1 : 0][mode];
   KernelTimer t(ctx, name, (double)a.nq * (double)rows);
   if (valu) {
-    if (a.metric == VSK_METRIC_L1)
-      launch_valu<OP_L1>(ctx, grid, a, mode, argmin);
-    else
-      launch_valu<OP_L2SEQ>(ctx, grid, a, mode, argmin);
+    switch (a.metric) {
+    case VSK_METRIC_L1: launch_valu<OP_L1>(ctx, grid, a, mode, argmin); break;
+    case METRIC_L2_EXACT: launch_valu<OP_L2SEQ>(ctx, grid, a, mode, argmin); break;
+    case METRIC_L2SQ_EXACT: launch_valu<OP_L2SQSEQ>(ctx, grid, a, mode, argmin); break;
+    case METRIC_CN_EXACT: launch_valu<OP_CNSEQ>(ctx, grid, a, mode, argmin); break;
+    case METRIC_DOT_EXACT: launch_valu<OP_DOTSEQ>(ctx, grid, a, mode, argmin); break;
+    default: fail(VSK_ERR_INVALID_ARGUMENT, "no exact kernel for this metric");
+    }
   } else {
     if (mode == MODE_ARGMIN)
       fail(VSK_ERR_UNSUPPORTED, "argmin needs an exact VALU metric");
@@ -371,15 +389,15 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   check_launch(name);
 }
 
-static const float *x_aux(const vsk_db *db, int32_t metric) {
+const float *x_aux(const vsk_db *db, int32_t metric) {
   if (metric == VSK_METRIC_L2SQ || metric == VSK_METRIC_L2)
     return db->sqnorm.as<float>();
   if (metric == VSK_METRIC_COSINE) return db->norm.as<float>();
   return nullptr;
 }
 
-static float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
-                    int32_t ld, int32_t metric) {
+float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
+             int32_t metric) {
   if (metric != VSK_METRIC_L2SQ && metric != VSK_METRIC_L2 &&
       metric != VSK_METRIC_COSINE)
     return nullptr;
@@ -392,28 +410,36 @@ static float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
 }
 
 static bool use_bf16x3(const vsk_ctx *ctx, int32_t metric) {
-  return !ctx->flat_fp32 && metric != VSK_METRIC_L1 && metric != METRIC_L2_EXACT;
+  return !ctx->flat_fp32 && metric != VSK_METRIC_L1 && metric < METRIC_L2_EXACT;
 }
 
-// hi/lo planes of the database (once) and of a query batch (per call)
-static SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
-                            int64_t nq) {
+SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+                     int64_t nq, bool qlo, float *qnh, float *qnr) {
   const int32_t ldb = (db->d + 31) & ~31;
   if (!db->split.p) {
     db->split.reserve(sizeof(uint16_t) * 2 * (size_t)db->n * ldb);
     db->ldb = ldb;
     uint16_t *h = db->split.as<uint16_t>();
+    uint32_t *mb =
+        static_cast<uint32_t *>(ctx->scratch_ptr("flat.splitmax", 2 * sizeof(uint32_t)));
+    fill_i32(ctx, reinterpret_cast<int32_t *>(mb), 2, 0);
     split_bf16(ctx, db->x.as<float>(), db->n, db->d, db->ld, h,
-               h + (size_t)db->n * ldb, ldb);
+               h + (size_t)db->n * ldb, ldb, nullptr, nullptr, mb);
+    uint32_t hb[2];
+    VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    std::memcpy(&db->split_max_hi, &hb[0], sizeof(float));
+    std::memcpy(&db->split_max_res, &hb[1], sizeof(float));
   }
-  uint16_t *qs = static_cast<uint16_t *>(
-      ctx->scratch_ptr("flat.qsplit", sizeof(uint16_t) * 2 * (size_t)nq * ldb));
-  split_bf16(ctx, dq, nq, db->d, db->ld, qs, qs + (size_t)nq * ldb, ldb);
+  uint16_t *qs = static_cast<uint16_t *>(ctx->scratch_ptr(
+      "flat.qsplit", sizeof(uint16_t) * (qlo ? 2 : 1) * (size_t)nq * ldb));
+  split_bf16(ctx, dq, nq, db->d, db->ld, qs, qlo ? qs + (size_t)nq * ldb : nullptr,
+             ldb, qnh, qnr, nullptr);
   SplitPtrs s;
   s.xh = db->split.as<uint16_t>();
   s.xl = s.xh + (size_t)db->n * ldb;
   s.qh = qs;
-  s.ql = qs + (size_t)nq * ldb;
+  s.ql = qlo ? qs + (size_t)nq * ldb : nullptr;
   s.ldxb = ldb;
   s.ldqb = ldb;
   s.kb = ldb;
@@ -421,8 +447,19 @@ static SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
 }
 
 // top-k over a resident database for queries already on the device
-void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                       int64_t nq, int32_t k, int32_t metric, uint64_t *best) {
+  if (!ctx->flat_no_screen && screen_applies(metric, k)) {
+    screen_topk(ctx, db, dq, nq, k, metric, best);
+    return true;
+  }
+  approx_topk(ctx, db, dq, nq, k, metric, best, 3);
+  return false;
+}
+
+void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
+                 int32_t k, int32_t metric, uint64_t *best, int passes,
+                 float *qnh, float *qnr, int64_t max_growth) {
   const int64_t cap = default_cap(k);
   const int64_t qb = query_batch(nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
@@ -441,7 +478,9 @@ void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
     base.metric = metric;
     const bool x3 = use_bf16x3(ctx, metric);
     SplitPtrs sp{};
-    if (x3) sp = make_split(ctx, db, qbat, nb);
+    if (x3)
+      sp = make_split(ctx, db, qbat, nb, passes == 3, qnh ? qnh + b0 : nullptr,
+                      qnr ? qnr + b0 : nullptr);
     ScanFn scan = [&](const ScanRequest &r) {
       FlatArgs a = base;
       a.r0 = r.r0;
@@ -451,13 +490,15 @@ void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
       a.cand = r.cand;
       a.cap = r.cap;
       a.counts = r.counts;
-      if (x3)
-        launch_flat_bf16x3(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER);
+      if (x3 && passes == 1)
+        launch_flat_screen(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER);
+      else if (x3)
+        launch_flat_bf16x3(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER, passes);
       else
         launch_flat(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER, nullptr);
     };
     progressive_topk(ctx, nb, db->n, k, cap, scan, best + b0 * k,
-                     "flat_select");
+                     "flat_select", max_growth);
   }
 }
 
@@ -486,11 +527,11 @@ vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
   const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("flat.best", sizeof(uint64_t) * (size_t)nq * k));
-  flat_topk_device(ctx, db, dq, nq, k, metric, best);
+  const bool final_keys = flat_topk_device(ctx, db, dq, nq, k, metric, best);
   OutputStage od(ctx, out_dist, sizeof(float) * (size_t)nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * (size_t)nq * k, "out.ids");
-  decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2, nullptr,
-              od.ptr<float>(), oi.ptr<int64_t>());
+  decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2 && !final_keys,
+              nullptr, od.ptr<float>(), oi.ptr<int64_t>());
   od.copy_back();
   oi.copy_back();
   cs.finish();
@@ -525,7 +566,8 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
   a.mat = om.ptr<float>();
   a.ldm = db->n;
   if (use_bf16x3(ctx, metric))
-    launch_flat_bf16x3(ctx, a, make_split(ctx, db, dq, nq), MODE_MATRIX);
+    launch_flat_bf16x3(ctx, a, make_split(ctx, db, dq, nq, true, nullptr, nullptr),
+                       MODE_MATRIX);
   else
     launch_flat(ctx, a, MODE_MATRIX, nullptr);
   om.copy_back();

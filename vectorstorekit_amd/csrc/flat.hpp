@@ -9,6 +9,22 @@ namespace vsk {
 // internal metric: sqrt(sum (q-x)^2) summed in dimension order without FMA
 // (bit-identical to a sequential fp32 loop; VALU kernel)
 constexpr int32_t METRIC_L2_EXACT = 100;
+// the same for L2^2, normalised cosine (1 - dot) and dot (-dot)
+constexpr int32_t METRIC_L2SQ_EXACT = 101;
+constexpr int32_t METRIC_CN_EXACT = 102;
+constexpr int32_t METRIC_DOT_EXACT = 103;
+// the exact VALU metric that computes a public metric as the CPU reference
+// does (-1 if none)
+inline int32_t exact_metric(int32_t metric) {
+  switch (metric) {
+  case VSK_METRIC_L2SQ: return METRIC_L2SQ_EXACT;
+  case VSK_METRIC_L2: return METRIC_L2_EXACT;
+  case VSK_METRIC_COSINE_NORMALIZED: return METRIC_CN_EXACT;
+  case VSK_METRIC_DOT: return METRIC_DOT_EXACT;
+  case VSK_METRIC_L1: return VSK_METRIC_L1;
+  default: return -1;
+  }
+}
 
 enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2, MODE_ARGMIN = 3 };
 
@@ -41,19 +57,57 @@ struct SplitPtrs {
   int64_t ldxb, ldqb;
   int32_t kb;               // padded dimension (multiple of 32)
 };
-// hi = bf16(x), lo = bf16(x - hi) of an (n x ld) fp32 matrix, ldb columns
+// hi = bf16(x) and (lo non-null) lo = bf16(x - hi) of an (n x ld) fp32
+// matrix, ldb columns; nhi/nres (optional): per-row |hi| and |x - hi|,
+// rounded up, with their maxima over the rows atomically max-ed (as float
+// bits) into maxbits[0..1] when maxbits is given
 void split_bf16(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
-                uint16_t *hi, uint16_t *lo, int32_t ldb);
-void launch_flat_bf16x3(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode);
+                uint16_t *hi, uint16_t *lo, int32_t ldb, float *nhi = nullptr,
+                float *nres = nullptr, uint32_t *maxbits = nullptr);
+// bf16 MFMA scan: passes 3 = hi/lo split products (fp32-level accuracy),
+// passes 1 = hi products only (the screen; no matrix mode, no COSINE)
+void launch_flat_bf16x3(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
+                        int passes = 3);
+// the screen's one-pass kernel on 256 x 256 tiles (dense or filter mode;
+// L2^2, L2, normalised cosine, dot)
+void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode);
 
 // launch one scan over rows [a.r0, a.r1) of a.X for the a.nq queries of a.Q
 // (mode MODE_*; argmin output only for MODE_ARGMIN).  a.rows_per_split is
 // chosen here.
 void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin);
 
-// exact top-k of queries dq (device, stride db->ld) over a resident
-// database; best: nq*k keys
-void flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+// top-k of queries dq (device, stride db->ld) over a resident database;
+// best: nq*k keys.  Returns true when the keys hold the final distances
+// (the screen path: exact fp32, sqrt applied for L2), false when they hold
+// the kernel's distances (squared for L2).
+bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                       int64_t nq, int32_t k, int32_t metric, uint64_t *best);
+// progressive top-k on the bf16 kernel with the given passes (3: fp32-level
+// distances; 1: the screen's hi products) or, for L1, the exact VALU kernel;
+// qnh/qnr (optional): per-query |hi| and |q - hi| of the split;
+// max_growth: the progressive scan's chunk growth limit (0: none)
+void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
+                 int32_t k, int32_t metric, uint64_t *best, int passes,
+                 float *qnh = nullptr, float *qnr = nullptr,
+                 int64_t max_growth = 0);
+// the bf16 planes of the database (built once, with the maxima of |hi| and
+// |x - hi| over its rows) and of a query batch (lo plane when qlo; per-query
+// |hi| into qnh and |q - hi| into qnr when given)
+SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+                     int64_t nq, bool qlo, float *qnh, float *qnr);
+// |x|^2 (L2 metrics) or |x| (cosine) of the rows / of a query batch
+const float *x_aux(const vsk_db *db, int32_t metric);
+float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
+             int32_t metric);
+// exact top-k through the screen (flat_screen.hip): a one-pass bf16 scan
+// keeps screen_keep(k) candidates per query, a proven error bound shows they
+// hold the exact top-k, and an fp32 rescore in the CPU reference's summation
+// order ranks them (a query failing the bound is redone by the exact VALU
+// scan); best: final keys (exact distances)
+bool screen_applies(int32_t metric, int32_t k);
+int32_t screen_keep(int32_t k);
+void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
+                 int32_t k, int32_t metric, uint64_t *best);
 
 }  // namespace vsk

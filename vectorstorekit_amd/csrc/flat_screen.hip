@@ -1,0 +1,355 @@
+// flat_screen.hip -- exact flat top-k for L2^2, L2, normalised cosine and
+// dot: a one-pass bf16 MFMA screen, a proven bound on its error, and an fp32
+// rescore of the survivors in the CPU reference's own summation order.
+//
+// Bound.  With qh = bf16(q), xh = bf16(x) and the exact residuals
+// dq = q - qh, dx = x - xh, Cauchy-Schwarz gives
+//   |q.x - qh.xh| <= |qh||dx| + |dq||xh| + |dq||dx|.
+// Each product qh_i xh_i is exact in fp32 (8-bit significands), and any fp32
+// summation of d of them, in any order and with round-to-nearest or
+// truncation, errs by at most 2(d-1)u sum|qh_i xh_i| <= 2(d-1)u |qh||xh|,
+// u = 2^-24.  Taking the maxima of |xh| and |dx| over the rows bounds every
+// pair of one query: eps_dot(q).  The screen's distance a(x) of each metric
+// is then within eps(q) of the distance d(x) the rescore computes; eps adds
+// the error of the reference's sequential fp32 sum and of the metric's last
+// operations (norms and the final subtraction for L2^2, 1 - s for cosine).
+//
+// Claim: if A_kc - eps > A_k + eps, where A_j is the j-th smallest a over
+// all rows and the screen kept the kc rows of smallest a, those kc rows hold
+// the exact top-k.  Any other row y has d(y) >= a(y) - eps >= A_kc - eps,
+// while the k rows with a <= A_k have d <= A_k + eps: y is strictly beaten
+// by k rows.  For L2 the ranking distance is sqrt(d), and the test asks for
+// a relative gap of 2^-20 so that rounding of the square root cannot tie
+// them.  A query failing the test (about 1 in 100 on config 2, where some
+// 2k rows fall within the margin of 2^-8 of the norms) is screened again
+// keeping 1024 candidates, and one failing that too is redone by the exact
+// VALU scan, which evaluates the reference's formula for every row.
+//
+// The rescore sums in dimension order without FMA, exactly as the CPU
+// reference (Indexes/IVFIndex.swift:542-549 and
+// Acceleration/AccelerateOptimizer.swift:251-383 restated sequentially), so
+// the returned distances are bit-identical to it and the order is (distance,
+// row id) over exact fp32 distances.
+#include <vector>
+
+#include "flat.hpp"
+
+namespace vsk {
+
+bool screen_applies(int32_t metric, int32_t k) {
+  if (metric != VSK_METRIC_L2SQ && metric != VSK_METRIC_L2 &&
+      metric != VSK_METRIC_COSINE_NORMALIZED && metric != VSK_METRIC_DOT)
+    return false;
+  return screen_keep(k) <= VSK_MAX_K;
+}
+
+// candidates kept per query: on config 2 (k = 100) some 200-250 rows fall
+// within the bound's margin of the k-th, so 3k + 64 makes the second,
+// wider screen rare
+int32_t screen_keep(int32_t k) {
+  const int32_t kc = 3 * k + 64;
+  return kc < 256 ? 256 : kc;
+}
+
+// Exact distance of each screened candidate, summed in dimension order
+// without FMA as the CPU reference does.  A block is 4 waves; a wave owns 64
+// candidates of one query (uniform query loads).  Per 64-dim block the wave
+// gathers its 64 rows with 256-byte segments (16 lanes per row) into its own
+// LDS tile, then every lane continues the sequential sum of its row from
+// there: coalesced reads, bit-exact sums.  out[q][c] = key(distance, row);
+// NONE candidates stay NONE.
+constexpr int RS_W = 64;       // dims per gathered block
+constexpr int RS_LD = RS_W + 4;  // LDS row stride (floats): conflict-free
+
+template <int METRIC>
+__global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
+                                                 const float *Q, int64_t ldq,
+                                                 int32_t d, const uint64_t *cand,
+                                                 int32_t kc, uint64_t *out) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float tile[4][64 * RS_LD];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t q = blockIdx.x;
+  const int32_t c = blockIdx.y * 256 + threadIdx.x;
+  const uint64_t key = c < kc ? cand[q * kc + c] : VSK_KEY_NONE;
+  const bool valid = key != VSK_KEY_NONE;
+  const uint32_t row = (uint32_t)key;
+  if (!__builtin_amdgcn_ballot_w64(valid)) return;  // wave past the candidates
+  const float *qq = Q + q * ldq;
+  float *t = tile[w];
+  const int seg = lane & 15, sub = lane >> 4;  // 16 lanes per row segment
+  float s = 0.f;
+  for (int32_t j0 = 0; j0 < d; j0 += RS_W) {
+    // gather: rows sub, sub+4, ..., 4 per instruction
+#pragma unroll 4
+    for (int r = sub; r < 64; r += 4) {
+      const uint64_t kr = __shfl(key, r);
+      const bool ok = kr != VSK_KEY_NONE && j0 + 4 * seg < d;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (ok)
+        v = *reinterpret_cast<const float4 *>(X + (int64_t)(uint32_t)kr * ldx + j0 +
+                                              4 * seg);
+      *reinterpret_cast<float4 *>(t + r * RS_LD + 4 * seg) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int32_t jn = d - j0 < RS_W ? d - j0 : RS_W;
+    const float *xr = t + lane * RS_LD;
+    for (int32_t j = 0; j < jn; ++j) {
+      const float qv = qq[j0 + j], xv = xr[j];
+      if constexpr (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2) {
+        const float tt = qv - xv;
+        s = s + tt * tt;
+      } else {
+        s = s + qv * xv;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (c >= kc) return;
+  if (!valid) {
+    out[q * kc + c] = VSK_KEY_NONE;
+    return;
+  }
+  float dist;
+  if constexpr (METRIC == VSK_METRIC_L2SQ) dist = s;
+  else if constexpr (METRIC == VSK_METRIC_L2) dist = sqrtf(s);
+  else if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED) dist = 1.0f - s;
+  else dist = -s;
+  out[q * kc + c] = vsk_key(dist, row);
+}
+
+struct CheckArgs {
+  const uint64_t *best;  // nq x kc screen keys, ascending, NONE last
+  int64_t nq;
+  int32_t k, kc, d, metric;
+  const float *qnh, *qnr;  // per query |qh|, |q - qh|
+  double xh, xr;           // maxima over the rows of |xh|, |x - xh|
+  uint8_t *ok;
+  int32_t *nvalid;
+  int32_t *fails;
+  bool test;  // false: count the valid keys only
+};
+
+// the screen's error bound eps(q) for the metric (see the file comment)
+__device__ double screen_eps(const CheckArgs &a, int64_t q) {
+  const double u = 0x1p-24;
+  const double qh = a.qnh[q], qr = a.qnr[q], xh = a.xh, xr = a.xr;
+  const double qn = qh + qr, xn = xh + xr, dd = (double)a.d;
+  const double e_dot =
+      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
+  const double e_ref = 1.01 * dd * u * qn * xn;
+  double eps;
+  if (a.metric == VSK_METRIC_DOT)
+    eps = e_dot + e_ref;
+  else if (a.metric == VSK_METRIC_COSINE_NORMALIZED)
+    eps = e_dot + e_ref + 2.02 * u * (1.0 + qn * xn + e_dot);
+  else
+    eps = 2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05;
+  return eps * 1.0001;
+}
+
+__global__ void k_screen_check(CheckArgs a) {
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= a.nq) return;
+  const uint64_t *b = a.best + q * a.kc;
+  int32_t lo = 0, hi = a.kc;  // first NONE (keys ascending, NONE last)
+  while (lo < hi) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (b[mid] == VSK_KEY_NONE) hi = mid;
+    else lo = mid + 1;
+  }
+  a.nvalid[q] = lo;
+  if (!a.test) return;
+  bool good = true;
+  if (lo == a.kc) {  // rows beyond the kept ones exist
+    const double ak = vsk_ord2f((uint32_t)(b[a.k - 1] >> 32));
+    const double akc = vsk_ord2f((uint32_t)(b[a.kc - 1] >> 32));
+    const double eps = screen_eps(a, q);
+    const double top = ak + eps, rest = akc - eps;
+    good = rest > top;
+    if (a.metric == VSK_METRIC_L2) good = good && rest > top * (1.0 + 0x1p-20);
+  }
+  a.ok[q] = good ? 1 : 0;
+  if (!good) atomicAdd(a.fails, 1);
+}
+
+__global__ void k_gather_rows(const float *src, int64_t ld, const int32_t *idx,
+                              int64_t m, float *dst) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m * ld;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / ld, c = i - r * ld;
+    dst[i] = src[(int64_t)idx[r] * ld + c];
+  }
+}
+
+__global__ void k_scatter_keys(const uint64_t *src, int64_t m, int32_t k,
+                               const int32_t *idx, uint64_t *dst) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m * k;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / k, c = i - r * k;
+    dst[(int64_t)idx[r] * k + c] = src[i];
+  }
+}
+
+static unsigned grid_for(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
+}
+
+static void rescore(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
+                    const uint64_t *cand, int32_t kc, int32_t metric,
+                    uint64_t *out) {
+  dim3 grid((unsigned)nq, (unsigned)ceil_div(kc, 256));
+  KernelTimer t(ctx, "screen_rescore", (double)nq * kc);
+  const float *X = db->x.as<float>();
+  switch (metric) {
+  case VSK_METRIC_L2SQ:
+    k_rescore<VSK_METRIC_L2SQ><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
+                                                              db->d, cand, kc, out);
+    break;
+  case VSK_METRIC_L2:
+    k_rescore<VSK_METRIC_L2><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
+                                                            db->d, cand, kc, out);
+    break;
+  case VSK_METRIC_COSINE_NORMALIZED:
+    k_rescore<VSK_METRIC_COSINE_NORMALIZED><<<grid, 256, 0, ctx->stream>>>(
+        X, db->ld, dq, db->ld, db->d, cand, kc, out);
+    break;
+  default:
+    k_rescore<VSK_METRIC_DOT><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
+                                                             db->d, cand, kc, out);
+  }
+  check_launch("screen_rescore");
+}
+
+// exact top-k of nb queries from their kc screened candidates: rescore,
+// then select k by (exact distance, row)
+static void rescore_select(vsk_ctx *ctx, const vsk_db *db, const float *dq,
+                           int64_t nb, int32_t k, int32_t kc, int32_t metric,
+                           const uint64_t *cand, const int32_t *nvalid,
+                           uint64_t *best) {
+  uint64_t *resc = static_cast<uint64_t *>(
+      ctx->scratch_ptr("screen.resc", sizeof(uint64_t) * (size_t)nb * kc));
+  rescore(ctx, db, dq, nb, cand, kc, metric, resc);
+  SelectArgs sa;
+  sa.nq = nb;
+  sa.k = k;
+  sa.cand = resc;
+  sa.cap = kc;
+  sa.counts = nvalid;
+  sa.best_out = best;
+  launch_select(ctx, sa, "screen_select");
+}
+
+// one screen tier over nb queries keeping kc candidates each: screen,
+// bound test, exact rescore and select into best (nb x k; rows of failing
+// queries are written too but must be redone).  Returns the failing query
+// indices.
+static std::vector<int32_t> screen_tier(vsk_ctx *ctx, const vsk_db *db,
+                                        const float *qbat, int64_t nb, int32_t k,
+                                        int32_t kc, int32_t metric,
+                                        uint64_t *best, const char *tag) {
+  uint64_t *cand = static_cast<uint64_t *>(ctx->scratch_ptr(
+      std::string("screen.cand") + tag, sizeof(uint64_t) * (size_t)nb * kc));
+  float *qn = static_cast<float *>(ctx->scratch_ptr(
+      std::string("screen.qnorm") + tag, sizeof(float) * 2 * (size_t)nb));
+  approx_topk(ctx, db, qbat, nb, kc, metric, cand, 1, qn, qn + nb, 8);
+
+  uint8_t *ok = static_cast<uint8_t *>(
+      ctx->scratch_ptr(std::string("screen.ok") + tag, (size_t)nb));
+  int32_t *nvalid = static_cast<int32_t *>(ctx->scratch_ptr(
+      std::string("screen.nvalid") + tag, sizeof(int32_t) * (size_t)nb));
+  int32_t *fails = static_cast<int32_t *>(
+      ctx->scratch_ptr(std::string("screen.fails") + tag, sizeof(int32_t)));
+  fill_i32(ctx, fails, 1, 0);
+  CheckArgs ca;
+  ca.best = cand;
+  ca.nq = nb;
+  ca.k = k;
+  ca.kc = kc;
+  ca.d = db->d;
+  ca.metric = metric;
+  ca.qnh = qn;
+  ca.qnr = qn + nb;
+  ca.xh = db->split_max_hi;
+  ca.xr = db->split_max_res;
+  ca.ok = ok;
+  ca.nvalid = nvalid;
+  ca.fails = fails;
+  ca.test = true;
+  {
+    KernelTimer t(ctx, "screen_check");
+    k_screen_check<<<grid_for(nb), 256, 0, ctx->stream>>>(ca);
+    check_launch("screen_check");
+  }
+  rescore_select(ctx, db, qbat, nb, k, kc, metric, cand, nvalid, best);
+
+  int32_t nfail = 0;
+  VSK_HIP(hipMemcpyAsync(&nfail, fails, sizeof(int32_t), hipMemcpyDeviceToHost,
+                         ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  std::vector<int32_t> idx;
+  if (nfail == 0) return idx;
+  std::vector<uint8_t> hok((size_t)nb);
+  VSK_HIP(hipMemcpyAsync(hok.data(), ok, (size_t)nb, hipMemcpyDeviceToHost,
+                         ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  for (int64_t i = 0; i < nb; ++i)
+    if (!hok[(size_t)i]) idx.push_back((int32_t)i);
+  return idx;
+}
+
+// queries idx of qbat, gathered; results scattered back into best (stride k)
+static void redo_queries(vsk_ctx *ctx, const vsk_db *db, const float *qbat,
+                         const std::vector<int32_t> &idx, int32_t k,
+                         int32_t metric, uint64_t *best, bool exact_scan) {
+  const int64_t m = (int64_t)idx.size();
+  // profiled as one "launch" whose work counter is the number of queries
+  KernelTimer tf(ctx, exact_scan ? "screen_fallback" : "screen_retry", (double)m);
+  const char *tag = exact_scan ? ".x" : ".r";
+  int32_t *didx = static_cast<int32_t *>(ctx->scratch_ptr(
+      std::string("screen.fidx") + tag, sizeof(int32_t) * (size_t)m));
+  VSK_HIP(hipMemcpyAsync(didx, idx.data(), sizeof(int32_t) * (size_t)m,
+                         hipMemcpyHostToDevice, ctx->stream));
+  float *q2 = static_cast<float *>(ctx->scratch_ptr(
+      std::string("screen.fq") + tag, sizeof(float) * (size_t)m * db->ld));
+  k_gather_rows<<<grid_for(m * db->ld), 256, 0, ctx->stream>>>(qbat, db->ld, didx,
+                                                               m, q2);
+  check_launch("screen_gather");
+  uint64_t *best2 = static_cast<uint64_t *>(ctx->scratch_ptr(
+      std::string("screen.fbest") + tag, sizeof(uint64_t) * (size_t)m * k));
+  if (exact_scan) {
+    // the reference's formula over every row: no cancellation, no bound
+    approx_topk(ctx, db, q2, m, k, exact_metric(metric), best2, 3);
+  } else {
+    // a wider screen (the candidate count within the margin is some 2-3 k
+    // on real data); queries failing it too take the exact scan
+    std::vector<int32_t> again =
+        screen_tier(ctx, db, q2, m, k, VSK_MAX_K, metric, best2, ".r");
+    if (!again.empty())
+      redo_queries(ctx, db, q2, again, k, metric, best2, true);
+  }
+  k_scatter_keys<<<grid_for(m * k), 256, 0, ctx->stream>>>(best2, m, k, didx, best);
+  check_launch("screen_scatter");
+}
+
+void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
+                 int32_t k, int32_t metric, uint64_t *best) {
+  const int32_t kc = screen_keep(k);
+  const int64_t qb = query_batch(nq, default_cap(kc));
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    const float *qbat = dq + b0 * db->ld;
+    std::vector<int32_t> fail =
+        screen_tier(ctx, db, qbat, nb, k, kc, metric, best + b0 * k, "");
+    if (fail.empty()) continue;
+    redo_queries(ctx, db, qbat, fail, k, metric, best + b0 * k,
+                 kc >= VSK_MAX_K);
+  }
+}
+
+}  // namespace vsk

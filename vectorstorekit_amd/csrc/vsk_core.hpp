@@ -65,9 +65,12 @@ struct vsk_ctx {
   std::map<std::string, std::unique_ptr<vsk::DevBuf>> scratch;
   void *scratch_ptr(const std::string &key, size_t bytes);
 
-  // flat dot-product kernel: bf16x3 split MFMA (default) or fp32 MFMA
-  // (environment VSK_FLAT_KERNEL=fp32 at context creation)
+  // flat top-k path, from the environment VSK_FLAT_KERNEL at context
+  // creation: unset = one-pass bf16 screen with exact fp32 rescore where the
+  // metric allows it (bf16x3 elsewhere); "bf16x3" = bf16x3 split MFMA
+  // only; "fp32" = fp32 MFMA only
   bool flat_fp32 = false;
+  bool flat_no_screen = false;
 
   // profiling
   bool profile = false;
@@ -91,9 +94,11 @@ struct vsk_db {
   vsk::DevBuf x;       // n x ld fp32
   vsk::DevBuf sqnorm;  // n: sum x^2 (fp32)
   vsk::DevBuf norm;    // n: sqrt(sum x^2)
-  // bf16 hi/lo planes for the bf16x3 MFMA kernel, built on first use
+  // bf16 hi/lo planes for the bf16 MFMA kernels, built on first use, and
+  // the maxima over the rows of |hi| and |x - hi| (the screen's bound)
   mutable vsk::DevBuf split;
   mutable int32_t ldb = 0;
+  mutable float split_max_hi = 0.f, split_max_res = 0.f;
 };
 
 namespace vsk {
