@@ -558,26 +558,13 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
                 vsk_key(dist_from_dot<METRIC>(acc[i][j][r], qa, xa), (uint32_t)row);
           }
       } else {
-        // fast path: the threshold as a distance; a key can only pass when
-        // its distance is <= that (ties are settled by the exact key)
+        // a key can only pass when its distance is <= the threshold's (ties
+        // are settled by the exact key): one compare per score, and the
+        // exact test only in the (row block, r) steps where a lane passes
         const uint64_t th = qok ? a.thresh[qi] : 0;
         const uint32_t th_hi = (uint32_t)(th >> 32);
         const float th_f = th_hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000)
                                                  : vsk_ord2f(th_hi);
-        bool hit = false;
-        if (qok) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              // rows past the slice (zeros) read the last row's norm: they
-              // can only send the tile to the exact test below
-              const int64_t rr = rbase + i * 16 + r;
-              const float xa = a.xaux ? a.xaux[rr < s1 ? rr : s1 - 1] : 0.f;
-              hit |= dist_from_dot<METRIC>(acc[i][j][r], qa, xa) <= th_f;
-            }
-        }
-        if (!__builtin_amdgcn_ballot_w64(hit)) continue;  // the common case
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -585,9 +572,11 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             const int64_t row = rbase + i * 16 + r;
             const bool in = qok && (full || row < s1);
             const float xa = (in && a.xaux) ? a.xaux[row] : 0.f;
-            const uint64_t key =
-                vsk_key(dist_from_dot<METRIC>(acc[i][j][r], qa, xa), (uint32_t)row);
-            wc_push(wc, a, in && key <= th, key, (int32_t)qi, lane);
+            const float dist = dist_from_dot<METRIC>(acc[i][j][r], qa, xa);
+            const bool maybe = in && dist <= th_f;
+            if (!__builtin_amdgcn_ballot_w64(maybe)) continue;  // the common case
+            const uint64_t key = vsk_key(dist, (uint32_t)row);
+            wc_push(wc, a, maybe && key <= th, key, (int32_t)qi, lane);
           }
       }
     }

@@ -25,6 +25,9 @@
 // keeping 1024 candidates, and one failing that too is redone by the exact
 // VALU scan, which evaluates the reference's formula for every row.
 //
+// Kept rows above that limit are beaten the same way, so only the rows of
+// a within 2 eps of A_k are rescored.
+//
 // The rescore sums in dimension order without FMA, exactly as the CPU
 // reference (Indexes/IVFIndex.swift:542-549 and
 // Acceleration/AccelerateOptimizer.swift:251-383 restated sequentially), so
@@ -56,8 +59,8 @@ int32_t screen_keep(int32_t k) {
 // candidates of one query (uniform query loads).  Per 64-dim block the wave
 // gathers its 64 rows with 256-byte segments (16 lanes per row) into its own
 // LDS tile, then every lane continues the sequential sum of its row from
-// there: coalesced reads, bit-exact sums.  out[q][c] = key(distance, row);
-// NONE candidates stay NONE.
+// there: coalesced reads, bit-exact sums.  out[q][c] = key(distance, row)
+// for the first nvalid[q] candidates, NONE for the rest.
 constexpr int RS_W = 64;       // dims per gathered block
 constexpr int RS_LD = RS_W + 4;  // LDS row stride (floats): conflict-free
 
@@ -65,13 +68,14 @@ template <int METRIC>
 __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
                                                  const float *Q, int64_t ldq,
                                                  int32_t d, const uint64_t *cand,
-                                                 int32_t kc, uint64_t *out) {
+                                                 int32_t kc, const int32_t *nvalid,
+                                                 uint64_t *out) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float tile[4][64 * RS_LD];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t q = blockIdx.x;
   const int32_t c = blockIdx.y * 256 + threadIdx.x;
-  const uint64_t key = c < kc ? cand[q * kc + c] : VSK_KEY_NONE;
+  const uint64_t key = c < nvalid[q] ? cand[q * kc + c] : VSK_KEY_NONE;
   const bool valid = key != VSK_KEY_NONE;
   const uint32_t row = (uint32_t)key;
   if (!__builtin_amdgcn_ballot_w64(valid)) return;  // wave past the candidates
@@ -165,13 +169,22 @@ __global__ void k_screen_check(CheckArgs a) {
   a.nvalid[q] = lo;
   if (!a.test) return;
   bool good = true;
-  if (lo == a.kc) {  // rows beyond the kept ones exist
+  if (lo >= a.k) {
+    // a kept row y with a(y) - eps > A_k + eps (relative gap 2^-20 for
+    // sqrt) is strictly beaten by k rows: only rows below lim are rescored,
+    // and rows past the kept ones can be ignored when A_kc > lim
     const double ak = vsk_ord2f((uint32_t)(b[a.k - 1] >> 32));
-    const double akc = vsk_ord2f((uint32_t)(b[a.kc - 1] >> 32));
     const double eps = screen_eps(a, q);
-    const double top = ak + eps, rest = akc - eps;
-    good = rest > top;
-    if (a.metric == VSK_METRIC_L2) good = good && rest > top * (1.0 + 0x1p-20);
+    double lim = ak + 2.0 * eps;
+    if (a.metric == VSK_METRIC_L2) lim = (ak + eps) * (1.0 + 0x1p-20) + eps;
+    int32_t l2 = a.k, h2 = lo;  // first kept key above lim
+    while (l2 < h2) {
+      const int32_t mid = (l2 + h2) >> 1;
+      if ((double)vsk_ord2f((uint32_t)(b[mid] >> 32)) > lim) h2 = mid;
+      else l2 = mid + 1;
+    }
+    a.nvalid[q] = l2;
+    if (lo == a.kc) good = l2 < a.kc;  // rows beyond the kept ones exist
   }
   a.ok[q] = good ? 1 : 0;
   if (!good) atomicAdd(a.fails, 1);
@@ -201,27 +214,27 @@ static unsigned grid_for(int64_t n) {
 }
 
 static void rescore(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
-                    const uint64_t *cand, int32_t kc, int32_t metric,
-                    uint64_t *out) {
+                    const uint64_t *cand, int32_t kc, const int32_t *nvalid,
+                    int32_t metric, uint64_t *out) {
   dim3 grid((unsigned)nq, (unsigned)ceil_div(kc, 256));
   KernelTimer t(ctx, "screen_rescore", (double)nq * kc);
   const float *X = db->x.as<float>();
   switch (metric) {
   case VSK_METRIC_L2SQ:
     k_rescore<VSK_METRIC_L2SQ><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
-                                                              db->d, cand, kc, out);
+                                                              db->d, cand, kc, nvalid, out);
     break;
   case VSK_METRIC_L2:
     k_rescore<VSK_METRIC_L2><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
-                                                            db->d, cand, kc, out);
+                                                            db->d, cand, kc, nvalid, out);
     break;
   case VSK_METRIC_COSINE_NORMALIZED:
     k_rescore<VSK_METRIC_COSINE_NORMALIZED><<<grid, 256, 0, ctx->stream>>>(
-        X, db->ld, dq, db->ld, db->d, cand, kc, out);
+        X, db->ld, dq, db->ld, db->d, cand, kc, nvalid, out);
     break;
   default:
     k_rescore<VSK_METRIC_DOT><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
-                                                             db->d, cand, kc, out);
+                                                             db->d, cand, kc, nvalid, out);
   }
   check_launch("screen_rescore");
 }
@@ -234,7 +247,7 @@ static void rescore_select(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                            uint64_t *best) {
   uint64_t *resc = static_cast<uint64_t *>(
       ctx->scratch_ptr("screen.resc", sizeof(uint64_t) * (size_t)nb * kc));
-  rescore(ctx, db, dq, nb, cand, kc, metric, resc);
+  rescore(ctx, db, dq, nb, cand, kc, nvalid, metric, resc);
   SelectArgs sa;
   sa.nq = nb;
   sa.k = k;
