@@ -48,6 +48,9 @@ struct FlatArgs {
   float *mat;  // MODE_MATRIX output, row-major nq x ldm
   int64_t ldm;
   int32_t splits_per_xcd;  // bf16x3 kernel: row splits owned by each XCD
+  // screen kernel, filter mode: candidate slots each workgroup reserves per
+  // query (0: append through per-candidate atomics)
+  int32_t sub;
 };
 
 // bf16 hi/lo operand planes of the bf16x3 kernel

@@ -380,56 +380,16 @@ void k_flat_bf16x3(FlatArgs a, SplitPtrs s) {
 // registers while the current one is multiplied.  Filtered candidates go
 // through per-wave LDS lists (24 KB).  Per MFMA this moves half
 // the global bytes and two thirds of the LDS bytes of the 128 x 128 tile.
-// Filtered candidates of one wave, staged in LDS (SC_CAP entries of key and
-// query) and appended to the global per-query lists 64 entries per atomic
-// round trip: an atomic that returns a value makes the wave wait for all
-// its memory operations in flight, the prefetched stages included.  Calls
-// are made in wave-uniform control flow, so the count n stays uniform.
-constexpr int SC_CAP = 256;
-struct WaveCands {
-  uint64_t *key;
-  int32_t *q;
-  int32_t n;
-};
-
-__device__ __forceinline__ void wc_flush(WaveCands &wc, const FlatArgs &a,
-                                         int lane) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int32_t e = lane; e < wc.n; e += 64) {
-    const int32_t q = wc.q[e];
-    const int c = atomicAdd(&a.counts[q], 1);
-    if (c < a.cap) a.cand[(int64_t)q * a.cap + c] = wc.key[e];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  wc.n = 0;
-}
-
-// append the passing lanes' keys in lane order; flush when fewer than 64
-// slots would be left
-__device__ __forceinline__ void wc_push(WaveCands &wc, const FlatArgs &a,
-                                        bool pass, uint64_t key, int32_t q,
-                                        int lane) {
-  const uint64_t m = __builtin_amdgcn_ballot_w64(pass);
-  if (!m) return;
-  if (pass) {
-    const int32_t pos =
-        wc.n + (int32_t)__builtin_amdgcn_mbcnt_hi(
-                   (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    wc.key[pos] = key;
-    wc.q[pos] = q;
-  }
-  wc.n += __builtin_popcountll(m);
-  if (wc.n > SC_CAP - 64) wc_flush(wc, a, lane);
-}
-
 constexpr int XS_N = 256, XS_Q = 256, XS_K = 64, XS_R = 128;
+// query tiles per XCD group: the 32 workgroups resident on an XCD then hold
+// 4 query tiles (1.5 MB of bf16 queries at d = 768) and 8 row slices
+constexpr int XS_GQ = 4;
 constexpr int XS_STAGE = (XS_N + XS_Q) * XS_R;  // bytes per stage buffer
-// two stage buffers, then the 8 waves' candidate lists (keys, queries)
-constexpr int XS_LDS = 2 * XS_STAGE + 8 * SC_CAP * (8 + 4);
+// two stage buffers, then per query: slot limit, slot count, active flag,
+// |q|^2 or |q| (metric), threshold as a distance, threshold key, index of
+// the first reserved slot in the candidate array
+constexpr int XS_LDS = 2 * XS_STAGE + 6 * XS_Q * 4 + 2 * XS_Q * 8;
+static_assert(XS_LDS <= 160 * 1024, "LDS of one workgroup");
 
 __device__ __forceinline__ int swz8(int r, int c) {
   return r * XS_R + ((c ^ ((r >> 1) & 7)) << 4);
@@ -443,16 +403,15 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   const int wr = w & 3, wq = w >> 2;
   const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
   const int sx = a.splits_per_xcd;
-  const int grp = slot / (XB_GQ * sx), rem = slot - grp * (XB_GQ * sx);
-  const int qtile = grp * XB_GQ + rem % XB_GQ;
-  const int split = (rem / XB_GQ) * 8 + xcd;
+  const int grp = slot / (XS_GQ * sx), rem = slot - grp * (XS_GQ * sx);
+  const int qtile = grp * XS_GQ + rem % XS_GQ;
+  const int split = (rem / XS_GQ) * 8 + xcd;
   const int64_t q0 = (int64_t)qtile * XS_Q;
   if (q0 >= a.nq) return;
   const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
   int64_t s1 = s0 + a.rows_per_split;
   if (s1 > a.r1) s1 = a.r1;
   if (s0 >= s1) return;
-  const int64_t qw = q0 + wq * 128 + (lane & 15);  // query of tile j: qw + 16 j
   // staging: thread t moves chunk t & 7 of rows (t >> 3) + 64 u, u = 0..3
   const int crow = tid >> 3, cch = tid & 7;
   const int nst = (s.kb + XS_K - 1) / XS_K;
@@ -466,10 +425,61 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) wpos[u] = swz8(crow + 64 * u, cch);
   const int cl = lane >> 4;
-  WaveCands wc;
-  wc.key = reinterpret_cast<uint64_t *>(lds + 2 * XS_STAGE) + w * SC_CAP;
-  wc.q = reinterpret_cast<int32_t *>(lds + 2 * XS_STAGE + 8 * SC_CAP * 8) + w * SC_CAP;
-  wc.n = 0;
+  // filter appends: the workgroup takes a.sub slots of each of its
+  // queries' candidate lists up front (one device atomic per query, not one
+  // per candidate: device-scope atomics are slow on the XCD-split L2) and
+  // fills them through LDS counters; unused slots become NONE, which the
+  // selection ignores, and a query whose slots overflow gets a count past
+  // cap, so the selection re-scans it
+  // The queries' flags, norms and thresholds are read once into LDS: in
+  // the epilogue a global load would wait (in-order vector memory counter)
+  // for every stage prefetch in flight, eight times per tile.
+  // (The slot addresses are read from LDS where used: computed from the
+  // query index, the compiler would hoist all eight out of the loops and
+  // keep them live.)
+  int32_t *s_lim = reinterpret_cast<int32_t *>(lds + 2 * XS_STAGE);
+  int32_t *s_cnt = s_lim + XS_Q;
+  int32_t *s_ok = s_cnt + XS_Q;
+  float *s_qa = reinterpret_cast<float *>(s_ok + XS_Q);
+  float *s_thf = s_qa + XS_Q;
+  float *s_tdot = s_thf + XS_Q;
+  uint64_t *s_th = reinterpret_cast<uint64_t *>(s_tdot + XS_Q);
+  int64_t *s_pb = reinterpret_cast<int64_t *>(s_th + XS_Q);
+  if (tid < XS_Q) {
+    const int64_t q = q0 + tid;
+    const bool ok = q < a.nq && (!a.active || a.active[q]);
+    s_ok[tid] = ok ? 1 : 0;
+    s_qa[tid] = (ok && a.qaux) ? a.qaux[q] : 0.f;
+    if constexpr (MODE == MODE_FILTER) {
+      const uint64_t th = ok ? a.thresh[q] : 0;
+      const uint32_t th_hi = (uint32_t)(th >> 32);
+      s_th[tid] = th;
+      const float thf = !ok ? -__int_as_float(0x7f800000)
+                            : (th_hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000)
+                                                    : vsk_ord2f(th_hi));
+      s_thf[tid] = thf;
+      // the same bound on the raw dot product (normalised cosine: a dot
+      // below 1 - thf less a margin of the rounding of 1 - dot cannot pass;
+      // dot: -dot <= thf exactly when dot >= -thf)
+      if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED) {
+        const double t = 1.0 - (double)thf;
+        const double m = t - 0x1p-22 * (fabs((double)thf) > 1.0 ? fabs((double)thf) : 1.0);
+        float f = (float)m;
+        if ((double)f > m) f = __uint_as_float(f > 0.f ? __float_as_uint(f) - 1u
+                                               : (f < 0.f ? __float_as_uint(f) + 1u
+                                                          : 0x80000001u));
+        s_tdot[tid] = f;
+      } else {
+        s_tdot[tid] = -thf;
+      }
+      const int64_t base = ok ? atomicAdd(&a.counts[q], a.sub) : a.cap;
+      const int64_t room = a.cap - base;
+      s_lim[tid] = (int32_t)(room < a.sub ? (room > 0 ? room : 0) : a.sub);
+      s_pb[tid] = q * a.cap + base;
+      s_cnt[tid] = 0;
+    }
+  }
+  __syncthreads();
 
   for (int64_t t0 = s0; t0 < s1; t0 += XS_N) {
     f4 acc[4][8];
@@ -540,13 +550,29 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     // D[row = 4*(lane/16) + r][query = lane%16] of each 16x16 tile
     const bool full = t0 + XS_N <= s1;
     const int64_t rbase = t0 + wr * 64 + 4 * (lane >> 4);
+    // this lane's query state: query j at element 16 j (a constant offset)
+    const int lq0 = wq * 128 + (lane & 15);
+    const int32_t *l_ok = s_ok + lq0, *l_lim = s_lim + lq0;
+    int32_t *l_cnt = s_cnt + lq0;
+    const float *l_qa = s_qa + lq0, *l_thf = s_thf + lq0, *l_tdot = s_tdot + lq0;
+    // rows of this lane inside the slice: bit 4i+r for row rbase + 16i + r
+    uint32_t vmask = 0xFFFFu;
+    if (!full) {
+      vmask = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (rbase + i * 16 + r < s1) vmask |= 1u << (4 * i + r);
+    }
+    const uint64_t *l_th = s_th + lq0;
+    const int64_t *l_pb = s_pb + lq0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int64_t qi = qw + 16 * j;
-      const bool qok = qi < a.nq && (!a.active || a.active[qi]);
-      const float qa = (qok && a.qaux) ? a.qaux[qi] : 0.f;
+      const int64_t qi = q0 + lq0 + 16 * j;
+      const float qa = a.qaux ? l_qa[16 * j] : 0.f;
       if constexpr (MODE == MODE_DENSE) {
-        if (!qok) continue;
+        if (!l_ok[16 * j]) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -561,28 +587,81 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         // a key can only pass when its distance is <= the threshold's (ties
         // are settled by the exact key): one compare per score, and the
         // exact test only in the (row block, r) steps where a lane passes
-        const uint64_t th = qok ? a.thresh[qi] : 0;
-        const uint32_t th_hi = (uint32_t)(th >> 32);
-        const float th_f = th_hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000)
-                                                 : vsk_ord2f(th_hi);
+        // fast test, one compare per score: bit 4i+r of m for a score that
+        // may pass (NaN included); rows past the slice masked off
+        uint32_t m = 0;
+        if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED ||
+                      METRIC == VSK_METRIC_DOT) {
+          const float tdot = l_tdot[16 * j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int64_t row = rbase + i * 16 + r;
-            const bool in = qok && (full || row < s1);
-            const float xa = (in && a.xaux) ? a.xaux[row] : 0.f;
-            const float dist = dist_from_dot<METRIC>(acc[i][j][r], qa, xa);
-            const bool maybe = in && dist <= th_f;
-            if (!__builtin_amdgcn_ballot_w64(maybe)) continue;  // the common case
-            const uint64_t key = vsk_key(dist, (uint32_t)row);
-            wc_push(wc, a, maybe && key <= th, key, (int32_t)qi, lane);
+            for (int r = 0; r < 4; ++r)
+              m |= (acc[i][j][r] < tdot) ? 0u : (1u << (4 * i + r));
+        } else {
+          const float th_f = l_thf[16 * j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t row = rbase + i * 16 + r;
+              const float xa = (full || row < s1) ? a.xaux[row] : 0.f;
+              m |= (dist_from_dot<METRIC>(acc[i][j][r], qa, xa) > th_f)
+                       ? 0u : (1u << (4 * i + r));
+            }
+        }
+        m &= vmask;
+        if (!__builtin_amdgcn_ballot_w64(m != 0)) continue;  // the common case
+        if (m && l_ok[16 * j]) {
+          // the few candidates of this lane: exact key test
+          const uint64_t th = l_th[16 * j];
+          // this query's 16 scores of the lane as named values behind an
+          // empty asm: a select between two loads of one array would be
+          // folded into one dynamically indexed load, which sends the array
+          // (and with it the accumulators) to scratch memory
+          float c0 = acc[0][j][0], c1 = acc[0][j][1], c2 = acc[0][j][2], c3 = acc[0][j][3];
+          float c4 = acc[1][j][0], c5 = acc[1][j][1], c6 = acc[1][j][2], c7 = acc[1][j][3];
+          float c8 = acc[2][j][0], c9 = acc[2][j][1], c10 = acc[2][j][2], c11 = acc[2][j][3];
+          float c12 = acc[3][j][0], c13 = acc[3][j][1], c14 = acc[3][j][2], c15 = acc[3][j][3];
+          asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3), "+v"(c4), "+v"(c5),
+                       "+v"(c6), "+v"(c7));
+          asm volatile("" : "+v"(c8), "+v"(c9), "+v"(c10), "+v"(c11), "+v"(c12), "+v"(c13),
+                       "+v"(c14), "+v"(c15));
+          while (m) {
+            const int b = __builtin_ctz(m);
+            m &= m - 1;
+            const bool b0 = b & 1, b1 = b & 2, b2 = b & 4;
+            const float s0 = b0 ? c1 : c0, s1 = b0 ? c3 : c2, s2 = b0 ? c5 : c4,
+                        s3 = b0 ? c7 : c6, s4 = b0 ? c9 : c8, s5 = b0 ? c11 : c10,
+                        s6 = b0 ? c13 : c12, s7 = b0 ? c15 : c14;
+            const float u0 = b1 ? s1 : s0, u1 = b1 ? s3 : s2, u2 = b1 ? s5 : s4,
+                        u3 = b1 ? s7 : s6;
+            const float w0 = b2 ? u1 : u0, w1 = b2 ? u3 : u2;
+            const float dot = (b & 8) ? w1 : w0;
+            const int64_t row = rbase + 16 * (b >> 2) + (b & 3);
+            const float xa = a.xaux ? a.xaux[row] : 0.f;
+            const uint64_t key = vsk_key(dist_from_dot<METRIC>(dot, qa, xa), (uint32_t)row);
+            if (key <= th) {
+              const int pos = atomicAdd(&l_cnt[16 * j], 1);
+              if (pos < l_lim[16 * j]) a.cand[l_pb[16 * j] + pos] = key;
+            }
           }
+        }
       }
     }
   }
   if constexpr (MODE == MODE_FILTER) {
-    if (wc.n > 0) wc_flush(wc, a, lane);
+    __syncthreads();
+    if (tid < XS_Q && s_ok[tid]) {
+      const int32_t n = s_cnt[tid];
+      if (n > a.sub) {
+        atomicAdd(&a.counts[q0 + tid], (int32_t)a.cap + 1);
+      } else {
+        const int64_t pb = s_pb[tid];
+        const int32_t lim = s_lim[tid];
+        for (int32_t i = n; i < lim; ++i) a.cand[pb + i] = VSK_KEY_NONE;
+      }
+    }
   }
 }
 
@@ -632,15 +711,25 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode) 
   const int64_t qt = ceil_div(a.nq, XS_Q);
   // row splits: a multiple of 8 (one share per XCD), about 2048 workgroups
   // (one per CU at a time)
+  // (filter mode: at most cap/32 splits, so that every split's workgroup
+  // reserves at least 32 slots per query within cap)
   int64_t splits = ceil_div(2048, qt);
   const int64_t max_splits = ceil_div(rows, XS_N);
   if (splits > max_splits) splits = max_splits;
+  if (mode == MODE_FILTER && splits > a.cap / 32 - 7) splits = a.cap / 32 - 7;
   if (splits < 1) splits = 1;
   a.rows_per_split = ceil_div(ceil_div(rows, splits), XS_N) * XS_N;
   splits = ceil_div(ceil_div(rows, a.rows_per_split), 8) * 8;
   a.splits_per_xcd = (int32_t)(splits / 8);
-  const int64_t groups = ceil_div(qt, XB_GQ);
-  const int64_t nblocks = 8 * a.splits_per_xcd * groups * XB_GQ;
+  // reserved slots per (workgroup, query), all splits within cap
+  a.sub = 0;
+  if (mode == MODE_FILTER) {
+    const int64_t sub = a.cap / splits < 128 ? a.cap / splits : 128;
+    if (sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
+    a.sub = (int32_t)sub;
+  }
+  const int64_t groups = ceil_div(qt, XS_GQ);
+  const int64_t nblocks = 8 * a.splits_per_xcd * groups * XS_GQ;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
   static const char *names[2] = {"flat_screen_dense", "flat_screen_filter"};
   KernelTimer t(ctx, names[mode], (double)a.nq * (double)rows);
