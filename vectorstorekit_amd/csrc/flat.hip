@@ -415,7 +415,8 @@ static bool use_bf16x3(const vsk_ctx *ctx, int32_t metric) {
 
 SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                      int64_t nq, bool qlo, float *qnh, float *qnr) {
-  const int32_t ldb = (db->d + 31) & ~31;
+  // whole 64-dimension stages of the screen (zero padding)
+  const int32_t ldb = (db->d + 63) & ~63;
   if (!db->split.p) {
     db->split.reserve(sizeof(uint16_t) * 2 * (size_t)db->n * ldb);
     db->ldb = ldb;

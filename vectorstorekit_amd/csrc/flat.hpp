@@ -58,7 +58,7 @@ struct SplitPtrs {
   const uint16_t *xh, *xl;  // row planes, stride ldxb
   const uint16_t *qh, *ql;  // query planes, stride ldqb
   int64_t ldxb, ldqb;
-  int32_t kb;               // padded dimension (multiple of 32)
+  int32_t kb;               // padded dimension (multiple of 64)
 };
 // hi = bf16(x) and (lo non-null) lo = bf16(x - hi) of an (n x ld) fp32
 // matrix, ldb columns; nhi/nres (optional): per-row |hi| and |x - hi|,

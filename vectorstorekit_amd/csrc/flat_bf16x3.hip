@@ -34,6 +34,10 @@ constexpr int XB_K = 32;    // dims per LDS stage (one MFMA k-step)
 constexpr int XR = 64;      // LDS row stride in bytes (chunks XOR-swizzled)
 constexpr int XB_GQ = 16;   // query tiles per XCD group
 constexpr int kBufFlags = 0x00020000;  // buffer descriptor word 3 (raw, dword data)
+// s_waitcnt immediates (gfx9 layout: vmcnt [3:0], expcnt [6:4], lgkmcnt [11:8]):
+// everything, and vector memory down to 8 outstanding
+constexpr int kWaitAll = 0x0000;
+constexpr int kWaitVm8 = 0x0F78;
 
 __device__ inline uint16_t bf16_rn(float v) {
   uint32_t u = __float_as_uint(v);
@@ -399,7 +403,8 @@ template <int MODE, int METRIC>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_flat_screen(FlatArgs a, SplitPtrs s) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wr = w & 3, wq = w >> 2;
   const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
   const int sx = a.splits_per_xcd;
@@ -412,18 +417,12 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   int64_t s1 = s0 + a.rows_per_split;
   if (s1 > a.r1) s1 = a.r1;
   if (s0 >= s1) return;
-  // staging: thread t moves chunk t & 7 of rows (t >> 3) + 64 u, u = 0..3
-  const int crow = tid >> 3, cch = tid & 7;
   const int nst = (s.kb + XS_K - 1) / XS_K;
   const int32_t qbytes =
       (int32_t)(((a.nq - q0) < XS_Q ? (a.nq - q0) : XS_Q) * s.ldqb * 2);
   const __amdgpu_buffer_rsrc_t rq =
       __builtin_amdgcn_make_buffer_rsrc((void *)(s.qh + q0 * s.ldqb), 0, qbytes, kBufFlags);
-  const int32_t ldx2 = (int32_t)s.ldxb * 2, ldq2 = (int32_t)s.ldqb * 2;
-  const int32_t ox = crow * ldx2 + cch * 16, oq = crow * ldq2 + cch * 16;
-  int wpos[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) wpos[u] = swz8(crow + 64 * u, cch);
+  const int32_t ldx2 = (int32_t)s.ldxb * 2;  // the query plane has the same pitch
   const int cl = lane >> 4;
   // filter appends: the workgroup takes a.sub slots of each of its
   // queries' candidate lists up front (one device atomic per query, not one
@@ -481,72 +480,101 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   }
   __syncthreads();
 
+  // Staging: the stages of all tiles of the slice form one sequence, and
+  // stage g goes into buffer g & 1 by buffer loads that write LDS directly
+  // (no registers): wave w moves the 8-row units 4w+u (u = 0..3) of the row
+  // half and of the query half, lane l the 16-byte chunk that belongs at
+  // position (row 8U + l/8, slot l%8) of the swizzled layout.  The MFMA
+  // operands of the next half-stage are read one step ahead into the second
+  // register set, so the MFMAs never wait on LDS, and the next tile's first
+  // stages are in flight during this tile's epilogue.
+  // Wait rules: a wave waits for its own copies (vector memory counter)
+  // and for its own operand reads (LDS counter), then the barrier makes
+  // every wave's copies visible and ends every wave's reads of the buffer
+  // the next copy overwrites.
+  // (units 4w+u and 4w+u+2 differ by 16 rows, the same swizzle: one lane
+  // offset per parity of u, the row step in the scalar offset)
+  int32_t voff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int r = 8 * (4 * w + u) + (lane >> 3);
+    voff[u] = r * ldx2 + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
+  }
+  int dst = 0;          // next stage to copy: stage dst of the tile at dt0
+  int64_t dt0 = s0;     // (past the slice: zero-length rows, nothing read)
+  int dbuf = 0;
+  auto copy_next = [&]() {
+    const int64_t left = s1 - dt0;
+    const int64_t rows = left < XS_N ? (left > 0 ? left : 0) : XS_N;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(s.xh + dt0 * s.ldxb), 0, (int32_t)(rows * ldx2), kBufFlags);
+    uint8_t *bx = lds + dbuf * XS_STAGE + 4 * w * 1024;
+    const int32_t kofs = dst * XS_K * 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t so = kofs + (u >> 1) * 16 * ldx2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void *)(bx + u * 1024), 16, voff[u & 1], so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rq, (__attribute__((address_space(3))) void *)(bx + XS_N * XS_R + u * 1024), 16,
+          voff[u & 1], so, 0, 0);
+    }
+    dbuf ^= 1;
+    if (++dst == nst) {
+      dst = 0;
+      dt0 += XS_N;
+    }
+  };
+  // operands: two sets, this step's and the next one's (read one step ahead)
+  bf8 ra[2][4], rb[2][8];
+  auto read_ops = [&](const uint8_t *buf, int kk, int n) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      rb[n][j] = __builtin_bit_cast(
+          bf8, *reinterpret_cast<const uint4 *>(
+                   buf + XS_N * XS_R + swz8(wq * 128 + j * 16 + (lane & 15), kk * 4 + cl)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ra[n][i] = __builtin_bit_cast(
+          bf8, *reinterpret_cast<const uint4 *>(
+                   buf + swz8(wr * 64 + i * 16 + (lane & 15), kk * 4 + cl)));
+  };
+  copy_next();
+  copy_next();
+  __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this wave's copies of stage 0
+  __builtin_amdgcn_s_barrier();
+  int g = 0;  // stage of the sequence being multiplied
   for (int64_t t0 = s0; t0 < s1; t0 += XS_N) {
+    // the tile's first operands are read here rather than before the
+    // previous epilogue, which then has the registers to itself
+    read_ops(lds + (g & 1) * XS_STAGE, 0, 0);
     f4 acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-    const int32_t xbytes = (int32_t)((s1 - t0) * s.ldxb * 2);
-    const __amdgpu_buffer_rsrc_t rx =
-        __builtin_amdgcn_make_buffer_rsrc((void *)(s.xh + t0 * s.ldxb), 0, xbytes, kBufFlags);
-    uint4 px[4], pq[4];
-#define XS_LOAD(ST)                                                           \
-  do {                                                                        \
-    const int kb_ = (ST) * XS_K * 2;                                          \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                           \
-      px[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(\
-                                            rx, ox + 64 * u * ldx2, kb_, 0)); \
-      pq[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(\
-                                            rq, oq + 64 * u * ldq2, kb_, 0)); \
-    }                                                                         \
+#define XS_MMA(N)                                                               \
+  do {                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                             \
+      _Pragma("unroll") for (int j = 0; j < 8; ++j) acc[i][j] =                 \
+          __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[N][i], rb[N][j], acc[i][j], 0, 0, 0); \
+    }                                                                           \
   } while (0)
-#define XS_STORE(BUF)                                                         \
-  do {                                                                        \
-    uint8_t *b_ = (BUF);                                                      \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                           \
-      *reinterpret_cast<uint4 *>(b_ + wpos[u]) = px[u];                       \
-      *reinterpret_cast<uint4 *>(b_ + XS_N * XS_R + wpos[u]) = pq[u];         \
-    }                                                                         \
-  } while (0)
-    __syncthreads();  // the previous tile's last reads are done
-    XS_LOAD(0);
-    XS_STORE(lds);
-    XS_LOAD(1);
-    __syncthreads();
-    for (int st = 0; st < nst; ++st) {
-      const uint8_t *cur = lds + (st & 1) * XS_STAGE;
-      // stage st+1 goes into the other buffer while this one is consumed
-      // (every wave finished reading it at the barrier closing stage st-1);
-      // loads past the padded dimension are never stored
-      if (st + 1 < nst) {
-        XS_STORE(lds + ((st + 1) & 1) * XS_STAGE);
-        XS_LOAD(st + 2);
-      }
-      const uint8_t *xs_ = cur, *qs_ = cur + XS_N * XS_R;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        if (kk == 1 && st * XS_K + 32 >= s.kb) break;  // past the padding
-        bf8 b[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          b[j] = __builtin_bit_cast(
-              bf8, *reinterpret_cast<const uint4 *>(
-                       qs_ + swz8(wq * 128 + j * 16 + (lane & 15), kk * 4 + cl)));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bf8 av = __builtin_bit_cast(
-              bf8, *reinterpret_cast<const uint4 *>(
-                       xs_ + swz8(wr * 64 + i * 16 + (lane & 15), kk * 4 + cl)));
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b[j], acc[i][j], 0, 0, 0);
-        }
-      }
-      __syncthreads();
+    for (int st = 0; st < nst; ++st, ++g) {
+      const uint8_t *cur = lds + (g & 1) * XS_STAGE;
+      read_ops(cur, 1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      XS_MMA(0);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);  // own copies of stage g+1, own reads of cur
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + 1 < nst) read_ops(lds + ((g + 1) & 1) * XS_STAGE, 0, 0);  // stage g+1
+      copy_next();                                                      // stage g+2 into cur
+      __builtin_amdgcn_sched_barrier(0);
+      XS_MMA(1);
     }
-#undef XS_STORE
-#undef XS_LOAD
+#undef XS_MMA
     // D[row = 4*(lane/16) + r][query = lane%16] of each 16x16 tile
     const bool full = t0 + XS_N <= s1;
     const int64_t rbase = t0 + wr * 64 + 4 * (lane >> 4);
@@ -650,6 +678,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       }
     }
   }
+  // the copies issued past the slice end land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
   if constexpr (MODE == MODE_FILTER) {
     __syncthreads();
     if (tid < XS_Q && s_ok[tid]) {
@@ -679,6 +709,8 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode) 
   const int64_t rows = a.r1 - a.r0;
   if (rows <= 0 || a.nq <= 0) return;
   if (mode == MODE_MATRIX) fail(VSK_ERR_UNSUPPORTED, "the screen has no matrix mode");
+  if (s.ldqb != s.ldxb || s.kb > s.ldxb || (s.kb & 63))
+    fail(VSK_ERR_INVALID_ARGUMENT, "screen planes need one pitch and a padded dimension");
   static bool lds_set = false;
   if (!lds_set) {
     const int bytes = XS_LDS;
