@@ -342,6 +342,10 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   if (hipSetDevice(device) != hipSuccess) return VSK_ERR_DEVICE_NOT_AVAILABLE;
   vsk_ctx *c = new vsk_ctx();
   c->device = device;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+      cus > 0)
+    c->cu_count = cus;
   const char *fk = getenv("VSK_FLAT_KERNEL");
   c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);

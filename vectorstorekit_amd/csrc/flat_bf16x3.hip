@@ -560,19 +560,38 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
           __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[N][i], rb[N][j], acc[i][j], 0, 0, 0); \
     }                                                                           \
   } while (0)
+    // (the operand reads are spread over the MFMAs: as a block, the eight
+    // waves' reads fill the LDS queue and hold up the MFMA issue)
     for (int st = 0; st < nst; ++st, ++g) {
       const uint8_t *cur = lds + (g & 1) * XS_STAGE;
       read_ops(cur, 1, 1);
-      __builtin_amdgcn_sched_barrier(0);
       XS_MMA(0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitAll);  // own copies of stage g+1, own reads of cur
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      if (st + 1 < nst) read_ops(lds + ((g + 1) & 1) * XS_STAGE, 0, 0);  // stage g+1
-      copy_next();                                                      // stage g+2 into cur
-      __builtin_amdgcn_sched_barrier(0);
+      // stage g+1 (at a tile's last stage the next tile's first one, read
+      // again at its start: unconditional, so the reads can interleave)
+      read_ops(lds + ((g + 1) & 1) * XS_STAGE, 0, 0);
+      copy_next();  // stage g+2 into cur
       XS_MMA(1);
+      __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // the copies first
+#pragma unroll
+      for (int t = 0; t < 12; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #undef XS_MMA
     // D[row = 4*(lane/16) + r][query = lane%16] of each 16x16 tile
@@ -741,22 +760,32 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode) 
     lds_set = true;
   }
   const int64_t qt = ceil_div(a.nq, XS_Q);
-  // row splits: a multiple of 8 (one share per XCD), about 2048 workgroups
-  // (one per CU at a time)
-  // (filter mode: at most cap/32 splits, so that every split's workgroup
-  // reserves at least 32 slots per query within cap)
-  int64_t splits = ceil_div(2048, qt);
-  const int64_t max_splits = ceil_div(rows, XS_N);
-  if (splits > max_splits) splits = max_splits;
-  if (mode == MODE_FILTER && splits > a.cap / 32 - 7) splits = a.cap / 32 - 7;
-  if (splits < 1) splits = 1;
-  a.rows_per_split = ceil_div(ceil_div(rows, splits), XS_N) * XS_N;
-  splits = ceil_div(ceil_div(rows, a.rows_per_split), 8) * 8;
+  // Row splits, a multiple of 8 (one share per XCD).  One workgroup fills a
+  // CU, so the launch runs in rounds of cu_count workgroups: take the split
+  // count with the fewest (rounds x tiles per split), the fewer splits on a
+  // tie, up to about 8 rounds.  (Filter mode: at most cap/32 - 7 splits, so
+  // that every split's workgroup reserves at least 32 slots per query.)
+  const int64_t tiles = ceil_div(rows, XS_N);
+  int64_t top = 8 * ceil_div(8 * (int64_t)ctx->cu_count, 8 * qt);
+  if (top > 8 * ceil_div(tiles, 8)) top = 8 * ceil_div(tiles, 8);
+  if (mode == MODE_FILTER && top > (a.cap / 32 - 7) / 8 * 8) top = (a.cap / 32 - 7) / 8 * 8;
+  if (top < 8) top = 8;
+  int64_t splits = 8, best = -1;
+  for (int64_t sp = 8; sp <= top; sp += 8) {
+    const int64_t tps = ceil_div(tiles, sp);
+    const int64_t used = ceil_div(tiles, tps);
+    const int64_t cost = ceil_div(qt * used, (int64_t)ctx->cu_count) * tps;
+    if (best < 0 || cost < best) {
+      best = cost;
+      splits = sp;
+    }
+  }
+  a.rows_per_split = ceil_div(tiles, splits) * XS_N;
   a.splits_per_xcd = (int32_t)(splits / 8);
   // reserved slots per (workgroup, query), all splits within cap
   a.sub = 0;
   if (mode == MODE_FILTER) {
-    const int64_t sub = a.cap / splits < 128 ? a.cap / splits : 128;
+    const int64_t sub = a.cap / splits < 256 ? a.cap / splits : 256;
     if (sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
     a.sub = (int32_t)sub;
   }

@@ -56,6 +56,7 @@ bool is_device_ptr(const void *p);
 // ---------------------------------------------------------------------------
 struct vsk_ctx {
   int device = 0;
+  int cu_count = 256;  // compute units of the device
   hipStream_t stream = nullptr;
   std::string last_error;
   float last_ms = 0.f;
