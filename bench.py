@@ -37,9 +37,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, datasheet
+PEAK_FP32_VALU_TFLOPS = 157.3   # fp32 vector, packed FMA
+PEAK_FP32_VALU_ISSUE_TOPS = 39.3  # 256 CU x 4 SIMD x 16 lanes x 2.4 GHz, one op per lane-cycle
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, datasheet
 PEAK_INT8_MFMA_TOPS = 5000.0  # MI355X dense int8 matrix, datasheet
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
+PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1)}
 
@@ -179,9 +182,18 @@ def setup(a, ctx, dev):
             qps, m, reps, el, (od, oi) = cpu_sample(
                 lambda m: O.search_flat(qh[:m], xh, k, metric, threads=th, fast=True),
                 nq, target_s, th)
+            # the timed port sums in 16 lanes like a SIMD loop; parity is
+            # against the exact (dimension-order) oracle, on a small sample
+            me = min(16, nq)
+            ed, ei = O.search_flat(qh[:me], xh, k, metric, threads=th, fast=False)
+            gd, gi = dist.cpu().numpy()[:me], ids.cpu().numpy()[:me]
+            exact = {"queries": me, "ids_equal": bool((gi == ei).all()),
+                     "distances_bitwise_equal": bool((gd.view(np.uint32) ==
+                                                      ed.view(np.uint32)).all())}
             return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
                      "sample": f"first {m} of {nq} queries against all {n} rows, "
-                               f"{reps} pass(es) ({el:.1f} s)"},
+                               f"{reps} pass(es) ({el:.1f} s); timed with 16-lane sums",
+                     "exact_oracle_check": exact},
                     id_agreement(ids.cpu().numpy()[:m], oi))
 
         spec = {
@@ -194,8 +206,8 @@ def setup(a, ctx, dev):
             "data": ("synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2)"
                      + (", L2-normalised" if c == "c2" else "")),
             "dtype": "f32", "nq": nq, "n": n, "d": d,
-            "kernels": [("flat_screen_filter", "k_flat_bf16x3<FILTER, 1 pass>", "mfma_bf16"),
-                        ("flat_screen_dense", "k_flat_bf16x3<DENSE, 1 pass>", "mfma_bf16"),
+            "kernels": [("flat_screen_filter", "k_flat_screen<FILTER>", "mfma_bf16"),
+                        ("flat_screen_dense", "k_flat_screen<DENSE>", "mfma_bf16"),
                         ("flat_bf16x3_filter", "k_flat_bf16x3<FILTER>", "mfma"),
                         ("flat_bf16x3_dense", "k_flat_bf16x3<DENSE>", "mfma"),
                         ("flat_mfma_filter", "k_flat_mfma<FILTER>", "mfma32"),
@@ -242,7 +254,7 @@ def setup(a, ctx, dev):
                     "points centre + 0.5 N(0,I) (seeds 5, 1, 2), centroids centre + "
                     "0.1 N(0,I) (seed 4); torch Philox",
             "dtype": "f32", "nq": nq, "n": n, "d": d,
-            "kernels": [("ivf_list_scan", "k_list_scan<16>", "hbm")],
+            "kernels": [("ivf_list_scan", "k_list_scan<16>", "valu")],
             "keep": (idx, x, q, dist, ids),
         }
         return spec, step, cpu_leg
@@ -282,8 +294,8 @@ def setup(a, ctx, dev):
             "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), "
                     "quantised per dimension",
             "dtype": "i8 (i32 accumulate)", "nq": nq, "n": n, "d": d,
-            "kernels": [("sq8_mfma_filter", "k_sq8_scan<FILTER>", "int8"),
-                        ("sq8_mfma_dense", "k_sq8_scan<DENSE>", "int8")],
+            "kernels": [("sq8_mfma_filter", "k_sq8_reg<FILTER> (int8 MFMA 16x16x64)", "int8"),
+                        ("sq8_mfma_dense", "k_sq8_reg<DENSE> (int8 MFMA 16x16x64)", "int8")],
             "keep": (db, codes, qc, score, ids),
         }
         return spec, step, cpu_leg
@@ -371,6 +383,24 @@ def roofline(spec, stats):
                   "unit": "TOP/s", "frac": round(ach / PEAK_INT8_MFMA_TOPS, 4),
                   "algorithmic": "2*d int8 OP per (query, row) pair",
                   "peak_basis": "int8 dense MFMA 5.0 POP/s"})
+    elif kind == "valu":
+        # exact fp32 (q - x)^2 sums in dimension order: a subtract, a multiply
+        # and an add per dimension, no fused multiply-add, no packed fp32
+        flop = 3.0 * d * pairs
+        ach = flop / sec / 1e12
+        r.update({"bound": "valu", "achieved": round(ach, 2), "peak": PEAK_FP32_VALU_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_VALU_TFLOPS, 4),
+                  "algorithmic": "3*d fp32 operations per (query, probed row) pair",
+                  "peak_basis": "fp32 vector 157.3 TFLOP/s (packed FMA); with one non-packed, "
+                                "non-fused operation per lane per cycle the issue ceiling is "
+                                f"{PEAK_FP32_VALU_ISSUE_TOPS} T operations/s",
+                  "frac_of_issue_ceiling": round(ach / PEAK_FP32_VALU_ISSUE_TOPS, 4),
+                  # the probed-list-bytes basis: above the HBM peak, because a list
+                  # row is read once for all the queries of a group that probe it
+                  "list_bytes_basis": {"bytes_per_pair": 4 * d,
+                                       "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
+                                       "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
+                                                            / PEAK_HBM_GBPS, 4)}})
     elif kind == "hbm":
         by = 4.0 * d * pairs
         ach = by / sec / 1e9
@@ -386,7 +416,11 @@ def roofline(spec, stats):
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
                   "algorithmic": "M code bytes per (query, row) pair: all codes read "
                                  "once per query",
-                  "lds_lookups_per_s": M * pairs / sec})
+                  "lds_lookups_per_s": M * pairs / sec,
+                  # one LUT lookup per code byte, each a 4-byte LDS read: 64 banks
+                  # per CU at 2.4 GHz bound the conflict-free rate
+                  "lds_lookup_peak_per_s": PEAK_LDS_LOOKUPS,
+                  "lds_lookup_frac": round(M * pairs / sec / PEAK_LDS_LOOKUPS, 4)})
     r["traffic"] = traffic_for(key, spec["workload"])
     return r
 
