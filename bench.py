@@ -336,8 +336,8 @@ def setup(a, ctx, dev):
                 "centre + 0.5 N(0,I) (seeds 5, 1, 2); codebooks: 8 Lloyd iterations "
                 "per segment on the first 65,536 rows (GPU assignment)",
         "dtype": "u8 codes, f32 LUT", "nq": nq, "n": n, "d": d, "M": M,
-        "kernels": [("pq_adc_filter", "k_pq_adc<FILTER,M16>", "hbm_pq"),
-                    ("pq_adc_dense", "k_pq_adc<DENSE,M16>", "hbm_pq")],
+        "kernels": [("pq_adc_filter", "k_pq_adc16<FILTER> (8 queries per workgroup)", "lds_pq"),
+                    ("pq_adc_dense", "k_pq_adc16<DENSE> (8 queries per workgroup)", "lds_pq")],
         "keep": (pq, db, x, q, codes, dist, ids),
     }
     return spec, step, cpu_leg
@@ -408,6 +408,26 @@ def roofline(spec, stats):
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
                   "algorithmic": "4*d bytes per (query, probed row) pair: every probed "
                                  "list row read once per query"})
+    elif kind == "lds_pq":
+        # the tables are read from LDS, one 4-byte lookup per (query, code
+        # byte); the code stream itself is shared by the 8 queries of a
+        # workgroup, so the per-query code bytes exceed the HBM peak
+        M = spec["M"]
+        look = 1.0 * M * pairs / sec
+        ach = 4.0 * look / 1e9
+        peak = 4.0 * PEAK_LDS_LOOKUPS / 1e9
+        r.update({"bound": "lds", "achieved": round(ach, 1), "peak": round(peak, 1),
+                  "unit": "GB/s", "frac": round(ach / peak, 4),
+                  "algorithmic": "M table lookups (4 bytes each, from LDS) per (query, row) "
+                                 "pair",
+                  "peak_basis": "64 four-byte LDS banks per CU x 256 CUs x 2.4 GHz (random "
+                                "8-bit codes make bank conflicts; the conflict-free rate is "
+                                "the ceiling)",
+                  "lds_lookups_per_s": look,
+                  "code_bytes_basis": {"bytes_per_pair": M,
+                                       "achieved_GBps": round(M * pairs / sec / 1e9, 1),
+                                       "frac_of_hbm": round(M * pairs / sec / 1e9
+                                                            / PEAK_HBM_GBPS, 4)}})
     else:  # hbm_pq
         M = spec["M"]
         by = 1.0 * M * pairs

@@ -16,11 +16,13 @@
 // separate multiply and add roundings (no FMA), so tables, ADC sums, re-rank
 // distances and ids are bit-identical to the CPU.
 //
-// ADC scan: a workgroup holds the tables of QG queries in LDS (M*ksub*4
-// bytes each) and streams a slice of the code rows; a thread owns a row,
-// loads its M code bytes once and accumulates the QG sums; each sum is keyed
-// (sum, row) and goes through the same threshold filter / append as the flat
-// scan.  Ranking is on the sum (sqrt is monotone); sqrt is applied to the
+// ADC scan: a workgroup holds the tables of several queries in LDS and
+// streams a slice of the code rows; a thread owns a row, loads its code
+// bytes once and accumulates one sum per query; each sum is keyed (sum, row)
+// and goes through the same threshold filter / append as the flat scan.
+// k_pq_adc16 serves M = 16, ksub = 256 (8 queries, tables interleaved four
+// queries to a 16-byte entry, survivors staged in LDS); k_pq_adc any other
+// shape.  Ranking is on the sum (sqrt is monotone); sqrt is applied to the
 // outputs only.
 #include "flat.hpp"
 
@@ -282,6 +284,266 @@ static void launch_adc(vsk_ctx *ctx, AdcArgs a, bool dense) {
   check_launch("pq_adc_scan");
 }
 
+// ADC scan for the common shape M = 16, ksub = 256 (16-byte code rows).
+// A workgroup of 8 waves holds the tables of 8 queries in LDS, interleaved
+// four queries to a 16-byte entry (entry [g][m][c] = table[m][c] of queries
+// 4g..4g+3), so one ds_read_b128 serves four queries and the entries of one
+// m spread over all 16 four-bank groups.  A thread owns a code row: one
+// 16-byte load, 32 LDS reads, the eight sums in m order (bit-exact).
+// Filter mode reserves `sub` slots of each query's candidate list up front
+// (one device atomic per query, not one per survivor: the counters of the
+// 8,000 survivors of a query would otherwise serialise at one L2 address)
+// and fills them through LDS counters; unused slots become NONE and a query
+// whose slots overflow gets a count past cap (the chunk is re-scanned).
+// Workgroup L runs on XCD L % 8; the query groups of one row split are
+// consecutive slots of one XCD, so they share its L2 for the code rows.
+constexpr int PQ16_QG = 8, PQ16_T = 512;
+typedef float pq_f4 __attribute__((ext_vector_type(4)));
+// the tables (128 KB), then per query: slot limit, slot count, active flag,
+// first slot, threshold key (all in the dynamic block: a static LDS array
+// placed before the tables would leave their alignment unknown)
+constexpr int PQ16_TAB = 2 * 16 * 256 * 16;
+constexpr int PQ16_STATE = PQ16_QG * (3 * 4 + 2 * 8);
+// filter survivors are staged per wave in LDS (key, then slot << 3 | query)
+// and stored in bulk: a global store between the prefetch loads and their
+// use would make every use wait for all of them (one vector memory counter
+// for loads and stores, which may then complete out of order)
+constexpr int PQ16_WBUF = 256;
+constexpr int PQ16_LDS = PQ16_TAB + PQ16_STATE + (PQ16_T / 64) * PQ16_WBUF * 12;
+
+struct Adc16Args {
+  const uint8_t *codes;
+  const float *lut;  // [nq][16][256]
+  int32_t nq, nqg, splits_per_xcd, sub;
+  int64_t r0, r1, rows_per_split;
+  const uint64_t *thresh;
+  const uint8_t *active;
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+};
+
+template <bool DENSE>
+__global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+  int32_t *s_lim = reinterpret_cast<int32_t *>(lds_raw + PQ16_TAB);
+  int32_t *s_cnt = s_lim + PQ16_QG, *s_ok = s_cnt + PQ16_QG;
+  int64_t *s_pb = reinterpret_cast<int64_t *>(s_ok + PQ16_QG + (PQ16_QG & 1));
+  uint64_t *s_th = reinterpret_cast<uint64_t *>(s_pb + PQ16_QG);
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  uint64_t *w_key = reinterpret_cast<uint64_t *>(lds_raw + PQ16_TAB + PQ16_STATE) +
+                    wv * PQ16_WBUF;
+  uint32_t *w_meta = reinterpret_cast<uint32_t *>(
+                         lds_raw + PQ16_TAB + PQ16_STATE + (PQ16_T / 64) * PQ16_WBUF * 8) +
+                     wv * PQ16_WBUF;
+  const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
+  const int qg = slot % a.nqg;
+  const int split = (slot / a.nqg) * 8 + xcd;
+  const int64_t q0 = (int64_t)qg * PQ16_QG;
+  const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1 || q0 >= a.nq) return;
+  {
+    float4 *w = reinterpret_cast<float4 *>(lds_raw);
+    for (int e = tid; e < 2 * 4096; e += PQ16_T) {
+      const int g = e >> 12, mc = e & 4095;
+      float v[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int64_t q = q0 + 4 * g + jj;
+        v[jj] = q < a.nq ? a.lut[q * 4096 + mc] : 0.f;
+      }
+      w[e] = float4{v[0], v[1], v[2], v[3]};
+    }
+  }
+  if (tid < PQ16_QG) {
+    const int64_t q = q0 + tid;
+    const bool ok = q < a.nq && (!a.active || a.active[q]);
+    s_ok[tid] = ok ? 1 : 0;
+    s_th[tid] = (ok && !DENSE) ? a.thresh[q] : VSK_KEY_NONE;
+    if constexpr (!DENSE) {
+      const int64_t base = ok ? atomicAdd(&a.counts[q], a.sub) : a.cap;
+      const int64_t room = a.cap - base;
+      s_lim[tid] = (int32_t)(room < a.sub ? (room > 0 ? room : 0) : a.sub);
+      s_pb[tid] = q * a.cap + base;
+      s_cnt[tid] = 0;
+    }
+  }
+  __syncthreads();
+  // threshold of each query as a sum: a row can pass only if its sum is at
+  // most this (NaN sums order last and never pass a finite threshold)
+  float thf[PQ16_QG];
+  uint64_t thk[PQ16_QG];
+  bool ok[PQ16_QG];
+#pragma unroll
+  for (int j = 0; j < PQ16_QG; ++j) {
+    const uint64_t th = s_th[j];
+    thk[j] = th;
+    ok[j] = s_ok[j] != 0;
+    const uint32_t hi = (uint32_t)(th >> 32);
+    thf[j] = hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000) : vsk_ord2f(hi);
+  }
+  // code rows of this split through a buffer descriptor (reads past the
+  // split return 0), prefetched two rows ahead so that the load latency of
+  // the stream hides behind the lookups
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.codes + s0 * 16), 0, (int32_t)((s1 - s0) * 16), 0x00020000);
+  // block b = rows s0 + 512 b + tid; every lane runs the same number of
+  // blocks (rows past the split read as zeros and are masked at the end)
+  auto load_blk = [&](int b) {
+    return __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(rc, (b * PQ16_T + tid) * 16, 0, 0));
+  };
+  int wcnt = 0;  // this wave's staged survivors (wave-uniform)
+  auto flush = [&]() {
+    for (int i = lane; i < wcnt; i += 64) {
+      const uint32_t meta = w_meta[i];
+      const int j = (int)(meta & 7u), pos = (int)(meta >> 3);
+      if (pos < s_lim[j]) a.cand[s_pb[j] + pos] = w_key[i];
+    }
+    wcnt = 0;
+    // the stores complete here, so none is pending beside the prefetch loads
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  };
+  // one row: 32 table reads (16 bytes each, four queries), the eight sums in
+  // m order, then the filter or the dense store
+  auto row = [&](int b, const uint4 cw) {
+    const int64_t r = s0 + (int64_t)b * PQ16_T + tid;
+    const bool valid = r < s1;
+    const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+    float sa[4] = {0.f, 0.f, 0.f, 0.f}, sb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int c = (w4[m >> 2] >> (8 * (m & 3))) & 0xFF;
+      // (a native 4-vector: one 16-byte read each; the HIP float4 struct is
+      // split into scalar loads, some of which come back 4 bytes wide)
+      const pq_f4 va = *reinterpret_cast<const pq_f4 *>(lds_raw + (m * 256 + c) * 16);
+      const pq_f4 vb = *reinterpret_cast<const pq_f4 *>(lds_raw + 65536 + (m * 256 + c) * 16);
+      sa[0] = sa[0] + va[0];
+      sa[1] = sa[1] + va[1];
+      sa[2] = sa[2] + va[2];
+      sa[3] = sa[3] + va[3];
+      sb[0] = sb[0] + vb[0];
+      sb[1] = sb[1] + vb[1];
+      sb[2] = sb[2] + vb[2];
+      sb[3] = sb[3] + vb[3];
+    }
+    const float sum[PQ16_QG] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+#pragma unroll
+    for (int j = 0; j < PQ16_QG; ++j) {
+      const uint64_t key = vsk_key(sum[j], (uint32_t)r);
+      if constexpr (DENSE) {
+        if (ok[j] && valid) a.cand[(q0 + j) * a.cap + (r - a.r0)] = key;
+      } else {
+        const bool pass = ok[j] && valid && !(sum[j] > thf[j]) && key <= thk[j];
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(pass);
+        if (mask == 0) continue;
+        if (pass) {
+          const int pos = atomicAdd(&s_cnt[j], 1);
+          const int at = wcnt + (int)__builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(mask >> 32),
+                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+          w_key[at] = key;
+          w_meta[at] = ((uint32_t)pos << 3) | (uint32_t)j;
+        }
+        wcnt += __builtin_popcountll(mask);
+        if (wcnt > PQ16_WBUF - 64) flush();
+      }
+    }
+  };
+  // four code buffers, each reloaded right after its row is consumed: the
+  // load of block b+4 is in flight while blocks b+1..b+3 are processed (a
+  // rotation of registers instead would wait for the load just issued)
+  const int nblk = (int)((s1 - s0 + PQ16_T - 1) / PQ16_T);
+  uint4 c0 = load_blk(0), c1 = load_blk(1), c2 = load_blk(2), c3 = load_blk(3);
+  // (no early exit between the four: a conditional reload makes every
+  // trip wait for all loads in flight; splits are whole multiples of 8
+  // blocks except a chunk's last)
+  for (int b = 0; b < nblk; b += 4) {
+    row(b, c0);
+    c0 = load_blk(b + 4);
+    row(b + 1, c1);
+    c1 = load_blk(b + 5);
+    row(b + 2, c2);
+    c2 = load_blk(b + 6);
+    row(b + 3, c3);
+    c3 = load_blk(b + 7);
+  }
+  if constexpr (!DENSE) {
+    flush();
+    __syncthreads();
+#pragma unroll 1
+    for (int j = 0; j < PQ16_QG; ++j) {
+      if (!ok[j]) continue;
+      const int32_t n = s_cnt[j], lim = s_lim[j];
+      if (n > lim) {
+        if (tid == 0) atomicAdd(&a.counts[q0 + j], (int32_t)a.cap + 1);
+      } else {
+        for (int32_t i = n + tid; i < lim; i += PQ16_T) a.cand[s_pb[j] + i] = VSK_KEY_NONE;
+      }
+    }
+  }
+}
+
+static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
+  const int64_t rows = in.r1 - in.r0;
+  if (rows <= 0 || in.nq <= 0) return;
+  static bool lds_set = false;
+  if (!lds_set) {
+    VSK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(k_pq_adc16<true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, PQ16_LDS));
+    VSK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(k_pq_adc16<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, PQ16_LDS));
+    lds_set = true;
+  }
+  Adc16Args a;
+  a.codes = in.codes;
+  a.lut = in.lut;
+  a.nq = in.nq;
+  a.nqg = (int32_t)ceil_div(in.nq, PQ16_QG);
+  a.r0 = in.r0;
+  a.r1 = in.r1;
+  a.thresh = in.thresh;
+  a.active = in.active;
+  a.cand = in.cand;
+  a.cap = in.cap;
+  a.counts = in.counts;
+  // Row splits, a multiple of 8: the fewest (rounds of one workgroup per CU
+  // x rows per split), up to about 8 rounds, each split at least 4,096 rows
+  // (the tables are 128 KB per workgroup); filter mode keeps at least 64
+  // reserved slots per (split, query).
+  const int64_t unit = PQ16_T * 8;
+  const int64_t units = ceil_div(rows, unit);
+  int64_t top = 8 * ceil_div(8 * (int64_t)ctx->cu_count, 8 * (int64_t)a.nqg);
+  if (top > 8 * ceil_div(units, 8)) top = 8 * ceil_div(units, 8);
+  if (!dense && top > in.cap / 64 / 8 * 8) top = in.cap / 64 / 8 * 8;
+  if (top < 8) top = 8;
+  int64_t splits = 8, best = -1;
+  for (int64_t sp = 8; sp <= top; sp += 8) {
+    const int64_t ups = ceil_div(units, sp);
+    const int64_t used = ceil_div(units, ups);
+    const int64_t cost = ceil_div((int64_t)a.nqg * used, (int64_t)ctx->cu_count) * ups;
+    if (best < 0 || cost < best) {
+      best = cost;
+      splits = sp;
+    }
+  }
+  a.rows_per_split = ceil_div(units, splits) * unit;
+  a.splits_per_xcd = (int32_t)(splits / 8);
+  a.sub = dense ? 0 : (int32_t)(in.cap / splits);
+  if (!dense && a.sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
+  const int64_t nblocks = (int64_t)a.nqg * splits;
+  if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
+  KernelTimer t(ctx, dense ? "pq_adc_dense" : "pq_adc_filter", (double)in.nq * (double)rows);
+  if (dense)
+    k_pq_adc16<true><<<(unsigned)nblocks, PQ16_T, PQ16_LDS, ctx->stream>>>(a);
+  else
+    k_pq_adc16<false><<<(unsigned)nblocks, PQ16_T, PQ16_LDS, ctx->stream>>>(a);
+  check_launch("pq_adc16");
+}
+
 // exact distance of each ADC candidate, summed in index order (no FMA);
 // one thread per (query, candidate)
 __global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
@@ -505,7 +767,10 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
       a.cand = r.cand;
       a.cap = r.cap;
       a.counts = r.counts;
-      launch_adc(ctx, a, r.dense);
+      if (pq->M == 16 && pq->ksub == 256)
+        launch_adc16(ctx, a, r.dense);
+      else
+        launch_adc(ctx, a, r.dense);
     };
     progressive_topk(ctx, nb, pq->n, k_adc, cap, scan, best + b0 * k_adc,
                      "pq_select");
