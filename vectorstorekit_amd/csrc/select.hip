@@ -8,10 +8,11 @@
 // carries its tie key in the low 32 bits, so all keys of a query are
 // distinct and "the k smallest keys" is exactly the stable-sort prefix.
 //
-// Selection is a most-significant-digit radix select: 8 passes of 8-bit
-// digits at most, each a 256-bin LDS histogram of the keys that still match
-// the resolved prefix; it stops early as soon as the bucket holding the
-// k-th key is taken whole.  The <= k winners are gathered into LDS and
+// Selection is a most-significant-digit radix select over the bits below
+// the highest one where the query's smallest and largest keys differ: 8-bit
+// digits (the last one narrower), each a 256-bin LDS histogram of the keys
+// that still match the resolved prefix; it stops early as soon as the bucket
+// holding the k-th key is taken whole.  The <= k winners are gathered into LDS and
 // bitonic-sorted (at most 1024 of them).
 #include "vsk_api.hpp"
 
@@ -56,18 +57,59 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   __shared__ int sh_bucket, sh_take_all;
   __shared__ uint32_t sh_before, sh_bcount;
   __shared__ int sel_count;
+  __shared__ uint64_t sh_lo[SEL_THREADS / 64], sh_hi[SEL_THREADS / 64];
+
+  // smallest and largest key: the digits start at the highest bit where
+  // they differ (the distances of one query share their leading bits, and a
+  // histogram of a digit every key agrees on is a pass spent on one bin)
+  uint64_t lo = VSK_KEY_NONE, hi = 0;
+  for (int64_t i = tid; i < total; i += SEL_THREADS) {
+    const uint64_t key = sel_elem(P, np, C, i);
+    if (key == VSK_KEY_NONE) continue;
+    lo = key < lo ? key : lo;
+    hi = key > hi ? key : hi;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 > hi ? h2 : hi;
+  }
+  if (lane == 0) {
+    sh_lo[tid >> 6] = lo;
+    sh_hi[tid >> 6] = hi;
+  }
+  __syncthreads();
+  lo = sh_lo[0];
+  hi = sh_hi[0];
+#pragma unroll
+  for (int wv = 1; wv < SEL_THREADS / 64; ++wv) {
+    lo = sh_lo[wv] < lo ? sh_lo[wv] : lo;
+    hi = sh_hi[wv] > hi ? sh_hi[wv] : hi;
+  }
 
   uint64_t prefix = 0, mask = 0, T = VSK_KEY_NONE;
   int64_t need = k;
   bool take_all = false;
+  // top: the highest undecided bit (inclusive); bits above it are common
+  int top = 63;
+  if (lo != VSK_KEY_NONE && lo != hi) {
+    top = 63 - __builtin_clzll(lo ^ hi);
+    mask = top == 63 ? 0 : ~((2ull << top) - 1);
+    prefix = lo & mask;
+  }
+  bool first = true;
 
-  for (int shift = 56; shift >= 0; shift -= 8) {
+  while (top >= 0) {
+    const int width = top + 1 >= 8 ? 8 : top + 1;
+    const int shift = top + 1 - width;
+    const uint32_t dmask = (1u << width) - 1;
     for (int i = tid; i < 256; i += SEL_THREADS) hist[i] = 0;
     __syncthreads();
     for (int64_t i = tid; i < total; i += SEL_THREADS) {
       uint64_t key = sel_elem(P, np, C, i);
       if (key != VSK_KEY_NONE && (key & mask) == prefix)
-        atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
+        atomicAdd(&hist[(uint32_t)(key >> shift) & dmask], 1u);
     }
     __syncthreads();
     if (tid < 64) {
@@ -81,7 +123,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
       }
       uint32_t all = __shfl(incl, 63);
       uint32_t excl = incl - s;
-      if (shift == 56 && all <= (uint32_t)k) {
+      if (first && all <= (uint32_t)k) {
         if (lane == 0) sh_take_all = 1;
       } else {
         if (lane == 0) sh_take_all = 0;
@@ -105,16 +147,18 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
       take_all = true;
       break;
     }
+    first = false;
     const uint32_t b = (uint32_t)sh_bucket;
     need -= sh_before;
     prefix |= (uint64_t)b << shift;
-    mask |= 0xFFull << shift;
+    mask |= (uint64_t)dmask << shift;
     const bool full = (uint64_t)sh_bcount == (uint64_t)need;
     __syncthreads();  // everyone has read the sh_* values
     if (full || shift == 0) {
       T = prefix | ~mask;
       break;
     }
+    top = shift - 1;
   }
 
   if (tid == 0) sel_count = 0;
