@@ -491,8 +491,11 @@ void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
       a.cand = r.cand;
       a.cap = r.cap;
       a.counts = r.counts;
-      if (x3 && passes == 1)
-        launch_flat_screen(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER);
+      if (x3 && passes == 1) {
+        a.seg_n = r.dense ? nullptr : r.seg_n;
+        launch_flat_screen(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER, r.seg_nseg,
+                           r.seg_stride);
+      }
       else if (x3)
         launch_flat_bf16x3(ctx, a, sp, r.dense ? MODE_DENSE : MODE_FILTER, passes);
       else

@@ -51,6 +51,9 @@ struct FlatArgs {
   // screen kernel, filter mode: candidate slots each workgroup reserves per
   // query (0: append through per-candidate atomics)
   int32_t sub;
+  // screen kernel, filter mode: segmented lists (segment = row split, at
+  // q*cap + split*sub) with their key counts here (nq x nseg), else null
+  int32_t *seg_n;
 };
 
 // bf16 hi/lo operand planes of the bf16x3 kernel
@@ -73,7 +76,9 @@ void launch_flat_bf16x3(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
                         int passes = 3);
 // the screen's one-pass kernel on 256 x 256 tiles (dense or filter mode;
 // L2^2, L2, normalised cosine, dot)
-void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode);
+// (filter mode with a.seg_n: *nseg and *stride receive the segment layout)
+void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
+                        int32_t *nseg = nullptr, int64_t *stride = nullptr);
 
 // launch one scan over rows [a.r0, a.r1) of a.X for the a.nq queries of a.Q
 // (mode MODE_*; argmin output only for MODE_ARGMIN).  a.rows_per_split is

@@ -471,7 +471,10 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       } else {
         s_tdot[tid] = -thf;
       }
-      const int64_t base = ok ? atomicAdd(&a.counts[q], a.sub) : a.cap;
+      // segmented: this split's fixed segment; else slots taken from the
+      // query's append counter
+      const int64_t base = a.seg_n ? (int64_t)split * a.sub
+                                   : (ok ? atomicAdd(&a.counts[q], a.sub) : a.cap);
       const int64_t room = a.cap - base;
       s_lim[tid] = (int32_t)(room < a.sub ? (room > 0 ? room : 0) : a.sub);
       s_pb[tid] = q * a.cap + base;
@@ -703,11 +706,13 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     __syncthreads();
     if (tid < XS_Q && s_ok[tid]) {
       const int32_t n = s_cnt[tid];
-      if (n > a.sub) {
-        atomicAdd(&a.counts[q0 + tid], (int32_t)a.cap + 1);
-      } else {
+      const int32_t lim = s_lim[tid];
+      // past the slots: the query re-scans the chunk
+      if (n > lim) atomicAdd(&a.counts[q0 + tid], (int32_t)a.cap + 1);
+      if (a.seg_n) {
+        a.seg_n[(q0 + tid) * (int64_t)(8 * a.splits_per_xcd) + split] = n < lim ? n : lim;
+      } else if (n <= lim) {
         const int64_t pb = s_pb[tid];
-        const int32_t lim = s_lim[tid];
         for (int32_t i = n; i < lim; ++i) a.cand[pb + i] = VSK_KEY_NONE;
       }
     }
@@ -724,7 +729,8 @@ static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a,
     k_flat_screen<MODE_FILTER, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
 }
 
-void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode) {
+void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
+                        int32_t *nseg, int64_t *stride) {
   const int64_t rows = a.r1 - a.r0;
   if (rows <= 0 || a.nq <= 0) return;
   if (mode == MODE_MATRIX) fail(VSK_ERR_UNSUPPORTED, "the screen has no matrix mode");
@@ -788,6 +794,13 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode) 
     const int64_t sub = a.cap / splits < 256 ? a.cap / splits : 256;
     if (sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
     a.sub = (int32_t)sub;
+  }
+  if (mode != MODE_FILTER || splits > VSK_MAX_SEG || !nseg || !stride) a.seg_n = nullptr;
+  if (a.seg_n) {
+    // splits without rows launch no writes: their segments start empty
+    fill_i32(ctx, a.seg_n, (int64_t)a.nq * splits, 0);
+    *nseg = (int32_t)splits;
+    *stride = a.sub;
   }
   const int64_t groups = ceil_div(qt, XS_GQ);
   const int64_t nblocks = 8 * a.splits_per_xcd * groups * XS_GQ;

@@ -51,6 +51,26 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   }
   const uint64_t *C = a.cand + base;
   const int64_t total = np + cnt;
+  // segmented lists: the segments' key counts in LDS; wave w walks the
+  // segments w, w + 4, ... (64 lanes per segment)
+  __shared__ int32_t seg_cnt[VSK_MAX_SEG];
+  const bool seg = a.seg_n != nullptr;
+  if (seg) {
+    for (int s = tid; s < a.nseg; s += SEL_THREADS) seg_cnt[s] = a.seg_n[q * a.nseg + s];
+    __syncthreads();
+  }
+  auto each_key = [&](auto &&f) {
+    if (!seg) {
+      for (int64_t i = tid; i < total; i += SEL_THREADS) f(sel_elem(P, np, C, i));
+      return;
+    }
+    for (int64_t i = tid; i < np; i += SEL_THREADS) f(P[i]);
+    for (int s = tid >> 6; s < a.nseg; s += SEL_THREADS / 64) {
+      const uint64_t *cs = a.cand + q * a.cap + (int64_t)s * a.seg_stride;
+      const int32_t ns = seg_cnt[s];
+      for (int32_t j = lane; j < ns; j += 64) f(cs[j]);
+    }
+  };
 
   __shared__ uint32_t hist[256];
   __shared__ uint64_t sel[VSK_MAX_K];
@@ -63,12 +83,11 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   // they differ (the distances of one query share their leading bits, and a
   // histogram of a digit every key agrees on is a pass spent on one bin)
   uint64_t lo = VSK_KEY_NONE, hi = 0;
-  for (int64_t i = tid; i < total; i += SEL_THREADS) {
-    const uint64_t key = sel_elem(P, np, C, i);
-    if (key == VSK_KEY_NONE) continue;
+  each_key([&](uint64_t key) {
+    if (key == VSK_KEY_NONE) return;
     lo = key < lo ? key : lo;
     hi = key > hi ? key : hi;
-  }
+  });
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
@@ -106,11 +125,10 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
     const uint32_t dmask = (1u << width) - 1;
     for (int i = tid; i < 256; i += SEL_THREADS) hist[i] = 0;
     __syncthreads();
-    for (int64_t i = tid; i < total; i += SEL_THREADS) {
-      uint64_t key = sel_elem(P, np, C, i);
+    each_key([&](uint64_t key) {
       if (key != VSK_KEY_NONE && (key & mask) == prefix)
         atomicAdd(&hist[(uint32_t)(key >> shift) & dmask], 1u);
-    }
+    });
     __syncthreads();
     if (tid < 64) {
       uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1],
@@ -163,13 +181,12 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
 
   if (tid == 0) sel_count = 0;
   __syncthreads();
-  for (int64_t i = tid; i < total; i += SEL_THREADS) {
-    uint64_t key = sel_elem(P, np, C, i);
+  each_key([&](uint64_t key) {
     if (key != VSK_KEY_NONE && (take_all || key <= T)) {
       int pos = atomicAdd(&sel_count, 1);
       if (pos < VSK_MAX_K) sel[pos] = key;
     }
-  }
+  });
   __syncthreads();
   int m = sel_count;
   if (m > k) m = k;  // cannot happen with distinct keys; keeps LDS in range
@@ -236,6 +253,8 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
       static_cast<int32_t *>(ctx->scratch_ptr("topk.counts", 4 * nq));
   uint8_t *ovf_mask =
       static_cast<uint8_t *>(ctx->scratch_ptr("topk.ovfmask", nq + 64));
+  int32_t *seg_n = static_cast<int32_t *>(
+      ctx->scratch_ptr("topk.segn", sizeof(int32_t) * (size_t)nq * VSK_MAX_SEG));
   int32_t *ovf_count =
       static_cast<int32_t *>(ctx->scratch_ptr("topk.ovfcount", 64));
   fill_u64(ctx, thresh, nq, VSK_KEY_NONE);
@@ -257,7 +276,17 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     }
     const bool dense = first;
     fill_i32(ctx, counts, nq, dense ? (int32_t)c : 0);
-    scan(ScanRequest{r0, r0 + c, thresh, nullptr, cand, cap, counts, dense});
+    int32_t nseg = 0;
+    int64_t seg_stride = 0;
+    {
+      ScanRequest rq{r0, r0 + c, thresh, nullptr, cand, cap, counts, dense};
+      if (!dense) {
+        rq.seg_n = seg_n;
+        rq.seg_nseg = &nseg;
+        rq.seg_stride = &seg_stride;
+      }
+      scan(rq);
+    }
     SelectArgs sa;
     sa.nq = nq;
     sa.k = k;
@@ -272,6 +301,11 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
       fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
       sa.overflow_mask = ovf_mask;
       sa.overflow_count = ovf_count;
+      if (nseg > 0) {
+        sa.seg_n = seg_n;
+        sa.nseg = nseg;
+        sa.seg_stride = seg_stride;
+      }
     }
     launch_select(ctx, sa, select_name);
     if (!dense) {

@@ -57,8 +57,17 @@ struct SelectArgs {
   const uint8_t *active = nullptr;
   uint8_t *overflow_mask = nullptr;
   int32_t *overflow_count = nullptr;
+  // segmented lists: query q's candidates are segments s = 0..nseg-1 at
+  // cand[q*cap + s*seg_stride], seg_n[q*nseg + s] keys each (counts then
+  // only flags overflow)
+  const int32_t *seg_n = nullptr;
+  int32_t nseg = 0;
+  int64_t seg_stride = 0;
 };
 void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name);
+
+// maximum segments per query of a segmented scan
+constexpr int32_t VSK_MAX_SEG = 512;
 
 // A scan kernel over database rows [r0, r1) that, for each active query q,
 // either writes the key of every row to cand[q*cap + (row - r0)] (dense) or
@@ -72,6 +81,12 @@ struct ScanRequest {
   int64_t cap;
   int32_t *counts;
   bool dense;
+  // a filter scan may write segmented lists instead (see SelectArgs): it
+  // fills seg_n (nq x VSK_MAX_SEG) and reports its layout in *seg_nseg and
+  // *seg_stride; left at 0, the lists are the appended kind
+  int32_t *seg_n = nullptr;
+  int32_t *seg_nseg = nullptr;
+  int64_t *seg_stride = nullptr;
 };
 using ScanFn = std::function<void(const ScanRequest &)>;
 
