@@ -208,6 +208,9 @@ def setup(a, ctx, dev):
             "dtype": "f32", "nq": nq, "n": n, "d": d,
             "kernels": [("flat_screen_filter", "k_flat_screen<FILTER>", "mfma_bf16"),
                         ("flat_screen_dense", "k_flat_screen<DENSE>", "mfma_bf16"),
+                        # small problems: the exact sequential scan alone
+                        ("flat_valu_dense", "k_flat_valu<DENSE> (exact, dimension order)",
+                         "valu_l2" if c == "c1" else "valu_dot"),
                         ("flat_bf16x3_filter", "k_flat_bf16x3<FILTER>", "mfma"),
                         ("flat_bf16x3_dense", "k_flat_bf16x3<DENSE>", "mfma"),
                         ("flat_mfma_filter", "k_flat_mfma<FILTER>", "mfma32"),
@@ -383,24 +386,27 @@ def roofline(spec, stats):
                   "unit": "TOP/s", "frac": round(ach / PEAK_INT8_MFMA_TOPS, 4),
                   "algorithmic": "2*d int8 OP per (query, row) pair",
                   "peak_basis": "int8 dense MFMA 5.0 POP/s"})
-    elif kind == "valu":
-        # exact fp32 (q - x)^2 sums in dimension order: a subtract, a multiply
-        # and an add per dimension, no fused multiply-add, no packed fp32
-        flop = 3.0 * d * pairs
+    elif kind in ("valu", "valu_l2", "valu_dot"):
+        # exact fp32 sums in dimension order, no fused multiply-add, no
+        # packed fp32: (q - x)^2 is a subtract, a multiply and an add per
+        # dimension, q.x a multiply and an add
+        flop = (2.0 if kind == "valu_dot" else 3.0) * d * pairs
         ach = flop / sec / 1e12
         r.update({"bound": "valu", "achieved": round(ach, 2), "peak": PEAK_FP32_VALU_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_VALU_TFLOPS, 4),
-                  "algorithmic": "3*d fp32 operations per (query, probed row) pair",
+                  "algorithmic": ("2*d" if kind == "valu_dot" else "3*d")
+                                 + " fp32 operations per (query, row) pair",
                   "peak_basis": "fp32 vector 157.3 TFLOP/s (packed FMA); with one non-packed, "
                                 "non-fused operation per lane per cycle the issue ceiling is "
                                 f"{PEAK_FP32_VALU_ISSUE_TOPS} T operations/s",
-                  "frac_of_issue_ceiling": round(ach / PEAK_FP32_VALU_ISSUE_TOPS, 4),
-                  # the probed-list-bytes basis: above the HBM peak, because a list
-                  # row is read once for all the queries of a group that probe it
-                  "list_bytes_basis": {"bytes_per_pair": 4 * d,
-                                       "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
-                                       "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
-                                                            / PEAK_HBM_GBPS, 4)}})
+                  "frac_of_issue_ceiling": round(ach / PEAK_FP32_VALU_ISSUE_TOPS, 4)})
+        if kind == "valu":
+            # the probed-list-bytes basis: above the HBM peak, because a list
+            # row is read once for all the queries of a group that probe it
+            r["list_bytes_basis"] = {"bytes_per_pair": 4 * d,
+                                     "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
+                                     "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
+                                                          / PEAK_HBM_GBPS, 4)}
     elif kind == "hbm":
         by = 4.0 * d * pairs
         ach = by / sec / 1e9

@@ -145,11 +145,36 @@ def test_errors(ctx):
 SCREEN = [METRIC_L2SQ, METRIC_L2, METRIC_COSINE_NORMALIZED, METRIC_DOT]
 
 
+@pytest.fixture(scope="module")
+def sctx():
+    """A context that runs the screen at every size (small problems
+    otherwise take the exact sequential scan alone)."""
+    import os
+
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vectorstorekit_amd.engine import Context
+
+    old = os.environ.get("VSK_FLAT_KERNEL")
+    os.environ["VSK_FLAT_KERNEL"] = "screen"
+    try:
+        c = Context(0)
+    finally:
+        if old is None:
+            del os.environ["VSK_FLAT_KERNEL"]
+        else:
+            os.environ["VSK_FLAT_KERNEL"] = old
+    yield c
+    c.close()
+
+
 @pytest.mark.parametrize("metric", SCREEN)
 @pytest.mark.parametrize("shape", [(3000, 20, 128, 10), (40_000, 64, 100, 50),
                                    (20_000, 33, 37, 100), (25_000, 10, 768, 320),
                                    (6000, 12, 96, 20)])
-def test_screen_bit_exact(ctx, metric, shape):
+def test_screen_bit_exact(sctx, metric, shape):
     """The screened metrics (one-pass bf16 screen, proven bound, fp32
     rescore) return the CPU reference's sequential fp32 distances and its
     (distance, id) order exactly: one dense chunk, filtered chunks, odd d,
@@ -157,11 +182,11 @@ def test_screen_bit_exact(ctx, metric, shape):
     n, nq, d, k = shape
     x, q = _data(n + d + metric, n, nq, d, normalize=metric == METRIC_COSINE_NORMALIZED)
     print(f"screen metric={metric} n={n} nq={nq} d={d} k={k}", flush=True)
-    ctx.profile(True)
-    ctx.profile_reset()
-    gd, gi = VectorDatabase(ctx, x).search(q, k, metric)
-    stats = ctx.profile_stats()
-    ctx.profile(False)
+    sctx.profile(True)
+    sctx.profile_reset()
+    gd, gi = VectorDatabase(sctx, x).search(q, k, metric)
+    stats = sctx.profile_stats()
+    sctx.profile(False)
     assert "flat_screen_dense" in stats and "screen_rescore" in stats
     od, oi = O.search_flat(q, x, k, metric)
     np.testing.assert_array_equal(gi, oi)
@@ -169,7 +194,7 @@ def test_screen_bit_exact(ctx, metric, shape):
 
 
 @pytest.mark.parametrize("metric", SCREEN)
-def test_screen_fallback_near_ties(ctx, metric):
+def test_screen_fallback_near_ties(sctx, metric):
     """Rows closer to each other than the screen's error bound: the margin
     test fails for every query, at the wide second screen too, the exact
     VALU scan redoes them, and the result is still the reference's, bit for
@@ -183,11 +208,11 @@ def test_screen_fallback_near_ties(ctx, metric):
         x /= np.linalg.norm(x, axis=1, keepdims=True)
         q /= np.linalg.norm(q, axis=1, keepdims=True)
     print(f"screen fallback metric={metric}", flush=True)
-    ctx.profile(True)
-    ctx.profile_reset()
-    gd, gi = VectorDatabase(ctx, x).search(q, 10, metric)
-    stats = ctx.profile_stats()
-    ctx.profile(False)
+    sctx.profile(True)
+    sctx.profile_reset()
+    gd, gi = VectorDatabase(sctx, x).search(q, 10, metric)
+    stats = sctx.profile_stats()
+    sctx.profile(False)
     assert stats["screen_retry"][2] == 8  # work counter: queries redone
     assert stats["screen_fallback"][2] == 8
     od, oi = O.search_flat(q, x, 10, metric)
@@ -195,19 +220,38 @@ def test_screen_fallback_near_ties(ctx, metric):
     np.testing.assert_array_equal(gd, od)
 
 
-def test_screen_normalized_db_and_device_queries(ctx):
+def test_screen_normalized_db_and_device_queries(sctx):
     """Rows normalised on upload and queries already on the device: the
     rescore reads the stored (normalised) rows."""
     import torch
 
     x, q = _data(31, 30_000, 40, 96)
-    db = VectorDatabase(ctx, x, normalize=True)
+    db = VectorDatabase(sctx, x, normalize=True)
     xn = db.read()
     qn = q / np.linalg.norm(q, axis=1, keepdims=True)
     gd, gi = db.search(torch.from_numpy(qn).cuda(), 25, METRIC_COSINE_NORMALIZED)
     od, oi = O.search_flat(qn, xn, 25, METRIC_COSINE_NORMALIZED)
     np.testing.assert_array_equal(gi.cpu().numpy(), oi)
     np.testing.assert_array_equal(gd.cpu().numpy(), od)
+
+
+@pytest.mark.parametrize("metric", SCREEN)
+def test_small_problem_exact_scan(ctx, metric):
+    """Config 1's size (at most 2^28 query x row x dimension terms) takes the
+    exact sequential scan alone, without the screen, and returns the CPU
+    reference's distances and order bit for bit."""
+    x, q = _data(90 + metric, 10_000, 100, 128,
+                 normalize=metric == METRIC_COSINE_NORMALIZED)
+    print(f"small exact metric={metric}", flush=True)
+    ctx.profile(True)
+    ctx.profile_reset()
+    gd, gi = VectorDatabase(ctx, x).search(q, 10, metric)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    assert "flat_screen_dense" not in stats and "screen_rescore" not in stats
+    od, oi = O.search_flat(q, x, 10, metric)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
 
 
 def test_upload_read_roundtrip_padded_chunked(ctx):

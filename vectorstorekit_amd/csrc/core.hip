@@ -349,6 +349,7 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   const char *fk = getenv("VSK_FLAT_KERNEL");
   c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
+  c->flat_force_screen = fk && strcmp(fk, "screen") == 0;
   // a blocking stream: it orders itself after work on the null stream, so
   // device buffers produced there (e.g. by torch) are complete when read
   if (hipStreamCreate(&c->stream) != hipSuccess ||

@@ -450,6 +450,14 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
 // top-k over a resident database for queries already on the device
 bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                       int64_t nq, int32_t k, int32_t metric, uint64_t *best) {
+  // a small problem (at most 2^28 query x row x dimension terms, some 20 us
+  // of exact VALU work) is cheaper by the exact sequential scan alone than
+  // by the screen's fixed chain of launches and its check read-back
+  if (!ctx->flat_no_screen && !ctx->flat_force_screen && screen_applies(metric, k) &&
+      (double)nq * (double)db->n * (double)db->d <= 268435456.0) {
+    approx_topk(ctx, db, dq, nq, k, exact_metric(metric), best, 3);
+    return true;
+  }
   if (!ctx->flat_no_screen && screen_applies(metric, k)) {
     screen_topk(ctx, db, dq, nq, k, metric, best);
     return true;

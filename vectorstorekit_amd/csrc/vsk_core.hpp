@@ -68,10 +68,12 @@ struct vsk_ctx {
 
   // flat top-k path, from the environment VSK_FLAT_KERNEL at context
   // creation: unset = one-pass bf16 screen with exact fp32 rescore where the
-  // metric allows it (bf16x3 elsewhere); "bf16x3" = bf16x3 split MFMA
-  // only; "fp32" = fp32 MFMA only
+  // metric allows it (the exact sequential scan alone for small problems,
+  // bf16x3 elsewhere); "screen" = the screen at every size; "bf16x3" =
+  // bf16x3 split MFMA only; "fp32" = fp32 MFMA only
   bool flat_fp32 = false;
   bool flat_no_screen = false;
+  bool flat_force_screen = false;
 
   // profiling
   bool profile = false;
