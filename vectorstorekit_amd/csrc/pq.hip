@@ -544,55 +544,119 @@ static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
   check_launch("pq_adc16");
 }
 
-// exact distance of each ADC candidate, summed in index order (no FMA);
-// one thread per (query, candidate)
-__global__ void k_rerank(const uint64_t *adc_best, int64_t nq, int32_t kadc,
-                         const float *q, int32_t ldq, const float *x,
-                         int32_t ldx, int32_t d, int32_t metric,
-                         uint64_t *out) {
+// exact distance of each ADC candidate, summed in index order (no FMA).
+// A workgroup takes 256 candidates of one query, a wave 64 of them: per
+// block of 64 dimensions the wave gathers its rows in 256-byte segments (16
+// lanes per row, coalesced) and the query's block into its LDS tile, then
+// every lane continues the sequential sums of its own row from there.
+constexpr int RR_W = 64;         // dimensions per gathered block
+constexpr int RR_LD = RR_W + 4;  // LDS row stride (floats)
+
+template <int METRIC>
+__global__ __launch_bounds__(256) void k_rerank(const uint64_t *adc_best, int32_t kadc,
+                                                const float *q, int32_t ldq,
+                                                const float *x, int32_t ldx, int32_t d,
+                                                uint64_t *out) {
 #pragma clang fp contract(off)
-  const int64_t total = nq * (int64_t)kadc;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const uint64_t key = adc_best[i];
-    if (key == VSK_KEY_NONE) {
-      out[i] = VSK_KEY_NONE;
-      continue;
-    }
-    const uint32_t row = (uint32_t)key;
-    const float *qr = q + (i / kadc) * ldq;
-    const float *xr = x + (int64_t)row * ldx;
-    float dist;
-    if (metric == VSK_METRIC_L1) {
-      float s = 0.f;
-      for (int j = 0; j < d; ++j) s = s + fabsf(qr[j] - xr[j]);
-      dist = s;
-    } else if (metric == VSK_METRIC_L2SQ || metric == VSK_METRIC_L2) {
-      float s = 0.f;
-      for (int j = 0; j < d; ++j) {
-        float t = qr[j] - xr[j];
-        s = s + t * t;
-      }
-      dist = metric == VSK_METRIC_L2 ? sqrtf(s) : s;
-    } else {
-      float dp = 0.f, qq = 0.f, xx = 0.f;
-      for (int j = 0; j < d; ++j) {
-        dp = dp + qr[j] * xr[j];
-        qq = qq + qr[j] * qr[j];
-        xx = xx + xr[j] * xr[j];
-      }
-      if (metric == VSK_METRIC_COSINE) {
-        float den = sqrtf(qq) * sqrtf(xx);
-        den = den + 1e-8f;
-        dist = 1.0f - dp / den;
-      } else if (metric == VSK_METRIC_COSINE_NORMALIZED) {
-        dist = 1.0f - dp;
-      } else {
-        dist = -dp;
-      }
-    }
-    out[i] = vsk_key(dist, row);
+  __shared__ __attribute__((aligned(16))) float tile[4][65 * RR_LD];  // rows, then the query
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t qi = blockIdx.x;
+  const int32_t c = blockIdx.y * 256 + threadIdx.x;
+  const uint64_t key = c < kadc ? adc_best[qi * kadc + c] : VSK_KEY_NONE;
+  const bool valid = key != VSK_KEY_NONE;
+  if (!__builtin_amdgcn_ballot_w64(valid)) {
+    if (c < kadc) out[qi * kadc + c] = VSK_KEY_NONE;
+    return;
   }
+  const uint32_t row = (uint32_t)key;
+  const float *qr = q + qi * ldq;
+  float *t = tile[w];
+  const int seg = lane & 15, sub = lane >> 4;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;  // the metric's sums (cosine: q.x, q.q, x.x)
+  for (int32_t j0 = 0; j0 < d; j0 += RR_W) {
+    const bool cin = j0 + 4 * seg < d;
+#pragma unroll 4
+    for (int r = sub; r < 64; r += 4) {
+      const uint64_t kr = __shfl(key, r);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (kr != VSK_KEY_NONE && cin)
+        v = *reinterpret_cast<const float4 *>(x + (int64_t)(uint32_t)kr * ldx + j0 + 4 * seg);
+      *reinterpret_cast<float4 *>(t + r * RR_LD + 4 * seg) = v;
+    }
+    // (query rows have stride d, not padded: four single reads, bounded)
+    if (sub == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t col = j0 + 4 * seg + e;
+        t[64 * RR_LD + 4 * seg + e] = col < d ? qr[col] : 0.f;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int32_t jn = d - j0 < RR_W ? d - j0 : RR_W;
+    const float *xr = t + lane * RR_LD, *qv = t + 64 * RR_LD;
+    for (int32_t j = 0; j < jn; ++j) {
+      const float a = qv[j], b = xr[j];
+      if constexpr (METRIC == VSK_METRIC_L1) {
+        s0 = s0 + fabsf(a - b);
+      } else if constexpr (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2) {
+        const float tt = a - b;
+        s0 = s0 + tt * tt;
+      } else if constexpr (METRIC == VSK_METRIC_COSINE) {
+        s0 = s0 + a * b;
+        s1 = s1 + a * a;
+        s2 = s2 + b * b;
+      } else {
+        s0 = s0 + a * b;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (c >= kadc) return;
+  if (!valid) {
+    out[qi * kadc + c] = VSK_KEY_NONE;
+    return;
+  }
+  float dist;
+  if constexpr (METRIC == VSK_METRIC_L1 || METRIC == VSK_METRIC_L2SQ) {
+    dist = s0;
+  } else if constexpr (METRIC == VSK_METRIC_L2) {
+    dist = sqrtf(s0);
+  } else if constexpr (METRIC == VSK_METRIC_COSINE) {
+    float den = sqrtf(s1) * sqrtf(s2);
+    den = den + 1e-8f;
+    dist = 1.0f - s0 / den;
+  } else if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED) {
+    dist = 1.0f - s0;
+  } else {
+    dist = -s0;
+  }
+  out[qi * kadc + c] = vsk_key(dist, row);
+}
+
+static void launch_rerank(vsk_ctx *ctx, const uint64_t *best, int64_t nq, int32_t kadc,
+                          const float *q, int32_t ldq, const float *x, int32_t ldx,
+                          int32_t d, int32_t metric, uint64_t *out) {
+  if (nq > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
+  const dim3 grid((unsigned)nq, (unsigned)ceil_div(kadc, 256));
+  switch (metric) {
+#define RR_CASE(M)                                                                 \
+  case M:                                                                          \
+    k_rerank<M><<<grid, 256, 0, ctx->stream>>>(best, kadc, q, ldq, x, ldx, d, out); \
+    break;
+    RR_CASE(VSK_METRIC_L1)
+    RR_CASE(VSK_METRIC_L2SQ)
+    RR_CASE(VSK_METRIC_L2)
+    RR_CASE(VSK_METRIC_COSINE)
+    RR_CASE(VSK_METRIC_COSINE_NORMALIZED)
+    RR_CASE(VSK_METRIC_DOT)
+#undef RR_CASE
+    default: fail(VSK_ERR_INVALID_ARGUMENT, "unknown re-rank metric");
+  }
+  check_launch("pq_rerank");
 }
 
 static void require_pq(const vsk_pq *pq) {
@@ -782,10 +846,8 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
         ctx->scratch_ptr("pq.rerank", sizeof(uint64_t) * nq * k_adc));
     {
       KernelTimer t(ctx, "pq_rerank");
-      k_rerank<<<grid1(nq * k_adc), 256, 0, ctx->stream>>>(
-          best, nq, k_adc, dq, pq->d, rerank_db->x.as<float>(), rerank_db->ld,
-          pq->d, rerank_metric, rk);
-      check_launch("pq_rerank");
+      launch_rerank(ctx, best, nq, k_adc, dq, pq->d, rerank_db->x.as<float>(),
+                    rerank_db->ld, pq->d, rerank_metric, rk);
     }
     uint64_t *fin = static_cast<uint64_t *>(
         ctx->scratch_ptr("pq.final", sizeof(uint64_t) * nq * k));
