@@ -231,7 +231,7 @@ def setup(a, ctx, dev):
 
         def step():
             ctx.check(lib.vsk_ivf_search(ctx.handle, idx.handle, q.data_ptr(), nq, nprobe, k,
-                                         dist.data_ptr(), ids.data_ptr()))
+                                         L.METRIC_L2, dist.data_ptr(), ids.data_ptr()))
 
         def cpu_leg(target_s):
             from oracle import oracle as O

@@ -157,6 +157,13 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
 vsk_status vsk_ivf_create(vsk_ctx *ctx, const float *centroids, int32_t nlist,
                           int32_t d, vsk_ivf **out);
 vsk_status vsk_ivf_free(vsk_ctx *ctx, vsk_ivf *ivf);
+/* One-call build: vsk_ivf_create with the trained centroids, then
+ * vsk_ivf_add of n rows x (n x d fp32; ids may be NULL; n may be 0) --
+ * IVFIndex.train (:397-446, centroids given) followed by insert (:80-122).
+ * On failure nothing is returned and *out is NULL. */
+vsk_status vsk_ivf_build(vsk_ctx *ctx, const float *centroids, int32_t nlist,
+                         const float *x, const int64_t *ids, int64_t n,
+                         int32_t d, vsk_ivf **out);
 /* IVFIndex.insert (:80-122): each row goes to its nearest centroid
  * (findNearestCentroid, :514-527, strict '<'), appended in call order.
  * ids may be NULL (then ids are the running row count). */
@@ -168,11 +175,15 @@ vsk_status vsk_ivf_assign(vsk_ctx *ctx, const vsk_ivf *ivf, const float *x,
 /* findNearestCentroids (:529-540): out_lists[nq x nprobe] */
 vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                          int64_t nq, int32_t nprobe, int32_t *out_lists);
-/* IVFIndex.search (:124-202): probe nprobe lists, exact L2 (sqrt) over
- * their union, top k.  nprobe >= nlist is the .exact strategy (:551-554). */
+/* IVFIndex.search (:124-202): probe nprobe lists, exact L2 over their
+ * union, top k.  nprobe >= nlist is the .exact strategy (:551-554).
+ * metric: VSK_METRIC_L2 (the reference's computeDistance, :542-549, sqrt of
+ * the sum) or VSK_METRIC_L2SQ (the sum itself); other metrics return
+ * VSK_ERR_UNSUPPORTED, as IVFIndex ranks by euclidean distance only.  The
+ * probe always ranks centroids by sqrt-L2 (:529-540). */
 vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                           int64_t nq, int32_t nprobe, int32_t k,
-                          float *out_dist, int64_t *out_ids);
+                          int32_t metric, float *out_dist, int64_t *out_ids);
 /* sizes[nlist] = rows per inverted list; total = sum */
 vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
                               int64_t *sizes);
@@ -204,6 +215,14 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
 vsk_status vsk_pq_create(vsk_ctx *ctx, const float *codebooks, int32_t M,
                          int32_t ksub, int32_t dsub, vsk_pq **out);
 vsk_status vsk_pq_free(vsk_ctx *ctx, vsk_pq *pq);
+/* One-call upload of a trained 8-bit quantizer (ksub = 256, the
+ * configuration ProductQuantizationConfig fixes with codeSize 8,
+ * Config/Quantization/ProductQuantizationConfig.swift:17-49) and n x M
+ * resident codes (n may be 0): vsk_pq_create + vsk_pq_add_codes.  On failure
+ * nothing is returned and *out is NULL. */
+vsk_status vsk_pq_upload(vsk_ctx *ctx, const float *codebooks,
+                         const uint8_t *codes, int64_t n, int32_t M,
+                         int32_t dsub, vsk_pq **out);
 /* encode (:68-112) via Codebook.encode (ProductQuantizerCodebook.swift:12-30):
  * codes n x M uint8 */
 vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,

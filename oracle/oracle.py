@@ -45,7 +45,7 @@ def lib():
             "vsko_ivf_assign": (None, [P, c_int64, P, c_int32, c_int32, P, c_int32]),
             "vsko_ivf_probe": (None, [P, c_int64, P, c_int32, c_int32, c_int32, P, c_int32]),
             "vsko_ivf_search": (None, [P, c_int64, P, P, P, c_int64, c_int32, P, c_int32,
-                                       c_int32, c_int32, P, P, c_int32]),
+                                       c_int32, c_int32, c_int32, P, P, c_int32]),
             "vsko_sq8_train": (None, [P, c_int64, c_int32, c_int32, P, P]),
             "vsko_sq8_encode": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
             "vsko_sq8_decode": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
@@ -129,7 +129,7 @@ def ivf_probe(q, centroids, nprobe, threads=0):
     return out
 
 
-def ivf_search(q, x, ids, list_of, centroids, nprobe, k, threads=0):
+def ivf_search(q, x, ids, list_of, centroids, nprobe, k, threads=0, squared=False):
     q, qp = _c(q, np.float32)
     x, xp = _c(x, np.float32)
     ids, ip = _c(ids, np.int64)
@@ -139,7 +139,7 @@ def ivf_search(q, x, ids, list_of, centroids, nprobe, k, threads=0):
     od = np.empty((nq, k), np.float32)
     oi = np.empty((nq, k), np.int64)
     lib().vsko_ivf_search(qp, nq, xp, ip, lp, x.shape[0], x.shape[1], cp, c.shape[0], nprobe, k,
-                          od.ctypes.data, oi.ctypes.data, threads)
+                          1 if squared else 0, od.ctypes.data, oi.ctypes.data, threads)
     return od, oi
 
 

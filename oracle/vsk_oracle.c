@@ -390,7 +390,7 @@ typedef struct {
   const int64_t *ids;
   const int64_t *list_start; /* [nlist+1] offsets into rows_by_list */
   const int64_t *rows_by_list;
-  int32_t d, nlist, nprobe, k;
+  int32_t d, nlist, nprobe, k, squared;
   float *od;
   int64_t *oi;
 } ivf_ctx;
@@ -421,7 +421,8 @@ static void ivf_range(void *p, int64_t lo, int64_t hi) {
       }
       for (int64_t r = b; r < e; ++r) {
         int64_t row = a->rows_by_list[r];
-        float v = sqrtf(vsko_l2sq(qi, a->x + row * a->d, a->d));
+        float s2 = vsko_l2sq(qi, a->x + row * a->d, a->d);
+        float v = a->squared ? s2 : sqrtf(s2);
         pos_row[pos] = row;
         topk_push(&s, v, pos);
         ++pos;
@@ -442,8 +443,8 @@ static void ivf_range(void *p, int64_t lo, int64_t hi) {
 void vsko_ivf_search(const float *q, int64_t nq, const float *x,
                      const int64_t *ids, const int32_t *list_of, int64_t n,
                      int32_t d, const float *centroids, int32_t nlist,
-                     int32_t nprobe, int32_t k, float *out_dist,
-                     int64_t *out_ids, int32_t nthreads) {
+                     int32_t nprobe, int32_t k, int32_t squared,
+                     float *out_dist, int64_t *out_ids, int32_t nthreads) {
   /* inverted lists keep insertion order (Indexes/IVFIndex.swift:80-122
    * appends to invertedLists[nearest]) */
   int64_t *start = (int64_t *)calloc((size_t)nlist + 1, sizeof(int64_t));
@@ -454,8 +455,8 @@ void vsko_ivf_search(const float *q, int64_t nq, const float *x,
   memcpy(fill, start, sizeof(int64_t) * (nlist + 1));
   for (int64_t i = 0; i < n; ++i) rows[fill[list_of[i]]++] = i;
   free(fill);
-  ivf_ctx a = {q,     x,     centroids, ids,      start,   rows,
-               d,     nlist, nprobe,    k,        out_dist, out_ids};
+  ivf_ctx a = {q, x,      centroids, ids, start,    rows,   d,
+               nlist, nprobe, k,      squared ? 1 : 0, out_dist, out_ids};
   parallel_for(nq, nthreads, ivf_range, &a);
   free(rows);
   free(start);

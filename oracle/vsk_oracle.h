@@ -61,12 +61,13 @@ void vsko_ivf_probe(const float *q, int64_t nq, const float *centroids,
                     int32_t nlist, int32_t d, int32_t nprobe,
                     int32_t *out_lists, int32_t nthreads);
 /* list_of[i] = inverted list of row i (rows keep insertion order inside a
- * list); ids[i] = user id of row i.  Output distances are L2 (sqrt). */
+ * list); ids[i] = user id of row i.  Output distances are L2 (sqrt), or the
+ * squared sum when squared != 0 (ranked on that sum). */
 void vsko_ivf_search(const float *q, int64_t nq, const float *x,
                      const int64_t *ids, const int32_t *list_of, int64_t n,
                      int32_t d, const float *centroids, int32_t nlist,
-                     int32_t nprobe, int32_t k, float *out_dist,
-                     int64_t *out_ids, int32_t nthreads);
+                     int32_t nprobe, int32_t k, int32_t squared,
+                     float *out_dist, int64_t *out_ids, int32_t nthreads);
 
 /* ---- scalar quantization (int8) ----------------------------------------- */
 /* per_dim != 0: scale[d], offset[d] from per-column min/max;

@@ -53,6 +53,44 @@ def test_ivf_bit_exact(ctx, shape):
     np.testing.assert_array_equal(gd, od)
 
 
+def test_ivf_build_one_call_matches_create_add(ctx):
+    x, q, c = _mixture(11, 32, 6000, 40, 25)
+    ids = np.arange(len(x), dtype=np.int64) * 5 + 1
+    cfg = IVFConfiguration(dimensions=40, numberOfCentroids=32, numberOfProbes=6)
+    for use_ids in (ids, None):
+        print(f"ivf build ids={'given' if use_ids is not None else 'none'}", flush=True)
+        built = IVFIndex.build(ctx, cfg, c, x, use_ids)
+        ref = _index(ctx, c, x, use_ids, 6)
+        np.testing.assert_array_equal(built.list_sizes(), ref.list_sizes())
+        bd, bi = built.search(q, 12)
+        rd, ri = ref.search(q, 12)
+        np.testing.assert_array_equal(bi, ri)
+        np.testing.assert_array_equal(bd, rd)
+    empty = IVFIndex.build(ctx, cfg, c, x[:0])
+    d, i = empty.search(q[:2], 3)
+    assert (i == -1).all() and np.isinf(d).all()
+
+
+def test_ivf_squared_metric_bit_exact(ctx):
+    x, q, c = _mixture(12, 48, 12_000, 64, 60)
+    ids = np.arange(len(x), dtype=np.int64)
+    idx = _index(ctx, c, x, ids, 7)
+    lists = O.ivf_assign(x, c)
+    gd, gi = idx.search(q, 16, metric="euclideanSquared")
+    od, oi = O.ivf_search(q, x, ids, lists, c, 7, 16, squared=True)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "dotProduct", "manhattan", "cosineNormalized"])
+def test_ivf_rejects_non_euclidean_metric(ctx, metric):
+    x, q, c = _mixture(13, 8, 500, 8, 4)
+    idx = _index(ctx, c, x, None, 2)
+    with pytest.raises(VSKError) as e:
+        idx.search(q, 3, metric=metric)
+    assert e.value.status == -8
+
+
 def test_ivf_incremental_inserts_keep_order(ctx):
     x, q, c = _mixture(9, 20, 4000, 16, 30)
     idx = _index(ctx, c, None, nprobe=6)

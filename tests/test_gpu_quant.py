@@ -6,7 +6,8 @@ import pytest
 
 from oracle import oracle as O
 from parity import assert_sorted_unique, recall
-from vectorstorekit_amd import ProductQuantizer, ScalarQuantizer, SQ8Database, VectorDatabase
+from vectorstorekit_amd import (ProductQuantizer, ScalarQuantizer, SQ8Database, VectorDatabase,
+                                VSKError)
 from vectorstorekit_amd._lib import METRIC_COSINE, METRIC_L1, METRIC_L2, METRIC_L2SQ
 
 pytestmark = pytest.mark.gpu
@@ -176,6 +177,23 @@ def test_pq_rerank_bit_exact(ctx, metric):
     od, oi = O.pq_search(q, cb, codes, 1000, 100, x=x, rerank_metric=metric)
     np.testing.assert_array_equal(gi, oi)
     np.testing.assert_array_equal(gd, od)
+
+
+def test_pq_upload_one_call_matches_create_add(ctx):
+    x, q, cb = _pq_data(6, 12_000, 32, 4, 256, 15)
+    codes = O.pq_encode(x, cb)
+    up = ProductQuantizer.upload(ctx, cb, codes)
+    ref = ProductQuantizer(ctx, cb)
+    ref.add(codes)
+    ud, ui = up.search(q, 50, k_adc=50)
+    rd, ri = ref.search(q, 50, k_adc=50)
+    np.testing.assert_array_equal(ui, ri)
+    np.testing.assert_array_equal(ud, rd)
+    od, oi = O.pq_search(q, cb, codes, 50, 50)
+    np.testing.assert_array_equal(ui, oi)
+    np.testing.assert_array_equal(ud, od)
+    with pytest.raises(VSKError):
+        ProductQuantizer.upload(ctx, cb[:, :100], codes)
 
 
 def test_config5_full_size(ctx):

@@ -70,6 +70,21 @@ def test_ivf_all_lists_equals_flat():
         assert set(a) == set(b)
 
 
+def test_ivf_squared_all_lists_equals_flat_l2sq():
+    """The squared variant ranks on the sum itself: probing every list gives
+    flat L2SQ's distances exactly, and its sqrt is the default output."""
+    x, q, c = _mixture(4, 16, 3000, 24, 30)
+    lists = O.ivf_assign(x, c)
+    ids = np.arange(len(x), dtype=np.int64)
+    d2, i2 = O.ivf_search(q, x, ids, lists, c, 16, 10, squared=True)
+    fd, fi = O.search_flat(q, x, 10, O.L2SQ)
+    np.testing.assert_array_equal(d2, fd)
+    for a, b in zip(i2, fi):
+        assert set(a) == set(b)
+    d1, _ = O.ivf_search(q, x, ids, lists, c, 16, 10)
+    np.testing.assert_array_equal(d1, np.sqrt(d2))
+
+
 def test_ivf_candidates_in_probe_order():
     x, q, c = _mixture(3, 8, 500, 8, 10)
     lists = O.ivf_assign(x, c)

@@ -97,7 +97,8 @@ SIGNATURES = {
     "vsk_ivf_add": (c_int32, [P, P, P, P, c_int64]),
     "vsk_ivf_assign": (c_int32, [P, P, P, c_int64, P]),
     "vsk_ivf_probe": (c_int32, [P, P, P, c_int64, c_int32, P]),
-    "vsk_ivf_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, P, P]),
+    "vsk_ivf_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P]),
+    "vsk_ivf_build": (c_int32, [P, P, c_int32, P, P, c_int64, c_int32, PP]),
     "vsk_ivf_list_sizes": (c_int32, [P, P, P]),
     "vsk_sq8_train": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_encode": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
@@ -106,6 +107,7 @@ SIGNATURES = {
     "vsk_sq8_search": (c_int32, [P, P, P, c_int64, c_int32, P, P]),
     "vsk_pq_create": (c_int32, [P, P, c_int32, c_int32, c_int32, PP]),
     "vsk_pq_free": (c_int32, [P, P]),
+    "vsk_pq_upload": (c_int32, [P, P, P, c_int64, c_int32, c_int32, PP]),
     "vsk_pq_encode": (c_int32, [P, P, P, c_int64, P]),
     "vsk_pq_add_codes": (c_int32, [P, P, P, c_int64]),
     "vsk_pq_lut": (c_int32, [P, P, P, c_int64, P]),

@@ -108,6 +108,7 @@ struct ListScanArgs {
   const int64_t *pos_base;  // [nq][np]
   const int64_t *seg_off;   // [nq+1] candidate segment offsets
   uint64_t *cand;
+  int32_t squared;          // 1: key on sum (q-x)^2, 0: on its sqrt
 };
 
 // one workgroup per group: up to QG queries probing the same list
@@ -160,8 +161,8 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
 #pragma unroll
     for (int j = 0; j < QG; ++j)
       if (j < npair)
-        a.cand[obase[j] + i] =
-            vsk_key(sqrtf(acc[j]), (uint32_t)(tbase[j] + i));
+        a.cand[obase[j] + i] = vsk_key(a.squared ? acc[j] : sqrtf(acc[j]),
+                                       (uint32_t)(tbase[j] + i));
   }
   (void)qidx;
 }
@@ -299,6 +300,28 @@ vsk_status vsk_ivf_create(vsk_ctx *ctx, const float *centroids, int32_t nlist,
   VSK_API_END(ctx);
 }
 
+vsk_status vsk_ivf_build(vsk_ctx *ctx, const float *centroids, int32_t nlist,
+                         const float *x, const int64_t *ids, int64_t n,
+                         int32_t d, vsk_ivf **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(n >= 0, VSK_ERR_INVALID_ARGUMENT, "row count is negative");
+  vsk_ivf *ivf = nullptr;
+  vsk_status st = vsk_ivf_create(ctx, centroids, nlist, d, &ivf);
+  if (st != VSK_OK) return st;
+  if (n > 0) {
+    st = vsk_ivf_add(ctx, ivf, x, ids, n);
+    if (st != VSK_OK) {
+      // keep the add's message: free does not touch the error state
+      vsk_ivf_free(ctx, ivf);
+      return st;
+    }
+  }
+  *out = ivf;
+  VSK_API_END(ctx);
+}
+
 vsk_status vsk_ivf_free(vsk_ctx *ctx, vsk_ivf *ivf) {
   if (ctx) {
     (void)hipSetDevice(ctx->device);
@@ -425,10 +448,14 @@ vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
 }
 
 vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
-                          int64_t nq, int32_t nprobe, int32_t k,
+                          int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
                           float *out_dist, int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
+  VSK_REQUIRE(metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ,
+              VSK_ERR_UNSUPPORTED,
+              "IVF search ranks by euclidean distance (VSK_METRIC_L2 or "
+              "VSK_METRIC_L2SQ)");
   VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
   VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT,
               "null buffer");
@@ -550,6 +577,7 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
       la.pos_base = pos_base + b0 * np;
       la.seg_off = dseg;
       la.cand = cand;
+      la.squared = metric == VSK_METRIC_L2SQ ? 1 : 0;
       const size_t lds = sizeof(float) * QG * ld;
       KernelTimer t(ctx, "ivf_list_scan", (double)tot);
       if (QG == 16)

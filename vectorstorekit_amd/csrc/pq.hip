@@ -711,6 +711,27 @@ vsk_status vsk_pq_create(vsk_ctx *ctx, const float *codebooks, int32_t M,
   VSK_API_END(ctx);
 }
 
+vsk_status vsk_pq_upload(vsk_ctx *ctx, const float *codebooks,
+                         const uint8_t *codes, int64_t n, int32_t M,
+                         int32_t dsub, vsk_pq **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(n >= 0, VSK_ERR_INVALID_ARGUMENT, "row count is negative");
+  vsk_pq *pq = nullptr;
+  vsk_status st = vsk_pq_create(ctx, codebooks, M, 256, dsub, &pq);
+  if (st != VSK_OK) return st;
+  if (n > 0) {
+    st = vsk_pq_add_codes(ctx, pq, codes, n);
+    if (st != VSK_OK) {
+      vsk_pq_free(ctx, pq);  // keeps the add's message
+      return st;
+    }
+  }
+  *out = pq;
+  VSK_API_END(ctx);
+}
+
 vsk_status vsk_pq_free(vsk_ctx *ctx, vsk_pq *pq) {
   if (ctx) {
     (void)hipSetDevice(ctx->device);

@@ -16,7 +16,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from ._lib import VSKError, as_buffer, out_buffer
-from .engine import Context
+from .engine import Context, metric_code
 
 
 @dataclass
@@ -59,6 +59,26 @@ class IVFIndex:
                                                    c.shape[1], ctypes.byref(h)))
         self.handle = h
         self._centroids = c
+
+    @classmethod
+    def build(cls, ctx: Context, configuration: IVFConfiguration, centroids, vectors,
+              ids=None) -> "IVFIndex":
+        """Trained centroids plus the rows in one call (``vsk_ivf_build``):
+        the same index as ``set_centroids`` followed by ``insert``."""
+        configuration.validate()
+        c = np.ascontiguousarray(centroids, np.float32)
+        if c.shape != (configuration.numberOfCentroids, configuration.dimensions):
+            raise VSKError(-4, f"centroids shape {c.shape}")
+        n = int(vectors.shape[0])
+        xp, xk = as_buffer(vectors, np.float32, (n, configuration.dimensions))
+        ip, ik = (as_buffer(ids, np.int64, (n,)) if ids is not None else (None, None))
+        h = ctypes.c_void_p()
+        ctx.check(ctx.lib.vsk_ivf_build(ctx.handle, c.ctypes.data, c.shape[0], xp, ip, n,
+                                        c.shape[1], ctypes.byref(h)))
+        idx = cls(ctx, configuration)
+        idx.handle = h
+        idx._centroids = c
+        return idx
 
     def train(self, on, iterations: int = 10, seed: int = 0):
         """Lloyd k-means (Clustering/KMeansClustering.swift:48-113): seeded
@@ -116,7 +136,10 @@ class IVFIndex:
                                                   nprobe, op))
         return out
 
-    def search(self, queries, k: int, strategy: str = "approximate", nprobe=None):
+    def search(self, queries, k: int, strategy: str = "approximate", nprobe=None,
+               metric="euclidean"):
+        """Top k by L2 over the probed lists; ``metric`` is "euclidean"
+        (the reference's sqrt distance) or "euclideanSquared"."""
         self._need()
         if strategy == "exact":
             nprobe = self.configuration.numberOfCentroids
@@ -129,7 +152,7 @@ class IVFIndex:
         dp, dist = out_buffer((nq, k), np.float32, q)
         ip, ids = out_buffer((nq, k), np.int64, q)
         self.ctx.check(self.ctx.lib.vsk_ivf_search(self.ctx.handle, self.handle, qp, nq,
-                                                   nprobe, k, dp, ip))
+                                                   nprobe, k, metric_code(metric), dp, ip))
         return dist, ids
 
     def list_sizes(self) -> np.ndarray:

@@ -141,6 +141,27 @@ class ProductQuantizer:
                                         self.dsub, ctypes.byref(h)))
         self.handle = h
 
+    @classmethod
+    def upload(cls, ctx: Context, codebooks, codes) -> "ProductQuantizer":
+        """Trained 8-bit codebooks (M, 256, dsub) and resident codes (n, M)
+        in one call (``vsk_pq_upload``)."""
+        cb = np.ascontiguousarray(codebooks, np.float32)
+        if cb.ndim != 3 or cb.shape[1] != 256:
+            raise VSKError(-4, "codebooks must be (M, 256, dsub)")
+        M, _, dsub = cb.shape
+        n = int(codes.shape[0])
+        cp, ck = as_buffer(codes, np.uint8, (n, M))
+        h = ctypes.c_void_p()
+        ctx.check(ctx.lib.vsk_pq_upload(ctx.handle, cb.ctypes.data, cp, n, M, dsub,
+                                        ctypes.byref(h)))
+        pq = cls.__new__(cls)
+        pq.ctx = ctx
+        pq.M, pq.ksub, pq.dsub = M, 256, dsub
+        pq.d = M * dsub
+        pq.codebooks = cb
+        pq.handle = h
+        return pq
+
     def encode(self, vectors):
         n = int(vectors.shape[0])
         xp, xk = as_buffer(vectors, np.float32, (n, self.d))
