@@ -21,7 +21,7 @@
 // bytes once and accumulates one sum per query; each sum is keyed (sum, row)
 // and goes through the same threshold filter / append as the flat scan.
 // k_pq_adc16 serves M = 16, ksub = 256 (8 queries, tables interleaved four
-// queries to a 16-byte entry, survivors staged in LDS); k_pq_adc any other
+// queries to a 16-byte half entry, survivors staged in LDS); k_pq_adc any other
 // shape.  Ranking is on the sum (sqrt is monotone); sqrt is applied to the
 // outputs only.
 #include "flat.hpp"
@@ -299,17 +299,25 @@ static void launch_adc(vsk_ctx *ctx, AdcArgs a, bool dense) {
 // consecutive slots of one XCD, so they share its L2 for the code rows.
 constexpr int PQ16_QG = 8, PQ16_T = 512;
 typedef float pq_f4 __attribute__((ext_vector_type(4)));
-// the tables (128 KB), then per query: slot limit, slot count, active flag,
-// first slot, threshold key (all in the dynamic block: a static LDS array
-// placed before the tables would leave their alignment unknown)
+// LDS (static, so every table address is known at compile time and its
+// segment offset folds into the read's immediate): the tables as two
+// halves of 16 x 256 entries of 16 bytes, entry (m, c) of half h holding
+// queries 4h..4h+3 of the group (a 16-byte stride keeps random codes spread
+// over all 16 bank quads), then the survivor
+// staging of each wave (key, then slot << 3 | query), then per query: first
+// slot, threshold key, slot limit, slot count, active flag.
 constexpr int PQ16_TAB = 2 * 16 * 256 * 16;
-constexpr int PQ16_STATE = PQ16_QG * (3 * 4 + 2 * 8);
-// filter survivors are staged per wave in LDS (key, then slot << 3 | query)
-// and stored in bulk: a global store between the prefetch loads and their
-// use would make every use wait for all of them (one vector memory counter
-// for loads and stores, which may then complete out of order)
+// filter survivors are staged per wave in LDS and stored in bulk: a global
+// store between the prefetch loads and their use would make every use wait
+// for all of them (one vector memory counter for loads and stores, which
+// may then complete out of order)
 constexpr int PQ16_WBUF = 256;
-constexpr int PQ16_LDS = PQ16_TAB + PQ16_STATE + (PQ16_T / 64) * PQ16_WBUF * 12;
+constexpr int PQ16_WAVES = PQ16_T / 64;
+constexpr int PQ16_KEYS = PQ16_TAB;
+constexpr int PQ16_META = PQ16_KEYS + PQ16_WAVES * PQ16_WBUF * 8;
+constexpr int PQ16_STATE = PQ16_META + PQ16_WAVES * PQ16_WBUF * 4;
+constexpr int PQ16_LDS = PQ16_STATE + PQ16_QG * (3 * 4 + 2 * 8);
+static_assert(PQ16_LDS <= 160 * 1024, "LDS of one workgroup");
 
 struct Adc16Args {
   const uint8_t *codes;
@@ -326,17 +334,14 @@ struct Adc16Args {
 template <bool DENSE>
 __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
 #pragma clang fp contract(off)
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
-  int32_t *s_lim = reinterpret_cast<int32_t *>(lds_raw + PQ16_TAB);
-  int32_t *s_cnt = s_lim + PQ16_QG, *s_ok = s_cnt + PQ16_QG;
-  int64_t *s_pb = reinterpret_cast<int64_t *>(s_ok + PQ16_QG + (PQ16_QG & 1));
-  uint64_t *s_th = reinterpret_cast<uint64_t *>(s_pb + PQ16_QG);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PQ16_LDS];
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-  uint64_t *w_key = reinterpret_cast<uint64_t *>(lds_raw + PQ16_TAB + PQ16_STATE) +
-                    wv * PQ16_WBUF;
-  uint32_t *w_meta = reinterpret_cast<uint32_t *>(
-                         lds_raw + PQ16_TAB + PQ16_STATE + (PQ16_T / 64) * PQ16_WBUF * 8) +
-                     wv * PQ16_WBUF;
+  uint64_t *w_key = reinterpret_cast<uint64_t *>(lds + PQ16_KEYS) + wv * PQ16_WBUF;
+  uint32_t *w_meta = reinterpret_cast<uint32_t *>(lds + PQ16_META) + wv * PQ16_WBUF;
+  int64_t *s_pb = reinterpret_cast<int64_t *>(lds + PQ16_STATE);
+  uint64_t *s_th = reinterpret_cast<uint64_t *>(s_pb + PQ16_QG);
+  int32_t *s_lim = reinterpret_cast<int32_t *>(s_th + PQ16_QG);
+  int32_t *s_cnt = s_lim + PQ16_QG, *s_ok = s_cnt + PQ16_QG;
   const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
   const int qg = slot % a.nqg;
   const int split = (slot / a.nqg) * 8 + xcd;
@@ -346,13 +351,14 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
   if (s1 > a.r1) s1 = a.r1;
   if (s0 >= s1 || q0 >= a.nq) return;
   {
-    float4 *w = reinterpret_cast<float4 *>(lds_raw);
+    // entry e = 4096 h + 256 m + c holds lut[q0 + 4h + 0..3][m][c]
+    float4 *w = reinterpret_cast<float4 *>(lds);
     for (int e = tid; e < 2 * 4096; e += PQ16_T) {
-      const int g = e >> 12, mc = e & 4095;
+      const int h = e >> 12, mc = e & 4095;
       float v[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int64_t q = q0 + 4 * g + jj;
+        const int64_t q = q0 + 4 * h + jj;
         v[jj] = q < a.nq ? a.lut[q * 4096 + mc] : 0.f;
       }
       w[e] = float4{v[0], v[1], v[2], v[3]};
@@ -373,7 +379,9 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
   }
   __syncthreads();
   // threshold of each query as a sum: a row can pass only if its sum is at
-  // most this (NaN sums order last and never pass a finite threshold)
+  // most this (NaN sums fail the compare and are kept for the exact key
+  // test, which orders them last); inactive queries: -inf, so only NaN
+  // sums reach the key test, which then drops them by the flag
   float thf[PQ16_QG];
   uint64_t thk[PQ16_QG];
   bool ok[PQ16_QG];
@@ -383,11 +391,11 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
     thk[j] = th;
     ok[j] = s_ok[j] != 0;
     const uint32_t hi = (uint32_t)(th >> 32);
-    thf[j] = hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000) : vsk_ord2f(hi);
+    thf[j] = !ok[j] ? -__int_as_float(0x7f800000)
+                    : (hi == 0xFFFFFFFFu ? __int_as_float(0x7f800000) : vsk_ord2f(hi));
   }
   // code rows of this split through a buffer descriptor (reads past the
-  // split return 0), prefetched two rows ahead so that the load latency of
-  // the stream hides behind the lookups
+  // split return 0)
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(a.codes + s0 * 16), 0, (int32_t)((s1 - s0) * 16), 0x00020000);
   // block b = rows s0 + 512 b + tid; every lane runs the same number of
@@ -407,6 +415,8 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
     // the stores complete here, so none is pending beside the prefetch loads
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   };
+  uint32_t hi_base = 65536;
+  asm volatile("" : "+s"(hi_base));
   // one row: 32 table reads (16 bytes each, four queries), the eight sums in
   // m order, then the filter or the dense store
   auto row = [&](int b, const uint4 cw) {
@@ -416,11 +426,15 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
     float sa[4] = {0.f, 0.f, 0.f, 0.f}, sb[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-      const int c = (w4[m >> 2] >> (8 * (m & 3))) & 0xFF;
+      const uint32_t c = (w4[m >> 2] >> (8 * (m & 3))) & 0xFFu;
       // (a native 4-vector: one 16-byte read each; the HIP float4 struct is
       // split into scalar loads, some of which come back 4 bytes wide)
-      const pq_f4 va = *reinterpret_cast<const pq_f4 *>(lds_raw + (m * 256 + c) * 16);
-      const pq_f4 vb = *reinterpret_cast<const pq_f4 *>(lds_raw + 65536 + (m * 256 + c) * 16);
+      // the second half lies past the 16-bit immediate offset: its base
+      // comes from a register (one add per code), the segment offsets of
+      // both halves fold into the reads
+      const pq_f4 va = *reinterpret_cast<const pq_f4 *>(lds + m * 4096 + c * 16);
+      const pq_f4 vb =
+          *reinterpret_cast<const pq_f4 *>(lds + hi_base + m * 4096 + c * 16);
       sa[0] = sa[0] + va[0];
       sa[1] = sa[1] + va[1];
       sa[2] = sa[2] + va[2];
@@ -433,11 +447,15 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
     const float sum[PQ16_QG] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
 #pragma unroll
     for (int j = 0; j < PQ16_QG; ++j) {
-      const uint64_t key = vsk_key(sum[j], (uint32_t)r);
       if constexpr (DENSE) {
-        if (ok[j] && valid) a.cand[(q0 + j) * a.cap + (r - a.r0)] = key;
+        if (ok[j] && valid)
+          a.cand[(q0 + j) * a.cap + (r - a.r0)] = vsk_key(sum[j], (uint32_t)r);
       } else {
-        const bool pass = ok[j] && valid && !(sum[j] > thf[j]) && key <= thk[j];
+        // one compare per (row, query) in the common case of no survivor
+        const bool maybe = !(sum[j] > thf[j]);
+        if (!__builtin_amdgcn_ballot_w64(maybe)) continue;
+        const uint64_t key = vsk_key(sum[j], (uint32_t)r);
+        const bool pass = maybe && valid && ok[j] && key <= thk[j];
         const uint64_t mask = __builtin_amdgcn_ballot_w64(pass);
         if (mask == 0) continue;
         if (pass) {
@@ -490,14 +508,6 @@ __global__ __launch_bounds__(PQ16_T) void k_pq_adc16(Adc16Args a) {
 static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
   const int64_t rows = in.r1 - in.r0;
   if (rows <= 0 || in.nq <= 0) return;
-  static bool lds_set = false;
-  if (!lds_set) {
-    VSK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(k_pq_adc16<true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, PQ16_LDS));
-    VSK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(k_pq_adc16<false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, PQ16_LDS));
-    lds_set = true;
-  }
   Adc16Args a;
   a.codes = in.codes;
   a.lut = in.lut;
@@ -538,9 +548,9 @@ static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
   KernelTimer t(ctx, dense ? "pq_adc_dense" : "pq_adc_filter", (double)in.nq * (double)rows);
   if (dense)
-    k_pq_adc16<true><<<(unsigned)nblocks, PQ16_T, PQ16_LDS, ctx->stream>>>(a);
+    k_pq_adc16<true><<<(unsigned)nblocks, PQ16_T, 0, ctx->stream>>>(a);
   else
-    k_pq_adc16<false><<<(unsigned)nblocks, PQ16_T, PQ16_LDS, ctx->stream>>>(a);
+    k_pq_adc16<false><<<(unsigned)nblocks, PQ16_T, 0, ctx->stream>>>(a);
   check_launch("pq_adc16");
 }
 
