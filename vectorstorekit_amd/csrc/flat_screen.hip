@@ -59,10 +59,15 @@ int32_t screen_keep(int32_t k) {
 // candidates of one query (uniform query loads).  Per 64-dim block the wave
 // gathers its 64 rows with 256-byte segments (16 lanes per row) into its own
 // LDS tile, then every lane continues the sequential sum of its row from
-// there: coalesced reads, bit-exact sums.  out[q][c] = key(distance, row)
-// for the first nvalid[q] candidates, NONE for the rest.
+// there: coalesced reads, bit-exact sums.  The 16 segment loads of a block
+// are unconditional (a missing candidate reads row 0, a segment past the
+// row's end is clamped into it; neither is summed), so all of them are in
+// flight at once, and the next block's loads run while this one is summed.
+// out[q][c] = key(distance, row) for the first nvalid[q] candidates, NONE
+// for the rest.
 constexpr int RS_W = 64;       // dims per gathered block
 constexpr int RS_LD = RS_W + 4;  // LDS row stride (floats): conflict-free
+typedef float rs_f4 __attribute__((ext_vector_type(4)));
 
 template <int METRIC>
 __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
@@ -82,22 +87,35 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
   const float *qq = Q + q * ldq;
   float *t = tile[w];
   const int seg = lane & 15, sub = lane >> 4;  // 16 lanes per row segment
+  // the rows this lane gathers: candidates sub, sub + 4, ..., sub + 60
+  const uint32_t my_row = valid ? row : 0u;
+  const float *src[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    src[i] = X + (int64_t)__shfl(my_row, sub + 4 * i) * ldx;
+  const int32_t cmax = (int32_t)ldx - 4;  // a segment past the row end is clamped
+  rs_f4 buf[16];
+  {
+    const int32_t col = 4 * seg < cmax ? 4 * seg : cmax;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) buf[i] = *reinterpret_cast<const rs_f4 *>(src[i] + col);
+  }
   float s = 0.f;
   for (int32_t j0 = 0; j0 < d; j0 += RS_W) {
-    // gather: rows sub, sub+4, ..., 4 per instruction
-#pragma unroll 4
-    for (int r = sub; r < 64; r += 4) {
-      const uint64_t kr = __shfl(key, r);
-      const bool ok = kr != VSK_KEY_NONE && j0 + 4 * seg < d;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (ok)
-        v = *reinterpret_cast<const float4 *>(X + (int64_t)(uint32_t)kr * ldx + j0 +
-                                              4 * seg);
-      *reinterpret_cast<float4 *>(t + r * RS_LD + 4 * seg) = v;
-    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      *reinterpret_cast<rs_f4 *>(t + (sub + 4 * i) * RS_LD + 4 * seg) = buf[i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
+      // the next block (the last one reloads itself: no condition on the
+      // loads)
+      const int32_t jnext = j0 + RS_W < d ? j0 + RS_W : j0;
+      const int32_t col = jnext + 4 * seg < cmax ? jnext + 4 * seg : cmax;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) buf[i] = *reinterpret_cast<const rs_f4 *>(src[i] + col);
+    }
     const int32_t jn = d - j0 < RS_W ? d - j0 : RS_W;
     const float *xr = t + lane * RS_LD;
     for (int32_t j = 0; j < jn; ++j) {

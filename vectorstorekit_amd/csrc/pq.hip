@@ -561,6 +561,7 @@ static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
 // every lane continues the sequential sums of its own row from there.
 constexpr int RR_W = 64;         // dimensions per gathered block
 constexpr int RR_LD = RR_W + 4;  // LDS row stride (floats)
+typedef float rr_f4 __attribute__((ext_vector_type(4)));
 
 template <int METRIC>
 __global__ __launch_bounds__(256) void k_rerank(const uint64_t *adc_best, int32_t kadc,
@@ -583,27 +584,51 @@ __global__ __launch_bounds__(256) void k_rerank(const uint64_t *adc_best, int32_
   float *t = tile[w];
   const int seg = lane & 15, sub = lane >> 4;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f;  // the metric's sums (cosine: q.x, q.q, x.x)
-  for (int32_t j0 = 0; j0 < d; j0 += RR_W) {
-    const bool cin = j0 + 4 * seg < d;
-#pragma unroll 4
-    for (int r = sub; r < 64; r += 4) {
-      const uint64_t kr = __shfl(key, r);
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (kr != VSK_KEY_NONE && cin)
-        v = *reinterpret_cast<const float4 *>(x + (int64_t)(uint32_t)kr * ldx + j0 + 4 * seg);
-      *reinterpret_cast<float4 *>(t + r * RR_LD + 4 * seg) = v;
+  // the rows this lane gathers: candidates sub, sub + 4, ..., sub + 60 (a
+  // missing candidate reads row 0, a segment past the row end is clamped
+  // into it; neither is summed).  All loads are unconditional, so the 16
+  // row segments and the query values of a block are in flight together,
+  // and the next block's loads run while this one is summed.
+  const uint32_t my_row = valid ? row : 0u;
+  const float *src[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) src[i] = x + (int64_t)__shfl(my_row, sub + 4 * i) * ldx;
+  const int32_t cmax = ldx - 4;
+  rr_f4 buf[16];
+  float qb[4];  // query values of the block (rows have stride d, not padded)
+  {
+    const int32_t col = 4 * seg < cmax ? 4 * seg : cmax;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) buf[i] = *reinterpret_cast<const rr_f4 *>(src[i] + col);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int32_t qc = 4 * seg + e;
+      qb[e] = qr[qc < d ? qc : d - 1];
     }
-    // (query rows have stride d, not padded: four single reads, bounded)
+  }
+  for (int32_t j0 = 0; j0 < d; j0 += RR_W) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      *reinterpret_cast<rr_f4 *>(t + (sub + 4 * i) * RR_LD + 4 * seg) = buf[i];
     if (sub == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t col = j0 + 4 * seg + e;
-        t[64 * RR_LD + 4 * seg + e] = col < d ? qr[col] : 0.f;
-      }
+      for (int e = 0; e < 4; ++e) t[64 * RR_LD + 4 * seg + e] = qb[e];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
+      // the next block (the last one reloads itself)
+      const int32_t jnext = j0 + RR_W < d ? j0 + RR_W : j0;
+      const int32_t col = jnext + 4 * seg < cmax ? jnext + 4 * seg : cmax;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) buf[i] = *reinterpret_cast<const rr_f4 *>(src[i] + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t qc = jnext + 4 * seg + e;
+        qb[e] = qr[qc < d ? qc : d - 1];
+      }
+    }
     const int32_t jn = d - j0 < RR_W ? d - j0 : RR_W;
     const float *xr = t + lane * RR_LD, *qv = t + 64 * RR_LD;
     for (int32_t j = 0; j < jn; ++j) {
