@@ -243,6 +243,40 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
                          int32_t rerank_metric, const vsk_db *rerank_db,
                          float *out_dist, int64_t *out_ids);
 
+/* ---- k-means -------------------------------------------------------------
+ * KMeansClustering.cluster (Clustering/KMeansClustering.swift:48-113), the
+ * trainer behind IVFIndex.train (Indexes/IVFIndex.swift:397-446) and
+ * ProductQuantizer's codebooks (Quantization/ProductQuantizer.swift:270-324).
+ * Each iteration assigns every row to its nearest centroid (sqrt-L2 summed in
+ * dimension order, strict '<', :271-295), replaces each centroid by the fp32
+ * mean of its rows summed in row order (x * weight, counts += weight,
+ * :342-380), and stops when |inertia - previous| < tolerance, inertia being
+ * the fp32 sum of the assigned distances in row order (:97-98).  An empty
+ * cluster takes row Int.random(in: 0..<n) of SeedableRNG(seed +
+ * 0x9E3779B97F4A7C15) (:374 draws it unseeded). */
+#define VSK_KMEANS_INIT_RANDOM 0    /* .random: first k of shuffled rows (:197-207) */
+#define VSK_KMEANS_INIT_CUSTOM 1    /* .custom(centroids) (:189-193)              */
+#define VSK_KMEANS_INIT_PLUSPLUS 2  /* .kMeansPlusPlus (:209-259), D^2 sampling     */
+
+/* ClusteringResult (:9-29) without the arrays */
+typedef struct {
+  int32_t iterations;
+  int32_t converged;
+  float inertia; /* +inf when no iteration ran */
+} vsk_kmeans_result;
+
+/* x: n x d rows; weights: n or NULL; init_centroids: k x d for
+ * VSK_KMEANS_INIT_CUSTOM (else ignored); out_centroids: k x d;
+ * out_assign: n or NULL (the last assignment step; zeros when max_iter = 0).
+ * Errors as ClusteringError (:453-478): n = 0 -> VSK_ERR_EMPTY_INPUT,
+ * k outside 1..n -> VSK_ERR_INVALID_ARGUMENT, degenerate data for
+ * k-means++ -> VSK_ERR_INVALID_ARGUMENT. */
+vsk_status vsk_kmeans(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                      int32_t k, const float *weights, int32_t init_method,
+                      const float *init_centroids, uint64_t seed,
+                      int32_t max_iter, float tolerance, float *out_centroids,
+                      int32_t *out_assign, vsk_kmeans_result *result);
+
 #ifdef __cplusplus
 }
 #endif

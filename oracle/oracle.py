@@ -59,6 +59,13 @@ def lib():
             "vsko_pq_search": (None, [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32,
                                       c_int32, c_int32, P, c_int32, P, P, c_int32]),
             "vsko_kmeans": (None, [P, c_int64, c_int32, c_int32, c_int32, c_uint64, P, c_int32]),
+            "vsko_swift_bounded": (c_uint64, [P, c_uint64]),
+            "vsko_kmeans_init_random": (None, [c_int64, c_int32, c_uint64, P]),
+            "vsko_kmeans_init_plusplus": (c_int32, [P, c_int64, c_int32, c_int32, c_uint64, P,
+                                                    c_int32]),
+            "vsko_kmeans_cluster": (c_int32, [P, c_int64, c_int32, c_int32, c_int32, P, P,
+                                              c_int32, c_float, c_uint64, P, P, P, P, P,
+                                              c_int32]),
             "vsko_num_threads": (c_int32, []),
         }
         for name, (res, args) in sig.items():
@@ -240,3 +247,53 @@ def kmeans(x, k, iters=10, seed=0, threads=0):
     out = np.empty((k, x.shape[1]), np.float32)
     lib().vsko_kmeans(xp, x.shape[0], x.shape[1], k, iters, seed, out.ctypes.data, threads)
     return out
+
+
+def swift_bounded(state: int, bound: int):
+    """Int.random(in: 0..<bound) on SeedableRNG(state): (value, new state)."""
+    st = c_uint64(state)
+    v = lib().vsko_swift_bounded(ctypes.byref(st), bound)
+    return int(v), int(st.value)
+
+
+def kmeans_init_random(n, k, seed):
+    rows = np.empty(k, np.int64)
+    lib().vsko_kmeans_init_random(n, k, seed, rows.ctypes.data)
+    return rows
+
+
+def kmeans_init_plusplus(x, k, seed, threads=0):
+    """k-means++ starting rows, or None on degenerate data."""
+    x, xp = _c(x, np.float32)
+    rows = np.empty(k, np.int64)
+    rc = lib().vsko_kmeans_init_plusplus(xp, x.shape[0], x.shape[1], k, seed, rows.ctypes.data,
+                                         threads)
+    return None if rc != 0 else rows
+
+
+INIT_METHODS = {"random": 0, "custom": 1, "kMeansPlusPlus": 2}
+
+
+def kmeans_cluster(x, k, init_method="random", init=None, weights=None, max_iter=100,
+                   tol=1e-4, seed=0, threads=0):
+    """KMeansClustering.cluster restated: (centroids, assignments, iterations,
+    converged, inertia); raises ValueError on degenerate data."""
+    x, xp = _c(x, np.float32)
+    n, d = x.shape
+    ip = wp = None
+    if init is not None:
+        init, ip = _c(init, np.float32)
+    if weights is not None:
+        weights, wp = _c(weights, np.float32)
+    cent = np.empty((k, d), np.float32)
+    assign = np.empty(n, np.int32)
+    it = c_int32(0)
+    conv = c_int32(0)
+    inertia = c_float(0)
+    rc = lib().vsko_kmeans_cluster(xp, n, d, k, INIT_METHODS[init_method], ip, wp, max_iter,
+                                   tol, seed, cent.ctypes.data, assign.ctypes.data,
+                                   ctypes.byref(it), ctypes.byref(conv), ctypes.byref(inertia),
+                                   threads)
+    if rc != 0:
+        raise ValueError("degenerate data")
+    return cent, assign, int(it.value), bool(conv.value), np.float32(inertia.value)

@@ -769,3 +769,234 @@ void vsko_kmeans(const float *x, int64_t n, int32_t d, int32_t k,
   free(sum);
   free(assign);
 }
+
+/* ------------------------------------------------------------------------ */
+/* KMeansClustering.cluster restated (Clustering/KMeansClustering.swift)      */
+/* ------------------------------------------------------------------------ */
+
+/* SeedableRNG.next (Clustering/KMeansClustering.swift:480-491): a 64-bit
+ * LCG, state = state * 2862933555777941757 + 3037000493, returns state. */
+static uint64_t swift_lcg(uint64_t *s) {
+  *s = *s * 2862933555777941757ull + 3037000493ull;
+  return *s;
+}
+/* Swift stdlib RandomNumberGenerator.next(upperBound:) for UInt64: Lemire's
+ * nearly-divisionless method (arXiv:1805.10941), which Int.random(in: 0..<n,
+ * using:) calls with upperBound n. */
+uint64_t vsko_swift_bounded(uint64_t *state, uint64_t bound) {
+  uint64_t r = swift_lcg(state);
+  unsigned __int128 m = (unsigned __int128)r * bound;
+  if ((uint64_t)m < bound) {
+    uint64_t t = (0 - bound) % bound;
+    while ((uint64_t)m < t) {
+      r = swift_lcg(state);
+      m = (unsigned __int128)r * bound;
+    }
+  }
+  return (uint64_t)(m >> 64);
+}
+
+/* initializeRandom (Clustering/KMeansClustering.swift:197-207): the first k
+ * of vectors.indices.shuffled(using: SeedableRNG(seed)).  Swift's
+ * MutableCollection.shuffle(using:) is Fisher-Yates from the front: step i
+ * swaps element i with element i + Int.random(in: 0..<(n - i)); element i
+ * is final after step i, so k steps give the prefix. */
+void vsko_kmeans_init_random(int64_t n, int32_t k, uint64_t seed,
+                             int64_t *rows) {
+  int64_t *perm = (int64_t *)malloc(sizeof(int64_t) * n);
+  for (int64_t i = 0; i < n; ++i) perm[i] = i;
+  uint64_t st = seed;
+  for (int64_t i = 0; i < k && i < n - 1; ++i) {
+    int64_t j = i + (int64_t)vsko_swift_bounded(&st, (uint64_t)(n - i));
+    int64_t t = perm[i];
+    perm[i] = perm[j];
+    perm[j] = t;
+  }
+  for (int32_t c = 0; c < k; ++c) rows[c] = perm[c];
+  free(perm);
+}
+
+/* euclideanDistance (Clustering/KMeansClustering.swift:421-428):
+ * sqrt of the sequential, unfused sum of squared differences */
+static float km_l2(const float *a, const float *b, int32_t d) {
+  return sqrtf(vsko_l2sq(a, b, d));
+}
+
+typedef struct {
+  const float *x, *c;
+  int32_t d, k;
+  int32_t *assign;
+  float *dist;
+} kmc_ctx;
+/* assignWithCPU (:271-295): strict '<' over the centroids in order, the
+ * first minimum wins; minDistance starts at +inf with index 0 */
+static void kmc_assign_range(void *p, int64_t lo, int64_t hi) {
+  kmc_ctx *a = (kmc_ctx *)p;
+  for (int64_t i = lo; i < hi; ++i) {
+    float best = INFINITY;
+    int32_t bi = 0;
+    for (int32_t c = 0; c < a->k; ++c) {
+      float v = km_l2(a->x + i * a->d, a->c + (int64_t)c * a->d, a->d);
+      if (v < best) {
+        best = v;
+        bi = c;
+      }
+    }
+    a->assign[i] = bi;
+    a->dist[i] = best;
+  }
+}
+
+/* k-means++ seeding (initializeKMeansPlusPlus, :209-259) with the D^2
+ * weighting the method defines: the reference's weights D^2 / sum(D) (:237)
+ * do not sum to one, and are not reproduced.  First row:
+ * Int.random(in: 0..<n) on SeedableRNG(seed) (:214-218).  Pick r + 1: D(x)
+ * = min over picked rows of the sqrt-L2 (computeMinDistances, :401-419),
+ * weight = floor(D^2 / max D^2 * 2^32) (an exact integer, so the total does
+ * not depend on a summation order), u = Int.random(in: 0..<total) drawn
+ * from the same SeedableRNG stream, and the pick is the first row whose
+ * running weight sum exceeds u.  (The reference reseeds every pick with
+ * seed + picks so far, :241; an LCG's first output is affine in its seed, so
+ * those draws are correlated from pick to pick, and one stream serves all
+ * picks here.)  Returns -1 when every weight is zero (degenerateData,
+ * :235-237), else 0. */
+static uint64_t kpp_fixed(float dm, float maxw) {
+  if (!(maxw > 0.0f)) return 0;
+  const float w = dm * dm;
+  return (uint64_t)((double)w / (double)maxw * 4294967296.0);
+}
+typedef struct {
+  const float *x, *c;
+  int32_t d;
+  float *D;
+} kpp_ctx;
+static void kpp_update_range(void *p, int64_t lo, int64_t hi) {
+  kpp_ctx *a = (kpp_ctx *)p;
+  for (int64_t i = lo; i < hi; ++i) {
+    const float dist = km_l2(a->x + i * a->d, a->c, a->d);
+    if (dist < a->D[i]) a->D[i] = dist;
+  }
+}
+int32_t vsko_kmeans_init_plusplus(const float *x, int64_t n, int32_t d,
+                                  int32_t k, uint64_t seed, int64_t *rows,
+                                  int32_t nthreads) {
+  float *D = (float *)malloc(sizeof(float) * n);
+  for (int64_t i = 0; i < n; ++i) D[i] = INFINITY;
+  uint64_t st = seed;
+  rows[0] = (int64_t)vsko_swift_bounded(&st, (uint64_t)n);
+  int32_t rc = 0;
+  for (int32_t r = 0; r + 1 < k; ++r) {
+    kpp_ctx a = {x, x + rows[r] * d, d, D};
+    parallel_for(n, nthreads, kpp_update_range, &a);
+    float maxw = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+      const float w = D[i] * D[i];
+      if (w > maxw) maxw = w;
+    }
+    uint64_t total = 0;
+    for (int64_t i = 0; i < n; ++i) total += kpp_fixed(D[i], maxw);
+    if (total == 0) {
+      rc = -1;
+      break;
+    }
+    const uint64_t u = vsko_swift_bounded(&st, total);
+    uint64_t cum = 0;
+    int64_t pick = -1;
+    for (int64_t i = 0; i < n; ++i) {
+      const uint64_t f = kpp_fixed(D[i], maxw);
+      if (f > 0 && u < cum + f) {
+        pick = i;
+        break;
+      }
+      cum += f;
+    }
+    rows[r + 1] = pick;
+  }
+  free(D);
+  return rc;
+}
+
+/* KMeansClustering.cluster (:48-113) with the update step of :342-380.
+ * Per iteration: assignment; fp32 sums in row order
+ * (newCentroids[a][j] += x[i][j] * w, counts[a] += w, w = 1 without
+ * weights); means by fp32 division; inertia = the fp32 sum of the assigned
+ * distances in row order; converged = |inertia - previous| < tol (previous
+ * starts at +inf).  An empty cluster takes row Int.random(in: 0..<n) of a
+ * SeedableRNG seeded with seed + 0x9E3779B97F4A7C15, drawn in ascending
+ * cluster order (the reference draws it from the unseeded system generator,
+ * :374, which no run can reproduce).  init_method: 0 initializeRandom with
+ * seed, 1 init = k x d starting centroids (.custom), 2 k-means++ as above
+ * (returns -1 on degenerate data).  Outputs the
+ * centroids after the last update, the assignments and inertia of the last
+ * assignment step, the iteration count and the converged flag, as
+ * ClusteringResult (:9-29). */
+int32_t vsko_kmeans_cluster(const float *x, int64_t n, int32_t d, int32_t k,
+                            int32_t init_method, const float *init,
+                            const float *weights, int32_t max_iter, float tol,
+                            uint64_t seed, float *centroids, int32_t *assign,
+                            int32_t *iters_out, int32_t *converged_out,
+                            float *inertia_out, int32_t nthreads) {
+  float *cur = (float *)malloc(sizeof(float) * (size_t)k * d);
+  if (init_method == 1) {
+    memcpy(cur, init, sizeof(float) * (size_t)k * d);
+  } else {
+    int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * k);
+    if (init_method == 2) {
+      if (vsko_kmeans_init_plusplus(x, n, d, k, seed, rows, nthreads) != 0) {
+        free(rows);
+        free(cur);
+        return -1;
+      }
+    } else {
+      vsko_kmeans_init_random(n, k, seed, rows);
+    }
+    for (int32_t c = 0; c < k; ++c)
+      memcpy(cur + (int64_t)c * d, x + rows[c] * d, sizeof(float) * d);
+    free(rows);
+  }
+  int32_t *a = (int32_t *)calloc((size_t)n, sizeof(int32_t));
+  float *dist = (float *)malloc(sizeof(float) * n);
+  float *sums = (float *)malloc(sizeof(float) * (size_t)k * d);
+  float *cnt = (float *)malloc(sizeof(float) * k);
+  uint64_t empty_rng = seed + 0x9E3779B97F4A7C15ull;
+  float prev = INFINITY, inertia = INFINITY;
+  int32_t it = 0, conv = 0;
+  while (it < max_iter && !conv) {
+    kmc_ctx ac = {x, cur, d, k, a, dist};
+    parallel_for(n, nthreads, kmc_assign_range, &ac);
+    memset(sums, 0, sizeof(float) * (size_t)k * d);
+    memset(cnt, 0, sizeof(float) * k);
+    for (int64_t i = 0; i < n; ++i) {
+      const float w = weights ? weights[i] : 1.0f;
+      float *s = sums + (int64_t)a[i] * d;
+      for (int32_t j = 0; j < d; ++j) s[j] += x[i * d + j] * w;
+      cnt[a[i]] += w;
+    }
+    for (int32_t c = 0; c < k; ++c) {
+      float *s = sums + (int64_t)c * d;
+      if (cnt[c] > 0) {
+        for (int32_t j = 0; j < d; ++j) s[j] /= cnt[c];
+      } else {
+        int64_t r = (int64_t)vsko_swift_bounded(&empty_rng, (uint64_t)n);
+        memcpy(s, x + r * d, sizeof(float) * d);
+      }
+    }
+    inertia = 0.0f;
+    for (int64_t i = 0; i < n; ++i) inertia += dist[i];
+    conv = fabsf(inertia - prev) < tol;
+    memcpy(cur, sums, sizeof(float) * (size_t)k * d);
+    prev = inertia;
+    ++it;
+  }
+  memcpy(centroids, cur, sizeof(float) * (size_t)k * d);
+  if (assign) memcpy(assign, a, sizeof(int32_t) * n);
+  *iters_out = it;
+  *converged_out = conv;
+  *inertia_out = it > 0 ? prev : INFINITY;
+  free(cnt);
+  free(sums);
+  free(dist);
+  free(a);
+  free(cur);
+  return 0;
+}

@@ -116,6 +116,28 @@ void vsko_kmeans(const float *x, int64_t n, int32_t d, int32_t k,
                  int32_t iters, uint64_t seed, float *centroids,
                  int32_t nthreads);
 
+/* ---- KMeansClustering.cluster (Clustering/KMeansClustering.swift:48-113) */
+/* Int.random(in: 0..<bound, using: &SeedableRNG): Swift's Lemire bounded
+ * draw on the reference's LCG; state is advanced in place */
+uint64_t vsko_swift_bounded(uint64_t *state, uint64_t bound);
+/* initializeRandom: rows[k] = the first k of (0..<n).shuffled(seed) */
+void vsko_kmeans_init_random(int64_t n, int32_t k, uint64_t seed,
+                             int64_t *rows);
+/* k-means++ rows[k] with exact fixed-point D^2 weights; -1 = degenerate */
+int32_t vsko_kmeans_init_plusplus(const float *x, int64_t n, int32_t d,
+                                  int32_t k, uint64_t seed, int64_t *rows,
+                                  int32_t nthreads);
+/* Lloyd loop as the reference runs it (fp32 row-order sums, fp32 means,
+ * fp32 sequential inertia, |inertia - previous| < tol); init_method 0
+ * random, 1 custom (init = k x d), 2 k-means++; weights may be NULL; assign
+ * may be NULL.  Returns -1 on degenerate data (k-means++), else 0. */
+int32_t vsko_kmeans_cluster(const float *x, int64_t n, int32_t d, int32_t k,
+                            int32_t init_method, const float *init,
+                            const float *weights, int32_t max_iter, float tol,
+                            uint64_t seed, float *centroids, int32_t *assign,
+                            int32_t *iters_out, int32_t *converged_out,
+                            float *inertia_out, int32_t nthreads);
+
 int32_t vsko_num_threads(void);
 
 #ifdef __cplusplus

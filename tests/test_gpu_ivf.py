@@ -9,7 +9,8 @@ import pytest
 
 from oracle import oracle as O
 from parity import assert_sorted_unique, recall
-from vectorstorekit_amd import IVFConfiguration, IVFIndex, VSKError
+from vectorstorekit_amd import (IVFConfiguration, IVFIndex, KMeansClusteringConfiguration,
+                                VSKError)
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
@@ -125,11 +126,13 @@ def test_ivf_reference_kats(ctx):
 
 def test_ivf_train_and_errors(ctx):
     x, q, c = _mixture(11, 8, 2000, 16, 5)
-    idx = IVFIndex(ctx, IVFConfiguration(dimensions=16, numberOfCentroids=8, numberOfProbes=2))
+    cfg = KMeansClusteringConfiguration(maxIterations=5, initMethod="random", seed=0)
+    idx = IVFIndex(ctx, IVFConfiguration(dimensions=16, numberOfCentroids=8, numberOfProbes=2,
+                                         clusteringConfig=cfg))
     with pytest.raises(VSKError) as e:
         idx.search(q, 3)
     assert e.value.kind == "notTrained"
-    idx.train(x, iterations=5)
+    idx.train(x)
     idx.insert(x)
     d, i = idx.search(q, 5, strategy="exact")
     fd, fi = O.search_flat(q, x, 5, O.L2)

@@ -145,26 +145,6 @@ def test_pq_encode_codebook_layouts(ctx, shape):
     np.testing.assert_array_equal(pq.encode(x), O.pq_encode(x, cb))
 
 
-def test_pq_train_on_gpu(ctx):
-    """ProductQuantizer.train: per-segment Lloyd k-means with GPU assignment;
-    the codebooks equal the oracle's k-means restarted from the same seeded
-    rows (same assignment rule, float64 means)."""
-    x, q, _ = _pq_data(3, 4000, 32, 4, 16, 2)
-    pq = ProductQuantizer.train(ctx, x, 4, 16, iterations=3, seed=5)
-    assert pq.codebooks.shape == (4, 16, 8)
-    for m in range(4):
-        seg = x[:, m * 8:(m + 1) * 8]
-        rng = np.random.default_rng(5 + m)
-        cent = seg[rng.choice(seg.shape[0], 16, replace=False)].copy()
-        for _ in range(3):
-            a = O.ivf_assign(seg, cent)
-            for c in range(16):
-                rows = seg[a == c]
-                if len(rows):
-                    cent[c] = rows.astype(np.float64).mean(axis=0).astype(np.float32)
-        np.testing.assert_allclose(pq.codebooks[m], cent, rtol=1e-6, atol=1e-6)
-
-
 @pytest.mark.parametrize("metric", [METRIC_L1, METRIC_L2, METRIC_L2SQ, METRIC_COSINE])
 def test_pq_rerank_bit_exact(ctx, metric):
     x, q, cb = _pq_data(5, 30_000, 64, 8, 256, 20)

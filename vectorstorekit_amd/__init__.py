@@ -12,5 +12,10 @@ from .engine import (  # noqa: F401
     HIPAcceleratorStrategy,
     VectorDatabase,
 )
+from .clustering import (  # noqa: F401,E402
+    ClusteringResult,
+    KMeansClustering,
+    KMeansClusteringConfiguration,
+)
 from .ivf import IVFConfiguration, IVFIndex  # noqa: F401,E402
 from .quantization import ProductQuantizer, ScalarQuantizer, SQ8Database  # noqa: F401,E402

@@ -112,6 +112,8 @@ SIGNATURES = {
     "vsk_pq_add_codes": (c_int32, [P, P, P, c_int64]),
     "vsk_pq_lut": (c_int32, [P, P, P, c_int64, P]),
     "vsk_pq_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P, P]),
+    "vsk_kmeans": (c_int32, [P, P, c_int64, c_int32, c_int32, P, c_int32, P, ctypes.c_uint64,
+                             c_int32, c_float, P, P, P]),
 }
 
 _lib = None

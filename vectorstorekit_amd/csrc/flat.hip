@@ -181,7 +181,8 @@ __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
 // (tid) owns rows (tid%32)+32u, u<4, and queries (tid/32)+8v, v<8.
 // MODE_ARGMIN keeps, per query, the smallest (distance, row) key over all
 // rows, i.e. the first minimum under strict '<' (findNearestCentroid,
-// Indexes/IVFIndex.swift:514-527), and writes the row index to argmin[q].
+// Indexes/IVFIndex.swift:514-527), and writes the row index to argmin[q]
+// (and its distance to a.amin[q] when a.amin is set).
 constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
 // sequential (dimension-order, no FMA) terms and final transforms of the
 // exact VALU kernel, one per metric of the CPU reference
@@ -315,7 +316,10 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
         uint64_t o = shfl_xor_u64(b, m);
         b = o < b ? o : b;
       }
-      if (rsub == 0 && qok[v]) argmin[qi[v]] = (int32_t)(uint32_t)b;
+      if (rsub == 0 && qok[v]) {
+        argmin[qi[v]] = (int32_t)(uint32_t)b;
+        if (a.amin) a.amin[qi[v]] = vsk_ord2f((uint32_t)(b >> 32));
+      }
     }
   }
 }

@@ -54,6 +54,8 @@ struct FlatArgs {
   // screen kernel, filter mode: segmented lists (segment = row split, at
   // q*cap + split*sub) with their key counts here (nq x nseg), else null
   int32_t *seg_n;
+  // MODE_ARGMIN: the winning distance per query (optional)
+  float *amin;
 };
 
 // bf16 hi/lo operand planes of the bf16x3 kernel

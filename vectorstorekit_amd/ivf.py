@@ -11,11 +11,12 @@ strategy)`` (:124-202; ``"exact"`` probes every list, :551-554),
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
 from ._lib import VSKError, as_buffer, out_buffer
+from .clustering import ClusteringResult, KMeansClustering, KMeansClusteringConfiguration
 from .engine import Context, metric_code
 
 
@@ -24,6 +25,10 @@ class IVFConfiguration:
     dimensions: int
     numberOfCentroids: int = 1024
     numberOfProbes: int = 10
+    # the k-means that train(on:) runs (IVFConfiguration.clusteringConfig,
+    # Config/Indexes/IVFConfiguration.swift:14,35; default .default)
+    clusteringConfig: KMeansClusteringConfiguration = field(
+        default_factory=KMeansClusteringConfiguration)
 
     def validate(self):
         if self.dimensions <= 0:
@@ -80,28 +85,18 @@ class IVFIndex:
         idx._centroids = c
         return idx
 
-    def train(self, on, iterations: int = 10, seed: int = 0):
-        """Lloyd k-means (Clustering/KMeansClustering.swift:48-113): seeded
-        sample of distinct rows as the start, assignment on the GPU with the
-        reference's strict-'<' nearest-centroid rule, mean update."""
-        x = np.ascontiguousarray(on, np.float32)
+    def train(self, on) -> ClusteringResult:
+        """IVFIndex.train(on:) (Indexes/IVFIndex.swift:397-446, .kmeans): k-means
+        with configuration.clusteringConfig on the GPU (vsk_kmeans), the
+        centroids adopted, the lists emptied."""
         k = self.configuration.numberOfCentroids
-        if x.shape[0] < k:
-            raise VSKError(-2, f"insufficient training data: {x.shape[0]} < {k}")
-        rng = np.random.default_rng(seed)
-        cent = x[rng.choice(x.shape[0], k, replace=False)].copy()
-        for _ in range(iterations):
-            self.set_centroids(cent)
-            a = np.asarray(self.assign(x))
-            # per-cluster sums in row order: stable sort by cluster, then one
-            # float64 reduction per contiguous segment
-            order = np.argsort(a, kind="stable")
-            cnt = np.bincount(a, minlength=k)
-            start = np.concatenate(([0], np.cumsum(cnt)[:-1]))
-            nz = cnt > 0
-            sums = np.add.reduceat(x[order].astype(np.float64), start[nz], axis=0)
-            cent[nz] = (sums / cnt[nz, None]).astype(np.float32)
-        self.set_centroids(cent)
+        if on.shape[0] < k:
+            raise VSKError(-2, f"insufficient training data: provided {on.shape[0]}, "
+                           f"required {k}")
+        res = KMeansClustering(self.ctx, self.configuration.clusteringConfig).cluster(on, k)
+        cent = res.centroids
+        self.set_centroids(cent.cpu().numpy() if hasattr(cent, "cpu") else cent)
+        return res
 
     def getCentroids(self) -> np.ndarray:
         self._need()

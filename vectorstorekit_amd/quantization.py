@@ -102,13 +102,16 @@ class ProductQuantizer:
     """PQ with trained codebooks (M, ksub, dsub) and resident codes."""
 
     @classmethod
-    def train(cls, ctx: Context, vectors, M: int, ksub: int = 256, iterations: int = 10,
-              seed: int = 0) -> "ProductQuantizer":
+    def train(cls, ctx: Context, vectors, M: int, ksub: int = 256, iterations: int = 25,
+              seed: int = 0, initMethod: str = "kMeansPlusPlus") -> "ProductQuantizer":
         """ProductQuantizer.train (Quantization/ProductQuantizer.swift:34-64):
-        per segment, Lloyd k-means (Clustering/KMeansClustering.swift:48-113)
-        from a seeded sample of distinct rows; nearest-codeword assignment
-        runs on the GPU (strict '<', first minimum), means on the host."""
-        from .ivf import IVFConfiguration, IVFIndex
+        per segment m, trainSegmentCodebook (:270-324) -- k-means with
+        maxIterations = iterations (config.trainingIterations), tolerance
+        1e-4, k-means++ seeded with the segment index (seed + m here; seed 0
+        is the reference's) -- run on the GPU by vsk_kmeans.  The reference
+        switches to unseeded mini-batch k-means above 10,000 rows (:287-293);
+        full Lloyd iterations are run at every size here."""
+        from .clustering import KMeansClustering, KMeansClusteringConfiguration
 
         x = np.asarray(vectors.cpu().numpy() if _lib._is_torch(vectors) else vectors,
                        np.float32)
@@ -121,11 +124,9 @@ class ProductQuantizer:
         books = np.empty((M, ksub, dsub), np.float32)
         for m in range(M):
             seg = np.ascontiguousarray(x[:, m * dsub:(m + 1) * dsub])
-            km = IVFIndex(ctx, IVFConfiguration(dimensions=dsub, numberOfCentroids=ksub,
-                                                numberOfProbes=1))
-            km.train(seg, iterations=iterations, seed=seed + m)
-            books[m] = km.getCentroids()
-            km.free()
+            cfg = KMeansClusteringConfiguration(maxIterations=iterations, tolerance=1e-4,
+                                                initMethod=initMethod, seed=seed + m)
+            books[m] = KMeansClustering(ctx, cfg).cluster(seg, ksub).centroids
         return cls(ctx, books)
 
     def __init__(self, ctx: Context, codebooks):
