@@ -13,7 +13,10 @@ The other BASELINE configs are measured with ``--config``:
   nprobe 32, 10,000 queries, k = 10 (one step = one vsk_ivf_search);
 * ``c4`` int8 SQ scan, 10M x 128 codes, 1,000 queries, k = 100;
 * ``c5`` PQ M=16 x 256 ADC over 10M codes, top-1000, exact L1 re-rank to
-  k = 100 (one step = one vsk_pq_search).
+  k = 100 (one step = one vsk_pq_search);
+* ``c3train`` IVF coarse training on config 3's data: k-means of 1M x 128
+  rows into 4,096 clusters, 10 Lloyd iterations per step (vsk_kmeans),
+  reported as row-iterations/s.
 
 Each prints one JSON line: QPS (value), the roofline of the dominant kernel
 (algorithmic FLOP/OP or bytes per (query, row) pair the library counted for
@@ -44,7 +47,8 @@ PEAK_INT8_MFMA_TOPS = 5000.0  # MI355X dense int8 matrix, datasheet
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
 PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 
-DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1)}
+DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
+                 "c3train": (2, 1)}
 
 
 def parse():
@@ -216,6 +220,62 @@ def setup(a, ctx, dev):
                         ("flat_mfma_filter", "k_flat_mfma<FILTER>", "mfma32"),
                         ("flat_mfma_dense", "k_flat_mfma<DENSE>", "mfma32")],
             "keep": (db, x, q, dist, ids),
+        }
+        return spec, step, cpu_leg
+
+    if c == "c3train":
+        # IVF coarse training at config 3's scale: one step = one vsk_kmeans
+        # call, 10 Lloyd iterations (tolerance 0 never stops early) from 4,096
+        # seeded random rows
+        from vectorstorekit_amd.clustering import (INIT_RANDOM, vsk_kmeans_result)
+        n, d, ncent, iters = 1_000_000, 128, 4096, 10
+        x, _, _ = gen_mixture(n, d, ncent, 1, dev, jitter=False)
+        cent = torch.empty(ncent, d, device=dev)
+        assign = torch.empty(n, dtype=torch.int32, device=dev)
+        res = vsk_kmeans_result()
+        import ctypes
+
+        def step():
+            ctx.check(lib.vsk_kmeans(ctx.handle, x.data_ptr(), n, d, ncent, None, INIT_RANDOM,
+                                     None, ctypes.c_uint64(7), iters, 0.0, cent.data_ptr(),
+                                     assign.data_ptr(), ctypes.byref(res)))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            th = host_threads()
+            xh = x.cpu().numpy()
+            # the oracle's Lloyd loop on a row sample: 2 iterations from the
+            # GPU's final centroids (an assignment of m x 4096 pairs and the
+            # update, per iteration)
+            ch = cent.cpu().numpy()
+            m = 4096
+            t0 = time.perf_counter()
+            O.kmeans_cluster(xh[:m], ncent, init_method="custom", init=ch, max_iter=1, tol=0.0,
+                             threads=th)
+            per = time.perf_counter() - t0
+            m = int(min(n, max(4096, m * target_s / 2 / max(per, 1e-3))))
+            t0 = time.perf_counter()
+            O.kmeans_cluster(xh[:m], ncent, init_method="custom", init=ch, max_iter=2, tol=0.0,
+                             threads=th)
+            el = time.perf_counter() - t0
+            return ({"value": m * 2 / el, "unit": "row-iterations/s", "cores": th,
+                     "kind": "port",
+                     "sample": f"first {m} of {n} rows, 2 Lloyd iterations against "
+                               f"{ncent} centroids ({el:.1f} s)"}, 1.0)
+
+        spec = {
+            "metric": "k-means row-iterations/s, 1M x 128, k = 4096 (IVF training at "
+                      "config 3's scale)",
+            "workload": "kmeans-1Mx128-k4096-iter10 (IVF coarse training, BASELINE config 3 data)",
+            "config": {"n": n, "d": d, "k": ncent, "iterations": iters, "init": "random (seed 7)"},
+            "data": "synthetic: 4,096-Gaussian mixture, centres 2 N(0,I) (seed 3), points "
+                    "centre + 0.5 N(0,I) (seeds 5, 1)",
+            "dtype": "f32", "nq": n, "n": ncent, "d": d,
+            "units_per_step": n * iters, "unit": "row-iterations/s",
+            "kernels": [("flat_valu_argmin", "k_flat_valu<ARGMIN> (exact sqrt-L2, dimension "
+                         "order)", "valu_l2"),
+                        ("flat_screen_min", "k_flat_screen<MIN> (bf16 screen)", "mfma_bf16")],
+            "keep": (x, cent, assign),
         }
         return spec, step, cpu_leg
 
@@ -505,11 +565,11 @@ def main():
     ctx.profile(False)
 
     nq, n = spec["nq"], spec["n"]
-    qps = nq * a.steps / el
+    qps = spec.get("units_per_step", nq) * a.steps / el
     out = {
         "metric": spec["metric"],
         "value": round(qps, 1),
-        "unit": "queries/s",
+        "unit": spec.get("unit", "queries/s"),
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,

@@ -166,3 +166,68 @@ def test_kmeans_config3_scale(ctx):
         dist[r:r + 100_000] = np.sqrt(np.cumsum(t * t, axis=1, dtype=np.float32)[:, -1])
     assert res.iterations == 1 and not res.converged
     assert np.float32(res.inertia) == np.cumsum(dist, dtype=np.float32)[-1]
+
+
+@pytest.fixture(scope="module")
+def screen_ctx():
+    """A context whose argmin takes the bf16 screen at every size."""
+    import os
+
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from vectorstorekit_amd import Context
+
+    old = os.environ.get("VSK_FLAT_KERNEL")
+    os.environ["VSK_FLAT_KERNEL"] = "screen"
+    try:
+        c = Context(0)
+    finally:
+        if old is None:
+            del os.environ["VSK_FLAT_KERNEL"]
+        else:
+            os.environ["VSK_FLAT_KERNEL"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("method", ["random", "kMeansPlusPlus"])
+@pytest.mark.parametrize("shape", [(5000, 37, 17), (2500, 128, 300), (1200, 64, 1200),
+                                   (20_000, 96, 64), (3001, 200, 257)])
+def test_kmeans_screen_bit_exact(screen_ctx, method, shape):
+    """The screened assignment (bf16 MFMA top-2, bound test, exact winner)
+    gives the oracle's k-means bit for bit: partial row and query tiles
+    (k = 17, 257, 300; n = 3001), padded dimensions (37 -> 64, 200 -> 256)."""
+    n, d, k = shape
+    print(f"kmeans screen {method} n={n} d={d} k={k}", flush=True)
+    x = _mixture(n * 3 + d + k, n, d, max(2, k // 2))
+    cfg = KMeansClusteringConfiguration(maxIterations=8, tolerance=1e-4, initMethod=method,
+                                        seed=n + 3 * k)
+    res = KMeansClustering(screen_ctx, cfg).cluster(x, k)
+    ref = O.kmeans_cluster(x, k, init_method=method, max_iter=8, tol=1e-4, seed=n + 3 * k)
+    _check(res, ref)
+
+
+def test_screen_argmin_ties_fall_back(screen_ctx):
+    """Duplicated centroids tie every row near them: the screen cannot
+    decide, the exact scan takes those rows and the first duplicate wins.
+    Rows far from a centroid (large |q - x| against a small gap) take the
+    screen's winner."""
+    rng = np.random.default_rng(8)
+    d = 64
+    cent = (rng.standard_normal((300, d)) * 3).astype(np.float32)
+    cent = np.concatenate([cent, cent[:50]]).astype(np.float32)  # rows 300..349 duplicate 0..49
+    x = (cent[rng.integers(0, 300, 30_000)] + rng.standard_normal((30_000, d))).astype(np.float32)
+    idx = IVFIndex(screen_ctx, IVFConfiguration(dimensions=d, numberOfCentroids=350,
+                                                numberOfProbes=4))
+    idx.set_centroids(cent)
+    got = idx.assign(x)
+    np.testing.assert_array_equal(got, O.ivf_assign(x, cent))
+    assert (got < 300).all()
+    screen_ctx.profile(True)
+    screen_ctx.profile_reset()
+    idx.assign(x)
+    stats = screen_ctx.profile_stats()
+    screen_ctx.profile(False)
+    assert "flat_screen_top2" in stats and "screen_argmin_fallback" in stats

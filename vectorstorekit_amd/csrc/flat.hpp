@@ -26,7 +26,11 @@ inline int32_t exact_metric(int32_t metric) {
   }
 }
 
-enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2, MODE_ARGMIN = 3 };
+enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2, MODE_ARGMIN = 3,
+       // the screen only: per (query, row split) the smallest key and the
+       // second smallest distance (a.cand[q * a.ldm + split] and
+       // a.mat[q * a.ldm + split])
+       MODE_TOP2 = 4 };
 
 struct FlatArgs {
   const float *X;
@@ -110,6 +114,28 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
 const float *x_aux(const vsk_db *db, int32_t metric);
 float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
              int32_t metric);
+// bf16 planes and norms of a query batch for screen_argmin: hi plane
+// (stride ldb = roundup(d, 64)), |hi|, |q - hi| and |q|^2 per query
+struct ArgminQueries {
+  const uint16_t *qh = nullptr;
+  const float *qnh = nullptr, *qnr = nullptr, *qsq = nullptr;
+  int32_t ldb = 0;
+};
+ArgminQueries argmin_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                             int32_t ld, const char *slot);
+// whether the screen serves an argmin of nq queries over n rows of d dims
+bool screen_argmin_applies(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t d);
+// exact nearest row of each query (sqrt-L2 summed in dimension order, the
+// first minimum under strict '<'): argmin[q] and its distance dist[q].  X:
+// n x ld rows with |x|^2 in xsq; dq: the queries (stride ld) with their
+// planes qp.  A bf16 screen keeps each query's smallest and second smallest
+// approximate distance; a query whose two are apart by more than the
+// screen's error bound takes the first (its exact distance recomputed), the
+// rest are redone by the exact VALU scan.
+void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
+                   int32_t d, int32_t ld, const float *dq, int64_t nq,
+                   const ArgminQueries &qp, int32_t *argmin, float *dist);
+
 // exact top-k through the screen (flat_screen.hip): a one-pass bf16 scan
 // keeps screen_keep(k) candidates per query, a proven error bound shows they
 // hold the exact top-k, and an fp32 rescore in the CPU reference's summation

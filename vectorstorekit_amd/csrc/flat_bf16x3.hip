@@ -393,7 +393,21 @@ constexpr int XS_STAGE = (XS_N + XS_Q) * XS_R;  // bytes per stage buffer
 // |q|^2 or |q| (metric), threshold as a distance, threshold key, index of
 // the first reserved slot in the candidate array
 constexpr int XS_LDS = 2 * XS_STAGE + 6 * XS_Q * 4 + 2 * XS_Q * 8;
-static_assert(XS_LDS <= 160 * 1024, "LDS of one workgroup");
+// MODE_TOP2: a (smallest key, second smallest distance) slot per row wave
+// and query
+constexpr int XS_LDS_TOP2 = XS_LDS + 4 * XS_Q * (8 + 4);
+static_assert(XS_LDS_TOP2 <= 160 * 1024, "LDS of one workgroup");
+
+__device__ __forceinline__ float top2_keydist(uint64_t k) {
+  return k == VSK_KEY_NONE ? __int_as_float(0x7f800000) : vsk_ord2f((uint32_t)(k >> 32));
+}
+// (k, m2) := the smallest key and the second smallest distance of the union
+// of two such pairs
+__device__ __forceinline__ void top2_merge(uint64_t &k, float &m2, uint64_t ko, float mo) {
+  const uint64_t hi = ko < k ? k : ko;
+  k = ko < k ? ko : k;
+  m2 = fminf(fminf(m2, mo), top2_keydist(hi));
+}
 
 __device__ __forceinline__ int swz8(int r, int c) {
   return r * XS_R + ((c ^ ((r >> 1) & 7)) << 4);
@@ -444,6 +458,14 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   float *s_tdot = s_thf + XS_Q;
   uint64_t *s_th = reinterpret_cast<uint64_t *>(s_tdot + XS_Q);
   int64_t *s_pb = reinterpret_cast<int64_t *>(s_th + XS_Q);
+  uint64_t *s_t1 = reinterpret_cast<uint64_t *>(lds + XS_LDS);  // [4][XS_Q]
+  float *s_t2 = reinterpret_cast<float *>(s_t1 + 4 * XS_Q);
+  if constexpr (MODE == MODE_TOP2) {
+    for (int i = tid; i < 4 * XS_Q; i += 512) {
+      s_t1[i] = VSK_KEY_NONE;
+      s_t2[i] = __int_as_float(0x7f800000);
+    }
+  }
   if (tid < XS_Q) {
     const int64_t q = q0 + tid;
     const bool ok = q < a.nq && (!a.active || a.active[q]);
@@ -633,6 +655,45 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             a.cand[qi * a.cap + (row - a.r0)] =
                 vsk_key(dist_from_dot<METRIC>(acc[i][j][r], qa, xa), (uint32_t)row);
           }
+      } else if constexpr (MODE == MODE_TOP2) {
+        // this lane's 16 rows in ascending order: the smallest distance
+        // (first one on a tie) and the second smallest (an equal distance
+        // counts: it makes the winner undecidable)
+        const float inf = __int_as_float(0x7f800000);
+        float m1 = inf, m2 = inf;
+        int b1 = -1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int e = 4 * i + r;
+            const int64_t row = rbase + i * 16 + r;
+            const float xa = (full || row < s1) ? a.xaux[row] : 0.f;
+            const float dd = dist_from_dot<METRIC>(acc[i][j][r], qa, xa);
+            const bool v = (vmask >> e) & 1u;
+            const bool lt = v && dd < m1;
+            m2 = lt ? m1 : (v ? fminf(m2, dd) : m2);
+            b1 = lt ? e : b1;
+            m1 = lt ? dd : m1;
+          }
+        uint64_t k1 = b1 < 0 ? VSK_KEY_NONE
+                             : vsk_key(m1, (uint32_t)(rbase + 16 * (b1 >> 2) + (b1 & 3)));
+        // the four lane groups hold other rows of the same query
+#pragma unroll
+        for (int mk = 16; mk <= 32; mk <<= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)k1, mk);
+          const uint32_t hi = __shfl_xor((uint32_t)(k1 >> 32), mk);
+          const float mo = __shfl_xor(m2, mk);
+          top2_merge(k1, m2, ((uint64_t)hi << 32) | lo, mo);
+        }
+        if (cl == 0 && l_ok[16 * j]) {
+          const int slot_i = wr * XS_Q + lq0 + 16 * j;  // this wave's own slot
+          uint64_t k = s_t1[slot_i];
+          float t2 = s_t2[slot_i];
+          top2_merge(k, t2, k1, m2);
+          s_t1[slot_i] = k;
+          s_t2[slot_i] = t2;
+        }
       } else {
         // a key can only pass when its distance is <= the threshold's (ties
         // are settled by the exact key): one compare per score, and the
@@ -702,6 +763,17 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   }
   // the copies issued past the slice end land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt(kWaitAll);
+  if constexpr (MODE == MODE_TOP2) {
+    __syncthreads();
+    if (tid < XS_Q && s_ok[tid]) {
+      uint64_t k = s_t1[tid];
+      float t2 = s_t2[tid];
+#pragma unroll
+      for (int u = 1; u < 4; ++u) top2_merge(k, t2, s_t1[u * XS_Q + tid], s_t2[u * XS_Q + tid]);
+      a.cand[(q0 + tid) * a.ldm + split] = k;
+      a.mat[(q0 + tid) * a.ldm + split] = t2;
+    }
+  }
   if constexpr (MODE == MODE_FILTER) {
     __syncthreads();
     if (tid < XS_Q && s_ok[tid]) {
@@ -723,6 +795,13 @@ template <int METRIC>
 static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a,
                      const SplitPtrs &s, int mode) {
   const size_t lds = XS_LDS;
+  if constexpr (METRIC == VSK_METRIC_L2SQ) {
+    if (mode == MODE_TOP2) {
+      k_flat_screen<MODE_TOP2, METRIC><<<grid, 512, XS_LDS_TOP2, ctx->stream>>>(a, s);
+      return;
+    }
+  }
+  if (mode == MODE_TOP2) fail(VSK_ERR_UNSUPPORTED, "the screen's argmin mode is L2^2 only");
   if (mode == MODE_DENSE)
     k_flat_screen<MODE_DENSE, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
   else
@@ -733,7 +812,8 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
                         int32_t *nseg, int64_t *stride) {
   const int64_t rows = a.r1 - a.r0;
   if (rows <= 0 || a.nq <= 0) return;
-  if (mode == MODE_MATRIX) fail(VSK_ERR_UNSUPPORTED, "the screen has no matrix mode");
+  if (mode == MODE_MATRIX || mode == MODE_ARGMIN)
+    fail(VSK_ERR_UNSUPPORTED, "the screen has no matrix or VALU argmin mode");
   if (s.ldqb != s.ldxb || s.kb > s.ldxb || (s.kb & 63))
     fail(VSK_ERR_INVALID_ARGUMENT, "screen planes need one pitch and a padded dimension");
   static bool lds_set = false;
@@ -763,6 +843,9 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_DOT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    VSK_HIP(hipFuncSetAttribute(
+        reinterpret_cast<const void *>(k_flat_screen<MODE_TOP2, VSK_METRIC_L2SQ>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_TOP2));
     lds_set = true;
   }
   const int64_t qt = ceil_div(a.nq, XS_Q);
@@ -795,6 +878,11 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     if (sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
     a.sub = (int32_t)sub;
   }
+  if (mode == MODE_TOP2) {
+    // one (key, distance) pair per query and split: the caller merges them
+    a.ldm = splits;
+    if (nseg) *nseg = (int32_t)splits;
+  }
   if (mode != MODE_FILTER || splits > VSK_MAX_SEG || !nseg || !stride) a.seg_n = nullptr;
   if (a.seg_n) {
     // splits without rows launch no writes: their segments start empty
@@ -805,7 +893,8 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
   const int64_t groups = ceil_div(qt, XS_GQ);
   const int64_t nblocks = 8 * a.splits_per_xcd * groups * XS_GQ;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
-  static const char *names[2] = {"flat_screen_dense", "flat_screen_filter"};
+  static const char *names[5] = {"flat_screen_dense", "flat_screen_filter", "",
+                                 "", "flat_screen_top2"};
   KernelTimer t(ctx, names[mode], (double)a.nq * (double)rows);
   switch (a.metric) {
   case VSK_METRIC_L2SQ: launch_s<VSK_METRIC_L2SQ>(ctx, (unsigned)nblocks, a, s, mode); break;

@@ -368,6 +368,199 @@ static void redo_queries(vsk_ctx *ctx, const vsk_db *db, const float *qbat,
   check_launch("screen_scatter");
 }
 
+// ---------------------------------------------------------------------------
+// exact argmin through the screen (k-means and IVF assignment)
+// ---------------------------------------------------------------------------
+// The bound of the file comment with k = 1: the screen's smallest
+// distance a1 (row w) and second smallest a2 over all rows; if
+// a2 > (a1 + eps)(1 + 2^-20) + eps, every other row y has
+// d(y) >= a(y) - eps >= a2 - eps > (a1 + eps)(1 + 2^-20) >= d(w)(1 + 2^-20),
+// so w is the unique exact minimum even after the square roots are rounded.
+// One thread per query merges the row splits' pairs, tests the bound and
+// recomputes the winner's exact distance in dimension order (no FMA);
+// queries failing the test are listed for the exact VALU scan.
+__global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsplit,
+                                int64_t nq, const float *qnh, const float *qnr,
+                                const uint32_t *maxbits, int32_t d, const float *X,
+                                int64_t ld, const float *Q, int32_t *argmin, float *dist,
+                                int64_t qoff, int32_t *fail_idx, int32_t *nfail) {
+#pragma clang fp contract(off)
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  uint64_t k = VSK_KEY_NONE;
+  float m2 = __int_as_float(0x7f800000);
+  for (int32_t sp = 0; sp < nsplit; ++sp) {
+    const uint64_t ko = k1[q * nsplit + sp];
+    const float mo = a2[q * nsplit + sp];
+    const uint64_t hi = ko < k ? k : ko;
+    k = ko < k ? ko : k;
+    const float hd = hi == VSK_KEY_NONE ? __int_as_float(0x7f800000)
+                                        : vsk_ord2f((uint32_t)(hi >> 32));
+    m2 = fminf(fminf(m2, mo), hd);
+  }
+  bool good = k != VSK_KEY_NONE;
+  if (good) {
+    CheckArgs ca{};
+    ca.d = d;
+    ca.metric = VSK_METRIC_L2SQ;
+    ca.qnh = qnh;
+    ca.qnr = qnr;
+    ca.xh = (double)__uint_as_float(maxbits[0]);
+    ca.xr = (double)__uint_as_float(maxbits[1]);
+    const double eps = screen_eps(ca, q);
+    const double a1 = vsk_ord2f((uint32_t)(k >> 32));
+    const double lim = (a1 + eps) * (1.0 + 0x1p-20) + eps;
+    good = (double)m2 > lim;
+  }
+  if (!good) {
+    fail_idx[atomicAdd(nfail, 1)] = (int32_t)(qoff + q);
+    return;
+  }
+  const uint32_t row = (uint32_t)k;
+  const float *qq = Q + q * ld, *xx = X + (int64_t)row * ld;
+  float s = 0.f;
+  for (int32_t j = 0; j < d; ++j) {
+    const float t = qq[j] - xx[j];
+    s = s + t * t;
+  }
+  argmin[q] = (int32_t)row;
+  dist[q] = sqrtf(s);
+}
+
+__global__ void k_scatter_argmin(const int32_t *src_a, const float *src_d, int64_t m,
+                                 const int32_t *idx, int32_t *argmin, float *dist) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    argmin[idx[i]] = src_a[i];
+    dist[idx[i]] = src_d[i];
+  }
+}
+
+ArgminQueries argmin_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                             int32_t ld, const char *slot) {
+  ArgminQueries qp;
+  qp.ldb = (d + 63) & ~63;
+  const std::string sl(slot);
+  uint16_t *qh = static_cast<uint16_t *>(
+      ctx->scratch_ptr(sl + ".qh", sizeof(uint16_t) * (size_t)nq * qp.ldb));
+  float *nrm = static_cast<float *>(ctx->scratch_ptr(sl + ".qn", sizeof(float) * 3 * (size_t)nq));
+  split_bf16(ctx, dq, nq, d, ld, qh, nullptr, qp.ldb, nrm, nrm + nq, nullptr);
+  row_norms(ctx, dq, nq, d, ld, nrm + 2 * nq, nullptr);
+  qp.qh = qh;
+  qp.qnh = nrm;
+  qp.qnr = nrm + nq;
+  qp.qsq = nrm + 2 * nq;
+  return qp;
+}
+
+bool screen_argmin_applies(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t d) {
+  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (n >= 0x7FFFFFFFll || d < 32) return false;  // narrow rows: the padding to 64 dims costs
+  // small problems take the exact scan alone (the screen's fixed launches)
+  return ctx->flat_force_screen || (double)nq * (double)n * d >= (double)(1ll << 30);
+}
+
+void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
+                   int32_t d, int32_t ld, const float *dq, int64_t nq,
+                   const ArgminQueries &qp, int32_t *argmin, float *dist) {
+  KernelTimer tm(ctx, "screen_argmin", (double)nq * (double)n);
+  const int32_t ldb = qp.ldb;
+  // the rows' hi plane and the maxima of |hi| and |x - hi| over them
+  uint16_t *xh = static_cast<uint16_t *>(
+      ctx->scratch_ptr("sam.xh", sizeof(uint16_t) * (size_t)n * ldb));
+  uint32_t *maxbits = static_cast<uint32_t *>(ctx->scratch_ptr("sam.max", 2 * sizeof(uint32_t)));
+  fill_i32(ctx, reinterpret_cast<int32_t *>(maxbits), 2, 0);
+  split_bf16(ctx, X, n, d, ld, xh, nullptr, ldb, nullptr, nullptr, maxbits);
+  SplitPtrs sp;
+  sp.xh = xh;
+  sp.xl = nullptr;
+  sp.qh = qp.qh;
+  sp.ql = nullptr;
+  sp.ldxb = ldb;
+  sp.ldqb = ldb;
+  sp.kb = ldb;
+  const int64_t qb_max = (int64_t)1 << 22;  // queries per launch
+  const int64_t qcap = nq < qb_max ? nq : qb_max;
+  // the most row splits launch_flat_screen picks for this shape (a multiple
+  // of 8, at most 8 rounds of workgroups and one tile per split)
+  // (fewer queries allow more splits: the bound is taken at the last,
+  // smallest batch)
+  const int64_t nlast = nq - ((nq - 1) / qb_max) * qb_max;
+  const int64_t tiles = ceil_div(n, 256);
+  int64_t top = 8 * ceil_div(8 * (int64_t)ctx->cu_count, 8 * ceil_div(nlast, 256));
+  if (top > 8 * ceil_div(tiles, 8)) top = 8 * ceil_div(tiles, 8);
+  if (top < 8) top = 8;
+  uint64_t *k1 = static_cast<uint64_t *>(
+      ctx->scratch_ptr("sam.k1", sizeof(uint64_t) * (size_t)qcap * top));
+  float *a2 = static_cast<float *>(
+      ctx->scratch_ptr("sam.a2", sizeof(float) * (size_t)qcap * top));
+  int32_t *fidx = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.fidx", sizeof(int32_t) * (size_t)(nq + 1)));
+  int32_t *nfail = fidx + nq;
+  fill_i32(ctx, nfail, 1, 0);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb_max) {
+    const int64_t nb = nq - b0 < qb_max ? nq - b0 : qb_max;
+    FlatArgs a{};
+    a.X = X;
+    a.ldx = ld;
+    a.Q = dq + b0 * ld;
+    a.ldq = ld;
+    a.xaux = xsq;
+    a.qaux = qp.qsq + b0;
+    a.kdim = ld;
+    a.nq = (int32_t)nb;
+    a.r0 = 0;
+    a.r1 = n;
+    a.metric = VSK_METRIC_L2SQ;
+    a.cand = k1;
+    a.mat = a2;
+    SplitPtrs sb = sp;
+    sb.qh = qp.qh + b0 * ldb;
+    // splits without rows write nothing: their pairs must read as empty
+    fill_u64(ctx, k1, nb * top, VSK_KEY_NONE);
+    fill_i32(ctx, reinterpret_cast<int32_t *>(a2), nb * top, 0x7f800000);
+    int32_t nsplit = 0;
+    launch_flat_screen(ctx, a, sb, MODE_TOP2, &nsplit, nullptr);
+    if (nsplit < 8 || nsplit > top)
+      fail(VSK_ERR_EXECUTION_FAILED, "argmin screen: unexpected split count");
+    k_argmin_finish<<<(unsigned)ceil_div(nb, 256), 256, 0, ctx->stream>>>(
+        k1, a2, nsplit, nb, qp.qnh + b0, qp.qnr + b0, maxbits, d, X, ld, dq + b0 * ld,
+        argmin + b0, dist + b0, b0, fidx, nfail);
+    check_launch("screen_argmin_finish");
+  }
+  int32_t hf = 0;
+  VSK_HIP(hipMemcpyAsync(&hf, nfail, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  if (hf == 0) return;
+  // near ties: the exact VALU argmin over every row for those queries
+  KernelTimer tf(ctx, "screen_argmin_fallback", (double)hf);
+  const int64_t m = hf;
+  float *q2 = static_cast<float *>(ctx->scratch_ptr("sam.fq", sizeof(float) * (size_t)m * ld));
+  k_gather_rows<<<grid_for(m * ld), 256, 0, ctx->stream>>>(dq, ld, fidx, m, q2);
+  check_launch("screen_argmin_gather");
+  int32_t *a_out = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.fa", (sizeof(int32_t) + sizeof(float)) * (size_t)m));
+  float *d_out = reinterpret_cast<float *>(a_out + m);
+  const int64_t chunk = 1 << 24;
+  for (int64_t r = 0; r < m; r += chunk) {
+    const int64_t mm = m - r < chunk ? m - r : chunk;
+    FlatArgs a{};
+    a.X = X;
+    a.ldx = ld;
+    a.Q = q2 + r * ld;
+    a.ldq = ld;
+    a.kdim = ld;
+    a.nq = (int32_t)mm;
+    a.r0 = 0;
+    a.r1 = n;
+    a.metric = METRIC_L2_EXACT;
+    a.amin = d_out + r;
+    launch_flat(ctx, a, MODE_ARGMIN, a_out + r);
+  }
+  k_scatter_argmin<<<grid_for(m), 256, 0, ctx->stream>>>(a_out, d_out, m, fidx, argmin, dist);
+  check_launch("screen_argmin_scatter");
+}
+
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  int32_t k, int32_t metric, uint64_t *best) {
   const int32_t kc = screen_keep(k);

@@ -214,9 +214,18 @@ static FlatArgs centroid_args(const vsk_ivf *ivf, const float *dq, int64_t nq) {
   return a;
 }
 
-// nearest centroid of every row (strict '<', first minimum)
+// nearest centroid of every row (strict '<', first minimum): the bf16
+// screen with exact recomputation for large problems, else the exact VALU
+// scan
 static void ivf_assign_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dx,
                               int64_t n, int32_t *out) {
+  if (screen_argmin_applies(ctx, n, ivf->nlist, ivf->d)) {
+    const ArgminQueries qp = argmin_queries(ctx, dx, n, ivf->d, ivf->ld, "ivf.aq");
+    float *dist = static_cast<float *>(ctx->scratch_ptr("ivf.adist", sizeof(float) * (size_t)n));
+    screen_argmin(ctx, ivf->centroids.x.as<float>(), ivf->centroids.sqnorm.as<float>(),
+                  ivf->nlist, ivf->d, ivf->ld, dx, n, qp, out, dist);
+    return;
+  }
   const int64_t chunk = 1 << 24;  // rows per launch (grid.x bound)
   for (int64_t r = 0; r < n; r += chunk) {
     int64_t m = n - r < chunk ? n - r : chunk;

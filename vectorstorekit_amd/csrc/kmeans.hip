@@ -4,9 +4,11 @@
 // (Quantization/ProductQuantizer.swift:270-324).
 //
 // One Lloyd iteration is
-//   assignment  the exact VALU argmin scan (flat.hip, MODE_ARGMIN with the
-//               sequential sqrt-L2 of :421-428, strict '<', :271-295), which
-//               also returns each row's winning distance;
+//   assignment  each row's nearest centroid under the sequential sqrt-L2 of
+//               :421-428 (strict '<', :271-295) and its distance: the bf16
+//               screen with a proven bound and an exact recomputation of the
+//               winner (flat_screen.hip, screen_argmin) when the problem is
+//               large, else the exact VALU argmin scan (flat.hip);
 //   inertia     distances.reduce(0, +) (:97): one wave adds the distances in
 //               row order, so the fp32 rounding is the reference's;
 //   grouping    a stable LSD radix pass per 4-bit digit of the cluster id
@@ -65,32 +67,50 @@ __host__ __device__ inline uint64_t swift_bounded(uint64_t &s, uint64_t bound) {
 }
 
 // ---------------------------------------------------------------------------
-// inertia: the fp32 sum of n values in index order, by one wave.  Each
-// 64-value chunk is loaded by the lanes (the next chunk is in flight while
-// this one is added) and added lane by lane from scalar registers.
+// inertia: the fp32 sum of n values in index order, by one wave.  The wave
+// copies blocks of 4096 values into LDS with coalesced loads (the next
+// block's loads in flight meanwhile), and lane 0 adds each block in order
+// from 16-byte LDS reads: the adds form one dependent chain with no
+// cross-lane moves in it.  v must be 16-byte aligned.
 // ---------------------------------------------------------------------------
+constexpr int SS_BLOCK = 4096;  // values per LDS block (16 KB)
+typedef float ss_f4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(64) void k_seq_sum(const float *v, int64_t n,
                                                 float *out) {
-#pragma clang fp contract(off)
+  __shared__ ss_f4 buf[SS_BLOCK / 4];
   const int lane = threadIdx.x;
-  float s = 0.f;
-  float cur = lane < n ? v[lane] : 0.f;
-  for (int64_t i0 = 0; i0 < n; i0 += 64) {
-    const int64_t nx = i0 + 64 + lane;
-    const float nxt = nx < n ? v[nx] : 0.f;
-    const int cb = __float_as_int(cur);
-    if (n - i0 >= 64) {
+  const int64_t nb = n / SS_BLOCK;  // whole blocks
+  const ss_f4 *src = reinterpret_cast<const ss_f4 *>(v);
+  ss_f4 r[SS_BLOCK / 256];
+  if (nb > 0) {
 #pragma unroll
-      for (int j = 0; j < 64; ++j)
-        s = s + __int_as_float(__builtin_amdgcn_readlane(cb, j));
-    } else {
-      const int m = (int)(n - i0);
-      for (int j = 0; j < m; ++j)
-        s = s + __int_as_float(__builtin_amdgcn_readlane(cb, j));
-    }
-    cur = nxt;
+    for (int u = 0; u < SS_BLOCK / 256; ++u) r[u] = src[u * 64 + lane];
   }
-  if (lane == 0) out[0] = s;
+  float s = 0.f;
+  for (int64_t b = 0; b < nb; ++b) {
+#pragma unroll
+    for (int u = 0; u < SS_BLOCK / 256; ++u) buf[u * 64 + lane] = r[u];
+    __syncthreads();
+    if (b + 1 < nb) {
+      const ss_f4 *nx = src + (b + 1) * (SS_BLOCK / 4);
+#pragma unroll
+      for (int u = 0; u < SS_BLOCK / 256; ++u) r[u] = nx[u * 64 + lane];
+    }
+    if (lane == 0) {
+      for (int i = 0; i < SS_BLOCK / 4; ++i) {
+        const ss_f4 t = buf[i];
+        s = s + t.x;
+        s = s + t.y;
+        s = s + t.z;
+        s = s + t.w;
+      }
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    for (int64_t i = nb * SS_BLOCK; i < n; ++i) s = s + v[i];
+    out[0] = s;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -444,9 +464,17 @@ static unsigned grid1d(int64_t n, int threads) {
   return (unsigned)(g < 1 ? 1 : (g > 65535 * 32 ? 65535 * 32 : g));
 }
 
-// nearest centroid and its distance for each of the n rows of dx
-static void kmeans_assign(vsk_ctx *ctx, const float *cent, int32_t k, int32_t ld,
-                          const float *dx, int64_t n, int32_t *assign, float *dist) {
+// nearest centroid and its distance for each of the n rows of dx: the bf16
+// screen with exact recomputation (qp.qh set) or the exact VALU scan
+static void kmeans_assign(vsk_ctx *ctx, const float *cent, int32_t k, int32_t d,
+                          int32_t ld, const float *dx, int64_t n, const ArgminQueries &qp,
+                          int32_t *assign, float *dist) {
+  if (qp.qh) {
+    float *csq = static_cast<float *>(ctx->scratch_ptr("km.csq", sizeof(float) * (size_t)k));
+    row_norms(ctx, cent, k, d, ld, csq, nullptr);
+    screen_argmin(ctx, cent, csq, k, d, ld, dx, n, qp, assign, dist);
+    return;
+  }
   const int64_t chunk = 1 << 24;  // rows per launch (grid.x bound)
   for (int64_t r = 0; r < n; r += chunk) {
     const int64_t m = n - r < chunk ? n - r : chunk;
@@ -627,12 +655,16 @@ vsk_status vsk_kmeans(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
   float *view = static_cast<float *>(ctx->scratch_ptr("km.view", sizeof(float) * (size_t)(k + 1)));
   std::vector<float> hview((size_t)k + 1);
   fill_i32(ctx, assign, n, 0);
+  // the rows' bf16 planes for the screened assignment, made once
+  ArgminQueries qp;
+  if (max_iter > 0 && screen_argmin_applies(ctx, n, k, d))
+    qp = argmin_queries(ctx, dx, n, d, ld, "km.q");
   uint64_t empty_rng = seed + 0x9E3779B97F4A7C15ull;
   float prev = INFINITY;
   int32_t it = 0;
   bool conv = false;
   while (it < max_iter && !conv) {
-    kmeans_assign(ctx, cur, k, ld, dx, n, assign, dist);
+    kmeans_assign(ctx, cur, k, d, ld, dx, n, qp, assign, dist);
     {
       KernelTimer tm(ctx, "kmeans_inertia", (double)n);
       k_seq_sum<<<1, 64, 0, ctx->stream>>>(dist, n, view);
