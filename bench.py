@@ -274,7 +274,8 @@ def setup(a, ctx, dev):
             "units_per_step": n * iters, "unit": "row-iterations/s",
             "kernels": [("flat_valu_argmin", "k_flat_valu<ARGMIN> (exact sqrt-L2, dimension "
                          "order)", "valu_l2"),
-                        ("flat_screen_min", "k_flat_screen<MIN> (bf16 screen)", "mfma_bf16")],
+                        ("flat_screen_top2", "k_flat_screen<TOP2> (bf16 screen, smallest two per "
+                         "row)", "mfma_bf16")],
             "keep": (x, cent, assign),
         }
         return spec, step, cpu_leg

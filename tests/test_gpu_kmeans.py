@@ -211,15 +211,17 @@ def test_kmeans_screen_bit_exact(screen_ctx, method, shape):
 
 def test_screen_argmin_ties_fall_back(screen_ctx):
     """Duplicated centroids tie every row near them: the screen cannot
-    decide, the exact scan takes those rows and the first duplicate wins.
-    Rows far from a centroid (large |q - x| against a small gap) take the
-    screen's winner."""
+    decide, the collecting pass rescores the tied rows exactly and the first
+    duplicate wins.  81 copies of one centroid overflow the 64-candidate
+    lists: those rows take the exact scan over every centroid."""
     rng = np.random.default_rng(8)
     d = 64
-    cent = (rng.standard_normal((300, d)) * 3).astype(np.float32)
-    cent = np.concatenate([cent, cent[:50]]).astype(np.float32)  # rows 300..349 duplicate 0..49
-    x = (cent[rng.integers(0, 300, 30_000)] + rng.standard_normal((30_000, d))).astype(np.float32)
-    idx = IVFIndex(screen_ctx, IVFConfiguration(dimensions=d, numberOfCentroids=350,
+    base = (rng.standard_normal((300, d)) * 3).astype(np.float32)
+    # rows 300..349 duplicate 0..49; rows 350..429 copy row 299
+    cent = np.concatenate([base, base[:50], np.repeat(base[299:300], 80, axis=0)])
+    cent = cent.astype(np.float32)
+    x = (base[rng.integers(0, 300, 30_000)] + rng.standard_normal((30_000, d))).astype(np.float32)
+    idx = IVFIndex(screen_ctx, IVFConfiguration(dimensions=d, numberOfCentroids=len(cent),
                                                 numberOfProbes=4))
     idx.set_centroids(cent)
     got = idx.assign(x)
@@ -230,4 +232,5 @@ def test_screen_argmin_ties_fall_back(screen_ctx):
     idx.assign(x)
     stats = screen_ctx.profile_stats()
     screen_ctx.profile(False)
-    assert "flat_screen_top2" in stats and "screen_argmin_fallback" in stats
+    for key in ("flat_screen_top2", "screen_argmin_collect", "screen_argmin_fallback"):
+        assert key in stats, key

@@ -59,6 +59,7 @@ CallScope::CallScope(vsk_ctx *c) : ctx(c) {
   VSK_HIP(hipEventRecord(ctx->call_begin, ctx->stream));
 }
 void CallScope::finish() {
+  if (ctx->aux) VSK_HIP(hipStreamSynchronize(ctx->aux));
   VSK_HIP(hipEventRecord(ctx->call_end, ctx->stream));
   VSK_HIP(hipStreamSynchronize(ctx->stream));
   float ms = 0.f;
@@ -67,8 +68,8 @@ void CallScope::finish() {
   ctx->resolve_pending();
 }
 
-KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items)
-    : ctx(c), work(work_items) {
+KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items, hipStream_t s)
+    : ctx(c), work(work_items), stream(s ? s : c->stream) {
   if (!ctx->profile) return;
   auto it = ctx->stat_index.find(name);
   if (it == ctx->stat_index.end()) {
@@ -80,12 +81,12 @@ KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items)
   }
   stat = it->second;
   a = ctx->take_event();
-  VSK_HIP(hipEventRecord(a, ctx->stream));
+  VSK_HIP(hipEventRecord(a, stream));
 }
 KernelTimer::~KernelTimer() {
   if (stat < 0) return;
   hipEvent_t b = ctx->take_event();
-  if (hipEventRecord(b, ctx->stream) == hipSuccess)
+  if (hipEventRecord(b, stream) == hipSuccess)
     ctx->pending.push_back({stat, a, b, work});
 }
 
@@ -295,9 +296,28 @@ void *vsk_ctx::scratch_ptr(const std::string &key, size_t bytes) {
   if (b->bytes < bytes || !b->p) {
     // a buffer in use by queued work must not be freed under it
     VSK_HIP(hipStreamSynchronize(stream));
+    if (aux) VSK_HIP(hipStreamSynchronize(aux));
     b->reserve(bytes + bytes / 8);
   }
   return b->p;
+}
+hipStream_t vsk_ctx::aux_stream() {
+  if (!aux) VSK_HIP(hipStreamCreate(&aux));
+  return aux;
+}
+void *vsk_ctx::pinned_ptr(size_t bytes) {
+  if (pinned_bytes < bytes) {
+    if (pinned) {
+      VSK_HIP(hipStreamSynchronize(stream));
+      if (aux) VSK_HIP(hipStreamSynchronize(aux));
+      (void)hipHostFree(pinned);
+      pinned = nullptr;
+      pinned_bytes = 0;
+    }
+    VSK_HIP(hipHostMalloc(&pinned, bytes, hipHostMallocDefault));
+    pinned_bytes = bytes;
+  }
+  return pinned;
 }
 hipEvent_t vsk_ctx::take_event() {
   if (!event_pool.empty()) {
@@ -366,8 +386,11 @@ vsk_status vsk_destroy(vsk_ctx *ctx) {
   if (!ctx) return VSK_OK;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);
   ctx->resolve_pending();
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
+  if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
+  if (ctx->pinned) (void)hipHostFree(ctx->pinned);
   ctx->scratch.clear();
   (void)hipEventDestroy(ctx->call_begin);
   (void)hipEventDestroy(ctx->call_end);

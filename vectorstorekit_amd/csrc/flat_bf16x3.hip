@@ -639,6 +639,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     }
     const uint64_t *l_th = s_th + lq0;
     const int64_t *l_pb = s_pb + lq0;
+    uint64_t *l_t1 = s_t1 + wr * XS_Q + lq0;
+    float *l_t2 = s_t2 + wr * XS_Q + lq0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t qi = q0 + lq0 + 16 * j;
@@ -656,12 +658,15 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
                 vsk_key(dist_from_dot<METRIC>(acc[i][j][r], qa, xa), (uint32_t)row);
           }
       } else if constexpr (MODE == MODE_TOP2) {
-        // this lane's 16 rows in ascending order: the smallest distance
-        // (first one on a tie) and the second smallest (an equal distance
-        // counts: it makes the winner undecidable)
+        // The screened distance less the query's constant |q|^2,
+        // t = |x|^2 - 2 q.x (one FMA), with this lane's slot (lane group cl,
+        // score e) in its 6 low mantissa bits: min and median-of-three then
+        // keep the two smallest and the first one's position.  The packing
+        // moves t by under 64 ulp, within 2^-17 (|q| + |x|)^2, which the
+        // argmin's bound adds; equal screened distances stay within that of
+        // each other, so the bound test still refuses to decide them.
         const float inf = __int_as_float(0x7f800000);
         float m1 = inf, m2 = inf;
-        int b1 = -1;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -669,30 +674,35 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             const int e = 4 * i + r;
             const int64_t row = rbase + i * 16 + r;
             const float xa = (full || row < s1) ? a.xaux[row] : 0.f;
-            const float dd = dist_from_dot<METRIC>(acc[i][j][r], qa, xa);
-            const bool v = (vmask >> e) & 1u;
-            const bool lt = v && dd < m1;
-            m2 = lt ? m1 : (v ? fminf(m2, dd) : m2);
-            b1 = lt ? e : b1;
-            m1 = lt ? dd : m1;
+            float t = __builtin_fmaf(-2.0f, acc[i][j][r], xa);
+            t = __uint_as_float((__float_as_uint(t) & ~63u) | (uint32_t)e);
+            if (!full) t = ((vmask >> e) & 1u) ? t : inf;
+            m2 = __builtin_amdgcn_fmed3f(m1, m2, t);
+            m1 = fminf(m1, t);
           }
-        uint64_t k1 = b1 < 0 ? VSK_KEY_NONE
-                             : vsk_key(m1, (uint32_t)(rbase + 16 * (b1 >> 2) + (b1 & 3)));
+        // the lane group in bits 4-5 (all 16 scores share it)
+        if (m1 < inf) m1 = __uint_as_float(__float_as_uint(m1) | (uint32_t)(cl << 4));
         // the four lane groups hold other rows of the same query
 #pragma unroll
         for (int mk = 16; mk <= 32; mk <<= 1) {
-          const uint32_t lo = __shfl_xor((uint32_t)k1, mk);
-          const uint32_t hi = __shfl_xor((uint32_t)(k1 >> 32), mk);
-          const float mo = __shfl_xor(m2, mk);
-          top2_merge(k1, m2, ((uint64_t)hi << 32) | lo, mo);
+          const float o1 = __shfl_xor(m1, mk), o2 = __shfl_xor(m2, mk);
+          m2 = fminf(fmaxf(m1, o1), fminf(m2, o2));
+          m1 = fminf(m1, o1);
         }
         if (cl == 0 && l_ok[16 * j]) {
-          const int slot_i = wr * XS_Q + lq0 + 16 * j;  // this wave's own slot
-          uint64_t k = s_t1[slot_i];
-          float t2 = s_t2[slot_i];
-          top2_merge(k, t2, k1, m2);
-          s_t1[slot_i] = k;
-          s_t2[slot_i] = t2;
+          uint64_t k1 = VSK_KEY_NONE;
+          if (m1 < inf) {
+            const uint32_t pos = __float_as_uint(m1) & 63u;
+            const int64_t row = t0 + wr * 64 + 4 * (pos >> 4) + 16 * ((pos & 15) >> 2) + (pos & 3);
+            k1 = vsk_key(fmaxf(qa + m1, 0.f), (uint32_t)row);
+          }
+          const float a2 = m2 < inf ? fmaxf(qa + m2, 0.f) : inf;
+          // this wave's own slot
+          uint64_t k = l_t1[16 * j];
+          float t2 = l_t2[16 * j];
+          top2_merge(k, t2, k1, a2);
+          l_t1[16 * j] = k;
+          l_t2[16 * j] = t2;
         }
       } else {
         // a key can only pass when its distance is <= the threshold's (ties

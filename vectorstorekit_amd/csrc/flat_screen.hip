@@ -383,7 +383,8 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
                                 int64_t nq, const float *qnh, const float *qnr,
                                 const uint32_t *maxbits, int32_t d, const float *X,
                                 int64_t ld, const float *Q, int32_t *argmin, float *dist,
-                                int64_t qoff, int32_t *fail_idx, int32_t *nfail) {
+                                int64_t qoff, int32_t *fail_idx, uint64_t *fail_thr,
+                                int32_t *nfail) {
 #pragma clang fp contract(off)
   const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (q >= nq) return;
@@ -399,6 +400,7 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
     m2 = fminf(fminf(m2, mo), hd);
   }
   bool good = k != VSK_KEY_NONE;
+  double lim = 0.0;
   if (good) {
     CheckArgs ca{};
     ca.d = d;
@@ -407,13 +409,21 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
     ca.qnr = qnr;
     ca.xh = (double)__uint_as_float(maxbits[0]);
     ca.xr = (double)__uint_as_float(maxbits[1]);
-    const double eps = screen_eps(ca, q);
+    // plus the screen's packing of positions into the distances' low bits
+    const double qn = (double)qnh[q] + qnr[q], xn = ca.xh + ca.xr;
+    const double eps = screen_eps(ca, q) + 0x1p-16 * (qn + xn) * (qn + xn);
     const double a1 = vsk_ord2f((uint32_t)(k >> 32));
-    const double lim = (a1 + eps) * (1.0 + 0x1p-20) + eps;
+    lim = (a1 + eps) * (1.0 + 0x1p-20) + eps;
     good = (double)m2 > lim;
   }
   if (!good) {
-    fail_idx[atomicAdd(nfail, 1)] = (int32_t)(qoff + q);
+    // the rows that can still win have screened distance <= lim: the
+    // threshold of the collecting pass (+inf when nothing was screened)
+    float f = (float)lim;
+    if ((double)f < lim) f = __uint_as_float(__float_as_uint(f) + 1u);
+    const int32_t pos = atomicAdd(nfail, 1);
+    fail_idx[pos] = (int32_t)(qoff + q);
+    fail_thr[pos] = k == VSK_KEY_NONE ? VSK_KEY_NONE : vsk_key(f, 0xFFFFFFFFu);
     return;
   }
   const uint32_t row = (uint32_t)k;
@@ -425,6 +435,65 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
   }
   argmin[q] = (int32_t)row;
   dist[q] = sqrtf(s);
+}
+
+// gathers the undecided queries: their fp32 rows, hi-plane rows and |q|^2
+__global__ void k_gather_argmin_queries(const float *Q, int64_t ld, const uint16_t *qh,
+                                        int32_t ldb, const float *qsq, const int32_t *idx,
+                                        int64_t m, float *Q2, uint16_t *qh2, float *qsq2) {
+  const int64_t i = blockIdx.x;
+  if (i >= m) return;
+  const int64_t src = idx[i];
+  for (int64_t c = threadIdx.x; c < ld; c += blockDim.x) Q2[i * ld + c] = Q[src * ld + c];
+  for (int64_t c = threadIdx.x; c < ldb; c += blockDim.x) qh2[i * ldb + c] = qh[src * ldb + c];
+  if (threadIdx.x == 0) qsq2[i] = qsq[src];
+}
+
+// The collected candidates of each undecided query: one wave per query, a
+// lane per slot; lanes holding a candidate compute its exact distance in
+// dimension order (no FMA) and the wave keeps the smallest (distance, row).
+// A query whose candidates overflowed (count > cap) or that had none is
+// listed for the exact scan.  cap <= 64.
+__global__ __launch_bounds__(64) void k_argmin_collect(
+    const uint64_t *cand, int32_t cap, const int32_t *counts, int64_t m, const float *X,
+    int64_t ld, const float *Q, int32_t d, const int32_t *idx, int32_t *argmin, float *dist,
+    int32_t *redo, int32_t *nredo) {
+#pragma clang fp contract(off)
+  const int64_t i = blockIdx.x;
+  const int lane = threadIdx.x;
+  if (i >= m) return;
+  const uint64_t key = lane < cap ? cand[i * cap + lane] : VSK_KEY_NONE;
+  uint64_t best = VSK_KEY_NONE;
+  if (key != VSK_KEY_NONE) {
+    const uint32_t row = (uint32_t)key;
+    const float *qq = Q + i * ld, *xx = X + (int64_t)row * ld;
+    float s = 0.f;
+    for (int32_t j = 0; j < d; ++j) {
+      const float t = qq[j] - xx[j];
+      s = s + t * t;
+    }
+    best = vsk_key(sqrtf(s), row);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)best, o), hi = __shfl_xor((uint32_t)(best >> 32), o);
+    const uint64_t v = ((uint64_t)hi << 32) | lo;
+    best = v < best ? v : best;
+  }
+  if (lane != 0) return;
+  if (counts[i] > cap || best == VSK_KEY_NONE) {
+    redo[atomicAdd(nredo, 1)] = (int32_t)i;
+    return;
+  }
+  argmin[idx[i]] = (int32_t)(uint32_t)best;
+  dist[idx[i]] = vsk_ord2f((uint32_t)(best >> 32));
+}
+
+// out[i] = map[idx[i]]
+__global__ void k_map_index(const int32_t *idx, const int32_t *map, int64_t m, int32_t *out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = map[idx[i]];
 }
 
 __global__ void k_scatter_argmin(const int32_t *src_a, const float *src_d, int64_t m,
@@ -497,6 +566,8 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
   int32_t *fidx = static_cast<int32_t *>(
       ctx->scratch_ptr("sam.fidx", sizeof(int32_t) * (size_t)(nq + 1)));
   int32_t *nfail = fidx + nq;
+  uint64_t *fthr = static_cast<uint64_t *>(
+      ctx->scratch_ptr("sam.fthr", sizeof(uint64_t) * (size_t)nq));
   fill_i32(ctx, nfail, 1, 0);
   for (int64_t b0 = 0; b0 < nq; b0 += qb_max) {
     const int64_t nb = nq - b0 < qb_max ? nq - b0 : qb_max;
@@ -525,29 +596,88 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
       fail(VSK_ERR_EXECUTION_FAILED, "argmin screen: unexpected split count");
     k_argmin_finish<<<(unsigned)ceil_div(nb, 256), 256, 0, ctx->stream>>>(
         k1, a2, nsplit, nb, qp.qnh + b0, qp.qnr + b0, maxbits, d, X, ld, dq + b0 * ld,
-        argmin + b0, dist + b0, b0, fidx, nfail);
+        argmin + b0, dist + b0, b0, fidx, fthr, nfail);
     check_launch("screen_argmin_finish");
   }
   int32_t hf = 0;
   VSK_HIP(hipMemcpyAsync(&hf, nfail, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
   VSK_HIP(hipStreamSynchronize(ctx->stream));
   if (hf == 0) return;
-  // near ties: the exact VALU argmin over every row for those queries
-  KernelTimer tf(ctx, "screen_argmin_fallback", (double)hf);
+  // Undecided queries (near ties).  A second screen pass over them keeps
+  // every row whose screened distance is within their limit (at most
+  // kCollect per query, kCollect / 8 per row split), those rows' exact
+  // distances are computed in dimension order and the smallest key wins.  A query with more candidates than that is redone by the exact
+  // VALU scan over every row.
+  constexpr int32_t kCollect = 64;
   const int64_t m = hf;
+  KernelTimer tf(ctx, "screen_argmin_collect", (double)m);
   float *q2 = static_cast<float *>(ctx->scratch_ptr("sam.fq", sizeof(float) * (size_t)m * ld));
-  k_gather_rows<<<grid_for(m * ld), 256, 0, ctx->stream>>>(dq, ld, fidx, m, q2);
+  uint16_t *qh2 = static_cast<uint16_t *>(
+      ctx->scratch_ptr("sam.fqh", sizeof(uint16_t) * (size_t)m * ldb));
+  float *qsq2 = static_cast<float *>(ctx->scratch_ptr("sam.fqsq", sizeof(float) * (size_t)m));
+  k_gather_argmin_queries<<<(unsigned)m, 128, 0, ctx->stream>>>(dq, ld, qp.qh, ldb, qp.qsq,
+                                                                 fidx, m, q2, qh2, qsq2);
   check_launch("screen_argmin_gather");
-  int32_t *a_out = static_cast<int32_t *>(
-      ctx->scratch_ptr("sam.fa", (sizeof(int32_t) + sizeof(float)) * (size_t)m));
-  float *d_out = reinterpret_cast<float *>(a_out + m);
-  const int64_t chunk = 1 << 24;
-  for (int64_t r = 0; r < m; r += chunk) {
-    const int64_t mm = m - r < chunk ? m - r : chunk;
+  uint64_t *cand = static_cast<uint64_t *>(
+      ctx->scratch_ptr("sam.cand", sizeof(uint64_t) * (size_t)m * kCollect));
+  int32_t *cnt = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.ccnt", sizeof(int32_t) * (size_t)m));
+  int32_t *redo = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.redo", sizeof(int32_t) * ((size_t)m + 1)));
+  int32_t *nredo = redo + m;
+  // slots no workgroup reserves are never written: they must read as empty
+  fill_u64(ctx, cand, m * kCollect, VSK_KEY_NONE);
+  fill_i32(ctx, cnt, m, 0);
+  fill_i32(ctx, nredo, 1, 0);
+  for (int64_t r0 = 0; r0 < m; r0 += qb_max) {
+    const int64_t mb = m - r0 < qb_max ? m - r0 : qb_max;
     FlatArgs a{};
     a.X = X;
     a.ldx = ld;
-    a.Q = q2 + r * ld;
+    a.Q = q2 + r0 * ld;
+    a.ldq = ld;
+    a.xaux = xsq;
+    a.qaux = qsq2 + r0;
+    a.kdim = ld;
+    a.nq = (int32_t)mb;
+    a.r0 = 0;
+    a.r1 = n;
+    a.metric = VSK_METRIC_L2SQ;
+    a.thresh = fthr + r0;
+    a.cand = cand + r0 * kCollect;
+    a.cap = kCollect;
+    a.counts = cnt + r0;
+    SplitPtrs sb = sp;
+    sb.qh = qh2 + r0 * ldb;
+    launch_flat_screen(ctx, a, sb, MODE_FILTER, nullptr, nullptr);
+  }
+  k_argmin_collect<<<(unsigned)m, 64, 0, ctx->stream>>>(cand, kCollect, cnt, m, X, ld, q2, d,
+                                                        fidx, argmin, dist, redo, nredo);
+  check_launch("screen_argmin_collect");
+  int32_t hr = 0;
+  VSK_HIP(hipMemcpyAsync(&hr, nredo, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  if (hr == 0) return;
+  // overflowing candidate lists: the exact VALU argmin over every row
+  KernelTimer tv(ctx, "screen_argmin_fallback", (double)hr);
+  const int64_t mr = hr;
+  float *q3 = static_cast<float *>(ctx->scratch_ptr("sam.rq", sizeof(float) * (size_t)mr * ld));
+  k_gather_rows<<<grid_for(mr * ld), 256, 0, ctx->stream>>>(q2, ld, redo, mr, q3);
+  check_launch("screen_argmin_gather");
+  int32_t *ridx = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.ridx", sizeof(int32_t) * (size_t)mr));
+  k_map_index<<<grid_for(mr), 256, 0, ctx->stream>>>(redo, fidx, mr, ridx);
+  check_launch("screen_argmin_map");
+  int32_t *a_out = static_cast<int32_t *>(
+      ctx->scratch_ptr("sam.fa", (sizeof(int32_t) + sizeof(float)) * (size_t)mr));
+  float *d_out = reinterpret_cast<float *>(a_out + mr);
+  const int64_t chunk = 1 << 24;
+  for (int64_t r = 0; r < mr; r += chunk) {
+    const int64_t mm = mr - r < chunk ? mr - r : chunk;
+    FlatArgs a{};
+    a.X = X;
+    a.ldx = ld;
+    a.Q = q3 + r * ld;
     a.ldq = ld;
     a.kdim = ld;
     a.nq = (int32_t)mm;
@@ -557,7 +687,8 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
     a.amin = d_out + r;
     launch_flat(ctx, a, MODE_ARGMIN, a_out + r);
   }
-  k_scatter_argmin<<<grid_for(m), 256, 0, ctx->stream>>>(a_out, d_out, m, fidx, argmin, dist);
+  k_scatter_argmin<<<grid_for(mr), 256, 0, ctx->stream>>>(a_out, d_out, mr, ridx, argmin,
+                                                          dist);
   check_launch("screen_argmin_scatter");
 }
 

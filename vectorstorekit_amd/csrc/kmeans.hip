@@ -17,9 +17,13 @@
 //               that order, x * weight then +=, and divides by the fp32
 //               count (:342-380), so every centroid is bit-identical to the
 //               reference's sequential loop.
-// The host reads the counts and the inertia once per iteration: it tests
-// convergence (|inertia - previous| < tolerance, :98) and refills empty
-// clusters with a seeded draw (the reference's draw, :374, is unseeded).
+// Empty clusters are refilled on the device from a seeded draw (the
+// reference's draw, :374, is unseeded).  The inertia is summed on a second
+// stream while the next iteration already runs; the host reads it back
+// (pinned memory) and tests convergence (|inertia - previous| < tolerance,
+// :98).  An iteration started past convergence writes only the other halves
+// of the double-buffered centroids, assignments and distances, and is
+// dropped.
 //
 // k-means++ (:209-259) picks each next centroid with probability
 // proportional to D(x)^2, D the distance to the nearest chosen centroid.  The
@@ -279,6 +283,30 @@ __global__ __launch_bounds__(64) void k_cluster_means(
   const float cnt = weights ? cw : (m > (1 << 24) ? 16777216.f : (float)m);
   if (colok) cent[c * ld + col] = (col < d && cnt > 0.f) ? s / cnt : 0.f;
   if (blockIdx.y == 0 && lane == 0) cntf[c] = cnt;
+}
+
+// empty clusters (fp32 count not > 0) in ascending order each take row
+// Int.random(in: 0..<n) of the SeedableRNG stream whose state is *rng: one
+// wave, every lane draws the same sequence, the lanes copy the row
+__global__ __launch_bounds__(64) void k_refill_empty(const float *cntf, int32_t k,
+                                                     const float *x, int64_t ld, int32_t d,
+                                                     int64_t n, uint64_t *rng, float *cent) {
+  const int lane = threadIdx.x;
+  uint64_t st = *rng;
+  for (int32_t c0 = 0; c0 < k; c0 += 64) {
+    const int32_t c = c0 + lane;
+    const bool empty = c < k && !(cntf[c] > 0.f);
+    uint64_t mask = __builtin_amdgcn_ballot_w64(empty);
+    while (mask) {
+      const int b = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int64_t r = (int64_t)swift_bounded(st, (uint64_t)n);
+      const float *src = x + r * ld;
+      float *dst = cent + (int64_t)(c0 + b) * ld;
+      for (int32_t j = lane; j < d; j += 64) dst[j] = src[j];
+    }
+  }
+  if (lane == 0) *rng = st;
 }
 
 __global__ void k_gather_rows_i64(const float *src, int64_t ld, const int64_t *rows,
@@ -622,11 +650,11 @@ vsk_status vsk_kmeans(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
                             : nullptr;
   float *cbuf = static_cast<float *>(
       ctx->scratch_ptr("km.cent", sizeof(float) * 2 * (size_t)k * ld));
-  float *cur = cbuf, *nxt = cbuf + (size_t)k * ld;
+  float *cur0 = cbuf;
   // starting centroids
   if (init_method == VSK_KMEANS_INIT_CUSTOM) {
-    if (ld != d) fill_i32(ctx, reinterpret_cast<int32_t *>(cur), (int64_t)k * ld, 0);
-    copy_rows(ctx, cur, sizeof(float) * ld, init_centroids, sizeof(float) * d,
+    if (ld != d) fill_i32(ctx, reinterpret_cast<int32_t *>(cur0), (int64_t)k * ld, 0);
+    copy_rows(ctx, cur0, sizeof(float) * ld, init_centroids, sizeof(float) * d,
               sizeof(float) * d, k);
   } else {
     int64_t *rows = static_cast<int64_t *>(
@@ -642,58 +670,78 @@ vsk_status vsk_kmeans(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
                   "data is degenerate (all points are identical)");
     }
     k_gather_rows_i64<<<grid1d((int64_t)k * ld, 256), 256, 0, ctx->stream>>>(
-        dx, ld, rows, k, cur);
+        dx, ld, rows, k, cur0);
     check_launch("kmeans_gather");
   }
-  int32_t *assign = static_cast<int32_t *>(
-      ctx->scratch_ptr("km.assign", sizeof(int32_t) * (size_t)n));
-  float *dist = static_cast<float *>(ctx->scratch_ptr("km.dist", sizeof(float) * (size_t)n));
+  // assignments and distances double-buffered: iteration i + 1 runs while
+  // iteration i's inertia is summed on the auxiliary stream
+  int32_t *assign2 = static_cast<int32_t *>(
+      ctx->scratch_ptr("km.assign", sizeof(int32_t) * 2 * (size_t)n));
+  float *dist2 = static_cast<float *>(
+      ctx->scratch_ptr("km.dist", sizeof(float) * 2 * (size_t)n));
   int32_t *counts = static_cast<int32_t *>(
       ctx->scratch_ptr("km.counts", sizeof(int32_t) * 2 * (size_t)k));
   int32_t *off = counts + k;
-  // [inertia, fp32 counts[k]]: read back once per iteration
-  float *view = static_cast<float *>(ctx->scratch_ptr("km.view", sizeof(float) * (size_t)(k + 1)));
-  std::vector<float> hview((size_t)k + 1);
-  fill_i32(ctx, assign, n, 0);
+  float *cntf = static_cast<float *>(ctx->scratch_ptr("km.cntf", sizeof(float) * (size_t)k));
+  float *dinert = static_cast<float *>(ctx->scratch_ptr("km.inertia", 2 * sizeof(float)));
+  uint64_t *rng = static_cast<uint64_t *>(ctx->scratch_ptr("km.rng", sizeof(uint64_t)));
+  fill_u64(ctx, rng, 1, seed + 0x9E3779B97F4A7C15ull);
+  float *h_inert = static_cast<float *>(ctx->pinned_ptr(2 * sizeof(float)));
+  hipStream_t aux = ctx->aux_stream();
+  hipEvent_t ev_assigned[2] = {ctx->take_event(), ctx->take_event()};
+  hipEvent_t ev_summed[2] = {ctx->take_event(), ctx->take_event()};
   // the rows' bf16 planes for the screened assignment, made once
   ArgminQueries qp;
   if (max_iter > 0 && screen_argmin_applies(ctx, n, k, d))
     qp = argmin_queries(ctx, dx, n, d, ld, "km.q");
-  uint64_t empty_rng = seed + 0x9E3779B97F4A7C15ull;
-  float prev = INFINITY;
-  int32_t it = 0;
-  bool conv = false;
-  while (it < max_iter && !conv) {
+  // one Lloyd iteration i: centroids cbuf[i & 1] -> cbuf[(i + 1) & 1]
+  auto enqueue = [&](int32_t i) {
+    const float *cur = cbuf + (size_t)(i & 1) * k * ld;
+    float *nxt = cbuf + (size_t)((i + 1) & 1) * k * ld;
+    int32_t *assign = assign2 + (size_t)(i & 1) * n;
+    float *dist = dist2 + (size_t)(i & 1) * n;
     kmeans_assign(ctx, cur, k, d, ld, dx, n, qp, assign, dist);
+    VSK_HIP(hipEventRecord(ev_assigned[i & 1], ctx->stream));
+    VSK_HIP(hipStreamWaitEvent(aux, ev_assigned[i & 1], 0));
     {
-      KernelTimer tm(ctx, "kmeans_inertia", (double)n);
-      k_seq_sum<<<1, 64, 0, ctx->stream>>>(dist, n, view);
+      KernelTimer tm(ctx, "kmeans_inertia", (double)n, aux);
+      k_seq_sum<<<1, 64, 0, aux>>>(dist, n, dinert + (i & 1));
       check_launch("kmeans_inertia");
     }
+    VSK_HIP(hipMemcpyAsync(h_inert + (i & 1), dinert + (i & 1), sizeof(float),
+                           hipMemcpyDeviceToHost, aux));
+    VSK_HIP(hipEventRecord(ev_summed[i & 1], aux));
     const int32_t *order = nullptr;
     group_rows(ctx, assign, n, k, counts, off, &order);
     {
       KernelTimer tm(ctx, "kmeans_means", (double)n * d);
       dim3 grid((unsigned)k, (unsigned)ceil_div(ld, 64));
-      k_cluster_means<<<grid, 64, 0, ctx->stream>>>(dx, ld, d, order, off, counts, dw,
-                                                    nxt, view + 1);
+      k_cluster_means<<<grid, 64, 0, ctx->stream>>>(dx, ld, d, order, off, counts, dw, nxt,
+                                                    cntf);
       check_launch("kmeans_means");
     }
-    VSK_HIP(hipMemcpyAsync(hview.data(), view, sizeof(float) * (k + 1),
-                           hipMemcpyDeviceToHost, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
-    for (int32_t c = 0; c < k; ++c) {
-      if (hview[(size_t)c + 1] > 0.f) continue;
-      const int64_t r = (int64_t)swift_bounded(empty_rng, (uint64_t)n);
-      VSK_HIP(hipMemcpyAsync(nxt + (size_t)c * ld, dx + r * ld, sizeof(float) * d,
-                             hipMemcpyDeviceToDevice, ctx->stream));
-    }
-    const float inertia = hview[0];
+    k_refill_empty<<<1, 64, 0, ctx->stream>>>(cntf, k, dx, ld, d, n, rng, nxt);
+    check_launch("kmeans_refill");
+  };
+  float prev = INFINITY;
+  int32_t it = 0;
+  bool conv = false;
+  if (max_iter > 0) enqueue(0);
+  while (it < max_iter && !conv) {
+    // the next iteration goes in before this one's inertia is known; if
+    // this one converged, its results (other buffers) are discarded
+    if (it + 1 < max_iter) enqueue(it + 1);
+    VSK_HIP(hipEventSynchronize(ev_summed[it & 1]));
+    const float inertia = h_inert[it & 1];
     conv = fabsf(inertia - prev) < tolerance;
     prev = inertia;
-    std::swap(cur, nxt);
     ++it;
   }
+  for (hipEvent_t e : {ev_assigned[0], ev_assigned[1], ev_summed[0], ev_summed[1]})
+    ctx->event_pool.push_back(e);
+  const float *cur = cbuf + (size_t)(it & 1) * k * ld;
+  const int32_t *assign = assign2 + (size_t)((it + 1) & 1) * n;  // iteration it - 1
+  if (it == 0) fill_i32(ctx, assign2 + n, n, 0);
   copy_rows(ctx, out_centroids, sizeof(float) * d, cur, sizeof(float) * ld,
             sizeof(float) * d, k);
   if (out_assign)

@@ -18,6 +18,7 @@
   catch (const ::vsk::Error &e) {                                             \
     (ctx)->last_error = e.msg;                                                \
     (void)hipStreamSynchronize((ctx)->stream);                                \
+    if ((ctx)->aux) (void)hipStreamSynchronize((ctx)->aux);                   \
     (void)hipGetLastError();                                                  \
     return e.code;                                                            \
   }                                                                           \

@@ -58,6 +58,14 @@ struct vsk_ctx {
   int device = 0;
   int cu_count = 256;  // compute units of the device
   hipStream_t stream = nullptr;
+  // a second stream for work a call overlaps with its own kernels (created
+  // on first use, default priority; every call still returns synchronised)
+  hipStream_t aux = nullptr;
+  hipStream_t aux_stream();
+  // a small pinned host buffer for asynchronous read-backs (grown on use)
+  void *pinned = nullptr;
+  size_t pinned_bytes = 0;
+  void *pinned_ptr(size_t bytes);
   std::string last_error;
   float last_ms = 0.f;
   hipEvent_t call_begin = nullptr, call_end = nullptr;
@@ -120,7 +128,9 @@ struct KernelTimer {
   int stat = -1;
   hipEvent_t a = nullptr;
   double work = 0;
-  KernelTimer(vsk_ctx *c, const char *name, double work_items = 0);
+  hipStream_t stream = nullptr;
+  // times on stream s (default: the context's stream)
+  KernelTimer(vsk_ctx *c, const char *name, double work_items = 0, hipStream_t s = nullptr);
   ~KernelTimer();
 };
 
