@@ -395,7 +395,8 @@ constexpr int XS_STAGE = (XS_N + XS_Q) * XS_R;  // bytes per stage buffer
 constexpr int XS_LDS = 2 * XS_STAGE + 6 * XS_Q * 4 + 2 * XS_Q * 8;
 // MODE_TOP2: a (smallest key, second smallest distance) slot per row wave
 // and query
-constexpr int XS_LDS_TOP2 = XS_LDS + 4 * XS_Q * (8 + 4);
+// and the row norms of four row tiles (copied with the tile's first stage)
+constexpr int XS_LDS_TOP2 = XS_LDS + 4 * XS_Q * (8 + 4) + 4 * XS_N * 4;
 static_assert(XS_LDS_TOP2 <= 160 * 1024, "LDS of one workgroup");
 
 __device__ __forceinline__ float top2_keydist(uint64_t k) {
@@ -422,9 +423,12 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   const int wr = w & 3, wq = w >> 2;
   const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
   const int sx = a.splits_per_xcd;
-  const int grp = slot / (XS_GQ * sx), rem = slot - grp * (XS_GQ * sx);
-  const int qtile = grp * XS_GQ + rem % XS_GQ;
-  const int split = (rem / XS_GQ) * 8 + xcd;
+  // sx == 0: one split, workgroup L takes query tile L over every row (the
+  // argmin with many queries: the rows stay in every XCD's L2, each query is
+  // read once)
+  const int grp = sx ? slot / (XS_GQ * sx) : 0, rem = sx ? slot - grp * (XS_GQ * sx) : 0;
+  const int qtile = sx ? grp * XS_GQ + rem % XS_GQ : L;
+  const int split = sx ? (rem / XS_GQ) * 8 + xcd : 0;
   const int64_t q0 = (int64_t)qtile * XS_Q;
   if (q0 >= a.nq) return;
   const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
@@ -460,6 +464,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   int64_t *s_pb = reinterpret_cast<int64_t *>(s_th + XS_Q);
   uint64_t *s_t1 = reinterpret_cast<uint64_t *>(lds + XS_LDS);  // [4][XS_Q]
   float *s_t2 = reinterpret_cast<float *>(s_t1 + 4 * XS_Q);
+  float *s_xa = s_t2 + 4 * XS_Q;  // [4][XS_N]: |x|^2 of row tile t in slot t & 3
   if constexpr (MODE == MODE_TOP2) {
     for (int i = tid; i < 4 * XS_Q; i += 512) {
       s_t1[i] = VSK_KEY_NONE;
@@ -527,12 +532,23 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   }
   int dst = 0;          // next stage to copy: stage dst of the tile at dt0
   int64_t dt0 = s0;     // (past the slice: zero-length rows, nothing read)
+  int dtile = 0;        // index of that tile in the slice
   int dbuf = 0;
   auto copy_next = [&]() {
     const int64_t left = s1 - dt0;
     const int64_t rows = left < XS_N ? (left > 0 ? left : 0) : XS_N;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(s.xh + dt0 * s.ldxb), 0, (int32_t)(rows * ldx2), kBufFlags);
+    if constexpr (MODE == MODE_TOP2) {
+      if (dst == 0 && w < 4) {
+        // the tile's row norms, 64 per wave (rows past the slice read 0)
+        const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(a.xaux + dt0), 0, (int32_t)(rows * 4), kBufFlags);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rn, (__attribute__((address_space(3))) void *)(s_xa + (dtile & 3) * XS_N + 64 * w),
+            4, lane * 4, w * 256, 0, 0);
+      }
+    }
     uint8_t *bx = lds + dbuf * XS_STAGE + 4 * w * 1024;
     const int32_t kofs = dst * XS_K * 2;
 #pragma unroll
@@ -548,6 +564,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     if (++dst == nst) {
       dst = 0;
       dt0 += XS_N;
+      ++dtile;
     }
   };
   // operands: two sets, this step's and the next one's (read one step ahead)
@@ -569,7 +586,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this wave's copies of stage 0
   __builtin_amdgcn_s_barrier();
   int g = 0;  // stage of the sequence being multiplied
-  for (int64_t t0 = s0; t0 < s1; t0 += XS_N) {
+  int tcur = 0;  // index of the tile being multiplied
+  for (int64_t t0 = s0; t0 < s1; t0 += XS_N, ++tcur) {
     // the tile's first operands are read here rather than before the
     // previous epilogue, which then has the registers to itself
     read_ops(lds + (g & 1) * XS_STAGE, 0, 0);
@@ -672,8 +690,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int e = 4 * i + r;
-            const int64_t row = rbase + i * 16 + r;
-            const float xa = (full || row < s1) ? a.xaux[row] : 0.f;
+            const float xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r];
             float t = __builtin_fmaf(-2.0f, acc[i][j][r], xa);
             t = __uint_as_float((__float_as_uint(t) & ~63u) | (uint32_t)e);
             if (!full) t = ((vmask >> e) & 1u) ? t : inf;
@@ -881,6 +898,12 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
   }
   a.rows_per_split = ceil_div(tiles, splits) * XS_N;
   a.splits_per_xcd = (int32_t)(splits / 8);
+  if (mode == MODE_TOP2 && qt >= 2 * (int64_t)ctx->cu_count) {
+    // enough query tiles to fill the chip twice: one split over every row
+    splits = 1;
+    a.rows_per_split = tiles * XS_N;
+    a.splits_per_xcd = 0;
+  }
   // reserved slots per (workgroup, query), all splits within cap
   a.sub = 0;
   if (mode == MODE_FILTER) {
@@ -901,7 +924,7 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     *stride = a.sub;
   }
   const int64_t groups = ceil_div(qt, XS_GQ);
-  const int64_t nblocks = 8 * a.splits_per_xcd * groups * XS_GQ;
+  const int64_t nblocks = a.splits_per_xcd ? 8 * a.splits_per_xcd * groups * XS_GQ : qt;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
   static const char *names[5] = {"flat_screen_dense", "flat_screen_filter", "",
                                  "", "flat_screen_top2"};

@@ -379,27 +379,37 @@ static void redo_queries(vsk_ctx *ctx, const vsk_db *db, const float *qbat,
 // One thread per query merges the row splits' pairs, tests the bound and
 // recomputes the winner's exact distance in dimension order (no FMA);
 // queries failing the test are listed for the exact VALU scan.
-__global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsplit,
-                                int64_t nq, const float *qnh, const float *qnr,
-                                const uint32_t *maxbits, int32_t d, const float *X,
-                                int64_t ld, const float *Q, int32_t *argmin, float *dist,
-                                int64_t qoff, int32_t *fail_idx, uint64_t *fail_thr,
-                                int32_t *nfail) {
+// One wave per 64 queries.  Each lane merges its query's split pairs and
+// tests the bound; then, per 64-dim block, the wave gathers the 64 query
+// rows and the 64 winners' rows in 256-byte segments (16 lanes per row) into
+// LDS and every lane continues its own sequential sum from there (no FMA),
+// so the winners' exact distances come from coalesced reads.
+__global__ __launch_bounds__(64) void k_argmin_finish(
+    const uint64_t *k1, const float *a2, int32_t nsplit, int64_t nq, const float *qnh,
+    const float *qnr, const uint32_t *maxbits, int32_t d, const float *X, int64_t ld,
+    const float *Q, int32_t *argmin, float *dist, int64_t qoff, int32_t *fail_idx,
+    uint64_t *fail_thr, int32_t *nfail) {
 #pragma clang fp contract(off)
-  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (q >= nq) return;
+  __shared__ __attribute__((aligned(16))) float tq[64 * RS_LD];
+  __shared__ __attribute__((aligned(16))) float tx[64 * RS_LD];
+  const int lane = threadIdx.x;
+  const int64_t qb = (int64_t)blockIdx.x * 64;
+  const int64_t q = qb + lane;
+  const bool live = q < nq;
   uint64_t k = VSK_KEY_NONE;
   float m2 = __int_as_float(0x7f800000);
-  for (int32_t sp = 0; sp < nsplit; ++sp) {
-    const uint64_t ko = k1[q * nsplit + sp];
-    const float mo = a2[q * nsplit + sp];
-    const uint64_t hi = ko < k ? k : ko;
-    k = ko < k ? ko : k;
-    const float hd = hi == VSK_KEY_NONE ? __int_as_float(0x7f800000)
-                                        : vsk_ord2f((uint32_t)(hi >> 32));
-    m2 = fminf(fminf(m2, mo), hd);
+  if (live) {
+    for (int32_t sp = 0; sp < nsplit; ++sp) {
+      const uint64_t ko = k1[q * nsplit + sp];
+      const float mo = a2[q * nsplit + sp];
+      const uint64_t hi = ko < k ? k : ko;
+      k = ko < k ? ko : k;
+      const float hd = hi == VSK_KEY_NONE ? __int_as_float(0x7f800000)
+                                          : vsk_ord2f((uint32_t)(hi >> 32));
+      m2 = fminf(fminf(m2, mo), hd);
+    }
   }
-  bool good = k != VSK_KEY_NONE;
+  bool good = live && k != VSK_KEY_NONE;
   double lim = 0.0;
   if (good) {
     CheckArgs ca{};
@@ -416,7 +426,7 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
     lim = (a1 + eps) * (1.0 + 0x1p-20) + eps;
     good = (double)m2 > lim;
   }
-  if (!good) {
+  if (live && !good) {
     // the rows that can still win have screened distance <= lim: the
     // threshold of the collecting pass (+inf when nothing was screened)
     float f = (float)lim;
@@ -424,17 +434,50 @@ __global__ void k_argmin_finish(const uint64_t *k1, const float *a2, int32_t nsp
     const int32_t pos = atomicAdd(nfail, 1);
     fail_idx[pos] = (int32_t)(qoff + q);
     fail_thr[pos] = k == VSK_KEY_NONE ? VSK_KEY_NONE : vsk_key(f, 0xFFFFFFFFu);
-    return;
   }
-  const uint32_t row = (uint32_t)k;
-  const float *qq = Q + q * ld, *xx = X + (int64_t)row * ld;
+  if (!__builtin_amdgcn_ballot_w64(good)) return;
+  // the exact distance of each decided query's winner
+  const uint32_t row = good ? (uint32_t)k : 0u;
+  const int64_t myq = live ? q : qb;  // lanes past nq gather the block's first query
+  const int seg = lane & 15, sub = lane >> 4;
+  const float *qsrc[16], *xsrc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qsrc[i] = Q + (int64_t)__shfl((int)myq - (int)qb, sub + 4 * i) * ld + qb * ld;
+    xsrc[i] = X + (int64_t)__shfl(row, sub + 4 * i) * ld;
+  }
+  const int32_t cmax = (int32_t)ld - 4;  // a segment past the row end is clamped
   float s = 0.f;
-  for (int32_t j = 0; j < d; ++j) {
-    const float t = qq[j] - xx[j];
-    s = s + t * t;
+  for (int32_t j0 = 0; j0 < d; j0 += RS_W) {
+    const int32_t col = j0 + 4 * seg < cmax ? j0 + 4 * seg : cmax;
+    rs_f4 bq[16], bx[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      bq[i] = *reinterpret_cast<const rs_f4 *>(qsrc[i] + col);
+      bx[i] = *reinterpret_cast<const rs_f4 *>(xsrc[i] + col);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      *reinterpret_cast<rs_f4 *>(tq + (sub + 4 * i) * RS_LD + 4 * seg) = bq[i];
+      *reinterpret_cast<rs_f4 *>(tx + (sub + 4 * i) * RS_LD + 4 * seg) = bx[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int32_t jn = d - j0 < RS_W ? d - j0 : RS_W;
+    const float *qr = tq + lane * RS_LD, *xr = tx + lane * RS_LD;
+    for (int32_t j = 0; j < jn; ++j) {
+      const float t = qr[j] - xr[j];
+      s = s + t * t;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  argmin[q] = (int32_t)row;
-  dist[q] = sqrtf(s);
+  if (good) {
+    argmin[q] = (int32_t)row;
+    dist[q] = sqrtf(s);
+  }
 }
 
 // gathers the undecided queries: their fp32 rows, hi-plane rows and |q|^2
@@ -592,9 +635,9 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
     fill_i32(ctx, reinterpret_cast<int32_t *>(a2), nb * top, 0x7f800000);
     int32_t nsplit = 0;
     launch_flat_screen(ctx, a, sb, MODE_TOP2, &nsplit, nullptr);
-    if (nsplit < 8 || nsplit > top)
+    if (nsplit < 1 || nsplit > top)
       fail(VSK_ERR_EXECUTION_FAILED, "argmin screen: unexpected split count");
-    k_argmin_finish<<<(unsigned)ceil_div(nb, 256), 256, 0, ctx->stream>>>(
+    k_argmin_finish<<<(unsigned)ceil_div(nb, 64), 64, 0, ctx->stream>>>(
         k1, a2, nsplit, nb, qp.qnh + b0, qp.qnr + b0, maxbits, d, X, ld, dq + b0 * ld,
         argmin + b0, dist + b0, b0, fidx, fthr, nfail);
     check_launch("screen_argmin_finish");
