@@ -16,7 +16,9 @@ The other BASELINE configs are measured with ``--config``:
   k = 100 (one step = one vsk_pq_search);
 * ``c3train`` IVF coarse training on config 3's data: k-means of 1M x 128
   rows into 4,096 clusters, 10 Lloyd iterations per step (vsk_kmeans),
-  reported as row-iterations/s.
+  reported as row-iterations/s;
+* ``c4bin`` binary quantization of config 4's data (10M x 128 -> 16-byte
+  codes), 1,000 queries, Hamming top-100 (vsk_bin_search).
 
 Each prints one JSON line: QPS (value), the roofline of the dominant kernel
 (algorithmic FLOP/OP or bytes per (query, row) pair the library counted for
@@ -48,7 +50,7 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
 PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
-                 "c3train": (2, 1)}
+                 "c3train": (2, 1), "c4bin": (5, 1)}
 
 
 def parse():
@@ -280,6 +282,50 @@ def setup(a, ctx, dev):
         }
         return spec, step, cpu_leg
 
+    if c == "c4bin":
+        # binary quantization of config 4's data (one bit per dimension,
+        # x > 0) and the Hamming top-k scan (vsk_bin_search)
+        from vectorstorekit_amd import BinaryDatabase, BinaryQuantizer
+        n, d, nq, k = 10_000_000, 128, 1000, 100
+        x, q = gen_flat(n, d, nq, False, dev)
+        bq = BinaryQuantizer(ctx)
+        xc, qc = bq.quantizeBatch(x), bq.quantizeBatch(q)
+        del x
+        db = BinaryDatabase(ctx, xc, d)
+        dist = torch.empty(nq, k, dtype=torch.int32, device=dev)
+        ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+
+        def step():
+            ctx.check(lib.vsk_bin_search(ctx.handle, db.handle, qc.data_ptr(), nq, k,
+                                         dist.data_ptr(), ids.data_ptr()))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            xh, qh = xc.cpu().numpy(), qc.cpu().numpy()
+            th = host_threads()
+            qps, m, reps, el, (od, oi) = cpu_sample(
+                lambda m: O.bin_search(qh[:m], xh, d, k, threads=th), nq, target_s, th)
+            gd, gi = dist.cpu().numpy()[:m], ids.cpu().numpy()[:m]
+            exact = {"queries": m, "ids_equal": bool((gi == oi).all()),
+                     "distances_equal": bool((gd == od).all())}
+            return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "sample": f"first {m} of {nq} queries against all {n} codes, {reps} "
+                               f"pass(es) ({el:.1f} s)", "exact_oracle_check": exact},
+                    id_agreement(gi, oi))
+
+        spec = {
+            "metric": "QPS @k=100, binary Hamming 10M x 128 bits",
+            "workload": "bin-hamming-10Mx128-q1000-k100 (BASELINE config 4 data, binary codes)",
+            "config": {"n": n, "d": d, "nq": nq, "k": k, "metric": "popcount(q xor x)"},
+            "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), one bit "
+                    "per dimension (x > 0)",
+            "dtype": "u32 words (popcount)", "nq": nq, "n": n, "d": d, "words": 4,
+            "kernels": [("bin_hamming_filter", "k_bin_scan<4, FILTER>", "valu_bin"),
+                        ("bin_hamming_dense", "k_bin_scan<4, DENSE>", "valu_bin")],
+            "keep": (db, xc, qc, dist, ids),
+        }
+        return spec, step, cpu_leg
+
     if c == "c3":
         n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
         x, q, cent = gen_mixture(n, d, ncent, nq, dev)
@@ -468,6 +514,21 @@ def roofline(spec, stats):
                                      "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
                                      "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
                                                           / PEAK_HBM_GBPS, 4)}
+    elif kind == "valu_bin":
+        # one v_xor_b32 and one v_bcnt_u32_b32 per 32-bit word per pair
+        ops = 2.0 * spec["words"] * pairs
+        ach = ops / sec / 1e12
+        r.update({"bound": "valu", "achieved": round(ach, 2),
+                  "peak": PEAK_FP32_VALU_ISSUE_TOPS, "unit": "TOP/s",
+                  "frac": round(ach / PEAK_FP32_VALU_ISSUE_TOPS, 4),
+                  "algorithmic": "2 integer operations (xor, popcount-add) per 32-bit code "
+                                 "word per (query, row) pair",
+                  "peak_basis": "one 32-bit VALU operation per lane per cycle: 256 CUs x "
+                                f"4 SIMDs x 16 lanes x 2.4 GHz = {PEAK_FP32_VALU_ISSUE_TOPS} "
+                                "T operations/s",
+                  "code_bytes_basis": {"bytes_per_pair": 4 * spec["words"],
+                                       "hbm_bytes_per_launch_min": 4.0 * spec["words"]
+                                       * spec["n"]}})
     elif kind == "hbm":
         by = 4.0 * d * pairs
         ach = by / sec / 1e9

@@ -55,7 +55,9 @@ typedef int32_t vsk_status;
 #define VSK_ERR_INVALID_BUFFER_SIZE (-9)  /* .invalidBufferSize (k or size over a limit) */
 
 /* Distance metrics: DistanceMetric raw values "euclidean", "cosine",
- * "dotProduct", "manhattan" (Core/SearchTypes.swift:105-110) plus the
+ * "dotProduct", "manhattan", "hamming" (Core/SearchTypes.swift:105-112; the
+ * five UnifiedDistanceComputation evaluates, Core/Distance/
+ * UnifiedDistanceComputation.swift:171-186,249-261) plus the
  * squared-L2 and pre-normalised cosine forms the reference's kernels use
  * (Acceleration/Metal/Shaders/DistanceShaders.metal:620-654, 815-845). */
 #define VSK_METRIC_L2SQ 0              /* sum (q-x)^2                        */
@@ -64,6 +66,7 @@ typedef int32_t vsk_status;
 #define VSK_METRIC_COSINE_NORMALIZED 3 /* 1 - q.x (unit-norm rows/queries)  */
 #define VSK_METRIC_DOT 4               /* -q.x                  "dotProduct" */
 #define VSK_METRIC_L1 5                /* sum |q-x|             "manhattan"  */
+#define VSK_METRIC_HAMMING 6           /* count of q_i != x_i   "hamming"    */
 
 #define VSK_MAX_K 1024 /* largest k of any top-k call */
 
@@ -76,6 +79,7 @@ typedef struct vsk_db vsk_db;
 typedef struct vsk_ivf vsk_ivf;
 typedef struct vsk_sq8 vsk_sq8;
 typedef struct vsk_pq vsk_pq;
+typedef struct vsk_bin vsk_bin;
 
 /* Device description; backs ComputeAccelerator.capabilities()
  * (Core/Protocols.swift:11-20). */
@@ -242,6 +246,30 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
                          int64_t nq, int32_t k_adc, int32_t k,
                          int32_t rerank_metric, const vsk_db *rerank_db,
                          float *out_dist, int64_t *out_ids);
+
+/* ---- binary quantization ---------------------------------------------------
+ * quantizeVectors(scheme: .binary) (Acceleration/MetalAccelerationEngine.swift:
+ * 234-262) -> AccelerateOptimizer.binaryQuantize
+ * (Acceleration/AccelerateOptimizer.swift:447-481): bit i of a code is
+ * x_i > 0, stored in byte i/8 at bit i%8 (the Metal binaryQuantize,
+ * Acceleration/Metal/Shaders/QuantizationShaders.metal:232-260, writes the
+ * same bits as little-endian 32-bit words).  codes: n x ceil(d/8) bytes. */
+vsk_status vsk_binary_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                             uint8_t *codes);
+/* Resident binary codes: n x ceil(d/8) bytes, d bits each. */
+vsk_status vsk_bin_upload(vsk_ctx *ctx, const uint8_t *codes, int64_t n,
+                          int32_t d, vsk_bin **out);
+vsk_status vsk_bin_free(vsk_ctx *ctx, vsk_bin *bin);
+/* Top k by Hamming distance popcount(q xor x) (binaryHammingDistance,
+ * QuantizationShaders.metal:285-305), ties by row id.  qcodes: nq x
+ * ceil(d/8) bytes; out_dist: nq x k int32 (INT32_MAX where missing). */
+vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
+                          int64_t nq, int32_t k, int32_t *out_dist,
+                          int64_t *out_ids);
+/* binaryHammingDistance for every (query, row): out nq x n float, as the
+ * Metal kernel writes it. */
+vsk_status vsk_bin_distances(vsk_ctx *ctx, const vsk_bin *bin,
+                             const uint8_t *qcodes, int64_t nq, float *out);
 
 /* ---- k-means -------------------------------------------------------------
  * KMeansClustering.cluster (Clustering/KMeansClustering.swift:48-113), the

@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "libvsk_oracle.so")
 
-L2SQ, L2, COSINE, COSINE_NORMALIZED, DOT, L1 = range(6)
+L2SQ, L2, COSINE, COSINE_NORMALIZED, DOT, L1, HAMMING = range(7)
 
 _lib = None
 
@@ -66,6 +66,9 @@ def lib():
             "vsko_kmeans_cluster": (c_int32, [P, c_int64, c_int32, c_int32, c_int32, P, P,
                                               c_int32, c_float, c_uint64, P, P, P, P, P,
                                               c_int32]),
+            "vsko_binary_encode": (None, [P, c_int64, c_int32, P]),
+            "vsko_bin_hamming": (c_int32, [P, P, c_int32]),
+            "vsko_bin_search": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, P, c_int32]),
             "vsko_num_threads": (c_int32, []),
         }
         for name, (res, args) in sig.items():
@@ -297,3 +300,23 @@ def kmeans_cluster(x, k, init_method="random", init=None, weights=None, max_iter
     if rc != 0:
         raise ValueError("degenerate data")
     return cent, assign, int(it.value), bool(conv.value), np.float32(inertia.value)
+
+
+def binary_encode(x):
+    """AccelerateOptimizer.binaryQuantize: (n, ceil(d/8)) uint8."""
+    x, xp = _c(x, np.float32)
+    n, d = x.shape
+    out = np.empty((n, (d + 7) // 8), np.uint8)
+    lib().vsko_binary_encode(xp, n, d, out.ctypes.data)
+    return out
+
+
+def bin_search(qcodes, codes, d, k, threads=0):
+    """top k by (Hamming distance, id): (int32 distances, int64 ids)."""
+    q, qp = _c(qcodes, np.uint8)
+    c, cp = _c(codes, np.uint8)
+    nq = q.shape[0]
+    od = np.empty((nq, k), np.int32)
+    oi = np.empty((nq, k), np.int64)
+    lib().vsko_bin_search(qp, nq, cp, c.shape[0], d, k, od.ctypes.data, oi.ctypes.data, threads)
+    return od, oi

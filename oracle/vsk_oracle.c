@@ -116,6 +116,14 @@ float vsko_distance(const float *q, const float *x, int32_t d,
     return -vsko_dot(q, x, d);
   case VSKO_L1:
     return vsko_l1(q, x, d);
+  case VSKO_HAMMING: {
+    /* Core/Distance/UnifiedDistanceComputation.swift:249-261: count += 1
+     * where a[i] != b[i] (fp32 counter) */
+    float c = 0.0f;
+    for (int32_t i = 0; i < d; ++i)
+      if (q[i] != x[i]) c += 1.0f;
+    return c;
+  }
   default:
     return NAN;
   }
@@ -176,6 +184,8 @@ static float distance_fast(const float *q, const float *x, int32_t d,
     return -dot16(q, x, d);
   case VSKO_L1:
     return l116(q, x, d);
+  case VSKO_HAMMING:
+    return vsko_distance(q, x, d, VSKO_HAMMING);
   default:
     return NAN;
   }
@@ -999,4 +1009,75 @@ int32_t vsko_kmeans_cluster(const float *x, int64_t n, int32_t d, int32_t k,
   free(a);
   free(cur);
   return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* binary quantization and Hamming search                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Acceleration/AccelerateOptimizer.swift:447-481 (binaryQuantize): bytes
+ * zeroed, then bit i%8 of byte i/8 set where x_i > 0. */
+void vsko_binary_encode(const float *x, int64_t n, int32_t d, uint8_t *codes) {
+  const int32_t nb = (d + 7) / 8;
+  for (int64_t r = 0; r < n; ++r) {
+    uint8_t *c = codes + r * nb;
+    memset(c, 0, (size_t)nb);
+    for (int32_t i = 0; i < d; ++i)
+      if (x[r * d + i] > 0.0f) c[i / 8] |= (uint8_t)(1u << (i % 8));
+  }
+}
+
+/* Acceleration/Metal/Shaders/QuantizationShaders.metal:285-305
+ * (binaryHammingDistance): popcount of the xor, summed */
+int32_t vsko_bin_hamming(const uint8_t *a, const uint8_t *b, int32_t nbytes) {
+  int32_t s = 0;
+  for (int32_t i = 0; i < nbytes; ++i) s += __builtin_popcount((unsigned)(a[i] ^ b[i]));
+  return s;
+}
+
+typedef struct {
+  const uint8_t *q, *x;
+  int64_t n;
+  int32_t d, k;
+  int32_t *od;
+  int64_t *oi;
+} bins_ctx;
+/* per query: every distance, a histogram over 0..d, then the rows of the
+ * smallest distances in ascending row order (the (distance, id) order) */
+static void bins_range(void *p, int64_t lo, int64_t hi) {
+  bins_ctx *a = (bins_ctx *)p;
+  const int32_t nb = (a->d + 7) / 8;
+  int32_t *dist = (int32_t *)malloc(sizeof(int32_t) * a->n);
+  int64_t *hist = (int64_t *)malloc(sizeof(int64_t) * (a->d + 1));
+  for (int64_t qi = lo; qi < hi; ++qi) {
+    memset(hist, 0, sizeof(int64_t) * (a->d + 1));
+    for (int64_t r = 0; r < a->n; ++r) {
+      dist[r] = vsko_bin_hamming(a->q + qi * nb, a->x + r * nb, nb);
+      hist[dist[r]]++;
+    }
+    int32_t *od = a->od + qi * a->k;
+    int64_t *oi = a->oi + qi * a->k;
+    int32_t got = 0;
+    for (int32_t dv = 0; dv <= a->d && got < a->k; ++dv) {
+      if (!hist[dv]) continue;
+      for (int64_t r = 0; r < a->n && got < a->k; ++r)
+        if (dist[r] == dv) {
+          od[got] = dv;
+          oi[got] = r;
+          ++got;
+        }
+    }
+    for (; got < a->k; ++got) {
+      od[got] = 0x7FFFFFFF;
+      oi[got] = -1;
+    }
+  }
+  free(hist);
+  free(dist);
+}
+void vsko_bin_search(const uint8_t *qcodes, int64_t nq, const uint8_t *codes,
+                     int64_t n, int32_t d, int32_t k, int32_t *out_dist,
+                     int64_t *out_ids, int32_t nthreads) {
+  bins_ctx a = {qcodes, codes, n, d, k, out_dist, out_ids};
+  parallel_for(nq, nthreads, bins_range, &a);
 }

@@ -32,7 +32,8 @@ enum {
   VSKO_COSINE = 2,            /* 1 - q.x / (|q||x| + 1e-8)                   */
   VSKO_COSINE_NORMALIZED = 3, /* 1 - q.x (unit-norm inputs)                  */
   VSKO_DOT = 4,               /* -q.x                                        */
-  VSKO_L1 = 5                 /* sum |q-x|                                   */
+  VSKO_L1 = 5,                /* sum |q-x|                                   */
+  VSKO_HAMMING = 6            /* count of q_i != x_i                         */
 };
 
 /* ---- distances ---------------------------------------------------------- */
@@ -115,6 +116,17 @@ void vsko_pq_adc_scan(const float *lut, const uint8_t *codes, int64_t n,
 void vsko_kmeans(const float *x, int64_t n, int32_t d, int32_t k,
                  int32_t iters, uint64_t seed, float *centroids,
                  int32_t nthreads);
+
+/* ---- binary quantization ------------------------------------------------ */
+/* AccelerateOptimizer.binaryQuantize: codes n x ceil(d/8) bytes, bit i =
+ * x_i > 0 at byte i/8, bit i%8 */
+void vsko_binary_encode(const float *x, int64_t n, int32_t d, uint8_t *codes);
+/* binaryHammingDistance: popcount(a xor b) over nbytes */
+int32_t vsko_bin_hamming(const uint8_t *a, const uint8_t *b, int32_t nbytes);
+/* top k by (Hamming distance, row id); missing: INT32_MAX and -1 */
+void vsko_bin_search(const uint8_t *qcodes, int64_t nq, const uint8_t *codes,
+                     int64_t n, int32_t d, int32_t k, int32_t *out_dist,
+                     int64_t *out_ids, int32_t nthreads);
 
 /* ---- KMeansClustering.cluster (Clustering/KMeansClustering.swift:48-113) */
 /* Int.random(in: 0..<bound, using: &SeedableRNG): Swift's Lemire bounded

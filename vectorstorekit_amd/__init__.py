@@ -18,4 +18,10 @@ from .clustering import (  # noqa: F401,E402
     KMeansClusteringConfiguration,
 )
 from .ivf import IVFConfiguration, IVFIndex  # noqa: F401,E402
-from .quantization import ProductQuantizer, ScalarQuantizer, SQ8Database  # noqa: F401,E402
+from .quantization import (  # noqa: F401,E402
+    BinaryDatabase,
+    BinaryQuantizer,
+    ProductQuantizer,
+    ScalarQuantizer,
+    SQ8Database,
+)

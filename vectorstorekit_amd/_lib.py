@@ -36,6 +36,7 @@ METRIC_COSINE = 2
 METRIC_COSINE_NORMALIZED = 3
 METRIC_DOT = 4
 METRIC_L1 = 5
+METRIC_HAMMING = 6
 MAX_K = 1024
 DB_NORMALIZE = 1
 
@@ -114,6 +115,11 @@ SIGNATURES = {
     "vsk_pq_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P, P]),
     "vsk_kmeans": (c_int32, [P, P, c_int64, c_int32, c_int32, P, c_int32, P, ctypes.c_uint64,
                              c_int32, c_float, P, P, P]),
+    "vsk_binary_encode": (c_int32, [P, P, c_int64, c_int32, P]),
+    "vsk_bin_upload": (c_int32, [P, P, c_int64, c_int32, PP]),
+    "vsk_bin_free": (c_int32, [P, P]),
+    "vsk_bin_search": (c_int32, [P, P, P, c_int64, c_int32, P, P]),
+    "vsk_bin_distances": (c_int32, [P, P, P, c_int64, P]),
 }
 
 _lib = None

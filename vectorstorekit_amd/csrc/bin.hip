@@ -1,0 +1,358 @@
+// bin.hip -- binary quantization (one bit per dimension) and the Hamming
+// top-k scan.
+//
+// Reference: quantizeVectors(scheme: .binary) ->
+// AccelerateOptimizer.binaryQuantize (Acceleration/AccelerateOptimizer.swift:
+// 447-481): bit i of a code is x_i > 0, in byte i/8 at bit i%8 (the Metal
+// binaryQuantize, Acceleration/Metal/Shaders/QuantizationShaders.metal:
+// 232-260, writes the same bits as little-endian 32-bit words).
+// binaryHammingDistance (:285-305): popcount(q xor x) over the words.
+//
+// Layout in HBM: W 32-bit words per code, W a multiple of 4 (whole 16-byte
+// loads); the padding bits are zero in every code and add nothing to a
+// distance.
+//
+// Scan: a lane owns one database code (W registers) and walks the queries.
+// The query words are the same for the whole wave, so they come by scalar
+// loads and each word costs one v_xor_b32 and one v_bcnt_u32_b32 with a
+// scalar operand; the codes are read from HBM once per launch whatever the
+// number of queries.  The filter appends the keys <= the query's threshold
+// with one atomic per (wave, query) that has any.
+#include "flat.hpp"
+
+struct vsk_bin {
+  int64_t n = 0;
+  int32_t d = 0;
+  int32_t words = 0;  // 32-bit words per code (multiple of 4)
+  vsk::DevBuf codes;
+};
+
+namespace vsk {
+
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+struct BinArgs {
+  const uint32_t *X;  // rows, `words` words each
+  const uint32_t *Q;  // queries, same stride
+  int32_t words;
+  int32_t nq;
+  int64_t r0, r1;
+  const uint64_t *thresh;
+  const uint8_t *active;
+  uint64_t *cand;
+  int64_t cap;
+  int32_t *counts;
+  float *mat;  // distance matrix (nq x ldm), else null
+  int64_t ldm;
+};
+
+constexpr int BIN_T = 256;
+
+// (pointers as separate restrict arguments: the query words and thresholds
+// are then provably never written by the kernel and load through the scalar
+// cache; ACT: an active mask is given, which only the progressive top-k's
+// overflow re-scans do)
+template <int W, int MODE, bool ACT>
+__global__ __launch_bounds__(BIN_T) void k_bin_scan(
+    const uint32_t *__restrict__ X, const uint32_t *__restrict__ Q,
+    const uint64_t *__restrict__ thresh, const uint8_t *__restrict__ active,
+    uint64_t *__restrict__ cand, int32_t *__restrict__ counts, float *__restrict__ mat,
+    BinArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = a.r0 + (int64_t)blockIdx.x * BIN_T + threadIdx.x;
+  const bool rok = row < a.r1;
+  uint32_t x[W];
+  {
+    const u4 *src = reinterpret_cast<const u4 *>(X + (rok ? row : a.r0) * W);
+#pragma unroll
+    for (int u = 0; u < W / 4; ++u) {
+      const u4 v = src[u];
+      x[4 * u] = v.x;
+      x[4 * u + 1] = v.y;
+      x[4 * u + 2] = v.z;
+      x[4 * u + 3] = v.w;
+    }
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  const uint32_t row32 = (uint32_t)row;
+  // queries in blocks of QB: their words and thresholds are scalar loads
+  // issued together, and the QB distances are independent chains
+  constexpr int QB = 8;
+  for (int32_t q0 = 0; q0 < a.nq; q0 += QB) {
+    uint32_t dist[QB];
+    uint64_t th[QB];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      const int32_t q = q0 + j < a.nq ? q0 + j : a.nq - 1;  // past the end: a repeat
+      if constexpr (MODE == MODE_FILTER) th[j] = thresh[q];
+      const uint32_t *qw = Q + (int64_t)q * W;
+      uint32_t s = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) s += __builtin_popcount(x[w] ^ qw[w]);
+      dist[j] = s;
+    }
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      const int32_t q = q0 + j;
+      if (q >= a.nq) break;
+      if constexpr (ACT) {
+        if (!active[q]) continue;
+      }
+      if constexpr (MODE == MODE_MATRIX) {
+        if (rok) mat[(int64_t)q * a.ldm + row] = (float)dist[j];
+      } else if constexpr (MODE == MODE_DENSE) {
+        if (rok) cand[(int64_t)q * a.cap + (row - a.r0)] = vsk_key_i32((int32_t)dist[j], row32);
+      } else {
+        // key <= threshold on (distance, row): the distance settles all but
+        // the tie with the threshold's own distance.  No threshold yet
+        // (fewer than k keys, NONE) decodes to distance 0x7FFFFFFF, which
+        // every distance is below.
+        const uint32_t thd = (uint32_t)(th[j] >> 32) ^ 0x80000000u;
+        const uint32_t thr = (uint32_t)th[j];
+        const bool pass = rok & ((dist[j] < thd) | ((dist[j] == thd) & (row32 <= thr)));
+        const uint64_t m = __builtin_amdgcn_ballot_w64(pass);
+        if (m) {
+          const int leader = __builtin_ctzll(m);
+          int32_t base = 0;
+          if (lane == leader) base = atomicAdd(&counts[q], (int32_t)__builtin_popcountll(m));
+          base = __builtin_amdgcn_readlane(base, leader);
+          if (pass) {
+            const int64_t slot = base + __builtin_popcountll(m & below);
+            if (slot < a.cap)
+              cand[(int64_t)q * a.cap + slot] = vsk_key_i32((int32_t)dist[j], row32);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, bool ACT>
+static void launch_bin_mode(vsk_ctx *ctx, const BinArgs &a, unsigned grid) {
+#define BIN_CASE(W)                                                                  \
+  case W:                                                                            \
+    k_bin_scan<W, MODE, ACT><<<grid, BIN_T, 0, ctx->stream>>>(                       \
+        a.X, a.Q, a.thresh, a.active, a.cand, a.counts, a.mat, a);                   \
+    break;
+  switch (a.words) {
+    BIN_CASE(4)
+    BIN_CASE(8)
+    BIN_CASE(12)
+    BIN_CASE(16)
+    BIN_CASE(20)
+    BIN_CASE(24)
+    BIN_CASE(28)
+    BIN_CASE(32)
+  default: fail(VSK_ERR_UNSUPPORTED, "binary codes of more than 1024 bits");
+  }
+#undef BIN_CASE
+}
+
+static void launch_bin(vsk_ctx *ctx, const BinArgs &a, int mode) {
+  const int64_t rows = a.r1 - a.r0;
+  if (rows <= 0 || a.nq <= 0) return;
+  const int64_t g = ceil_div(rows, BIN_T);
+  if (g > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many rows");
+  static const char *names[3] = {"bin_hamming_dense", "bin_hamming_filter",
+                                 "bin_hamming_matrix"};
+  KernelTimer t(ctx, names[mode], (double)a.nq * (double)rows);
+  if (mode == MODE_DENSE && a.active)
+    launch_bin_mode<MODE_DENSE, true>(ctx, a, (unsigned)g);
+  else if (mode == MODE_DENSE)
+    launch_bin_mode<MODE_DENSE, false>(ctx, a, (unsigned)g);
+  else if (mode == MODE_FILTER && a.active)
+    launch_bin_mode<MODE_FILTER, true>(ctx, a, (unsigned)g);
+  else if (mode == MODE_FILTER)
+    launch_bin_mode<MODE_FILTER, false>(ctx, a, (unsigned)g);
+  else
+    launch_bin_mode<MODE_MATRIX, false>(ctx, a, (unsigned)g);
+  check_launch(names[mode]);
+}
+
+// bit i of row r: x[r][i] > 0, at word i/32, bit i%32 (little-endian bytes:
+// byte i/8, bit i%8); one thread per output word, zero padding words
+__global__ void k_binary_encode(const float *x, int64_t n, int32_t d, int32_t ld,
+                                int32_t words, uint32_t *codes) {
+  const int64_t total = n * words;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / words;
+    const int32_t w = (int32_t)(i - r * words);
+    uint32_t v = 0;
+    const int32_t j0 = w * 32;
+    for (int32_t b = 0; b < 32 && j0 + b < d; ++b)
+      v |= (x[r * ld + j0 + b] > 0.f ? 1u : 0u) << b;
+    codes[i] = v;
+  }
+}
+
+__global__ void k_bin_decode(const uint64_t *best, int64_t total, int32_t *dist,
+                             int64_t *ids) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t key = best[i];
+    if (key == VSK_KEY_NONE) {
+      dist[i] = 0x7FFFFFFF;
+      ids[i] = -1;
+    } else {
+      dist[i] = (int32_t)((uint32_t)(key >> 32) ^ 0x80000000u);
+      ids[i] = (uint32_t)key;
+    }
+  }
+}
+
+static unsigned grid_n(int64_t n) {
+  const int64_t g = ceil_div(n, 256);
+  return (unsigned)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
+}
+
+static int32_t bin_words(int32_t d) { return (int32_t)(ceil_div(d, 128) * 4); }
+
+// codes of ceil(d/8) bytes per row (host or device) -> words per row, zero
+// padded, on the device
+static const uint32_t *codes_to_words(vsk_ctx *ctx, const uint8_t *p, int64_t n,
+                                      int32_t d, int32_t words, const std::string &slot) {
+  const int32_t bytes = (d + 7) / 8;
+  uint32_t *out = static_cast<uint32_t *>(
+      ctx->scratch_ptr(slot, sizeof(uint32_t) * (size_t)n * words));
+  if (bytes != words * 4) fill_i32(ctx, reinterpret_cast<int32_t *>(out), n * words, 0);
+  copy_rows(ctx, out, (size_t)words * 4, p, bytes, bytes, n);
+  return out;
+}
+
+}  // namespace vsk
+
+using namespace vsk;
+
+extern "C" {
+
+vsk_status vsk_binary_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                             uint8_t *codes) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no vectors");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(x && codes, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const int32_t ld = padded_ld(d);
+  const float *dx = rows_to_device_padded(ctx, x, n, d, ld, "bin.x");
+  const int32_t words = (d + 31) / 32;
+  uint32_t *w = static_cast<uint32_t *>(
+      ctx->scratch_ptr("bin.enc", sizeof(uint32_t) * (size_t)n * words));
+  {
+    KernelTimer t(ctx, "binary_encode", (double)n);
+    k_binary_encode<<<grid_n(n * words), 256, 0, ctx->stream>>>(dx, n, d, ld, words, w);
+    check_launch("binary_encode");
+  }
+  const int32_t bytes = (d + 7) / 8;
+  copy_rows(ctx, codes, bytes, w, (size_t)words * 4, bytes, n);
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_bin_upload(vsk_ctx *ctx, const uint8_t *codes, int64_t n, int32_t d,
+                          vsk_bin **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no codes");
+  VSK_REQUIRE(d > 0 && d <= 1024, VSK_ERR_UNSUPPORTED, "binary codes of 1 to 1024 bits");
+  VSK_REQUIRE(codes, VSK_ERR_INVALID_ARGUMENT, "codes is null");
+  VSK_REQUIRE(n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "a binary database holds at most 2^31-1 rows");
+  CallScope cs(ctx);
+  std::unique_ptr<vsk_bin> b(new vsk_bin());
+  b->n = n;
+  b->d = d;
+  b->words = bin_words(d);
+  b->codes.reserve(sizeof(uint32_t) * (size_t)n * b->words);
+  const int32_t bytes = (d + 7) / 8;
+  if (bytes != b->words * 4)
+    fill_i32(ctx, b->codes.as<int32_t>(), n * b->words, 0);
+  copy_rows(ctx, b->codes.p, (size_t)b->words * 4, codes, bytes, bytes, n);
+  cs.finish();
+  *out = b.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_bin_free(vsk_ctx *ctx, vsk_bin *bin) {
+  VSK_API_BEGIN(ctx);
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  delete bin;
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
+                          int64_t nq, int32_t k, int32_t *out_dist, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(bin, VSK_ERR_INVALID_ARGUMENT, "bin is null");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(qcodes && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE, "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
+  CallScope cs(ctx);
+  const uint32_t *dq = codes_to_words(ctx, qcodes, nq, bin->d, bin->words, "bin.q");
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("bin.best", sizeof(uint64_t) * (size_t)nq * k));
+  const int64_t cap = default_cap(k);
+  const int64_t qb = query_batch(nq, cap);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    BinArgs base{};
+    base.X = bin->codes.as<uint32_t>();
+    base.Q = dq + b0 * bin->words;
+    base.words = bin->words;
+    base.nq = (int32_t)nb;
+    ScanFn scan = [&](const ScanRequest &r) {
+      BinArgs a = base;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_bin(ctx, a, r.dense ? MODE_DENSE : MODE_FILTER);
+    };
+    progressive_topk(ctx, nb, bin->n, k, cap, scan, best + b0 * k, "bin_select", 8);
+  }
+  OutputStage od(ctx, out_dist, sizeof(int32_t) * (size_t)nq * k, "out.bdist");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * (size_t)nq * k, "out.ids");
+  {
+    KernelTimer t(ctx, "bin_decode");
+    k_bin_decode<<<grid_n(nq * k), 256, 0, ctx->stream>>>(best, nq * k, od.ptr<int32_t>(),
+                                                          oi.ptr<int64_t>());
+    check_launch("bin_decode");
+  }
+  od.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_bin_distances(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
+                             int64_t nq, float *out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(bin, VSK_ERR_INVALID_ARGUMENT, "bin is null");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(qcodes && out, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
+  CallScope cs(ctx);
+  const uint32_t *dq = codes_to_words(ctx, qcodes, nq, bin->d, bin->words, "bin.q");
+  OutputStage om(ctx, out, sizeof(float) * (size_t)nq * bin->n, "out.bmatrix");
+  BinArgs a{};
+  a.X = bin->codes.as<uint32_t>();
+  a.Q = dq;
+  a.words = bin->words;
+  a.nq = (int32_t)nq;
+  a.r0 = 0;
+  a.r1 = bin->n;
+  a.mat = om.ptr<float>();
+  a.ldm = bin->n;
+  launch_bin(ctx, a, MODE_MATRIX);
+  om.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"

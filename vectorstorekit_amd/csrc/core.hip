@@ -186,7 +186,7 @@ const float *rows_to_device_padded(vsk_ctx *ctx, const float *p, int64_t rows,
 }
 
 bool metric_valid(int32_t m) {
-  return m >= VSK_METRIC_L2SQ && m <= VSK_METRIC_L1;
+  return m >= VSK_METRIC_L2SQ && m <= VSK_METRIC_HAMMING;
 }
 
 // ---------------------------------------------------------------------------

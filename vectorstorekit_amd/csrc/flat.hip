@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
 constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
 // sequential (dimension-order, no FMA) terms and final transforms of the
 // exact VALU kernel, one per metric of the CPU reference
-enum { OP_L1 = 0, OP_L2SEQ = 1, OP_L2SQSEQ = 2, OP_CNSEQ = 3, OP_DOTSEQ = 4 };
+enum { OP_L1 = 0, OP_L2SEQ = 1, OP_L2SQSEQ = 2, OP_CNSEQ = 3, OP_DOTSEQ = 4, OP_HAM = 5 };
 
 __device__ inline uint64_t shfl_xor_u64(uint64_t v, int m) {
   uint32_t lo = __shfl_xor((uint32_t)v, m);
@@ -199,6 +199,10 @@ __device__ inline float valu_term(float q, float x) {
 #pragma clang fp contract(off)
   if constexpr (OP == OP_L1) {
     return fabsf(q - x);
+  } else if constexpr (OP == OP_HAM) {
+    // hammingDistance: count += 1 where the components differ
+    // (Core/Distance/UnifiedDistanceComputation.swift:249-261; NaN differs)
+    return q != x ? 1.0f : 0.0f;
   } else if constexpr (OP == OP_L2SEQ || OP == OP_L2SQSEQ) {
     float t = q - x;
     return t * t;
@@ -362,7 +366,8 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   splits = ceil_div(rows, a.rows_per_split);
   if (qt > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
   dim3 grid((unsigned)qt, (unsigned)splits);
-  const bool valu = a.metric == VSK_METRIC_L1 || a.metric >= METRIC_L2_EXACT;
+  const bool valu = a.metric == VSK_METRIC_L1 || a.metric == VSK_METRIC_HAMMING ||
+                    a.metric >= METRIC_L2_EXACT;
   static const char *names[2][4] = {
       {"flat_mfma_dense", "flat_mfma_filter", "flat_mfma_matrix", "flat_mfma_argmin"},
       {"flat_valu_dense", "flat_valu_filter", "flat_valu_matrix", "flat_valu_argmin"}};
@@ -371,6 +376,7 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   if (valu) {
     switch (a.metric) {
     case VSK_METRIC_L1: launch_valu<OP_L1>(ctx, grid, a, mode, argmin); break;
+    case VSK_METRIC_HAMMING: launch_valu<OP_HAM>(ctx, grid, a, mode, argmin); break;
     case METRIC_L2_EXACT: launch_valu<OP_L2SEQ>(ctx, grid, a, mode, argmin); break;
     case METRIC_L2SQ_EXACT: launch_valu<OP_L2SQSEQ>(ctx, grid, a, mode, argmin); break;
     case METRIC_CN_EXACT: launch_valu<OP_CNSEQ>(ctx, grid, a, mode, argmin); break;
@@ -414,7 +420,8 @@ float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
 }
 
 static bool use_bf16x3(const vsk_ctx *ctx, int32_t metric) {
-  return !ctx->flat_fp32 && metric != VSK_METRIC_L1 && metric < METRIC_L2_EXACT;
+  return !ctx->flat_fp32 && metric != VSK_METRIC_L1 && metric != VSK_METRIC_HAMMING &&
+         metric < METRIC_L2_EXACT;
 }
 
 SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,

@@ -22,6 +22,7 @@ inline int32_t exact_metric(int32_t metric) {
   case VSK_METRIC_COSINE_NORMALIZED: return METRIC_CN_EXACT;
   case VSK_METRIC_DOT: return METRIC_DOT_EXACT;
   case VSK_METRIC_L1: return VSK_METRIC_L1;
+  case VSK_METRIC_HAMMING: return VSK_METRIC_HAMMING;
   default: return -1;
   }
 }

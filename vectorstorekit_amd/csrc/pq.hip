@@ -854,6 +854,8 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
   if (rerank) {
     VSK_REQUIRE(metric_valid(rerank_metric), VSK_ERR_INVALID_ARGUMENT,
                 "unknown re-rank metric");
+    VSK_REQUIRE(rerank_metric != VSK_METRIC_HAMMING, VSK_ERR_UNSUPPORTED,
+                "the re-rank has no hamming metric");
     VSK_REQUIRE(rerank_db->d == pq->d, VSK_ERR_DIMENSION_MISMATCH,
                 "re-rank rows have another dimension");
     VSK_REQUIRE(rerank_db->n >= pq->n, VSK_ERR_DIMENSION_MISMATCH,

@@ -29,14 +29,16 @@ from ._lib import VSKError, as_buffer, check, load_library, out_buffer
 
 
 class DistanceMetric(str, enum.Enum):
-    """``DistanceMetric`` raw values (Core/SearchTypes.swift:105-110) for the
-    four hot-path metrics, plus the squared-L2 and pre-normalised cosine
-    forms of the reference's kernels."""
+    """``DistanceMetric`` raw values (Core/SearchTypes.swift:105-112) for the
+    five metrics UnifiedDistanceComputation evaluates (the four hot-path
+    ones and hamming), plus the squared-L2 and pre-normalised cosine forms
+    of the reference's kernels."""
 
     euclidean = "euclidean"
     cosine = "cosine"
     dotProduct = "dotProduct"
     manhattan = "manhattan"
+    hamming = "hamming"
     euclideanSquared = "euclideanSquared"
     cosineNormalized = "cosineNormalized"
 
@@ -52,6 +54,7 @@ _METRIC_CODES = {
     DistanceMetric.cosineNormalized: _lib.METRIC_COSINE_NORMALIZED,
     DistanceMetric.dotProduct: _lib.METRIC_DOT,
     DistanceMetric.manhattan: _lib.METRIC_L1,
+    DistanceMetric.hamming: _lib.METRIC_HAMMING,
 }
 
 

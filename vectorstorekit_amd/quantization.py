@@ -206,3 +206,62 @@ class ProductQuantizer:
             self.free()
         except Exception:
             pass
+
+
+class BinaryQuantizer:
+    """quantizeVectors(scheme: .binary) (AccelerateOptimizer.binaryQuantize,
+    Acceleration/AccelerateOptimizer.swift:447-481): one bit per dimension,
+    x_i > 0, byte i/8 bit i%8 -- encoded on the GPU (vsk_binary_encode)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+
+    def quantizeBatch(self, vectors):
+        n, d = int(vectors.shape[0]), int(vectors.shape[1])
+        xp, xk = as_buffer(vectors, np.float32, (n, d))
+        cp, codes = out_buffer((n, (d + 7) // 8), np.uint8, vectors)
+        self.ctx.check(self.ctx.lib.vsk_binary_encode(self.ctx.handle, xp, n, d, cp))
+        return codes
+
+
+class BinaryDatabase:
+    """Resident binary codes (``vsk_bin``) searched by Hamming distance
+    (binaryHammingDistance, QuantizationShaders.metal:285-305)."""
+
+    def __init__(self, ctx: Context, codes, d: int):
+        self.ctx = ctx
+        self.n, self.d = int(codes.shape[0]), int(d)
+        nb = (self.d + 7) // 8
+        cp, ck = as_buffer(codes, np.uint8, (self.n, nb))
+        h = ctypes.c_void_p()
+        ctx.check(ctx.lib.vsk_bin_upload(ctx.handle, cp, self.n, self.d, ctypes.byref(h)))
+        self.handle = h
+
+    def search(self, qcodes, k: int):
+        """Top-k by Hamming distance, ties by id: (int32 distances, ids)."""
+        nq = int(qcodes.shape[0])
+        qp, qk = as_buffer(qcodes, np.uint8, (nq, (self.d + 7) // 8))
+        dp, dist = out_buffer((nq, k), np.int32, qcodes)
+        ip, ids = out_buffer((nq, k), np.int64, qcodes)
+        self.ctx.check(self.ctx.lib.vsk_bin_search(self.ctx.handle, self.handle, qp, nq, k,
+                                                   dp, ip))
+        return dist, ids
+
+    def distances(self, qcodes):
+        """Every (query, row) Hamming distance as float32 (nq, n)."""
+        nq = int(qcodes.shape[0])
+        qp, qk = as_buffer(qcodes, np.uint8, (nq, (self.d + 7) // 8))
+        op, out = out_buffer((nq, self.n), np.float32, qcodes)
+        self.ctx.check(self.ctx.lib.vsk_bin_distances(self.ctx.handle, self.handle, qp, nq, op))
+        return out
+
+    def free(self):
+        if getattr(self, "handle", None):
+            self.ctx.lib.vsk_bin_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
