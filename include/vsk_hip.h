@@ -202,6 +202,10 @@ vsk_status vsk_sq8_train(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
 vsk_status vsk_sq8_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
                           int32_t per_dim, const float *scale,
                           const float *offset, int8_t *codes);
+/* dequantizeFromInt8 (:568-580): x = (code - offset) / scale, n x d fp32 */
+vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t d,
+                          int32_t per_dim, const float *scale, const float *offset,
+                          float *out);
 /* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81). */
 vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
                           int32_t d, vsk_sq8 **out);
@@ -231,6 +235,11 @@ vsk_status vsk_pq_upload(vsk_ctx *ctx, const float *codebooks,
  * codes n x M uint8 */
 vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,
                          int64_t n, uint8_t *codes);
+/* decode (:142-160, without the optional norm correction of :162-180, whose
+ * norm these codes do not carry): out n x (M * dsub) fp32, each segment's
+ * codeword */
+vsk_status vsk_pq_decode(vsk_ctx *ctx, const vsk_pq *pq, const uint8_t *codes,
+                         int64_t n, float *out);
 /* Append n x M codes to the resident code database. */
 vsk_status vsk_pq_add_codes(vsk_ctx *ctx, vsk_pq *pq, const uint8_t *codes,
                             int64_t n);

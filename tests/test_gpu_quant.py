@@ -215,3 +215,27 @@ def test_config5_full_size(ctx):
     td, ti = O.search_flat(qh[:sub], xh, 100, O.L1)
     assert recall(gi[:sub], ti) == recall(oi, ti)
     print(f"config5 recall@100 on {sub} queries: {recall(gi[:sub], ti):.4f}", flush=True)
+
+
+@pytest.mark.parametrize("per_dim", [True, False])
+def test_sq8_dequantize_bit_exact(ctx, per_dim):
+    """dequantizeFromInt8 on the GPU: (code - offset) / scale, rounded per
+    operation, bit-exact against the oracle; device tensors stay on device."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((4000, 33)).astype(np.float32) * 2
+    sq = ScalarQuantizer(ctx, per_dim=per_dim)
+    s, o = sq.train(x)
+    codes = sq.quantizeBatch(x)
+    np.testing.assert_array_equal(sq.dequantize(codes), O.sq8_decode(codes, s, o))
+    out = sq.dequantize(torch.from_numpy(codes).cuda())
+    assert out.is_cuda
+    np.testing.assert_array_equal(out.cpu().numpy(), O.sq8_decode(codes, s, o))
+
+
+def test_pq_decode_bit_exact(ctx):
+    x, q, cb = _pq_data(11, 5000, 48, 6, 256, 3)
+    pq = ProductQuantizer(ctx, cb)
+    codes = O.pq_encode(x, cb)
+    np.testing.assert_array_equal(pq.decode(codes), O.pq_decode(codes, cb))

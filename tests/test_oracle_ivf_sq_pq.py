@@ -244,3 +244,19 @@ def test_pq_search_brute_force_and_rerank():
         order = np.lexsort((cand, l1))[:10]
         np.testing.assert_array_equal(ri[qi], cand[order])
         np.testing.assert_array_equal(rd[qi], l1[order])
+
+
+def test_decoders_exact():
+    """dequantizeFromInt8 (ScalarQuantizer.swift:568-580) is numpy's fp32
+    (code - offset) / scale; PQ decode (ProductQuantizer.swift:142-160) is
+    numpy indexing of each segment's codebook."""
+    rng = np.random.default_rng(9)
+    codes = rng.integers(-128, 128, (300, 17)).astype(np.int8)
+    s = rng.random(17).astype(np.float32) * 50 + 1
+    o = (rng.standard_normal(17) * 30).astype(np.float32)
+    want = (codes.astype(np.float32) - o) / s
+    np.testing.assert_array_equal(O.sq8_decode(codes, s, o), want.astype(np.float32))
+    cb = rng.standard_normal((4, 256, 5)).astype(np.float32)
+    pc = rng.integers(0, 256, (200, 4)).astype(np.uint8)
+    want = np.concatenate([cb[m][pc[:, m]] for m in range(4)], axis=1)
+    np.testing.assert_array_equal(O.pq_decode(pc, cb), want)

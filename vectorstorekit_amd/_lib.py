@@ -115,6 +115,8 @@ SIGNATURES = {
     "vsk_pq_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P, P]),
     "vsk_kmeans": (c_int32, [P, P, c_int64, c_int32, c_int32, P, c_int32, P, ctypes.c_uint64,
                              c_int32, c_float, P, P, P]),
+    "vsk_sq8_decode": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
+    "vsk_pq_decode": (c_int32, [P, P, P, c_int64, P]),
     "vsk_binary_encode": (c_int32, [P, P, c_int64, c_int32, P]),
     "vsk_bin_upload": (c_int32, [P, P, c_int64, c_int32, PP]),
     "vsk_bin_free": (c_int32, [P, P]),

@@ -35,6 +35,20 @@ struct vsk_pq {
 
 namespace vsk {
 
+// decode (Quantization/ProductQuantizer.swift:142-160, the codeword of each
+// segment; productDequantize, QuantizationShaders.metal:177-198): out[i][j]
+// = codebook[j / dsub][code[i][j / dsub]][j % dsub]
+__global__ void k_pq_decode(const uint8_t *codes, int64_t n, const float *cb, int32_t M,
+                            int32_t ksub, int32_t dsub, float *out) {
+  const int64_t d = (int64_t)M * dsub, total = n * d;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / d;
+    const int32_t j = (int32_t)(i - r * d), m = j / dsub;
+    out[i] = cb[((int64_t)m * ksub + codes[r * M + m]) * dsub + (j - m * dsub)];
+  }
+}
+
 constexpr int PQ_QG = 4;  // queries per ADC workgroup
 
 // lut[q][m][c], one thread per entry
@@ -788,6 +802,29 @@ vsk_status vsk_pq_encode(vsk_ctx *ctx, const vsk_pq *pq, const float *x,
   OutputStage oc(ctx, codes, (size_t)n * pq->M, "out.codes");
   launch_encode(ctx, pq, dx, n, oc.ptr<uint8_t>());
   oc.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_pq_decode(vsk_ctx *ctx, const vsk_pq *pq, const uint8_t *codes,
+                         int64_t n, float *out) {
+  VSK_API_BEGIN(ctx);
+  require_pq(pq);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no codes");
+  VSK_REQUIRE(codes && out, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const uint8_t *dc = static_cast<const uint8_t *>(
+      input_to_device(ctx, codes, (size_t)n * pq->M, "pq.dcodes"));
+  OutputStage ox(ctx, out, sizeof(float) * (size_t)n * pq->d, "out.decoded");
+  {
+    KernelTimer t(ctx, "pq_decode", (double)n);
+    const int64_t total = n * pq->d;
+    const int64_t g = ceil_div(total, 256);
+    k_pq_decode<<<(unsigned)(g < 16384 ? (g > 0 ? g : 1) : 16384), 256, 0, ctx->stream>>>(
+        dc, n, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, ox.ptr<float>());
+    check_launch("pq_decode");
+  }
+  ox.copy_back();
   cs.finish();
   VSK_API_END(ctx);
 }

@@ -431,6 +431,22 @@ __global__ void k_sq8_encode(const float *x, int64_t n, int32_t d,
   }
 }
 
+// dequantizeFromInt8 (Quantization/ScalarQuantizer.swift:568-580):
+// x = (Float(code) - offset) / scale, each operation rounded on its own
+__global__ void k_sq8_dequantize(const int8_t *codes, int64_t n, int32_t d,
+                                 int32_t per_dim, const float *scale,
+                                 const float *offset, float *out) {
+#pragma clang fp contract(off)
+  const int64_t total = n * d;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t j = (int32_t)(i % d);
+    const float s = per_dim ? scale[j] : scale[0];
+    const float o = per_dim ? offset[j] : offset[0];
+    out[i] = ((float)codes[i] - o) / s;
+  }
+}
+
 __global__ void k_sq8_decode(const uint64_t *best, int64_t total,
                              int32_t *score, int64_t *ids) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -558,6 +574,33 @@ vsk_status vsk_sq8_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
     check_launch("sq8_encode");
   }
   oc.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t d,
+                          int32_t per_dim, const float *scale, const float *offset,
+                          float *out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no codes");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(codes && scale && offset && out, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  CallScope cs(ctx);
+  const size_t cnt = per_dim ? d : 1;
+  const int8_t *dc = static_cast<const int8_t *>(
+      input_to_device(ctx, codes, (size_t)n * d, "sq8.dcodes"));
+  const float *ds = static_cast<const float *>(
+      input_to_device(ctx, scale, 4 * cnt, "sq8.scale"));
+  const float *dof = static_cast<const float *>(
+      input_to_device(ctx, offset, 4 * cnt, "sq8.offset"));
+  OutputStage ox(ctx, out, sizeof(float) * (size_t)n * d, "out.decoded");
+  {
+    KernelTimer t(ctx, "sq8_dequantize");
+    k_sq8_dequantize<<<grid1(n * d), 256, 0, ctx->stream>>>(dc, n, d, per_dim, ds, dof,
+                                                           ox.ptr<float>());
+    check_launch("sq8_dequantize");
+  }
+  ox.copy_back();
   cs.finish();
   VSK_API_END(ctx);
 }

@@ -59,10 +59,17 @@ class ScalarQuantizer:
             self.scale.ctypes.data, self.offset.ctypes.data, cp))
         return codes
 
-    def dequantize(self, codes) -> np.ndarray:
+    def dequantize(self, codes):
+        """dequantizeFromInt8 (Quantization/ScalarQuantizer.swift:568-580) on the
+        GPU (vsk_sq8_decode): (code - offset) / scale."""
         self._need()
-        c = np.asarray(codes, np.int8).astype(np.float32)
-        return ((c - self.offset) / self.scale).astype(np.float32)
+        n, d = int(codes.shape[0]), int(codes.shape[1])
+        cp, ck = as_buffer(codes, np.int8, (n, d))
+        op, out = out_buffer((n, d), np.float32, codes)
+        self.ctx.check(self.ctx.lib.vsk_sq8_decode(
+            self.ctx.handle, cp, n, d, 1 if self.per_dim else 0,
+            self.scale.ctypes.data, self.offset.ctypes.data, op))
+        return out
 
 
 class SQ8Database:
@@ -169,6 +176,15 @@ class ProductQuantizer:
         cp, codes = out_buffer((n, self.M), np.uint8, vectors)
         self.ctx.check(self.ctx.lib.vsk_pq_encode(self.ctx.handle, self.handle, xp, n, cp))
         return codes
+
+    def decode(self, codes):
+        """ProductQuantizer.decode (Quantization/ProductQuantizer.swift:142-160)
+        on the GPU (vsk_pq_decode): each segment's codeword."""
+        n = int(codes.shape[0])
+        cp, ck = as_buffer(codes, np.uint8, (n, self.M))
+        op, out = out_buffer((n, self.d), np.float32, codes)
+        self.ctx.check(self.ctx.lib.vsk_pq_decode(self.ctx.handle, self.handle, cp, n, op))
+        return out
 
     def add(self, codes):
         n = int(codes.shape[0])
