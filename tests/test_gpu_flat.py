@@ -322,3 +322,30 @@ def test_config2_cosine_full_size(ctx):
     for qi in some:
         ref = O.distances(qh[qi:qi + 1], xh[gi[qi]], METRIC_COSINE_NORMALIZED)[0]
         np.testing.assert_allclose(gd[qi], ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("metric", ["euclidean", "manhattan", "cosine", "hamming"])
+def test_distance_matrix_symmetric(ctx, metric):
+    """computeDistanceMatrix(vectorsA) is the symmetric matrix of A: equal to
+    its transpose bit for bit, a zero diagonal for the distance metrics, and
+    the oracle's values within the float bar (exact for manhattan and
+    hamming, summed in index order)."""
+    from vectorstorekit_amd import HIPAccelerationEngine
+
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((700, 45)).astype(np.float32)
+    if metric == "hamming":
+        a = rng.integers(0, 3, (700, 45)).astype(np.float32)
+    eng = HIPAccelerationEngine(ctx)
+    m = np.asarray(eng.computeDistanceMatrix(a, metric=metric))
+    np.testing.assert_array_equal(m, m.T)
+    code = {"euclidean": O.L2, "manhattan": O.L1, "cosine": O.COSINE, "hamming": O.HAMMING}[metric]
+    ref = O.distances(a, a, code)
+    if metric in ("manhattan", "hamming"):
+        np.testing.assert_array_equal(m, ref)
+        assert (np.diag(m) == 0).all()
+    else:
+        np.testing.assert_allclose(m, ref, rtol=1e-4, atol=1e-4)
+    b = rng.standard_normal((33, 45)).astype(np.float32)
+    mb = np.asarray(eng.computeDistanceMatrix(b, a, metric="manhattan"))
+    np.testing.assert_array_equal(mb, O.distances(b, a, O.L1))

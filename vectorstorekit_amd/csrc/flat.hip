@@ -588,7 +588,15 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
   a.metric = metric;
   a.mat = om.ptr<float>();
   a.ldm = db->n;
-  if (use_bf16x3(ctx, metric))
+  // L2 and L2^2 sum (q - x)^2 in dimension order, as the reference does: the
+  // norm expansion |q|^2 + |x|^2 - 2 q.x of the MFMA path cancels for close
+  // pairs (a duplicate row gets sqrt of the rounding error, not 0)
+  if (metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ) {
+    a.metric = exact_metric(metric);
+    a.xaux = nullptr;
+    a.qaux = nullptr;
+  }
+  if (use_bf16x3(ctx, a.metric))
     launch_flat_bf16x3(ctx, a, make_split(ctx, db, dq, nq, true, nullptr, nullptr),
                        MODE_MATRIX);
   else

@@ -255,3 +255,27 @@ class HIPAccelerationEngine:
     def search(self, queries, candidates, k: int, metric="euclidean"):
         """Top-k distances and ids."""
         return self._db(candidates, metric).search(queries, k, metric)
+
+    def computeDistanceMatrix(self, vectorsA, vectorsB=None, metric="euclidean"):
+        """MetalDistanceMatrix.computeDistanceMatrix (Acceleration/Metal/
+        MetalDistanceMatrix.swift:49-120): the |A| x |B| distance matrix;
+        vectorsB None is the symmetric matrix of A, whose upper triangle
+        (i <= j) is mirrored below the diagonal as the reference does
+        (:340-385): the split-bf16 products add their two cross terms in
+        opposite orders for (i, j) and (j, i), so only the mirror is exactly
+        symmetric."""
+        b = vectorsA if vectorsB is None else vectorsB
+        db = self._db(b, metric)
+        try:
+            m = db.distances(vectorsA, metric)
+        finally:
+            if db is not b:
+                db.free()
+        if vectorsB is None:
+            if _lib._is_torch(m):
+                import torch
+
+                m = torch.triu(m) + torch.triu(m, 1).T
+            else:
+                m = np.triu(m) + np.triu(m, 1).T
+        return m
