@@ -319,9 +319,12 @@ def setup(a, ctx, dev):
             "config": {"n": n, "d": d, "nq": nq, "k": k, "metric": "popcount(q xor x)"},
             "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), one bit "
                     "per dimension (x > 0)",
-            "dtype": "u32 words (popcount)", "nq": nq, "n": n, "d": d, "words": 4,
-            "kernels": [("bin_hamming_filter", "k_bin_scan<4, FILTER>", "valu_bin"),
-                        ("bin_hamming_dense", "k_bin_scan<4, DENSE>", "valu_bin")],
+            "dtype": "u1 codes (int8 MFMA on 0/1 bytes)", "nq": nq, "n": n, "d": d, "words": 4,
+            "kernels": [("bin_mfma_filter", "k_bin_mfma<2, 2, 8, FILTER> (int8 MFMA on bits "
+                         "spread to bytes: H = |q| + |x| - 2 q.x)", "int8"),
+                        ("bin_mfma_dense", "k_bin_mfma<2, 2, 8, DENSE>", "int8"),
+                        ("bin_hamming_filter", "k_bin_scan<4, FILTER> (popcount)", "valu_bin"),
+                        ("bin_hamming_dense", "k_bin_scan<4, DENSE> (popcount)", "valu_bin")],
             "keep": (db, xc, qc, dist, ids),
         }
         return spec, step, cpu_leg

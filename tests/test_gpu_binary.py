@@ -23,10 +23,14 @@ def test_binary_encode_bit_exact(ctx, d):
 
 @pytest.mark.parametrize("shape", [(50_000, 128, 37, 100), (3000, 37, 50, 10),
                                    (20_000, 1024, 9, 1024), (100, 64, 5, 300),
-                                   (200_000, 256, 70, 20), (9_000, 500, 33, 1)])
+                                   (200_000, 256, 70, 20), (9_000, 500, 33, 1),
+                                   (12_000, 1000, 40, 64), (30_001, 130, 16, 100),
+                                   (5_003, 96, 600, 7)])
 def test_bin_search_bit_exact(ctx, shape):
-    """Code widths of 1..8 16-byte groups (d = 37 .. 1024), k = 1 .. 1024,
-    k > n (padding), several chunks of the progressive scan; distances and
+    """Code widths of 4, 8, 16 and 32 words (d = 37 .. 1024), k = 1 .. 1024,
+    k > n (padding), several chunks of the progressive scan, partial row
+    groups (n = 5,003, 30,001), a partial query tile (16 and 600 queries on
+    the int8 matrix-core scan; under 16 on the popcount scan); distances and
     ids equal the oracle's (distance, id) order despite the large ties of
     integer distances."""
     n, d, nq, k = shape
