@@ -415,29 +415,25 @@ static void launch_bin_mfma(vsk_ctx *ctx, const BinMArgs &a, bool dense) {
 }
 
 // bit i of row r: x[r][i] > 0, at word i/32, bit i%32 (little-endian bytes:
-// byte i/8, bit i%8); one thread per output word, zero padding words
-__global__ void k_binary_encode(const float *x, int64_t n, int32_t d, int32_t ld,
-                                int32_t words, uint32_t *codes) {
-  const int64_t total = n * words;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / words;
-    const int32_t w = (int32_t)(i - r * words);
-    uint32_t v = 0;
-    const int32_t j0 = w * 32;
-    for (int32_t b = 0; b < 32 && j0 + b < d; ++b)
-      v |= (x[r * ld + j0 + b] > 0.f ? 1u : 0u) << b;
-    codes[i] = v;
-  }
-}
-
-__global__ void k_bin_popcount(const uint32_t *codes, int64_t n, int32_t words,
-                               int32_t *pop) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    int32_t s = 0;
-    for (int32_t w = 0; w < words; ++w) s += __builtin_popcount(codes[i * words + w]);
-    pop[i] = s;
+// byte i/8, bit i%8).  One wave per (row, 64 dimensions): the lanes read 64
+// consecutive components (coalesced) and one ballot of x > 0 is the two
+// words; lanes past d read 0, so padding bits are 0.
+__global__ __launch_bounds__(256) void k_binary_encode(const float *x, int64_t n, int32_t d,
+                                                       int32_t ld, int32_t words,
+                                                       uint32_t *codes) {
+  const int lane = threadIdx.x & 63;
+  const int32_t chunks = (words + 1) / 2;  // 64-bit pieces per row
+  const int64_t total = n * chunks;
+  const int64_t wid = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t t = wid; t < total; t += nw) {
+    const int64_t r = t / chunks;
+    const int32_t c = (int32_t)(t - r * chunks);
+    const int32_t j = 64 * c + lane;
+    const float v = j < d ? x[r * ld + j] : 0.f;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(v > 0.f);
+    if (lane < 2 && 2 * c + lane < words)
+      codes[r * words + 2 * c + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
   }
 }
 
@@ -461,8 +457,16 @@ static unsigned grid_n(int64_t n) {
   return (unsigned)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
 }
 
-// words per code: 4, 8, 16 or 32 (the MFMA scan's k-steps of 64 bits come
-// in powers of two)
+__global__ void k_bin_popcount(const uint32_t *codes, int64_t n, int32_t words,
+                               int32_t *pop) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int32_t s = 0;
+    for (int32_t w = 0; w < words; ++w) s += __builtin_popcount(codes[i * words + w]);
+    pop[i] = s;
+  }
+}
+
 static int32_t bin_words(int32_t d) {
   int32_t w = 4;
   while (w * 32 < d) w *= 2;
@@ -501,7 +505,10 @@ vsk_status vsk_binary_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
       ctx->scratch_ptr("bin.enc", sizeof(uint32_t) * (size_t)n * words));
   {
     KernelTimer t(ctx, "binary_encode", (double)n);
-    k_binary_encode<<<grid_n(n * words), 256, 0, ctx->stream>>>(dx, n, d, ld, words, w);
+    const int64_t waves = n * ((words + 1) / 2);
+    const int64_t g = ceil_div(waves, 4);
+    k_binary_encode<<<(unsigned)(g < 65536 ? (g > 0 ? g : 1) : 65536), 256, 0, ctx->stream>>>(
+        dx, n, d, ld, words, w);
     check_launch("binary_encode");
   }
   const int32_t bytes = (d + 7) / 8;
