@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="target length of the CPU baseline sample")
+    p.add_argument("--kmeans-init", default="random", choices=["random", "kmeans++"],
+                   help="c3train: the seeding (random rows or k-means++ on the device)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 3 times (the "
                         "reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -229,8 +231,10 @@ def setup(a, ctx, dev):
         # IVF coarse training at config 3's scale: one step = one vsk_kmeans
         # call, 10 Lloyd iterations (tolerance 0 never stops early) from 4,096
         # seeded random rows
-        from vectorstorekit_amd.clustering import (INIT_RANDOM, vsk_kmeans_result)
+        from vectorstorekit_amd.clustering import (INIT_PLUSPLUS, INIT_RANDOM,
+                                                   vsk_kmeans_result)
         n, d, ncent, iters = 1_000_000, 128, 4096, 10
+        init = INIT_PLUSPLUS if a.kmeans_init == "kmeans++" else INIT_RANDOM
         x, _, _ = gen_mixture(n, d, ncent, 1, dev, jitter=False)
         cent = torch.empty(ncent, d, device=dev)
         assign = torch.empty(n, dtype=torch.int32, device=dev)
@@ -238,7 +242,7 @@ def setup(a, ctx, dev):
         import ctypes
 
         def step():
-            ctx.check(lib.vsk_kmeans(ctx.handle, x.data_ptr(), n, d, ncent, None, INIT_RANDOM,
+            ctx.check(lib.vsk_kmeans(ctx.handle, x.data_ptr(), n, d, ncent, None, init,
                                      None, ctypes.c_uint64(7), iters, 0.0, cent.data_ptr(),
                                      assign.data_ptr(), ctypes.byref(res)))
 
@@ -269,12 +273,15 @@ def setup(a, ctx, dev):
             "metric": "k-means row-iterations/s, 1M x 128, k = 4096 (IVF training at "
                       "config 3's scale)",
             "workload": "kmeans-1Mx128-k4096-iter10 (IVF coarse training, BASELINE config 3 data)",
-            "config": {"n": n, "d": d, "k": ncent, "iterations": iters, "init": "random (seed 7)"},
+            "config": {"n": n, "d": d, "k": ncent, "iterations": iters,
+                       "init": f"{a.kmeans_init} (seed 7)"},
             "data": "synthetic: 4,096-Gaussian mixture, centres 2 N(0,I) (seed 3), points "
                     "centre + 0.5 N(0,I) (seeds 5, 1)",
             "dtype": "f32", "nq": n, "n": ncent, "d": d,
             "units_per_step": n * iters, "unit": "row-iterations/s",
-            "kernels": [("flat_valu_argmin", "k_flat_valu<ARGMIN> (exact sqrt-L2, dimension "
+            "kernels": [("kmeans_plusplus", "k-means++ seeding (k_kpp_update / blocksum / "
+                         "pick per centroid)", "kpp"),
+                        ("flat_valu_argmin", "k_flat_valu<ARGMIN> (exact sqrt-L2, dimension "
                          "order)", "valu_l2"),
                         ("flat_screen_top2", "k_flat_screen<TOP2> (bf16 screen, smallest two per "
                          "row)", "mfma_bf16")],
@@ -517,6 +524,15 @@ def roofline(spec, stats):
                                      "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
                                      "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
                                                           / PEAK_HBM_GBPS, 4)}
+    elif kind == "kpp":
+        # per pick every row's distance to the new centroid: 4*d bytes read
+        # per (row, pick) pair at least (the rows stream from HBM)
+        by = 4.0 * d * pairs
+        ach = by / sec / 1e9
+        r.update({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                  "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
+                  "algorithmic": "4*d bytes per (row, pick): every row read once per new "
+                                 "centroid"})
     elif kind == "valu_bin":
         # one v_xor_b32 and one v_bcnt_u32_b32 per 32-bit word per pair
         ops = 2.0 * spec["words"] * pairs

@@ -323,38 +323,156 @@ __global__ void k_gather_rows_i64(const float *src, int64_t ld, const int64_t *r
 // ---------------------------------------------------------------------------
 constexpr int KP_T = 256;
 
-// D[i] = min(D[i], |x_i - x_c|) with c = chosen[r] (sequential sqrt-L2, as
-// computeMinDistances, :401-419); maxbits[r + 1] = max over rows of D^2
-// (non-negative floats order as their bits)
-__global__ __launch_bounds__(KP_T) void k_kpp_update(const float *x, int64_t ld,
-                                                     int32_t d, int64_t n,
-                                                     const int64_t *chosen, int r,
-                                                     float *D, uint32_t *maxbits) {
+constexpr int KPU_C = 32;     // columns of one staged chunk in k_kpp_update
+constexpr int KP_SLOTS = 64;  // max slots per pick (a power of two, one wave's lanes)
+constexpr int KPU_GRID = 4096;  // waves of k_kpp_update at most (16 per CU)
+
+// cc[a] = |x_c - x_{chosen[a]}| for the picks a < r, c = chosen[r]: one
+// wave per a, lanes over the coordinates.  Only the triangle test of
+// k_kpp_update reads it, so any summation order with a small relative error
+// serves (this one's is under (d / 64 + 11) 2^-25).
+__global__ __launch_bounds__(256) void k_kpp_cc(const float *x, int64_t ld, int32_t d,
+                                                const int64_t *chosen, int r, float *cc) {
 #pragma clang fp contract(off)
   const int64_t c = chosen[r];
-  if (c < 0) return;  // an earlier pick found degenerate data
-  const int64_t i = blockIdx.x * (int64_t)KP_T + threadIdx.x;
-  float w = 0.f;
-  if (i < n) {
-    const float *xi = x + i * ld, *xc = x + c * ld;
-    float s = 0.f;
-    for (int32_t j = 0; j < d; ++j) {
-      const float t = xi[j] - xc[j];
-      s = s + t * t;
-    }
-    const float dist = sqrtf(s);
-    float dm = D[i];
-    dm = dist < dm ? dist : dm;
-    D[i] = dm;
-    w = dm * dm;
+  if (c < 0) return;
+  const int a = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (a >= r) return;  // wave-uniform
+  const float *xc = x + c * ld, *xa = x + chosen[a] * ld;
+  float s = 0.f;
+  for (int32_t j = lane; j < d; j += 64) {
+    const float t = xc[j] - xa[j];
+    s = s + t * t;
   }
-  uint32_t b = __float_as_uint(w);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) s = s + __shfl_xor(s, m);
+  if (lane == 0) cc[a] = sqrtf(s);
+}
+
+// D[i] = min(D[i], |x_i - x_c|) with c = chosen[r] (sequential sqrt-L2, as
+// computeMinDistances, :401-419), near[i] = the pick that set D[i]; the max
+// over rows of D^2 lands in maxbits[(r + 1) * KP_SLOTS + s] for the KP_SLOTS
+// slots s (non-negative floats order as their bits; spread so the atomics
+// do not queue on one address).
+//
+// One wave per block strides over groups of 64 rows.  A row is skipped
+// (not read) when its nearest pick a has |x_c - x_a| >= 2 D skipm,
+// skipm = 1 + (d + 4) 2^-22.  The exact distance is >= |x_c - x_a| -
+// |x_i - x_a|, and (d + 4) 2^-22 exceeds the relative errors of the three
+// computed distances taken together (a sequential one: under (d + 4) 2^-25;
+// k_kpp_cc's: under (d / 64 + 11) 2^-25, counted twice), so the computed
+// distance would be >= D and D[i] would not change.  The test is only taken
+// for 2^-60 <= D <= 2^60, where no sum under- or overflows enough to break
+// the relative bounds.  The rows that do need the distance queue in LDS;
+// each full batch of 64 is staged through LDS in 128-byte column chunks
+// (coalesced) and every lane sums its own row in coordinate order.
+__global__ __launch_bounds__(64) void k_kpp_update(const float *__restrict__ x, int64_t ld,
+                                                   int32_t d, int64_t n,
+                                                   const int64_t *__restrict__ chosen, int r,
+                                                   const float *__restrict__ cc, float skipm,
+                                                   float *__restrict__ D,
+                                                   int32_t *__restrict__ near,
+                                                   uint32_t *__restrict__ maxbits) {
+#pragma clang fp contract(off)
+  __shared__ float tile[64 * (KPU_C + 1)];
+  __shared__ int64_t l_row[128];
+  __shared__ float l_dm[128];
+  const int64_t c = chosen[r];
+  if (c < 0) return;  // an earlier pick found degenerate data
+  const int lane = threadIdx.x;
+  const float *__restrict__ xc = x + c * ld;
+  uint32_t b = 0;  // max D^2 bits seen by this lane
+  // the distances of the first m <= 64 queued rows
+  auto run = [&](int m) {
+    float s = 0.f;
+    for (int32_t j0 = 0; j0 < d; j0 += KPU_C) {
+      const int cw = d - j0 < KPU_C ? d - j0 : KPU_C;
+      __syncthreads();  // the previous chunk has been read
+#pragma unroll
+      for (int t = 0; t < KPU_C; ++t) {
+        const int rr = t * (64 / KPU_C) + lane / KPU_C, col = lane % KPU_C;
+        if (rr < m && col < cw)
+          tile[rr * (KPU_C + 1) + col] = x[l_row[rr] * ld + j0 + col];
+      }
+      __syncthreads();
+      if (lane < m)
+        for (int jj = 0; jj < cw; ++jj) {
+          const float t = tile[lane * (KPU_C + 1) + jj] - xc[j0 + jj];
+          s = s + t * t;
+        }
+    }
+    if (lane < m) {
+      float dm = l_dm[lane];
+      const float dist = sqrtf(s);
+      if (dist < dm) {
+        dm = dist;
+        const int64_t i = l_row[lane];
+        D[i] = dm;
+        near[i] = r;
+      }
+      const uint32_t bw = __float_as_uint(dm * dm);
+      b = bw > b ? bw : b;
+    }
+  };
+  int cnt = 0;  // queued rows (wave-uniform)
+  for (int64_t row0 = (int64_t)blockIdx.x * 64; row0 < n; row0 += (int64_t)gridDim.x * 64) {
+    const int64_t i = row0 + lane;
+    bool need = false;
+    float dm = 0.f;
+    if (i < n) {
+      dm = D[i];
+      const int32_t a = near[i];
+      need = !(a >= 0 && dm >= 0x1p-60f && dm <= 0x1p60f && cc[a] >= 2.0f * dm * skipm);
+      if (!need) {
+        const uint32_t bw = __float_as_uint(dm * dm);
+        b = bw > b ? bw : b;
+      }
+    }
+    const uint64_t mask = __ballot(need);
+    if (need) {
+      const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi(
+                                (uint32_t)(mask >> 32),
+                                __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+      l_row[pos] = i;
+      l_dm[pos] = dm;
+    }
+    cnt += __popcll(mask);
+    if (cnt >= 64) {
+      __syncthreads();
+      run(64);
+      __syncthreads();
+      if (lane < cnt - 64) {
+        l_row[lane] = l_row[64 + lane];
+        l_dm[lane] = l_dm[64 + lane];
+      }
+      cnt -= 64;
+    }
+  }
+  if (cnt > 0) {
+    __syncthreads();
+    run(cnt);
+  }
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) {
     const uint32_t o = __shfl_xor(b, m);
     b = o > b ? o : b;
   }
-  if ((threadIdx.x & 63) == 0) atomicMax(&maxbits[r + 1], b);
+  if (lane == 0) atomicMax(&maxbits[(r + 1) * KP_SLOTS + blockIdx.x % KP_SLOTS], b);
+}
+
+// the max of pick r + 1's KP_SLOTS slots, through LDS to the whole block
+__device__ inline float kpp_maxw(const uint32_t *maxbits, int r, uint32_t *sm) {
+  if (threadIdx.x < 64) {
+    uint32_t b = maxbits[(r + 1) * KP_SLOTS + threadIdx.x];
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+      const uint32_t o = __shfl_xor(b, m);
+      b = o > b ? o : b;
+    }
+    if (threadIdx.x == 0) *sm = b;
+  }
+  __syncthreads();
+  return __uint_as_float(*sm);
 }
 
 // the 32-bit fixed-point weight of D^2 (exact: one correctly rounded
@@ -371,8 +489,9 @@ __global__ __launch_bounds__(KP_T) void k_kpp_blocksum(const float *D, int64_t n
                                                        const int64_t *chosen, int r,
                                                        uint64_t *bsum) {
   __shared__ uint64_t ws[KP_T / 64];
+  __shared__ uint32_t s_mx;
   if (chosen[r] < 0) return;
-  const float maxw = __uint_as_float(maxbits[r + 1]);
+  const float maxw = kpp_maxw(maxbits, r, &s_mx);
   const int64_t i = blockIdx.x * (int64_t)KP_T + threadIdx.x;
   uint64_t f = i < n ? kpp_fixed(D[i], maxw) : 0;
 #pragma unroll
@@ -474,7 +593,8 @@ __global__ __launch_bounds__(1024) void k_kpp_pick(const uint64_t *bsum, int64_t
     if (t == 0) chosen[r + 1] = -1;
     return;
   }
-  const float maxw = __uint_as_float(maxbits[r + 1]);
+  __shared__ uint32_t s_mx;
+  const float maxw = kpp_maxw(maxbits, r, &s_mx);
   const int64_t i = blk * KP_T + t;
   const uint64_t f = (t < KP_T && i < n) ? kpp_fixed(D[i], maxw) : 0;
   uint64_t tot2;
@@ -586,9 +706,14 @@ static bool init_plusplus(vsk_ctx *ctx, const float *dx, int64_t n, int32_t d,
   KernelTimer tm(ctx, "kmeans_plusplus", (double)n * k);
   float *D = static_cast<float *>(ctx->scratch_ptr("km.kppD", sizeof(float) * (size_t)n));
   fill_i32(ctx, reinterpret_cast<int32_t *>(D), n, 0x7F800000);  // +inf
+  int32_t *near = static_cast<int32_t *>(
+      ctx->scratch_ptr("km.kppnear", sizeof(int32_t) * (size_t)n));
+  fill_i32(ctx, near, n, -1);
+  float *cc = static_cast<float *>(ctx->scratch_ptr("km.kppcc", sizeof(float) * (size_t)k));
+  const float skipm = 1.0f + (float)(d + 4) * 0x1p-22f;
   uint32_t *maxbits = static_cast<uint32_t *>(
-      ctx->scratch_ptr("km.kppmax", sizeof(uint32_t) * (size_t)(k + 1)));
-  fill_i32(ctx, reinterpret_cast<int32_t *>(maxbits), k + 1, 0);
+      ctx->scratch_ptr("km.kppmax", sizeof(uint32_t) * (size_t)(k + 1) * KP_SLOTS));
+  fill_i32(ctx, reinterpret_cast<int32_t *>(maxbits), (int64_t)(k + 1) * KP_SLOTS, 0);
   const int64_t nb = ceil_div(n, KP_T);
   uint64_t *bsum = static_cast<uint64_t *>(
       ctx->scratch_ptr("km.kppbsum", sizeof(uint64_t) * (size_t)nb));
@@ -602,8 +727,11 @@ static bool init_plusplus(vsk_ctx *ctx, const float *dx, int64_t n, int32_t d,
   VSK_HIP(hipMemcpyAsync(rng, &init[1], sizeof(uint64_t), hipMemcpyHostToDevice,
                          ctx->stream));
   for (int r = 0; r + 1 < k; ++r) {
-    k_kpp_update<<<(unsigned)nb, KP_T, 0, ctx->stream>>>(dx, ld, d, n, chosen, r, D,
-                                                         maxbits);
+    if (r > 0)
+      k_kpp_cc<<<(unsigned)ceil_div(r, 4), 256, 0, ctx->stream>>>(dx, ld, d, chosen, r, cc);
+    k_kpp_update<<<(unsigned)std::min<int64_t>(ceil_div(n, 64), KPU_GRID), 64, 0,
+                   ctx->stream>>>(
+        dx, ld, d, n, chosen, r, cc, skipm, D, near, maxbits);
     k_kpp_blocksum<<<(unsigned)nb, KP_T, 0, ctx->stream>>>(D, n, maxbits, chosen, r,
                                                            bsum);
     k_kpp_pick<<<1, 1024, 0, ctx->stream>>>(bsum, nb, D, n, maxbits, rng, r, chosen);
