@@ -191,6 +191,37 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
 /* sizes[nlist] = rows per inverted list; total = sum */
 vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
                               int64_t *sizes);
+/* ---- IVF-SQ8 and IVF-PQ ----------------------------------------------------
+ * IVFConfiguration declares quantized lists (Config/Indexes/IVFConfiguration.
+ * swift:13,18-21) that IVFIndex never implements.  Here an IVF index can
+ * carry codes of its stored rows in the same list order, and a search
+ * probes lists exactly as vsk_ivf_search (IVFIndex.search, Indexes/
+ * IVFIndex.swift:149-202) but scores the probed lists' codes:
+ *  - SQ8: score = sum_j qcode_j * code_j, the vsk_sq8_search score
+ *    (codes from vsk_sq8_encode with the given parameters, ScalarQuantizer.
+ *    quantizeToInt8, Quantization/ScalarQuantizer.swift:251-270);
+ *  - PQ: the ADC sum of vsk_pq_search (DistanceTables.computeDistance,
+ *    Quantization/ProductQuantizerTypes.swift:14-20), codes from
+ *    vsk_pq_encode; returned as its square root.
+ * Candidates are ordered as the stable sort of IVFIndex.search orders them:
+ * by score (descending) or ADC sum (ascending), ties in probe order then
+ * list order.  Codes are made from the rows the index holds at the call;
+ * rows added later make the search fail with VSK_ERR_NOT_TRAINED until
+ * the index is encoded again. */
+vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,
+                              const float *scale, const float *offset);
+vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq);
+/* q: nq x d fp32 (probing); qcodes: nq x d int8 (vsk_sq8_encode of q with
+ * the same parameters).  out_score nq x k (INT32_MIN / -1 where missing). */
+vsk_status vsk_ivf_search_sq8(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                              const int8_t *qcodes, int64_t nq, int32_t nprobe, int32_t k,
+                              int32_t *out_score, int64_t *out_ids);
+/* pq: the quantizer the codes were made with.  out_dist nq x k = sqrt of
+ * the ADC sum (+inf / -1 where missing). */
+vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
+                             const float *q, int64_t nq, int32_t nprobe, int32_t k,
+                             float *out_dist, int64_t *out_ids);
+
 
 /* ---- int8 scalar quantization ---------------------------------------------
  * ScalarQuantizer (Quantization/ScalarQuantizer.swift).  per_dim = 0 is the

@@ -320,3 +320,59 @@ def bin_search(qcodes, codes, d, k, threads=0):
     oi = np.empty((nq, k), np.int64)
     lib().vsko_bin_search(qp, nq, cp, c.shape[0], d, k, od.ctypes.data, oi.ctypes.data, threads)
     return od, oi
+
+
+def _ivf_candidates(q, list_of, centroids, nprobe):
+    """Per query: the candidate rows of IVFIndex.search (Indexes/
+    IVFIndex.swift:149-202) in its concatenation order -- probed lists in
+    probe order, each list's rows in insertion (row) order."""
+    list_of = np.asarray(list_of)
+    probes = ivf_probe(q, centroids, nprobe)
+    members = {}
+    out = []
+    for pr in probes:
+        rows = []
+        for l in pr:
+            if l < 0:
+                continue
+            if l not in members:
+                members[l] = np.nonzero(list_of == l)[0]
+            rows.append(members[l])
+        out.append(np.concatenate(rows) if rows else np.zeros(0, np.int64))
+    return out
+
+
+def ivf_sq8_search(q, qcodes, codes, ids, list_of, centroids, nprobe, k):
+    """IVF-SQ8: probe as ivf_search, score the candidates' codes with
+    sq8 scores (int64 dot of int8 codes), stable order by descending
+    score; (scores int32 [nq, k], ids) padded with INT32_MIN / -1."""
+    qc = np.asarray(qcodes, np.int64)
+    codes = np.asarray(codes, np.int64)
+    ids = np.asarray(ids, np.int64)
+    nq = qc.shape[0]
+    os_ = np.full((nq, k), np.iinfo(np.int32).min, np.int32)
+    oi = np.full((nq, k), -1, np.int64)
+    for i, rows in enumerate(_ivf_candidates(q, list_of, centroids, nprobe)):
+        sc = codes[rows] @ qc[i]
+        order = np.argsort(-sc, kind="stable")[:k]
+        os_[i, :len(order)] = sc[order]
+        oi[i, :len(order)] = ids[rows[order]]
+    return os_, oi
+
+
+def ivf_pq_search(q, codebooks, codes, ids, list_of, centroids, nprobe, k):
+    """IVF-PQ: probe as ivf_search, ADC sums of the candidates' codes
+    (pq_adc_scan: fp32 in segment order), stable ascending order; returns
+    (sqrt of the sum float32 [nq, k], ids) padded with +inf / -1."""
+    q = np.ascontiguousarray(q, np.float32)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    ids = np.asarray(ids, np.int64)
+    nq = q.shape[0]
+    od = np.full((nq, k), np.inf, np.float32)
+    oi = np.full((nq, k), -1, np.int64)
+    for i, rows in enumerate(_ivf_candidates(q, list_of, centroids, nprobe)):
+        s = pq_adc_scan(pq_lut(q[i], codebooks), codes[rows])
+        order = np.argsort(s, kind="stable")[:k]
+        od[i, :len(order)] = np.sqrt(s[order])
+        oi[i, :len(order)] = ids[rows[order]]
+    return od, oi

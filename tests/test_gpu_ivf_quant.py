@@ -1,0 +1,108 @@
+"""IVF-SQ8 and IVF-PQ on the GPU against the oracle's composition (IVF
+probing + SQ8 scores / PQ ADC sums, stable candidate order).  Probing is
+exact and the scores are exact integers or fixed-order fp32 sums, so
+scores, distances and ids must be bit-identical."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from vectorstorekit_amd import (IVFConfiguration, IVFIndex, ProductQuantizer, ScalarQuantizer,
+                                VSKError)
+
+pytestmark = pytest.mark.gpu
+
+
+def _mixture(seed, ncent, n, d, nq):
+    rng = np.random.default_rng(seed)
+    cent = (2.0 * rng.standard_normal((ncent, d))).astype(np.float32)
+    a = rng.integers(0, ncent, n)
+    x = (cent[a] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    qa = rng.integers(0, ncent, nq)
+    q = (cent[qa] + 0.5 * rng.standard_normal((nq, d))).astype(np.float32)
+    c = (cent + 0.1 * rng.standard_normal(cent.shape)).astype(np.float32)
+    return x, q, c
+
+
+def _index(ctx, c, x, nprobe):
+    idx = IVFIndex(ctx, IVFConfiguration(dimensions=c.shape[1], numberOfCentroids=c.shape[0],
+                                         numberOfProbes=nprobe))
+    idx.set_centroids(c)
+    idx.insert(x)
+    return idx
+
+
+# (nlist, n, d, nq, nprobe, k, per_dim)
+SQ_SHAPES = [(64, 20_000, 128, 100, 8, 10, True), (37, 5000, 33, 50, 5, 7, False),
+             (16, 3000, 24, 40, 16, 20, True), (8, 600, 200, 17, 2, 300, True)]
+
+
+@pytest.mark.parametrize("shape", SQ_SHAPES)
+def test_ivf_sq8_bit_exact(ctx, shape):
+    nlist, n, d, nq, nprobe, k, per_dim = shape
+    x, q, c = _mixture(nlist + d, nlist, n, d, nq)
+    idx = _index(ctx, c, x, nprobe)
+    sq = ScalarQuantizer(ctx, per_dim=per_dim)
+    sq.train(x)
+    idx.encodeSQ8(sq)
+    score, ids = idx.searchSQ8(q, k)
+    codes = O.sq8_encode(x, sq.scale, sq.offset)
+    qc = O.sq8_encode(q, sq.scale, sq.offset)
+    es, ei = O.ivf_sq8_search(q, qc, codes, np.arange(n), O.ivf_assign(x, c), c, nprobe, k)
+    np.testing.assert_array_equal(score, es)
+    np.testing.assert_array_equal(ids, ei)
+
+
+# (nlist, n, M, dsub, nq, nprobe, k)
+PQ_SHAPES = [(64, 20_000, 16, 8, 100, 8, 10), (37, 5000, 8, 4, 50, 5, 7),
+             (16, 3000, 6, 5, 40, 16, 20), (8, 600, 16, 12, 17, 2, 300)]
+
+
+@pytest.mark.parametrize("shape", PQ_SHAPES)
+def test_ivf_pq_bit_exact(ctx, shape):
+    nlist, n, M, dsub, nq, nprobe, k = shape
+    d = M * dsub
+    x, q, c = _mixture(nlist + M, nlist, n, d, nq)
+    rng = np.random.default_rng(M)
+    cb = x[rng.choice(n, 256, replace=False)].reshape(256, M, dsub).transpose(1, 0, 2).copy()
+    idx = _index(ctx, c, x, nprobe)
+    pq = ProductQuantizer(ctx, cb)
+    idx.encodePQ(pq)
+    dist, ids = idx.searchPQ(q, k)
+    codes = O.pq_encode(x, cb)
+    ed, ei = O.ivf_pq_search(q, cb, codes, np.arange(n), O.ivf_assign(x, c), c, nprobe, k)
+    np.testing.assert_array_equal(dist, ed)
+    np.testing.assert_array_equal(ids, ei)
+
+
+def test_ivf_sq8_all_lists_is_the_flat_sq8_scan(ctx):
+    x, q, c = _mixture(5, 16, 4000, 64, 30)
+    idx = _index(ctx, c, x, 16)
+    sq = ScalarQuantizer(ctx)
+    sq.train(x)
+    idx.encodeSQ8(sq)
+    score, _ = idx.searchSQ8(q, 25, strategy="exact")
+    codes = O.sq8_encode(x, sq.scale, sq.offset)
+    es, _ = O.sq8_search(O.sq8_encode(q, sq.scale, sq.offset), codes, 25)
+    np.testing.assert_array_equal(score, es)
+
+
+def test_ivf_codes_follow_inserts(ctx):
+    x, q, c = _mixture(9, 8, 2000, 32, 10)
+    idx = _index(ctx, c, x[:1500], 3)
+    sq = ScalarQuantizer(ctx)
+    sq.train(x)
+    with pytest.raises(VSKError):
+        idx.searchSQ8(q, 5)  # nothing encoded yet
+    idx.encodeSQ8(sq)
+    idx.insert(x[1500:])
+    with pytest.raises(VSKError):
+        idx.searchSQ8(q, 5)  # stale codes
+    idx.encodeSQ8(sq)
+    score, ids = idx.searchSQ8(q, 5)
+    codes = O.sq8_encode(x, sq.scale, sq.offset)
+    es, ei = O.ivf_sq8_search(q, O.sq8_encode(q, sq.scale, sq.offset), codes, np.arange(2000),
+                              O.ivf_assign(x, c), c, 3, 5)
+    np.testing.assert_array_equal(score, es)
+    np.testing.assert_array_equal(ids, ei)
+    with pytest.raises(VSKError):
+        idx.searchPQ(q, 5)  # the index holds SQ8 codes

@@ -260,3 +260,31 @@ def test_decoders_exact():
     pc = rng.integers(0, 256, (200, 4)).astype(np.uint8)
     want = np.concatenate([cb[m][pc[:, m]] for m in range(4)], axis=1)
     np.testing.assert_array_equal(O.pq_decode(pc, cb), want)
+
+
+def test_ivf_coded_oracles_over_every_list():
+    """nprobe = nlist: the IVF-SQ8 / IVF-PQ oracles see every row, so their
+    scores and distances are those of the flat SQ8 scan and of the
+    non-re-ranked PQ search; and a hand-built candidate set for one query
+    (the numpy-float64-nearest lists) gives the same top scores."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((900, 16)).astype(np.float32)
+    q = rng.standard_normal((6, 16)).astype(np.float32)
+    c = rng.standard_normal((12, 16)).astype(np.float32)
+    lo = O.ivf_assign(x, c)
+    s, o = O.sq8_train(x)
+    codes, qc = O.sq8_encode(x, s, o), O.sq8_encode(q, s, o)
+    es, _ = O.ivf_sq8_search(q, qc, codes, np.arange(900), lo, c, 12, 40)
+    fs, _ = O.sq8_search(qc, codes, 40)
+    np.testing.assert_array_equal(es, fs)
+    cb = x[:256 * 1].reshape(256, 4, 4).transpose(1, 0, 2).copy()
+    pc = O.pq_encode(x, cb)
+    ed, _ = O.ivf_pq_search(q, cb, pc, np.arange(900), lo, c, 12, 40)
+    fd, _ = O.pq_search(q, cb, pc, 40, 40)
+    np.testing.assert_array_equal(ed, fd)
+    # three probes of query 0 by float64 distance
+    d0 = ((c.astype(np.float64) - q[0]) ** 2).sum(1)
+    rows = np.nonzero(np.isin(lo, np.argsort(d0)[:3]))[0]
+    sc = codes[rows].astype(np.int64) @ qc[0].astype(np.int64)
+    ps, _ = O.ivf_sq8_search(q[:1], qc[:1], codes, np.arange(900), lo, c, 3, 10)
+    np.testing.assert_array_equal(ps[0], np.sort(sc)[::-1][:10])

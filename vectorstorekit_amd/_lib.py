@@ -101,6 +101,10 @@ SIGNATURES = {
     "vsk_ivf_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P]),
     "vsk_ivf_build": (c_int32, [P, P, c_int32, P, P, c_int64, c_int32, PP]),
     "vsk_ivf_list_sizes": (c_int32, [P, P, P]),
+    "vsk_ivf_encode_sq8": (c_int32, [P, P, c_int32, P, P]),
+    "vsk_ivf_encode_pq": (c_int32, [P, P, P]),
+    "vsk_ivf_search_sq8": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
+    "vsk_ivf_search_pq": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_train": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_encode": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
     "vsk_sq8_upload": (c_int32, [P, P, c_int64, c_int32, PP]),

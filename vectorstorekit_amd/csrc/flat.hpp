@@ -147,4 +147,8 @@ int32_t screen_keep(int32_t k);
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  int32_t k, int32_t metric, uint64_t *best);
 
+// a PQ quantizer's shape for other translation units: returns d
+int32_t pq_shape(const vsk_pq *pq, int32_t *M, int32_t *ksub);
+bool pq_shape_matches(const vsk_pq *pq, int32_t d, int32_t M, int32_t ksub);
+
 }  // namespace vsk

@@ -39,6 +39,12 @@ struct vsk_ivf {
   std::vector<int64_t> off;  // nlist+1
   int64_t total = 0;
   int64_t next_id = 0;
+  // codes of the stored rows, same list-grouped order (vsk_ivf_encode_*):
+  // kind 1 = SQ8 (d int8), 2 = PQ (M uint8); rows of cstride bytes, zero
+  // padded; valid while ctotal == total
+  vsk::DevBuf codes;
+  int32_t ckind = 0, cstride = 0, cM = 0, cksub = 0;
+  int64_t ctotal = -1;
 };
 
 namespace vsk {
@@ -109,7 +115,101 @@ struct ListScanArgs {
   const int64_t *seg_off;   // [nq+1] candidate segment offsets
   uint64_t *cand;
   int32_t squared;          // 1: key on sum (q-x)^2, 0: on its sqrt
+  // coded scans
+  const uint8_t *codes;     // list-grouped codes, cstride bytes per row
+  int32_t cstride;
+  const int8_t *qc;         // SQ8: query codes, cstride bytes each (batch)
+  const float *lut;         // PQ: [nq][M][ksub] (batch)
+  int32_t M, ksub;
 };
+
+// the QG query slots of a group: query index, candidate-segment base and
+// position base of each (slots past the group's count repeat its first)
+#define VSK_GROUP_SLOTS(QG)                                        \
+  const int4 g = a.groups[blockIdx.x];                             \
+  const int32_t l = g.x;                                           \
+  const int npair = g.z;                                           \
+  const int64_t v0 = a.list_off[l], v1 = a.list_off[l + 1];        \
+  int32_t qidx[QG];                                                \
+  int64_t obase[QG], tbase[QG];                                    \
+  _Pragma("unroll") for (int j = 0; j < QG; ++j) {                 \
+    const int32_t pid = a.pairs[g.y + (j < npair ? j : 0)];        \
+    qidx[j] = pid / a.np;                                          \
+    obase[j] = a.seg_off[qidx[j]] + a.pos_base[pid];               \
+    tbase[j] = a.pos_base[pid];                                    \
+  }
+
+// IVF-SQ8 list scan: score = sum_j qcode_j * code_j (exact int32, four
+// products per v_dot4), keyed as distance -score.  Query codes of the group
+// in LDS, one row per thread, 16-byte code loads.
+template <int QG>
+__global__ __launch_bounds__(256) void k_list_scan_sq8(ListScanArgs a) {
+  extern __shared__ int32_t qw[];  // QG x cstride bytes
+  VSK_GROUP_SLOTS(QG)
+  const int cw = a.cstride / 4;
+  for (int i = threadIdx.x; i < QG * cw; i += blockDim.x) {
+    const int j = i / cw, c = i - j * cw;
+    qw[i] = reinterpret_cast<const int32_t *>(a.qc + (int64_t)qidx[j] * a.cstride)[c];
+  }
+  __syncthreads();
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+    const int4 *x = reinterpret_cast<const int4 *>(a.codes + v * a.cstride);
+    int32_t acc[QG];
+#pragma unroll
+    for (int j = 0; j < QG; ++j) acc[j] = 0;
+    for (int c = 0; c < cw / 4; ++c) {
+      const int4 xv = x[c];
+#pragma unroll
+      for (int j = 0; j < QG; ++j) {
+        const int4 qv = reinterpret_cast<const int4 *>(qw + j * cw)[c];
+        acc[j] = __builtin_amdgcn_sdot4(qv.x, xv.x, acc[j], false);
+        acc[j] = __builtin_amdgcn_sdot4(qv.y, xv.y, acc[j], false);
+        acc[j] = __builtin_amdgcn_sdot4(qv.z, xv.z, acc[j], false);
+        acc[j] = __builtin_amdgcn_sdot4(qv.w, xv.w, acc[j], false);
+      }
+    }
+    const int64_t i = v - v0;
+#pragma unroll
+    for (int j = 0; j < QG; ++j)
+      if (j < npair) a.cand[obase[j] + i] = vsk_key_i32(-acc[j], (uint32_t)(tbase[j] + i));
+  }
+}
+
+// IVF-PQ list scan: ADC sum = sum over segments m, in order, of
+// lut[q][m][code_m] (fp32, each addition rounded: DistanceTables.
+// computeDistance, Quantization/ProductQuantizerTypes.swift:14-20).  The
+// group's tables in LDS, one row per thread, 4-byte code loads.
+template <int QG>
+__global__ __launch_bounds__(256) void k_list_scan_pq(ListScanArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float tl[];  // QG x M x ksub
+  VSK_GROUP_SLOTS(QG)
+  const int tsz = a.M * a.ksub;
+  for (int i = threadIdx.x; i < QG * tsz; i += blockDim.x) {
+    const int j = i / tsz, c = i - j * tsz;
+    tl[i] = a.lut[(int64_t)qidx[j] * tsz + c];
+  }
+  __syncthreads();
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+    const uint32_t *x = reinterpret_cast<const uint32_t *>(a.codes + v * a.cstride);
+    float acc[QG];
+#pragma unroll
+    for (int j = 0; j < QG; ++j) acc[j] = 0.f;
+    for (int m0 = 0; m0 < a.M; m0 += 4) {
+      const uint32_t w = x[m0 >> 2];
+      const int mm = a.M - m0 < 4 ? a.M - m0 : 4;
+      for (int t = 0; t < mm; ++t) {
+        const int off = (m0 + t) * a.ksub + (int)((w >> (8 * t)) & 0xFFu);
+#pragma unroll
+        for (int j = 0; j < QG; ++j) acc[j] = acc[j] + tl[j * tsz + off];
+      }
+    }
+    const int64_t i = v - v0;
+#pragma unroll
+    for (int j = 0; j < QG; ++j)
+      if (j < npair) a.cand[obase[j] + i] = vsk_key(acc[j], (uint32_t)(tbase[j] + i));
+  }
+}
 
 // one workgroup per group: up to QG queries probing the same list
 template <int QG>
@@ -171,14 +271,19 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
 __global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
                              const int32_t *probes, int32_t np,
                              const int64_t *pos_base, const int64_t *list_off,
-                             const int64_t *ids, float *out_dist,
-                             int64_t *out_ids) {
+                             const int64_t *ids, void *out_dist,
+                             int64_t *out_ids, int32_t kind) {
   int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= nq * k) return;
   const int64_t q = i / k;
   const uint64_t key = best[i];
+  float *of = static_cast<float *>(out_dist);
+  int32_t *os = static_cast<int32_t *>(out_dist);
   if (key == VSK_KEY_NONE) {
-    out_dist[i] = __int_as_float(0x7f800000);
+    if (kind == 1)
+      os[i] = INT32_MIN;
+    else
+      of[i] = __int_as_float(0x7f800000);
     out_ids[i] = -1;
     return;
   }
@@ -188,7 +293,13 @@ __global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
   while (p > 0 && (pb[p] > pos || probes[q * np + p] < 0)) --p;
   const int32_t l = probes[q * np + p];
   const int64_t row = list_off[l] + (pos - pb[p]);
-  out_dist[i] = vsk_ord2f((uint32_t)(key >> 32));
+  const uint32_t hi = (uint32_t)(key >> 32);
+  if (kind == 1)
+    os[i] = -(int32_t)(hi ^ 0x80000000u);  // the score
+  else if (kind == 2)
+    of[i] = sqrtf(vsk_ord2f(hi));  // ADC sum -> its square root
+  else
+    of[i] = vsk_ord2f(hi);
   out_ids[i] = ids[row];
 }
 
@@ -456,15 +567,35 @@ vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
-                          int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
-                          float *out_dist, int64_t *out_ids) {
+}  // extern "C"
+
+// kind 0: the rows (metric L2 / L2SQ); 1: SQ8 codes, qextra = nq x d int8
+// query codes; 2: PQ codes, qextra = the vsk_pq whose tables score them
+static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                                 const void *qextra, int64_t nq, int32_t nprobe, int32_t k,
+                                 int32_t metric, int32_t kind, void *out_dist,
+                                 int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
-  VSK_REQUIRE(metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ,
-              VSK_ERR_UNSUPPORTED,
-              "IVF search ranks by euclidean distance (VSK_METRIC_L2 or "
-              "VSK_METRIC_L2SQ)");
+  if (kind == 0)
+    VSK_REQUIRE(metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ,
+                VSK_ERR_UNSUPPORTED,
+                "IVF search ranks by euclidean distance (VSK_METRIC_L2 or "
+                "VSK_METRIC_L2SQ)");
+  if (kind != 0) {
+    VSK_REQUIRE(ivf->ckind == kind, VSK_ERR_NOT_TRAINED,
+                kind == 1 ? "the index holds no SQ8 codes (vsk_ivf_encode_sq8)"
+                          : "the index holds no PQ codes (vsk_ivf_encode_pq)");
+    VSK_REQUIRE(ivf->ctotal == ivf->total, VSK_ERR_NOT_TRAINED,
+                "rows were added after the codes were made: encode again");
+    VSK_REQUIRE(qextra, VSK_ERR_INVALID_ARGUMENT,
+                kind == 1 ? "query codes are null" : "pq is null");
+  }
+  if (kind == 2) {
+    const vsk_pq *pq = static_cast<const vsk_pq *>(qextra);
+    VSK_REQUIRE(pq_shape_matches(pq, ivf->d, ivf->cM, ivf->cksub), VSK_ERR_DIMENSION_MISMATCH,
+                "pq does not match the codebook the codes were made with");
+  }
   VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
   VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT,
               "null buffer");
@@ -475,9 +606,28 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
   const int32_t np = nprobe < ivf->nlist ? nprobe : ivf->nlist;  // .exact
   VSK_REQUIRE(np <= VSK_MAX_K || np == ivf->nlist, VSK_ERR_INVALID_ARGUMENT,
               "nprobe must be <= VSK_MAX_K or cover every list");
+  float *dlut = nullptr;
+  if (kind == 2) {
+    // the tables first: that call syncs the stream itself
+    dlut = static_cast<float *>(ctx->scratch_ptr(
+        "ivf.lut", sizeof(float) * (size_t)nq * ivf->cM * ivf->cksub));
+    const vsk_status st = vsk_pq_lut(ctx, static_cast<const vsk_pq *>(qextra), q, nq, dlut);
+    if (st != VSK_OK) return st;
+  }
   CallScope cs(ctx);
   const int32_t ld = ivf->ld;
   const float *dq = rows_to_device_padded(ctx, q, nq, ivf->d, ld, "ivf.q");
+  int8_t *dqc = nullptr;
+  if (kind == 1) {
+    // query codes at the code stride, zero padded
+    const int8_t *src = static_cast<const int8_t *>(
+        input_to_device(ctx, qextra, (size_t)nq * ivf->d, "ivf.qc_in"));
+    dqc = static_cast<int8_t *>(
+        ctx->scratch_ptr("ivf.qc", (size_t)nq * ivf->cstride));
+    fill_i32(ctx, reinterpret_cast<int32_t *>(dqc), nq * (ivf->cstride / 4), 0);
+    VSK_HIP(hipMemcpy2DAsync(dqc, ivf->cstride, src, ivf->d, ivf->d, nq,
+                             hipMemcpyDeviceToDevice, ctx->stream));
+  }
   OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
 
@@ -516,9 +666,17 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                          hipMemcpyDeviceToHost, ctx->stream));
   VSK_HIP(hipStreamSynchronize(ctx->stream));
 
-  const int QG = ld <= 512 ? 16 : (ld <= 1024 ? 8 : 1);
-  VSK_REQUIRE((int64_t)QG * ld * 4 <= 64 * 1024, VSK_ERR_UNSUPPORTED,
-              "dimension too large for the IVF list scan");
+  // queries per group: their rows, codes or tables fit 64 KiB of LDS
+  const int64_t per_q = kind == 0 ? (int64_t)ld * 4
+                        : kind == 1 ? (int64_t)ivf->cstride
+                                    : (int64_t)ivf->cM * ivf->cksub * 4;
+  const int QG = per_q * 16 <= 64 * 1024 ? 16
+                 : per_q * 8 <= 64 * 1024 ? 8
+                 : per_q * 4 <= 64 * 1024 ? 4
+                                           : 1;
+  VSK_REQUIRE(per_q * QG <= 64 * 1024, VSK_ERR_UNSUPPORTED,
+              kind == 2 ? "PQ tables too large for the IVF list scan (M x ksub > 16384)"
+                        : "dimension too large for the IVF list scan");
   int64_t max_cnt = 0;
   for (auto c : h_cnt) max_cnt = std::max(max_cnt, c);
   const int64_t budget = std::max<int64_t>(1ll << 27, max_cnt);
@@ -587,15 +745,30 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
       la.seg_off = dseg;
       la.cand = cand;
       la.squared = metric == VSK_METRIC_L2SQ ? 1 : 0;
-      const size_t lds = sizeof(float) * QG * ld;
-      KernelTimer t(ctx, "ivf_list_scan", (double)tot);
-      if (QG == 16)
-        k_list_scan<16><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
-      else if (QG == 8)
-        k_list_scan<8><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
-      else
-        k_list_scan<1><<<(unsigned)groups.size(), 256, lds, ctx->stream>>>(la);
-      check_launch("ivf_list_scan");
+      la.codes = ivf->codes.as<uint8_t>();
+      la.cstride = ivf->cstride;
+      la.qc = dqc ? dqc + b0 * ivf->cstride : nullptr;
+      la.lut = dlut ? dlut + b0 * ivf->cM * ivf->cksub : nullptr;
+      la.M = ivf->cM;
+      la.ksub = ivf->cksub;
+      const size_t lds = (size_t)(per_q * QG);
+      const unsigned ng = (unsigned)groups.size();
+      static const char *names[3] = {"ivf_list_scan", "ivf_sq8_list_scan", "ivf_pq_list_scan"};
+      KernelTimer t(ctx, names[kind], (double)tot);
+#define VSK_SCAN_QG(K)                                                  \
+  if (QG == 16) K<16><<<ng, 256, lds, ctx->stream>>>(la);              \
+  else if (QG == 8) K<8><<<ng, 256, lds, ctx->stream>>>(la);           \
+  else if (QG == 4) K<4><<<ng, 256, lds, ctx->stream>>>(la);           \
+  else K<1><<<ng, 256, lds, ctx->stream>>>(la);
+      if (kind == 0) {
+        VSK_SCAN_QG(k_list_scan)
+      } else if (kind == 1) {
+        VSK_SCAN_QG(k_list_scan_sq8)
+      } else {
+        VSK_SCAN_QG(k_list_scan_pq)
+      }
+#undef VSK_SCAN_QG
+      check_launch(names[kind]);
     }
     // 4. selection per query segment
     SelectArgs sa;
@@ -612,12 +785,95 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
     KernelTimer t(ctx, "ivf_decode");
     k_ivf_decode<<<grid1(nq * k), 256, 0, ctx->stream>>>(
         best, nq, k, probes, np, pos_base, ivf->list_off.as<int64_t>(),
-        ivf->ids.as<int64_t>(), od.ptr<float>(), oi.ptr<int64_t>());
+        ivf->ids.as<int64_t>(), od.ptr<float>(), oi.ptr<int64_t>(), kind);
     check_launch("ivf_decode");
   }
   od.copy_back();
   oi.copy_back();
   cs.finish();
+  VSK_API_END(ctx);
+}
+
+// the rows of the index, contiguous (total x d fp32), into dst
+static void ivf_rows_dense(vsk_ctx *ctx, const vsk_ivf *ivf, float *dst) {
+  VSK_HIP(hipMemcpy2DAsync(dst, sizeof(float) * ivf->d, ivf->rows.p, sizeof(float) * ivf->ld,
+                           sizeof(float) * ivf->d, ivf->total, hipMemcpyDeviceToDevice,
+                           ctx->stream));
+}
+
+// codes (total x w bytes, dense) -> the index's code store at stride
+// round_up(w, align), zero padded
+static void ivf_store_codes(vsk_ctx *ctx, vsk_ivf *ivf, const void *dense, int32_t w,
+                            int32_t align, int32_t kind) {
+  const int32_t stride = (w + align - 1) / align * align;
+  auto buf = std::make_unique<DevBuf>();
+  buf->reserve((size_t)ivf->total * stride + 16);
+  fill_i32(ctx, buf->as<int32_t>(), ((int64_t)ivf->total * stride + 16) / 4, 0);
+  VSK_HIP(hipMemcpy2DAsync(buf->p, stride, dense, w, w, ivf->total, hipMemcpyDeviceToDevice,
+                           ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  std::swap(ivf->codes.p, buf->p);
+  std::swap(ivf->codes.bytes, buf->bytes);
+  ivf->ckind = kind;
+  ivf->cstride = stride;
+  ivf->ctotal = ivf->total;
+}
+
+extern "C" {
+
+vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                          int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
+                          float *out_dist, int64_t *out_ids) {
+  return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids);
+}
+
+vsk_status vsk_ivf_search_sq8(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                              const int8_t *qcodes, int64_t nq, int32_t nprobe, int32_t k,
+                              int32_t *out_score, int64_t *out_ids) {
+  return ivf_search_any(ctx, ivf, q, qcodes, nq, nprobe, k, -1, 1, out_score, out_ids);
+}
+
+vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
+                             const float *q, int64_t nq, int32_t nprobe, int32_t k,
+                             float *out_dist, int64_t *out_ids) {
+  return ivf_search_any(ctx, ivf, q, pq, nq, nprobe, k, -1, 2, out_dist, out_ids);
+}
+
+vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,
+                              const float *scale, const float *offset) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(ivf->total > 0, VSK_ERR_EMPTY_INPUT, "the index holds no rows");
+  VSK_REQUIRE(scale && offset, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  DevBuf dense, codes;
+  dense.reserve(sizeof(float) * (size_t)ivf->total * ivf->d);
+  codes.reserve((size_t)ivf->total * ivf->d);
+  ivf_rows_dense(ctx, ivf, dense.as<float>());
+  const vsk_status st = vsk_sq8_encode(ctx, dense.as<float>(), ivf->total, ivf->d, per_dim,
+                                       scale, offset, codes.as<int8_t>());
+  if (st != VSK_OK) return st;
+  ivf_store_codes(ctx, ivf, codes.p, ivf->d, 16, 1);
+  ivf->cM = ivf->cksub = 0;
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(ivf->total > 0, VSK_ERR_EMPTY_INPUT, "the index holds no rows");
+  VSK_REQUIRE(pq, VSK_ERR_INVALID_ARGUMENT, "pq is null");
+  int32_t M = 0, ksub = 0;
+  VSK_REQUIRE(pq_shape(pq, &M, &ksub) == ivf->d, VSK_ERR_DIMENSION_MISMATCH,
+              "pq dimension differs from the index's");
+  DevBuf dense, codes;
+  dense.reserve(sizeof(float) * (size_t)ivf->total * ivf->d);
+  codes.reserve((size_t)ivf->total * M);
+  ivf_rows_dense(ctx, ivf, dense.as<float>());
+  const vsk_status st = vsk_pq_encode(ctx, pq, dense.as<float>(), ivf->total, codes.as<uint8_t>());
+  if (st != VSK_OK) return st;
+  ivf_store_codes(ctx, ivf, codes.p, M, 4, 2);
+  ivf->cM = M;
+  ivf->cksub = ksub;
   VSK_API_END(ctx);
 }
 

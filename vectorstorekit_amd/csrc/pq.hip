@@ -977,3 +977,17 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
 }
 
 }  // extern "C"
+
+namespace vsk {
+
+int32_t pq_shape(const vsk_pq *pq, int32_t *M, int32_t *ksub) {
+  *M = pq->M;
+  *ksub = pq->ksub;
+  return pq->d;
+}
+
+bool pq_shape_matches(const vsk_pq *pq, int32_t d, int32_t M, int32_t ksub) {
+  return pq && pq->d == d && pq->M == M && pq->ksub == ksub;
+}
+
+}  // namespace vsk

@@ -48,6 +48,8 @@ class IVFIndex:
         self.configuration = configuration
         self.handle = None
         self._centroids = None
+        self._sq8 = None  # the quantizers the stored codes were made with
+        self._pq = None
 
     @property
     def trained(self) -> bool:
@@ -148,6 +150,68 @@ class IVFIndex:
         ip, ids = out_buffer((nq, k), np.int64, q)
         self.ctx.check(self.ctx.lib.vsk_ivf_search(self.ctx.handle, self.handle, qp, nq,
                                                    nprobe, k, metric_code(metric), dp, ip))
+        return dist, ids
+
+    # ---- quantized lists (IVFConfiguration's declared quantization,
+    # Config/Indexes/IVFConfiguration.swift:13,18-21, which IVFIndex leaves
+    # unimplemented): codes of the stored rows, scored per probed list
+    def encodeSQ8(self, quantizer):
+        """Codes of every stored row with a trained ``ScalarQuantizer``;
+        rows inserted later need another call before ``searchSQ8``."""
+        self._need()
+        quantizer._need()
+        self.ctx.check(self.ctx.lib.vsk_ivf_encode_sq8(
+            self.ctx.handle, self.handle, 1 if quantizer.per_dim else 0,
+            quantizer.scale.ctypes.data, quantizer.offset.ctypes.data))
+        self._sq8, self._pq = quantizer, None
+
+    def encodePQ(self, pq):
+        """PQ codes of every stored row with a trained ``ProductQuantizer``."""
+        self._need()
+        self.ctx.check(self.ctx.lib.vsk_ivf_encode_pq(self.ctx.handle, self.handle, pq.handle))
+        self._sq8, self._pq = None, pq
+
+    def _queries(self, queries):
+        q = queries
+        if not hasattr(q, "shape") or len(q.shape) == 1:
+            q = np.asarray(q, np.float32).reshape(1, -1)
+        return q, int(q.shape[0])
+
+    def searchSQ8(self, queries, k: int, nprobe=None, strategy: str = "approximate"):
+        """(scores [nq, k] int32 descending, ids): the int8 dot score of the
+        query's codes with the probed lists' codes."""
+        self._need()
+        if strategy == "exact":
+            nprobe = self.configuration.numberOfCentroids
+        nprobe = nprobe or self.configuration.numberOfProbes
+        if self._sq8 is None:
+            raise VSKError(-7, "the index holds no SQ8 codes (encodeSQ8)")
+        q, nq = self._queries(queries)
+        qc = self._sq8.quantizeBatch(q)
+        qp, qk = as_buffer(q, np.float32, (nq, self.configuration.dimensions))
+        cp, ck = as_buffer(qc, np.int8, (nq, self.configuration.dimensions))
+        sp, score = out_buffer((nq, k), np.int32, q)
+        ip, ids = out_buffer((nq, k), np.int64, q)
+        self.ctx.check(self.ctx.lib.vsk_ivf_search_sq8(self.ctx.handle, self.handle, qp, cp,
+                                                       nq, nprobe, k, sp, ip))
+        return score, ids
+
+    def searchPQ(self, queries, k: int, nprobe=None, strategy: str = "approximate"):
+        """(sqrt of the ADC sum [nq, k] ascending, ids) over the probed
+        lists' PQ codes."""
+        self._need()
+        if strategy == "exact":
+            nprobe = self.configuration.numberOfCentroids
+        nprobe = nprobe or self.configuration.numberOfProbes
+        if self._pq is None:
+            raise VSKError(-7, "the index holds no PQ codes (encodePQ)")
+        q, nq = self._queries(queries)
+        qp, qk = as_buffer(q, np.float32, (nq, self.configuration.dimensions))
+        dp, dist = out_buffer((nq, k), np.float32, q)
+        ip, ids = out_buffer((nq, k), np.int64, q)
+        self.ctx.check(self.ctx.lib.vsk_ivf_search_pq(self.ctx.handle, self.handle,
+                                                      self._pq.handle, qp, nq, nprobe, k,
+                                                      dp, ip))
         return dist, ids
 
     def list_sizes(self) -> np.ndarray:
