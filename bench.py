@@ -50,7 +50,7 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
 PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
-                 "c3train": (2, 1), "c4bin": (5, 1)}
+                 "c3train": (2, 1), "c4bin": (5, 1), "c3sq8": (5, 1), "c3pq": (5, 1)}
 
 
 def parse():
@@ -379,6 +379,81 @@ def setup(a, ctx, dev):
         }
         return spec, step, cpu_leg
 
+    if c in ("c3sq8", "c3pq"):
+        # config 3's index with quantized lists: the same probing, the
+        # probed lists scanned over SQ8 (per-dimension) or PQ M16x256 codes
+        n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
+        x, q, cent = gen_mixture(n, d, ncent, nq, dev)
+        idx = IVFIndex(ctx, IVFConfiguration(dimensions=d, numberOfCentroids=ncent,
+                                             numberOfProbes=nprobe))
+        idx.set_centroids(cent.cpu().numpy())
+        idx.insert(x)
+        ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
+        M = 16
+        if c == "c3sq8":
+            sq = ScalarQuantizer(ctx, per_dim=True)
+            sq.train(x)
+            idx.encodeSQ8(sq)
+            qc = sq.quantizeBatch(q)
+            score = torch.empty(nq, k, dtype=torch.int32, device=dev)
+
+            def step():
+                ctx.check(lib.vsk_ivf_search_sq8(ctx.handle, idx.handle, q.data_ptr(),
+                                                 qc.data_ptr(), nq, nprobe, k,
+                                                 score.data_ptr(), ids.data_ptr()))
+        else:
+            g = torch.Generator(device="cpu").manual_seed(6)
+            pick = torch.randperm(n, generator=g)[:256].to(dev)
+            cb = x[pick].reshape(256, M, d // M).permute(1, 0, 2).contiguous().cpu().numpy()
+            pq = ProductQuantizer(ctx, cb)
+            idx.encodePQ(pq)
+            dist = torch.empty(nq, k, device=dev)
+
+            def step():
+                ctx.check(lib.vsk_ivf_search_pq(ctx.handle, idx.handle, pq.handle,
+                                                q.data_ptr(), nq, nprobe, k, dist.data_ptr(),
+                                                ids.data_ptr()))
+
+        def cpu_leg(target_s):
+            from oracle import oracle as O
+            xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), idx.getCentroids()
+            lists = idx.assign(x).cpu().numpy()
+            rid = np.arange(n, dtype=np.int64)
+            if c == "c3sq8":
+                codes = O.sq8_encode(xh, sq.scale, sq.offset)
+                qch = qc.cpu().numpy()
+                run = lambda m: O.ivf_sq8_search(qh[:m], qch[:m], codes, rid, lists, ch,
+                                                 nprobe, k)
+            else:
+                codes = O.pq_encode(xh, cb, threads=host_threads())
+                run = lambda m: O.ivf_pq_search(qh[:m], cb, codes, rid, lists, ch, nprobe, k)
+            qps, m, reps, el, (od, oi) = cpu_sample(run, nq, target_s, 1)
+            return ({"value": qps, "unit": "queries/s", "cores": 1, "kind": "port",
+                     "sample": f"first {m} of {nq} queries, probe + scan of 32 lists' codes "
+                               f"(numpy over the oracle's probe; codes encoded outside the "
+                               f"timing), {reps} pass(es) ({el:.1f} s)"},
+                    id_agreement(ids.cpu().numpy()[:m], oi))
+
+        sq8 = c == "c3sq8"
+        spec = {
+            "metric": ("QPS @k=10, IVF-SQ8 (per-dim int8) 1M x 128, nlist 4096, nprobe 32" if sq8
+                       else "QPS @k=10, IVF-PQ M16x256 1M x 128, nlist 4096, nprobe 32"),
+            "workload": (f"ivf-{'sq8' if sq8 else 'pq16'}-1Mx128-nlist4096-nprobe32-q10000-k10 "
+                         "(BASELINE config 3's index, quantized lists)"),
+            "config": {"n": n, "d": d, "nlist": ncent, "nprobe": nprobe, "nq": nq, "k": k,
+                       "metric": ("score sum qcode*code (descending)" if sq8 else
+                                  "sqrt of the ADC sum of LUT[m][code_m]")},
+            "data": "synthetic: config 3's mixture (as c3)"
+                    + ("" if sq8 else "; codebooks: 256 random rows (seed 6) split in 16 "
+                                      "segments"),
+            "dtype": "i8 codes, i32 scores" if sq8 else "u8 codes, f32 LUT",
+            "nq": nq, "n": n, "d": d, "M": M,
+            "kernels": [("ivf_sq8_list_scan", "k_list_scan_sq8<16>", "valu_dot4")] if sq8
+                       else [("ivf_pq_list_scan", "k_list_scan_pq_q (one workgroup per query)", "lds_pq")],
+            "keep": (idx, x, q, ids, sq if sq8 else pq),
+        }
+        return spec, step, cpu_leg
+
     if c == "c4":
         n, d, nq, k = 10_000_000, 128, 1000, 100
         x, q = gen_flat(n, d, nq, False, dev)
@@ -555,6 +630,16 @@ def roofline(spec, stats):
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
                   "algorithmic": "4*d bytes per (query, probed row) pair: every probed "
                                  "list row read once per query"})
+    elif kind == "valu_dot4":
+        # v_dot4_i32_i8: four int8 products and their sum per lane per op
+        ops = 2.0 * d * pairs
+        ach = ops / sec / 1e12
+        peak = PEAK_FP32_VALU_ISSUE_TOPS * 8
+        r.update({"bound": "valu", "achieved": round(ach, 2), "peak": round(peak, 1),
+                  "unit": "TOP/s", "frac": round(ach / peak, 4),
+                  "algorithmic": "2*d int8 OP per (query, row) pair",
+                  "peak_basis": "v_dot4_i32_i8 at one op per lane-cycle: 8 OP x "
+                                f"{PEAK_FP32_VALU_ISSUE_TOPS} T lane-cycles/s"})
     elif kind == "lds_pq":
         # the tables are read from LDS, one 4-byte lookup per (query, code
         # byte); the code stream itself is shared by the 8 queries of a

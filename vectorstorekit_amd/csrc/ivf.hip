@@ -175,42 +175,6 @@ __global__ __launch_bounds__(256) void k_list_scan_sq8(ListScanArgs a) {
   }
 }
 
-// IVF-PQ list scan: ADC sum = sum over segments m, in order, of
-// lut[q][m][code_m] (fp32, each addition rounded: DistanceTables.
-// computeDistance, Quantization/ProductQuantizerTypes.swift:14-20).  The
-// group's tables in LDS, one row per thread, 4-byte code loads.
-template <int QG>
-__global__ __launch_bounds__(256) void k_list_scan_pq(ListScanArgs a) {
-#pragma clang fp contract(off)
-  extern __shared__ float tl[];  // QG x M x ksub
-  VSK_GROUP_SLOTS(QG)
-  const int tsz = a.M * a.ksub;
-  for (int i = threadIdx.x; i < QG * tsz; i += blockDim.x) {
-    const int j = i / tsz, c = i - j * tsz;
-    tl[i] = a.lut[(int64_t)qidx[j] * tsz + c];
-  }
-  __syncthreads();
-  for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
-    const uint32_t *x = reinterpret_cast<const uint32_t *>(a.codes + v * a.cstride);
-    float acc[QG];
-#pragma unroll
-    for (int j = 0; j < QG; ++j) acc[j] = 0.f;
-    for (int m0 = 0; m0 < a.M; m0 += 4) {
-      const uint32_t w = x[m0 >> 2];
-      const int mm = a.M - m0 < 4 ? a.M - m0 : 4;
-      for (int t = 0; t < mm; ++t) {
-        const int off = (m0 + t) * a.ksub + (int)((w >> (8 * t)) & 0xFFu);
-#pragma unroll
-        for (int j = 0; j < QG; ++j) acc[j] = acc[j] + tl[j * tsz + off];
-      }
-    }
-    const int64_t i = v - v0;
-#pragma unroll
-    for (int j = 0; j < QG; ++j)
-      if (j < npair) a.cand[obase[j] + i] = vsk_key(acc[j], (uint32_t)(tbase[j] + i));
-  }
-}
-
 // one workgroup per group: up to QG queries probing the same list
 template <int QG>
 __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
@@ -265,6 +229,39 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
                                        (uint32_t)(tbase[j] + i));
   }
   (void)qidx;
+}
+
+// IVF-PQ list scan: ADC sum = sum over segments m, in order, of
+// lut[q][m][code_m] (fp32, each addition rounded: DistanceTables.
+// computeDistance, Quantization/ProductQuantizerTypes.swift:14-20), keyed
+// (sum, position).  One workgroup per query: its tables stay in LDS while it
+// walks its probed lists (a table is 4 M ksub bytes, a probed list's codes
+// a few KB, so keeping the table and streaming the codes moves the least).
+__global__ __launch_bounds__(256) void k_list_scan_pq_q(ListScanArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float tl[];  // M x ksub
+  const int64_t q = blockIdx.x;
+  const int tsz = a.M * a.ksub;
+  for (int i = threadIdx.x; i < tsz; i += blockDim.x) tl[i] = a.lut[q * tsz + i];
+  __syncthreads();
+  const int64_t seg = a.seg_off[q];
+  for (int p = 0; p < a.np; ++p) {
+    const int32_t l = a.probes[q * a.np + p];
+    if (l < 0) continue;
+    const int64_t v0 = a.list_off[l], v1 = a.list_off[l + 1];
+    const int64_t tb = a.pos_base[q * a.np + p];
+    for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+      const uint32_t *x = reinterpret_cast<const uint32_t *>(a.codes + v * a.cstride);
+      float acc = 0.f;
+      for (int m0 = 0; m0 < a.M; m0 += 4) {
+        const uint32_t w = x[m0 >> 2];
+        const int mm = a.M - m0 < 4 ? a.M - m0 : 4;
+        for (int t = 0; t < mm; ++t)
+          acc = acc + tl[(m0 + t) * a.ksub + (int)((w >> (8 * t)) & 0xFFu)];
+      }
+      a.cand[seg + tb + (v - v0)] = vsk_key(acc, (uint32_t)(tb + (v - v0)));
+    }
+  }
 }
 
 // best keys (dist, position) -> (dist, user id)
@@ -765,7 +762,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       } else if (kind == 1) {
         VSK_SCAN_QG(k_list_scan_sq8)
       } else {
-        VSK_SCAN_QG(k_list_scan_pq)
+        k_list_scan_pq_q<<<(unsigned)nb, 256, (size_t)per_q, ctx->stream>>>(la);
       }
 #undef VSK_SCAN_QG
       check_launch(names[kind]);
