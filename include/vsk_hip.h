@@ -53,6 +53,7 @@ typedef int32_t vsk_status;
 #define VSK_ERR_NOT_TRAINED (-7)          /* IVFError/QuantizationError.notTrained */
 #define VSK_ERR_UNSUPPORTED (-8)          /* .unsupportedOperation            */
 #define VSK_ERR_INVALID_BUFFER_SIZE (-9)  /* .invalidBufferSize (k or size over a limit) */
+#define VSK_ERR_IO (-10)                  /* index file unreadable, unwritable or malformed */
 
 /* Distance metrics: DistanceMetric raw values "euclidean", "cosine",
  * "dotProduct", "manhattan", "hamming" (Core/SearchTypes.swift:105-112; the
@@ -221,6 +222,23 @@ vsk_status vsk_ivf_search_sq8(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
 vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
                              const float *q, int64_t nq, int32_t nprobe, int32_t k,
                              float *out_dist, int64_t *out_ids);
+
+/* ---- IVF index file ----------------------------------------------------------
+ * IVFIndex persistence keeps only the centroids and counts
+ * (Indexes/IVFIndex.swift:297-328: the lists are dropped).  This file holds
+ * the whole index, little-endian:
+ *   "VSKIVF01"; int32 nlist, d; int64 total, next_id;
+ *   int32 code_kind, code_stride, pq_M, pq_ksub (code_kind 0 = none);
+ *   float centroids[nlist][d]; int64 list_off[nlist + 1]; int64 ids[total];
+ *   float rows[total][d] (list order); uint8 codes[total][code_stride];
+ *   uint64 FNV-1a of every byte before it.
+ * Stale codes (rows added after the last encode) are not written.  Loading
+ * checks the magic, the sizes, the offsets and the checksum (VSK_ERR_IO). */
+vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path);
+vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out);
+/* nlist, d, total rows and code kind (0 none, 1 SQ8, 2 PQ) of an index */
+vsk_status vsk_ivf_info(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *nlist, int32_t *d,
+                        int64_t *total, int32_t *code_kind);
 
 
 /* ---- int8 scalar quantization ---------------------------------------------

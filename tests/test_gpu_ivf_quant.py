@@ -106,3 +106,62 @@ def test_ivf_codes_follow_inserts(ctx):
     np.testing.assert_array_equal(ids, ei)
     with pytest.raises(VSKError):
         idx.searchPQ(q, 5)  # the index holds SQ8 codes
+
+
+def test_ivf_index_file_round_trip(ctx, tmp_path):
+    x, q, c = _mixture(21, 32, 6000, 40, 25)
+    idx = _index(ctx, c, x[:5000], 6)
+    idx.insert(x[5000:], ids=np.arange(5000, 6000, dtype=np.int64) * 7)
+    sq = ScalarQuantizer(ctx)
+    sq.train(x)
+    idx.encodeSQ8(sq)
+    path = str(tmp_path / "ivf.vsk")
+    idx.save(path)
+    back = IVFIndex.load(ctx, path, numberOfProbes=6, sq8=sq)
+    np.testing.assert_array_equal(back.getCentroids(), c)
+    np.testing.assert_array_equal(back.list_sizes(), idx.list_sizes())
+    for a, b in zip(idx.search(q, 9), back.search(q, 9)):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(idx.searchSQ8(q, 9), back.searchSQ8(q, 9)):
+        np.testing.assert_array_equal(a, b)
+    # later inserts take the next ids in both
+    idx.insert(x[:10])
+    back.insert(x[:10])
+    for a, b in zip(idx.search(q, 9), back.search(q, 9)):
+        np.testing.assert_array_equal(a, b)
+    # stale codes are not written
+    idx.save(path)
+    with pytest.raises(VSKError):
+        IVFIndex.load(ctx, path, sq8=sq).searchSQ8(q, 3)
+
+
+def test_ivf_index_file_pq_round_trip(ctx, tmp_path):
+    x, q, c = _mixture(22, 16, 3000, 32, 20)
+    rng = np.random.default_rng(1)
+    cb = x[rng.choice(3000, 256, replace=False)].reshape(256, 8, 4).transpose(1, 0, 2).copy()
+    idx = _index(ctx, c, x, 4)
+    pq = ProductQuantizer(ctx, cb)
+    idx.encodePQ(pq)
+    path = str(tmp_path / "ivfpq.vsk")
+    idx.save(path)
+    back = IVFIndex.load(ctx, path, numberOfProbes=4, pq=pq)
+    for a, b in zip(idx.searchPQ(q, 11), back.searchPQ(q, 11)):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_ivf_index_file_damage(ctx, tmp_path):
+    x, q, c = _mixture(23, 8, 800, 16, 5)
+    idx = _index(ctx, c, x, 2)
+    path = tmp_path / "ivf.vsk"
+    idx.save(str(path))
+    raw = path.read_bytes()
+    cases = {"flipped": raw[:3000] + bytes([raw[3000] ^ 1]) + raw[3001:],
+             "truncated": raw[:-9], "magic": b"VSKIVF02" + raw[8:], "longer": raw + b"\0"}
+    for name, blob in cases.items():
+        bad = tmp_path / f"{name}.vsk"
+        bad.write_bytes(blob)
+        with pytest.raises(VSKError) as e:
+            IVFIndex.load(ctx, str(bad))
+        assert e.value.status == -10, name
+    with pytest.raises(VSKError):
+        IVFIndex.load(ctx, str(tmp_path / "missing.vsk"))

@@ -27,6 +27,7 @@ STATUS_NAMES = {
     -7: "notTrained",
     -8: "unsupportedOperation",
     -9: "invalidBufferSize",
+    -10: "persistenceFailed",
 }
 
 # metric codes (vsk_hip.h)
@@ -103,6 +104,9 @@ SIGNATURES = {
     "vsk_ivf_list_sizes": (c_int32, [P, P, P]),
     "vsk_ivf_encode_sq8": (c_int32, [P, P, c_int32, P, P]),
     "vsk_ivf_encode_pq": (c_int32, [P, P, P]),
+    "vsk_ivf_save": (c_int32, [P, P, ctypes.c_char_p]),
+    "vsk_ivf_load": (c_int32, [P, ctypes.c_char_p, PP]),
+    "vsk_ivf_info": (c_int32, [P, P, P, P, P]),
     "vsk_ivf_search_sq8": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_ivf_search_pq": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_train": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P]),

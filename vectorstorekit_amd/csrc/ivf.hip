@@ -26,6 +26,9 @@
 //  4. per-query selection over the segment -> k smallest (distance,
 //     position), i.e. the stable-sort prefix; positions map back to ids.
 #include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <memory>
 #include <numeric>
 
 #include "flat.hpp"
@@ -871,6 +874,198 @@ vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq) {
   ivf_store_codes(ctx, ivf, codes.p, M, 4, 2);
   ivf->cM = M;
   ivf->cksub = ksub;
+  VSK_API_END(ctx);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// index file (layout in the header's comment on vsk_ivf_save)
+// ---------------------------------------------------------------------------
+namespace vsk {
+namespace {
+
+constexpr char kIvfMagic[8] = {'V', 'S', 'K', 'I', 'V', 'F', '0', '1'};
+constexpr size_t kIoChunk = 64u << 20;  // host staging per transfer
+
+struct Fnv1a {
+  uint64_t h = 0xcbf29ce484222325ull;
+  void add(const void *p, size_t n) {
+    const uint8_t *b = static_cast<const uint8_t *>(p);
+    for (size_t i = 0; i < n; ++i) {
+      h ^= b[i];
+      h *= 0x100000001b3ull;
+    }
+  }
+};
+
+struct FileCloser {
+  void operator()(FILE *f) const { fclose(f); }
+};
+using File = std::unique_ptr<FILE, FileCloser>;
+
+void put(FILE *f, Fnv1a &h, const void *p, size_t n) {
+  if (n && fwrite(p, 1, n, f) != n) fail(VSK_ERR_IO, "index file: write failed");
+  h.add(p, n);
+}
+
+void get(FILE *f, Fnv1a &h, void *p, size_t n) {
+  if (n && fread(p, 1, n, f) != n) fail(VSK_ERR_IO, "index file: truncated");
+  h.add(p, n);
+}
+
+// rows x w bytes at a device pitch -> file, through host chunks
+void put_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, const void *dev, int64_t rows, size_t pitch,
+              size_t w) {
+  if (rows == 0) return;
+  const int64_t per = std::max<int64_t>(1, (int64_t)(kIoChunk / w));
+  std::vector<uint8_t> buf((size_t)std::min(per, rows) * w);
+  for (int64_t r = 0; r < rows; r += per) {
+    const int64_t cnt = std::min(per, rows - r);
+    VSK_HIP(hipMemcpy2DAsync(buf.data(), w, static_cast<const uint8_t *>(dev) + r * pitch,
+                             pitch, w, cnt, hipMemcpyDeviceToHost, ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    put(f, h, buf.data(), (size_t)cnt * w);
+  }
+}
+
+// file -> rows x w bytes at a device pitch
+void get_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, void *dev, int64_t rows, size_t pitch,
+              size_t w) {
+  if (rows == 0) return;
+  const int64_t per = std::max<int64_t>(1, (int64_t)(kIoChunk / w));
+  std::vector<uint8_t> buf((size_t)std::min(per, rows) * w);
+  for (int64_t r = 0; r < rows; r += per) {
+    const int64_t cnt = std::min(per, rows - r);
+    get(f, h, buf.data(), (size_t)cnt * w);
+    VSK_HIP(hipMemcpy2DAsync(static_cast<uint8_t *>(dev) + r * pitch, pitch, buf.data(), w, w,
+                             cnt, hipMemcpyHostToDevice, ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+  }
+}
+
+struct IvfDeleter {
+  vsk_ctx *ctx;
+  void operator()(vsk_ivf *p) const { vsk_ivf_free(ctx, p); }
+};
+
+}  // namespace
+}  // namespace vsk
+
+extern "C" {
+
+vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(path, VSK_ERR_INVALID_ARGUMENT, "path is null");
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  File f(fopen(path, "wb"));
+  VSK_REQUIRE(f, VSK_ERR_IO, std::string("cannot open for writing: ") + path);
+  Fnv1a h;
+  const bool coded = ivf->ckind != 0 && ivf->ctotal == ivf->total;
+  const int32_t hdr32[6] = {ivf->nlist, ivf->d, coded ? ivf->ckind : 0,
+                            coded ? ivf->cstride : 0, coded ? ivf->cM : 0,
+                            coded ? ivf->cksub : 0};
+  const int64_t hdr64[2] = {ivf->total, ivf->next_id};
+  put(f.get(), h, kIvfMagic, 8);
+  put(f.get(), h, &hdr32[0], 8);
+  put(f.get(), h, hdr64, 16);
+  put(f.get(), h, &hdr32[2], 16);
+  const size_t ldb = sizeof(float) * ivf->ld, db = sizeof(float) * ivf->d;
+  put_rows(ctx, f.get(), h, ivf->centroids.x.p, ivf->nlist, ldb, db);
+  put(f.get(), h, ivf->off.data(), sizeof(int64_t) * (ivf->nlist + 1));
+  put_rows(ctx, f.get(), h, ivf->ids.p, ivf->total, 8, 8);
+  put_rows(ctx, f.get(), h, ivf->rows.p, ivf->total, ldb, db);
+  if (coded)
+    put_rows(ctx, f.get(), h, ivf->codes.p, ivf->total, ivf->cstride, ivf->cstride);
+  const uint64_t sum = h.h;
+  VSK_REQUIRE(fwrite(&sum, 8, 1, f.get()) == 1 && fflush(f.get()) == 0, VSK_ERR_IO,
+              "index file: write failed");
+  VSK_REQUIRE(fclose(f.release()) == 0, VSK_ERR_IO, "index file: close failed");
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  VSK_REQUIRE(path, VSK_ERR_INVALID_ARGUMENT, "path is null");
+  File f(fopen(path, "rb"));
+  VSK_REQUIRE(f, VSK_ERR_IO, std::string("cannot open: ") + path);
+  Fnv1a h;
+  char magic[8];
+  get(f.get(), h, magic, 8);
+  VSK_REQUIRE(memcmp(magic, kIvfMagic, 8) == 0, VSK_ERR_IO, "not an IVF index file");
+  int32_t nd[2], ck[4];
+  int64_t tn[2];
+  get(f.get(), h, nd, 8);
+  get(f.get(), h, tn, 16);
+  get(f.get(), h, ck, 16);
+  const int32_t nlist = nd[0], d = nd[1];
+  const int64_t total = tn[0], next_id = tn[1];
+  VSK_REQUIRE(nlist > 0 && d > 0 && total >= 0 && total <= 0x7FFFFFFFll && next_id >= 0,
+              VSK_ERR_IO, "index file: bad header");
+  bool kind_ok = false;
+  if (ck[0] == 0) kind_ok = ck[1] == 0 && ck[2] == 0 && ck[3] == 0;
+  if (ck[0] == 1) kind_ok = ck[1] == (d + 15) / 16 * 16 && ck[2] == 0 && ck[3] == 0;
+  if (ck[0] == 2)
+    kind_ok = ck[2] > 0 && d % ck[2] == 0 && ck[3] >= 1 && ck[3] <= 256 &&
+              ck[1] == (ck[2] + 3) / 4 * 4;
+  VSK_REQUIRE(kind_ok, VSK_ERR_IO, "index file: bad code header");
+  // the file's length must be exactly what the header describes
+  const int64_t body = 8 + 8 + 16 + 16 + 4ll * nlist * d + 8ll * (nlist + 1) + 8 * total +
+                       4 * total * d + (int64_t)ck[1] * total + 8;
+  VSK_REQUIRE(fseek(f.get(), 0, SEEK_END) == 0 && ftell(f.get()) == body &&
+                  fseek(f.get(), 48, SEEK_SET) == 0,
+              VSK_ERR_IO, "index file: length does not match its header");
+  std::vector<float> cent((size_t)nlist * d);
+  get(f.get(), h, cent.data(), 4 * cent.size());
+  std::vector<int64_t> off((size_t)nlist + 1);
+  get(f.get(), h, off.data(), 8 * off.size());
+  bool off_ok = off[0] == 0 && off[nlist] == total;
+  for (int32_t l = 0; l < nlist && off_ok; ++l) off_ok = off[l] <= off[l + 1];
+  VSK_REQUIRE(off_ok, VSK_ERR_IO, "index file: bad list offsets");
+  vsk_ivf *raw = nullptr;
+  const vsk_status st = vsk_ivf_create(ctx, cent.data(), nlist, d, &raw);
+  if (st != VSK_OK) return st;
+  std::unique_ptr<vsk_ivf, IvfDeleter> ivf(raw, IvfDeleter{ctx});
+  const int32_t ld = ivf->ld;
+  ivf->rows.reserve(sizeof(float) * (size_t)std::max<int64_t>(total, 1) * ld);
+  ivf->ids.reserve(sizeof(int64_t) * (size_t)std::max<int64_t>(total, 1));
+  fill_i32(ctx, ivf->rows.as<int32_t>(), std::max<int64_t>(total, 1) * ld, 0);
+  get_rows(ctx, f.get(), h, ivf->ids.p, total, 8, 8);
+  get_rows(ctx, f.get(), h, ivf->rows.p, total, sizeof(float) * ld, sizeof(float) * d);
+  if (ck[0] != 0) {
+    ivf->codes.reserve((size_t)total * ck[1] + 16);
+    fill_i32(ctx, ivf->codes.as<int32_t>(), ((int64_t)total * ck[1] + 16) / 4, 0);
+    get_rows(ctx, f.get(), h, ivf->codes.p, total, ck[1], ck[1]);
+  }
+  uint64_t sum = 0;
+  VSK_REQUIRE(fread(&sum, 8, 1, f.get()) == 1 && sum == h.h, VSK_ERR_IO,
+              "index file: checksum mismatch");
+  VSK_HIP(hipMemcpyAsync(ivf->list_off.p, off.data(), sizeof(int64_t) * (nlist + 1),
+                         hipMemcpyHostToDevice, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  ivf->off = off;
+  ivf->total = total;
+  ivf->next_id = next_id;
+  ivf->ckind = ck[0];
+  ivf->cstride = ck[1];
+  ivf->cM = ck[2];
+  ivf->cksub = ck[3];
+  ivf->ctotal = ck[0] ? total : -1;
+  *out = ivf.release();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_info(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *nlist, int32_t *d,
+                        int64_t *total, int32_t *code_kind) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  if (nlist) *nlist = ivf->nlist;
+  if (d) *d = ivf->d;
+  if (total) *total = ivf->total;
+  if (code_kind) *code_kind = ivf->ctotal == ivf->total ? ivf->ckind : 0;
   VSK_API_END(ctx);
 }
 

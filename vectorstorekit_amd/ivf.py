@@ -11,6 +11,7 @@ strategy)`` (:124-202; ``"exact"`` probes every list, :551-554),
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -213,6 +214,35 @@ class IVFIndex:
                                                       self._pq.handle, qp, nq, nprobe, k,
                                                       dp, ip))
         return dist, ids
+
+    # ---- index file (the whole index; the reference's persistence keeps
+    # only centroids and counts, Indexes/IVFIndex.swift:297-328)
+    def save(self, path: str):
+        self._need()
+        self.ctx.check(self.ctx.lib.vsk_ivf_save(self.ctx.handle, self.handle,
+                                                 os.fsencode(path)))
+
+    @classmethod
+    def load(cls, ctx: Context, path: str, numberOfProbes: int = 10, sq8=None, pq=None):
+        """An index written by ``save``.  ``sq8`` / ``pq``: the quantizer its
+        codes were made with, needed to search them."""
+        h = ctypes.c_void_p()
+        ctx.check(ctx.lib.vsk_ivf_load(ctx.handle, os.fsencode(path), ctypes.byref(h)))
+        nlist, d, kind = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        total = ctypes.c_int64()
+        ctx.check(ctx.lib.vsk_ivf_info(ctx.handle, h, ctypes.byref(nlist), ctypes.byref(d),
+                                       ctypes.byref(total), ctypes.byref(kind)))
+        idx = cls(ctx, IVFConfiguration(dimensions=d.value, numberOfCentroids=nlist.value,
+                                        numberOfProbes=min(numberOfProbes, nlist.value)))
+        idx.handle = h
+        # the centroids follow the 48-byte header
+        idx._centroids = np.fromfile(path, np.float32, nlist.value * d.value,
+                                     offset=48).reshape(nlist.value, d.value)
+        if kind.value == 1:
+            idx._sq8 = sq8
+        elif kind.value == 2:
+            idx._pq = pq
+        return idx
 
     def list_sizes(self) -> np.ndarray:
         self._need()
