@@ -25,6 +25,12 @@ __device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np,
   return i < np ? P[i] : C[i - np];
 }
 
+// REG: keys per thread held in registers when a query's list fits (REG x
+// SEL_THREADS keys): every pass then reads registers, not the list again.
+// The registers cost occupancy, so only callers whose lists are a few
+// thousand keys (IVF candidate segments, a dense chunk as small as the IVF
+// probe's centroids) take it.
+template <int REG>
 __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -59,7 +65,22 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
     for (int s = tid; s < a.nseg; s += SEL_THREADS) seg_cnt[s] = a.seg_n[q * a.nseg + s];
     __syncthreads();
   }
+  const bool inreg = REG > 0 && !seg && total <= (int64_t)REG * SEL_THREADS;  // uniform
+  uint64_t regs[REG > 0 ? REG : 1];
+  if (inreg) {
+#pragma unroll
+    for (int r = 0; r < REG; ++r) {
+      const int64_t i = tid + (int64_t)r * SEL_THREADS;
+      regs[r] = i < total ? sel_elem(P, np, C, i) : VSK_KEY_NONE;
+    }
+  }
   auto each_key = [&](auto &&f) {
+    if (inreg) {
+#pragma unroll
+      for (int r = 0; r < REG; ++r)
+        if (tid + (int64_t)r * SEL_THREADS < total) f(regs[r]);
+      return;
+    }
     if (!seg) {
       for (int64_t i = tid; i < total; i += SEL_THREADS) f(sel_elem(P, np, C, i));
       return;
@@ -220,7 +241,10 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   if (a.k < 1 || a.k > VSK_MAX_K)
     fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
   KernelTimer t(ctx, name);
-  k_select<<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  if (a.seg_off || a.regs)
+    k_select<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  else
+    k_select<0><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   check_launch(name);
 }
 
@@ -296,6 +320,7 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     sa.counts = counts;
     sa.best_out = best;
     sa.thresh = thresh;
+    sa.regs = dense && cap + k <= 32 * SEL_THREADS;  // e.g. IVF probing over the centroids
     if (!dense) {
       fill_i32(ctx, ovf_count, 1, 0);
       fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);

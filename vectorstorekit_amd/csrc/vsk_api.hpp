@@ -64,6 +64,7 @@ struct SelectArgs {
   const int32_t *seg_n = nullptr;
   int32_t nseg = 0;
   int64_t seg_stride = 0;
+  bool regs = false;  // small lists: the register-resident variant
 };
 void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name);
 
