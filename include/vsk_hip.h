@@ -265,6 +265,20 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
                           const int8_t *qcodes, int64_t nq, int32_t k,
                           int32_t *out_score, int64_t *out_ids);
 
+/* No counterpart in the reference: vsk_sq8_search without any device
+ * allocation, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as vsk_sq8_search, bit for bit, but qcodes,
+ * out_score and out_ids must be device memory, and the working buffers
+ * (candidate keys, thresholds, counters, padded query codes) live in one
+ * static 64 MiB device array per GPU, held until the process ends.  Queries
+ * run in batches that fit it; a (k, d) whose single query does not fit
+ * returns VSK_ERR_INVALID_BUFFER_SIZE.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (several contexts or threads) race. */
+vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
+                                  const int8_t *qcodes, int64_t nq, int32_t k,
+                                  int32_t *out_score, int64_t *out_ids);
+
 /* ---- product quantization -------------------------------------------------
  * ProductQuantizer (Quantization/ProductQuantizer.swift): M segments of
  * dsub dims, ksub codewords each (ksub <= 256, codes uint8).

@@ -114,6 +114,7 @@ SIGNATURES = {
     "vsk_sq8_upload": (c_int32, [P, P, c_int64, c_int32, PP]),
     "vsk_sq8_free": (c_int32, [P, P]),
     "vsk_sq8_search": (c_int32, [P, P, P, c_int64, c_int32, P, P]),
+    "vsk_sq8_search_noalloc": (c_int32, [P, P, P, c_int64, c_int32, P, P]),
     "vsk_pq_create": (c_int32, [P, P, c_int32, c_int32, c_int32, PP]),
     "vsk_pq_free": (c_int32, [P, P]),
     "vsk_pq_upload": (c_int32, [P, P, P, c_int64, c_int32, c_int32, PP]),

@@ -360,6 +360,9 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   }
   if (device < 0 || device >= count) return VSK_ERR_DEVICE_NOT_AVAILABLE;
   if (hipSetDevice(device) != hipSuccess) return VSK_ERR_DEVICE_NOT_AVAILABLE;
+  // the device address of this GPU's no-allocation scratch (sq8.hip), once
+  // per device; a failure is reported by the entry point that needs it
+  sq8_noalloc_setup(device);
   vsk_ctx *c = new vsk_ctx();
   c->device = device;
   int cus = 0;

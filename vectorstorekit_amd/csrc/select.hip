@@ -264,23 +264,28 @@ int64_t query_batch(int64_t nq, int64_t cap) {
 
 void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
                       int64_t cap, const ScanFn &scan, uint64_t *best,
-                      const char *select_name, int64_t max_growth) {
+                      const char *select_name, int64_t max_growth,
+                      const TopkWorkspace *ws) {
   if (nq <= 0) return;
   fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
   if (n <= 0) return;
   if (cap > n) cap = n;  // the whole database is one dense chunk
-  uint64_t *thresh =
-      static_cast<uint64_t *>(ctx->scratch_ptr("topk.thresh", 8 * nq));
-  uint64_t *cand = static_cast<uint64_t *>(
-      ctx->scratch_ptr("topk.cand", sizeof(uint64_t) * (size_t)nq * cap));
-  int32_t *counts =
-      static_cast<int32_t *>(ctx->scratch_ptr("topk.counts", 4 * nq));
-  uint8_t *ovf_mask =
-      static_cast<uint8_t *>(ctx->scratch_ptr("topk.ovfmask", nq + 64));
-  int32_t *seg_n = static_cast<int32_t *>(
-      ctx->scratch_ptr("topk.segn", sizeof(int32_t) * (size_t)nq * VSK_MAX_SEG));
-  int32_t *ovf_count =
-      static_cast<int32_t *>(ctx->scratch_ptr("topk.ovfcount", 64));
+  TopkWorkspace w;
+  if (ws) {
+    w = *ws;
+  } else {
+    w.thresh = static_cast<uint64_t *>(ctx->scratch_ptr("topk.thresh", 8 * nq));
+    w.cand = static_cast<uint64_t *>(
+        ctx->scratch_ptr("topk.cand", sizeof(uint64_t) * (size_t)nq * cap));
+    w.counts = static_cast<int32_t *>(ctx->scratch_ptr("topk.counts", 4 * nq));
+    w.ovf_mask = static_cast<uint8_t *>(ctx->scratch_ptr("topk.ovfmask", nq + 64));
+    w.seg_n = static_cast<int32_t *>(
+        ctx->scratch_ptr("topk.segn", sizeof(int32_t) * (size_t)nq * VSK_MAX_SEG));
+    w.ovf_count = static_cast<int32_t *>(ctx->scratch_ptr("topk.ovfcount", 64));
+  }
+  uint64_t *thresh = w.thresh, *cand = w.cand;
+  int32_t *counts = w.counts, *seg_n = w.seg_n, *ovf_count = w.ovf_count;
+  uint8_t *ovf_mask = w.ovf_mask;
   fill_u64(ctx, thresh, nq, VSK_KEY_NONE);
 
   int64_t r0 = 0;
@@ -304,7 +309,7 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     int64_t seg_stride = 0;
     {
       ScanRequest rq{r0, r0 + c, thresh, nullptr, cand, cap, counts, dense};
-      if (!dense) {
+      if (!dense && seg_n) {
         rq.seg_n = seg_n;
         rq.seg_nseg = &nseg;
         rq.seg_stride = &seg_stride;

@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "vsk_api.hpp"
 
@@ -489,6 +490,56 @@ static const int8_t *codes_to_device(vsk_ctx *ctx, const int8_t *p, int64_t n,
   return out;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation search (vsk_sq8_search_noalloc): one static
+// device array per GPU, held until the process ends.  Host code never passes
+// `scratch` itself to a kernel (on the host the name is only a stand-in);
+// it uses the device address hipGetSymbolAddress gives, per device, at
+// context creation.  Every call on one GPU shares that GPU's array, so calls
+// that overlap on one GPU (two contexts, two threads) race.
+// ---------------------------------------------------------------------------
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_noalloc_mu;
+static bool g_noalloc_done[NOALLOC_MAX_DEVICES];
+static hipError_t g_noalloc_err[NOALLOC_MAX_DEVICES];
+static unsigned char *g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+
+// Resolves the device address of this GPU's scratch array once per device;
+// the device must be current.  Called by vsk_create.
+void sq8_noalloc_setup(int device) {
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES) return;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_done[device]) return;
+  void *p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    p = nullptr;
+  }
+  g_noalloc_err[device] = e;
+  g_noalloc_ptr[device] = static_cast<unsigned char *>(p);
+  g_noalloc_done[device] = true;
+}
+
+static unsigned char *noalloc_scratch(int device) {
+  VSK_REQUIRE(device >= 0 && device < NOALLOC_MAX_DEVICES, VSK_ERR_DEVICE_NOT_AVAILABLE,
+              "device index beyond the no-allocation scratch table");
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  VSK_REQUIRE(g_noalloc_done[device], VSK_ERR_EXECUTION_FAILED,
+              "no-allocation scratch not set up for this device");
+  if (!g_noalloc_ptr[device])
+    fail(VSK_ERR_EXECUTION_FAILED,
+         std::string("hipGetSymbolAddress of the no-allocation scratch failed: ") +
+             hipGetErrorString(g_noalloc_err[device]));
+  return g_noalloc_ptr[device];
+}
+
+// bytes of one carved region, rounded to 256
+static size_t region(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+
 }  // namespace vsk
 
 using namespace vsk;
@@ -692,6 +743,96 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
   }
   os.copy_back();
   oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
+                                  const int8_t *qcodes, int64_t nq, int32_t k,
+                                  int32_t *out_score, int64_t *out_ids) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db, VSK_ERR_INVALID_ARGUMENT, "db is null");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(qcodes && out_score && out_ids, VSK_ERR_INVALID_ARGUMENT,
+              "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE,
+              "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
+              "too many queries");
+  // staging a host buffer would need device memory: only device buffers
+  VSK_REQUIRE(is_device_ptr(qcodes) && is_device_ptr(out_score) && is_device_ptr(out_ids),
+              VSK_ERR_INVALID_ARGUMENT,
+              "vsk_sq8_search_noalloc takes device buffers only (qcodes, out_score, out_ids)");
+  unsigned char *base = noalloc_scratch(ctx->device);
+  const int64_t cap = std::min<int64_t>(default_cap(k), db->n);
+  const bool pad = db->ldc != db->d;
+  // scratch per query: best keys, threshold, candidates, count, overflow
+  // flag, the padded query codes; fixed: overflow counter + slack
+  const size_t fixed = 6 * 256 + 64 + 256;
+  const size_t per_q = sizeof(uint64_t) * (size_t)k + 8 + sizeof(uint64_t) * (size_t)cap + 4 +
+                       1 + (pad ? (size_t)db->ldc : 0);
+  int64_t qb = (int64_t)((NOALLOC_SCRATCH_BYTES - fixed) / per_q);
+  if (qb > nq) qb = nq;
+  if (qb < 1)
+    fail(VSK_ERR_INVALID_BUFFER_SIZE,
+         "one query needs " + std::to_string(per_q + fixed) +
+             " bytes of scratch, more than the no-allocation maximum of " +
+             std::to_string(NOALLOC_SCRATCH_BYTES) + " bytes (k or d too large)");
+  // carve the array for a batch of qb queries
+  size_t off = 0;
+  auto carve = [&](size_t bytes) {
+    unsigned char *p = base + off;
+    off += region(bytes);
+    return p;
+  };
+  uint64_t *best = reinterpret_cast<uint64_t *>(carve(sizeof(uint64_t) * (size_t)qb * k));
+  TopkWorkspace ws;
+  ws.thresh = reinterpret_cast<uint64_t *>(carve(8 * (size_t)qb));
+  ws.cand = reinterpret_cast<uint64_t *>(carve(sizeof(uint64_t) * (size_t)qb * cap));
+  ws.counts = reinterpret_cast<int32_t *>(carve(4 * (size_t)qb));
+  ws.ovf_mask = carve((size_t)qb + 64);
+  ws.ovf_count = reinterpret_cast<int32_t *>(carve(64));
+  ws.seg_n = nullptr;  // the SQ8 scans append; no segmented lists
+  int8_t *qpad = pad ? reinterpret_cast<int8_t *>(carve((size_t)qb * db->ldc)) : nullptr;
+  if (off > NOALLOC_SCRATCH_BYTES)
+    fail(VSK_ERR_INVALID_BUFFER_SIZE, "no-allocation scratch layout exceeds its maximum");
+
+  CallScope cs(ctx);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    const int8_t *dq = qcodes + b0 * db->d;
+    if (pad) {
+      // zero padding adds 0 to every dot product
+      fill_i32(ctx, reinterpret_cast<int32_t *>(qpad), nb * db->ldc / 4, 0);
+      VSK_HIP(hipMemcpy2DAsync(qpad, db->ldc, dq, db->d, db->d, (size_t)nb,
+                               hipMemcpyDeviceToDevice, ctx->stream));
+      dq = qpad;
+    }
+    Sq8Args a0{};
+    a0.X = db->codes.as<int8_t>();
+    a0.ldx = db->ldc;
+    a0.Q = dq;
+    a0.ldq = db->ldc;
+    a0.kbytes = db->ldc;
+    a0.nq = (int32_t)nb;
+    ScanFn scan = [&](const ScanRequest &r) {
+      Sq8Args a = a0;
+      a.r0 = r.r0;
+      a.r1 = r.r1;
+      a.thresh = r.thresh;
+      a.active = r.active;
+      a.cand = r.cand;
+      a.cap = r.cap;
+      a.counts = r.counts;
+      launch_sq8(ctx, a, r.dense);
+    };
+    progressive_topk(ctx, nb, db->n, k, cap, scan, best, "sq8_select", 8, &ws);
+    KernelTimer t(ctx, "sq8_decode");
+    k_sq8_decode<<<grid1(nb * k), 256, 0, ctx->stream>>>(best, nb * k, out_score + b0 * k,
+                                                         out_ids + b0 * k);
+    check_launch("sq8_decode");
+  }
   cs.finish();
   VSK_API_END(ctx);
 }

@@ -92,6 +92,18 @@ struct ScanRequest {
 };
 using ScanFn = std::function<void(const ScanRequest &)>;
 
+// Device buffers of one progressive_topk call, for callers that bring their
+// own memory (nothing is allocated then).  cand holds nq*cap keys with cap
+// already clamped to the row count; seg_n may be null (appended lists only).
+struct TopkWorkspace {
+  uint64_t *thresh = nullptr;    // nq
+  uint64_t *cand = nullptr;      // nq * cap
+  int32_t *counts = nullptr;     // nq
+  uint8_t *ovf_mask = nullptr;   // roundup(nq, 4) + 64
+  int32_t *ovf_count = nullptr;  // 1
+  int32_t *seg_n = nullptr;      // nq * VSK_MAX_SEG, or null
+};
+
 // Exact top-k over n rows for nq queries by streaming the rows in growing
 // chunks: the first chunk is kept whole, later chunks only keep rows that
 // beat the running k-th key of their query; a query whose survivors
@@ -99,9 +111,12 @@ using ScanFn = std::function<void(const ScanRequest &)>;
 // (device), sorted ascending per query on return.  A chunk after the first
 // holds at most cap/(2k) times the rows already seen, and at most max_growth
 // times when that is positive.
+// ws: the buffers to use (sized for nq and min(cap, n)); null = the
+// context's scratch slots.
 void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
                       int64_t cap, const ScanFn &scan, uint64_t *best,
-                      const char *select_name, int64_t max_growth = 0);
+                      const char *select_name, int64_t max_growth = 0,
+                      const TopkWorkspace *ws = nullptr);
 
 // candidate buffer capacity per query used by the progressive scans
 int64_t default_cap(int32_t k);
@@ -113,5 +128,9 @@ int64_t query_batch(int64_t nq, int64_t cap);
 void decode_keys(vsk_ctx *ctx, const uint64_t *best, int64_t total,
                  bool sqrt_out, const int64_t *id_map, float *out_dist,
                  int64_t *out_ids);
+
+// Resolves, once per device (the device current), the device address of the
+// static scratch array that vsk_sq8_search_noalloc uses (sq8.hip).
+void sq8_noalloc_setup(int device);
 
 }  // namespace vsk
