@@ -122,6 +122,15 @@ void *vsk_stream(vsk_ctx *ctx);
  * MetalProfiler.recordOperation (Acceleration/Metal/MetalProfiler.swift:
  * 74-110). */
 float vsk_last_kernel_ms(const vsk_ctx *ctx);
+/* Which queries of the last vsk_search_flat call on ctx the exact screen
+ * redid: tier 1 = screened again keeping 1024 candidates, tier 2 = the
+ * exact scan over every row (queries whose bound test failed; see
+ * flat_screen.hip).  *count receives their number; the first min(cap,
+ * count) query indices, ascending, go to out (out may be NULL if cap is 0).
+ * Complements MetalProfiler's per-operation records
+ * (Acceleration/Metal/MetalProfiler.swift:74-110). */
+vsk_status vsk_last_screen_redo(const vsk_ctx *ctx, int32_t tier, int64_t *out,
+                                int64_t cap, int64_t *count);
 /* Per-kernel event timing (off by default). */
 vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on);
 vsk_status vsk_profile_reset(vsk_ctx *ctx);

@@ -38,6 +38,7 @@ def lib():
             "vsko_dot": (c_float, [P, P, c_int32]),
             "vsko_l1": (c_float, [P, P, c_int32]),
             "vsko_distance": (c_float, [P, P, c_int32, c_int32]),
+            "vsko_normalize": (None, [P, c_int64, c_int32, P]),
             "vsko_distances": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, c_int32]),
             "vsko_search_flat": (None, [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P, P,
                                         c_int32, c_int32]),
@@ -92,6 +93,14 @@ def distance(q, x, metric) -> float:
     q, qp = _c(q, np.float32)
     x, xp = _c(x, np.float32)
     return float(lib().vsko_distance(qp, xp, q.shape[-1], metric))
+
+
+def normalize(x):
+    """normalizeVectors: each row divided by sqrt(sum x^2) + 1e-8."""
+    x, xp = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().vsko_normalize(xp, x.shape[0], x.shape[1], out.ctypes.data)
+    return out
 
 
 def distances(q, x, metric, threads=0):

@@ -129,6 +129,23 @@ float vsko_distance(const float *q, const float *x, int32_t d,
   }
 }
 
+/* normalizeVectors (Acceleration/Metal/Shaders/DistanceShaders.metal:
+ * 403-429): magnitude = sum of x_i * x_i in index order, then
+ * sqrt(magnitude) + 1e-8, then every component divided by it (a division,
+ * not a multiply by the reciprocal). */
+void vsko_normalize(const float *x, int64_t n, int32_t d, float *out) {
+  for (int64_t r = 0; r < n; ++r) {
+    const float *xr = x + r * d;
+    float m = 0.0f;
+    for (int32_t i = 0; i < d; ++i) {
+      float v = xr[i];
+      m += v * v;
+    }
+    m = sqrtf(m) + 1e-8f;
+    for (int32_t i = 0; i < d; ++i) out[r * d + i] = xr[i] / m;
+  }
+}
+
 /* 16 independent accumulators: what a SIMD library loop does.  Used only by
  * the CPU-baseline timing (fast != 0), never by parity checks. */
 static float dot16(const float *a, const float *b, int32_t d) {
@@ -324,11 +341,182 @@ static void flat_range(void *p, int64_t lo, int64_t hi) {
   }
   free(s.h);
 }
+/* ---- the exact path vectorised across rows ------------------------------
+ * Each SIMD lane holds one row's running sum, taken in dimension order with
+ * no FMA, so every lane computes exactly what vsko_distance computes for its
+ * row; only the rows are processed side by side.  Rows are first copied into
+ * blocks of RB rows stored dimension-major (xt[(b*d + i)*RB + r] = row
+ * b*RB + r, dimension i; rows past n are zero and never reported). */
+#define RB 16
+#define QG 4
+typedef float vrow __attribute__((vector_size(RB * 4), aligned(64)));
+typedef int32_t vrowi __attribute__((vector_size(RB * 4), aligned(64)));
+
+typedef struct {
+  const float *x;
+  int64_t n;
+  int32_t d;
+  float *xt;
+  float *xnorm; /* sqrtf(sum x^2) per row, COSINE only */
+} xt_ctx;
+static void xt_range(void *p, int64_t lo, int64_t hi) {
+  xt_ctx *c = (xt_ctx *)p;
+  const int32_t d = c->d;
+  for (int64_t b = lo; b < hi; ++b) {
+    float *blk = c->xt + b * (int64_t)d * RB;
+    for (int32_t r = 0; r < RB; ++r) {
+      const int64_t row = b * RB + r;
+      const float *xr = row < c->n ? c->x + row * d : NULL;
+      for (int32_t i = 0; i < d; ++i) blk[(int64_t)i * RB + r] = xr ? xr[i] : 0.0f;
+    }
+    if (c->xnorm) {
+      vrow a = {0};
+      for (int32_t i = 0; i < d; ++i) {
+        vrow v = *(const vrow *)(blk + (int64_t)i * RB);
+        a += v * v;
+      }
+      for (int32_t r = 0; r < RB && b * RB + r < c->n; ++r) c->xnorm[b * RB + r] = sqrtf(a[r]);
+    }
+  }
+}
+
+/* acc[g][r] = the metric's running sum for query g and row r of one block.
+ * A block's RB = 16 lanes are two 8-lane halves (AVX2 registers), so the
+ * 4 x 2 accumulators stay in registers. */
+typedef float v8f __attribute__((vector_size(32)));
+typedef int32_t v8i __attribute__((vector_size(32)));
+#define V8_STEP(OP)                                                             \
+  for (int32_t i = 0; i < d; ++i) {                                             \
+    const v8f xl = *(const v8f *)(blk + (int64_t)i * RB);                       \
+    const v8f xh = *(const v8f *)(blk + (int64_t)i * RB + 8);                   \
+    const float s0 = q0[i], s1 = q1[i], s2 = q2[i], s3 = q3[i];                 \
+    OP(a0l, a0h, s0);                                                           \
+    OP(a1l, a1h, s1);                                                           \
+    OP(a2l, a2h, s2);                                                           \
+    OP(a3l, a3h, s3);                                                           \
+  }
+#define OP_L2(al, ah, sc)                                                       \
+  {                                                                             \
+    v8f tl = sc - xl, th = sc - xh;                                             \
+    al += tl * tl;                                                              \
+    ah += th * th;                                                              \
+  }
+#define OP_L1(al, ah, sc)                                                       \
+  {                                                                             \
+    v8f tl = sc - xl, th = sc - xh;                                             \
+    al += (v8f)((v8i)tl & absmask);                                             \
+    ah += (v8f)((v8i)th & absmask);                                             \
+  }
+#define OP_DOT(al, ah, sc)                                                      \
+  {                                                                             \
+    al += sc * xl;                                                              \
+    ah += sc * xh;                                                              \
+  }
+static void block_sums(const float *blk, int32_t d, const float *const *qs, int32_t metric,
+                       vrow acc[QG]) {
+  v8f a0l = {0}, a0h = {0}, a1l = {0}, a1h = {0}, a2l = {0}, a2h = {0}, a3l = {0}, a3h = {0};
+  const float *q0 = qs[0], *q1 = qs[1], *q2 = qs[2], *q3 = qs[3];
+  const v8i absmask = (v8i){0} + 0x7fffffff;
+  switch (metric) {
+  case VSKO_L2SQ:
+  case VSKO_L2:
+    V8_STEP(OP_L2);
+    break;
+  case VSKO_L1:
+    V8_STEP(OP_L1);
+    break;
+  default: /* the dot-product metrics */
+    V8_STEP(OP_DOT);
+  }
+  for (int r = 0; r < 8; ++r) {
+    acc[0][r] = a0l[r], acc[0][r + 8] = a0h[r];
+    acc[1][r] = a1l[r], acc[1][r + 8] = a1h[r];
+    acc[2][r] = a2l[r], acc[2][r + 8] = a2h[r];
+    acc[3][r] = a3l[r], acc[3][r + 8] = a3h[r];
+  }
+}
+
+typedef struct {
+  const float *q, *xt, *xnorm;
+  int64_t n;
+  int32_t d, k, metric;
+  float *od;
+  int64_t *oi;
+} flatv_ctx;
+
+/* vsko_distance's final step on a lane's sum (same operations, same order) */
+static float finish_sum(float s, int32_t metric, float qn, float xn) {
+  switch (metric) {
+  case VSKO_L2:
+    return sqrtf(s);
+  case VSKO_COSINE:
+    return 1.0f - s / (qn * xn + 1e-8f);
+  case VSKO_COSINE_NORMALIZED:
+    return 1.0f - s;
+  case VSKO_DOT:
+    return -s;
+  default: /* L2SQ, L1 */
+    return s;
+  }
+}
+
+static void flatv_range(void *p, int64_t lo, int64_t hi) {
+  flatv_ctx *c = (flatv_ctx *)p;
+  const int64_t m = hi - lo;
+  if (m <= 0) return;
+  const int32_t d = c->d, k = c->k;
+  topk_t *heaps = (topk_t *)malloc(sizeof(topk_t) * (size_t)m);
+  pair_t *store = (pair_t *)malloc(sizeof(pair_t) * (size_t)m * (k > 0 ? k : 1));
+  float *qn = (float *)malloc(sizeof(float) * (size_t)m);
+  for (int64_t i = 0; i < m; ++i) {
+    heaps[i].h = store + i * (k > 0 ? k : 1);
+    heaps[i].n = 0;
+    heaps[i].k = k;
+    const float *qi = c->q + (lo + i) * d;
+    qn[i] = c->metric == VSKO_COSINE ? sqrtf(vsko_dot(qi, qi, d)) : 0.0f;
+  }
+  const int64_t nblocks = (c->n + RB - 1) / RB;
+  vrow acc[QG];
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const float *blk = c->xt + b * (int64_t)d * RB;
+    const int32_t rows = (int32_t)(c->n - b * RB < RB ? c->n - b * RB : RB);
+    for (int64_t g0 = 0; g0 < m; g0 += QG) {
+      const float *qs[QG];
+      const int32_t ng = (int32_t)(m - g0 < QG ? m - g0 : QG);
+      for (int32_t g = 0; g < QG; ++g) qs[g] = c->q + (lo + g0 + (g < ng ? g : 0)) * d;
+      block_sums(blk, d, qs, c->metric, acc);
+      for (int32_t g = 0; g < ng; ++g)
+        for (int32_t r = 0; r < rows; ++r) {
+          const int64_t row = b * RB + r;
+          const float xn = c->xnorm ? c->xnorm[row] : 0.0f;
+          topk_push(&heaps[g0 + g], finish_sum(acc[g][r], c->metric, qn[g0 + g], xn), row);
+        }
+    }
+  }
+  for (int64_t i = 0; i < m; ++i)
+    topk_finish(&heaps[i], c->od + (lo + i) * k, c->oi + (lo + i) * k);
+  free(qn);
+  free(store);
+  free(heaps);
+}
+
 void vsko_search_flat(const float *q, int64_t nq, const float *x, int64_t n,
                       int32_t d, int32_t k, int32_t metric, float *out_dist,
                       int64_t *out_ids, int32_t nthreads, int32_t fast) {
-  flat_ctx c = {q, x, n, d, k, metric, fast, out_dist, out_ids};
-  parallel_for(nq, nthreads, flat_range, &c);
+  if (fast || metric == VSKO_HAMMING || n <= 0 || d <= 0) {
+    flat_ctx c = {q, x, n, d, k, metric, fast, out_dist, out_ids};
+    parallel_for(nq, nthreads, flat_range, &c);
+    return;
+  }
+  const int64_t nblocks = (n + RB - 1) / RB;
+  float *xt = (float *)aligned_alloc(64, sizeof(float) * (size_t)nblocks * d * RB);
+  float *xnorm = metric == VSKO_COSINE ? (float *)malloc(sizeof(float) * (size_t)n) : NULL;
+  xt_ctx tc = {x, n, d, xt, xnorm};
+  parallel_for(nblocks, nthreads, xt_range, &tc);
+  flatv_ctx c = {q, xt, xnorm, n, d, k, metric, out_dist, out_ids};
+  parallel_for(nq, nthreads, flatv_range, &c);
+  free(xnorm);
+  free(xt);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -556,25 +744,62 @@ typedef struct {
   int32_t *os;
   int64_t *oi;
 } sq8_ctx;
+/* top-k on integer keys (distance = -score as int64, tie = row): the same
+ * max-heap as pair_t, exact for any score */
+typedef struct {
+  int64_t v, t;
+} ipair_t;
+static int ipair_less(ipair_t a, ipair_t b) { return a.v < b.v || (a.v == b.v && a.t < b.t); }
+static void iheap_push(ipair_t *h, int32_t *n, int32_t k, ipair_t p) {
+  if (*n < k) {
+    int32_t i = (*n)++;
+    h[i] = p;
+    while (i > 0) {
+      int32_t up = (i - 1) / 2;
+      if (!ipair_less(h[up], h[i])) break;
+      ipair_t t = h[i];
+      h[i] = h[up];
+      h[up] = t;
+      i = up;
+    }
+  } else if (k > 0 && ipair_less(p, h[0])) {
+    h[0] = p;
+    for (int32_t i = 0;;) {
+      int32_t l = 2 * i + 1, r = l + 1, m = i;
+      if (l < *n && ipair_less(h[m], h[l])) m = l;
+      if (r < *n && ipair_less(h[m], h[r])) m = r;
+      if (m == i) break;
+      ipair_t t = h[i];
+      h[i] = h[m];
+      h[m] = t;
+      i = m;
+    }
+  }
+}
+static int ipair_cmp(const void *a, const void *b) {
+  ipair_t x = *(const ipair_t *)a, y = *(const ipair_t *)b;
+  return ipair_less(x, y) ? -1 : (ipair_less(y, x) ? 1 : 0);
+}
+
 static void sq8_range(void *p, int64_t lo, int64_t hi) {
   sq8_ctx *c = (sq8_ctx *)p;
-  pair_t *buf = (pair_t *)malloc(sizeof(pair_t) * (c->k > 0 ? c->k : 1));
-  float *tmpd = (float *)malloc(sizeof(float) * (c->k > 0 ? c->k : 1));
+  ipair_t *h = (ipair_t *)malloc(sizeof(ipair_t) * (c->k > 0 ? c->k : 1));
   for (int64_t i = lo; i < hi; ++i) {
-    topk_t s = {buf, 0, c->k};
-    for (int64_t j = 0; j < c->n; ++j)
-      topk_push(&s, (float)(-vsko_sq8_dot(c->q + i * c->d, c->x + j * c->d,
-                                          c->d)),
-                j);
-    topk_finish(&s, tmpd, c->oi + i * c->k);
-    for (int32_t t = 0; t < c->k; ++t)
-      c->os[i * c->k + t] =
-          c->oi[i * c->k + t] >= 0 ? (int32_t)(-tmpd[t]) : INT32_MIN;
+    int32_t m = 0;
+    for (int64_t j = 0; j < c->n; ++j) {
+      ipair_t e = {-(int64_t)vsko_sq8_dot(c->q + i * c->d, c->x + j * c->d, c->d), j};
+      iheap_push(h, &m, c->k, e);
+    }
+    qsort(h, (size_t)m, sizeof(ipair_t), ipair_cmp);
+    for (int32_t t = 0; t < c->k; ++t) {
+      c->os[i * c->k + t] = t < m ? (int32_t)(-h[t].v) : INT32_MIN;
+      c->oi[i * c->k + t] = t < m ? h[t].t : -1;
+    }
   }
-  free(tmpd);
-  free(buf);
+  free(h);
 }
-/* |score| <= 128*128*d < 2^24 for d <= 1024, so the float key is exact. */
+/* Keys are the int64 negated scores, so the order is exact for any d (an
+ * int32 score itself holds |score| <= 128 * 128 * d for d < 131072). */
 void vsko_sq8_search(const int8_t *qcodes, int64_t nq, const int8_t *codes,
                      int64_t n, int32_t d, int32_t k, int32_t *out_score,
                      int64_t *out_ids, int32_t nthreads) {

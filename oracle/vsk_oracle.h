@@ -41,6 +41,8 @@ float vsko_l2sq(const float *a, const float *b, int32_t d);
 float vsko_dot(const float *a, const float *b, int32_t d);
 float vsko_l1(const float *a, const float *b, int32_t d);
 float vsko_distance(const float *q, const float *x, int32_t d, int32_t metric);
+/* normalizeVectors: out = x / (sqrt(sum x^2) + 1e-8) per row */
+void vsko_normalize(const float *x, int64_t n, int32_t d, float *out);
 /* out[i*n + j] = distance(q_i, x_j) */
 void vsko_distances(const float *q, int64_t nq, const float *x, int64_t n,
                     int32_t d, int32_t metric, float *out, int32_t nthreads);

@@ -146,8 +146,8 @@ def test_ivf_train_and_errors(ctx):
 def test_config3_full_size(ctx):
     """1M x 128 from a 4,096-Gaussian mixture, nlist 4096,
     nprobe 32, 10,000 queries, k=10.  Assignment checked bit-exact on a row
-    sample, search bit-exact on 200 queries, recall@10 vs exact search equal
-    to the oracle's on those queries."""
+    sample, search bit-exact on all 10,000 queries, recall@10 vs exact search
+    equal to the oracle's on the first 1,000."""
     import torch
 
     n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
@@ -172,10 +172,10 @@ def test_config3_full_size(ctx):
     gd, gi = idx.search(q, k)
     gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
     assert_sorted_unique(gd, gi)
-    sub = 200
-    od, oi = O.ivf_search(qh[:sub], xh, np.arange(n, dtype=np.int64), lists, ch, nprobe, k)
-    np.testing.assert_array_equal(gi[:sub], oi)
-    np.testing.assert_array_equal(gd[:sub], od)
+    od, oi = O.ivf_search(qh, xh, np.arange(n, dtype=np.int64), lists, ch, nprobe, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    sub = 1000
     td, ti = O.search_flat(qh[:sub], xh, k, O.L2)
-    assert recall(gi[:sub], ti) == recall(oi, ti)
+    assert recall(gi[:sub], ti) == recall(oi[:sub], ti)
     print(f"config3 recall@10 on {sub} queries: {recall(gi[:sub], ti):.4f}", flush=True)

@@ -150,3 +150,33 @@ def test_fast_variant_close():
         d0, i0 = O.search_flat(q, x, 5, m)
         d1, i1 = O.search_flat(q, x, 5, m, fast=True)
         np.testing.assert_allclose(d0, d1, rtol=1e-4, atol=1e-4)
+
+
+def test_normalize_pinned():
+    """vsko_normalize = normalizeVectors (DistanceShaders.metal:403-429):
+    pinned by an explicit fp32 left fold of the squares (np.cumsum on
+    float32 adds in index order), sqrt + 1e-8 in fp32 and a numpy fp32
+    division per component; closed forms for a zero row (stays 0) and a
+    constant row; and sensitivity: a reciprocal multiply and a pairwise
+    (tree) sum each change some outputs, so this test tells them apart."""
+    rng = np.random.default_rng(5)
+    for n, d in ((200, 768), (300, 37), (50, 1), (64, 100)):
+        x = (rng.standard_normal((n, d)) * rng.uniform(0.01, 100, (n, 1))).astype(np.float32)
+        x[3] = 0.0
+        got = O.normalize(x)
+        sq = np.cumsum(x * x, axis=1, dtype=np.float32)[:, -1]
+        m = (np.sqrt(sq, dtype=np.float32) + np.float32(1e-8)).astype(np.float32)
+        want = (x / m[:, None]).astype(np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert (got[3] == 0).all()
+        if d >= 37:
+            recip = (x * (np.float32(1) / m)[:, None]).astype(np.float32)
+            assert (recip != got).any()
+            tree = np.sqrt(np.sum(x * x, axis=1, dtype=np.float32)) + np.float32(1e-8)
+            assert (tree.astype(np.float32) != m).any() or d < 64
+    # constant row c: |x| = |c| sqrt(d) exactly for d a perfect square
+    c = np.full((1, 64), 3.0, np.float32)
+    np.testing.assert_array_equal(O.normalize(c), c / np.float32(np.float32(24.0) + np.float32(1e-8)))
+    # unit length within rounding
+    x = rng.standard_normal((100, 128)).astype(np.float32)
+    assert np.allclose(np.linalg.norm(O.normalize(x).astype(np.float64), axis=1), 1.0, atol=1e-6)

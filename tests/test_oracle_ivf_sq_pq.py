@@ -288,3 +288,21 @@ def test_ivf_coded_oracles_over_every_list():
     sc = codes[rows].astype(np.int64) @ qc[0].astype(np.int64)
     ps, _ = O.ivf_sq8_search(q[:1], qc[:1], codes, np.arange(900), lo, c, 3, 10)
     np.testing.assert_array_equal(ps[0], np.sort(sc)[::-1][:10])
+
+
+def test_sq8_search_scores_past_float_precision():
+    """Scores above 2^24 that differ by 1: a float key would merge them and
+    fall back to the row order; the int64 keys keep the higher score first.
+    Pinned by int64 brute force."""
+    d = 2048
+    q = np.full((1, d), 127, np.int8)
+    q[0, 5] = 1
+    codes = np.full((4, d), 127, np.int8)
+    codes[0, 5] = 126  # score S + 126 at row 0
+    codes[2, 7] = 126  # score S + 127 - 127 at row 2
+    score, ids = O.sq8_search(q, codes, 4)
+    ref = codes.astype(np.int64) @ q[0].astype(np.int64)
+    order = np.lexsort((np.arange(4), -ref))
+    assert ref[1] - ref[0] == 1 and ref[0] > 2 ** 24
+    np.testing.assert_array_equal(ids[0], order)
+    np.testing.assert_array_equal(score[0], ref[order])

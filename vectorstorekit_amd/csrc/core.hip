@@ -241,19 +241,45 @@ void row_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
   check_launch("row_norms");
 }
 
-// x <- x / (|x| + 1e-8), as normalizeVectors
-// (Acceleration/Metal/Shaders/DistanceShaders.metal:403-429)
+// normalizeVectors (Acceleration/Metal/Shaders/DistanceShaders.metal:
+// 403-429): m = sqrt(sum x_i^2) + 1e-8 with the squares added in dimension
+// order (no FMA), then x_i <- x_i / m, a division per component.  One lane
+// per row keeps the sequential sum; each wave stages 64 rows x 32 columns
+// at a time through LDS so the row reads stay coalesced.
+constexpr int NRM_COLS = 32;
 __global__ __launch_bounds__(256) void k_normalize_rows(float *x, int64_t n,
                                                        int32_t d, int32_t ld) {
-  const int lane = threadIdx.x & 63;
-  int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= n) return;
-  float *r = x + row * ld;
+#pragma clang fp contract(off)
+  __shared__ float tile[4][64][NRM_COLS + 1];
+  __shared__ float mag[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + w) * 64;
+  // every wave reaches the barriers; a wave past the last row has no rows
+  const int rows = n - row0 >= 64 ? 64 : (n > row0 ? (int)(n - row0) : 0);
   float s = 0.f;
-  for (int j = lane; j < d; j += 64) s += r[j] * r[j];
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-  float inv = 1.0f / (sqrtf(s) + 1e-8f);
-  for (int j = lane; j < d; j += 64) r[j] = r[j] * inv;
+  for (int32_t c0 = 0; c0 < d; c0 += NRM_COLS) {
+    // lanes 0-31 read one row's 32 columns, lanes 32-63 the next row's
+#pragma unroll 4
+    for (int j = 0; j < 32; ++j) {
+      const int r = 2 * j + (lane >> 5), c = c0 + (lane & 31);
+      tile[w][r][lane & 31] = (r < rows && c < d) ? x[(row0 + r) * ld + c] : 0.f;
+    }
+    __syncthreads();
+    const int cn = d - c0 < NRM_COLS ? d - c0 : NRM_COLS;
+    for (int c = 0; c < cn; ++c) {
+      const float v = tile[w][lane][c];
+      s = s + v * v;
+    }
+    __syncthreads();
+  }
+  mag[w][lane] = sqrtf(s) + 1e-8f;
+  __syncthreads();
+  if (rows == 0) return;
+  for (int r = 0; r < rows; ++r) {
+    const float m = mag[w][r];
+    float *xr = x + (row0 + r) * ld;
+    for (int32_t c = lane; c < d; c += 64) xr[c] = xr[c] / m;
+  }
 }
 
 // decode composite keys into (distance, id) outputs
@@ -408,6 +434,17 @@ const char *vsk_last_error(const vsk_ctx *ctx) {
 void *vsk_stream(vsk_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 float vsk_last_kernel_ms(const vsk_ctx *ctx) { return ctx ? ctx->last_ms : 0.f; }
 
+vsk_status vsk_last_screen_redo(const vsk_ctx *ctx, int32_t tier, int64_t *out,
+                                int64_t cap, int64_t *count) {
+  if (!ctx || !count || (tier != 1 && tier != 2) || cap < 0 || (cap > 0 && !out))
+    return VSK_ERR_INVALID_ARGUMENT;
+  const auto &rec = ctx->screen_redo[tier - 1];
+  *count = (int64_t)rec.size();
+  const int64_t m = cap < *count ? cap : *count;
+  for (int64_t i = 0; i < m; ++i) out[i] = rec[(size_t)i];
+  return VSK_OK;
+}
+
 vsk_status vsk_device_info(vsk_ctx *ctx, vsk_caps *caps) {
   VSK_API_BEGIN(ctx);
   VSK_REQUIRE(caps, VSK_ERR_INVALID_ARGUMENT, "caps is null");
@@ -472,7 +509,7 @@ vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
   copy_rows(ctx, db->x.p, sizeof(float) * db->ld, x, sizeof(float) * d,
             sizeof(float) * d, n);
   if (flags & VSK_DB_NORMALIZE) {
-    k_normalize_rows<<<(unsigned)ceil_div(n, 4), 256, 0, ctx->stream>>>(
+    k_normalize_rows<<<(unsigned)ceil_div(n, 256), 256, 0, ctx->stream>>>(
         db->x.as<float>(), n, d, db->ld);
     check_launch("normalize_rows");
   }

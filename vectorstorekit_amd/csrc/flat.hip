@@ -547,6 +547,7 @@ vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
   VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
               "too many queries");
   CallScope cs(ctx);
+  for (auto &rec : ctx->screen_redo) rec.clear();
   const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("flat.best", sizeof(uint64_t) * (size_t)nq * k));

@@ -334,11 +334,17 @@ static std::vector<int32_t> screen_tier(vsk_ctx *ctx, const vsk_db *db,
   return idx;
 }
 
-// queries idx of qbat, gathered; results scattered back into best (stride k)
+// queries idx of qbat, gathered; results scattered back into best (stride k).
+// gidx[i] is the call-wide index of query i of qbat (recorded per tier).
 static void redo_queries(vsk_ctx *ctx, const vsk_db *db, const float *qbat,
                          const std::vector<int32_t> &idx, int32_t k,
-                         int32_t metric, uint64_t *best, bool exact_scan) {
+                         int32_t metric, uint64_t *best, bool exact_scan,
+                         const std::vector<int64_t> &gidx) {
   const int64_t m = (int64_t)idx.size();
+  std::vector<int64_t> sub((size_t)m);
+  for (int64_t i = 0; i < m; ++i) sub[(size_t)i] = gidx[(size_t)idx[(size_t)i]];
+  auto &rec = ctx->screen_redo[exact_scan ? 1 : 0];
+  rec.insert(rec.end(), sub.begin(), sub.end());
   // profiled as one "launch" whose work counter is the number of queries
   KernelTimer tf(ctx, exact_scan ? "screen_fallback" : "screen_retry", (double)m);
   const char *tag = exact_scan ? ".x" : ".r";
@@ -362,7 +368,7 @@ static void redo_queries(vsk_ctx *ctx, const vsk_db *db, const float *qbat,
     std::vector<int32_t> again =
         screen_tier(ctx, db, q2, m, k, VSK_MAX_K, metric, best2, ".r");
     if (!again.empty())
-      redo_queries(ctx, db, q2, again, k, metric, best2, true);
+      redo_queries(ctx, db, q2, again, k, metric, best2, true, sub);
   }
   k_scatter_keys<<<grid_for(m * k), 256, 0, ctx->stream>>>(best2, m, k, didx, best);
   check_launch("screen_scatter");
@@ -745,9 +751,12 @@ void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
     std::vector<int32_t> fail =
         screen_tier(ctx, db, qbat, nb, k, kc, metric, best + b0 * k, "");
     if (fail.empty()) continue;
+    std::vector<int64_t> gidx((size_t)nb);
+    for (int64_t i = 0; i < nb; ++i) gidx[(size_t)i] = b0 + i;
     redo_queries(ctx, db, qbat, fail, k, metric, best + b0 * k,
-                 kc >= VSK_MAX_K);
+                 kc >= VSK_MAX_K, gidx);
   }
+  for (auto &rec : ctx->screen_redo) std::sort(rec.begin(), rec.end());
 }
 
 }  // namespace vsk

@@ -83,6 +83,11 @@ struct vsk_ctx {
   bool flat_no_screen = false;
   bool flat_force_screen = false;
 
+  // queries the last vsk_search_flat redid in the screen's fallback tiers
+  // (indices into that call's queries, ascending): [0] the wider screen,
+  // [1] the exact scan over every row
+  std::vector<int64_t> screen_redo[2];
+
   // profiling
   bool profile = false;
   struct Pending {

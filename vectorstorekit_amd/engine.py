@@ -98,6 +98,17 @@ class Context:
     def last_kernel_ms(self) -> float:
         return float(self.lib.vsk_last_kernel_ms(self.handle))
 
+    def last_screen_redo(self, tier: int) -> np.ndarray:
+        """Query indices the last flat search redid in the screen's tier 1
+        (wider screen) or tier 2 (exact scan over every row)."""
+        cnt = ctypes.c_int64()
+        self.check(self.lib.vsk_last_screen_redo(self.handle, tier, None, 0, ctypes.byref(cnt)))
+        out = np.empty(cnt.value, np.int64)
+        if cnt.value:
+            self.check(self.lib.vsk_last_screen_redo(self.handle, tier, out.ctypes.data,
+                                                     cnt.value, ctypes.byref(cnt)))
+        return out
+
     def capabilities(self) -> dict:
         caps = _lib.vsk_caps()
         self.check(self.lib.vsk_device_info(self.handle, ctypes.byref(caps)))
