@@ -1,12 +1,16 @@
 """Benchmark of the search hot path on one MI355X.
 
-Default workload (the headline metric): flat cosine search,
-1,000,000 x 768 fp32 rows (i.i.d. N(0,1), each L2-normalised), 10,000
-queries drawn the same way, k = 100, distance 1 - q.x.  One step = one
-vsk_search_flat call over all 10,000 queries with the database and the
-queries already in HBM.
+The default run measures all five BASELINE configs, one after the other, and
+prints ONE JSON line: the headline at the top level and
+configs 1, 3, 4 and 5 under "configs", each with its own value, roofline,
+host-buffer rate, CPU baseline and exact-oracle check.
 
-The other BASELINE configs are measured with ``--config``:
+Headline workload: flat cosine search, 1,000,000 x 768
+fp32 rows (i.i.d. N(0,1), each L2-normalised), 10,000 queries drawn the same
+way, k = 100, distance 1 - q.x.  One step = one vsk_search_flat call over all
+10,000 queries with the database and the queries already in HBM.
+
+The configs (also runnable alone with ``--config``):
 
 * ``c1`` flat L2^2, 10,000 x 128, 100 queries, k = 10 (latency-bound);
 * ``c3`` IVF-Flat L2, 1M x 128 from a 4,096-Gaussian mixture, nlist 4096,
@@ -20,17 +24,20 @@ The other BASELINE configs are measured with ``--config``:
 * ``c4bin`` binary quantization of config 4's data (10M x 128 -> 16-byte
   codes), 1,000 queries, Hamming top-100 (vsk_bin_search).
 
-Each prints one JSON line: QPS (value), the roofline of the dominant kernel
-(algorithmic FLOP/OP or bytes per (query, row) pair the library counted for
-that kernel's launches, over its HIP-event time on the library's stream), and
-a CPU baseline (the oracle on this host's cores over the first queries of the
-same workload, plus the agreement of the GPU's ids with the CPU's there).
-``traffic`` is the kernel's HBM bytes per launch read from
-profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes, scaled by
-a plain-copy calibration) when that file holds an entry for this kernel and
-workload, else null.
+Per config: QPS (value, inputs and outputs resident in HBM), the roofline of
+the dominant kernel (algorithmic FLOP/OP or bytes per (query, row) pair the
+library counted for that kernel's launches, over its HIP-event time on the
+library's stream), the same call on host buffers (``host_io_inclusive``, the
+PCIe-inclusive rate, never the value), and a CPU baseline: the oracle on this
+host's cores over the first queries of the same workload, its CPU model,
+and the GPU's results on those queries checked against it bit for bit
+(``exact_oracle_check``).  ``traffic`` is the kernel's HBM bytes per launch
+looked up in profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE
+passes, scaled by a plain-copy calibration; ``traffic_source`` names the
+commit) when that file holds an entry for this kernel and workload, else null.
 
-    python bench.py [--config c2] [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py [--config all|c1..c5|...] [--steps K] [--warmup W] [--gpus 1]
+                    [--no-cpu] [--no-host-io]
 """
 import argparse
 import json
@@ -50,18 +57,26 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
 PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
-                 "c3train": (2, 1), "c4bin": (5, 1), "c3sq8": (5, 1), "c3pq": (5, 1)}
+                 "c3train": (2, 1), "c4bin": (5, 1), "c3sq8": (5, 1), "c3pq": (5, 1),
+                 "all": (20, 5)}
+# the BASELINE configs the default run measures; the first is the headline
+BASELINE_CONFIGS = ("c2", "c1", "c3", "c4", "c5")
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=sorted(DEFAULT_STEPS))
+    p.add_argument("--config", default="all", choices=sorted(DEFAULT_STEPS),
+                   help="all (default): the five BASELINE configs, config 2 as the "
+                        "headline and the others under 'configs'")
     p.add_argument("--steps", type=int, default=None)
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--cpu-seconds", type=float, default=15.0,
-                   help="target length of the CPU baseline sample")
+    p.add_argument("--no-host-io", action="store_true",
+                   help="skip the host-buffer (PCIe-inclusive) timing")
+    p.add_argument("--cpu-seconds", type=float, default=None,
+                   help="target length of each CPU baseline sample (default 15 s, 8 s "
+                        "per config for --config all)")
     p.add_argument("--kmeans-init", default="random", choices=["random", "kmeans++"],
                    help="c3train: the seeding (random rows or k-means++ on the device)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -71,7 +86,30 @@ def parse():
     s, w = DEFAULT_STEPS[a.config]
     a.steps = s if a.steps is None else a.steps
     a.warmup = w if a.warmup is None else a.warmup
+    if a.cpu_seconds is None:
+        a.cpu_seconds = 8.0 if a.config == "all" else 15.0
     return a
+
+
+def cpu_model():
+    """The host CPU as /proc/cpuinfo names it (vendor, family, model)."""
+    info = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" in line:
+                    k, v = (t.strip() for t in line.split(":", 1))
+                    info.setdefault(k, v)
+                if not line.strip() and info:
+                    break
+    except OSError:
+        return "unknown"
+    return (f"{info.get('model name', 'unknown')} ({info.get('vendor_id', '?')}, family "
+            f"{info.get('cpu family', '?')}, model {info.get('model', '?')})")
+
+
+def progress(msg):
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def copy_calibration(mib):
@@ -159,9 +197,22 @@ def gen_mixture(n, d, ncent, nq, dev, jitter=True):
     return x, q, c
 
 
-def setup(a, ctx, dev):
-    """Builds the resident index for the config; returns (spec, step,
-    cpu_leg) where cpu_leg(target_s) gives (baseline dict, agreement)."""
+def exact_check(gd, gi, od, oi, m):
+    """The GPU's first m results against the oracle's, bit for bit."""
+    import numpy as np
+
+    gd, gi = np.asarray(gd)[:m], np.asarray(gi)[:m]
+    same_d = gd.view(np.uint32) == np.asarray(od).view(np.uint32) if gd.dtype == np.float32 \
+        else gd == np.asarray(od)
+    return {"queries": int(m), "ids_equal": bool((gi == np.asarray(oi)).all()),
+            "distances_bitwise_equal": bool(same_d.all())}
+
+
+def setup(c, a, ctx, dev):
+    """Builds the resident index for config c; returns (spec, step, cpu_leg,
+    host_step): cpu_leg(target_s) gives (baseline dict, agreement), and
+    host_step (or None) runs the same call on host buffers (queries read
+    from and results written to host memory, the PCIe-inclusive case)."""
     import numpy as np
     import torch
 
@@ -170,7 +221,6 @@ def setup(a, ctx, dev):
                                     ScalarQuantizer, SQ8Database, VectorDatabase)
 
     lib = ctx.lib
-    c = a.config
     if c in ("c1", "c2"):
         n, d, nq, k = (10_000, 128, 100, 10) if c == "c1" else (1_000_000, 768, 10_000, 100)
         metric = L.METRIC_L2SQ if c == "c1" else L.METRIC_COSINE_NORMALIZED
@@ -183,26 +233,31 @@ def setup(a, ctx, dev):
             ctx.check(lib.vsk_search_flat(ctx.handle, db.handle, q.data_ptr(), nq, k, metric,
                                           dist.data_ptr(), ids.data_ptr()))
 
+        qhost = q.cpu().numpy()
+        hd, hi = np.empty((nq, k), np.float32), np.empty((nq, k), np.int64)
+
+        def host_step():
+            ctx.check(lib.vsk_search_flat(ctx.handle, db.handle, qhost.ctypes.data, nq, k,
+                                          metric, hd.ctypes.data, hi.ctypes.data))
+
         def cpu_leg(target_s):
             from oracle import oracle as O
-            xh, qh = x.cpu().numpy(), q.cpu().numpy()
+            qh = qhost
             th = host_threads()
+            # the exact restatement (dimension-order sums, rows side by side
+            # in SIMD lanes) over its resident database: the timed port is
+            # also the parity check
+            cdb = O.FlatDB(x.cpu().numpy(), threads=th)
             qps, m, reps, el, (od, oi) = cpu_sample(
-                lambda m: O.search_flat(qh[:m], xh, k, metric, threads=th, fast=True),
-                nq, target_s, th)
-            # the timed port sums in 16 lanes like a SIMD loop; parity is
-            # against the exact (dimension-order) oracle, on a small sample
-            me = min(16, nq)
-            ed, ei = O.search_flat(qh[:me], xh, k, metric, threads=th, fast=False)
-            gd, gi = dist.cpu().numpy()[:me], ids.cpu().numpy()[:me]
-            exact = {"queries": me, "ids_equal": bool((gi == ei).all()),
-                     "distances_bitwise_equal": bool((gd.view(np.uint32) ==
-                                                      ed.view(np.uint32)).all())}
+                lambda m: cdb.search(qh[:m], k, metric, threads=th), nq, target_s, th)
+            del cdb
+            gd, gi = dist.cpu().numpy(), ids.cpu().numpy()
             return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "cpu": cpu_model(),
                      "sample": f"first {m} of {nq} queries against all {n} rows, "
-                               f"{reps} pass(es) ({el:.1f} s); timed with 16-lane sums",
-                     "exact_oracle_check": exact},
-                    id_agreement(ids.cpu().numpy()[:m], oi))
+                               f"{reps} pass(es) ({el:.1f} s), exact dimension-order sums",
+                     "exact_oracle_check": exact_check(gd, gi, od, oi, m)},
+                    id_agreement(gi[:m], oi))
 
         spec = {
             "metric": ("QPS @k=100, 1M x 768 fp32 flat cosine" if c == "c2"
@@ -225,7 +280,7 @@ def setup(a, ctx, dev):
                         ("flat_mfma_dense", "k_flat_mfma<DENSE>", "mfma32")],
             "keep": (db, x, q, dist, ids),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, host_step
 
     if c == "c3train":
         # IVF coarse training at config 3's scale: one step = one vsk_kmeans
@@ -265,7 +320,7 @@ def setup(a, ctx, dev):
                              threads=th)
             el = time.perf_counter() - t0
             return ({"value": m * 2 / el, "unit": "row-iterations/s", "cores": th,
-                     "kind": "port",
+                     "kind": "port", "cpu": cpu_model(),
                      "sample": f"first {m} of {n} rows, 2 Lloyd iterations against "
                                f"{ncent} centroids ({el:.1f} s)"}, 1.0)
 
@@ -287,7 +342,7 @@ def setup(a, ctx, dev):
                          "row)", "mfma_bf16")],
             "keep": (x, cent, assign),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, None
 
     if c == "c4bin":
         # binary quantization of config 4's data (one bit per dimension,
@@ -316,6 +371,7 @@ def setup(a, ctx, dev):
             exact = {"queries": m, "ids_equal": bool((gi == oi).all()),
                      "distances_equal": bool((gd == od).all())}
             return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "cpu": cpu_model(),
                      "sample": f"first {m} of {nq} queries against all {n} codes, {reps} "
                                f"pass(es) ({el:.1f} s)", "exact_oracle_check": exact},
                     id_agreement(gi, oi))
@@ -334,7 +390,7 @@ def setup(a, ctx, dev):
                         ("bin_hamming_dense", "k_bin_scan<4, DENSE> (popcount)", "valu_bin")],
             "keep": (db, xc, qc, dist, ids),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, None
 
     if c == "c3":
         n, d, ncent, nq, nprobe, k = 1_000_000, 128, 4096, 10_000, 32, 10
@@ -350,20 +406,30 @@ def setup(a, ctx, dev):
             ctx.check(lib.vsk_ivf_search(ctx.handle, idx.handle, q.data_ptr(), nq, nprobe, k,
                                          L.METRIC_L2, dist.data_ptr(), ids.data_ptr()))
 
+        qhost = q.cpu().numpy()
+        hd, hi = np.empty((nq, k), np.float32), np.empty((nq, k), np.int64)
+
+        def host_step():
+            ctx.check(lib.vsk_ivf_search(ctx.handle, idx.handle, qhost.ctypes.data, nq, nprobe,
+                                         k, L.METRIC_L2, hd.ctypes.data, hi.ctypes.data))
+
         def cpu_leg(target_s):
             from oracle import oracle as O
-            xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), idx.getCentroids()
+            xh, qh, ch = x.cpu().numpy(), qhost, idx.getCentroids()
             lists = idx.assign(x).cpu().numpy()
             rid = np.arange(n, dtype=np.int64)
             th = host_threads()
             qps, m, reps, el, (od, oi) = cpu_sample(
                 lambda m: O.ivf_search(qh[:m], xh, rid, lists, ch, nprobe, k, threads=th),
                 nq, target_s, th)
+            gd, gi = dist.cpu().numpy(), ids.cpu().numpy()
             return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "cpu": cpu_model(),
                      "sample": f"first {m} of {nq} queries, probe + scan of 32 lists "
                                f"(index built from the GPU's assignment; list build inside "
-                               f"each oracle call), {reps} pass(es) ({el:.1f} s)"},
-                    id_agreement(ids.cpu().numpy()[:m], oi))
+                               f"each oracle call), {reps} pass(es) ({el:.1f} s)",
+                     "exact_oracle_check": exact_check(gd, gi, od, oi, m)},
+                    id_agreement(gi[:m], oi))
 
         spec = {
             "metric": "QPS @k=10, IVF-Flat L2 1M x 128, nlist 4096, nprobe 32",
@@ -377,7 +443,7 @@ def setup(a, ctx, dev):
             "kernels": [("ivf_list_scan", "k_list_scan<16>", "valu")],
             "keep": (idx, x, q, dist, ids),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, host_step
 
     if c in ("c3sq8", "c3pq"):
         # config 3's index with quantized lists: the same probing, the
@@ -429,6 +495,7 @@ def setup(a, ctx, dev):
                 run = lambda m: O.ivf_pq_search(qh[:m], cb, codes, rid, lists, ch, nprobe, k)
             qps, m, reps, el, (od, oi) = cpu_sample(run, nq, target_s, 1)
             return ({"value": qps, "unit": "queries/s", "cores": 1, "kind": "port",
+                     "cpu": cpu_model(),
                      "sample": f"first {m} of {nq} queries, probe + scan of 32 lists' codes "
                                f"(numpy over the oracle's probe; codes encoded outside the "
                                f"timing), {reps} pass(es) ({el:.1f} s)"},
@@ -452,7 +519,7 @@ def setup(a, ctx, dev):
                        else [("ivf_pq_list_scan", "k_list_scan_pq_q (one workgroup per query)", "lds_pq")],
             "keep": (idx, x, q, ids, sq if sq8 else pq),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, None
 
     if c == "c4":
         n, d, nq, k = 10_000_000, 128, 1000, 100
@@ -470,16 +537,26 @@ def setup(a, ctx, dev):
             ctx.check(lib.vsk_sq8_search(ctx.handle, db.handle, qc.data_ptr(), nq, k,
                                          score.data_ptr(), ids.data_ptr()))
 
+        qhost = qc.cpu().numpy()
+        hs, hi = np.empty((nq, k), np.int32), np.empty((nq, k), np.int64)
+
+        def host_step():
+            ctx.check(lib.vsk_sq8_search(ctx.handle, db.handle, qhost.ctypes.data, nq, k,
+                                         hs.ctypes.data, hi.ctypes.data))
+
         def cpu_leg(target_s):
             from oracle import oracle as O
-            ch, qh = codes.cpu().numpy(), qc.cpu().numpy()
+            ch, qh = codes.cpu().numpy(), qhost
             th = host_threads()
             qps, m, reps, el, (os_, oi) = cpu_sample(
                 lambda m: O.sq8_search(qh[:m], ch, k, threads=th), nq, target_s, th)
+            gs, gi = score.cpu().numpy(), ids.cpu().numpy()
             return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                     "cpu": cpu_model(),
                      "sample": f"first {m} of {nq} queries against all {n} codes, "
-                               f"{reps} pass(es) ({el:.1f} s)"},
-                    id_agreement(ids.cpu().numpy()[:m], oi))
+                               f"{reps} pass(es) ({el:.1f} s)",
+                     "exact_oracle_check": exact_check(gs, gi, os_, oi, m)},
+                    id_agreement(gi[:m], oi))
 
         spec = {
             "metric": "QPS @k=100, int8 SQ dot scan 10M x 128",
@@ -493,7 +570,7 @@ def setup(a, ctx, dev):
                         ("sq8_mfma_dense", "k_sq8_reg<DENSE> (int8 MFMA 16x16x64)", "int8")],
             "keep": (db, codes, qc, score, ids),
         }
-        return spec, step, cpu_leg
+        return spec, step, cpu_leg, host_step
 
     # c5
     n, d, nq, M, ksub, k_adc, k = 10_000_000, 128, 1000, 16, 256, 1000, 100
@@ -510,17 +587,27 @@ def setup(a, ctx, dev):
         ctx.check(lib.vsk_pq_search(ctx.handle, pq.handle, q.data_ptr(), nq, k_adc, k, l1,
                                     db.handle, dist.data_ptr(), ids.data_ptr()))
 
+    qhost = q.cpu().numpy()
+    hd, hi = np.empty((nq, k), np.float32), np.empty((nq, k), np.int64)
+
+    def host_step():
+        ctx.check(lib.vsk_pq_search(ctx.handle, pq.handle, qhost.ctypes.data, nq, k_adc, k, l1,
+                                    db.handle, hd.ctypes.data, hi.ctypes.data))
+
     def cpu_leg(target_s):
         from oracle import oracle as O
-        xh, qh, ch = x.cpu().numpy(), q.cpu().numpy(), codes.cpu().numpy()
+        xh, qh, ch = x.cpu().numpy(), qhost, codes.cpu().numpy()
         th = host_threads()
         qps, m, reps, el, (od, oi) = cpu_sample(
             lambda m: O.pq_search(qh[:m], pq.codebooks, ch, k_adc, k, x=xh, rerank_metric=l1,
                                   threads=th), nq, target_s, th)
+        gd, gi = dist.cpu().numpy(), ids.cpu().numpy()
         return ({"value": qps, "unit": "queries/s", "cores": th, "kind": "port",
+                 "cpu": cpu_model(),
                  "sample": f"first {m} of {nq} queries: ADC over all {n} codes, top-1000, "
-                           f"L1 re-rank, {reps} pass(es) ({el:.1f} s)"},
-                id_agreement(ids.cpu().numpy()[:m], oi))
+                           f"L1 re-rank, {reps} pass(es) ({el:.1f} s)",
+                 "exact_oracle_check": exact_check(gd, gi, od, oi, m)},
+                id_agreement(gi[:m], oi))
 
     spec = {
         "metric": "QPS @k=100, PQ M16x256 ADC 10M x 128, top-1000 L1 re-rank",
@@ -535,7 +622,7 @@ def setup(a, ctx, dev):
                     ("pq_adc_dense", "k_pq_adc16<DENSE> (8 queries per workgroup)", "lds_pq")],
         "keep": (pq, db, x, q, codes, dist, ids),
     }
-    return spec, step, cpu_leg
+    return spec, step, cpu_leg, host_step
 
 
 # ----------------------------------------------------------------- roofline
@@ -673,48 +760,44 @@ def roofline(spec, stats):
                   # per CU at 2.4 GHz bound the conflict-free rate
                   "lds_lookup_peak_per_s": PEAK_LDS_LOOKUPS,
                   "lds_lookup_frac": round(M * pairs / sec / PEAK_LDS_LOOKUPS, 4)})
-    r["traffic"] = traffic_for(key, spec["workload"])
+    r["traffic"], r["traffic_source"] = traffic_for(key, spec["workload"])
     return r
 
 
 def traffic_for(kernel_key, workload):
-    """HBM bytes per launch of this kernel on this workload, from the
-    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, else None."""
+    """HBM bytes per launch of this kernel on this workload, looked up in the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (not measured by this
+    run), and where it came from; (None, None) when the summary has no entry."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            rows = json.load(f)["entries"]
+            doc = json.load(f)
+        rows = doc["entries"]
     except (OSError, ValueError, KeyError):
-        return None
+        return None, None
     tag = workload.split(" ")[0]
     for e in rows:
         if e.get("kernel") == kernel_key and e.get("workload") == tag:
-            return e.get("traffic_bytes_per_launch")
-    return None
+            src = ("profiles/hbm_traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes "
+                   f"at commit {e.get('commit', doc.get('commit', 'unrecorded'))}, scaled by "
+                   "the plain-copy calibration; a lookup, not a counter of this run")
+            return e.get("traffic_bytes_per_launch"), src
+    return None, None
 
 
 # --------------------------------------------------------------------- main
 
-def main():
-    a = parse()
-    if a.copy_calibration:
-        copy_calibration(a.copy_calibration)
-        return
-    if a.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding "
-                          "is design-only (rows split across GPUs, one merge of k results)",
-                          "n_gpus": a.gpus}))
-        sys.exit(2)
+def measure(c, a, ctx, dev):
+    """One configuration: build, W warm-up steps, K timed steps with inputs
+    and outputs in HBM (the value), then the host-buffer timing and the CPU
+    baseline.  Returns the JSON object of that configuration."""
     import torch
 
-    from vectorstorekit_amd import Context
-
-    dev = torch.device("cuda:0")
-    ctx = Context(0)
     t0 = time.perf_counter()
-    spec, step, cpu_leg = setup(a, ctx, dev)
+    spec, step, cpu_leg, host_step = setup(c, a, ctx, dev)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
+    progress(f"{c}: setup {build_s:.1f} s")
 
     for _ in range(a.warmup):
         step()
@@ -729,6 +812,7 @@ def main():
     el = time.perf_counter() - t0
     stats = ctx.profile_stats()
     ctx.profile(False)
+    progress(f"{c}: {a.steps} steps in {el * 1e3:.1f} ms")
 
     nq, n = spec["nq"], spec["n"]
     qps = spec.get("units_per_step", nq) * a.steps / el
@@ -739,7 +823,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(el * 1e3 / a.steps, 3),
+        "ms_per_step": round(el * 1e3 / a.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -752,14 +836,68 @@ def main():
         "kernels": {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
                     for k, v in stats.items()},
     }
+    if host_step is not None and not a.no_host_io:
+        # queries read from and results written to pageable host memory:
+        # the library stages them through device buffers (PCIe both ways)
+        host_step()
+        torch.cuda.synchronize()
+        reps = max(1, min(a.steps, 10))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            host_step()
+        torch.cuda.synchronize()
+        hel = time.perf_counter() - t0
+        out["host_io_inclusive"] = {
+            "value": round(spec.get("units_per_step", nq) * reps / hel, 1),
+            "unit": out["unit"], "steps": reps, "ms_per_step": round(hel * 1e3 / reps, 4),
+            "note": "same call with host query and result buffers (H2D + D2H inside the "
+                    "timed region); not the value basis"}
     if not a.no_cpu:
         base, agree = cpu_leg(a.cpu_seconds)
         out["cpu_baseline"] = base
         out["ids_agreement_vs_cpu"] = round(agree, 5)
+        progress(f"{c}: cpu baseline {base['value']:.1f} {base['unit']}")
     else:
         out["cpu_baseline"] = None
+    del spec, step, cpu_leg, host_step
+    return out
+
+
+def main():
+    a = parse()
+    if a.copy_calibration:
+        copy_calibration(a.copy_calibration)
+        return
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding "
+                          "is design-only (rows split across GPUs, one merge of k results)",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    import gc
+
+    import torch
+
+    from vectorstorekit_amd import Context
+
+    dev = torch.device("cuda:0")
+    ctx = Context(0)
+    if a.config != "all":
+        out = measure(a.config, a, ctx, dev)
+    else:
+        # the headline (config 2) at the top level, the other BASELINE
+        # configs under "configs", each measured the same way
+        out = None
+        others = {}
+        for c in BASELINE_CONFIGS:
+            r = measure(c, a, ctx, dev)
+            gc.collect()
+            torch.cuda.empty_cache()
+            if out is None:
+                out = r
+            else:
+                others[c] = r
+        out["configs"] = others
     print(json.dumps(out), flush=True)
-    del spec
     ctx.close()
 
 

@@ -43,6 +43,9 @@ def lib():
             "vsko_search_flat": (None, [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P, P,
                                         c_int32, c_int32]),
             "vsko_topk": (None, [P, c_int64, c_int32, P, P]),
+            "vsko_flat_prepare": (c_void_p, [P, c_int64, c_int32, c_int32]),
+            "vsko_flat_free": (None, [P]),
+            "vsko_flat_search": (None, [P, P, c_int64, c_int32, c_int32, P, P, c_int32]),
             "vsko_ivf_assign": (None, [P, c_int64, P, c_int32, c_int32, P, c_int32]),
             "vsko_ivf_probe": (None, [P, c_int64, P, c_int32, c_int32, c_int32, P, c_int32]),
             "vsko_ivf_search": (None, [P, c_int64, P, P, P, c_int64, c_int32, P, c_int32,
@@ -121,6 +124,30 @@ def search_flat(q, x, k, metric, threads=0, fast=False):
     lib().vsko_search_flat(qp, nq, xp, x.shape[0], x.shape[1], k, metric, od.ctypes.data,
                            oi.ctypes.data, threads, 1 if fast else 0)
     return od, oi
+
+
+class FlatDB:
+    """A database prepared once for repeated exact searches (the CPU
+    baseline's resident index); same results as search_flat."""
+
+    def __init__(self, x, threads=0):
+        self.x, xp = _c(x, np.float32)
+        self.d = self.x.shape[1]
+        self.h = lib().vsko_flat_prepare(xp, self.x.shape[0], self.d, threads)
+
+    def search(self, q, k, metric, threads=0):
+        q, qp = _c(q, np.float32)
+        nq = q.shape[0]
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.int64)
+        lib().vsko_flat_search(self.h, qp, nq, k, metric, od.ctypes.data, oi.ctypes.data,
+                               threads)
+        return od, oi
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().vsko_flat_free(self.h)
+            self.h = None
 
 
 def topk(dist, k):

@@ -500,6 +500,42 @@ static void flatv_range(void *p, int64_t lo, int64_t hi) {
   free(heaps);
 }
 
+/* A database in the row-vectorised layout (and its row norms), made once
+ * and searched many times, as a CPU index keeps its rows resident. */
+struct vsko_flatdb {
+  int64_t n;
+  int32_t d;
+  float *xt, *xnorm;
+};
+
+vsko_flatdb *vsko_flat_prepare(const float *x, int64_t n, int32_t d, int32_t nthreads) {
+  if (n <= 0 || d <= 0) return NULL;
+  vsko_flatdb *db = (vsko_flatdb *)malloc(sizeof(vsko_flatdb));
+  const int64_t nblocks = (n + RB - 1) / RB;
+  db->n = n;
+  db->d = d;
+  db->xt = (float *)aligned_alloc(64, sizeof(float) * (size_t)nblocks * d * RB);
+  db->xnorm = (float *)malloc(sizeof(float) * (size_t)n);
+  xt_ctx tc = {x, n, d, db->xt, db->xnorm};
+  parallel_for(nblocks, nthreads, xt_range, &tc);
+  return db;
+}
+
+void vsko_flat_free(vsko_flatdb *db) {
+  if (!db) return;
+  free(db->xt);
+  free(db->xnorm);
+  free(db);
+}
+
+/* the exact flat search over a prepared database (not the hamming metric) */
+void vsko_flat_search(const vsko_flatdb *db, const float *q, int64_t nq, int32_t k,
+                      int32_t metric, float *out_dist, int64_t *out_ids, int32_t nthreads) {
+  flatv_ctx c = {q, db->xt, metric == VSKO_COSINE ? db->xnorm : NULL, db->n, db->d, k,
+                 metric, out_dist, out_ids};
+  parallel_for(nq, nthreads, flatv_range, &c);
+}
+
 void vsko_search_flat(const float *q, int64_t nq, const float *x, int64_t n,
                       int32_t d, int32_t k, int32_t metric, float *out_dist,
                       int64_t *out_ids, int32_t nthreads, int32_t fast) {
@@ -508,15 +544,9 @@ void vsko_search_flat(const float *q, int64_t nq, const float *x, int64_t n,
     parallel_for(nq, nthreads, flat_range, &c);
     return;
   }
-  const int64_t nblocks = (n + RB - 1) / RB;
-  float *xt = (float *)aligned_alloc(64, sizeof(float) * (size_t)nblocks * d * RB);
-  float *xnorm = metric == VSKO_COSINE ? (float *)malloc(sizeof(float) * (size_t)n) : NULL;
-  xt_ctx tc = {x, n, d, xt, xnorm};
-  parallel_for(nblocks, nthreads, xt_range, &tc);
-  flatv_ctx c = {q, xt, xnorm, n, d, k, metric, out_dist, out_ids};
-  parallel_for(nq, nthreads, flatv_range, &c);
-  free(xnorm);
-  free(xt);
+  vsko_flatdb *db = vsko_flat_prepare(x, n, d, nthreads);
+  vsko_flat_search(db, q, nq, k, metric, out_dist, out_ids, nthreads);
+  vsko_flat_free(db);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -180,3 +180,17 @@ def test_normalize_pinned():
     # unit length within rounding
     x = rng.standard_normal((100, 128)).astype(np.float32)
     assert np.allclose(np.linalg.norm(O.normalize(x).astype(np.float64), axis=1), 1.0, atol=1e-6)
+
+
+def test_prepared_db_equals_search_flat():
+    """O.FlatDB (the CPU baseline's resident index) returns search_flat's
+    results bit for bit for every metric it serves."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3000, 45)).astype(np.float32)
+    q = rng.standard_normal((11, 45)).astype(np.float32)
+    db = O.FlatDB(x)
+    for metric in (O.L2SQ, O.L2, O.COSINE, O.COSINE_NORMALIZED, O.DOT, O.L1):
+        a = db.search(q, 30, metric)
+        b = O.search_flat(q, x, 30, metric)
+        np.testing.assert_array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
+        np.testing.assert_array_equal(a[1], b[1])
