@@ -264,6 +264,15 @@ vsk_status vsk_sq8_encode(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
 vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t d,
                           int32_t per_dim, const float *scale, const float *offset,
                           float *out);
+/* quantizeVectors(vectors:scheme: .scalar(bits:)) of MetalAccelerationEngine
+ * (Acceleration/MetalAccelerationEngine.swift:234-262) as its CPU path
+ * computes it (AccelerateOptimizer.scalarQuantize, Acceleration/
+ * AccelerateOptimizer.swift:387-430): per vector, scale = (2^bits - 1) /
+ * (max - min) (1 when max == min) and code_i = UInt8(clamp((x_i - min) *
+ * scale, 0, 255)), truncated toward zero.  codes: n x d uint8; scale, minv:
+ * n floats each (may be NULL; the reference keeps them for dequantisation). */
+vsk_status vsk_scalar_quantize_u8(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                                  int32_t bits, uint8_t *codes, float *scale, float *minv);
 /* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81). */
 vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
                           int32_t d, vsk_sq8 **out);

@@ -39,6 +39,7 @@ def lib():
             "vsko_l1": (c_float, [P, P, c_int32]),
             "vsko_distance": (c_float, [P, P, c_int32, c_int32]),
             "vsko_normalize": (None, [P, c_int64, c_int32, P]),
+            "vsko_scalar_quantize_u8": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
             "vsko_distances": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, c_int32]),
             "vsko_search_flat": (None, [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P, P,
                                         c_int32, c_int32]),
@@ -96,6 +97,19 @@ def distance(q, x, metric) -> float:
     q, qp = _c(q, np.float32)
     x, xp = _c(x, np.float32)
     return float(lib().vsko_distance(qp, xp, q.shape[-1], metric))
+
+
+def scalar_quantize_u8(x, bits=8):
+    """quantizeVectors(.scalar(bits:)) on the reference's CPU path: (codes
+    n x d uint8, scale n, min n)."""
+    x, xp = _c(x, np.float32)
+    n, d = x.shape
+    codes = np.empty((n, d), np.uint8)
+    sc = np.empty(n, np.float32)
+    mn = np.empty(n, np.float32)
+    lib().vsko_scalar_quantize_u8(xp, n, d, bits, codes.ctypes.data, sc.ctypes.data,
+                                  mn.ctypes.data)
+    return codes, sc, mn
 
 
 def normalize(x):

@@ -129,6 +129,35 @@ float vsko_distance(const float *q, const float *x, int32_t d,
   }
 }
 
+/* AccelerateOptimizer.scalarQuantize (Acceleration/AccelerateOptimizer.swift:
+ * 387-430), the CPU path of MetalAccelerationEngine.quantizeVectors(scheme:
+ * .scalar(bits:)): min and max of the vector (vDSP_minv / vDSP_maxv),
+ * scale = Float(1 << bits - 1) / range (Swift's << binds tighter than -, so
+ * 2^bits - 1), or 1 when range == 0; code = UInt8(min(max((v - min) *
+ * scale, 0), 255)), the conversion truncating toward zero. */
+void vsko_scalar_quantize_u8(const float *x, int64_t n, int32_t d, int32_t bits,
+                             uint8_t *codes, float *scale, float *minv) {
+  const float levels = (float)((1 << bits) - 1);
+  for (int64_t r = 0; r < n; ++r) {
+    const float *xr = x + r * d;
+    float mn = xr[0], mx = xr[0];
+    for (int32_t i = 1; i < d; ++i) {
+      if (xr[i] < mn) mn = xr[i];
+      if (xr[i] > mx) mx = xr[i];
+    }
+    const float range = mx - mn;
+    const float s = range > 0.0f ? levels / range : 1.0f;
+    for (int32_t i = 0; i < d; ++i) {
+      float t = (xr[i] - mn) * s;
+      if (t < 0.0f) t = 0.0f;
+      if (t > 255.0f) t = 255.0f;
+      codes[r * d + i] = (uint8_t)t;
+    }
+    if (scale) scale[r] = s;
+    if (minv) minv[r] = mn;
+  }
+}
+
 /* normalizeVectors (Acceleration/Metal/Shaders/DistanceShaders.metal:
  * 403-429): magnitude = sum of x_i * x_i in index order, then
  * sqrt(magnitude) + 1e-8, then every component divided by it (a division,

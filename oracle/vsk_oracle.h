@@ -41,6 +41,10 @@ float vsko_l2sq(const float *a, const float *b, int32_t d);
 float vsko_dot(const float *a, const float *b, int32_t d);
 float vsko_l1(const float *a, const float *b, int32_t d);
 float vsko_distance(const float *q, const float *x, int32_t d, int32_t metric);
+/* quantizeVectors(.scalar(bits)) on the CPU path: per-vector min/max,
+ * uint8 codes truncated; scale/minv per vector (either may be NULL) */
+void vsko_scalar_quantize_u8(const float *x, int64_t n, int32_t d, int32_t bits,
+                             uint8_t *codes, float *scale, float *minv);
 /* normalizeVectors: out = x / (sqrt(sum x^2) + 1e-8) per row */
 void vsko_normalize(const float *x, int64_t n, int32_t d, float *out);
 /* out[i*n + j] = distance(q_i, x_j) */

@@ -1,0 +1,136 @@
+"""The VectorStore.search drop-in: the C calls the Swift HIPIVFIndex /
+HIPIVFIndexingStrategy wrappers make, replayed through ctypes in the same
+order, and their Python twin (vectorstorekit_amd.index), against the oracle.
+
+Swift call sequence (the wrappers):
+  HIPAcceleratorStrategy.initialize()      -> vsk_create
+  capabilities()                           -> vsk_device_info
+  HIPIVFIndex.train(on:)                   -> vsk_kmeans, vsk_ivf_create
+  insert(_:) for each VectorEntry          -> vsk_ivf_add(n = 1, ids = NULL)
+  search(query:k:strategy:filter:)         -> vsk_ivf_search(nq = 1,
+                                              nprobe = nlist for .exact)
+  deinit                                   -> vsk_ivf_free, vsk_destroy
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from vectorstorekit_amd import HIPAcceleratorStrategy, IVFConfiguration
+from vectorstorekit_amd._lib import METRIC_L2, check, load_library, vsk_caps
+from vectorstorekit_amd.clustering import INIT_PLUSPLUS, vsk_kmeans_result
+from vectorstorekit_amd.index import (HIPIVFIndex, HIPIVFIndexingStrategy, SearchStrategy,
+                                      VectorEntry)
+
+pytestmark = pytest.mark.gpu
+
+
+def _data(seed, n=3000, d=24, ncent=16, nq=5):
+    rng = np.random.default_rng(seed)
+    cent = (2.0 * rng.standard_normal((ncent, d))).astype(np.float32)
+    x = (cent[rng.integers(0, ncent, n)] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    q = (cent[rng.integers(0, ncent, nq)] + 0.5 * rng.standard_normal((nq, d))).astype(np.float32)
+    x[17] = x[3]  # an exact tie: the earlier insert ranks first
+    return x, q
+
+
+def test_swift_call_sequence_exact_and_approximate(ctx):
+    lib = load_library()
+    x, q = _data(1)
+    n, d = x.shape
+    nlist, nprobe, k = 16, 3, 7
+    h = ctypes.c_void_p()
+    assert lib.vsk_create(0, ctypes.byref(h)) == 0
+    try:
+        caps = vsk_caps()
+        check(h, lib.vsk_device_info(h, ctypes.byref(caps)))
+        assert caps.arch.decode().startswith("gfx950")
+        # train(on:): k-means (the configuration's seed and k-means++), then
+        # the index over the trained centroids
+        cent = np.empty((nlist, d), np.float32)
+        res = vsk_kmeans_result()
+        check(h, lib.vsk_kmeans(h, x.ctypes.data, n, d, nlist, None, INIT_PLUSPLUS, None,
+                                ctypes.c_uint64(42), 25, ctypes.c_float(1e-4), cent.ctypes.data,
+                                None, ctypes.byref(res)))
+        ivf = ctypes.c_void_p()
+        check(h, lib.vsk_ivf_create(h, cent.ctypes.data, nlist, d, ctypes.byref(ivf)))
+        # insert(_:) one entry at a time, ids = the running row count
+        for i in range(n):
+            check(h, lib.vsk_ivf_add(h, ivf, x[i:i + 1].ctypes.data, None, 1))
+        lists = O.ivf_assign(x, cent)
+        rid = np.arange(n, dtype=np.int64)
+        for qi in range(q.shape[0]):
+            qq = np.ascontiguousarray(q[qi:qi + 1])
+            for strategy, probes in (("exact", nlist), ("approximate", nprobe)):
+                dist = np.empty((1, k), np.float32)
+                ids = np.empty((1, k), np.int64)
+                check(h, lib.vsk_ivf_search(h, ivf, qq.ctypes.data, 1, probes, k, METRIC_L2,
+                                            dist.ctypes.data, ids.ctypes.data))
+                od, oi = O.ivf_search(qq, x, rid, lists, cent, probes, k)
+                np.testing.assert_array_equal(ids, oi)
+                np.testing.assert_array_equal(dist, od)
+                if strategy == "exact":
+                    # .exact probes every list: the flat search's answer
+                    fd, fi = O.search_flat(qq, x, k, O.L2)
+                    np.testing.assert_array_equal(ids, fi)
+                    np.testing.assert_array_equal(dist, fd)
+        # the tie: row 3 before row 17
+        qq = np.ascontiguousarray(x[3:4])
+        dist = np.empty((1, 2), np.float32)
+        ids = np.empty((1, 2), np.int64)
+        check(h, lib.vsk_ivf_search(h, ivf, qq.ctypes.data, 1, nlist, 2, METRIC_L2,
+                                    dist.ctypes.data, ids.ctypes.data))
+        assert list(ids[0]) == [3, 17] and (dist == 0).all()
+        check(h, lib.vsk_ivf_free(h, ivf))
+    finally:
+        lib.vsk_destroy(h)
+
+
+def test_vector_index_twin_results_filter_delete(ctx):
+    """HIPIVFIndex (the twin of the Swift wrapper): SearchResult ids map
+    back to VectorIDs with their metadata; .exact equals the flat search;
+    a filter and deleted rows give the reference's answer (the probed
+    candidates filtered first, then sorted), pinned by the oracle over the
+    remaining rows."""
+    x, q = _data(2)
+    n, d = x.shape
+    acc = HIPAcceleratorStrategy(0)
+    strat = HIPIVFIndexingStrategy(acc, d, numClusters=16, nprobe=4)
+    idx = strat.createIndex()
+    with pytest.raises(Exception):
+        idx.insert(VectorEntry("v0", x[0], {"i": 0}))  # not trained
+    idx.train(x)
+    for i in range(n):
+        r = idx.insert(VectorEntry(f"vec{i}", x[i], {"i": i, "even": i % 2 == 0}))
+        assert r.success
+    assert idx.count == n and idx.contains("vec5")
+    cent = idx.ivf.getCentroids()
+    lists = O.ivf_assign(x, cent)
+    rid = np.arange(n, dtype=np.int64)
+    k = 9
+    for qi in range(q.shape[0]):
+        res = idx.search(q[qi], k, SearchStrategy.exact)
+        fd, fi = O.search_flat(q[qi:qi + 1], x, k, O.L2)
+        assert [r.id for r in res] == [f"vec{i}" for i in fi[0]]
+        assert [r.metadata["i"] for r in res] == list(fi[0])
+        np.testing.assert_array_equal(np.array([r.distance for r in res], np.float32), fd[0])
+        assert all(r.indexAlgorithm == "IVF" for r in res)
+        res = idx.search(q[qi], k, "approximate")
+        od, oi = O.ivf_search(q[qi:qi + 1], x, rid, lists, cent, 4, k)
+        assert [r.id for r in res] == [f"vec{i}" for i in oi[0]]
+    # delete 40 of the exact answer's rows and filter to even rows
+    gone = [int(i) for i in O.search_flat(q[:1], x, 40, O.L2)[1][0]]
+    for i in gone:
+        assert idx.delete(f"vec{i}")
+    assert not idx.delete("vec-missing") and idx.count == n - 40
+    keep = np.array([i % 2 == 0 and i not in set(gone) for i in range(n)])
+    sub = np.flatnonzero(keep)
+    for strategy, probes in ((SearchStrategy.exact, 16), (SearchStrategy.approximate, 4)):
+        res = idx.search(q[0], k, strategy, filter=lambda vid, m: m["even"])
+        od, oi = O.ivf_search(q[:1], x[sub], sub.astype(np.int64), lists[sub], cent, probes, k)
+        want = [f"vec{i}" for i in oi[0] if i >= 0]
+        assert [r.id for r in res] == want
+        np.testing.assert_array_equal(np.array([r.distance for r in res], np.float32),
+                                      od[0][:len(want)])
+    acc.initialize().close()

@@ -194,3 +194,30 @@ def test_prepared_db_equals_search_flat():
         b = O.search_flat(q, x, 30, metric)
         np.testing.assert_array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
         np.testing.assert_array_equal(a[1], b[1])
+
+
+def test_scalar_quantize_u8_pinned():
+    """quantizeVectors(.scalar(bits:)) CPU path (AccelerateOptimizer.swift:
+    387-430): numpy fp32 restatement (two roundings, clamp, truncation);
+    closed forms: a ramp 0..255 maps to itself, a constant vector to all
+    zeros with scale 1; truncation, not rounding (x = min + 0.7/scale gives
+    code 0)."""
+    rng = np.random.default_rng(9)
+    for bits in (8, 4, 1):
+        x = (rng.standard_normal((500, 37)) * rng.uniform(0.1, 50, (500, 1))).astype(np.float32)
+        codes, sc, mn = O.scalar_quantize_u8(x, bits)
+        emn, emx = x.min(axis=1), x.max(axis=1)
+        rng_ = (emx - emn).astype(np.float32)
+        es = np.where(rng_ > 0, np.float32(2 ** bits - 1) / rng_, np.float32(1)).astype(np.float32)
+        t = ((x - emn[:, None]).astype(np.float32) * es[:, None]).astype(np.float32)
+        want = np.clip(t, 0, 255).astype(np.uint8)  # astype truncates toward zero
+        np.testing.assert_array_equal(sc, es)
+        np.testing.assert_array_equal(mn, emn)
+        np.testing.assert_array_equal(codes, want)
+        assert codes.max() <= 2 ** bits - 1
+    ramp = np.arange(256, dtype=np.float32)[None, :]
+    np.testing.assert_array_equal(O.scalar_quantize_u8(ramp)[0][0], np.arange(256))
+    c, s, _ = O.scalar_quantize_u8(np.full((1, 9), 2.5, np.float32))
+    assert (c == 0).all() and s[0] == 1.0
+    x = np.array([[0.0, 0.7, 255.0]], np.float32)
+    assert O.scalar_quantize_u8(x)[0][0, 1] == 0

@@ -10,6 +10,10 @@ from .engine import (  # noqa: F401
     DistanceMetric,
     HIPAccelerationEngine,
     HIPAcceleratorStrategy,
+    QuantizationMetadata,
+    QuantizationParameters,
+    QuantizationScheme,
+    QuantizedVector,
     VectorDatabase,
 )
 from .clustering import (  # noqa: F401,E402

@@ -112,6 +112,7 @@ SIGNATURES = {
     "vsk_ivf_search_pq": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_train": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_encode": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
+    "vsk_scalar_quantize_u8": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
     "vsk_sq8_upload": (c_int32, [P, P, c_int64, c_int32, PP]),
     "vsk_sq8_free": (c_int32, [P, P]),
     "vsk_sq8_search": (c_int32, [P, P, P, c_int64, c_int32, P, P]),

@@ -463,6 +463,47 @@ __global__ void k_sq8_decode(const uint64_t *best, int64_t total,
   }
 }
 
+// quantizeVectors(scheme: .scalar(bits:)) on the CPU path
+// (Acceleration/AccelerateOptimizer.swift:387-430): per vector, min and max
+// of its values, scale = (2^bits - 1) / (max - min) (1 when max == min),
+// code_i = UInt8(min(max((x_i - min) * scale, 0), 255)), the conversion
+// truncating toward zero.  One wave per row; min and max are exact in any
+// order.
+__global__ __launch_bounds__(256) void k_scalar_quantize_u8(const float *x, int64_t n,
+                                                           int32_t d, float levels,
+                                                           uint8_t *codes, float *scale,
+                                                           float *minv) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const float *xr = x + row * d;
+  float mn = __int_as_float(0x7f800000), mx = -__int_as_float(0x7f800000);
+  for (int32_t j = lane; j < d; j += 64) {
+    const float v = xr[j];
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o));
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+  }
+  const float range = mx - mn;
+  const float s = range > 0.0f ? levels / range : 1.0f;
+  uint8_t *cr = codes + row * d;
+  for (int32_t j = lane; j < d; j += 64) {
+    float t = xr[j] - mn;
+    t = t * s;
+    t = fminf(fmaxf(t, 0.0f), 255.0f);
+    cr[j] = (uint8_t)(uint32_t)t;
+  }
+  if (lane == 0) {
+    if (scale) scale[row] = s;
+    if (minv) minv[row] = mn;
+  }
+}
+
 static unsigned grid1(int64_t n) {
   int64_t g = ceil_div(n, 256);
   return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
@@ -652,6 +693,34 @@ vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t 
     check_launch("sq8_dequantize");
   }
   ox.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_scalar_quantize_u8(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
+                                  int32_t bits, uint8_t *codes, float *scale, float *minv) {
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "no vectors");
+  VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(x && codes, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(bits >= 1 && bits <= 8, VSK_ERR_INVALID_ARGUMENT, "bits must be in 1..8");
+  VSK_REQUIRE(n <= 0x7FFFFFFFll * 4, VSK_ERR_INVALID_BUFFER_SIZE, "too many vectors");
+  CallScope cs(ctx);
+  const float *dx = static_cast<const float *>(
+      input_to_device(ctx, x, sizeof(float) * (size_t)n * d, "squ8.x"));
+  OutputStage oc(ctx, codes, (size_t)n * d, "squ8.codes");
+  OutputStage os(ctx, scale, scale ? sizeof(float) * (size_t)n : 0, "squ8.scale");
+  OutputStage om(ctx, minv, minv ? sizeof(float) * (size_t)n : 0, "squ8.min");
+  {
+    KernelTimer t(ctx, "scalar_quantize_u8", (double)n);
+    k_scalar_quantize_u8<<<(unsigned)ceil_div(n, 4), 256, 0, ctx->stream>>>(
+        dx, n, d, (float)((1 << bits) - 1), oc.ptr<uint8_t>(),
+        scale ? os.ptr<float>() : nullptr, minv ? om.ptr<float>() : nullptr);
+    check_launch("scalar_quantize_u8");
+  }
+  oc.copy_back();
+  if (scale) os.copy_back();
+  if (minv) om.copy_back();
   cs.finish();
   VSK_API_END(ctx);
 }

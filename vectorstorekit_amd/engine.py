@@ -58,6 +58,10 @@ _METRIC_CODES = {
 }
 
 
+def _to_host(a):
+    return a.cpu().numpy() if _lib._is_torch(a) else a
+
+
 def metric_code(metric) -> int:
     if isinstance(metric, int):
         return metric
@@ -231,41 +235,185 @@ class HIPAcceleratorStrategy:
         return self.initialize().capabilities()
 
 
+@dataclass(frozen=True)
+class QuantizationScheme:
+    """``QuantizationScheme`` (Core/VectorTypes.swift:474-505): ``kind`` is its
+    raw value ("scalar", "product", "binary", "vector", "learned", "none")."""
+
+    kind: str
+    bits: int = 8
+    segments: int = 0
+
+    @staticmethod
+    def scalar(bits: int = 8) -> "QuantizationScheme":
+        return QuantizationScheme("scalar", bits)
+
+    @staticmethod
+    def product(segments: int, bits: int = 8) -> "QuantizationScheme":
+        return QuantizationScheme("product", bits, segments)
+
+    @staticmethod
+    def binary() -> "QuantizationScheme":
+        return QuantizationScheme("binary", 1)
+
+    @staticmethod
+    def none() -> "QuantizationScheme":
+        return QuantizationScheme("none", 32)
+
+
+@dataclass(frozen=True)
+class QuantizationParameters:
+    """``QuantizationParameters`` (Core/VectorTypes.swift:508-540)."""
+
+    trainingIterations: int = 25
+    useAsymmetricDistance: bool = True
+    useOptimizedLayout: bool = True
+    compressionTarget: float | None = None
+    precision: int = 8
+    centroids: int | None = None
+    subvectors: int | None = None
+    seed: int = 0
+
+
+@dataclass(frozen=True)
+class QuantizationMetadata:
+    scheme: QuantizationScheme
+    originalDimensions: int
+    compressionRatio: float
+
+
+@dataclass(frozen=True)
+class QuantizedVector:
+    """``QuantizedVector`` (Core/VectorTypes.swift:543-580): the codes of one
+    vector and its metadata; ``scale`` / ``minimum`` carry the per-vector
+    parameters of the scalar scheme (the reference computes them and drops
+    them, AccelerateOptimizer.swift:415-419)."""
+
+    codes: bytes
+    metadata: QuantizationMetadata
+    scale: float | None = None
+    minimum: float | None = None
+
+    @property
+    def originalDimensions(self) -> int:
+        return self.metadata.originalDimensions
+
+    @property
+    def scheme(self) -> QuantizationScheme:
+        return self.metadata.scheme
+
+
 class HIPAccelerationEngine:
-    """``MetalAccelerationEngine``'s distance API on the HIP library
-    (Acceleration/MetalAccelerationEngine.swift:76-204).  Candidates may be
-    a ``VectorDatabase`` (resident) or an array uploaded for the call."""
+    """``MetalAccelerationEngine``'s distance and quantization API on the HIP
+    library (Acceleration/MetalAccelerationEngine.swift:76-262).  Candidates
+    may be a ``VectorDatabase`` (resident) or an array uploaded for the call
+    and freed when it returns."""
 
     def __init__(self, device: int | Context = 0):
         self.ctx = device if isinstance(device, Context) else Context(device)
 
-    def _db(self, candidates, metric):
+    def _db(self, candidates):
+        """(database, uploaded_here): the candidates as a resident database."""
         if isinstance(candidates, VectorDatabase):
-            return candidates
+            return candidates, False
         if len(candidates) == 0:
             raise VSKError(-3, "candidates is empty")
         return VectorDatabase(self.ctx, np.asarray(candidates, np.float32)
-                              if not _lib._is_torch(candidates) else candidates)
+                              if not _lib._is_torch(candidates) else candidates), True
+
+    def _with_db(self, candidates, fn):
+        db, temp = self._db(candidates)
+        try:
+            return fn(db)
+        finally:
+            if temp:
+                db.free()
 
     def computeDistances(self, query, candidates, metric="euclidean"):
         """Distances from one query to every candidate (:76-136)."""
         q = np.asarray(query, np.float32).reshape(1, -1) if not _lib._is_torch(query) \
             else query.reshape(1, -1)
-        return self._db(candidates, metric).distances(q, metric)[0]
+        return self._with_db(candidates, lambda db: db.distances(q, metric)[0])
 
     def batchComputeDistances(self, queries, candidates, metric="euclidean", topK=None):
         """Per query: all distances (topK None) or the topK smallest,
         ascending (:139-204)."""
-        db = self._db(candidates, metric)
-        if topK is None:
-            return db.distances(queries, metric)
-        k = min(int(topK), db.n)
-        dist, _ = db.search(queries, k, metric)
-        return dist
+        def run(db):
+            if topK is None:
+                return db.distances(queries, metric)
+            dist, _ = db.search(queries, min(int(topK), db.n), metric)
+            return dist
+
+        return self._with_db(candidates, run)
 
     def search(self, queries, candidates, k: int, metric="euclidean"):
         """Top-k distances and ids."""
-        return self._db(candidates, metric).search(queries, k, metric)
+        return self._with_db(candidates, lambda db: db.search(queries, k, metric))
+
+    def quantizeVectors(self, vectors, scheme: QuantizationScheme,
+                        parameters: QuantizationParameters | None = None):
+        """``quantizeVectors(vectors:scheme:parameters:)`` (:234-262), on the
+        device, with the reference CPU path's semantics
+        (AccelerateOptimizer.quantizeVectors, Acceleration/
+        AccelerateOptimizer.swift:217-247):
+
+        * scalar(bits): per-vector min/max, uint8 codes truncated
+          (``vsk_scalar_quantize_u8``, :387-430);
+        * binary: one bit per dimension, x > 0 (``vsk_binary_encode``,
+          :447-481);
+        * product(segments, bits): codebooks trained by k-means
+          (``parameters.trainingIterations``, 2^bits codewords) and the
+          vectors encoded, one byte per segment (``ProductQuantizer``).  The
+          reference's CPU path is a placeholder that falls back to scalar
+          quantization (:432-445); this is the product quantizer it names;
+        * any other scheme: the raw fp32 bytes (the reference's default
+          branch, :233-245).
+
+        Returns a list of ``QuantizedVector``."""
+        parameters = parameters or QuantizationParameters()
+        x = vectors
+        if not _lib._is_torch(x):
+            x = np.ascontiguousarray(np.asarray(x, np.float32))
+        n, d = int(x.shape[0]), int(x.shape[1])
+        if n == 0:
+            raise VSKError(-3, "no vectors")
+        if scheme.kind == "scalar":
+            xp, xk = as_buffer(x, np.float32, (n, d))
+            codes = np.empty((n, d), np.uint8)
+            sc = np.empty(n, np.float32)
+            mn = np.empty(n, np.float32)
+            self.ctx.check(self.ctx.lib.vsk_scalar_quantize_u8(
+                self.ctx.handle, xp, n, d, scheme.bits, codes.ctypes.data, sc.ctypes.data,
+                mn.ctypes.data))
+            ratio = d * 4.0 / (d + 8)
+            meta = QuantizationMetadata(scheme, d, ratio)
+            return [QuantizedVector(codes[i].tobytes(), meta, float(sc[i]), float(mn[i]))
+                    for i in range(n)]
+        if scheme.kind == "binary":
+            from .quantization import BinaryQuantizer
+
+            codes = np.asarray(_to_host(BinaryQuantizer(self.ctx).quantizeBatch(x)))
+            meta = QuantizationMetadata(scheme, d, d * 4.0 / codes.shape[1])
+            return [QuantizedVector(codes[i].tobytes(), meta) for i in range(n)]
+        if scheme.kind == "product":
+            from .quantization import ProductQuantizer
+
+            M = scheme.segments or parameters.subvectors
+            if not M or d % M:
+                raise VSKError(-2, "product quantization needs segments dividing the dimension")
+            ksub = min(parameters.centroids or (1 << scheme.bits), 256)
+            pq = ProductQuantizer.train(self.ctx, x, M, ksub,
+                                        iterations=parameters.trainingIterations,
+                                        seed=parameters.seed)
+            try:
+                codes = np.asarray(_to_host(pq.encode(x)))
+            finally:
+                pq.free()
+            meta = QuantizationMetadata(scheme, d, d * 4.0 / M)
+            return [QuantizedVector(codes[i].tobytes(), meta) for i in range(n)]
+        raw = np.asarray(_to_host(x), np.float32)
+        meta = QuantizationMetadata(scheme, d, 1.0)
+        return [QuantizedVector(raw[i].tobytes(), meta) for i in range(n)]
 
     def computeDistanceMatrix(self, vectorsA, vectorsB=None, metric="euclidean"):
         """MetalDistanceMatrix.computeDistanceMatrix (Acceleration/Metal/
@@ -276,12 +424,7 @@ class HIPAccelerationEngine:
         opposite orders for (i, j) and (j, i), so only the mirror is exactly
         symmetric."""
         b = vectorsA if vectorsB is None else vectorsB
-        db = self._db(b, metric)
-        try:
-            m = db.distances(vectorsA, metric)
-        finally:
-            if db is not b:
-                db.free()
+        m = self._with_db(b, lambda db: db.distances(vectorsA, metric))
         if vectorsB is None:
             if _lib._is_torch(m):
                 import torch
