@@ -68,6 +68,8 @@ typedef int32_t vsk_status;
 #define VSK_METRIC_DOT 4               /* -q.x                  "dotProduct" */
 #define VSK_METRIC_L1 5                /* sum |q-x|             "manhattan"  */
 #define VSK_METRIC_HAMMING 6           /* count of q_i != x_i   "hamming"    */
+#define VSK_METRIC_COSINE_NOEPS 7      /* 1 - q.x/(|q||x|), HNSW's cosine
+                                          (vsk_hnsw_distances only)          */
 
 #define VSK_MAX_K 1024 /* largest k of any top-k call */
 
@@ -360,6 +362,25 @@ vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcode
  * Metal kernel writes it. */
 vsk_status vsk_bin_distances(vsk_ctx *ctx, const vsk_bin *bin,
                              const uint8_t *qcodes, int64_t nq, float *out);
+
+/* ---- HNSW neighbour distances ---------------------------------------------
+ * The distance evaluations of HNSWIndex's graph walk (greedySearchLayer /
+ * searchLayer0, Indexes/HNSWIndex.swift:1035-1221), batched over many
+ * concurrent searches: for query i, the rows rows[offsets[i] ..
+ * offsets[i+1]) of db (the nodes' vectors; a CSR list of its frontier's
+ * neighbours) get out[j] = DistanceComputer.distance(q_i, x_rows[j])
+ * (:1920-1959): VSK_METRIC_L2 sqrt of SIMD.sum() of the squared differences,
+ * VSK_METRIC_COSINE_NOEPS 1 - dot/(|q||x|) (no epsilon), VSK_METRIC_L1 the
+ * sum of |q_i - x_i|; VSK_METRIC_L2SQ the sum without the sqrt.  Sums run in
+ * dimension order without FMA (SIMD.sum() from -0, reduce(0) from +0), so
+ * the distances equal the reference's bit for bit.  DistanceComputer falls
+ * back to euclidean for the other metrics; other codes return
+ * VSK_ERR_UNSUPPORTED.  offsets: nq + 1 non-decreasing int64 starting at 0;
+ * rows: offsets[nq] int32 row indices of db (an index outside it returns
+ * VSK_ERR_INVALID_ARGUMENT); out: offsets[nq] floats. */
+vsk_status vsk_hnsw_distances(vsk_ctx *ctx, const vsk_db *db, const float *q, int64_t nq,
+                              const int64_t *offsets, const int32_t *rows, int32_t metric,
+                              float *out);
 
 /* ---- k-means -------------------------------------------------------------
  * KMeansClustering.cluster (Clustering/KMeansClustering.swift:48-113), the

@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "libvsk_oracle.so")
 
-L2SQ, L2, COSINE, COSINE_NORMALIZED, DOT, L1, HAMMING = range(7)
+L2SQ, L2, COSINE, COSINE_NORMALIZED, DOT, L1, HAMMING, COSINE_NOEPS = range(8)
 
 _lib = None
 
@@ -39,6 +39,8 @@ def lib():
             "vsko_l1": (c_float, [P, P, c_int32]),
             "vsko_distance": (c_float, [P, P, c_int32, c_int32]),
             "vsko_normalize": (None, [P, c_int64, c_int32, P]),
+            "vsko_hnsw_distance": (c_float, [P, P, c_int32, c_int32]),
+            "vsko_hnsw_distances": (None, [P, c_int64, P, c_int32, P, P, c_int32, P]),
             "vsko_scalar_quantize_u8": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
             "vsko_distances": (None, [P, c_int64, P, c_int64, c_int32, c_int32, P, c_int32]),
             "vsko_search_flat": (None, [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P, P,
@@ -110,6 +112,24 @@ def scalar_quantize_u8(x, bits=8):
     lib().vsko_scalar_quantize_u8(xp, n, d, bits, codes.ctypes.data, sc.ctypes.data,
                                   mn.ctypes.data)
     return codes, sc, mn
+
+
+def hnsw_distance(q, x, metric) -> float:
+    """HNSWIndex DistanceComputer.distance of two vectors."""
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    return float(lib().vsko_hnsw_distance(qp, xp, q.shape[-1], metric))
+
+
+def hnsw_distances(q, x, offsets, rows, metric):
+    """Query i against rows[offsets[i]:offsets[i+1]] of x (CSR)."""
+    q, qp = _c(q, np.float32)
+    x, xp = _c(x, np.float32)
+    off, op = _c(offsets, np.int64)
+    r, rp = _c(rows, np.int32)
+    out = np.empty(int(off[-1]), np.float32)
+    lib().vsko_hnsw_distances(qp, q.shape[0], xp, x.shape[1], op, rp, metric, out.ctypes.data)
+    return out
 
 
 def normalize(x):
@@ -426,3 +446,42 @@ def ivf_pq_search(q, codebooks, codes, ids, list_of, centroids, nprobe, k):
         od[i, :len(order)] = np.sqrt(s[order])
         oi[i, :len(order)] = ids[rows[order]]
     return od, oi
+
+
+def search_layer0(query, x, adjacency, entry, ef, metric, deleted=()):
+    """HNSWIndex.searchLayer0 (Indexes/HNSWIndex.swift:1151-1212) restated
+    in Python over adjacency lists, with DistanceComputer's distances
+    (vsko_hnsw_distance).  The sorts are stable (Python's sort; Swift's
+    sort is stable in its implementation, not by contract).  Returns the
+    ef closest (distance, node) pairs ascending.  Small cases only."""
+    deleted = set(deleted)
+    d0 = hnsw_distance(query, x[entry], metric)
+    visited = {entry}
+    candidates = [(d0, entry)]
+    w = [(d0, entry)]
+    while candidates:
+        candidates.sort(key=lambda t: t[0])
+        cur = candidates.pop(0)
+        if len(w) >= ef:
+            w.sort(key=lambda t: t[0], reverse=True)
+            if cur[0] > w[0][0]:
+                break
+        if cur[1] in deleted:
+            continue
+        for nb in adjacency[cur[1]]:
+            if nb in visited:
+                continue
+            visited.add(nb)
+            if nb in deleted:
+                continue
+            dist = hnsw_distance(query, x[nb], metric)
+            if len(w) < ef:
+                candidates.append((dist, nb))
+                w.append((dist, nb))
+            else:
+                w.sort(key=lambda t: t[0], reverse=True)
+                if dist < w[0][0]:
+                    candidates.append((dist, nb))
+                    w[0] = (dist, nb)
+    w.sort(key=lambda t: t[0])
+    return w

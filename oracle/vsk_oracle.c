@@ -158,6 +158,45 @@ void vsko_scalar_quantize_u8(const float *x, int64_t n, int32_t d, int32_t bits,
   }
 }
 
+/* HNSWIndex's DistanceComputer.distance (Indexes/HNSWIndex.swift:1920-1959).
+ * Swift's SIMD.sum() on floating point adds the lanes in index order starting
+ * from -0.0 (the standard library's generic implementation); reduce(0)
+ * starts from +0.0.
+ *   euclidean: sqrt(((v1 - v2) * (v1 - v2)).sum())
+ *   cosine:    1 - (v1 * v2).sum() / (sqrt((v1*v1).sum()) * sqrt((v2*v2).sum()))
+ *   manhattan: reduce(0) { sum + abs(diff[i]) }
+ * VSKO_L2SQ is the euclidean sum before its sqrt. */
+float vsko_hnsw_distance(const float *q, const float *x, int32_t d, int32_t metric) {
+  if (metric == VSKO_L1) {
+    float s = 0.0f;
+    for (int32_t i = 0; i < d; ++i) s += fabsf(q[i] - x[i]);
+    return s;
+  }
+  if (metric == VSKO_COSINE_NOEPS) {
+    float dot = -0.0f, qq = -0.0f, xx = -0.0f;
+    for (int32_t i = 0; i < d; ++i) dot += q[i] * x[i];
+    for (int32_t i = 0; i < d; ++i) qq += q[i] * q[i];
+    for (int32_t i = 0; i < d; ++i) xx += x[i] * x[i];
+    const float m1 = sqrtf(qq), m2 = sqrtf(xx);
+    return 1.0f - dot / (m1 * m2);
+  }
+  float s = -0.0f;
+  for (int32_t i = 0; i < d; ++i) {
+    const float t = q[i] - x[i];
+    s += t * t;
+  }
+  return metric == VSKO_L2SQ ? s : sqrtf(s);
+}
+
+/* query i against rows[offsets[i] .. offsets[i+1]) of x */
+void vsko_hnsw_distances(const float *q, int64_t nq, const float *x, int32_t d,
+                         const int64_t *offsets, const int32_t *rows, int32_t metric,
+                         float *out) {
+  for (int64_t i = 0; i < nq; ++i)
+    for (int64_t j = offsets[i]; j < offsets[i + 1]; ++j)
+      out[j] = vsko_hnsw_distance(q + i * d, x + (int64_t)rows[j] * d, d, metric);
+}
+
 /* normalizeVectors (Acceleration/Metal/Shaders/DistanceShaders.metal:
  * 403-429): magnitude = sum of x_i * x_i in index order, then
  * sqrt(magnitude) + 1e-8, then every component divided by it (a division,

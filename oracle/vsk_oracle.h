@@ -33,7 +33,8 @@ enum {
   VSKO_COSINE_NORMALIZED = 3, /* 1 - q.x (unit-norm inputs)                  */
   VSKO_DOT = 4,               /* -q.x                                        */
   VSKO_L1 = 5,                /* sum |q-x|                                   */
-  VSKO_HAMMING = 6            /* count of q_i != x_i                         */
+  VSKO_HAMMING = 6,           /* count of q_i != x_i                         */
+  VSKO_COSINE_NOEPS = 7       /* 1 - q.x / (|q||x|), HNSW's cosine           */
 };
 
 /* ---- distances ---------------------------------------------------------- */
@@ -45,6 +46,12 @@ float vsko_distance(const float *q, const float *x, int32_t d, int32_t metric);
  * uint8 codes truncated; scale/minv per vector (either may be NULL) */
 void vsko_scalar_quantize_u8(const float *x, int64_t n, int32_t d, int32_t bits,
                              uint8_t *codes, float *scale, float *minv);
+/* HNSWIndex DistanceComputer.distance (L2, L2SQ, L1, COSINE_NOEPS) and its
+ * batched form over CSR neighbour lists */
+float vsko_hnsw_distance(const float *q, const float *x, int32_t d, int32_t metric);
+void vsko_hnsw_distances(const float *q, int64_t nq, const float *x, int32_t d,
+                         const int64_t *offsets, const int32_t *rows, int32_t metric,
+                         float *out);
 /* normalizeVectors: out = x / (sqrt(sum x^2) + 1e-8) per row */
 void vsko_normalize(const float *x, int64_t n, int32_t d, float *out);
 /* out[i*n + j] = distance(q_i, x_j) */

@@ -38,6 +38,7 @@ METRIC_COSINE_NORMALIZED = 3
 METRIC_DOT = 4
 METRIC_L1 = 5
 METRIC_HAMMING = 6
+METRIC_COSINE_NOEPS = 7
 MAX_K = 1024
 DB_NORMALIZE = 1
 
@@ -124,6 +125,7 @@ SIGNATURES = {
     "vsk_pq_add_codes": (c_int32, [P, P, P, c_int64]),
     "vsk_pq_lut": (c_int32, [P, P, P, c_int64, P]),
     "vsk_pq_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P, P]),
+    "vsk_hnsw_distances": (c_int32, [P, P, P, c_int64, P, P, c_int32, P]),
     "vsk_kmeans": (c_int32, [P, P, c_int64, c_int32, c_int32, P, c_int32, P, ctypes.c_uint64,
                              c_int32, c_float, P, P, P]),
     "vsk_sq8_decode": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P, P]),
