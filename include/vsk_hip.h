@@ -235,18 +235,40 @@ vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
                              float *out_dist, int64_t *out_ids);
 
 /* ---- IVF index file ----------------------------------------------------------
- * IVFIndex persistence keeps only the centroids and counts
- * (Indexes/IVFIndex.swift:297-328: the lists are dropped).  This file holds
- * the whole index, little-endian:
- *   "VSKIVF01"; int32 nlist, d; int64 total, next_id;
- *   int32 code_kind, code_stride, pq_M, pq_ksub (code_kind 0 = none);
+ * IVFIndex persistence keeps only the configuration and centroids
+ * (export(format:), Indexes/IVFIndex.swift:297-328: the lists are dropped).
+ * This file holds the whole index, little-endian:
+ *   "VSKIVF02"; int32 nlist, d; int64 total, next_id;
+ *   int32 code_kind, code_stride, pq_M, pq_ksub, sq8_per_dim, pq_dsub
+ *   (code_kind 0 = none, 1 = SQ8, 2 = PQ); int64 meta_bytes;
  *   float centroids[nlist][d]; int64 list_off[nlist + 1]; int64 ids[total];
  *   float rows[total][d] (list order); uint8 codes[total][code_stride];
+ *   float quantizer[] (SQ8: scale then offset, d each when per-dimension,
+ *   else 1 each; PQ: the codebooks, pq_M x pq_ksub x pq_dsub);
+ *   uint8 meta[meta_bytes] (vsk_ivf_set_meta);
  *   uint64 FNV-1a of every byte before it.
  * Stale codes (rows added after the last encode) are not written.  Loading
- * checks the magic, the sizes, the offsets and the checksum (VSK_ERR_IO). */
+ * bounds every header size (d <= 65536, nlist <= 2^24, total < 2^31, meta
+ * <= 1 GiB), requires the file length the header implies, checks the list
+ * offsets, that every PQ code is below pq_ksub, and the checksum
+ * (VSK_ERR_IO otherwise). */
 vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path);
 vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out);
+/* Caller bytes kept with the index and its file (e.g. the encoded
+ * IVFConfiguration, which IVFIndex's export keeps, :297-303).  get: *n =
+ * the stored size; the first min(cap, *n) bytes go to out. */
+vsk_status vsk_ivf_set_meta(vsk_ctx *ctx, vsk_ivf *ivf, const void *bytes, int64_t n);
+vsk_status vsk_ivf_get_meta(vsk_ctx *ctx, const vsk_ivf *ivf, void *out, int64_t cap,
+                            int64_t *n);
+/* getCentroids() (:483): out nlist x d */
+vsk_status vsk_ivf_centroids(vsk_ctx *ctx, const vsk_ivf *ivf, float *out);
+/* The SQ8 parameters the index's codes were made with (scale and offset: d
+ * floats each when *per_dim, else 1); VSK_ERR_NOT_TRAINED without current
+ * SQ8 codes.  vsk_ivf_search_pq likewise refuses a quantizer whose
+ * codebooks differ from the ones the codes were made with
+ * (VSK_ERR_DIMENSION_MISMATCH). */
+vsk_status vsk_ivf_sq8_params(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *per_dim,
+                              float *scale, float *offset);
 /* nlist, d, total rows and code kind (0 none, 1 SQ8, 2 PQ) of an index */
 vsk_status vsk_ivf_info(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *nlist, int32_t *d,
                         int64_t *total, int32_t *code_kind);

@@ -117,8 +117,19 @@ def test_ivf_index_file_round_trip(ctx, tmp_path):
     idx.encodeSQ8(sq)
     path = str(tmp_path / "ivf.vsk")
     idx.save(path)
-    back = IVFIndex.load(ctx, path, numberOfProbes=6, sq8=sq)
+    back = IVFIndex.load(ctx, path, sq8=sq)
+    assert back.configuration.numberOfProbes == 6  # the configuration travels in the file
     np.testing.assert_array_equal(back.getCentroids(), c)
+    # the SQ8 parameters travel too: without a quantizer the loaded index
+    # searches its codes with the stored one; a different one is refused
+    alone = IVFIndex.load(ctx, path)
+    for a, b in zip(idx.searchSQ8(q, 9), alone.searchSQ8(q, 9)):
+        np.testing.assert_array_equal(a, b)
+    other = ScalarQuantizer(ctx)
+    other.train(x[:100])
+    with pytest.raises(VSKError) as e:
+        IVFIndex.load(ctx, path, sq8=other)
+    assert e.value.status == -4
     np.testing.assert_array_equal(back.list_sizes(), idx.list_sizes())
     for a, b in zip(idx.search(q, 9), back.search(q, 9)):
         np.testing.assert_array_equal(a, b)
@@ -144,9 +155,65 @@ def test_ivf_index_file_pq_round_trip(ctx, tmp_path):
     idx.encodePQ(pq)
     path = str(tmp_path / "ivfpq.vsk")
     idx.save(path)
-    back = IVFIndex.load(ctx, path, numberOfProbes=4, pq=pq)
+    back = IVFIndex.load(ctx, path, pq=pq)
     for a, b in zip(idx.searchPQ(q, 11), back.searchPQ(q, 11)):
         np.testing.assert_array_equal(a, b)
+    # a quantizer of the same shape with other codebooks is refused
+    cb2 = cb.copy()
+    cb2[3, 17, 1] += 1.0
+    with pytest.raises(VSKError) as e:
+        IVFIndex.load(ctx, path, pq=ProductQuantizer(ctx, cb2)).searchPQ(q, 11)
+    assert e.value.status == -4
+
+
+def _fnv1a(b: bytes) -> int:
+    h = 0xcbf29ce484222325
+    for byte in b:
+        h = ((h ^ byte) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_ivf_index_file_crafted_headers_and_codes(ctx, tmp_path):
+    """Files with a valid checksum but bad contents are refused: a header
+    whose sizes overflow, and a PQ code past the codebook size."""
+    import struct
+
+    x, q, c = _mixture(24, 8, 600, 16, 4)
+    rng = np.random.default_rng(2)
+    cb = x[rng.choice(600, 16, replace=False)].reshape(16, 4, 4).transpose(1, 0, 2).copy()
+    idx = _index(ctx, c, x, 2)
+    pq = ProductQuantizer(ctx, cb)  # ksub = 16
+    idx.encodePQ(pq)
+    path = tmp_path / "ivfpq.vsk"
+    idx.save(str(path))
+    raw = path.read_bytes()
+
+    def seal(body: bytes) -> bytes:
+        return body + struct.pack("<Q", _fnv1a(body))
+
+    assert seal(raw[:-8]) == raw
+    nlist, d = struct.unpack_from("<ii", raw, 8)
+    total = struct.unpack_from("<q", raw, 16)[0]
+    stride = struct.unpack_from("<i", raw, 36)[0]
+    codes_at = 64 + 4 * nlist * d + 8 * (nlist + 1) + 8 * total + 4 * total * d
+    assert raw[codes_at] < 16
+    bad_code = bytearray(raw[:-8])
+    bad_code[codes_at + stride * 5 + 1] = 200  # row 5, segment 1: >= ksub
+    cases = {"code past ksub": seal(bytes(bad_code))}
+    for name, dd, nn in (("huge d", 0x7FFFFFFF, nlist), ("huge nlist", d, 0x7FFFFFFF),
+                         ("negative d", -4, nlist)):
+        b = bytearray(raw[:-8])
+        struct.pack_into("<ii", b, 8, nn, dd)
+        cases[name] = seal(bytes(b))
+    b = bytearray(raw[:-8])
+    struct.pack_into("<q", b, 56, 1 << 40)  # metadata size
+    cases["huge meta"] = seal(bytes(b))
+    for name, blob in cases.items():
+        bad = tmp_path / "bad.vsk"
+        bad.write_bytes(blob)
+        with pytest.raises(VSKError) as e:
+            IVFIndex.load(ctx, str(bad), pq=pq)
+        assert e.value.status == -10, name
 
 
 def test_ivf_index_file_damage(ctx, tmp_path):
@@ -156,7 +223,7 @@ def test_ivf_index_file_damage(ctx, tmp_path):
     idx.save(str(path))
     raw = path.read_bytes()
     cases = {"flipped": raw[:3000] + bytes([raw[3000] ^ 1]) + raw[3001:],
-             "truncated": raw[:-9], "magic": b"VSKIVF02" + raw[8:], "longer": raw + b"\0"}
+             "truncated": raw[:-9], "magic": b"VSKIVF01" + raw[8:], "longer": raw + b"\0"}
     for name, blob in cases.items():
         bad = tmp_path / f"{name}.vsk"
         bad.write_bytes(blob)

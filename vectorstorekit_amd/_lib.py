@@ -109,6 +109,10 @@ SIGNATURES = {
     "vsk_ivf_save": (c_int32, [P, P, ctypes.c_char_p]),
     "vsk_ivf_load": (c_int32, [P, ctypes.c_char_p, PP]),
     "vsk_ivf_info": (c_int32, [P, P, P, P, P]),
+    "vsk_ivf_set_meta": (c_int32, [P, P, P, c_int64]),
+    "vsk_ivf_get_meta": (c_int32, [P, P, P, c_int64, P]),
+    "vsk_ivf_centroids": (c_int32, [P, P, P]),
+    "vsk_ivf_sq8_params": (c_int32, [P, P, P, P, P]),
     "vsk_ivf_search_sq8": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_ivf_search_pq": (c_int32, [P, P, P, P, c_int64, c_int32, c_int32, P, P]),
     "vsk_sq8_train": (c_int32, [P, P, c_int64, c_int32, c_int32, P, P]),

@@ -493,6 +493,7 @@ vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
   *out = nullptr;
   VSK_REQUIRE(n > 0, VSK_ERR_EMPTY_INPUT, "database has no rows");
   VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(d <= (1 << 24), VSK_ERR_INVALID_BUFFER_SIZE, "at most 2^24 dimensions");
   VSK_REQUIRE(x, VSK_ERR_INVALID_ARGUMENT, "x is null");
   VSK_REQUIRE(n <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE,
               "a database holds at most 2^31-1 rows");

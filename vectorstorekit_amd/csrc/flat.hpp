@@ -150,5 +150,7 @@ void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
 // a PQ quantizer's shape for other translation units: returns d
 int32_t pq_shape(const vsk_pq *pq, int32_t *M, int32_t *ksub);
 bool pq_shape_matches(const vsk_pq *pq, int32_t d, int32_t M, int32_t ksub);
+// the quantizer's codebooks on the host (M x ksub x dsub) and its dsub
+const std::vector<float> &pq_host_codebooks(const vsk_pq *pq, int32_t *dsub);
 
 }  // namespace vsk

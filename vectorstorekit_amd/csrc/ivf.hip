@@ -28,10 +28,14 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <numeric>
 
 #include "flat.hpp"
+
+// largest dimension and list count an index (and its file) may have
+constexpr int32_t kMaxDim = 65536, kMaxLists = 1 << 24;
 
 struct vsk_ivf {
   int32_t nlist = 0, d = 0, ld = 0;
@@ -48,6 +52,12 @@ struct vsk_ivf {
   vsk::DevBuf codes;
   int32_t ckind = 0, cstride = 0, cM = 0, cksub = 0;
   int64_t ctotal = -1;
+  // the quantizer the codes were made with: SQ8 scale then offset (d values
+  // each when cper_dim, else 1), or the PQ codebooks (cM x cksub x cdsub)
+  std::vector<float> cparams;
+  int32_t cper_dim = 0, cdsub = 0;
+  // caller bytes stored with the index file (e.g. the index configuration)
+  std::vector<uint8_t> meta;
 };
 
 namespace vsk {
@@ -392,6 +402,8 @@ vsk_status vsk_ivf_create(vsk_ctx *ctx, const float *centroids, int32_t nlist,
   VSK_REQUIRE(centroids, VSK_ERR_NOT_TRAINED, "no centroids (index not trained)");
   VSK_REQUIRE(nlist > 0, VSK_ERR_NOT_TRAINED, "nlist must be positive");
   VSK_REQUIRE(d > 0, VSK_ERR_INVALID_ARGUMENT, "dimension must be positive");
+  VSK_REQUIRE(d <= kMaxDim && nlist <= kMaxLists, VSK_ERR_INVALID_BUFFER_SIZE,
+              "at most 65536 dimensions and 2^24 lists");
   std::unique_ptr<vsk_ivf> ivf(new vsk_ivf());
   ivf->nlist = nlist;
   ivf->d = d;
@@ -593,7 +605,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   }
   if (kind == 2) {
     const vsk_pq *pq = static_cast<const vsk_pq *>(qextra);
-    VSK_REQUIRE(pq_shape_matches(pq, ivf->d, ivf->cM, ivf->cksub), VSK_ERR_DIMENSION_MISMATCH,
+    int32_t dsub = 0;
+    VSK_REQUIRE(pq_shape_matches(pq, ivf->d, ivf->cM, ivf->cksub) &&
+                    pq_host_codebooks(pq, &dsub) == ivf->cparams,
+                VSK_ERR_DIMENSION_MISMATCH,
                 "pq does not match the codebook the codes were made with");
   }
   VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
@@ -853,7 +868,13 @@ vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,
                                        scale, offset, codes.as<int8_t>());
   if (st != VSK_OK) return st;
   ivf_store_codes(ctx, ivf, codes.p, ivf->d, 16, 1);
-  ivf->cM = ivf->cksub = 0;
+  ivf->cM = ivf->cksub = ivf->cdsub = 0;
+  // keep the parameters: they identify the codes and travel with the file
+  const size_t ns = per_dim ? (size_t)ivf->d : 1;
+  ivf->cparams.assign(2 * ns, 0.f);
+  VSK_HIP(hipMemcpy(ivf->cparams.data(), scale, sizeof(float) * ns, hipMemcpyDefault));
+  VSK_HIP(hipMemcpy(ivf->cparams.data() + ns, offset, sizeof(float) * ns, hipMemcpyDefault));
+  ivf->cper_dim = per_dim ? 1 : 0;
   VSK_API_END(ctx);
 }
 
@@ -874,6 +895,55 @@ vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq) {
   ivf_store_codes(ctx, ivf, codes.p, M, 4, 2);
   ivf->cM = M;
   ivf->cksub = ksub;
+  ivf->cparams = pq_host_codebooks(pq, &ivf->cdsub);
+  ivf->cper_dim = 0;
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_centroids(vsk_ctx *ctx, const vsk_ivf *ivf, float *out) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(out, VSK_ERR_INVALID_ARGUMENT, "out is null");
+  CallScope cs(ctx);
+  copy_rows(ctx, out, sizeof(float) * ivf->d, ivf->centroids.x.p, sizeof(float) * ivf->ld,
+            sizeof(float) * ivf->d, ivf->nlist);
+  cs.finish();
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_sq8_params(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *per_dim,
+                              float *scale, float *offset) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(ivf->ckind == 1 && ivf->ctotal == ivf->total, VSK_ERR_NOT_TRAINED,
+              "the index holds no current SQ8 codes");
+  const size_t ns = ivf->cper_dim ? (size_t)ivf->d : 1;
+  if (per_dim) *per_dim = ivf->cper_dim;
+  if (scale) memcpy(scale, ivf->cparams.data(), sizeof(float) * ns);
+  if (offset) memcpy(offset, ivf->cparams.data() + ns, sizeof(float) * ns);
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_set_meta(vsk_ctx *ctx, vsk_ivf *ivf, const void *bytes, int64_t n) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(n >= 0 && n <= (int64_t(1) << 30), VSK_ERR_INVALID_BUFFER_SIZE,
+              "metadata is limited to 1 GiB");
+  VSK_REQUIRE(n == 0 || bytes, VSK_ERR_INVALID_ARGUMENT, "bytes is null");
+  const uint8_t *b = static_cast<const uint8_t *>(bytes);
+  ivf->meta.assign(b, b + n);
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_get_meta(vsk_ctx *ctx, const vsk_ivf *ivf, void *out, int64_t cap,
+                            int64_t *n) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(n, VSK_ERR_INVALID_ARGUMENT, "n is null");
+  VSK_REQUIRE(cap >= 0 && (cap == 0 || out), VSK_ERR_INVALID_ARGUMENT, "bad output buffer");
+  *n = (int64_t)ivf->meta.size();
+  const size_t m = (size_t)std::min<int64_t>(cap, *n);
+  if (m) memcpy(out, ivf->meta.data(), m);
   VSK_API_END(ctx);
 }
 
@@ -885,7 +955,9 @@ vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq) {
 namespace vsk {
 namespace {
 
-constexpr char kIvfMagic[8] = {'V', 'S', 'K', 'I', 'V', 'F', '0', '1'};
+constexpr char kIvfMagic[8] = {'V', 'S', 'K', 'I', 'V', 'F', '0', '2'};
+constexpr int64_t kHeaderBytes = 8 + 8 + 16 + 16 + 8 + 8;  // magic .. meta size
+constexpr int64_t kMaxMeta = int64_t(1) << 30;
 constexpr size_t kIoChunk = 64u << 20;  // host staging per transfer
 
 struct Fnv1a {
@@ -929,15 +1001,17 @@ void put_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, const void *dev, int64_t rows, si
   }
 }
 
-// file -> rows x w bytes at a device pitch
+// file -> rows x w bytes at a device pitch; check(chunk, rows) may reject a
+// chunk before it is uploaded
 void get_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, void *dev, int64_t rows, size_t pitch,
-              size_t w) {
+              size_t w, const std::function<bool(const uint8_t *, int64_t)> &check = nullptr) {
   if (rows == 0) return;
   const int64_t per = std::max<int64_t>(1, (int64_t)(kIoChunk / w));
   std::vector<uint8_t> buf((size_t)std::min(per, rows) * w);
   for (int64_t r = 0; r < rows; r += per) {
     const int64_t cnt = std::min(per, rows - r);
     get(f, h, buf.data(), (size_t)cnt * w);
+    if (check && !check(buf.data(), cnt)) fail(VSK_ERR_IO, "index file: bad code values");
     VSK_HIP(hipMemcpy2DAsync(static_cast<uint8_t *>(dev) + r * pitch, pitch, buf.data(), w, w,
                              cnt, hipMemcpyHostToDevice, ctx->stream));
     VSK_HIP(hipStreamSynchronize(ctx->stream));
@@ -963,21 +1037,31 @@ vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path) {
   VSK_REQUIRE(f, VSK_ERR_IO, std::string("cannot open for writing: ") + path);
   Fnv1a h;
   const bool coded = ivf->ckind != 0 && ivf->ctotal == ivf->total;
-  const int32_t hdr32[6] = {ivf->nlist, ivf->d, coded ? ivf->ckind : 0,
-                            coded ? ivf->cstride : 0, coded ? ivf->cM : 0,
-                            coded ? ivf->cksub : 0};
+  const int32_t hdr32[8] = {ivf->nlist,
+                            ivf->d,
+                            coded ? ivf->ckind : 0,
+                            coded ? ivf->cstride : 0,
+                            coded ? ivf->cM : 0,
+                            coded ? ivf->cksub : 0,
+                            coded ? ivf->cper_dim : 0,
+                            coded ? ivf->cdsub : 0};
   const int64_t hdr64[2] = {ivf->total, ivf->next_id};
+  const int64_t meta_n = (int64_t)ivf->meta.size();
   put(f.get(), h, kIvfMagic, 8);
   put(f.get(), h, &hdr32[0], 8);
   put(f.get(), h, hdr64, 16);
-  put(f.get(), h, &hdr32[2], 16);
+  put(f.get(), h, &hdr32[2], 24);
+  put(f.get(), h, &meta_n, 8);
   const size_t ldb = sizeof(float) * ivf->ld, db = sizeof(float) * ivf->d;
   put_rows(ctx, f.get(), h, ivf->centroids.x.p, ivf->nlist, ldb, db);
   put(f.get(), h, ivf->off.data(), sizeof(int64_t) * (ivf->nlist + 1));
   put_rows(ctx, f.get(), h, ivf->ids.p, ivf->total, 8, 8);
   put_rows(ctx, f.get(), h, ivf->rows.p, ivf->total, ldb, db);
-  if (coded)
+  if (coded) {
     put_rows(ctx, f.get(), h, ivf->codes.p, ivf->total, ivf->cstride, ivf->cstride);
+    put(f.get(), h, ivf->cparams.data(), sizeof(float) * ivf->cparams.size());
+  }
+  put(f.get(), h, ivf->meta.data(), ivf->meta.size());
   const uint64_t sum = h.h;
   VSK_REQUIRE(fwrite(&sum, 8, 1, f.get()) == 1 && fflush(f.get()) == 0, VSK_ERR_IO,
               "index file: write failed");
@@ -995,28 +1079,39 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   Fnv1a h;
   char magic[8];
   get(f.get(), h, magic, 8);
-  VSK_REQUIRE(memcmp(magic, kIvfMagic, 8) == 0, VSK_ERR_IO, "not an IVF index file");
-  int32_t nd[2], ck[4];
-  int64_t tn[2];
+  VSK_REQUIRE(memcmp(magic, kIvfMagic, 8) == 0, VSK_ERR_IO, "not an IVF index file (VSKIVF02)");
+  int32_t nd[2], ck[6];
+  int64_t tn[2], meta_n = 0;
   get(f.get(), h, nd, 8);
   get(f.get(), h, tn, 16);
-  get(f.get(), h, ck, 16);
+  get(f.get(), h, ck, 24);
+  get(f.get(), h, &meta_n, 8);
   const int32_t nlist = nd[0], d = nd[1];
   const int64_t total = tn[0], next_id = tn[1];
-  VSK_REQUIRE(nlist > 0 && d > 0 && total >= 0 && total <= 0x7FFFFFFFll && next_id >= 0,
+  // every size is bounded before any arithmetic on it
+  VSK_REQUIRE(nlist > 0 && nlist <= kMaxLists && d > 0 && d <= kMaxDim && total >= 0 &&
+                  total <= 0x7FFFFFFFll && next_id >= 0 && meta_n >= 0 && meta_n <= kMaxMeta,
               VSK_ERR_IO, "index file: bad header");
+  int64_t nparams = 0;  // floats of quantizer parameters
   bool kind_ok = false;
-  if (ck[0] == 0) kind_ok = ck[1] == 0 && ck[2] == 0 && ck[3] == 0;
-  if (ck[0] == 1) kind_ok = ck[1] == (d + 15) / 16 * 16 && ck[2] == 0 && ck[3] == 0;
-  if (ck[0] == 2)
+  if (ck[0] == 0) kind_ok = ck[1] == 0 && ck[2] == 0 && ck[3] == 0 && ck[4] == 0 && ck[5] == 0;
+  if (ck[0] == 1) {
+    kind_ok = ck[1] == (d + 15) / 16 * 16 && ck[2] == 0 && ck[3] == 0 &&
+              (ck[4] == 0 || ck[4] == 1) && ck[5] == 0;
+    nparams = 2 * (ck[4] ? (int64_t)d : 1);
+  }
+  if (ck[0] == 2) {
     kind_ok = ck[2] > 0 && d % ck[2] == 0 && ck[3] >= 1 && ck[3] <= 256 &&
-              ck[1] == (ck[2] + 3) / 4 * 4;
+              ck[1] == (ck[2] + 3) / 4 * 4 && ck[4] == 0 && ck[5] == d / ck[2];
+    nparams = kind_ok ? (int64_t)ck[2] * ck[3] * ck[5] : 0;
+  }
   VSK_REQUIRE(kind_ok, VSK_ERR_IO, "index file: bad code header");
-  // the file's length must be exactly what the header describes
-  const int64_t body = 8 + 8 + 16 + 16 + 4ll * nlist * d + 8ll * (nlist + 1) + 8 * total +
-                       4 * total * d + (int64_t)ck[1] * total + 8;
+  // the file's length must be exactly what the header describes (bounded
+  // sizes: no product below can overflow int64)
+  const int64_t body = kHeaderBytes + 4ll * nlist * d + 8ll * (nlist + 1) + 8 * total +
+                       4 * total * d + (int64_t)ck[1] * total + 4 * nparams + meta_n + 8;
   VSK_REQUIRE(fseek(f.get(), 0, SEEK_END) == 0 && ftell(f.get()) == body &&
-                  fseek(f.get(), 48, SEEK_SET) == 0,
+                  fseek(f.get(), kHeaderBytes, SEEK_SET) == 0,
               VSK_ERR_IO, "index file: length does not match its header");
   std::vector<float> cent((size_t)nlist * d);
   get(f.get(), h, cent.data(), 4 * cent.size());
@@ -1038,8 +1133,24 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   if (ck[0] != 0) {
     ivf->codes.reserve((size_t)total * ck[1] + 16);
     fill_i32(ctx, ivf->codes.as<int32_t>(), ((int64_t)total * ck[1] + 16) / 4, 0);
-    get_rows(ctx, f.get(), h, ivf->codes.p, total, ck[1], ck[1]);
+    // PQ codes index the ksub-entry tables: every code byte must be < ksub
+    // and the row padding zero
+    const int32_t stride = ck[1], M = ck[2], ksub = ck[3];
+    auto pq_ok = [&](const uint8_t *b, int64_t rows) {
+      for (int64_t r = 0; r < rows; ++r)
+        for (int32_t j = 0; j < stride; ++j) {
+          const uint8_t c = b[r * stride + j];
+          if (j < M ? c >= ksub : c != 0) return false;
+        }
+      return true;
+    };
+    get_rows(ctx, f.get(), h, ivf->codes.p, total, stride, stride,
+             ck[0] == 2 ? std::function<bool(const uint8_t *, int64_t)>(pq_ok) : nullptr);
+    ivf->cparams.resize((size_t)nparams);
+    get(f.get(), h, ivf->cparams.data(), sizeof(float) * ivf->cparams.size());
   }
+  ivf->meta.resize((size_t)meta_n);
+  get(f.get(), h, ivf->meta.data(), ivf->meta.size());
   uint64_t sum = 0;
   VSK_REQUIRE(fread(&sum, 8, 1, f.get()) == 1 && sum == h.h, VSK_ERR_IO,
               "index file: checksum mismatch");
@@ -1053,6 +1164,8 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   ivf->cstride = ck[1];
   ivf->cM = ck[2];
   ivf->cksub = ck[3];
+  ivf->cper_dim = ck[4];
+  ivf->cdsub = ck[5];
   ivf->ctotal = ck[0] ? total : -1;
   *out = ivf.release();
   VSK_API_END(ctx);

@@ -29,6 +29,7 @@
 struct vsk_pq {
   int32_t M = 0, ksub = 0, dsub = 0, d = 0;
   vsk::DevBuf codebooks;  // M x ksub x dsub fp32
+  std::vector<float> host_codebooks;  // the same, for identity checks and files
   vsk::DevBuf codes;      // n x M uint8
   int64_t n = 0, cap_rows = 0;
 };
@@ -755,6 +756,9 @@ vsk_status vsk_pq_create(vsk_ctx *ctx, const float *codebooks, int32_t M,
   pq->codebooks.reserve(bytes);
   VSK_HIP(hipMemcpyAsync(pq->codebooks.p, codebooks, bytes, hipMemcpyDefault,
                          ctx->stream));
+  pq->host_codebooks.resize((size_t)M * ksub * dsub);
+  VSK_HIP(hipMemcpyAsync(pq->host_codebooks.data(), pq->codebooks.p, bytes,
+                         hipMemcpyDeviceToHost, ctx->stream));
   cs.finish();
   *out = pq.release();
   VSK_API_END(ctx);
@@ -988,6 +992,11 @@ int32_t pq_shape(const vsk_pq *pq, int32_t *M, int32_t *ksub) {
 
 bool pq_shape_matches(const vsk_pq *pq, int32_t d, int32_t M, int32_t ksub) {
   return pq && pq->d == d && pq->M == M && pq->ksub == ksub;
+}
+
+const std::vector<float> &pq_host_codebooks(const vsk_pq *pq, int32_t *dsub) {
+  *dsub = pq->dsub;
+  return pq->host_codebooks;
 }
 
 }  // namespace vsk

@@ -11,6 +11,7 @@ strategy)`` (:124-202; ``"exact"`` probes every list, :551-554),
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 from dataclasses import dataclass, field
 
@@ -216,30 +217,77 @@ class IVFIndex:
         return dist, ids
 
     # ---- index file (the whole index; the reference's persistence keeps
-    # only centroids and counts, Indexes/IVFIndex.swift:297-328)
+    # only the configuration and centroids, Indexes/IVFIndex.swift:297-328)
     def save(self, path: str):
+        """The index, its codes and quantizer parameters, and this
+        configuration (as JSON in the file's metadata) in one file."""
         self._need()
+        cfg = self.configuration
+        meta = json.dumps({
+            "dimensions": cfg.dimensions, "numberOfCentroids": cfg.numberOfCentroids,
+            "numberOfProbes": cfg.numberOfProbes,
+            "clusteringConfig": {"maxIterations": cfg.clusteringConfig.maxIterations,
+                                 "tolerance": cfg.clusteringConfig.tolerance,
+                                 "initMethod": cfg.clusteringConfig.initMethod,
+                                 "seed": cfg.clusteringConfig.seed}}).encode()
+        self.ctx.check(self.ctx.lib.vsk_ivf_set_meta(self.ctx.handle, self.handle, meta,
+                                                     len(meta)))
         self.ctx.check(self.ctx.lib.vsk_ivf_save(self.ctx.handle, self.handle,
                                                  os.fsencode(path)))
 
     @classmethod
-    def load(cls, ctx: Context, path: str, numberOfProbes: int = 10, sq8=None, pq=None):
-        """An index written by ``save``.  ``sq8`` / ``pq``: the quantizer its
-        codes were made with, needed to search them."""
+    def load(cls, ctx: Context, path: str, sq8=None, pq=None) -> "IVFIndex":
+        """An index written by ``save``, with its saved configuration.  SQ8
+        codes come back with their quantizer (a passed ``sq8`` must equal
+        it); PQ codes need the ``pq`` they were made with, which the library
+        checks against the codebooks stored in the file at search time."""
         h = ctypes.c_void_p()
         ctx.check(ctx.lib.vsk_ivf_load(ctx.handle, os.fsencode(path), ctypes.byref(h)))
-        nlist, d, kind = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-        total = ctypes.c_int64()
-        ctx.check(ctx.lib.vsk_ivf_info(ctx.handle, h, ctypes.byref(nlist), ctypes.byref(d),
-                                       ctypes.byref(total), ctypes.byref(kind)))
-        idx = cls(ctx, IVFConfiguration(dimensions=d.value, numberOfCentroids=nlist.value,
-                                        numberOfProbes=min(numberOfProbes, nlist.value)))
+        try:
+            nlist, d, kind = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+            total = ctypes.c_int64()
+            ctx.check(ctx.lib.vsk_ivf_info(ctx.handle, h, ctypes.byref(nlist), ctypes.byref(d),
+                                           ctypes.byref(total), ctypes.byref(kind)))
+            n = ctypes.c_int64()
+            ctx.check(ctx.lib.vsk_ivf_get_meta(ctx.handle, h, None, 0, ctypes.byref(n)))
+            raw = ctypes.create_string_buffer(max(1, n.value))
+            ctx.check(ctx.lib.vsk_ivf_get_meta(ctx.handle, h, raw, n.value, ctypes.byref(n)))
+            meta = json.loads(raw.raw[:n.value].decode()) if n.value else {}
+            cc = meta.get("clusteringConfig", {})
+            cfg = IVFConfiguration(
+                dimensions=d.value, numberOfCentroids=nlist.value,
+                numberOfProbes=min(int(meta.get("numberOfProbes", 10)), nlist.value),
+                clusteringConfig=KMeansClusteringConfiguration(
+                    **{k: cc[k] for k in ("maxIterations", "tolerance", "initMethod", "seed")
+                       if k in cc}))
+            cent = np.empty((nlist.value, d.value), np.float32)
+            ctx.check(ctx.lib.vsk_ivf_centroids(ctx.handle, h, cent.ctypes.data))
+            sq = None
+            if kind.value == 1:
+                from .quantization import ScalarQuantizer
+
+                pdim = ctypes.c_int32()
+                ctx.check(ctx.lib.vsk_ivf_sq8_params(ctx.handle, h, ctypes.byref(pdim), None,
+                                                     None))
+                ns = d.value if pdim.value else 1
+                sc, of = np.empty(ns, np.float32), np.empty(ns, np.float32)
+                ctx.check(ctx.lib.vsk_ivf_sq8_params(ctx.handle, h, ctypes.byref(pdim),
+                                                     sc.ctypes.data, of.ctypes.data))
+                if sq8 is not None and (bool(sq8.per_dim) != bool(pdim.value)
+                                        or not np.array_equal(sq8.scale, sc)
+                                        or not np.array_equal(sq8.offset, of)):
+                    raise VSKError(-4, "sq8 differs from the quantizer the codes were made "
+                                   "with")
+                sq = sq8 or ScalarQuantizer(ctx, per_dim=bool(pdim.value))
+                sq.scale, sq.offset, sq.dimensions = sc, of, d.value
+        except BaseException:
+            ctx.lib.vsk_ivf_free(ctx.handle, h)
+            raise
+        idx = cls(ctx, cfg)
         idx.handle = h
-        # the centroids follow the 48-byte header
-        idx._centroids = np.fromfile(path, np.float32, nlist.value * d.value,
-                                     offset=48).reshape(nlist.value, d.value)
+        idx._centroids = cent
         if kind.value == 1:
-            idx._sq8 = sq8
+            idx._sq8 = sq
         elif kind.value == 2:
             idx._pq = pq
         return idx
