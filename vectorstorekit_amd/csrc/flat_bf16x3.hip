@@ -21,6 +21,8 @@
 // slice.  LDS is double-buffered: while a stage is consumed by the MFMAs,
 // the next one is written to the other buffer from registers and the one
 // after is loaded from memory, with one barrier per stage.
+#include <type_traits>
+
 #include "flat.hpp"
 
 namespace vsk {
@@ -731,6 +733,17 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED ||
                       METRIC == VSK_METRIC_DOT) {
           const float tdot = l_tdot[16 * j];
+          // the block's largest dot first: when it is below the bound in
+          // every lane, no score of the block can pass (one compare and a
+          // ballot instead of sixteen).  A NaN score is dropped by the max;
+          // it needs a non-finite input, whose bound is not finite, so such
+          // a query fails the screen's check and is redone exactly.
+          float mx = acc[0][j][0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, acc[i][j][r]);
+          if (!__builtin_amdgcn_ballot_w64(!(mx < tdot))) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll

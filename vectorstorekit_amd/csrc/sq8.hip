@@ -146,6 +146,8 @@ __global__ __launch_bounds__(256) void k_sq8_scan(Sq8Args a) {
 // groups of one row split are consecutive slots of one XCD so they share its
 // L2.
 
+// the first k-step takes the constant 0 as its accumulator operand (no
+// register moves to clear the accumulators)
 template <int RT, int KS, int QT>
 __device__ __forceinline__ void sq8_mma(const i4 (&ar)[RT][KS],
                                         const i4 (&bq)[QT][KS],
@@ -153,9 +155,11 @@ __device__ __forceinline__ void sq8_mma(const i4 (&ar)[RT][KS],
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int j = 0; j < QT; ++j) acc[i][j] = i4{0, 0, 0, 0};
+    for (int j = 0; j < QT; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ar[i][0], bq[j][0], i4{0, 0, 0, 0},
+                                                        0, 0, 0);
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
+  for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
     for (int i = 0; i < RT; ++i)
 #pragma unroll
@@ -203,38 +207,47 @@ __device__ __forceinline__ void sq8_epilogue(
             a.cand[q * a.cap + (rb + r - a.r0)] =
                 vsk_key_i32(-acc[i][j][r], (uint32_t)(rb + r));
       }
-    } else {
+    }
+  }
+  if (DENSE) return;
+  // filter: per query tile, the largest of the lane's 4 * RT scores first,
+  // so the common case (nothing passes anywhere in the wave) is a few maxima,
+  // one compare and one ballot per query tile
 #pragma unroll
-      for (int j = 0; j < QT; ++j) {
-        const int32_t m01 = acc[i][j][0] > acc[i][j][1] ? acc[i][j][0] : acc[i][j][1];
-        const int32_t m23 = acc[i][j][2] > acc[i][j][3] ? acc[i][j][2] : acc[i][j][3];
-        const bool hit = (m01 > m23 ? m01 : m23) >= smin[j];
-        if (!__builtin_amdgcn_ballot_w64(hit)) continue;  // the common case
-        // key <= th[j]: a higher score, or the floor score at a row id not
-        // above the threshold's.  Control flow stays wave-uniform so nbuf
-        // stays uniform: passing keys take consecutive slots of the wave's
-        // LDS list in lane order.
-        const uint32_t trow = (uint32_t)th[j];
-        const int32_t q = (int32_t)(qw0 + 16 * j + (lane & 15));
+  for (int j = 0; j < QT; ++j) {
+    int32_t mx = acc[0][j][0];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int32_t v = acc[i][j][r];
-          const bool p = rb + r < s1 &&
-                         (v > smin[j] || (v == smin[j] && (uint32_t)(rb + r) <= trow));
-          const uint64_t m = __builtin_amdgcn_ballot_w64(p);
-          if (!m) continue;
-          if (p) {
-            const int32_t pos =
-                nbuf + (int32_t)__builtin_amdgcn_mbcnt_hi(
-                           (uint32_t)(m >> 32),
-                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            lkey[pos] = vsk_key_i32(-v, (uint32_t)(rb + r));
-            lq[pos] = q;
-          }
-          nbuf += __builtin_popcountll(m);
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = acc[i][j][r] > mx ? acc[i][j][r] : mx;
+    if (!__builtin_amdgcn_ballot_w64(mx >= smin[j])) continue;  // the common case
+    // key <= th[j]: a higher score, or the floor score at a row id not
+    // above the threshold's.  Control flow stays wave-uniform so nbuf
+    // stays uniform: passing keys take consecutive slots of the wave's
+    // LDS list in lane order.
+    const uint32_t trow = (uint32_t)th[j];
+    const int32_t q = (int32_t)(qw0 + 16 * j + (lane & 15));
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int64_t rb = t0 + 16 * i + 4 * (lane >> 4);  // + r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t v = acc[i][j][r];
+        const bool p = rb + r < s1 &&
+                       (v > smin[j] || (v == smin[j] && (uint32_t)(rb + r) <= trow));
+        const uint64_t m = __builtin_amdgcn_ballot_w64(p);
+        if (!m) continue;
+        if (p) {
+          const int32_t pos =
+              nbuf + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                         (uint32_t)(m >> 32),
+                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          lkey[pos] = vsk_key_i32(-v, (uint32_t)(rb + r));
+          lq[pos] = q;
         }
-        if (nbuf > SQ_WBUF - 256) sq8_flush(a, lkey, lq, nbuf, lane);
+        nbuf += __builtin_popcountll(m);
       }
+      if (nbuf > SQ_WBUF - 256) sq8_flush(a, lkey, lq, nbuf, lane);
     }
   }
 }
