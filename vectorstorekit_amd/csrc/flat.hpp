@@ -53,6 +53,9 @@ struct FlatArgs {
   float *mat;  // MODE_MATRIX output, row-major nq x ldm
   int64_t ldm;
   int32_t splits_per_xcd;  // bf16x3 kernel: row splits owned by each XCD
+  // screen kernel: > 0 selects the split-major order, XCD x taking query
+  // tiles x*Q .. x*Q+Q-1 (Q = this value) over every row split in turn
+  int32_t qtiles_per_xcd;
   // screen kernel, filter mode: candidate slots each workgroup reserves per
   // query (0: append through per-candidate atomics)
   int32_t sub;

@@ -428,9 +428,12 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   // sx == 0: one split, workgroup L takes query tile L over every row (the
   // argmin with many queries: the rows stay in every XCD's L2, each query is
   // read once)
+  // qx > 0: split-major, XCD x taking query tiles x*qx .. x*qx+qx-1 over
+  // every split in turn
+  const int qx = a.qtiles_per_xcd;
   const int grp = sx ? slot / (XS_GQ * sx) : 0, rem = sx ? slot - grp * (XS_GQ * sx) : 0;
-  const int qtile = sx ? grp * XS_GQ + rem % XS_GQ : L;
-  const int split = sx ? (rem / XS_GQ) * 8 + xcd : 0;
+  const int qtile = qx ? xcd * qx + slot % qx : (sx ? grp * XS_GQ + rem % XS_GQ : L);
+  const int split = qx ? slot / qx : (sx ? (rem / XS_GQ) * 8 + xcd : 0);
   const int64_t q0 = (int64_t)qtile * XS_Q;
   if (q0 >= a.nq) return;
   const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
@@ -909,6 +912,18 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
       splits = sp;
     }
   }
+  // Order of the (query tile, split) workgroups.  Split-major (XCD x takes
+  // query tiles x*qx .. x*qx+qx-1 over every split in turn) when the query
+  // tiles divide evenly over the XCDs, to within 1/32: all XCDs then stream
+  // the same rows at a time, read from HBM once and served to the other XCDs
+  // by the memory-side cache.  (Measured at 1M x 768, 10,000 queries: 7%
+  // faster than the group order.)  Otherwise groups of XS_GQ query tiles
+  // over the splits that each XCD owns: every XCD gets an equal share.
+  a.qtiles_per_xcd = 0;
+  if (mode != MODE_TOP2) {
+    const int64_t qx = ceil_div(qt, 8);
+    if (32 * (8 * qx - qt) <= qt) a.qtiles_per_xcd = (int32_t)qx;
+  }
   a.rows_per_split = ceil_div(tiles, splits) * XS_N;
   a.splits_per_xcd = (int32_t)(splits / 8);
   if (mode == MODE_TOP2 && qt >= 2 * (int64_t)ctx->cu_count) {
@@ -937,7 +952,8 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     *stride = a.sub;
   }
   const int64_t groups = ceil_div(qt, XS_GQ);
-  const int64_t nblocks = a.splits_per_xcd ? 8 * a.splits_per_xcd * groups * XS_GQ : qt;
+  const int64_t nblocks = a.qtiles_per_xcd ? 8 * (int64_t)a.qtiles_per_xcd * splits
+                         : a.splits_per_xcd ? 8 * a.splits_per_xcd * groups * XS_GQ : qt;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
   static const char *names[5] = {"flat_screen_dense", "flat_screen_filter", "",
                                  "", "flat_screen_top2"};
