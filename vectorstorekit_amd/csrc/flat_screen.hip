@@ -744,7 +744,7 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  int32_t k, int32_t metric, uint64_t *best) {
   const int32_t kc = screen_keep(k);
-  const int64_t qb = query_batch(nq, default_cap(kc));
+  const int64_t qb = query_batch(nq, screen_cap(kc));
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     const float *qbat = dq + b0 * db->ld;

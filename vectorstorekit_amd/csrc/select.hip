@@ -254,6 +254,12 @@ int64_t default_cap(int32_t k) {
   return c;
 }
 
+int64_t screen_cap(int32_t k) {
+  int64_t c = 2048;
+  while (c < 4ll * k) c <<= 1;
+  return c;
+}
+
 int64_t query_batch(int64_t nq, int64_t cap) {
   // candidate buffers of one batch stay under ~2 GiB of HBM
   const int64_t budget = 2ll << 30;
