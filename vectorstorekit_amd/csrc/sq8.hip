@@ -338,6 +338,151 @@ void k_sq8_reg(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
 #undef SR_LOAD
 }
 
+// Filter scan with the test software-pipelined: the two waves of a SIMD run
+// the same code in step, so a test that follows its own block's multiplies
+// leaves the matrix pipe idle while both waves test.  Here each wave
+// multiplies row block b into one accumulator set while it tests block b-1
+// in the other (the test's maxima and compares fill the MFMA shadow; the
+// exact candidate path is a rare branch after the multiplies).  16-row
+// blocks, NPF of them in flight in registers.
+// does any lane hold a score >= its query's floor (wave-uniform)
+template <int QT>
+__device__ __forceinline__ bool sq8_any_pass(const i4 (&acc)[1][QT], const int32_t (&smin)[QT]) {
+  uint64_t any = 0;
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const i4 v = acc[0][j];
+    const int32_t m01 = v[0] > v[1] ? v[0] : v[1];
+    const int32_t m23 = v[2] > v[3] ? v[2] : v[3];
+    const int32_t mx = m01 > m23 ? m01 : m23;
+    any |= __builtin_amdgcn_ballot_w64(mx >= smin[j]);
+  }
+  return any != 0;
+}
+
+template <int KS, int QT, int NPF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
+  constexpr int RT = 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
+  const int grp = slot % groups;
+  const int split = (slot / groups) * 8 + xcd;
+  if (split >= 8 * splits_per_xcd) return;
+  const int64_t s0 = a.r0 + (int64_t)split * a.rows_per_split;
+  int64_t s1 = s0 + a.rows_per_split;
+  if (s1 > a.r1) s1 = a.r1;
+  if (s0 >= s1) return;
+  const int64_t qw0 = ((int64_t)grp * 4 + w) * (QT * 16);
+  if (qw0 >= a.nq) return;
+  const int kc = 16 * (lane >> 4);  // this lane's byte chunk of a k-step
+
+  i4 bq[QT][KS];
+  int32_t smin[QT];
+  uint64_t th[QT];
+  bool qok[QT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int64_t q = qw0 + 16 * j + (lane & 15);
+    qok[j] = q < a.nq && (!a.active || a.active[q]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int off = 64 * ks + kc;
+      bq[j][ks] = (qok[j] && off < a.kbytes)
+                      ? *reinterpret_cast<const i4 *>(a.Q + q * a.ldq + off)
+                      : i4{0, 0, 0, 0};
+    }
+    th[j] = qok[j] ? a.thresh[q] : 0;
+    // key <= th needs -score <= the distance half of th: score >= smin
+    smin[j] = qok[j] ? -(int32_t)((uint32_t)(th[j] >> 32) ^ 0x80000000u) : 0x7FFFFFFF;
+  }
+
+  const int64_t nrows = s1 - s0;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.X + s0 * a.ldx), 0, (int32_t)(nrows * a.ldx), 0x00020000);
+  const int32_t lrow = (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  i4 ar[NPF][RT][KS];
+#define SP_LOAD(AR, T)                                                          \
+  _Pragma("unroll") for (int ks = 0; ks < KS; ++ks) AR[0][ks] = __builtin_bit_cast( \
+      i4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int32_t)(T) * (int32_t)a.ldx + lrow, \
+                                                64 * ks, 0))
+  __shared__ uint64_t s_key[4][SQ_WBUF];
+  __shared__ int32_t s_q[4][SQ_WBUF];
+  int32_t nbuf = 0;  // wave-uniform count of staged candidates
+  constexpr int32_t RB = 16;
+  const int32_t nr = (int32_t)nrows;
+  i4 acc[2][RT][QT];
+  // the "previous block" of the first: scores that pass no floor
+#pragma unroll
+  for (int j = 0; j < QT; ++j) acc[1][0][j] = i4{INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+#pragma unroll
+  for (int p = 0; p < NPF; ++p) {
+    SP_LOAD(ar[p], p * RB);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // block b: multiply into set b & 1 while testing block b - 1 (set
+  // (b + 1) & 1), refill b's registers with block b + NPF, then the exact
+  // path for block b - 1 if a score of it may pass.  A split is a whole
+  // number of NPF-block steps (but the last), and blocks past it read zeros
+  // whose rows the exact path drops.
+#define SP_BLOCK(P)                                                             \
+  do {                                                                          \
+    constexpr int X = (P) & 1, Y = X ^ 1;                                       \
+    sq8_mma<RT, KS, QT>(ar[P], bq, acc[X]);                                     \
+    const bool hit = sq8_any_pass<QT>(acc[Y], smin);                            \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          \
+    _Pragma("unroll") for (int u = 0; u < QT * KS - 1; ++u) {                   \
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                        \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        \
+    }                                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                          \
+    SP_LOAD(ar[P], t + ((P) + NPF) * RB);                                       \
+    __builtin_amdgcn_sched_barrier(0);                                          \
+    if (hit)                                                                    \
+      sq8_epilogue<RT, QT, false>(a, acc[Y], s0 + t + ((P) - 1) * RB, s1, lane, qw0, qok, \
+                                  smin, th, s_key[w], s_q[w], nbuf);           \
+  } while (0)
+  static_assert(NPF == 4, "four blocks per step: the register sets are fixed per position");
+  for (int32_t t = 0; t < nr; t += NPF * RB) {
+    SP_BLOCK(0);
+    SP_BLOCK(1);
+    SP_BLOCK(2);
+    SP_BLOCK(3);
+  }
+#undef SP_BLOCK
+#undef SP_LOAD
+  // the last block (set 1: NPF is even)
+  if (sq8_any_pass<QT>(acc[1], smin))
+    sq8_epilogue<RT, QT, false>(a, acc[1], s0 + ((nr + NPF * RB - 1) / (NPF * RB)) * NPF * RB - RB,
+                                s1, lane, qw0, qok, smin, th, s_key[w], s_q[w], nbuf);
+  if (nbuf > 0) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
+}
+
+template <int KS, int QT, int NPF>
+static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
+  const int64_t rows = a.r1 - a.r0;
+  const int64_t qpg = 4 * QT * 16;  // queries per workgroup
+  const int64_t groups = ceil_div(a.nq, qpg);
+  // row splits: a multiple of 8 (one share per XCD), about 4096 workgroups
+  int64_t splits = ceil_div(4096, groups);
+  constexpr int64_t step = (int64_t)NPF * 16;  // rows per loop trip
+  const int64_t max_splits = ceil_div(rows, step);
+  if (splits > max_splits) splits = max_splits;
+  if (splits < 1) splits = 1;
+  Sq8Args b = a;
+  b.rows_per_split = ceil_div(ceil_div(rows, splits), step) * step;
+  // buffer offsets (row * ldx, prefetch up to 2 NPF blocks past the end)
+  // stay within int32
+  const int64_t max_rows = 0x7FFFFFFFll / a.ldx - 2 * step;
+  if (b.rows_per_split > max_rows) b.rows_per_split = max_rows / step * step;
+  splits = ceil_div(ceil_div(rows, b.rows_per_split), 8) * 8;
+  const int64_t spx = splits / 8;
+  const int64_t nblocks = 8 * spx * groups;
+  if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
+  k_sq8_pipe<KS, QT, NPF><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
+                                                                      (int32_t)spx);
+}
+
 template <int RT, int KS, int QT>
 static void launch_reg(vsk_ctx *ctx, const Sq8Args &a, bool dense) {
   const int64_t rows = a.r1 - a.r0;
@@ -382,7 +527,18 @@ static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
   KernelTimer t(ctx, dense ? "sq8_mfma_dense" : "sq8_mfma_filter",
                 (double)a.nq * (double)rows);
   const int32_t ksteps = (a.kbytes + 63) / 64;
-  if (ksteps <= 1)
+  // the filter scan pipelines its test (up to 512-byte codes; longer ones
+  // leave no registers for four row blocks in flight)
+  if (!dense && ksteps <= 8) {
+    if (ksteps <= 1)
+      launch_pipe<1, 8, 4>(ctx, a);
+    else if (ksteps <= 2)
+      launch_pipe<2, 8, 4>(ctx, a);
+    else if (ksteps <= 4)
+      launch_pipe<4, 4, 4>(ctx, a);
+    else
+      launch_pipe<8, 2, 4>(ctx, a);
+  } else if (ksteps <= 1)
     launch_reg<2, 1, 8>(ctx, a, dense);
   else if (ksteps <= 2)
     launch_reg<2, 2, 8>(ctx, a, dense);
