@@ -566,7 +566,8 @@ def setup(c, a, ctx, dev):
             "data": "synthetic: N(0,1) rows and queries (torch Philox seeds 1, 2), "
                     "quantised per dimension",
             "dtype": "i8 (i32 accumulate)", "nq": nq, "n": n, "d": d,
-            "kernels": [("sq8_mfma_filter", "k_sq8_reg<FILTER> (int8 MFMA 16x16x64)", "int8"),
+            "kernels": [("sq8_mfma_filter", "k_sq8_pipe (int8 MFMA 16x16x64, filter test "
+                                            "pipelined with the next block's MFMAs)", "int8"),
                         ("sq8_mfma_dense", "k_sq8_reg<DENSE> (int8 MFMA 16x16x64)", "int8")],
             "keep": (db, codes, qc, score, ids),
         }
