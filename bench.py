@@ -75,7 +75,7 @@ def parse():
     p.add_argument("--no-host-io", action="store_true",
                    help="skip the host-buffer (PCIe-inclusive) timing")
     p.add_argument("--cpu-seconds", type=float, default=None,
-                   help="target length of each CPU baseline sample (default 15 s, 8 s "
+                   help="target length of each CPU baseline sample (default 15 s, 10 s "
                         "per config for --config all)")
     p.add_argument("--kmeans-init", default="random", choices=["random", "kmeans++"],
                    help="c3train: the seeding (random rows or k-means++ on the device)")
@@ -87,7 +87,7 @@ def parse():
     a.steps = s if a.steps is None else a.steps
     a.warmup = w if a.warmup is None else a.warmup
     if a.cpu_seconds is None:
-        a.cpu_seconds = 8.0 if a.config == "all" else 15.0
+        a.cpu_seconds = 10.0 if a.config == "all" else 15.0
     return a
 
 
@@ -132,22 +132,32 @@ def host_threads():
 
 def cpu_sample(run, nq_total, target_s, threads):
     """Times ``run(m)`` (the oracle over the first m queries, all threads):
-    one probe round of ``threads`` queries, then a sample sized to about
-    target_s seconds (the whole set repeated when it is quicker).  Returns
-    (queries/s, m, repeats, seconds, result of the last call)."""
+    a warm-up and a probe round of ``threads`` queries, then samples sized
+    from the last measured rate until one lasts at least half of target_s
+    (the whole set repeated when it is quicker).  A probe underestimates the
+    rate of a large sample (the flat oracle keeps one thread per 4-query
+    group busy), hence the re-sizing.  Returns (queries/s, m, repeats,
+    seconds, result of the last call)."""
     m0 = min(nq_total, threads)
-    t0 = time.perf_counter()
     run(m0)
-    per = time.perf_counter() - t0
-    rounds = max(1, int(target_s / max(per, 1e-4)))
-    m = min(nq_total, rounds * m0)
-    reps = 1
-    if m == nq_total:  # whole query set is quick: repeat it
-        reps = max(1, int(target_s / max(per * nq_total / m0, 1e-4)))
     t0 = time.perf_counter()
-    for _ in range(reps):
-        res = run(m)
+    res = run(m0)
     el = time.perf_counter() - t0
+    m, reps = m0, 1
+    for _ in range(4):
+        if el >= 0.5 * target_s:
+            break
+        per_q = max(el, 1e-4) / (m * reps)
+        want = max(1, int(target_s / per_q))
+        nm = min(nq_total, want)
+        nreps = max(1, want // nq_total) if nm == nq_total else 1
+        if (nm, nreps) == (m, reps):
+            break
+        m, reps = nm, nreps
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            res = run(m)
+        el = time.perf_counter() - t0
     return m * reps / el, m, reps, el, res
 
 
