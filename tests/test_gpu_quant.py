@@ -131,8 +131,12 @@ def _pq_data(seed, n, d, M, ksub, nq, ncent=64):
     return x, q, cb
 
 
-@pytest.mark.parametrize("shape", [(20_000, 128, 16, 256, 30), (5000, 24, 6, 100, 9)])
+@pytest.mark.parametrize("shape", [(20_000, 128, 16, 256, 30), (5000, 24, 6, 100, 9),
+                                   (6000, 64, 4, 256, 70)])
 def test_pq_lut_encode_adc_bit_exact(ctx, shape):
+    """Tables, codes and ADC search bit-exact; the shapes cover the table
+    kernel's segment lengths 8, 4 and 16, fewer codewords than threads, and
+    two query batches (70 queries)."""
     n, d, M, ksub, nq = shape
     print(f"pq n={n} d={d} M={M} ksub={ksub} nq={nq}", flush=True)
     x, q, cb = _pq_data(n, n, d, M, ksub, nq)

@@ -74,6 +74,38 @@ __global__ void k_pq_lut(const float *q, int64_t nq, int32_t ldq,
   }
 }
 
+// lut[q][m][c] for segment lengths DS up to 32: block (query batch, m),
+// thread c = codeword c (codebooks hold at most 256) with the codeword in
+// registers; the batch's query segments are wave-uniform loads, and each
+// (q, m) row of the table is one coalesced store.  The sums are the same as
+// k_pq_lut's (j ascending, no FMA).
+constexpr int PQL_QB = 64;  // queries per block
+template <int DS>
+__global__ __launch_bounds__(256) void k_pq_lut_seg(const float *q, int64_t nq, int32_t ldq,
+                                                    const float *cb, int32_t M, int32_t ksub,
+                                                    float *lut) {
+#pragma clang fp contract(off)
+  const int32_t m = blockIdx.y;
+  const int64_t qa = (int64_t)blockIdx.x * PQL_QB;
+  const int64_t qb = qa + PQL_QB < nq ? qa + PQL_QB : nq;
+  const int32_t c = threadIdx.x;
+  if (c >= ksub) return;
+  float cw[DS];
+  const float *cp = cb + ((int64_t)m * ksub + c) * DS;
+#pragma unroll
+  for (int j = 0; j < DS; ++j) cw[j] = cp[j];
+  for (int64_t qi = qa; qi < qb; ++qi) {
+    const float *qs = q + qi * ldq + (int64_t)m * DS;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+      const float t = qs[j] - cw[j];
+      s = s + t * t;
+    }
+    lut[(qi * M + m) * ksub + c] = s;
+  }
+}
+
 // codes[i][m] = argmin_c |x_m - C_m[c]|^2 (strict '<': the first minimum
 // wins), each sum over j in ascending order without FMA.  Block (bx, m):
 // codebook m staged in LDS (every lane reads the same codeword, a broadcast),
@@ -723,8 +755,22 @@ static const float *pq_queries(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
 static void pq_lut_device(vsk_ctx *ctx, const vsk_pq *pq, const float *dq,
                           int64_t nq, float *lut) {
   KernelTimer t(ctx, "pq_lut");
-  k_pq_lut<<<grid1(nq * pq->M * pq->ksub), 256, 0, ctx->stream>>>(
-      dq, nq, pq->d, pq->codebooks.as<float>(), pq->M, pq->ksub, pq->dsub, lut);
+  const dim3 grid((unsigned)ceil_div(nq, PQL_QB), (unsigned)pq->M);
+  const float *cb = pq->codebooks.as<float>();
+  if (ceil_div(nq, PQL_QB) > 0x7FFFFFFF || pq->M > 65535)
+    fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries or segments");
+  if (pq->ksub > 256) fail(VSK_ERR_INVALID_ARGUMENT, "codebooks hold at most 256 codewords");
+  switch (pq->dsub) {
+  case 1: k_pq_lut_seg<1><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  case 2: k_pq_lut_seg<2><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  case 4: k_pq_lut_seg<4><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  case 8: k_pq_lut_seg<8><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  case 16: k_pq_lut_seg<16><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  case 32: k_pq_lut_seg<32><<<grid, 256, 0, ctx->stream>>>(dq, nq, pq->d, cb, pq->M, pq->ksub, lut); break;
+  default:
+    k_pq_lut<<<grid1(nq * pq->M * pq->ksub), 256, 0, ctx->stream>>>(
+        dq, nq, pq->d, cb, pq->M, pq->ksub, pq->dsub, lut);
+  }
   check_launch("pq_lut");
 }
 
