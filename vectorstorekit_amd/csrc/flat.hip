@@ -219,41 +219,44 @@ __device__ inline float valu_final(float s) {
   else return s;
 }
 
-template <int MODE, int OP>
+template <int MODE, int OP, int U, int V>
 __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) {
 #pragma clang fp contract(off)
-  __shared__ float xs[FB_N * LS];
-  __shared__ float qs[FB_Q * LS];
+  // a tile of 32 U rows x 8 V queries; thread (rsub, qsub) owns rows
+  // rsub + 32 u and queries qsub + 8 v
+  static_assert(V % 4 == 0, "queries are staged 32 at a time");
+  __shared__ float xs[32 * U * LS];
+  __shared__ float qs[8 * V * LS];
   const int tid = threadIdx.x;
-  const int64_t q0 = (int64_t)blockIdx.x * FB_Q;
+  const int64_t q0 = (int64_t)blockIdx.x * (8 * V);
   const int64_t s0 = a.r0 + (int64_t)blockIdx.y * a.rows_per_split;
   int64_t s1 = s0 + a.rows_per_split;
   if (s1 > a.r1) s1 = a.r1;
   if (s0 >= s1) return;
   const int rsub = tid & 31, qsub = tid >> 5;
-  int64_t qi[8];
-  bool qok[8];
-  uint64_t th[8];
-  uint64_t best[8];
+  int64_t qi[V];
+  bool qok[V];
+  uint64_t th[V];
+  uint64_t best[V];
 #pragma unroll
-  for (int v = 0; v < 8; ++v) {
+  for (int v = 0; v < V; ++v) {
     qi[v] = q0 + qsub + 8 * v;
     qok[v] = qi[v] < a.nq && (!a.active || a.active[qi[v]]);
     th[v] = (MODE == MODE_FILTER && qok[v]) ? a.thresh[qi[v]] : 0;
     best[v] = VSK_KEY_NONE;
   }
   const int crow = tid >> 3, ccol = (tid & 7) * 4;
-  for (int64_t t0 = s0; t0 < s1; t0 += FB_N) {
-    float acc[4][8];
+  for (int64_t t0 = s0; t0 < s1; t0 += 32 * U) {
+    float acc[U][V];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int v = 0; v < 8; ++v) acc[u][v] = 0.f;
+      for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
     for (int k0 = 0; k0 < a.kdim; k0 += FB_K) {
       const bool kin = k0 + ccol < a.kdim;
       __syncthreads();
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < U; ++u) {
         int64_t grow = t0 + u * 32 + crow;
         f4 v = (kin && grow < s1)
                    ? *reinterpret_cast<const f4 *>(a.X + grow * a.ldx + k0 +
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
         p[3] = v.w;
       }
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < V / 4; ++u) {
         int64_t gq = q0 + u * 32 + crow;
         f4 v = (kin && gq < a.nq)
                    ? *reinterpret_cast<const f4 *>(a.Q + gq * a.ldq + k0 +
@@ -281,23 +284,23 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
       __syncthreads();
       const int kend = a.kdim - k0 < FB_K ? a.kdim - k0 : FB_K;
       for (int kk = 0; kk < kend; ++kk) {
-        float xv[4], qv[8];
+        float xv[U], qv[V];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xv[u] = xs[(rsub + 32 * u) * LS + kk];
+        for (int u = 0; u < U; ++u) xv[u] = xs[(rsub + 32 * u) * LS + kk];
 #pragma unroll
-        for (int v = 0; v < 8; ++v) qv[v] = qs[(qsub + 8 * v) * LS + kk];
+        for (int v = 0; v < V; ++v) qv[v] = qs[(qsub + 8 * v) * LS + kk];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int v = 0; v < 8; ++v) acc[u][v] += valu_term<OP>(qv[v], xv[u]);
+          for (int v = 0; v < V; ++v) acc[u][v] += valu_term<OP>(qv[v], xv[u]);
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t row = t0 + rsub + 32 * u;
       if (row >= s1) continue;
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
+      for (int v = 0; v < V; ++v) {
         if (!qok[v]) continue;
         const float dist = valu_final<OP>(acc[u][v]);
         if constexpr (MODE == MODE_ARGMIN) {
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
   if constexpr (MODE == MODE_ARGMIN) {
     // the 32 lanes with equal qsub hold disjoint rows of the same queries
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
+    for (int v = 0; v < V; ++v) {
       uint64_t b = best[v];
 #pragma unroll
       for (int m = 16; m > 0; m >>= 1) {
@@ -338,17 +341,41 @@ static void launch_mfma(vsk_ctx *ctx, dim3 grid, const FlatArgs &a, int mode) {
     k_flat_mfma<MODE_MATRIX, METRIC><<<grid, 256, 0, ctx->stream>>>(a);
 }
 
-template <int OP>
+template <int OP, int U, int V>
 static void launch_valu(vsk_ctx *ctx, dim3 grid, const FlatArgs &a, int mode,
                         int32_t *argmin) {
   if (mode == MODE_DENSE)
-    k_flat_valu<MODE_DENSE, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+    k_flat_valu<MODE_DENSE, OP, U, V><<<grid, 256, 0, ctx->stream>>>(a, argmin);
   else if (mode == MODE_FILTER)
-    k_flat_valu<MODE_FILTER, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+    k_flat_valu<MODE_FILTER, OP, U, V><<<grid, 256, 0, ctx->stream>>>(a, argmin);
   else if (mode == MODE_MATRIX)
-    k_flat_valu<MODE_MATRIX, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+    k_flat_valu<MODE_MATRIX, OP, U, V><<<grid, 256, 0, ctx->stream>>>(a, argmin);
   else
-    k_flat_valu<MODE_ARGMIN, OP><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+    k_flat_valu<MODE_ARGMIN, OP, U, V><<<grid, 256, 0, ctx->stream>>>(a, argmin);
+}
+
+// the exact VALU scan in tiles of 128 rows x 64 queries, or, when those
+// leave fewer than 4 workgroups per CU, 64 rows x 32 queries (a quarter of
+// the work per thread: small problems are latency-bound)
+template <int OP>
+static void launch_valu_sized(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin,
+                              bool small) {
+  const int64_t rows = a.r1 - a.r0;
+  const int64_t tq = small ? 32 : FB_Q, tn = small ? 64 : FB_N;
+  const int64_t qt = ceil_div(a.nq, tq);
+  int64_t splits = mode == MODE_ARGMIN ? 1 : ceil_div(4096, qt);
+  const int64_t max_splits = ceil_div(rows, tn);
+  if (splits > max_splits) splits = max_splits;
+  if (splits > 65535) splits = 65535;
+  if (splits < 1) splits = 1;
+  a.rows_per_split = ceil_div(ceil_div(rows, splits), tn) * tn;
+  splits = ceil_div(rows, a.rows_per_split);
+  if (qt > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
+  const dim3 grid((unsigned)qt, (unsigned)splits);
+  if (small)
+    launch_valu<OP, 2, 4>(ctx, grid, a, mode, argmin);
+  else
+    launch_valu<OP, 4, 8>(ctx, grid, a, mode, argmin);
 }
 
 // grid: query tiles x row splits, enough workgroups to fill 256 CUs (argmin
@@ -374,13 +401,14 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
   const char *name = names[valu ? 1 : 0][mode];
   KernelTimer t(ctx, name, (double)a.nq * (double)rows);
   if (valu) {
+    const bool small = mode != MODE_ARGMIN && qt * splits < 4 * (int64_t)ctx->cu_count;
     switch (a.metric) {
-    case VSK_METRIC_L1: launch_valu<OP_L1>(ctx, grid, a, mode, argmin); break;
-    case VSK_METRIC_HAMMING: launch_valu<OP_HAM>(ctx, grid, a, mode, argmin); break;
-    case METRIC_L2_EXACT: launch_valu<OP_L2SEQ>(ctx, grid, a, mode, argmin); break;
-    case METRIC_L2SQ_EXACT: launch_valu<OP_L2SQSEQ>(ctx, grid, a, mode, argmin); break;
-    case METRIC_CN_EXACT: launch_valu<OP_CNSEQ>(ctx, grid, a, mode, argmin); break;
-    case METRIC_DOT_EXACT: launch_valu<OP_DOTSEQ>(ctx, grid, a, mode, argmin); break;
+    case VSK_METRIC_L1: launch_valu_sized<OP_L1>(ctx, a, mode, argmin, small); break;
+    case VSK_METRIC_HAMMING: launch_valu_sized<OP_HAM>(ctx, a, mode, argmin, small); break;
+    case METRIC_L2_EXACT: launch_valu_sized<OP_L2SEQ>(ctx, a, mode, argmin, small); break;
+    case METRIC_L2SQ_EXACT: launch_valu_sized<OP_L2SQSEQ>(ctx, a, mode, argmin, small); break;
+    case METRIC_CN_EXACT: launch_valu_sized<OP_CNSEQ>(ctx, a, mode, argmin, small); break;
+    case METRIC_DOT_EXACT: launch_valu_sized<OP_DOTSEQ>(ctx, a, mode, argmin, small); break;
     default: fail(VSK_ERR_INVALID_ARGUMENT, "no exact kernel for this metric");
     }
   } else {

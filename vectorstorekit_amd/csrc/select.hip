@@ -241,7 +241,9 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   if (a.k < 1 || a.k > VSK_MAX_K)
     fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
   KernelTimer t(ctx, name);
-  if (a.seg_off || a.regs)
+  if (a.regs && !a.seg_off && a.cap + a.k > 32 * SEL_THREADS)
+    k_select<64><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  else if (a.seg_off || a.regs)
     k_select<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   else
     k_select<0><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
@@ -273,8 +275,14 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
                       const char *select_name, int64_t max_growth,
                       const TopkWorkspace *ws) {
   if (nq <= 0) return;
-  fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
-  if (n <= 0) return;
+  if (n <= 0) {
+    fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);
+    return;
+  }
+  // The first chunk is dense and taken by every query: its selection reads
+  // no previous list and no counts (each query has exactly cap keys) and
+  // writes every query's list and threshold, so neither needs clearing
+  // (three fewer launches per call, which small problems notice).
   if (cap > n) cap = n;  // the whole database is one dense chunk
   TopkWorkspace w;
   if (ws) {
@@ -292,7 +300,6 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
   uint64_t *thresh = w.thresh, *cand = w.cand;
   int32_t *counts = w.counts, *seg_n = w.seg_n, *ovf_count = w.ovf_count;
   uint8_t *ovf_mask = w.ovf_mask;
-  fill_u64(ctx, thresh, nq, VSK_KEY_NONE);
 
   int64_t r0 = 0;
   bool first = true;
@@ -310,7 +317,7 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
       if (c > n - r0) c = n - r0;
     }
     const bool dense = first;
-    fill_i32(ctx, counts, nq, dense ? (int32_t)c : 0);
+    if (!dense) fill_i32(ctx, counts, nq, 0);
     int32_t nseg = 0;
     int64_t seg_stride = 0;
     {
@@ -325,13 +332,15 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     SelectArgs sa;
     sa.nq = nq;
     sa.k = k;
-    sa.prev = best;
+    sa.prev = dense ? nullptr : best;
     sa.cand = cand;
     sa.cap = cap;
-    sa.counts = counts;
+    sa.counts = dense ? nullptr : counts;
     sa.best_out = best;
     sa.thresh = thresh;
-    sa.regs = dense && cap + k <= 32 * SEL_THREADS;  // e.g. IVF probing over the centroids
+    // small dense lists (IVF probing over the centroids, small problems)
+    // are read into registers once
+    sa.regs = dense && cap + k <= 64 * SEL_THREADS;
     if (!dense) {
       fill_i32(ctx, ovf_count, 1, 0);
       fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
