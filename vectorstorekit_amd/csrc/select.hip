@@ -241,7 +241,9 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   if (a.k < 1 || a.k > VSK_MAX_K)
     fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
   KernelTimer t(ctx, name);
-  if (a.regs && !a.seg_off && a.cap + a.k > 32 * SEL_THREADS)
+  // keys per query: the previous list (k) and up to cap candidates
+  const int64_t most = a.cap + (a.prev ? a.k : 0);
+  if (a.regs && !a.seg_off && most > 32 * SEL_THREADS)
     k_select<64><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   else if (a.seg_off || a.regs)
     k_select<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
@@ -340,7 +342,7 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     sa.thresh = thresh;
     // small dense lists (IVF probing over the centroids, small problems)
     // are read into registers once
-    sa.regs = dense && cap + k <= 64 * SEL_THREADS;
+    sa.regs = dense && cap <= 64 * SEL_THREADS;  // (no previous list)
     if (!dense) {
       fill_i32(ctx, ovf_count, 1, 0);
       fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
