@@ -211,6 +211,14 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   __syncthreads();
   int m = sel_count;
   if (m > k) m = k;  // cannot happen with distinct keys; keeps LDS in range
+  if (!a.sorted) {
+    // the set and a threshold: T bounds the selected keys and no other key
+    // lies at or below it (taken whole: the largest key)
+    uint64_t *out = a.best_out + q * (int64_t)k;
+    for (int i = tid; i < k; i += SEL_THREADS) out[i] = i < m ? sel[i] : VSK_KEY_NONE;
+    if (tid == 0 && a.thresh) a.thresh[q] = m < k ? VSK_KEY_NONE : (take_all ? hi : T);
+    return;
+  }
   int P2 = 1;
   while (P2 < m) P2 <<= 1;
   for (int i = m + tid; i < P2; i += SEL_THREADS) sel[i] = VSK_KEY_NONE;
@@ -340,6 +348,8 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     sa.counts = dense ? nullptr : counts;
     sa.best_out = best;
     sa.thresh = thresh;
+    // only the last chunk's list is returned: the others stay unsorted
+    sa.sorted = r0 + c >= n;
     // small dense lists (IVF probing over the centroids, small problems)
     // are read into registers once
     sa.regs = dense && cap <= 64 * SEL_THREADS;  // (no previous list)

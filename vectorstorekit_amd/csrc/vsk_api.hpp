@@ -65,6 +65,10 @@ struct SelectArgs {
   int32_t nseg = 0;
   int64_t seg_stride = 0;
   bool regs = false;  // small lists: the register-resident variant
+  // false: best_out gets the k smallest keys in no particular order and
+  // thresh a key T with exactly those k keys <= T (a chunk's list that only
+  // the next chunk's selection reads)
+  bool sorted = true;
 };
 void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name);
 
