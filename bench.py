@@ -629,7 +629,12 @@ def setup(c, a, ctx, dev):
                 "centre + 0.5 N(0,I) (seeds 5, 1, 2); codebooks: 8 Lloyd iterations "
                 "per segment on the first 65,536 rows (GPU assignment)",
         "dtype": "u8 codes, f32 LUT", "nq": nq, "n": n, "d": d, "M": M,
-        "kernels": [("pq_adc_filter", "k_pq_adc16<FILTER> (8 queries per workgroup)", "lds_pq"),
+        # filtered chunks: the bf16 screen over the decoded rows (one bf16
+        # product per pair), then the survivors' exact ADC sums; the dense
+        # first chunk: the LUT scan
+        "kernels": [("flat_screen_filter", "k_flat_screen<FILTER> over the decoded PQ rows",
+                     "mfma_bf16"),
+                    ("pq_adc_filter", "k_pq_adc16<FILTER> (8 queries per workgroup)", "lds_pq"),
                     ("pq_adc_dense", "k_pq_adc16<DENSE> (8 queries per workgroup)", "lds_pq")],
         "keep": (pq, db, x, q, codes, dist, ids),
     }

@@ -180,6 +180,55 @@ def test_pq_rerank_bit_exact(ctx, metric):
     np.testing.assert_array_equal(gd, od)
 
 
+@pytest.mark.parametrize("shape", [(200_000, 32, 8, 256, 40, 300, 50),
+                                   (60_000, 128, 16, 256, 20, 1000, 100),
+                                   (60_000, 64, 32, 64, 25, 200, 20)])
+def test_pq_screen_bit_exact(shape):
+    """The ADC scan through the bf16 screen (forced at these sizes): decoded
+    rows in a bf16 plane, the flat screen with each query's exact threshold
+    plus the bound, the survivors' exact ADC keys.  Segment lengths 4, 8 and
+    2; one or two filtered chunks after the dense first; with and without
+    the L1 re-rank; rows added after the plane was made.  Bit-exact against
+    the oracle."""
+    import os
+
+    from vectorstorekit_amd import Context
+
+    n, d, M, ksub, nq, k_adc, k = shape
+    print(f"pq screen n={n} d={d} M={M} nq={nq} kadc={k_adc} k={k}", flush=True)
+    x, q, cb = _pq_data(n + d, n, d, M, ksub, nq)
+    codes = O.pq_encode(x, cb)
+    old = os.environ.get("VSK_FLAT_KERNEL")
+    os.environ["VSK_FLAT_KERNEL"] = "screen"
+    try:
+        sctx = Context(0)
+    finally:
+        if old is None:
+            del os.environ["VSK_FLAT_KERNEL"]
+        else:
+            os.environ["VSK_FLAT_KERNEL"] = old
+    sctx.profile(True)
+    pq = ProductQuantizer(sctx, cb)
+    pq.add(codes)
+    gd, gi = pq.search(q, k, k_adc=k_adc)
+    assert "pq_screen_rescore" in sctx.profile_stats(), "the screen did not run"
+    od, oi = O.pq_search(q, cb, codes, k_adc, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    db = VectorDatabase(sctx, x)
+    gd, gi = pq.search(q, k, k_adc=k_adc, rerank_metric=METRIC_L1, rerank_db=db)
+    od, oi = O.pq_search(q, cb, codes, k_adc, k, x=x, rerank_metric=O.L1)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    # rows added after the plane was made: it is made again
+    pq.add(codes[:5000])
+    gd, gi = pq.search(q[:5], k, k_adc=k_adc)
+    od, oi = O.pq_search(q[:5], cb, np.concatenate([codes, codes[:5000]]), k_adc, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    sctx.close()
+
+
 def test_pq_upload_one_call_matches_create_add(ctx):
     x, q, cb = _pq_data(6, 12_000, 32, 4, 256, 15)
     codes = O.pq_encode(x, cb)

@@ -66,6 +66,21 @@ struct FlatArgs {
   float *amin;
 };
 
+// bf16 of an fp32 value, round to nearest even (NaN stays NaN)
+__device__ inline uint16_t bf16_rn(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFF) ? 0x40 : 0));
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// float not below a non-negative double (the error bounds round up)
+__device__ inline float f_up(double v) {
+  float f = (float)v;
+  if ((double)f < v) f = __uint_as_float(__float_as_uint(f) + 1u);
+  return f;
+}
+
 // bf16 hi/lo operand planes of the bf16x3 kernel
 struct SplitPtrs {
   const uint16_t *xh, *xl;  // row planes, stride ldxb

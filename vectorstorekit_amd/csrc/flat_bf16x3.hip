@@ -41,19 +41,6 @@ constexpr int kBufFlags = 0x00020000;  // buffer descriptor word 3 (raw, dword d
 constexpr int kWaitAll = 0x0000;
 constexpr int kWaitVm8 = 0x0F78;
 
-__device__ inline uint16_t bf16_rn(float v) {
-  uint32_t u = __float_as_uint(v);
-  if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFF) ? 0x40 : 0));
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-// float not below a non-negative double (the error bounds round up)
-__device__ inline float f_up(double v) {
-  float f = (float)v;
-  if ((double)f < v) f = __uint_as_float(__float_as_uint(f) + 1u);
-  return f;
-}
 
 // hi = bf16(v) and (when lo is given) lo = bf16(v - hi) planes of an
 // (n x ld) fp32 matrix, zero-padded to ldb columns, one wave per row.  With

@@ -32,6 +32,14 @@ struct vsk_pq {
   std::vector<float> host_codebooks;  // the same, for identity checks and files
   vsk::DevBuf codes;      // n x M uint8
   int64_t n = 0, cap_rows = 0;
+  // the bf16 screen of the ADC scan: the decoded rows x^ (each segment's
+  // codeword) as a bf16 plane of xldb columns, |x^|^2 per row, and the
+  // maxima over the rows of |bf16(x^)| and |x^ - bf16(x^)|; made by the
+  // first screened search and again when rows were added since (xrows)
+  mutable vsk::DevBuf xplane, xsq;
+  mutable int32_t xldb = 0;
+  mutable int64_t xrows = 0;
+  mutable double xh_max = 0, xr_max = 0;
 };
 
 namespace vsk {
@@ -601,6 +609,213 @@ static void launch_adc16(vsk_ctx *ctx, const AdcArgs &in, bool dense) {
   check_launch("pq_adc16");
 }
 
+// ---------------------------------------------------------------------------
+// The ADC scan through the bf16 matrix cores.  The ADC distance of a row is
+// a sequential fp32 sum of d squared differences q_j - x^_j (segment by
+// segment, then over the segments), x^ the row's decoded codewords: the
+// same kind of sum the flat screen's L2^2 bound covers.  So the flat screen
+// kernel runs over the decoded rows (a bf16 plane) and keeps every row whose
+// screened distance a(x) is within eps(q) of the query's exact threshold
+// key: a row whose ADC key is at most that threshold has a(x) <= ADC + eps.
+// The survivors' keys are then rescored exactly (the LUT sum in m order,
+// as the LUT scan adds it) and those above the threshold dropped, so the
+// selection sees exactly the keys the LUT scan would have kept.
+// ---------------------------------------------------------------------------
+
+// decoded rows: M lanes per row (M divides 64), lane m decodes segment m
+template <int DS>
+__global__ __launch_bounds__(256) void k_pq_plane(const uint8_t *codes, int64_t n, int32_t M,
+                                                  int32_t ksub, const float *cb, int32_t ldb,
+                                                  uint16_t *plane, float *sq,
+                                                  uint32_t *maxbits) {
+#pragma clang fp contract(off)
+  const int rpb = 256 / M;
+  const int m = threadIdx.x % M;
+  const int64_t r = (int64_t)blockIdx.x * rpb + threadIdx.x / M;
+  const bool valid = r < n;
+  float s2 = 0.f;
+  double sh = 0.0, sr = 0.0;
+  if (valid) {
+    const float *c = cb + ((int64_t)m * ksub + codes[r * M + m]) * DS;
+    uint16_t h[DS];
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+      const float v = c[j];
+      h[j] = bf16_rn(v);
+      const float hv = __uint_as_float((uint32_t)h[j] << 16);
+      const float rv = v - hv;
+      s2 = s2 + v * v;
+      sh += (double)hv * (double)hv;
+      sr += (double)rv * (double)rv;
+    }
+    uint16_t *dst = plane + r * ldb + m * DS;
+    if constexpr (DS % 2 == 0) {
+#pragma unroll
+      for (int j = 0; j < DS; j += 2)
+        *reinterpret_cast<uint32_t *>(dst + j) = (uint32_t)h[j] | ((uint32_t)h[j + 1] << 16);
+    } else {
+#pragma unroll
+      for (int j = 0; j < DS; ++j) dst[j] = h[j];
+    }
+  }
+  // the row's sums over its M lanes (aligned groups within the wave)
+  for (int o = M >> 1; o > 0; o >>= 1) {
+    s2 += __shfl_xor(s2, o);
+    sh += __shfl_xor(sh, o);
+    sr += __shfl_xor(sr, o);
+  }
+  if (valid && m == 0) sq[r] = s2;
+  uint32_t mh = valid ? __float_as_uint(f_up(sqrt(sh) * (1.0 + 1e-12))) : 0u;
+  uint32_t mr = valid ? __float_as_uint(f_up(sqrt(sr) * (1.0 + 1e-12))) : 0u;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t a = __shfl_xor(mh, o), b = __shfl_xor(mr, o);
+    mh = a > mh ? a : mh;
+    mr = b > mr ? b : mr;
+  }
+  if ((threadIdx.x & 63) == 0 && (mh | mr)) {
+    atomicMax(&maxbits[0], mh);
+    atomicMax(&maxbits[1], mr);
+  }
+}
+
+// the screen's filter threshold of each query: its exact threshold's
+// distance plus eps(q), every row id (NONE stays NONE).  eps is the flat
+// screen's L2^2 bound with x^ for x: 2 e_dot + (2d + 8) u (|q| + |x^|)^2,
+// where e_dot = |qh||dx| + |dq||xh| + |dq||dx| + 2(d-1)u|qh||xh| bounds the
+// bf16 dot's error and the second term the rounding of |q|^2, |x^|^2, the
+// screen's last operations and the ADC sum itself (at most d + 2 roundings of
+// a sum bounded by (|q| + |x^|)^2).
+__global__ void k_pq_screen_thresh(const uint64_t *thresh, int64_t nq, const float *qnh,
+                                   const float *qnr, double xh, double xr, int32_t d,
+                                   uint64_t *out) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  const uint64_t t = thresh[q];
+  if (t == VSK_KEY_NONE) {
+    out[q] = VSK_KEY_NONE;
+    return;
+  }
+  const double u = 0x1p-24, dd = (double)d;
+  const double qh = qnh[q], qr = qnr[q], qn = qh + qr, xn = xh + xr;
+  const double e_dot =
+      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
+  const double eps = (2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05) * 1.0001;
+  const double lim = (double)vsk_ord2f((uint32_t)(t >> 32)) + eps;
+  out[q] = vsk_key(f_up(lim), 0xFFFFFFFFu);
+}
+
+// exact ADC keys of the screen's survivors, in place (a workgroup per
+// query, its table in LDS): the sum of lut[q][m][code_m] in m order from
+// 0, as the LUT scan adds it; keys above the exact threshold become NONE.
+// A row's M code bytes load as whole 4- or 16-byte words.  Segmented lists
+// (seg_n) or appended ones (counts, capped at cap).
+template <int M>
+__global__ __launch_bounds__(256) void k_pq_rescore_keys(
+    const uint8_t *codes, int32_t ksub, const float *lut, const uint64_t *thresh,
+    const uint8_t *active, uint64_t *cand, int64_t cap, const int32_t *counts,
+    const int32_t *seg_n, int32_t nseg, int64_t seg_stride) {
+#pragma clang fp contract(off)
+  extern __shared__ float lut_s[];  // M x ksub
+  const int64_t q = blockIdx.x;
+  if (active && !active[q]) return;
+  const int mk = M * ksub;
+  for (int i = threadIdx.x; i < mk; i += 256) lut_s[i] = lut[q * mk + i];
+  __syncthreads();
+  const uint64_t th = thresh[q];
+  constexpr int NW = M >= 4 ? M / 4 : 1;  // 32-bit words per code row
+  auto rescore = [&](uint64_t &key) {
+    if (key == VSK_KEY_NONE) return;
+    const uint32_t row = (uint32_t)key;
+    const uint8_t *c = codes + (int64_t)row * M;
+    uint32_t w[NW];
+    if constexpr (M >= 16) {
+#pragma unroll
+      for (int i = 0; i < M / 16; ++i) {
+        const uint4 v = reinterpret_cast<const uint4 *>(c)[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+      }
+    } else if constexpr (M >= 4) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = reinterpret_cast<const uint32_t *>(c)[i];
+    } else {
+      w[0] = 0;
+#pragma unroll
+      for (int m = 0; m < M; ++m) w[0] |= (uint32_t)c[m] << (8 * m);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) s = s + lut_s[m * ksub + ((w[m >> 2] >> (8 * (m & 3))) & 0xFFu)];
+    const uint64_t ek = vsk_key(s, row);
+    key = ek <= th ? ek : VSK_KEY_NONE;
+  };
+  uint64_t *base = cand + q * cap;
+  if (seg_n) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int sgi = w; sgi < nseg; sgi += 4) {
+      const int32_t ns = seg_n[q * nseg + sgi];
+      uint64_t *cs = base + (int64_t)sgi * seg_stride;
+      for (int32_t i = lane; i < ns; i += 64) rescore(cs[i]);
+    }
+  } else {
+    int64_t cnt = counts[q];
+    if (cnt > cap) return;  // overflowed: the chunk is re-scanned whole
+    for (int64_t i = threadIdx.x; i < cnt; i += 256) rescore(base[i]);
+  }
+}
+
+// the decoded plane of the screen, made when missing or stale
+static void pq_screen_plane(vsk_ctx *ctx, const vsk_pq *pq) {
+  if (pq->xrows == pq->n && pq->xplane.p) return;
+  const int32_t ldb = (pq->d + 63) & ~63;
+  pq->xplane.reserve(sizeof(uint16_t) * (size_t)pq->n * ldb);
+  pq->xsq.reserve(sizeof(float) * (size_t)pq->n);
+  uint16_t *plane = pq->xplane.as<uint16_t>();
+  if (ldb > pq->d) fill_i32(ctx, reinterpret_cast<int32_t *>(plane), (int64_t)pq->n * ldb / 2, 0);
+  uint32_t *mb = static_cast<uint32_t *>(ctx->scratch_ptr("pq.planemax", 2 * sizeof(uint32_t)));
+  fill_i32(ctx, reinterpret_cast<int32_t *>(mb), 2, 0);
+  const int64_t rpb = 256 / pq->M;
+  const unsigned grid = (unsigned)ceil_div(pq->n, rpb);
+  {
+    KernelTimer t(ctx, "pq_screen_plane", (double)pq->n);
+    const float *cb = pq->codebooks.as<float>();
+    const uint8_t *codes = pq->codes.as<uint8_t>();
+    float *sq = pq->xsq.as<float>();
+    switch (pq->dsub) {
+    case 1: k_pq_plane<1><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    case 2: k_pq_plane<2><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    case 4: k_pq_plane<4><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    case 8: k_pq_plane<8><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    case 16: k_pq_plane<16><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    default: k_pq_plane<32><<<grid, 256, 0, ctx->stream>>>(codes, pq->n, pq->M, pq->ksub, cb, ldb, plane, sq, mb); break;
+    }
+    check_launch("pq_screen_plane");
+  }
+  uint32_t hb[2];
+  VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  pq->xh_max = __builtin_bit_cast(float, hb[0]);
+  pq->xr_max = __builtin_bit_cast(float, hb[1]);
+  pq->xldb = ldb;
+  pq->xrows = pq->n;
+}
+
+// the screen serves a search of nq queries: segments of at most 32 values
+// whose count divides a wave, and a problem large enough that the screen's
+// fixed launches pay (forced by VSK_FLAT_KERNEL=screen, off by =exact)
+static bool pq_screen_applies(const vsk_ctx *ctx, const vsk_pq *pq, int64_t nq) {
+  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (pq->M < 1 || pq->M > 64 || (64 % pq->M) != 0) return false;
+  if (pq->dsub != 1 && pq->dsub != 2 && pq->dsub != 4 && pq->dsub != 8 && pq->dsub != 16 &&
+      pq->dsub != 32)
+    return false;
+  if (pq->n >= 0x7FFFFFFFll) return false;
+  return ctx->flat_force_screen || (double)nq * (double)pq->n * pq->d >= (double)(1ll << 30);
+}
+
 // exact distance of each ADC candidate, summed in index order (no FMA).
 // A workgroup takes 256 candidates of one query, a wave 64 of them: per
 // block of 64 dimensions the wave gathers its rows in 256-byte segments (16
@@ -959,6 +1174,16 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
       ctx->scratch_ptr("pq.best", sizeof(uint64_t) * nq * k_adc));
   const int64_t cap = default_cap(k_adc);
   const int64_t qb = query_batch(nq, cap);
+  // the bf16 screen: decoded rows (kept with the codes), the queries' bf16
+  // plane and norms, a threshold slot per query
+  const bool screen = pq_screen_applies(ctx, pq, nq);
+  ArgminQueries qp;
+  uint64_t *sthr = nullptr;
+  if (screen) {
+    pq_screen_plane(ctx, pq);
+    qp = argmin_queries(ctx, dq, nq, pq->d, pq->d, "pq.sq");
+    sthr = static_cast<uint64_t *>(ctx->scratch_ptr("pq.sthr", sizeof(uint64_t) * nq));
+  }
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     AdcArgs base{};
@@ -968,6 +1193,60 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
     base.lut = lut + b0 * pq->M * pq->ksub;
     base.nq = (int32_t)nb;
     ScanFn scan = [&](const ScanRequest &r) {
+      if (!r.dense && screen) {
+        // filtered chunks: the bf16 screen over the decoded rows, then the
+        // survivors' exact keys
+        k_pq_screen_thresh<<<(unsigned)ceil_div(nb, 256), 256, 0, ctx->stream>>>(
+            r.thresh, nb, qp.qnh + b0, qp.qnr + b0, pq->xh_max, pq->xr_max, pq->d, sthr);
+        check_launch("pq_screen_thresh");
+        FlatArgs f{};
+        f.xaux = pq->xsq.as<float>();
+        f.qaux = qp.qsq + b0;
+        f.kdim = pq->xldb;
+        f.nq = (int32_t)nb;
+        f.r0 = r.r0;
+        f.r1 = r.r1;
+        f.metric = VSK_METRIC_L2SQ;
+        f.thresh = sthr;
+        f.active = r.active;
+        f.cand = r.cand;
+        f.cap = r.cap;
+        f.counts = r.counts;
+        f.seg_n = r.seg_n;
+        SplitPtrs sp{};
+        sp.xh = pq->xplane.as<uint16_t>();
+        sp.qh = qp.qh + b0 * qp.ldb;
+        sp.ldxb = pq->xldb;
+        sp.ldqb = qp.ldb;
+        sp.kb = pq->xldb;
+        int32_t nseg = 0;
+        int64_t stride = 0;
+        launch_flat_screen(ctx, f, sp, MODE_FILTER, r.seg_n ? &nseg : nullptr,
+                           r.seg_n ? &stride : nullptr);
+        if (r.seg_nseg) *r.seg_nseg = nseg;
+        if (r.seg_stride) *r.seg_stride = stride;
+        {
+          KernelTimer t(ctx, "pq_screen_rescore");
+          const size_t lds = sizeof(float) * pq->M * pq->ksub;
+          const int32_t *sn = nseg > 0 ? r.seg_n : nullptr;
+          const uint8_t *cd = pq->codes.as<uint8_t>();
+#define PQ_RESCORE(MM)                                                                  \
+  k_pq_rescore_keys<MM><<<(unsigned)nb, 256, lds, ctx->stream>>>(                       \
+      cd, pq->ksub, base.lut, r.thresh, r.active, r.cand, r.cap, r.counts, sn, nseg, stride)
+          switch (pq->M) {
+          case 1: PQ_RESCORE(1); break;
+          case 2: PQ_RESCORE(2); break;
+          case 4: PQ_RESCORE(4); break;
+          case 8: PQ_RESCORE(8); break;
+          case 16: PQ_RESCORE(16); break;
+          case 32: PQ_RESCORE(32); break;
+          default: PQ_RESCORE(64); break;
+          }
+#undef PQ_RESCORE
+          check_launch("pq_screen_rescore");
+        }
+        return;
+      }
       AdcArgs a = base;
       a.r0 = r.r0;
       a.r1 = r.r1;
