@@ -1172,11 +1172,16 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
   pq_lut_device(ctx, pq, dq, nq, lut);
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("pq.best", sizeof(uint64_t) * nq * k_adc));
-  const int64_t cap = default_cap(k_adc);
-  const int64_t qb = query_batch(nq, cap);
   // the bf16 screen: decoded rows (kept with the codes), the queries' bf16
-  // plane and norms, a threshold slot per query
+  // plane and norms, a threshold slot per query.  Its chunks grow at most
+  // 4-8x: the survivors (k_adc times the growth, plus the bound's band) then
+  // stay well inside the screen's 256 slots per (row split, query), whose
+  // overflow costs a dense re-scan (measured at config 5: 8,192 slots,
+  // growth 4, 2 % faster than 16,384 and growth 8)
   const bool screen = pq_screen_applies(ctx, pq, nq);
+  const int64_t cap = screen ? std::max<int64_t>(default_cap(k_adc) / 2, 4 * (int64_t)k_adc)
+                             : default_cap(k_adc);
+  const int64_t qb = query_batch(nq, cap);
   ArgminQueries qp;
   uint64_t *sthr = nullptr;
   if (screen) {
@@ -1261,7 +1266,7 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
         launch_adc(ctx, a, r.dense);
     };
     progressive_topk(ctx, nb, pq->n, k_adc, cap, scan, best + b0 * k_adc,
-                     "pq_select");
+                     "pq_select", screen ? 8 : 0);
   }
   OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
