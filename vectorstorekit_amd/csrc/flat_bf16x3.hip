@@ -387,6 +387,14 @@ constexpr int XS_LDS = 2 * XS_STAGE + 6 * XS_Q * 4 + 2 * XS_Q * 8;
 // and the row norms of four row tiles (copied with the tile's first stage)
 constexpr int XS_LDS_TOP2 = XS_LDS + 4 * XS_Q * (8 + 4) + 4 * XS_N * 4;
 static_assert(XS_LDS_TOP2 <= 160 * 1024, "LDS of one workgroup");
+// filter mode on L2 and L2^2: the row norms of four row tiles in LDS too (a
+// global load in the epilogue would wait for every stage copy in flight)
+constexpr int XS_LDS_XA = XS_LDS + 4 * XS_N * 4;
+template <int MODE, int METRIC>
+constexpr bool xs_norms_in_lds() {
+  return MODE == MODE_TOP2 ||
+         (MODE == MODE_FILTER && (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2));
+}
 
 __device__ __forceinline__ float top2_keydist(uint64_t k) {
   return k == VSK_KEY_NONE ? __int_as_float(0x7f800000) : vsk_ord2f((uint32_t)(k >> 32));
@@ -456,7 +464,9 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   int64_t *s_pb = reinterpret_cast<int64_t *>(s_th + XS_Q);
   uint64_t *s_t1 = reinterpret_cast<uint64_t *>(lds + XS_LDS);  // [4][XS_Q]
   float *s_t2 = reinterpret_cast<float *>(s_t1 + 4 * XS_Q);
-  float *s_xa = s_t2 + 4 * XS_Q;  // [4][XS_N]: |x|^2 of row tile t in slot t & 3
+  // [4][XS_N]: |x|^2 of row tile t in slot t & 3
+  float *s_xa = MODE == MODE_TOP2 ? s_t2 + 4 * XS_Q : reinterpret_cast<float *>(lds + XS_LDS);
+  constexpr bool XA = xs_norms_in_lds<MODE, METRIC>();
   if constexpr (MODE == MODE_TOP2) {
     for (int i = tid; i < 4 * XS_Q; i += 512) {
       s_t1[i] = VSK_KEY_NONE;
@@ -531,7 +541,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     const int64_t rows = left < XS_N ? (left > 0 ? left : 0) : XS_N;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(s.xh + dt0 * s.ldxb), 0, (int32_t)(rows * ldx2), kBufFlags);
-    if constexpr (MODE == MODE_TOP2) {
+    if constexpr (XA) {
       if (dst == 0 && w < 4) {
         // the tile's row norms, 64 per wave (rows past the slice read 0)
         const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
@@ -745,8 +755,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int64_t row = rbase + i * 16 + r;
-              const float xa = (full || row < s1) ? a.xaux[row] : 0.f;
+              // (rows past the slice read 0 and are masked off below)
+              const float xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r];
               m |= (dist_from_dot<METRIC>(acc[i][j][r], qa, xa) > th_f)
                        ? 0u : (1u << (4 * i + r));
             }
@@ -780,7 +790,11 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             const float w0 = b2 ? u1 : u0, w1 = b2 ? u3 : u2;
             const float dot = (b & 8) ? w1 : w0;
             const int64_t row = rbase + 16 * (b >> 2) + (b & 3);
-            const float xa = a.xaux ? a.xaux[row] : 0.f;
+            float xa = 0.f;
+            if constexpr (XA)
+              xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * (b >> 2) + (b & 3)];
+            else if (a.xaux)
+              xa = a.xaux[row];
             const uint64_t key = vsk_key(dist_from_dot<METRIC>(dot, qa, xa), (uint32_t)row);
             if (key <= th) {
               const int pos = atomicAdd(&l_cnt[16 * j], 1);
@@ -835,7 +849,9 @@ static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a,
   if (mode == MODE_DENSE)
     k_flat_screen<MODE_DENSE, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
   else
-    k_flat_screen<MODE_FILTER, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
+    k_flat_screen<MODE_FILTER, METRIC><<<grid, 512,
+                                         xs_norms_in_lds<MODE_FILTER, METRIC>() ? XS_LDS_XA : lds,
+                                         ctx->stream>>>(a, s);
 }
 
 void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
@@ -854,13 +870,13 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2SQ>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_L2>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_COSINE_NORMALIZED>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
