@@ -751,6 +751,19 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
               m |= (acc[i][j][r] < tdot) ? 0u : (1u << (4 * i + r));
         } else {
           const float th_f = l_thf[16 * j];
+          // the block's smallest distance first, the same expression as the
+          // per-score test below (its max with 0 maps NaN to 0, so the two
+          // agree exactly): when it is above the bound in every lane, no
+          // score of the block can pass
+          float mn = __int_as_float(0x7f800000);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              mn = fminf(mn, dist_from_dot<METRIC>(
+                                 acc[i][j][r], qa,
+                                 s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r]));
+          if (!__builtin_amdgcn_ballot_w64(mn <= th_f)) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
