@@ -54,6 +54,93 @@ def test_ivf_bit_exact(ctx, shape):
     np.testing.assert_array_equal(gd, od)
 
 
+def _screen_ctx():
+    """A context whose list scans always take the bf16 screen."""
+    from vectorstorekit_amd import Context
+
+    old = os.environ.get("VSK_FLAT_KERNEL")
+    os.environ["VSK_FLAT_KERNEL"] = "screen"
+    try:
+        sctx = Context(0)
+    finally:
+        if old is None:
+            del os.environ["VSK_FLAT_KERNEL"]
+        else:
+            os.environ["VSK_FLAT_KERNEL"] = old
+    sctx.profile(True)
+    return sctx
+
+
+@pytest.mark.parametrize("shape", [(64, 20_000, 128, 200, 8, 10, "euclidean"),
+                                   (37, 5000, 33, 150, 5, 7, "euclideanSquared"),
+                                   (40, 12_000, 160, 90, 40, 100, "euclidean"),
+                                   (24, 9000, 256, 70, 6, 64, "euclideanSquared"),
+                                   (16, 3000, 24, 40, 16, 20, "euclidean")])
+def test_ivf_screen_bit_exact(shape):
+    """The list scan through the bf16 screen (forced at these sizes): query
+    groups of up to 64 per list, the kept screened keys per query, the bound
+    check and the exact rescore.  Plane widths of 2, 4, 6 and 8 k-steps, both
+    euclidean metrics, k above 64, every list probed; then rows added (the
+    plane is made again), and a block of identical rows that makes the check
+    fail for the queries next to it (their whole candidate set is rescored).
+    Bit-exact against the oracle."""
+    ncent, n, d, nq, nprobe, k, metric = shape
+    print(f"ivf screen ncent={ncent} n={n} d={d} nq={nq} nprobe={nprobe} k={k} {metric}",
+          flush=True)
+    sq = metric == "euclideanSquared"
+    x, q, c = _mixture(ncent + n + 1, ncent, n, d, nq)
+    ids = np.arange(n, dtype=np.int64) * 3 + 7
+    sctx = _screen_ctx()
+    idx = _index(sctx, c, x, ids, nprobe)
+    lists = O.ivf_assign(x, c)
+    gd, gi = idx.search(q, k, metric=metric)
+    assert "ivf_list_screen" in sctx.profile_stats(), "the screen did not run"
+    od, oi = O.ivf_search(q, x, ids, lists, c, nprobe, k, squared=sq)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    # rows added after the plane was made, among them 400 copies of one row
+    # next to the first queries
+    rng = np.random.default_rng(n)
+    dup = np.repeat(q[:1] + 0.01 * rng.standard_normal((1, d)).astype(np.float32), 400, 0)
+    extra = np.concatenate([x[:1000] + 0.1, dup]).astype(np.float32)
+    eids = np.arange(n, n + len(extra), dtype=np.int64) * 3 + 7
+    idx.insert(extra, eids)
+    x2 = np.concatenate([x, extra])
+    ids2 = np.concatenate([ids, eids])
+    lists2 = O.ivf_assign(x2, c)
+    before = sctx.profile_stats().get("ivf_screen_redo", (0, 0.0, 0.0))[2]
+    gd, gi = idx.search(q, k, metric=metric)
+    od, oi = O.ivf_search(q, x2, ids2, lists2, c, nprobe, k, squared=sq)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    # the fallback's work count is the number of queries that failed
+    assert sctx.profile_stats()["ivf_screen_redo"][2] > before, "no query failed the check"
+    sctx.close()
+
+
+def test_ivf_screen_unclustered_bit_exact():
+    """Rows without cluster structure (i.i.d. normal), many probes, so many
+    candidates lie within the screen's margin of the k-th.  Bit-exact
+    against the oracle, both euclidean metrics."""
+    rng = np.random.default_rng(77)
+    ncent, n, d, nq, nprobe, k = 64, 20_000, 48, 120, 24, 10
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    c = rng.standard_normal((ncent, d)).astype(np.float32)
+    sctx = _screen_ctx()
+    idx = _index(sctx, c, x, None, nprobe)
+    lists = O.ivf_assign(x, c)
+    ids = np.arange(n, dtype=np.int64)
+    for metric in ("euclidean", "euclideanSquared"):
+        print(f"ivf screen unclustered {metric}", flush=True)
+        gd, gi = idx.search(q, k, metric=metric)
+        od, oi = O.ivf_search(q, x, ids, lists, c, nprobe, k, squared=metric != "euclidean")
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    assert "ivf_list_screen" in sctx.profile_stats()
+    sctx.close()
+
+
 def test_ivf_build_one_call_matches_create_add(ctx):
     x, q, c = _mixture(11, 32, 6000, 40, 25)
     ids = np.arange(len(x), dtype=np.int64) * 5 + 1

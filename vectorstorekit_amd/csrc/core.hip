@@ -86,8 +86,19 @@ KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items, hipStr
 KernelTimer::~KernelTimer() {
   if (stat < 0) return;
   hipEvent_t b = ctx->take_event();
-  if (hipEventRecord(b, stream) == hipSuccess)
-    ctx->pending.push_back({stat, a, b, work});
+  if (hipEventRecord(b, stream) != hipSuccess) return;
+  int slot = -1;
+  if (work_dev) {
+    if (!ctx->work_pinned &&
+        hipHostMalloc(reinterpret_cast<void **>(&ctx->work_pinned),
+                      sizeof(int64_t) * vsk_ctx::kWorkSlots, hipHostMallocDefault) != hipSuccess)
+      ctx->work_pinned = nullptr;
+    if (ctx->work_pinned && ctx->work_used < vsk_ctx::kWorkSlots &&
+        hipMemcpyAsync(ctx->work_pinned + ctx->work_used, work_dev, sizeof(int64_t),
+                       hipMemcpyDeviceToHost, stream) == hipSuccess)
+      slot = ctx->work_used++;
+  }
+  ctx->pending.push_back({stat, a, b, work, slot});
 }
 
 void check_launch(const char *name) {
@@ -361,12 +372,13 @@ void vsk_ctx::resolve_pending() {
     if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
       stats[p.stat].launches += 1;
       stats[p.stat].total_ms += ms;
-      stats[p.stat].work += p.work;
+      stats[p.stat].work += p.work_slot >= 0 ? (double)work_pinned[p.work_slot] : p.work;
     }
     event_pool.push_back(p.a);
     event_pool.push_back(p.b);
   }
   pending.clear();
+  work_used = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -420,6 +432,7 @@ vsk_status vsk_destroy(vsk_ctx *ctx) {
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
   if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
   if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+  if (ctx->work_pinned) (void)hipHostFree(ctx->work_pinned);
   ctx->scratch.clear();
   (void)hipEventDestroy(ctx->call_begin);
   (void)hipEventDestroy(ctx->call_end);

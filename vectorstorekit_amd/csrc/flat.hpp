@@ -135,6 +135,22 @@ float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
              int32_t metric);
 // bf16 planes and norms of a query batch for screen_argmin: hi plane
 // (stride ldb = roundup(d, 64)), |hi|, |q - hi| and |q|^2 per query
+// the screen's bound check over each query's kc kept screen keys (see
+// flat_screen.hip): ok[q] when the kept keys hold the exact top k, and
+// nvalid[q] = how many kept keys lie within the bound's margin of the k-th
+struct CheckArgs {
+  const uint64_t *best;  // nq x kc screen keys, ascending, NONE last
+  int64_t nq;
+  int32_t k, kc, d, metric;
+  const float *qnh, *qnr;  // per query |qh|, |q - qh|
+  double xh, xr;           // maxima over the rows of |xh|, |x - xh|
+  uint8_t *ok;
+  int32_t *nvalid;
+  int32_t *fails;
+  bool test;  // false: count the valid keys only
+};
+void launch_screen_check(vsk_ctx *ctx, const CheckArgs &ca);
+
 struct ArgminQueries {
   const uint16_t *qh = nullptr;
   const float *qnh = nullptr, *qnr = nullptr, *qsq = nullptr;

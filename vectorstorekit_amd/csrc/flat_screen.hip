@@ -144,18 +144,6 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
   out[q * kc + c] = vsk_key(dist, row);
 }
 
-struct CheckArgs {
-  const uint64_t *best;  // nq x kc screen keys, ascending, NONE last
-  int64_t nq;
-  int32_t k, kc, d, metric;
-  const float *qnh, *qnr;  // per query |qh|, |q - qh|
-  double xh, xr;           // maxima over the rows of |xh|, |x - xh|
-  uint8_t *ok;
-  int32_t *nvalid;
-  int32_t *fails;
-  bool test;  // false: count the valid keys only
-};
-
 // the screen's error bound eps(q) for the metric (see the file comment)
 __device__ double screen_eps(const CheckArgs &a, int64_t q) {
   const double u = 0x1p-24;
@@ -206,6 +194,12 @@ __global__ void k_screen_check(CheckArgs a) {
   }
   a.ok[q] = good ? 1 : 0;
   if (!good) atomicAdd(a.fails, 1);
+}
+
+void launch_screen_check(vsk_ctx *ctx, const CheckArgs &ca) {
+  KernelTimer t(ctx, "screen_check");
+  k_screen_check<<<(unsigned)ceil_div(ca.nq, 256), 256, 0, ctx->stream>>>(ca);
+  check_launch("screen_check");
 }
 
 __global__ void k_gather_rows(const float *src, int64_t ld, const int32_t *idx,

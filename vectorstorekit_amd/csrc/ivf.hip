@@ -58,6 +58,15 @@ struct vsk_ivf {
   int32_t cper_dim = 0, cdsub = 0;
   // caller bytes stored with the index file (e.g. the index configuration)
   std::vector<uint8_t> meta;
+  // the bf16 screen of the list scan: the stored rows as a bf16 plane of
+  // xldb columns, |x|^2 per row and the maxima of |bf16(x)| and
+  // |x - bf16(x)| over the rows, valid while xversion == version (version
+  // counts the changes of the stored rows)
+  int64_t version = 0;
+  mutable int64_t xversion = -1;
+  mutable vsk::DevBuf xplane, xsq;
+  mutable int32_t xldb = 0;
+  mutable double xh_max = 0, xr_max = 0;
 };
 
 namespace vsk {
@@ -115,6 +124,108 @@ __global__ void k_group_pairs(const int32_t *probes, int64_t npairs, int32_t np,
   }
 }
 
+// exclusive prefix over a block of 1024 threads of NV values per thread,
+// continuing the running totals carry[0..NV) (shared memory)
+template <int NV>
+__device__ void block_scan_1024(const int64_t (&v)[NV], int64_t (&out)[NV],
+                                int64_t (*wsum)[NV], int64_t *carry) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t incl[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    incl[j] = v[j];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t u = __shfl_up(incl[j], o);
+      if (lane >= o) incl[j] += u;
+    }
+  }
+  if (lane == 63)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) wsum[w][j] = incl[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int64_t before = carry[j];
+    for (int i = 0; i < w; ++i) before += wsum[i][j];
+    out[j] = before + incl[j] - v[j];
+  }
+  __syncthreads();
+  if (t == 1023)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) carry[j] = out[j] + v[j];
+  __syncthreads();
+}
+
+// seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024)
+__global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_t m,
+                                                      int64_t *seg) {
+  __shared__ int64_t wsum[16][1];
+  __shared__ int64_t carry[1];
+  if (threadIdx.x == 0) carry[0] = 0;
+  __syncthreads();
+  for (int64_t base = 0; base < m; base += 1024) {
+    const int64_t i = base + threadIdx.x;
+    const int64_t v[1] = {i < m ? cnt[i] : 0};
+    int64_t o[1];
+    block_scan_1024<1>(v, o, wsum, carry);
+    if (i < m) seg[i] = o[0];
+  }
+  if (threadIdx.x == 0) seg[m] = carry[0];
+}
+
+// pairs per list
+__global__ void k_list_pair_counts(const int32_t *probes, int64_t npairs, int32_t *lcnt) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t l = probes[i];
+    if (l >= 0) atomicAdd(&lcnt[l], 1);
+  }
+}
+
+// per list: its first pair slot (lstart, and cursor for the pair scatter)
+// and its first group (gstart; ceil(pairs / G) groups for a list holding
+// rows, none for an empty one); totals at [nlist].  One block of 1024.
+__global__ __launch_bounds__(1024) void k_list_offsets(const int32_t *lcnt,
+                                                       const int64_t *list_off, int32_t nlist,
+                                                       int32_t G, int64_t *lstart,
+                                                       int64_t *cursor, int64_t *gstart) {
+  __shared__ int64_t wsum[16][2];
+  __shared__ int64_t carry[2];
+  if (threadIdx.x < 2) carry[threadIdx.x] = 0;
+  __syncthreads();
+  for (int64_t base = 0; base < nlist; base += 1024) {
+    const int64_t l = base + threadIdx.x;
+    int64_t v[2] = {0, 0};
+    if (l < nlist) {
+      v[0] = lcnt[l];
+      v[1] = v[0] > 0 && list_off[l + 1] > list_off[l] ? (v[0] + G - 1) / G : 0;
+    }
+    int64_t o[2];
+    block_scan_1024<2>(v, o, wsum, carry);
+    if (l < nlist) {
+      lstart[l] = o[0];
+      cursor[l] = o[0];
+      gstart[l] = o[1];
+    }
+  }
+  if (threadIdx.x == 0) {
+    lstart[nlist] = carry[0];
+    gstart[nlist] = carry[1];
+  }
+}
+
+// the groups of each list: (list, first pair slot, pairs, 0), up to G pairs
+__global__ void k_make_groups(const int32_t *lcnt, const int64_t *lstart, const int64_t *gstart,
+                              int32_t nlist, int32_t G, int4 *groups) {
+  const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (l >= nlist) return;
+  const int64_t g0 = gstart[l], n = gstart[l + 1] - g0;
+  const int32_t c = lcnt[l];
+  for (int64_t j = 0; j < n; ++j)
+    groups[g0 + j] = int4{(int)l, (int)(lstart[l] + j * G), (int)min<int64_t>(G, c - j * G), 0};
+}
+
 struct ListScanArgs {
   const float *rows;     // list rows, ld stride
   const int64_t *list_off;
@@ -124,6 +235,7 @@ struct ListScanArgs {
   const int32_t *probes; // [nq][np]
   const int32_t *pairs;  // pair ids (q*np+p) grouped by list
   const int4 *groups;    // (list, pair_begin, pair_count, 0)
+  const int64_t *ngroups;   // groups made (the grid is an upper bound)
   const int64_t *pos_base;  // [nq][np]
   const int64_t *seg_off;   // [nq+1] candidate segment offsets
   uint64_t *cand;
@@ -139,6 +251,7 @@ struct ListScanArgs {
 // the QG query slots of a group: query index, candidate-segment base and
 // position base of each (slots past the group's count repeat its first)
 #define VSK_GROUP_SLOTS(QG)                                        \
+  if (blockIdx.x >= *a.ngroups) return;                            \
   const int4 g = a.groups[blockIdx.x];                             \
   const int32_t l = g.x;                                           \
   const int npair = g.z;                                           \
@@ -193,6 +306,7 @@ template <int QG>
 __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float qs[];  // QG x ld
+  if (blockIdx.x >= *a.ngroups) return;
   const int4 g = a.groups[blockIdx.x];
   const int32_t l = g.x;
   const int npair = g.z;
@@ -313,6 +427,155 @@ __global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
   out_ids[i] = ids[row];
 }
 
+// ---------------------------------------------------------------------------
+// The list scan through the bf16 matrix cores (IVF-Flat, L2 and L2^2).  The
+// flat screen's argument carries over: with bf16 planes of the rows and the
+// queries, every (query, candidate) pair gets a screened distance a within
+// eps(q) of the exact one (flat_screen.hip); the kc smallest screened keys
+// per query are kept, the bound check proves they hold the exact top k (or
+// the query's whole candidate set is rescored), and only the kept keys
+// within the margin get their exact distances -- the reference's sequential
+// fp32 sums -- with their (distance, position) keys unchanged in form.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// one workgroup per group of up to 64 queries probing one list.  A is the
+// group's query fragments (4 tiles of 16 queries x KS k-steps of 32 dims,
+// held in registers for the whole list), B a 16-row block of the list's
+// plane, so lane l of a product holds query 4 (l / 16) + r of the tile
+// against row l % 16 of the block: 16 lanes write 16 consecutive values of
+// one query.  Wave w takes the list's blocks w, w + 4, ...  Each screened
+// distance goes, as its order-preserving 32-bit word, to its candidate
+// position in the query's segment, out[seg_off[q] + position].
+template <int KS>
+__global__ __launch_bounds__(256) void k_list_screen(
+    const uint16_t *xplane, const float *xsq, int32_t ldb, const int64_t *list_off,
+    const uint16_t *qplane, const float *qsq, const int32_t *pairs, const int4 *groups,
+    const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *seg_off,
+    uint32_t *out) {
+  if (blockIdx.x >= *ngroups) return;
+  __shared__ int64_t s_out[64];  // value address of the list's first row (-1: no query)
+  __shared__ float s_qa[64];     // |q|^2
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int4 g = groups[blockIdx.x];
+  const int64_t v0 = list_off[g.x], v1 = list_off[g.x + 1];
+  const int npair = g.z;
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    const int32_t pid = pairs[g.y + (j < npair ? j : 0)];
+    const int32_t q = pid / np;
+    s_out[j] = j < npair ? seg_off[q] + pos_base[pid] : -1;
+    s_qa[j] = qsq[q];
+  }
+  const int kc = 8 * (lane >> 4);  // this lane's 8 dims of a k-step
+  const int ntile = (npair + 15) >> 4;
+  bf8v qf[4][KS];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int j = 16 * t + (lane & 15);
+    const int32_t q = pairs[g.y + (j < npair ? j : 0)] / np;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + (int64_t)q * ldb + 32 * ks + kc);
+  }
+  __syncthreads();
+  for (int64_t b = v0 + 16 * w; b < v1; b += 64) {
+    const int64_t row = b + (lane & 15);
+    const bool live = row < v1;
+    bf8v xf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      xf[ks] = live ? *reinterpret_cast<const bf8v *>(xplane + row * ldb + 32 * ks + kc)
+                    : bf8v{};
+    const float xa = live ? xsq[row] : 0.f;
+    const int64_t i = row - v0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (t >= ntile) break;  // uniform
+      f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t][ks], xf[ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * t + 4 * (lane >> 4) + r;
+        const int64_t o = s_out[j];
+        if (live && o >= 0) out[o + i] = vsk_f2ord(fmaxf(s_qa[j] + xa - 2.0f * acc[r], 0.0f));
+      }
+    }
+  }
+}
+
+// exact keys for screened ones: key (a, position) -> (the reference's
+// sequential fp32 distance, position), the same sum as k_list_scan.  Query
+// q's keys are the first cnt[q] of in[q*in_stride ...], written to
+// out[q*in_stride ...]; or (cnt null) every position of the query's
+// candidates gets its exact key in its segment of seg_off, in[seg_off[q] +
+// position]; only queries with active[q].  One wave per query, a
+// key per lane; each lane loads 64 floats of its row and of the query ahead
+// of their sequential sum.  A position maps to its probe slot -- the last
+// one whose base is at or below it, which holds at least one row past the
+// base -- and so to the row.
+__global__ __launch_bounds__(256) void k_list_rescore(
+    const float *rows, int32_t ld, const int64_t *list_off, const float *Q,
+    const int32_t *probes, int32_t np, const int64_t *pos_base, uint64_t *in,
+    int64_t in_stride, const int32_t *cnt, const int64_t *seg_off, uint64_t *out,
+    const uint8_t *active, int64_t nq, int32_t squared) {
+#pragma clang fp contract(off)
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (q >= nq || !active[q]) return;
+  const uint64_t *src = cnt ? in + q * in_stride : nullptr;
+  uint64_t *dst = cnt ? out + q * in_stride : in + seg_off[q];
+  const int64_t n = cnt ? (int64_t)cnt[q] : seg_off[q + 1] - seg_off[q];
+  const float *qq = Q + q * ld;
+  const int64_t *pb = pos_base + q * np;
+  const int32_t *pr = probes + q * np;
+  for (int64_t i = lane; i < n; i += 64) {
+    const int64_t p = src ? (int64_t)(uint32_t)src[i] : i;
+    int lo = 0, hi = np;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pb[mid] <= p) lo = mid;
+      else hi = mid;
+    }
+    const float *x = rows + (list_off[pr[lo]] + (p - pb[lo])) * ld;
+    float acc = 0.f;
+    for (int c0 = 0; c0 < ld; c0 += 64) {
+      const int m = ld - c0 < 64 ? (ld - c0) >> 2 : 16;  // ld is a multiple of 4
+      f4 xv[16], qv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) {
+          xv[u] = *reinterpret_cast<const f4 *>(x + c0 + 4 * u);
+          qv[u] = *reinterpret_cast<const f4 *>(qq + c0 + 4 * u);
+        }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) {
+          float t;
+          t = qv[u].x - xv[u].x;
+          acc = acc + t * t;
+          t = qv[u].y - xv[u].y;
+          acc = acc + t * t;
+          t = qv[u].z - xv[u].z;
+          acc = acc + t * t;
+          t = qv[u].w - xv[u].w;
+          acc = acc + t * t;
+        }
+    }
+    dst[i] = vsk_key(squared ? acc : sqrtf(acc), (uint32_t)p);
+  }
+}
+
+__global__ void k_mask_not(const uint8_t *ok, int64_t n, uint8_t *out, const int32_t *fails,
+                           int64_t *fails64) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = ok[i] ? 0 : 1;
+  if (i == 0 && fails64) *fails64 = *fails;
+}
+
 static unsigned grid1(int64_t n, int threads = 256) {
   int64_t g = ceil_div(n, threads);
   return (unsigned)(g < 65535 * 16 ? (g > 0 ? g : 1) : 65535 * 16);
@@ -355,11 +618,23 @@ static void ivf_assign_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dx,
   }
 }
 
+static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
+                            int64_t nq, int32_t np, uint64_t *keys);
+
 // top-nprobe centroids per query (ties by centroid index)
 static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
                              int64_t nq, int32_t np, int32_t *probes) {
   uint64_t *keys = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.probe_keys", sizeof(uint64_t) * nq * np));
+  ivf_probe_exact(ctx, ivf, dq, nq, np, keys);
+  KernelTimer t(ctx, "ivf_probe_ids");
+  k_keys_to_tie<<<grid1(nq * np), 256, 0, ctx->stream>>>(keys, nq * np, probes);
+  check_launch("ivf_probe_ids");
+}
+
+// the exact VALU scan over every centroid, one dense chunk per query batch
+static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
+                            int64_t nq, int32_t np, uint64_t *keys) {
   const int64_t cap = ivf->nlist;  // one dense chunk
   const int64_t qb = query_batch(nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
@@ -379,9 +654,53 @@ static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
     progressive_topk(ctx, nb, ivf->nlist, np, cap, scan, keys + b0 * np,
                      "ivf_probe_select");
   }
-  KernelTimer t(ctx, "ivf_probe_ids");
-  k_keys_to_tie<<<grid1(nq * np), 256, 0, ctx->stream>>>(keys, nq * np, probes);
-  check_launch("ivf_probe_ids");
+}
+
+// whether the list scan of kind 0 goes through the bf16 screen: L2 / L2^2,
+// at most 256 dims (the query fragments stay in registers), k whose kept
+// candidates fit a selection, and enough work to pay for the extra
+// launches (forced by VSK_FLAT_KERNEL=screen, off by =exact / =bf16x3)
+static bool list_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t metric, int32_t k,
+                                double ncand) {
+  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (metric != VSK_METRIC_L2 && metric != VSK_METRIC_L2SQ) return false;
+  if (ivf->d > 256 || screen_keep(k) > VSK_MAX_K) return false;
+  return ctx->flat_force_screen || ncand * ivf->d >= (double)(1ll << 30);
+}
+
+// candidates a query can have with np probes: the sizes of the np largest
+// lists summed (every row when every list is probed)
+static int64_t probe_bound(const vsk_ivf *ivf, int32_t np) {
+  if (np >= ivf->nlist) return ivf->total;
+  std::vector<int64_t> sz(ivf->nlist);
+  for (int32_t l = 0; l < ivf->nlist; ++l) sz[l] = ivf->off[l + 1] - ivf->off[l];
+  std::nth_element(sz.begin(), sz.begin() + np, sz.end(), std::greater<int64_t>());
+  int64_t s = 0;
+  for (int32_t i = 0; i < np; ++i) s += sz[i];
+  return s;
+}
+
+// the stored rows' bf16 plane (roundup(d, 64) columns), |x|^2 per row and
+// the maxima of |bf16(x)| and |x - bf16(x)|, rebuilt after the rows change
+static void list_screen_plane(vsk_ctx *ctx, const vsk_ivf *ivf) {
+  if (ivf->xversion == ivf->version) return;
+  const int32_t ldb = (ivf->d + 63) & ~63;
+  const int64_t n = std::max<int64_t>(ivf->total, 1);
+  ivf->xplane.reserve(sizeof(uint16_t) * (size_t)n * ldb);
+  ivf->xsq.reserve(sizeof(float) * (size_t)n);
+  uint32_t *mb = static_cast<uint32_t *>(ctx->scratch_ptr("ivf.planemax", 2 * sizeof(uint32_t)));
+  fill_i32(ctx, reinterpret_cast<int32_t *>(mb), 2, 0);
+  split_bf16(ctx, ivf->rows.as<float>(), ivf->total, ivf->d, ivf->ld,
+             ivf->xplane.as<uint16_t>(), nullptr, ldb, nullptr, nullptr, mb);
+  row_norms(ctx, ivf->rows.as<float>(), ivf->total, ivf->d, ivf->ld, ivf->xsq.as<float>(),
+            nullptr);
+  uint32_t hb[2];
+  VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  ivf->xh_max = __builtin_bit_cast(float, hb[0]);
+  ivf->xr_max = __builtin_bit_cast(float, hb[1]);
+  ivf->xldb = ldb;
+  ivf->xversion = ivf->version;
 }
 
 static void require_ivf(const vsk_ivf *ivf) {
@@ -543,6 +862,7 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
   VSK_HIP(hipStreamSynchronize(ctx->stream));
   std::swap(ivf->rows.p, rows2->p);
   std::swap(ivf->rows.bytes, rows2->bytes);
+  ++ivf->version;
   std::swap(ivf->ids.p, ids2->p);
   std::swap(ivf->ids.bytes, ids2->bytes);
   ivf->off = noff;
@@ -580,6 +900,149 @@ vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
 }
 
 }  // extern "C"
+
+// the pair and group arrays of a batch (sized for the largest batch)
+struct ListGroups {
+  int32_t *lcnt;                    // pairs per list
+  int64_t *lstart, *cursor, *gstart;  // nlist + 1 each
+  int32_t *pairs;
+  int4 *groups;
+};
+
+// the batch's pairs grouped by list, up to G a group; the group count
+// lands in gstart[nlist]
+static void make_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes,
+                        int64_t npairs, int32_t np, int G, const ListGroups &lg) {
+  const int32_t nlist = ivf->nlist;
+  fill_i32(ctx, lg.lcnt, nlist, 0);
+  k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt);
+  check_launch("ivf_list_pair_counts");
+  k_list_offsets<<<1, 1024, 0, ctx->stream>>>(lg.lcnt, ivf->list_off.as<int64_t>(), nlist, G,
+                                               lg.lstart, lg.cursor, lg.gstart);
+  check_launch("ivf_list_offsets");
+  k_make_groups<<<grid1(nlist), 256, 0, ctx->stream>>>(lg.lcnt, lg.lstart, lg.gstart, nlist,
+                                                       G, lg.groups);
+  check_launch("ivf_make_groups");
+  k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, np, lg.cursor,
+                                                        lg.pairs);
+  check_launch("ivf_group_pairs");
+}
+
+// one query batch of the screened list scan: the screened distance of
+// every candidate (32 bits, at its position in the query's segment), the
+// kc smallest per query, the bound check, then the exact top k of the kept
+// keys within the margin -- or, for a query failing the check, of every
+// candidate -- into best[b0 * k ...].  No read-back: the fallback's launches
+// find no active query when none fails.
+static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQueries &qp,
+                              const float *dq, int64_t b0, int64_t nb, int32_t np, int32_t k,
+                              int32_t kc, int32_t metric, const int32_t *probes,
+                              const int64_t *pos_base, const int64_t *dseg,
+                              const ListGroups &lg, uint64_t *cand, uint64_t *best) {
+  const int32_t ld = ivf->ld, ldb = ivf->xldb, nlist = ivf->nlist;
+  const int64_t npairs = nb * np;
+  const int32_t *bprobes = probes + b0 * np;
+  const int64_t *bpos = pos_base + b0 * np;
+  // the screened words share cand's memory: its first half holds them
+  uint32_t *words = reinterpret_cast<uint32_t *>(cand);
+  {
+    KernelTimer t(ctx, "ivf_list_screen");
+    t.device_work(dseg + nb);
+    const unsigned gmax = (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, 64));
+#define VSK_LS(KS)                                                                          \
+  k_list_screen<KS><<<gmax, 256, 0, ctx->stream>>>(                                        \
+      ivf->xplane.as<uint16_t>(), ivf->xsq.as<float>(), ldb, ivf->list_off.as<int64_t>(),   \
+      qp.qh + b0 * qp.ldb, qp.qsq + b0, lg.pairs, lg.groups, lg.gstart + nlist, np, bpos,   \
+      dseg, words)
+    switch (ldb / 32) {
+    case 2: VSK_LS(2); break;
+    case 4: VSK_LS(4); break;
+    case 6: VSK_LS(6); break;
+    default: VSK_LS(8); break;
+    }
+#undef VSK_LS
+    check_launch("ivf_list_screen");
+  }
+  uint64_t *kept = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.kept", sizeof(uint64_t) * nb * kc));
+  uint64_t *exact = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.kexact", sizeof(uint64_t) * nb * kc));
+  uint8_t *ok = static_cast<uint8_t *>(ctx->scratch_ptr("ivf.ok", 2 * (size_t)nb));
+  uint8_t *bad = ok + nb;
+  int32_t *nvalid = static_cast<int32_t *>(ctx->scratch_ptr("ivf.nvalid", 4 * (nb + 4)));
+  int32_t *fails = nvalid + nb;
+  // the failing queries' count as the fallback's work (profiling)
+  int64_t *fails64 = ctx->profile ? reinterpret_cast<int64_t *>(nvalid + ceil_div(nb + 1, 2) * 2)
+                                  : nullptr;
+  fill_i32(ctx, fails, 1, 0);
+  {
+    SelectArgs sa;
+    sa.nq = nb;
+    sa.k = kc;
+    sa.cand32 = words;
+    sa.seg_off = dseg;
+    sa.best_out = kept;
+    launch_select(ctx, sa, "ivf_screen_select");
+  }
+  CheckArgs ca{};
+  ca.best = kept;
+  ca.nq = nb;
+  ca.k = k;
+  ca.kc = kc;
+  ca.d = ivf->d;
+  ca.metric = metric;
+  ca.qnh = qp.qnh + b0;
+  ca.qnr = qp.qnr + b0;
+  ca.xh = ivf->xh_max;
+  ca.xr = ivf->xr_max;
+  ca.ok = ok;
+  ca.nvalid = nvalid;
+  ca.fails = fails;
+  ca.test = true;
+  launch_screen_check(ctx, ca);
+  k_mask_not<<<grid1(nb), 256, 0, ctx->stream>>>(ok, nb, bad, fails, fails64);
+  check_launch("ivf_mask");
+  const int32_t sq = metric == VSK_METRIC_L2SQ ? 1 : 0;
+  const float *rows = ivf->rows.as<float>();
+  const int64_t *loff = ivf->list_off.as<int64_t>();
+  {
+    KernelTimer t(ctx, "ivf_screen_rescore");
+    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(
+        rows, ld, loff, dq + b0 * ld, bprobes, np, bpos, kept, kc, nvalid, nullptr, exact, ok,
+        nb, sq);
+    check_launch("ivf_screen_rescore");
+  }
+  {
+    SelectArgs sa;
+    sa.nq = nb;
+    sa.k = k;
+    sa.cand = exact;
+    sa.cap = kc;
+    sa.counts = nvalid;
+    sa.active = ok;
+    sa.best_out = best + b0 * k;
+    launch_select(ctx, sa, "ivf_select");
+  }
+  // queries whose kept keys could miss a top-k row: every candidate exact,
+  // in its segment of cand (over the screened words, which only the
+  // selection above read)
+  {
+    KernelTimer t(ctx, "ivf_screen_redo");
+    if (fails64) t.device_work(fails64);
+    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(
+        rows, ld, loff, dq + b0 * ld, bprobes, np, bpos, cand, 0, nullptr, dseg, nullptr, bad,
+        nb, sq);
+    check_launch("ivf_screen_redo");
+  }
+  SelectArgs sa;
+  sa.nq = nb;
+  sa.k = k;
+  sa.cand = cand;
+  sa.seg_off = dseg;
+  sa.active = bad;
+  sa.best_out = best + b0 * k;
+  launch_select(ctx, sa, "ivf_select");
+}
 
 // kind 0: the rows (metric L2 / L2SQ); 1: SQ8 codes, qextra = nq x d int8
 // query codes; 2: PQ codes, qextra = the vsk_pq whose tables score them
@@ -667,19 +1130,6 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       ctx->scratch_ptr("ivf.pos_base", sizeof(int64_t) * nq * np));
   int64_t *cnt =
       static_cast<int64_t *>(ctx->scratch_ptr("ivf.cnt", sizeof(int64_t) * nq));
-  {
-    KernelTimer t(ctx, "ivf_probe_bases");
-    k_probe_bases<<<grid1(nq), 256, 0, ctx->stream>>>(
-        probes, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt);
-    check_launch("ivf_probe_bases");
-  }
-  std::vector<int64_t> h_cnt(nq);
-  std::vector<int32_t> h_probes((size_t)nq * np);
-  VSK_HIP(hipMemcpyAsync(h_cnt.data(), cnt, 8 * nq, hipMemcpyDeviceToHost,
-                         ctx->stream));
-  VSK_HIP(hipMemcpyAsync(h_probes.data(), probes, 4 * h_probes.size(),
-                         hipMemcpyDeviceToHost, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
 
   // queries per group: their rows, codes or tables fit 64 KiB of LDS
   const int64_t per_q = kind == 0 ? (int64_t)ld * 4
@@ -692,89 +1142,101 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   VSK_REQUIRE(per_q * QG <= 64 * 1024, VSK_ERR_UNSUPPORTED,
               kind == 2 ? "PQ tables too large for the IVF list scan (M x ksub > 16384)"
                         : "dimension too large for the IVF list scan");
-  int64_t max_cnt = 0;
-  for (auto c : h_cnt) max_cnt = std::max(max_cnt, c);
-  const int64_t budget = std::max<int64_t>(1ll << 27, max_cnt);
+  // candidates per query: at most the np largest lists; query batches
+  // whose bound fits 2^27 keys (one query at least).  Everything below runs
+  // on the stream without a read-back: segment offsets, pairs and groups
+  // are made on the device, and grids take their upper bounds.
+  const int64_t ubound = probe_bound(ivf, np);
+  const int64_t qb = std::max<int64_t>(
+      1, std::min<int64_t>(nq, (1ll << 27) / std::max<int64_t>(ubound, 1)));
+  const double per_query = ivf->nlist > 0 ? (double)ivf->total * np / ivf->nlist : 0.0;
+  // the bf16 screen (kind 0): groups of 64 queries, kc screened keys kept
+  // per query
+  const bool screen =
+      kind == 0 && list_screen_applies(ctx, ivf, metric, k, (double)nq * per_query);
+  const int G = screen ? 64 : QG;
+  const int32_t kc = screen ? screen_keep(k) : 0;
+  ArgminQueries qp;
+  if (screen) {
+    list_screen_plane(ctx, ivf);
+    qp = argmin_queries(ctx, dq, nq, ivf->d, ld, "ivf.sq");
+  }
+  {
+    KernelTimer t(ctx, "ivf_probe_bases");
+    k_probe_bases<<<grid1(nq), 256, 0, ctx->stream>>>(
+        probes, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt);
+    check_launch("ivf_probe_bases");
+  }
+  const int64_t nbmax = qb, npmax = nbmax * np;
+  const int32_t nlist = ivf->nlist;
+  const int64_t gmax = std::min<int64_t>(nlist, npmax) + ceil_div(npmax, G);
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.best", sizeof(uint64_t) * nq * k));
+  int64_t *dseg = static_cast<int64_t *>(
+      ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * (nbmax + 1)));
+  int64_t *loffs = static_cast<int64_t *>(
+      ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
+  int64_t *lstart = loffs, *cursor = loffs + (nlist + 1), *gstart = loffs + 2 * (nlist + 1);
+  int32_t *lcnt = static_cast<int32_t *>(ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * nlist));
+  const ListGroups lg{lcnt, lstart, cursor, gstart, nullptr, nullptr};
+  int32_t *dpairs = static_cast<int32_t *>(
+      ctx->scratch_ptr("ivf.pairs", sizeof(int32_t) * (npmax + 1)));
+  int4 *dgroups = static_cast<int4 *>(ctx->scratch_ptr("ivf.groups", sizeof(int4) * (gmax + 1)));
+  ListGroups lgp = lg;
+  lgp.pairs = dpairs;
+  lgp.groups = dgroups;
+  uint64_t *cand = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.cand", sizeof(uint64_t) * (nbmax * ubound + 1)));
+  const int64_t *loff = ivf->list_off.as<int64_t>();
 
-  // query batches whose candidate segments fit the budget
-  int64_t b0 = 0;
-  while (b0 < nq) {
-    int64_t b1 = b0, tot = 0;
-    while (b1 < nq && tot + h_cnt[b1] <= budget) tot += h_cnt[b1++];
-    const int64_t nb = b1 - b0;
-    std::vector<int64_t> seg(nb + 1, 0);
-    for (int64_t i = 0; i < nb; ++i) seg[i + 1] = seg[i] + h_cnt[b0 + i];
-    // 3. pairs grouped by list
-    std::vector<int64_t> lcount(ivf->nlist + 1, 0);
-    for (int64_t i = 0; i < nb * np; ++i) {
-      int32_t l = h_probes[b0 * np + i];
-      if (l >= 0) lcount[l + 1]++;
-    }
-    for (int32_t l = 0; l < ivf->nlist; ++l) lcount[l + 1] += lcount[l];
-    std::vector<int4> groups;
-    for (int32_t l = 0; l < ivf->nlist; ++l) {
-      int64_t c = lcount[l + 1] - lcount[l];
-      if (c == 0 || ivf->off[l + 1] == ivf->off[l]) continue;
-      for (int64_t j = 0; j < c; j += QG)
-        groups.push_back(int4{l, (int)(lcount[l] + j),
-                              (int)std::min<int64_t>(QG, c - j), 0});
-    }
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     const int64_t npairs = nb * np;
-    int64_t *dseg = static_cast<int64_t *>(
-        ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * (nb + 1)));
-    int64_t *dcursor = static_cast<int64_t *>(
-        ctx->scratch_ptr("ivf.cursor", sizeof(int64_t) * (ivf->nlist + 1)));
-    int32_t *dpairs = static_cast<int32_t *>(
-        ctx->scratch_ptr("ivf.pairs", sizeof(int32_t) * (npairs + 1)));
-    int4 *dgroups = static_cast<int4 *>(
-        ctx->scratch_ptr("ivf.groups", sizeof(int4) * (groups.size() + 1)));
-    uint64_t *cand = static_cast<uint64_t *>(
-        ctx->scratch_ptr("ivf.cand", sizeof(uint64_t) * (tot + 1)));
-    VSK_HIP(hipMemcpyAsync(dseg, seg.data(), 8 * (nb + 1),
-                           hipMemcpyHostToDevice, ctx->stream));
-    VSK_HIP(hipMemcpyAsync(dcursor, lcount.data(), 8 * (ivf->nlist + 1),
-                           hipMemcpyHostToDevice, ctx->stream));
-    if (!groups.empty())
-      VSK_HIP(hipMemcpyAsync(dgroups, groups.data(),
-                             sizeof(int4) * groups.size(),
-                             hipMemcpyHostToDevice, ctx->stream));
+    const int64_t ng = std::min<int64_t>(nlist, npairs) + ceil_div(npairs, G);
+    // 3. segment offsets; pairs grouped by list, groups of up to G pairs
     {
       KernelTimer t(ctx, "ivf_group_pairs");
-      k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(
-          probes + b0 * np, npairs, np, dcursor, dpairs);
-      check_launch("ivf_group_pairs");
+      k_seg_offsets<<<1, 1024, 0, ctx->stream>>>(cnt + b0, nb, dseg);
+      check_launch("ivf_seg_offsets");
+      if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     }
-    if (!groups.empty()) {
-      ListScanArgs la;
-      la.rows = ivf->rows.as<float>();
-      la.list_off = ivf->list_off.as<int64_t>();
-      la.Q = dq + b0 * ld;
-      la.ld = ld;
-      la.np = np;
-      la.probes = probes + b0 * np;
-      la.pairs = dpairs;
-      la.groups = dgroups;
-      la.pos_base = pos_base + b0 * np;
-      la.seg_off = dseg;
-      la.cand = cand;
-      la.squared = metric == VSK_METRIC_L2SQ ? 1 : 0;
-      la.codes = ivf->codes.as<uint8_t>();
-      la.cstride = ivf->cstride;
-      la.qc = dqc ? dqc + b0 * ivf->cstride : nullptr;
-      la.lut = dlut ? dlut + b0 * ivf->cM * ivf->cksub : nullptr;
-      la.M = ivf->cM;
-      la.ksub = ivf->cksub;
+    if (screen) {
+      list_screen_batch(ctx, ivf, qp, dq, b0, nb, np, k, kc, metric, probes, pos_base, dseg,
+                        lgp, cand, best);
+      continue;
+    }
+    const int64_t *ngroups = gstart + nlist;
+    ListScanArgs la;
+    la.rows = ivf->rows.as<float>();
+    la.list_off = loff;
+    la.Q = dq + b0 * ld;
+    la.ld = ld;
+    la.np = np;
+    la.probes = probes + b0 * np;
+    la.pairs = dpairs;
+    la.groups = dgroups;
+    la.ngroups = ngroups;
+    la.pos_base = pos_base + b0 * np;
+    la.seg_off = dseg;
+    la.cand = cand;
+    la.squared = metric == VSK_METRIC_L2SQ ? 1 : 0;
+    la.codes = ivf->codes.as<uint8_t>();
+    la.cstride = ivf->cstride;
+    la.qc = dqc ? dqc + b0 * ivf->cstride : nullptr;
+    la.lut = dlut ? dlut + b0 * ivf->cM * ivf->cksub : nullptr;
+    la.M = ivf->cM;
+    la.ksub = ivf->cksub;
+    {
       const size_t lds = (size_t)(per_q * QG);
-      const unsigned ng = (unsigned)groups.size();
+      const unsigned g = (unsigned)ng;
       static const char *names[3] = {"ivf_list_scan", "ivf_sq8_list_scan", "ivf_pq_list_scan"};
-      KernelTimer t(ctx, names[kind], (double)tot);
+      KernelTimer t(ctx, names[kind]);
+      t.device_work(dseg + nb);
 #define VSK_SCAN_QG(K)                                                  \
-  if (QG == 16) K<16><<<ng, 256, lds, ctx->stream>>>(la);              \
-  else if (QG == 8) K<8><<<ng, 256, lds, ctx->stream>>>(la);           \
-  else if (QG == 4) K<4><<<ng, 256, lds, ctx->stream>>>(la);           \
-  else K<1><<<ng, 256, lds, ctx->stream>>>(la);
+  if (QG == 16) K<16><<<g, 256, lds, ctx->stream>>>(la);               \
+  else if (QG == 8) K<8><<<g, 256, lds, ctx->stream>>>(la);            \
+  else if (QG == 4) K<4><<<g, 256, lds, ctx->stream>>>(la);            \
+  else K<1><<<g, 256, lds, ctx->stream>>>(la);
       if (kind == 0) {
         VSK_SCAN_QG(k_list_scan)
       } else if (kind == 1) {
@@ -793,8 +1255,6 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     sa.seg_off = dseg;
     sa.best_out = best + b0 * k;
     launch_select(ctx, sa, "ivf_select");
-    VSK_HIP(hipStreamSynchronize(ctx->stream));  // host vectors reused
-    b0 = b1;
   }
   {
     KernelTimer t(ctx, "ivf_decode");
@@ -1130,6 +1590,7 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   fill_i32(ctx, ivf->rows.as<int32_t>(), std::max<int64_t>(total, 1) * ld, 0);
   get_rows(ctx, f.get(), h, ivf->ids.p, total, 8, 8);
   get_rows(ctx, f.get(), h, ivf->rows.p, total, sizeof(float) * ld, sizeof(float) * d);
+  ++ivf->version;
   if (ck[0] != 0) {
     ivf->codes.reserve((size_t)total * ck[1] + 16);
     fill_i32(ctx, ivf->codes.as<int32_t>(), ((int64_t)total * ck[1] + 16) / 4, 0);

@@ -20,8 +20,12 @@ namespace vsk {
 
 constexpr int SEL_THREADS = 256;
 
-__device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np,
-                                    const uint64_t *C, int64_t i) {
+// element i of a query's keys: the previous list, then the candidates --
+// 64-bit keys, or (W32) 32-bit distances keyed by their index in the list
+template <bool W32>
+__device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np, const uint64_t *C,
+                                    const uint32_t *C32, int64_t i) {
+  if constexpr (W32) return ((uint64_t)C32[i] << 32) | (uint32_t)i;
   return i < np ? P[i] : C[i - np];
 }
 
@@ -30,7 +34,8 @@ __device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np,
 // The registers cost occupancy, so only callers whose lists are a few
 // thousand keys (IVF candidate segments, a dense chunk as small as the IVF
 // probe's centroids) take it.
-template <int REG>
+// W32: the candidates are a.cand32 (no previous list)
+template <int REG, bool W32>
 __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -55,7 +60,8 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
     }
     return;
   }
-  const uint64_t *C = a.cand + base;
+  const uint64_t *C = W32 ? nullptr : a.cand + base;
+  const uint32_t *C32 = W32 ? a.cand32 + base : nullptr;
   const int64_t total = np + cnt;
   // segmented lists: the segments' key counts in LDS; wave w walks the
   // segments w, w + 4, ... (64 lanes per segment)
@@ -71,7 +77,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
 #pragma unroll
     for (int r = 0; r < REG; ++r) {
       const int64_t i = tid + (int64_t)r * SEL_THREADS;
-      regs[r] = i < total ? sel_elem(P, np, C, i) : VSK_KEY_NONE;
+      regs[r] = i < total ? sel_elem<W32>(P, np, C, C32, i) : VSK_KEY_NONE;
     }
   }
   auto each_key = [&](auto &&f) {
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
       return;
     }
     if (!seg) {
-      for (int64_t i = tid; i < total; i += SEL_THREADS) f(sel_elem(P, np, C, i));
+      for (int64_t i = tid; i < total; i += SEL_THREADS) f(sel_elem<W32>(P, np, C, C32, i));
       return;
     }
     for (int64_t i = tid; i < np; i += SEL_THREADS) f(P[i]);
@@ -251,12 +257,15 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   KernelTimer t(ctx, name);
   // keys per query: the previous list (k) and up to cap candidates
   const int64_t most = a.cap + (a.prev ? a.k : 0);
-  if (a.regs && !a.seg_off && most > 32 * SEL_THREADS)
-    k_select<64><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  if (a.cand32) {
+    if (a.prev || a.seg_n) fail(VSK_ERR_INVALID_ARGUMENT, "32-bit lists take no previous list or segments");
+    k_select<32, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  } else if (a.regs && !a.seg_off && most > 32 * SEL_THREADS)
+    k_select<64, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   else if (a.seg_off || a.regs)
-    k_select<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+    k_select<32, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   else
-    k_select<0><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+    k_select<0, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   check_launch(name);
 }
 

@@ -50,6 +50,9 @@ struct SelectArgs {
   int32_t k = 0;
   const uint64_t *prev = nullptr;
   const uint64_t *cand = nullptr;
+  // 32-bit distances instead of cand (no prev): key = (value << 32) | the
+  // value's index in its query's list
+  const uint32_t *cand32 = nullptr;
   int64_t cap = 0;
   const int64_t *seg_off = nullptr;
   const int32_t *counts = nullptr;

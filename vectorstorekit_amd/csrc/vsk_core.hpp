@@ -94,7 +94,12 @@ struct vsk_ctx {
     int stat;
     hipEvent_t a, b;
     double work;
+    int work_slot;  // >= 0: the work count read back into work_pinned[slot]
   };
+  // pinned slots for work counts the device computes (profiling only)
+  static constexpr int kWorkSlots = 1024;
+  int64_t *work_pinned = nullptr;
+  int work_used = 0;
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
   std::vector<vsk_kernel_stat> stats;
@@ -135,7 +140,10 @@ struct KernelTimer {
   double work = 0;
   hipStream_t stream = nullptr;
   // times on stream s (default: the context's stream)
+  const int64_t *work_dev = nullptr;
   KernelTimer(vsk_ctx *c, const char *name, double work_items = 0, hipStream_t s = nullptr);
+  // the work count is a device value, final once the timed launch ends
+  void device_work(const int64_t *p) { work_dev = p; }
   ~KernelTimer();
 };
 
