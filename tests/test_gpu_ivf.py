@@ -78,12 +78,12 @@ def _screen_ctx():
                                    (16, 3000, 24, 40, 16, 20, "euclidean")])
 def test_ivf_screen_bit_exact(shape):
     """The list scan through the bf16 screen (forced at these sizes): query
-    groups of up to 64 per list, the kept screened keys per query, the bound
-    check and the exact rescore.  Plane widths of 2, 4, 6 and 8 k-steps, both
-    euclidean metrics, k above 64, every list probed; then rows added (the
-    plane is made again), and a block of identical rows that makes the check
-    fail for the queries next to it (their whole candidate set is rescored).
-    Bit-exact against the oracle."""
+    groups of up to 64 per list, the screened keys within the bound's margin
+    of the k-th, their exact rescore.  Plane widths of 2, 4, 6 and 8 k-steps,
+    both euclidean metrics, k above 64, every list probed; then rows added
+    (the plane is made again), among them a block of 1,100 identical rows,
+    more than the margin's slots hold, so the queries next to it have their
+    whole candidate set rescored.  Bit-exact against the oracle."""
     ncent, n, d, nq, nprobe, k, metric = shape
     print(f"ivf screen ncent={ncent} n={n} d={d} nq={nq} nprobe={nprobe} k={k} {metric}",
           flush=True)
@@ -93,15 +93,17 @@ def test_ivf_screen_bit_exact(shape):
     sctx = _screen_ctx()
     idx = _index(sctx, c, x, ids, nprobe)
     lists = O.ivf_assign(x, c)
+    np.testing.assert_array_equal(idx.probe(q, nprobe), O.ivf_probe(q, c, nprobe))
     gd, gi = idx.search(q, k, metric=metric)
     assert "ivf_list_screen" in sctx.profile_stats(), "the screen did not run"
+    assert "ivf_probe_screen" in sctx.profile_stats(), "the probe's screen did not run"
     od, oi = O.ivf_search(q, x, ids, lists, c, nprobe, k, squared=sq)
     np.testing.assert_array_equal(gi, oi)
     np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
-    # rows added after the plane was made, among them 400 copies of one row
-    # next to the first queries
+    # rows added after the plane was made, among them 1,100 copies of one
+    # row next to the first query
     rng = np.random.default_rng(n)
-    dup = np.repeat(q[:1] + 0.01 * rng.standard_normal((1, d)).astype(np.float32), 400, 0)
+    dup = np.repeat(q[:1] + 0.01 * rng.standard_normal((1, d)).astype(np.float32), 1100, 0)
     extra = np.concatenate([x[:1000] + 0.1, dup]).astype(np.float32)
     eids = np.arange(n, n + len(extra), dtype=np.int64) * 3 + 7
     idx.insert(extra, eids)
@@ -113,8 +115,33 @@ def test_ivf_screen_bit_exact(shape):
     od, oi = O.ivf_search(q, x2, ids2, lists2, c, nprobe, k, squared=sq)
     np.testing.assert_array_equal(gi, oi)
     np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
-    # the fallback's work count is the number of queries that failed
-    assert sctx.profile_stats()["ivf_screen_redo"][2] > before, "no query failed the check"
+    # the fallback's work count is the number of queries that overflowed
+    assert sctx.profile_stats()["ivf_screen_redo"][2] > before, "no query overflowed"
+    sctx.close()
+
+
+def test_ivf_probe_screen_overflow():
+    """The probe through the screen when more centroids than its margin
+    slots (1,024) tie with the nprobe-th: 1,100 copies of one centroid next
+    to the queries.  Those queries have every centroid's exact distance
+    ranked instead; probes (ties by centroid index) and results bit-exact
+    against the oracle."""
+    rng = np.random.default_rng(5)
+    d, n, nq, nprobe, k = 32, 6000, 40, 8, 10
+    base = rng.standard_normal((100, d)).astype(np.float32) * 3
+    q = (base[0] + 0.3 * rng.standard_normal((nq, d))).astype(np.float32)
+    c = np.concatenate([base, np.repeat(base[:1] + 0.05, 1100, 0)]).astype(np.float32)
+    x = (base[rng.integers(0, 100, n)] + 0.3 * rng.standard_normal((n, d))).astype(np.float32)
+    sctx = _screen_ctx()
+    idx = _index(sctx, c, x, None, nprobe)
+    np.testing.assert_array_equal(idx.probe(q, nprobe), O.ivf_probe(q, c, nprobe))
+    # the fallback's work count is the number of queries that overflowed
+    assert sctx.profile_stats()["ivf_probe_redo"][2] > 0
+    lists = O.ivf_assign(x, c)
+    gd, gi = idx.search(q, k)
+    od, oi = O.ivf_search(q, x, np.arange(n, dtype=np.int64), lists, c, nprobe, k)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
     sctx.close()
 
 

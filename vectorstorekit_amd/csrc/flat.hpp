@@ -80,6 +80,61 @@ __device__ inline float f_up(double v) {
   if ((double)f < v) f = __uint_as_float(__float_as_uint(f) + 1u);
   return f;
 }
+// the largest float at or below v >= 0
+__device__ inline float f_down(double v) {
+  float f = (float)v;
+  if ((double)f > v) f = __uint_as_float(__float_as_uint(f) - 1u);
+  return f;
+}
+
+// The screen's error bound eps for a query with |bf16(q)| = qh and
+// |q - bf16(q)| = qr against rows whose maxima of |bf16(x)| and |x - bf16(x)|
+// are xh and xr, over d dimensions (the derivation heads flat_screen.hip):
+// every screened distance lies within eps of the reference's fp32 one.
+__device__ inline double screen_eps_of(double qh, double qr, double xh, double xr, int32_t d,
+                                       int32_t metric) {
+  const double u = 0x1p-24;
+  const double qn = qh + qr, xn = xh + xr, dd = (double)d;
+  const double e_dot =
+      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
+  const double e_ref = 1.01 * dd * u * qn * xn;
+  double eps;
+  if (metric == VSK_METRIC_DOT)
+    eps = e_dot + e_ref;
+  else if (metric == VSK_METRIC_COSINE_NORMALIZED)
+    eps = e_dot + e_ref + 2.02 * u * (1.0 + qn * xn + e_dot);
+  else
+    eps = 2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05;
+  return eps * 1.0001;
+}
+
+// Screened keys a within the margin of the k-th.  With A_k the k-th
+// smallest screened distance, a row whose a exceeds A_k + 2 eps (for sqrt-L2
+// ranking (A_k + eps)(1 + 2^-20) + eps, so that the square root's rounding
+// cannot tie it) has an exact distance strictly above k rows' and cannot be
+// in the top k: only the keys at or below that limit need their exact
+// distances.  One workgroup per query over 32-bit screened words: word i of
+// query q is words[wseg[q] + i], i < cnt[q] (wseg a multiple of 4), keyed
+// (word, i).  The keys within the margin go to out[q * cap ...], unordered,
+// their number to nout[q]; ok[q] = nout[q] <= cap and bad[q] its negation.
+struct MarginArgs {
+  int64_t nq = 0;
+  int32_t k = 0;
+  const uint32_t *words = nullptr;
+  // query q's words: at wseg[q], cnt[q] of them; or, wseg and cnt null, at
+  // q * wstride (a multiple of 4), wn of them
+  const int64_t *wseg = nullptr, *cnt = nullptr;
+  int64_t wstride = 0, wn = 0;
+  const float *qnh = nullptr, *qnr = nullptr;  // per query |qh|, |q - qh|
+  double xh = 0, xr = 0;
+  int32_t d = 0, metric = 0;
+  uint64_t *out = nullptr;
+  int32_t cap = 0;
+  int32_t *nout = nullptr;
+  uint8_t *ok = nullptr, *bad = nullptr;
+  unsigned long long *nbad = nullptr;  // optional: += the queries over cap
+};
+void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a);
 
 // bf16 hi/lo operand planes of the bf16x3 kernel
 struct SplitPtrs {

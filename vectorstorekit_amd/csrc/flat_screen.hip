@@ -146,20 +146,7 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
 
 // the screen's error bound eps(q) for the metric (see the file comment)
 __device__ double screen_eps(const CheckArgs &a, int64_t q) {
-  const double u = 0x1p-24;
-  const double qh = a.qnh[q], qr = a.qnr[q], xh = a.xh, xr = a.xr;
-  const double qn = qh + qr, xn = xh + xr, dd = (double)a.d;
-  const double e_dot =
-      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
-  const double e_ref = 1.01 * dd * u * qn * xn;
-  double eps;
-  if (a.metric == VSK_METRIC_DOT)
-    eps = e_dot + e_ref;
-  else if (a.metric == VSK_METRIC_COSINE_NORMALIZED)
-    eps = e_dot + e_ref + 2.02 * u * (1.0 + qn * xn + e_dot);
-  else
-    eps = 2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05;
-  return eps * 1.0001;
+  return screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
 }
 
 __global__ void k_screen_check(CheckArgs a) {

@@ -157,21 +157,29 @@ __device__ void block_scan_1024(const int64_t (&v)[NV], int64_t (&out)[NV],
   __syncthreads();
 }
 
-// seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024)
+// seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024);
+// with wseg, the same over the counts rounded up to multiples of 4
 __global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_t m,
-                                                      int64_t *seg) {
-  __shared__ int64_t wsum[16][1];
-  __shared__ int64_t carry[1];
-  if (threadIdx.x == 0) carry[0] = 0;
+                                                      int64_t *seg, int64_t *wseg) {
+  __shared__ int64_t wsum[16][2];
+  __shared__ int64_t carry[2];
+  if (threadIdx.x < 2) carry[threadIdx.x] = 0;
   __syncthreads();
   for (int64_t base = 0; base < m; base += 1024) {
     const int64_t i = base + threadIdx.x;
-    const int64_t v[1] = {i < m ? cnt[i] : 0};
-    int64_t o[1];
-    block_scan_1024<1>(v, o, wsum, carry);
-    if (i < m) seg[i] = o[0];
+    const int64_t c = i < m ? cnt[i] : 0;
+    const int64_t v[2] = {c, (c + 3) & ~3ll};
+    int64_t o[2];
+    block_scan_1024<2>(v, o, wsum, carry);
+    if (i < m) {
+      seg[i] = o[0];
+      if (wseg) wseg[i] = o[1];
+    }
   }
-  if (threadIdx.x == 0) seg[m] = carry[0];
+  if (threadIdx.x == 0) {
+    seg[m] = carry[0];
+    if (wseg) wseg[m] = carry[1];
+  }
 }
 
 // pairs per list
@@ -447,25 +455,54 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // against row l % 16 of the block: 16 lanes write 16 consecutive values of
 // one query.  Wave w takes the list's blocks w, w + 4, ...  Each screened
 // distance goes, as its order-preserving 32-bit word, to its candidate
-// position in the query's segment, out[seg_off[q] + position].
-template <int KS>
+// position in the query's word segment, out[wseg[q] + position].
+//
+// DENSE: the same over one block of rows for every query -- the probe's
+// screen over the centroids: workgroup b takes rows 256 (b % nchunks) ..
+// (at most 256, below nrows) for queries 64 (b / nchunks) .. (below nq),
+// writing out[q * wstride + row].
+struct DenseScreen {
+  int64_t nq, nrows, wstride;
+  int32_t nchunks;
+};
+template <int KS, bool DENSE>
 __global__ __launch_bounds__(256) void k_list_screen(
     const uint16_t *xplane, const float *xsq, int32_t ldb, const int64_t *list_off,
     const uint16_t *qplane, const float *qsq, const int32_t *pairs, const int4 *groups,
-    const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *seg_off,
-    uint32_t *out) {
-  if (blockIdx.x >= *ngroups) return;
+    const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *wseg,
+    uint32_t *out, DenseScreen ds) {
+  if (!DENSE && blockIdx.x >= *ngroups) return;
   __shared__ int64_t s_out[64];  // value address of the list's first row (-1: no query)
   __shared__ float s_qa[64];     // |q|^2
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int4 g = groups[blockIdx.x];
-  const int64_t v0 = list_off[g.x], v1 = list_off[g.x + 1];
-  const int npair = g.z;
+  int64_t v0, v1, q0 = 0;
+  int npair;
+  int4 g{};
+  if constexpr (DENSE) {
+    v0 = 256 * (int64_t)(blockIdx.x % ds.nchunks);
+    v1 = v0 + 256 < ds.nrows ? v0 + 256 : ds.nrows;
+    q0 = 64 * (int64_t)(blockIdx.x / ds.nchunks);
+    npair = ds.nq - q0 < 64 ? (int)(ds.nq - q0) : 64;
+  } else {
+    g = groups[blockIdx.x];
+    v0 = list_off[g.x];
+    v1 = list_off[g.x + 1];
+    npair = g.z;
+  }
+  // the query of slot j (slots past npair repeat the first)
+  auto query = [&](int j) -> int64_t {
+    if constexpr (DENSE) return q0 + (j < npair ? j : 0);
+    return pairs[g.y + (j < npair ? j : 0)] / np;
+  };
   if (threadIdx.x < 64) {
     const int j = threadIdx.x;
-    const int32_t pid = pairs[g.y + (j < npair ? j : 0)];
-    const int32_t q = pid / np;
-    s_out[j] = j < npair ? seg_off[q] + pos_base[pid] : -1;
+    const int64_t q = query(j);
+    if constexpr (DENSE) {
+      s_out[j] = j < npair ? q * ds.wstride + v0 : -1;
+    } else {
+      const int32_t pid = pairs[g.y + (j < npair ? j : 0)];
+      s_out[j] = j < npair ? wseg[q] + pos_base[pid] : -1;
+    }
     s_qa[j] = qsq[q];
   }
   const int kc = 8 * (lane >> 4);  // this lane's 8 dims of a k-step
@@ -474,10 +511,10 @@ __global__ __launch_bounds__(256) void k_list_screen(
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int j = 16 * t + (lane & 15);
-    const int32_t q = pairs[g.y + (j < npair ? j : 0)] / np;
+    const int64_t q = query(j);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + (int64_t)q * ldb + 32 * ks + kc);
+      qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + q * ldb + 32 * ks + kc);
   }
   __syncthreads();
   for (int64_t b = v0 + 16 * w; b < v1; b += 64) {
@@ -508,39 +545,62 @@ __global__ __launch_bounds__(256) void k_list_screen(
 }
 
 // exact keys for screened ones: key (a, position) -> (the reference's
-// sequential fp32 distance, position), the same sum as k_list_scan.  Query
-// q's keys are the first cnt[q] of in[q*in_stride ...], written to
-// out[q*in_stride ...]; or (cnt null) every position of the query's
-// candidates gets its exact key in its segment of seg_off, in[seg_off[q] +
-// position]; only queries with active[q].  One wave per query, a
-// key per lane; each lane loads 64 floats of its row and of the query ahead
-// of their sequential sum.  A position maps to its probe slot -- the last
-// one whose base is at or below it, which holds at least one row past the
-// base -- and so to the row.
-__global__ __launch_bounds__(256) void k_list_rescore(
-    const float *rows, int32_t ld, const int64_t *list_off, const float *Q,
-    const int32_t *probes, int32_t np, const int64_t *pos_base, uint64_t *in,
-    int64_t in_stride, const int32_t *cnt, const int64_t *seg_off, uint64_t *out,
-    const uint8_t *active, int64_t nq, int32_t squared) {
+// sequential fp32 distance, position), the same sum as k_list_scan (and,
+// sqrt taken, as the exact centroid scan).  Query q's keys are the first
+// cnt[q] of in[q*in_stride ...], written to out[q*in_stride ...]; or (cnt
+// null) every position of the query's candidates gets its exact key in
+// place, at in[seg_off[q] + position] (or in[q*all_n + position], all_n
+// positions each, without seg_off); only queries with active[q].  One wave
+// per query, a key per lane; each lane loads 64 floats of its row and of
+// the query ahead of their sequential sum.  With list_off, a position maps
+// to its probe slot -- the last one whose base is at or below it, which
+// holds at least one row past the base -- and so to the row; without, the
+// position is the row.
+struct RescoreArgs {
+  const float *rows;
+  int32_t ld;
+  const int64_t *list_off;
+  const float *Q;
+  const int32_t *probes;
+  int32_t np;
+  const int64_t *pos_base;
+  uint64_t *in;
+  int64_t in_stride;
+  const int32_t *cnt;
+  const int64_t *seg_off;
+  int64_t all_n;
+  uint64_t *out;
+  const uint8_t *active;
+  int64_t nq;
+  int32_t squared;
+};
+__global__ __launch_bounds__(256) void k_list_rescore(RescoreArgs a) {
 #pragma clang fp contract(off)
   const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (q >= nq || !active[q]) return;
-  const uint64_t *src = cnt ? in + q * in_stride : nullptr;
-  uint64_t *dst = cnt ? out + q * in_stride : in + seg_off[q];
-  const int64_t n = cnt ? (int64_t)cnt[q] : seg_off[q + 1] - seg_off[q];
-  const float *qq = Q + q * ld;
-  const int64_t *pb = pos_base + q * np;
-  const int32_t *pr = probes + q * np;
+  if (q >= a.nq || !a.active[q]) return;
+  const int32_t ld = a.ld;
+  const uint64_t *src = a.cnt ? a.in + q * a.in_stride : nullptr;
+  uint64_t *dst = a.cnt ? a.out + q * a.in_stride
+                        : a.in + (a.seg_off ? a.seg_off[q] : q * a.all_n);
+  const int64_t n = a.cnt ? (int64_t)a.cnt[q]
+                          : (a.seg_off ? a.seg_off[q + 1] - a.seg_off[q] : a.all_n);
+  const float *qq = a.Q + q * ld;
+  const int64_t *pb = a.list_off ? a.pos_base + q * a.np : nullptr;
+  const int32_t *pr = a.list_off ? a.probes + q * a.np : nullptr;
   for (int64_t i = lane; i < n; i += 64) {
     const int64_t p = src ? (int64_t)(uint32_t)src[i] : i;
-    int lo = 0, hi = np;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (pb[mid] <= p) lo = mid;
-      else hi = mid;
+    int64_t row = p;
+    if (a.list_off) {
+      int lo = 0, hi = a.np;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pb[mid] <= p) lo = mid;
+        else hi = mid;
+      }
+      row = a.list_off[pr[lo]] + (p - pb[lo]);
     }
-    const float *x = rows + (list_off[pr[lo]] + (p - pb[lo])) * ld;
+    const float *x = a.rows + row * ld;
     float acc = 0.f;
     for (int c0 = 0; c0 < ld; c0 += 64) {
       const int m = ld - c0 < 64 ? (ld - c0) >> 2 : 16;  // ld is a multiple of 4
@@ -565,15 +625,8 @@ __global__ __launch_bounds__(256) void k_list_rescore(
           acc = acc + t * t;
         }
     }
-    dst[i] = vsk_key(squared ? acc : sqrtf(acc), (uint32_t)p);
+    dst[i] = vsk_key(a.squared ? acc : sqrtf(acc), (uint32_t)p);
   }
-}
-
-__global__ void k_mask_not(const uint8_t *ok, int64_t n, uint8_t *out, const int32_t *fails,
-                           int64_t *fails64) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = ok[i] ? 0 : 1;
-  if (i == 0 && fails64) *fails64 = *fails;
 }
 
 static unsigned grid1(int64_t n, int threads = 256) {
@@ -620,13 +673,36 @@ static void ivf_assign_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dx,
 
 static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
                             int64_t nq, int32_t np, uint64_t *keys);
+static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int64_t nq,
+                         int32_t np, const ArgminQueries &qp, uint64_t *keys);
 
-// top-nprobe centroids per query (ties by centroid index)
+// whether the probe goes through the bf16 screen over the centroids: at
+// most 256 dims, enough work (forced by VSK_FLAT_KERNEL=screen, off by
+// =exact / =bf16x3 / =fp32)
+static bool probe_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t nq, int32_t np) {
+  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (ivf->d > 256 || np > VSK_MAX_K) return false;
+  return ctx->flat_force_screen ||
+         (double)nq * (double)ivf->nlist * (double)ivf->d >= (double)(1ll << 30);
+}
+
+// top-nprobe centroids per query (ties by centroid index); qp: the
+// queries' bf16 planes when the caller has them
 static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
-                             int64_t nq, int32_t np, int32_t *probes) {
+                             int64_t nq, int32_t np, int32_t *probes,
+                             const ArgminQueries *qp = nullptr) {
   uint64_t *keys = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.probe_keys", sizeof(uint64_t) * nq * np));
-  ivf_probe_exact(ctx, ivf, dq, nq, np, keys);
+  if (probe_screen_applies(ctx, ivf, nq, np)) {
+    if (qp) {
+      probe_screen(ctx, ivf, dq, nq, np, *qp, keys);
+    } else {
+      const ArgminQueries own = argmin_queries(ctx, dq, nq, ivf->d, ivf->ld, "ivf.sq");
+      probe_screen(ctx, ivf, dq, nq, np, own, keys);
+    }
+  } else {
+    ivf_probe_exact(ctx, ivf, dq, nq, np, keys);
+  }
   KernelTimer t(ctx, "ivf_probe_ids");
   k_keys_to_tie<<<grid1(nq * np), 256, 0, ctx->stream>>>(keys, nq * np, probes);
   check_launch("ivf_probe_ids");
@@ -664,7 +740,7 @@ static bool list_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t metric
                                 double ncand) {
   if (ctx->flat_no_screen || ctx->flat_fp32) return false;
   if (metric != VSK_METRIC_L2 && metric != VSK_METRIC_L2SQ) return false;
-  if (ivf->d > 256 || screen_keep(k) > VSK_MAX_K) return false;
+  if (ivf->d > 256) return false;
   return ctx->flat_force_screen || ncand * ivf->d >= (double)(1ll << 30);
 }
 
@@ -929,31 +1005,34 @@ static void make_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes,
 }
 
 // one query batch of the screened list scan: the screened distance of
-// every candidate (32 bits, at its position in the query's segment), the
-// kc smallest per query, the bound check, then the exact top k of the kept
-// keys within the margin -- or, for a query failing the check, of every
-// candidate -- into best[b0 * k ...].  No read-back: the fallback's launches
-// find no active query when none fails.
+// every candidate (a 32-bit word at its position in the query's word
+// segment, wseg), the keys within the margin of the k-th screened distance
+// (at most cap per query), their exact distances and the top k of those --
+// or, for a query with more than cap keys in the margin, the top k of
+// every candidate's exact distance (in its segment of cand, seg_off) --
+// into best[b0 * k ...].  No read-back: the fallback's launches find no
+// active query when none overflows.
 static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQueries &qp,
                               const float *dq, int64_t b0, int64_t nb, int32_t np, int32_t k,
-                              int32_t kc, int32_t metric, const int32_t *probes,
-                              const int64_t *pos_base, const int64_t *dseg,
+                              int32_t metric, const int32_t *probes, const int64_t *pos_base,
+                              const int64_t *cnt, const int64_t *dseg, const int64_t *wseg,
                               const ListGroups &lg, uint64_t *cand, uint64_t *best) {
   const int32_t ld = ivf->ld, ldb = ivf->xldb, nlist = ivf->nlist;
   const int64_t npairs = nb * np;
   const int32_t *bprobes = probes + b0 * np;
   const int64_t *bpos = pos_base + b0 * np;
-  // the screened words share cand's memory: its first half holds them
+  // the screened words share cand's memory; the fallback's exact keys
+  // overwrite them after the margin gather has read them
   uint32_t *words = reinterpret_cast<uint32_t *>(cand);
   {
     KernelTimer t(ctx, "ivf_list_screen");
     t.device_work(dseg + nb);
     const unsigned gmax = (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, 64));
 #define VSK_LS(KS)                                                                          \
-  k_list_screen<KS><<<gmax, 256, 0, ctx->stream>>>(                                        \
+  k_list_screen<KS, false><<<gmax, 256, 0, ctx->stream>>>(                                 \
       ivf->xplane.as<uint16_t>(), ivf->xsq.as<float>(), ldb, ivf->list_off.as<int64_t>(),   \
       qp.qh + b0 * qp.ldb, qp.qsq + b0, lg.pairs, lg.groups, lg.gstart + nlist, np, bpos,   \
-      dseg, words)
+      wseg, words, DenseScreen{})
     switch (ldb / 32) {
     case 2: VSK_LS(2); break;
     case 4: VSK_LS(4); break;
@@ -963,53 +1042,60 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
 #undef VSK_LS
     check_launch("ivf_list_screen");
   }
+  const int32_t cap = std::max<int32_t>(1024, 4 * k);
   uint64_t *kept = static_cast<uint64_t *>(
-      ctx->scratch_ptr("ivf.kept", sizeof(uint64_t) * nb * kc));
+      ctx->scratch_ptr("ivf.kept", sizeof(uint64_t) * nb * cap));
   uint64_t *exact = static_cast<uint64_t *>(
-      ctx->scratch_ptr("ivf.kexact", sizeof(uint64_t) * nb * kc));
+      ctx->scratch_ptr("ivf.kexact", sizeof(uint64_t) * nb * cap));
   uint8_t *ok = static_cast<uint8_t *>(ctx->scratch_ptr("ivf.ok", 2 * (size_t)nb));
   uint8_t *bad = ok + nb;
-  int32_t *nvalid = static_cast<int32_t *>(ctx->scratch_ptr("ivf.nvalid", 4 * (nb + 4)));
-  int32_t *fails = nvalid + nb;
-  // the failing queries' count as the fallback's work (profiling)
-  int64_t *fails64 = ctx->profile ? reinterpret_cast<int64_t *>(nvalid + ceil_div(nb + 1, 2) * 2)
-                                  : nullptr;
-  fill_i32(ctx, fails, 1, 0);
+  int32_t *nout = static_cast<int32_t *>(ctx->scratch_ptr("ivf.nout", 4 * (size_t)nb + 8));
+  // the overflowing queries' count as the fallback's work (profiling)
+  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.nbad", 8)) : nullptr;
+  if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
   {
-    SelectArgs sa;
-    sa.nq = nb;
-    sa.k = kc;
-    sa.cand32 = words;
-    sa.seg_off = dseg;
-    sa.best_out = kept;
-    launch_select(ctx, sa, "ivf_screen_select");
+    MarginArgs ma;
+    ma.nq = nb;
+    ma.k = k;
+    ma.words = words;
+    ma.wseg = wseg;
+    ma.cnt = cnt + b0;
+    ma.qnh = qp.qnh + b0;
+    ma.qnr = qp.qnr + b0;
+    ma.xh = ivf->xh_max;
+    ma.xr = ivf->xr_max;
+    ma.d = ivf->d;
+    ma.metric = metric;
+    ma.out = kept;
+    ma.cap = cap;
+    ma.nout = nout;
+    ma.ok = ok;
+    ma.bad = bad;
+    ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
+    launch_screen_margin(ctx, ma);
   }
-  CheckArgs ca{};
-  ca.best = kept;
-  ca.nq = nb;
-  ca.k = k;
-  ca.kc = kc;
-  ca.d = ivf->d;
-  ca.metric = metric;
-  ca.qnh = qp.qnh + b0;
-  ca.qnr = qp.qnr + b0;
-  ca.xh = ivf->xh_max;
-  ca.xr = ivf->xr_max;
-  ca.ok = ok;
-  ca.nvalid = nvalid;
-  ca.fails = fails;
-  ca.test = true;
-  launch_screen_check(ctx, ca);
-  k_mask_not<<<grid1(nb), 256, 0, ctx->stream>>>(ok, nb, bad, fails, fails64);
-  check_launch("ivf_mask");
   const int32_t sq = metric == VSK_METRIC_L2SQ ? 1 : 0;
   const float *rows = ivf->rows.as<float>();
   const int64_t *loff = ivf->list_off.as<int64_t>();
+  RescoreArgs ra{};
+  ra.rows = rows;
+  ra.ld = ld;
+  ra.list_off = loff;
+  ra.Q = dq + b0 * ld;
+  ra.probes = bprobes;
+  ra.np = np;
+  ra.pos_base = bpos;
+  ra.nq = nb;
+  ra.squared = sq;
   {
     KernelTimer t(ctx, "ivf_screen_rescore");
-    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(
-        rows, ld, loff, dq + b0 * ld, bprobes, np, bpos, kept, kc, nvalid, nullptr, exact, ok,
-        nb, sq);
+    RescoreArgs r = ra;
+    r.in = kept;
+    r.in_stride = cap;
+    r.cnt = nout;
+    r.out = exact;
+    r.active = ok;
+    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(r);
     check_launch("ivf_screen_rescore");
   }
   {
@@ -1017,21 +1103,23 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     sa.nq = nb;
     sa.k = k;
     sa.cand = exact;
-    sa.cap = kc;
-    sa.counts = nvalid;
+    sa.cap = cap;
+    sa.counts = nout;
     sa.active = ok;
+    sa.regs = cap <= 8192;
+    sa.small = cap <= 1024;
     sa.best_out = best + b0 * k;
     launch_select(ctx, sa, "ivf_select");
   }
-  // queries whose kept keys could miss a top-k row: every candidate exact,
-  // in its segment of cand (over the screened words, which only the
-  // selection above read)
+  // queries with more than cap keys in the margin: every candidate exact
   {
     KernelTimer t(ctx, "ivf_screen_redo");
-    if (fails64) t.device_work(fails64);
-    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(
-        rows, ld, loff, dq + b0 * ld, bprobes, np, bpos, cand, 0, nullptr, dseg, nullptr, bad,
-        nb, sq);
+    if (nbad) t.device_work(nbad);
+    RescoreArgs r = ra;
+    r.in = cand;
+    r.seg_off = dseg;
+    r.active = bad;
+    k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(r);
     check_launch("ivf_screen_redo");
   }
   SelectArgs sa;
@@ -1043,6 +1131,128 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
   sa.best_out = best + b0 * k;
   launch_select(ctx, sa, "ivf_select");
 }
+
+namespace vsk {
+
+// The probe through the bf16 screen: the screened distance of every (query,
+// centroid) as a 32-bit word, the keys within the margin of the np-th
+// screened distance, their exact sqrt-L2 (dimension order, the exact
+// scan's own sum) keyed (distance, centroid) and the top np of those; a
+// query with more than cap keys in the margin has every centroid's exact
+// key ranked instead.  No read-back.
+static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int64_t nq,
+                         int32_t np, const ArgminQueries &qp, uint64_t *keys) {
+  const vsk_db *cdb = &ivf->centroids;
+  make_split(ctx, cdb, dq, 0, false, nullptr, nullptr);  // the centroids' planes
+  const int32_t nlist = ivf->nlist, ld = ivf->ld, ldb = cdb->ldb;
+  const int64_t wstride = ceil_div(nlist, 4) * 4;
+  // batches whose words and fallback keys stay under 1 GiB
+  const int64_t qb = std::max<int64_t>(1, std::min<int64_t>(nq, (1ll << 27) / wstride));
+  const int32_t cap = std::max<int32_t>(1024, 4 * np);
+  uint32_t *words = static_cast<uint32_t *>(
+      ctx->scratch_ptr("ivf.pwords", sizeof(uint32_t) * qb * wstride));
+  uint64_t *all = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.pall", sizeof(uint64_t) * qb * nlist));
+  uint64_t *kept = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.pkept", sizeof(uint64_t) * qb * cap));
+  uint64_t *exact = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.pexact", sizeof(uint64_t) * qb * cap));
+  uint8_t *ok = static_cast<uint8_t *>(ctx->scratch_ptr("ivf.pok", 2 * (size_t)qb));
+  uint8_t *bad = ok + qb;
+  int32_t *nout = static_cast<int32_t *>(ctx->scratch_ptr("ivf.pnout", 4 * (size_t)qb));
+  // the overflowing queries' count as the fallback's work (profiling)
+  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.pnbad", 8)) : nullptr;
+  const int32_t nchunks = (int32_t)ceil_div(nlist, 256);
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    {
+      KernelTimer t(ctx, "ivf_probe_screen", (double)nb * nlist);
+      const unsigned grid = (unsigned)(nchunks * ceil_div(nb, 64));
+      const DenseScreen ds{nb, nlist, wstride, nchunks};
+#define VSK_PS(KS)                                                                            \
+  k_list_screen<KS, true><<<grid, 256, 0, ctx->stream>>>(                                    \
+      cdb->split.as<uint16_t>(), cdb->sqnorm.as<float>(), ldb, nullptr, qp.qh + b0 * qp.ldb, \
+      qp.qsq + b0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, words, ds)
+      switch (ldb / 32) {
+      case 2: VSK_PS(2); break;
+      case 4: VSK_PS(4); break;
+      case 6: VSK_PS(6); break;
+      default: VSK_PS(8); break;
+      }
+#undef VSK_PS
+      check_launch("ivf_probe_screen");
+    }
+    MarginArgs ma;
+    ma.nq = nb;
+    ma.k = np;
+    ma.words = words;
+    ma.wstride = wstride;
+    ma.wn = nlist;
+    ma.qnh = qp.qnh + b0;
+    ma.qnr = qp.qnr + b0;
+    ma.xh = cdb->split_max_hi;
+    ma.xr = cdb->split_max_res;
+    ma.d = ivf->d;
+    ma.metric = VSK_METRIC_L2;
+    ma.out = kept;
+    ma.cap = cap;
+    ma.nout = nout;
+    ma.ok = ok;
+    ma.bad = bad;
+    if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
+    ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
+    launch_screen_margin(ctx, ma);
+    RescoreArgs ra{};
+    ra.rows = cdb->x.as<float>();
+    ra.ld = ld;
+    ra.Q = dq + b0 * ld;
+    ra.nq = nb;
+    {
+      KernelTimer t(ctx, "ivf_probe_rescore");
+      RescoreArgs r = ra;
+      r.in = kept;
+      r.in_stride = cap;
+      r.cnt = nout;
+      r.out = exact;
+      r.active = ok;
+      k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(r);
+      check_launch("ivf_probe_rescore");
+    }
+    SelectArgs sa;
+    sa.nq = nb;
+    sa.k = np;
+    sa.cand = exact;
+    sa.cap = cap;
+    sa.counts = nout;
+    sa.active = ok;
+    sa.regs = cap <= 8192;
+    sa.small = cap <= 1024;
+    sa.best_out = keys + b0 * np;
+    launch_select(ctx, sa, "ivf_probe_select");
+    // queries with more than cap keys in the margin: every centroid exact
+    {
+      KernelTimer t(ctx, "ivf_probe_redo");
+      if (nbad) t.device_work(nbad);
+      RescoreArgs r = ra;
+      r.in = all;
+      r.all_n = nlist;
+      r.active = bad;
+      k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(r);
+      check_launch("ivf_probe_redo");
+    }
+    SelectArgs sb;
+    sb.nq = nb;
+    sb.k = np;
+    sb.cand = all;
+    sb.cap = nlist;
+    sb.active = bad;
+    sb.regs = true;
+    sb.best_out = keys + b0 * np;
+    launch_select(ctx, sb, "ivf_probe_select");
+  }
+}
+
+}  // namespace vsk
 
 // kind 0: the rows (metric L2 / L2SQ); 1: SQ8 codes, qextra = nq x d int8
 // query codes; 2: PQ codes, qextra = the vsk_pq whose tables score them
@@ -1109,10 +1319,20 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
 
+  // the bf16 screen of the list scan (kind 0) and of the probe share the
+  // queries' bf16 planes
+  const double per_query = ivf->nlist > 0 ? (double)ivf->total * np / ivf->nlist : 0.0;
+  const bool screen =
+      kind == 0 && list_screen_applies(ctx, ivf, metric, k, (double)nq * per_query);
+  const bool exact_all = np == ivf->nlist && np > VSK_MAX_K;
+  ArgminQueries qp;
+  if (screen || (!exact_all && probe_screen_applies(ctx, ivf, nq, np)))
+    qp = argmin_queries(ctx, dq, nq, ivf->d, ld, "ivf.sq");
+
   // 1. probes
   int32_t *probes = static_cast<int32_t *>(
       ctx->scratch_ptr("ivf.probes", sizeof(int32_t) * nq * np));
-  if (np == ivf->nlist && np > VSK_MAX_K) {
+  if (exact_all) {
     // .exact with more lists than a selection holds: every list, in index
     // order (the stable sort's order when all lists are kept is by
     // distance, but the candidate set -- and so the result -- is the same
@@ -1123,7 +1343,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     VSK_HIP(hipMemcpyAsync(probes, all.data(), 4 * all.size(),
                            hipMemcpyHostToDevice, ctx->stream));
   } else {
-    ivf_probe_device(ctx, ivf, dq, nq, np, probes);
+    ivf_probe_device(ctx, ivf, dq, nq, np, probes, qp.qh ? &qp : nullptr);
   }
   // 2. candidate counts and probe position bases
   int64_t *pos_base = static_cast<int64_t *>(
@@ -1149,18 +1369,9 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   const int64_t ubound = probe_bound(ivf, np);
   const int64_t qb = std::max<int64_t>(
       1, std::min<int64_t>(nq, (1ll << 27) / std::max<int64_t>(ubound, 1)));
-  const double per_query = ivf->nlist > 0 ? (double)ivf->total * np / ivf->nlist : 0.0;
-  // the bf16 screen (kind 0): groups of 64 queries, kc screened keys kept
-  // per query
-  const bool screen =
-      kind == 0 && list_screen_applies(ctx, ivf, metric, k, (double)nq * per_query);
+  // the screen's groups are 64 queries
   const int G = screen ? 64 : QG;
-  const int32_t kc = screen ? screen_keep(k) : 0;
-  ArgminQueries qp;
-  if (screen) {
-    list_screen_plane(ctx, ivf);
-    qp = argmin_queries(ctx, dq, nq, ivf->d, ld, "ivf.sq");
-  }
+  if (screen) list_screen_plane(ctx, ivf);
   {
     KernelTimer t(ctx, "ivf_probe_bases");
     k_probe_bases<<<grid1(nq), 256, 0, ctx->stream>>>(
@@ -1173,7 +1384,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.best", sizeof(uint64_t) * nq * k));
   int64_t *dseg = static_cast<int64_t *>(
-      ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * (nbmax + 1)));
+      ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * 2 * (nbmax + 1)));
+  int64_t *wseg = screen ? dseg + (nbmax + 1) : nullptr;
   int64_t *loffs = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
   int64_t *lstart = loffs, *cursor = loffs + (nlist + 1), *gstart = loffs + 2 * (nlist + 1);
@@ -1185,8 +1397,11 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   ListGroups lgp = lg;
   lgp.pairs = dpairs;
   lgp.groups = dgroups;
-  uint64_t *cand = static_cast<uint64_t *>(
-      ctx->scratch_ptr("ivf.cand", sizeof(uint64_t) * (nbmax * ubound + 1)));
+  // (the screen's 32-bit words, each query's padded to a multiple of 4,
+  // share this memory)
+  uint64_t *cand = static_cast<uint64_t *>(ctx->scratch_ptr(
+      "ivf.cand", std::max(sizeof(uint64_t) * (nbmax * ubound + 1),
+                           sizeof(uint32_t) * (nbmax * (ubound + 3) + 4))));
   const int64_t *loff = ivf->list_off.as<int64_t>();
 
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
@@ -1196,13 +1411,13 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     // 3. segment offsets; pairs grouped by list, groups of up to G pairs
     {
       KernelTimer t(ctx, "ivf_group_pairs");
-      k_seg_offsets<<<1, 1024, 0, ctx->stream>>>(cnt + b0, nb, dseg);
+      k_seg_offsets<<<1, 1024, 0, ctx->stream>>>(cnt + b0, nb, dseg, wseg);
       check_launch("ivf_seg_offsets");
       if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     }
     if (screen) {
-      list_screen_batch(ctx, ivf, qp, dq, b0, nb, np, k, kc, metric, probes, pos_base, dseg,
-                        lgp, cand, best);
+      list_screen_batch(ctx, ivf, qp, dq, b0, nb, np, k, metric, probes, pos_base, cnt, dseg,
+                        wseg, lgp, cand, best);
       continue;
     }
     const int64_t *ngroups = gstart + nlist;

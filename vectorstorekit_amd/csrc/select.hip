@@ -14,7 +14,7 @@
 // that still match the resolved prefix; it stops early as soon as the bucket
 // holding the k-th key is taken whole.  The <= k winners are gathered into LDS and
 // bitonic-sorted (at most 1024 of them).
-#include "vsk_api.hpp"
+#include "flat.hpp"
 
 namespace vsk {
 
@@ -27,6 +27,131 @@ __device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np, const uint64_
                                     const uint32_t *C32, int64_t i) {
   if constexpr (W32) return ((uint64_t)C32[i] << 32) | (uint32_t)i;
   return i < np ? P[i] : C[i - np];
+}
+
+// block-wide shared state of a threshold search
+struct SelShared {
+  uint32_t hist[256 + 32];
+  int bucket, take_all;
+  uint32_t before, bcount;
+  uint64_t lo[SEL_THREADS / 64], hi[SEL_THREADS / 64];
+};
+
+// Most-significant-digit radix search over one query's keys, which
+// each_key(f) hands to f (every thread its share; NONE skipped): T_out is a
+// key with exactly the k smallest keys at or below it, or take_all when
+// there are at most k keys; hi_out the largest key.  Called by every
+// thread of the block.
+template <class EachKey>
+__device__ void radix_threshold(EachKey &&each_key, int32_t k, SelShared &sh, uint64_t &T_out,
+                                bool &take_all_out, uint64_t &hi_out) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  // smallest and largest key: the digits start at the highest bit where
+  // they differ (the distances of one query share their leading bits, and a
+  // histogram of a digit every key agrees on is a pass spent on one bin)
+  uint64_t lo = VSK_KEY_NONE, hi = 0;
+  each_key([&](uint64_t key) {
+    if (key == VSK_KEY_NONE) return;
+    lo = key < lo ? key : lo;
+    hi = key > hi ? key : hi;
+  });
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 > hi ? h2 : hi;
+  }
+  if (lane == 0) {
+    sh.lo[tid >> 6] = lo;
+    sh.hi[tid >> 6] = hi;
+  }
+  __syncthreads();
+  lo = sh.lo[0];
+  hi = sh.hi[0];
+#pragma unroll
+  for (int wv = 1; wv < SEL_THREADS / 64; ++wv) {
+    lo = sh.lo[wv] < lo ? sh.lo[wv] : lo;
+    hi = sh.hi[wv] > hi ? sh.hi[wv] : hi;
+  }
+
+  uint64_t prefix = 0, mask = 0, T = VSK_KEY_NONE;
+  int64_t need = k;
+  bool take_all = false;
+  // top: the highest undecided bit (inclusive); bits above it are common
+  int top = 63;
+  if (lo != VSK_KEY_NONE && lo != hi) {
+    top = 63 - __builtin_clzll(lo ^ hi);
+    mask = top == 63 ? 0 : ~((2ull << top) - 1);
+    prefix = lo & mask;
+  }
+  bool first = true;
+
+  while (top >= 0) {
+    const int width = top + 1 >= 8 ? 8 : top + 1;
+    const int shift = top + 1 - width;
+    const uint32_t dmask = (1u << width) - 1;
+    for (int i = tid; i < 256 + 32; i += SEL_THREADS) sh.hist[i] = 0;
+    __syncthreads();
+    // without branches: a key outside the prefix counts into one of 32
+    // spare bins (distinct banks across a half-wave)
+    const uint32_t spare = 256u + (uint32_t)(lane & 31);
+    each_key([&](uint64_t key) {
+      const bool in = key != VSK_KEY_NONE && (key & mask) == prefix;
+      atomicAdd(&sh.hist[in ? (uint32_t)(key >> shift) & dmask : spare], 1u);
+    });
+    __syncthreads();
+    if (tid < 64) {
+      uint32_t h0 = sh.hist[4 * lane], h1 = sh.hist[4 * lane + 1],
+               h2 = sh.hist[4 * lane + 2], h3 = sh.hist[4 * lane + 3];
+      uint32_t s = h0 + h1 + h2 + h3;
+      uint32_t incl = s;
+      for (int o = 1; o < 64; o <<= 1) {
+        uint32_t v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      uint32_t all = __shfl(incl, 63);
+      uint32_t excl = incl - s;
+      if (first && all <= (uint32_t)k) {
+        if (lane == 0) sh.take_all = 1;
+      } else {
+        if (lane == 0) sh.take_all = 0;
+        bool here = excl < (uint64_t)need && (uint64_t)need <= incl;
+        if (here) {
+          uint32_t hs[4] = {h0, h1, h2, h3};
+          uint32_t before = excl;
+          int j = 0;
+          while (before + hs[j] < (uint64_t)need) {
+            before += hs[j];
+            ++j;
+          }
+          sh.bucket = 4 * lane + j;
+          sh.before = before;
+          sh.bcount = hs[j];
+        }
+      }
+    }
+    __syncthreads();
+    if (sh.take_all) {
+      take_all = true;
+      break;
+    }
+    first = false;
+    const uint32_t b = (uint32_t)sh.bucket;
+    need -= sh.before;
+    prefix |= (uint64_t)b << shift;
+    mask |= (uint64_t)dmask << shift;
+    const bool full = (uint64_t)sh.bcount == (uint64_t)need;
+    __syncthreads();  // everyone has read the sh_* values
+    if (full || shift == 0) {
+      T = prefix | ~mask;
+      break;
+    }
+    top = shift - 1;
+  }
+
+  T_out = T;
+  take_all_out = take_all;
+  hi_out = hi;
 }
 
 // REG: keys per thread held in registers when a query's list fits (REG x
@@ -99,112 +224,12 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
     }
   };
 
-  __shared__ uint32_t hist[256];
+  __shared__ SelShared sh;
   __shared__ uint64_t sel[VSK_MAX_K];
-  __shared__ int sh_bucket, sh_take_all;
-  __shared__ uint32_t sh_before, sh_bcount;
   __shared__ int sel_count;
-  __shared__ uint64_t sh_lo[SEL_THREADS / 64], sh_hi[SEL_THREADS / 64];
-
-  // smallest and largest key: the digits start at the highest bit where
-  // they differ (the distances of one query share their leading bits, and a
-  // histogram of a digit every key agrees on is a pass spent on one bin)
-  uint64_t lo = VSK_KEY_NONE, hi = 0;
-  each_key([&](uint64_t key) {
-    if (key == VSK_KEY_NONE) return;
-    lo = key < lo ? key : lo;
-    hi = key > hi ? key : hi;
-  });
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
-    lo = l2 < lo ? l2 : lo;
-    hi = h2 > hi ? h2 : hi;
-  }
-  if (lane == 0) {
-    sh_lo[tid >> 6] = lo;
-    sh_hi[tid >> 6] = hi;
-  }
-  __syncthreads();
-  lo = sh_lo[0];
-  hi = sh_hi[0];
-#pragma unroll
-  for (int wv = 1; wv < SEL_THREADS / 64; ++wv) {
-    lo = sh_lo[wv] < lo ? sh_lo[wv] : lo;
-    hi = sh_hi[wv] > hi ? sh_hi[wv] : hi;
-  }
-
-  uint64_t prefix = 0, mask = 0, T = VSK_KEY_NONE;
-  int64_t need = k;
-  bool take_all = false;
-  // top: the highest undecided bit (inclusive); bits above it are common
-  int top = 63;
-  if (lo != VSK_KEY_NONE && lo != hi) {
-    top = 63 - __builtin_clzll(lo ^ hi);
-    mask = top == 63 ? 0 : ~((2ull << top) - 1);
-    prefix = lo & mask;
-  }
-  bool first = true;
-
-  while (top >= 0) {
-    const int width = top + 1 >= 8 ? 8 : top + 1;
-    const int shift = top + 1 - width;
-    const uint32_t dmask = (1u << width) - 1;
-    for (int i = tid; i < 256; i += SEL_THREADS) hist[i] = 0;
-    __syncthreads();
-    each_key([&](uint64_t key) {
-      if (key != VSK_KEY_NONE && (key & mask) == prefix)
-        atomicAdd(&hist[(uint32_t)(key >> shift) & dmask], 1u);
-    });
-    __syncthreads();
-    if (tid < 64) {
-      uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1],
-               h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
-      uint32_t s = h0 + h1 + h2 + h3;
-      uint32_t incl = s;
-      for (int o = 1; o < 64; o <<= 1) {
-        uint32_t v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
-      }
-      uint32_t all = __shfl(incl, 63);
-      uint32_t excl = incl - s;
-      if (first && all <= (uint32_t)k) {
-        if (lane == 0) sh_take_all = 1;
-      } else {
-        if (lane == 0) sh_take_all = 0;
-        bool here = excl < (uint64_t)need && (uint64_t)need <= incl;
-        if (here) {
-          uint32_t hs[4] = {h0, h1, h2, h3};
-          uint32_t before = excl;
-          int j = 0;
-          while (before + hs[j] < (uint64_t)need) {
-            before += hs[j];
-            ++j;
-          }
-          sh_bucket = 4 * lane + j;
-          sh_before = before;
-          sh_bcount = hs[j];
-        }
-      }
-    }
-    __syncthreads();
-    if (sh_take_all) {
-      take_all = true;
-      break;
-    }
-    first = false;
-    const uint32_t b = (uint32_t)sh_bucket;
-    need -= sh_before;
-    prefix |= (uint64_t)b << shift;
-    mask |= (uint64_t)dmask << shift;
-    const bool full = (uint64_t)sh_bcount == (uint64_t)need;
-    __syncthreads();  // everyone has read the sh_* values
-    if (full || shift == 0) {
-      T = prefix | ~mask;
-      break;
-    }
-    top = shift - 1;
-  }
+  uint64_t T, hi;
+  bool take_all;
+  radix_threshold(each_key, k, sh, T, take_all, hi);
 
   if (tid == 0) sel_count = 0;
   __syncthreads();
@@ -250,11 +275,253 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   if (tid == 0 && a.thresh) a.thresh[q] = (m >= k) ? sel[k - 1] : VSK_KEY_NONE;
 }
 
+// Short lists (at most 1,024 keys a query, counts given): one wave per
+// query sorts its whole list in registers -- a bitonic network over 64 R
+// keys, R a lane (R the smallest power of two holding the list), the
+// partner of key e at distance j in the same lane when j < R, else in lane
+// ^ j / R by a shuffle -- and writes the first k.  No LDS, no barrier.
+template <int R>
+__device__ void wave_sort_write(const uint64_t *C, int64_t n, int32_t k, uint64_t *out) {
+  const int lane = threadIdx.x & 63;
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t e = (int64_t)lane * R + r;
+    v[r] = e < n ? C[e] : VSK_KEY_NONE;
+  }
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      if (j < R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r & j) continue;
+          const int e = lane * R + r;  // the lower of the pair
+          const bool asc = (e & size) == 0;
+          const uint64_t a = v[r], b = v[r + j];
+          const bool sw = (a > b) == asc;
+          v[r] = sw ? b : a;
+          v[r + j] = sw ? a : b;
+        }
+      } else {
+        const int lj = j / R;
+        const bool lower = (lane & lj) == 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int e = lane * R + r;
+          const bool asc = (e & size) == 0;
+          const uint64_t p = __shfl_xor(v[r], lj);
+          const uint64_t mn = v[r] < p ? v[r] : p, mx = v[r] < p ? p : v[r];
+          v[r] = lower == asc ? mn : mx;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int e = lane * R + r;
+    if (e < k) out[e] = v[r];
+  }
+}
+
+__global__ __launch_bounds__(SEL_THREADS) void k_select_small(SelectArgs a) {
+  const int64_t q = (int64_t)blockIdx.x * (SEL_THREADS / 64) + (threadIdx.x >> 6);
+  if (q >= a.nq || (a.active && !a.active[q])) return;
+  const uint64_t *C = a.cand + q * a.cap;
+  int64_t n = a.counts[q];
+  if (n > a.cap) n = a.cap;  // callers mark such queries inactive
+  uint64_t *out = a.best_out + q * (int64_t)a.k;
+  const int lane = threadIdx.x & 63;
+  for (int i = lane + (int)(n < a.k ? n : a.k); i < a.k; i += 64) out[i] = VSK_KEY_NONE;
+  if (n <= 64) wave_sort_write<1>(C, n, a.k, out);
+  else if (n <= 128) wave_sort_write<2>(C, n, a.k, out);
+  else if (n <= 256) wave_sort_write<4>(C, n, a.k, out);
+  else if (n <= 512) wave_sort_write<8>(C, n, a.k, out);
+  else wave_sort_write<16>(C, n, a.k, out);
+}
+
+// the margin gather (declared with MarginArgs).  Only the k-th smallest
+// screened distance matters here, not which key holds it, so the search is
+// a radix select over the 32-bit words themselves (ties counted): at most
+// four 8-bit digits below the highest bit where the smallest and largest
+// word differ, each a 256-bin histogram taken without branches (a word
+// outside the prefix counts into one of 32 spare bins).  REG words per
+// thread stay in registers when the list fits, loaded 16 bytes at a time;
+// longer lists are read from memory on every pass.
+constexpr uint32_t kWordNone = 0xFFFFFFFFu;  // no distance has this word
+
+template <int REG>
+__global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t *W = a.words + (a.wseg ? a.wseg[q] : q * a.wstride);
+  const int64_t n = a.cnt ? a.cnt[q] : a.wn;
+  const bool inreg = n <= (int64_t)REG * SEL_THREADS;  // uniform
+  const int chunks = (int)((n + 4 * SEL_THREADS - 1) / (4 * SEL_THREADS));
+  uint32_t w[REG];
+  if (inreg) {
+#pragma unroll
+    for (int j = 0; j < REG / 4; ++j) {
+      const int64_t c = 4 * (tid + (int64_t)j * SEL_THREADS);
+      // words past n (up to the segment's multiple of 4) are read, not used
+      uint4 v = make_uint4(kWordNone, kWordNone, kWordNone, kWordNone);
+      if (c < n) v = *reinterpret_cast<const uint4 *>(W + c);
+      w[4 * j] = c < n ? v.x : kWordNone;
+      w[4 * j + 1] = c + 1 < n ? v.y : kWordNone;
+      w[4 * j + 2] = c + 2 < n ? v.z : kWordNone;
+      w[4 * j + 3] = c + 3 < n ? v.w : kWordNone;
+    }
+  }
+  // f(word, index) over this thread's share
+  auto each = [&](auto &&f) {
+    if (inreg) {
+#pragma unroll
+      for (int j = 0; j < REG / 4; ++j) {
+        if (j >= chunks) break;  // uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f(w[4 * j + e], 4 * (tid + j * SEL_THREADS) + e);
+      }
+      return;
+    }
+    for (int64_t i = tid; i < n; i += SEL_THREADS) f(W[i], (uint32_t)i);
+  };
+  __shared__ uint32_t hist[256 + 32];
+  __shared__ uint32_t s_lo[SEL_THREADS / 64], s_hi[SEL_THREADS / 64];
+  __shared__ uint32_t s_bucket, s_before, s_total;
+  __shared__ int s_cnt;
+
+  // smallest and largest word
+  uint32_t lo = kWordNone, hi = 0;
+  each([&](uint32_t x, uint32_t) {
+    if (x != kWordNone) {
+      lo = x < lo ? x : lo;
+      hi = x > hi ? x : hi;
+    }
+  });
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, (uint32_t)__shfl_xor(lo, o));
+    hi = max(hi, (uint32_t)__shfl_xor(hi, o));
+  }
+  if (lane == 0) {
+    s_lo[wv] = lo;
+    s_hi[wv] = hi;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < SEL_THREADS / 64; ++i) {
+    lo = min(lo, s_lo[i]);
+    hi = max(hi, s_hi[i]);
+  }
+  // the k-th smallest word (kWordNone: fewer than k words)
+  uint32_t kth = kWordNone;
+  if (lo != kWordNone) {
+    uint32_t prefix = lo, mask = 0xFFFFFFFFu, need = (uint32_t)a.k;
+    int top = -1;
+    if (lo != hi) {
+      top = 31 - __builtin_clz(lo ^ hi);
+      mask = top == 31 ? 0u : ~((2u << top) - 1u);
+      prefix = lo & mask;
+    }
+    bool first = true, short_list = false;
+    while (top >= 0) {
+      const int width = top + 1 >= 8 ? 8 : top + 1;
+      const int shift = top + 1 - width;
+      const uint32_t dmask = (1u << width) - 1u;
+      for (int i = tid; i < 256 + 32; i += SEL_THREADS) hist[i] = 0;
+      __syncthreads();
+      const uint32_t spare = 256u + (uint32_t)(lane & 31);
+      each([&](uint32_t x, uint32_t) {
+        const bool in = x != kWordNone && (x & mask) == prefix;
+        atomicAdd(&hist[in ? (x >> shift) & dmask : spare], 1u);
+      });
+      __syncthreads();
+      if (tid < 64) {
+        const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
+                       h3 = hist[4 * lane + 3];
+        const uint32_t s4 = h0 + h1 + h2 + h3;
+        uint32_t incl = s4;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t v = __shfl_up(incl, o);
+          if (lane >= o) incl += v;
+        }
+        const uint32_t excl = incl - s4;
+        if (lane == 63) s_total = incl;
+        if (excl < need && need <= incl) {
+          const uint32_t hs[4] = {h0, h1, h2, h3};
+          uint32_t before = excl;
+          int j = 0;
+          while (before + hs[j] < need) {
+            before += hs[j];
+            ++j;
+          }
+          s_bucket = 4 * lane + j;
+          s_before = before;
+        }
+      }
+      __syncthreads();
+      if (first && s_total < need) {
+        short_list = true;  // fewer than k words
+        break;
+      }
+      first = false;
+      need -= s_before;
+      prefix |= s_bucket << shift;
+      mask |= dmask << shift;
+      __syncthreads();  // every thread has read the shared values
+      top = shift - 1;
+    }
+    if (!short_list) kth = prefix;
+  }
+  // every key when there are fewer than k, else those within the margin
+  uint32_t lim_word = kWordNone - 1u;
+  if (kth != kWordNone) {
+    const double ak = vsk_ord2f(kth);
+    const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
+    const double lim = a.metric == VSK_METRIC_L2 ? (ak + eps) * (1.0 + 0x1p-20) + eps
+                                                 : ak + 2.0 * eps;
+    lim_word = vsk_f2ord(f_down(lim));
+  }
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  uint64_t *out = a.out + q * (int64_t)a.cap;
+  each([&](uint32_t x, uint32_t i) {
+    if (x <= lim_word) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < a.cap) out[slot] = ((uint64_t)x << 32) | i;
+    }
+  });
+  __syncthreads();
+  if (tid == 0) {
+    const int c = s_cnt;
+    a.nout[q] = c;
+    a.ok[q] = c <= a.cap ? 1 : 0;
+    a.bad[q] = c <= a.cap ? 0 : 1;
+    if (c > a.cap && a.nbad) atomicAdd(a.nbad, 1ull);
+  }
+}
+
+void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a) {
+  if (a.nq <= 0) return;
+  KernelTimer t(ctx, "screen_margin");
+  k_screen_margin<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  check_launch("screen_margin");
+}
+
 void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   if (a.nq <= 0) return;
   if (a.k < 1 || a.k > VSK_MAX_K)
     fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
   KernelTimer t(ctx, name);
+  if (a.small) {
+    if (!a.counts || a.prev || a.seg_off || a.seg_n || a.cand32 || a.cap > 1024 || !a.sorted)
+      fail(VSK_ERR_INVALID_ARGUMENT, "short-list selection takes counted lists of at most 1024");
+    k_select_small<<<(unsigned)ceil_div(a.nq, SEL_THREADS / 64), SEL_THREADS, 0, ctx->stream>>>(a);
+    check_launch(name);
+    return;
+  }
   // keys per query: the previous list (k) and up to cap candidates
   const int64_t most = a.cap + (a.prev ? a.k : 0);
   if (a.cand32) {

@@ -68,6 +68,9 @@ struct SelectArgs {
   int32_t nseg = 0;
   int64_t seg_stride = 0;
   bool regs = false;  // small lists: the register-resident variant
+  // short counted lists (cap <= 1024, sorted output, no thresh): one wave
+  // per query sorts the whole list
+  bool small = false;
   // false: best_out gets the k smallest keys in no particular order and
   // thresh a key T with exactly those k keys <= T (a chunk's list that only
   // the next chunk's selection reads)
