@@ -114,12 +114,12 @@ __global__ void k_probe_bases(const int32_t *probes, int64_t nq, int32_t np,
 
 // pair (q, p) -> its slot in the list-grouped pair array
 __global__ void k_group_pairs(const int32_t *probes, int64_t npairs, int32_t np,
-                              int64_t *cursor, int32_t *pairs) {
+                              int32_t *cursor, int32_t *pairs) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
        i += (int64_t)gridDim.x * blockDim.x) {
     int32_t l = probes[i];
     if (l < 0) continue;
-    int64_t slot = atomicAdd((unsigned long long *)&cursor[l], 1ull);
+    const int32_t slot = atomicAdd(&cursor[l], 1);
     pairs[slot] = (int32_t)i;  // i = q * np + p
   }
 }
@@ -157,7 +157,8 @@ __device__ void block_scan_1024(const int64_t (&v)[NV], int64_t (&out)[NV],
   __syncthreads();
 }
 
-// seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024);
+// seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024, each
+// thread a run of consecutive counts, one block scan of the runs' sums);
 // with wseg, the same over the counts rounded up to multiples of 4
 __global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_t m,
                                                       int64_t *seg, int64_t *wseg) {
@@ -165,16 +166,22 @@ __global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_
   __shared__ int64_t carry[2];
   if (threadIdx.x < 2) carry[threadIdx.x] = 0;
   __syncthreads();
-  for (int64_t base = 0; base < m; base += 1024) {
-    const int64_t i = base + threadIdx.x;
-    const int64_t c = i < m ? cnt[i] : 0;
-    const int64_t v[2] = {c, (c + 3) & ~3ll};
-    int64_t o[2];
-    block_scan_1024<2>(v, o, wsum, carry);
-    if (i < m) {
-      seg[i] = o[0];
-      if (wseg) wseg[i] = o[1];
-    }
+  const int64_t run = (m + 1023) / 1024;
+  const int64_t i0 = threadIdx.x * run, i1 = i0 + run < m ? i0 + run : m;
+  int64_t v[2] = {0, 0};
+  for (int64_t i = i0; i < i1; ++i) {
+    const int64_t c = cnt[i];
+    v[0] += c;
+    v[1] += (c + 3) & ~3ll;
+  }
+  int64_t o[2];
+  block_scan_1024<2>(v, o, wsum, carry);
+  for (int64_t i = i0; i < i1; ++i) {
+    const int64_t c = cnt[i];
+    seg[i] = o[0];
+    if (wseg) wseg[i] = o[1];
+    o[0] += c;
+    o[1] += (c + 3) & ~3ll;
   }
   if (threadIdx.x == 0) {
     seg[m] = carry[0];
@@ -193,29 +200,36 @@ __global__ void k_list_pair_counts(const int32_t *probes, int64_t npairs, int32_
 
 // per list: its first pair slot (lstart, and cursor for the pair scatter)
 // and its first group (gstart; ceil(pairs / G) groups for a list holding
-// rows, none for an empty one); totals at [nlist].  One block of 1024.
+// rows, none for an empty one); totals at [nlist].  One block of 1024,
+// each thread a run of consecutive lists.
+__device__ inline int64_t list_groups(const int32_t *lcnt, const int64_t *list_off, int64_t l,
+                                      int32_t G) {
+  const int64_t c = lcnt[l];
+  return c > 0 && list_off[l + 1] > list_off[l] ? (c + G - 1) / G : 0;
+}
 __global__ __launch_bounds__(1024) void k_list_offsets(const int32_t *lcnt,
                                                        const int64_t *list_off, int32_t nlist,
                                                        int32_t G, int64_t *lstart,
-                                                       int64_t *cursor, int64_t *gstart) {
+                                                       int32_t *cursor, int64_t *gstart) {
   __shared__ int64_t wsum[16][2];
   __shared__ int64_t carry[2];
   if (threadIdx.x < 2) carry[threadIdx.x] = 0;
   __syncthreads();
-  for (int64_t base = 0; base < nlist; base += 1024) {
-    const int64_t l = base + threadIdx.x;
-    int64_t v[2] = {0, 0};
-    if (l < nlist) {
-      v[0] = lcnt[l];
-      v[1] = v[0] > 0 && list_off[l + 1] > list_off[l] ? (v[0] + G - 1) / G : 0;
-    }
-    int64_t o[2];
-    block_scan_1024<2>(v, o, wsum, carry);
-    if (l < nlist) {
-      lstart[l] = o[0];
-      cursor[l] = o[0];
-      gstart[l] = o[1];
-    }
+  const int64_t run = (nlist + 1023) / 1024;
+  const int64_t l0 = threadIdx.x * run, l1 = l0 + run < nlist ? l0 + run : nlist;
+  int64_t v[2] = {0, 0};
+  for (int64_t l = l0; l < l1; ++l) {
+    v[0] += lcnt[l];
+    v[1] += list_groups(lcnt, list_off, l, G);
+  }
+  int64_t o[2];
+  block_scan_1024<2>(v, o, wsum, carry);
+  for (int64_t l = l0; l < l1; ++l) {
+    lstart[l] = o[0];
+    cursor[l] = (int32_t)o[0];
+    gstart[l] = o[1];
+    o[0] += lcnt[l];
+    o[1] += list_groups(lcnt, list_off, l, G);
   }
   if (threadIdx.x == 0) {
     lstart[nlist] = carry[0];
@@ -979,8 +993,9 @@ vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
 
 // the pair and group arrays of a batch (sized for the largest batch)
 struct ListGroups {
-  int32_t *lcnt;                    // pairs per list
-  int64_t *lstart, *cursor, *gstart;  // nlist + 1 each
+  int32_t *lcnt;            // pairs per list
+  int64_t *lstart, *gstart;  // nlist + 1 each
+  int32_t *cursor;          // nlist + 1
   int32_t *pairs;
   int4 *groups;
 };
@@ -991,17 +1006,29 @@ static void make_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes,
                         int64_t npairs, int32_t np, int G, const ListGroups &lg) {
   const int32_t nlist = ivf->nlist;
   fill_i32(ctx, lg.lcnt, nlist, 0);
-  k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt);
-  check_launch("ivf_list_pair_counts");
-  k_list_offsets<<<1, 1024, 0, ctx->stream>>>(lg.lcnt, ivf->list_off.as<int64_t>(), nlist, G,
-                                               lg.lstart, lg.cursor, lg.gstart);
-  check_launch("ivf_list_offsets");
-  k_make_groups<<<grid1(nlist), 256, 0, ctx->stream>>>(lg.lcnt, lg.lstart, lg.gstart, nlist,
-                                                       G, lg.groups);
-  check_launch("ivf_make_groups");
-  k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, np, lg.cursor,
-                                                        lg.pairs);
-  check_launch("ivf_group_pairs");
+  {
+    KernelTimer t(ctx, "ivf_pair_counts");
+    k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt);
+    check_launch("ivf_list_pair_counts");
+  }
+  {
+    KernelTimer t(ctx, "ivf_list_offsets");
+    k_list_offsets<<<1, 1024, 0, ctx->stream>>>(lg.lcnt, ivf->list_off.as<int64_t>(), nlist, G,
+                                                 lg.lstart, lg.cursor, lg.gstart);
+    check_launch("ivf_list_offsets");
+  }
+  {
+    KernelTimer t(ctx, "ivf_make_groups");
+    k_make_groups<<<grid1(nlist), 256, 0, ctx->stream>>>(lg.lcnt, lg.lstart, lg.gstart, nlist,
+                                                         G, lg.groups);
+    check_launch("ivf_make_groups");
+  }
+  {
+    KernelTimer t(ctx, "ivf_group_pairs");
+    k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, np, lg.cursor,
+                                                          lg.pairs);
+    check_launch("ivf_group_pairs");
+  }
 }
 
 // one query batch of the screened list scan: the screened distance of
@@ -1367,8 +1394,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   // on the stream without a read-back: segment offsets, pairs and groups
   // are made on the device, and grids take their upper bounds.
   const int64_t ubound = probe_bound(ivf, np);
+  // (pair ids q * np + p are 32-bit)
   const int64_t qb = std::max<int64_t>(
-      1, std::min<int64_t>(nq, (1ll << 27) / std::max<int64_t>(ubound, 1)));
+      1, std::min<int64_t>({nq, (1ll << 27) / std::max<int64_t>(ubound, 1),
+                            (int64_t)INT32_MAX / np}));
   // the screen's groups are 64 queries
   const int G = screen ? 64 : QG;
   if (screen) list_screen_plane(ctx, ivf);
@@ -1388,9 +1417,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   int64_t *wseg = screen ? dseg + (nbmax + 1) : nullptr;
   int64_t *loffs = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
-  int64_t *lstart = loffs, *cursor = loffs + (nlist + 1), *gstart = loffs + 2 * (nlist + 1);
+  int64_t *lstart = loffs, *gstart = loffs + 2 * (nlist + 1);
+  int32_t *cursor = reinterpret_cast<int32_t *>(loffs + (nlist + 1));
   int32_t *lcnt = static_cast<int32_t *>(ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * nlist));
-  const ListGroups lg{lcnt, lstart, cursor, gstart, nullptr, nullptr};
+  const ListGroups lg{lcnt, lstart, gstart, cursor, nullptr, nullptr};
   int32_t *dpairs = static_cast<int32_t *>(
       ctx->scratch_ptr("ivf.pairs", sizeof(int32_t) * (npmax + 1)));
   int4 *dgroups = static_cast<int4 *>(ctx->scratch_ptr("ivf.groups", sizeof(int4) * (gmax + 1)));
@@ -1410,11 +1440,11 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     const int64_t ng = std::min<int64_t>(nlist, npairs) + ceil_div(npairs, G);
     // 3. segment offsets; pairs grouped by list, groups of up to G pairs
     {
-      KernelTimer t(ctx, "ivf_group_pairs");
+      KernelTimer t(ctx, "ivf_seg_offsets");
       k_seg_offsets<<<1, 1024, 0, ctx->stream>>>(cnt + b0, nb, dseg, wseg);
       check_launch("ivf_seg_offsets");
-      if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     }
+    if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     if (screen) {
       list_screen_batch(ctx, ivf, qp, dq, b0, nb, np, k, metric, probes, pos_base, cnt, dseg,
                         wseg, lgp, cand, best);

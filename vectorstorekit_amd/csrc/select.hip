@@ -414,7 +414,11 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
     lo = min(lo, s_lo[i]);
     hi = max(hi, s_hi[i]);
   }
-  // the k-th smallest word (kWordNone: fewer than k words)
+  // the k-th smallest word (kWordNone: fewer than k words), or a word a
+  // little above it: the search stops once the words left in the k-th's
+  // bucket span less than 1/64 of the margin (the limit then only grows by
+  // that much, and every key it adds is rescored like the others)
+  const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
   uint32_t kth = kWordNone;
   if (lo != kWordNone) {
     uint32_t prefix = lo, mask = 0xFFFFFFFFu, need = (uint32_t)a.k;
@@ -472,6 +476,11 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
       mask |= dmask << shift;
       __syncthreads();  // every thread has read the shared values
       top = shift - 1;
+      if (top >= 0 && (double)vsk_ord2f(prefix | ~mask) - (double)vsk_ord2f(prefix) <
+                          0x1p-6 * eps) {
+        prefix |= ~mask;  // the bucket's largest word
+        break;
+      }
     }
     if (!short_list) kth = prefix;
   }
@@ -479,7 +488,6 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
   uint32_t lim_word = kWordNone - 1u;
   if (kth != kWordNone) {
     const double ak = vsk_ord2f(kth);
-    const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
     const double lim = a.metric == VSK_METRIC_L2 ? (ak + eps) * (1.0 + 0x1p-20) + eps
                                                  : ak + 2.0 * eps;
     lim_word = vsk_f2ord(f_down(lim));
