@@ -136,6 +136,21 @@ struct MarginArgs {
 };
 void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a);
 
+// Exact top k per query of 32-bit words keyed (word, index), sorted
+// ascending into best_out[q * k ...] (NONE past the words): query q's words
+// are words[wseg[q] + i], i < cnt[q] (wseg a multiple of 4); only queries
+// with active[q] (all when null).  The keys are those of a scan writing
+// (word << 32) | position.
+struct WordSelectArgs {
+  int64_t nq = 0;
+  int32_t k = 0;
+  const uint32_t *words = nullptr;
+  const int64_t *wseg = nullptr, *cnt = nullptr;
+  uint64_t *best_out = nullptr;
+  const uint8_t *active = nullptr;
+};
+void launch_select_words(vsk_ctx *ctx, const WordSelectArgs &a, const char *name);
+
 // bf16 hi/lo operand planes of the bf16x3 kernel
 struct SplitPtrs {
   const uint16_t *xh, *xl;  // row planes, stride ldxb

@@ -259,8 +259,10 @@ struct ListScanArgs {
   const int4 *groups;    // (list, pair_begin, pair_count, 0)
   const int64_t *ngroups;   // groups made (the grid is an upper bound)
   const int64_t *pos_base;  // [nq][np]
-  const int64_t *seg_off;   // [nq+1] candidate segment offsets
-  uint64_t *cand;
+  // each candidate's distance as its order-preserving 32-bit word (the
+  // high half of its (distance, position) key) at words[wseg[q] + position]
+  const int64_t *wseg;      // [nq+1] word segment offsets (multiples of 4)
+  uint32_t *words;
   int32_t squared;          // 1: key on sum (q-x)^2, 0: on its sqrt
   // coded scans
   const uint8_t *codes;     // list-grouped codes, cstride bytes per row
@@ -283,7 +285,7 @@ struct ListScanArgs {
   _Pragma("unroll") for (int j = 0; j < QG; ++j) {                 \
     const int32_t pid = a.pairs[g.y + (j < npair ? j : 0)];        \
     qidx[j] = pid / a.np;                                          \
-    obase[j] = a.seg_off[qidx[j]] + a.pos_base[pid];               \
+    obase[j] = a.wseg[qidx[j]] + a.pos_base[pid];                  \
     tbase[j] = a.pos_base[pid];                                    \
   }
 
@@ -319,7 +321,7 @@ __global__ __launch_bounds__(256) void k_list_scan_sq8(ListScanArgs a) {
     const int64_t i = v - v0;
 #pragma unroll
     for (int j = 0; j < QG; ++j)
-      if (j < npair) a.cand[obase[j] + i] = vsk_key_i32(-acc[j], (uint32_t)(tbase[j] + i));
+      if (j < npair) a.words[obase[j] + i] = (uint32_t)(-acc[j]) ^ 0x80000000u;
   }
 }
 
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
     int32_t pid = a.pairs[g.y + (j < npair ? j : 0)];
     int32_t q = pid / a.np;
     qidx[j] = q;
-    obase[j] = a.seg_off[q] + a.pos_base[pid];
+    obase[j] = a.wseg[q] + a.pos_base[pid];
     tbase[j] = a.pos_base[pid];
   }
   for (int i = threadIdx.x; i < QG * a.ld; i += blockDim.x) {
@@ -374,8 +376,7 @@ __global__ __launch_bounds__(256) void k_list_scan(ListScanArgs a) {
 #pragma unroll
     for (int j = 0; j < QG; ++j)
       if (j < npair)
-        a.cand[obase[j] + i] = vsk_key(a.squared ? acc[j] : sqrtf(acc[j]),
-                                       (uint32_t)(tbase[j] + i));
+        a.words[obase[j] + i] = vsk_f2ord(a.squared ? acc[j] : sqrtf(acc[j]));
   }
   (void)qidx;
 }
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(256) void k_list_scan_pq_q(ListScanArgs a) {
   const int tsz = a.M * a.ksub;
   for (int i = threadIdx.x; i < tsz; i += blockDim.x) tl[i] = a.lut[q * tsz + i];
   __syncthreads();
-  const int64_t seg = a.seg_off[q];
+  const int64_t seg = a.wseg[q];
   for (int p = 0; p < a.np; ++p) {
     const int32_t l = a.probes[q * a.np + p];
     if (l < 0) continue;
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(256) void k_list_scan_pq_q(ListScanArgs a) {
         for (int t = 0; t < mm; ++t)
           acc = acc + tl[(m0 + t) * a.ksub + (int)((w >> (8 * t)) & 0xFFu)];
       }
-      a.cand[seg + tb + (v - v0)] = vsk_key(acc, (uint32_t)(tb + (v - v0)));
+      a.words[seg + tb + (v - v0)] = vsk_f2ord(acc);
     }
   }
 }
@@ -462,41 +463,44 @@ __global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// one workgroup per group of up to 64 queries probing one list.  A is the
-// group's query fragments (4 tiles of 16 queries x KS k-steps of 32 dims,
-// held in registers for the whole list), B a 16-row block of the list's
-// plane, so lane l of a product holds query 4 (l / 16) + r of the tile
-// against row l % 16 of the block: 16 lanes write 16 consecutive values of
-// one query.  Wave w takes the list's blocks w, w + 4, ...  Each screened
+// one workgroup per group of up to 128 queries probing one list, two
+// halves of 4 waves with 64 queries each (the second half reads the rows
+// the first just read, from cache).  A is the half's query fragments (4
+// tiles of 16 queries x KS k-steps of 32 dims, held in registers for the
+// whole list), B a 16-row block of the list's plane, so lane l of a product
+// holds query 4 (l / 16) + r of the tile against row l % 16 of the block:
+// 16 lanes write 16 consecutive values of one query.  Wave w of a half
+// takes the list's blocks w, w + 4, ...  Each screened
 // distance goes, as its order-preserving 32-bit word, to its candidate
 // position in the query's word segment, out[wseg[q] + position].
 //
 // DENSE: the same over one block of rows for every query -- the probe's
 // screen over the centroids: workgroup b takes rows 256 (b % nchunks) ..
-// (at most 256, below nrows) for queries 64 (b / nchunks) .. (below nq),
+// (at most 256, below nrows) for queries 128 (b / nchunks) .. (below nq),
 // writing out[q * wstride + row].
 struct DenseScreen {
   int64_t nq, nrows, wstride;
   int32_t nchunks;
 };
+constexpr int kScreenQ = 128;  // queries per screen workgroup: 2 halves of 4 waves
 template <int KS, bool DENSE>
-__global__ __launch_bounds__(256) void k_list_screen(
+__global__ __launch_bounds__(512) void k_list_screen(
     const uint16_t *xplane, const float *xsq, int32_t ldb, const int64_t *list_off,
     const uint16_t *qplane, const float *qsq, const int32_t *pairs, const int4 *groups,
     const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *wseg,
     uint32_t *out, DenseScreen ds) {
   if (!DENSE && blockIdx.x >= *ngroups) return;
-  __shared__ int64_t s_out[64];  // value address of the list's first row (-1: no query)
-  __shared__ float s_qa[64];     // |q|^2
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ int64_t s_out[kScreenQ];  // value address of the list's first row (-1: none)
+  __shared__ float s_qa[kScreenQ];     // |q|^2
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3, half = threadIdx.x >> 8;
   int64_t v0, v1, q0 = 0;
   int npair;
   int4 g{};
   if constexpr (DENSE) {
     v0 = 256 * (int64_t)(blockIdx.x % ds.nchunks);
     v1 = v0 + 256 < ds.nrows ? v0 + 256 : ds.nrows;
-    q0 = 64 * (int64_t)(blockIdx.x / ds.nchunks);
-    npair = ds.nq - q0 < 64 ? (int)(ds.nq - q0) : 64;
+    q0 = kScreenQ * (int64_t)(blockIdx.x / ds.nchunks);
+    npair = ds.nq - q0 < kScreenQ ? (int)(ds.nq - q0) : kScreenQ;
   } else {
     g = groups[blockIdx.x];
     v0 = list_off[g.x];
@@ -508,7 +512,7 @@ __global__ __launch_bounds__(256) void k_list_screen(
     if constexpr (DENSE) return q0 + (j < npair ? j : 0);
     return pairs[g.y + (j < npair ? j : 0)] / np;
   };
-  if (threadIdx.x < 64) {
+  if (threadIdx.x < kScreenQ) {
     const int j = threadIdx.x;
     const int64_t q = query(j);
     if constexpr (DENSE) {
@@ -520,17 +524,20 @@ __global__ __launch_bounds__(256) void k_list_screen(
     s_qa[j] = qsq[q];
   }
   const int kc = 8 * (lane >> 4);  // this lane's 8 dims of a k-step
-  const int ntile = (npair + 15) >> 4;
+  // this half's query tiles: slots 64 half + 16 t
+  const int hbase = 64 * half;
+  const int ntile = npair - hbase <= 0 ? 0 : (npair - hbase + 15) >> 4;
   bf8v qf[4][KS];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const int j = 16 * t + (lane & 15);
+    const int j = hbase + 16 * t + (lane & 15);
     const int64_t q = query(j);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + q * ldb + 32 * ks + kc);
   }
   __syncthreads();
+  if (ntile == 0) return;  // (after the block's only barrier)
   for (int64_t b = v0 + 16 * w; b < v1; b += 64) {
     const int64_t row = b + (lane & 15);
     const bool live = row < v1;
@@ -550,7 +557,7 @@ __global__ __launch_bounds__(256) void k_list_screen(
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t][ks], xf[ks], acc, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int j = 16 * t + 4 * (lane >> 4) + r;
+        const int j = hbase + 16 * t + 4 * (lane >> 4) + r;
         const int64_t o = s_out[j];
         if (live && o >= 0) out[o + i] = vsk_f2ord(fmaxf(s_qa[j] + xa - 2.0f * acc[r], 0.0f));
       }
@@ -1054,9 +1061,10 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
   {
     KernelTimer t(ctx, "ivf_list_screen");
     t.device_work(dseg + nb);
-    const unsigned gmax = (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, 64));
+    const unsigned gmax =
+        (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, kScreenQ));
 #define VSK_LS(KS)                                                                          \
-  k_list_screen<KS, false><<<gmax, 256, 0, ctx->stream>>>(                                 \
+  k_list_screen<KS, false><<<gmax, 512, 0, ctx->stream>>>(                                 \
       ivf->xplane.as<uint16_t>(), ivf->xsq.as<float>(), ldb, ivf->list_off.as<int64_t>(),   \
       qp.qh + b0 * qp.ldb, qp.qsq + b0, lg.pairs, lg.groups, lg.gstart + nlist, np, bpos,   \
       wseg, words, DenseScreen{})
@@ -1194,10 +1202,10 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     {
       KernelTimer t(ctx, "ivf_probe_screen", (double)nb * nlist);
-      const unsigned grid = (unsigned)(nchunks * ceil_div(nb, 64));
+      const unsigned grid = (unsigned)(nchunks * ceil_div(nb, kScreenQ));
       const DenseScreen ds{nb, nlist, wstride, nchunks};
 #define VSK_PS(KS)                                                                            \
-  k_list_screen<KS, true><<<grid, 256, 0, ctx->stream>>>(                                    \
+  k_list_screen<KS, true><<<grid, 512, 0, ctx->stream>>>(                                    \
       cdb->split.as<uint16_t>(), cdb->sqnorm.as<float>(), ldb, nullptr, qp.qh + b0 * qp.ldb, \
       qp.qsq + b0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, words, ds)
       switch (ldb / 32) {
@@ -1398,8 +1406,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   const int64_t qb = std::max<int64_t>(
       1, std::min<int64_t>({nq, (1ll << 27) / std::max<int64_t>(ubound, 1),
                             (int64_t)INT32_MAX / np}));
-  // the screen's groups are 64 queries
-  const int G = screen ? 64 : QG;
+  // the screen's groups are up to kScreenQ queries
+  const int G = screen ? kScreenQ : QG;
   if (screen) list_screen_plane(ctx, ivf);
   {
     KernelTimer t(ctx, "ivf_probe_bases");
@@ -1414,7 +1422,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       ctx->scratch_ptr("ivf.best", sizeof(uint64_t) * nq * k));
   int64_t *dseg = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.seg", sizeof(int64_t) * 2 * (nbmax + 1)));
-  int64_t *wseg = screen ? dseg + (nbmax + 1) : nullptr;
+  int64_t *wseg = dseg + (nbmax + 1);
   int64_t *loffs = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
   int64_t *lstart = loffs, *gstart = loffs + 2 * (nlist + 1);
@@ -1462,8 +1470,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     la.groups = dgroups;
     la.ngroups = ngroups;
     la.pos_base = pos_base + b0 * np;
-    la.seg_off = dseg;
-    la.cand = cand;
+    la.wseg = wseg;
+    la.words = reinterpret_cast<uint32_t *>(cand);
     la.squared = metric == VSK_METRIC_L2SQ ? 1 : 0;
     la.codes = ivf->codes.as<uint8_t>();
     la.cstride = ivf->cstride;
@@ -1493,13 +1501,14 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       check_launch(names[kind]);
     }
     // 4. selection per query segment
-    SelectArgs sa;
+    WordSelectArgs sa;
     sa.nq = nb;
     sa.k = k;
-    sa.cand = cand;
-    sa.seg_off = dseg;
+    sa.words = la.words;
+    sa.wseg = wseg;
+    sa.cnt = cnt + b0;
     sa.best_out = best + b0 * k;
-    launch_select(ctx, sa, "ivf_select");
+    launch_select_words(ctx, sa, "ivf_select");
   }
   {
     KernelTimer t(ctx, "ivf_decode");

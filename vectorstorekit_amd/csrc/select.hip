@@ -29,6 +29,31 @@ __device__ inline uint64_t sel_elem(const uint64_t *P, int64_t np, const uint64_
   return i < np ? P[i] : C[i - np];
 }
 
+// ascending bitonic sort of sel[0..m) in LDS by the whole block (sel holds
+// the next power of two; the padding is NONE); ends with a barrier
+__device__ void block_sort(uint64_t *sel, int m) {
+  const int tid = threadIdx.x;
+  int P2 = 1;
+  while (P2 < m) P2 <<= 1;
+  for (int i = m + tid; i < P2; i += SEL_THREADS) sel[i] = VSK_KEY_NONE;
+  __syncthreads();
+  for (int size = 2; size <= P2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < (P2 >> 1); i += SEL_THREADS) {
+        int lo = 2 * i - (i & (stride - 1));
+        int hi = lo + stride;
+        bool up = (lo & size) == 0;
+        uint64_t x = sel[lo], y = sel[hi];
+        if ((x > y) == up) {
+          sel[lo] = y;
+          sel[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
 // block-wide shared state of a threshold search
 struct SelShared {
   uint32_t hist[256 + 32];
@@ -250,25 +275,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
     if (tid == 0 && a.thresh) a.thresh[q] = m < k ? VSK_KEY_NONE : (take_all ? hi : T);
     return;
   }
-  int P2 = 1;
-  while (P2 < m) P2 <<= 1;
-  for (int i = m + tid; i < P2; i += SEL_THREADS) sel[i] = VSK_KEY_NONE;
-  __syncthreads();
-  for (int size = 2; size <= P2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < (P2 >> 1); i += SEL_THREADS) {
-        int lo = 2 * i - (i & (stride - 1));
-        int hi = lo + stride;
-        bool up = (lo & size) == 0;
-        uint64_t x = sel[lo], y = sel[hi];
-        if ((x > y) == up) {
-          sel[lo] = y;
-          sel[hi] = x;
-        }
-      }
-      __syncthreads();
-    }
-  }
+  block_sort(sel, m);
   uint64_t *out = a.best_out + q * (int64_t)k;
   for (int i = tid; i < k; i += SEL_THREADS)
     out[i] = i < m ? sel[i] : VSK_KEY_NONE;
@@ -351,47 +358,20 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select_small(SelectArgs a) {
 // longer lists are read from memory on every pass.
 constexpr uint32_t kWordNone = 0xFFFFFFFFu;  // no distance has this word
 
-template <int REG>
-__global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
-  const int64_t q = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t *W = a.words + (a.wseg ? a.wseg[q] : q * a.wstride);
-  const int64_t n = a.cnt ? a.cnt[q] : a.wn;
-  const bool inreg = n <= (int64_t)REG * SEL_THREADS;  // uniform
-  const int chunks = (int)((n + 4 * SEL_THREADS - 1) / (4 * SEL_THREADS));
-  uint32_t w[REG];
-  if (inreg) {
-#pragma unroll
-    for (int j = 0; j < REG / 4; ++j) {
-      const int64_t c = 4 * (tid + (int64_t)j * SEL_THREADS);
-      // words past n (up to the segment's multiple of 4) are read, not used
-      uint4 v = make_uint4(kWordNone, kWordNone, kWordNone, kWordNone);
-      if (c < n) v = *reinterpret_cast<const uint4 *>(W + c);
-      w[4 * j] = c < n ? v.x : kWordNone;
-      w[4 * j + 1] = c + 1 < n ? v.y : kWordNone;
-      w[4 * j + 2] = c + 2 < n ? v.z : kWordNone;
-      w[4 * j + 3] = c + 3 < n ? v.w : kWordNone;
-    }
-  }
-  // f(word, index) over this thread's share
-  auto each = [&](auto &&f) {
-    if (inreg) {
-#pragma unroll
-      for (int j = 0; j < REG / 4; ++j) {
-        if (j >= chunks) break;  // uniform
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f(w[4 * j + e], 4 * (tid + j * SEL_THREADS) + e);
-      }
-      return;
-    }
-    for (int64_t i = tid; i < n; i += SEL_THREADS) f(W[i], (uint32_t)i);
-  };
-  __shared__ uint32_t hist[256 + 32];
-  __shared__ uint32_t s_lo[SEL_THREADS / 64], s_hi[SEL_THREADS / 64];
-  __shared__ uint32_t s_bucket, s_before, s_total;
-  __shared__ int s_cnt;
+struct WordShared {
+  uint32_t hist[256 + 32];
+  uint32_t lo[SEL_THREADS / 64], hi[SEL_THREADS / 64];
+  uint32_t bucket, before, total;
+};
 
-  // smallest and largest word
+// The k-th smallest of the words each(f) hands to f(word, index) (ties
+// counted; kWordNone words skipped), kWordNone when there are fewer than k.
+// stop_span > 0: the search may stop early once the words left in the
+// k-th's bucket span less than stop_span as floats, returning the bucket's
+// largest word (at or above the k-th).  Called by every thread of the block.
+template <class Each>
+__device__ uint32_t word_kth(Each &&each, uint32_t k, WordShared &sh, double stop_span) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   uint32_t lo = kWordNone, hi = 0;
   each([&](uint32_t x, uint32_t) {
     if (x != kWordNone) {
@@ -405,85 +385,143 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
     hi = max(hi, (uint32_t)__shfl_xor(hi, o));
   }
   if (lane == 0) {
-    s_lo[wv] = lo;
-    s_hi[wv] = hi;
+    sh.lo[wv] = lo;
+    sh.hi[wv] = hi;
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < SEL_THREADS / 64; ++i) {
-    lo = min(lo, s_lo[i]);
-    hi = max(hi, s_hi[i]);
+    lo = min(lo, sh.lo[i]);
+    hi = max(hi, sh.hi[i]);
   }
+  __syncthreads();  // sh.lo / sh.hi read by every thread
+  if (lo == kWordNone) return kWordNone;
+  uint32_t prefix = lo, mask = 0xFFFFFFFFu, need = k;
+  int top = -1;
+  if (lo != hi) {
+    top = 31 - __builtin_clz(lo ^ hi);
+    mask = top == 31 ? 0u : ~((2u << top) - 1u);
+    prefix = lo & mask;
+  }
+  bool first = true;
+  while (top >= 0) {
+    const int width = top + 1 >= 8 ? 8 : top + 1;
+    const int shift = top + 1 - width;
+    const uint32_t dmask = (1u << width) - 1u;
+    for (int i = tid; i < 256 + 32; i += SEL_THREADS) sh.hist[i] = 0;
+    __syncthreads();
+    // without branches: a word outside the prefix counts into one of 32
+    // spare bins
+    const uint32_t spare = 256u + (uint32_t)(lane & 31);
+    each([&](uint32_t x, uint32_t) {
+      const bool in = x != kWordNone && (x & mask) == prefix;
+      atomicAdd(&sh.hist[in ? (x >> shift) & dmask : spare], 1u);
+    });
+    __syncthreads();
+    if (tid < 64) {
+      const uint32_t h0 = sh.hist[4 * lane], h1 = sh.hist[4 * lane + 1],
+                     h2 = sh.hist[4 * lane + 2], h3 = sh.hist[4 * lane + 3];
+      const uint32_t s4 = h0 + h1 + h2 + h3;
+      uint32_t incl = s4;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      const uint32_t excl = incl - s4;
+      if (lane == 63) sh.total = incl;
+      if (excl < need && need <= incl) {
+        const uint32_t hs[4] = {h0, h1, h2, h3};
+        uint32_t before = excl;
+        int j = 0;
+        while (before + hs[j] < need) {
+          before += hs[j];
+          ++j;
+        }
+        sh.bucket = 4 * lane + j;
+        sh.before = before;
+      }
+    }
+    __syncthreads();
+    if (first && sh.total < need) {
+      __syncthreads();
+      return kWordNone;  // fewer than k words
+    }
+    first = false;
+    need -= sh.before;
+    prefix |= sh.bucket << shift;
+    mask |= dmask << shift;
+    __syncthreads();  // every thread has read the shared values
+    top = shift - 1;
+    if (stop_span > 0 && top >= 0 &&
+        (double)vsk_ord2f(prefix | ~mask) - (double)vsk_ord2f(prefix) < stop_span) {
+      prefix |= ~mask;  // the bucket's largest word
+      break;
+    }
+  }
+  return prefix;
+}
+
+// One query's words, word i at W[i] for i < n (W 16-byte aligned, words
+// readable up to the next multiple of 4): REG a thread in registers when
+// they fit, loaded 16 bytes at a time, else read from memory on each pass.
+template <int REG>
+struct WordList {
+  const uint32_t *W;
+  int64_t n;
+  bool inreg;
+  int chunks;
+  uint32_t w[REG];
+  __device__ void load(const uint32_t *W_, int64_t n_) {
+    W = W_;
+    n = n_;
+    inreg = n <= (int64_t)REG * SEL_THREADS;  // uniform
+    chunks = (int)((n + 4 * SEL_THREADS - 1) / (4 * SEL_THREADS));
+    if (!inreg) return;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < REG / 4; ++j) {
+      const int64_t c = 4 * (tid + (int64_t)j * SEL_THREADS);
+      uint4 v = make_uint4(kWordNone, kWordNone, kWordNone, kWordNone);
+      if (c < n) v = *reinterpret_cast<const uint4 *>(W + c);
+      w[4 * j] = c < n ? v.x : kWordNone;
+      w[4 * j + 1] = c + 1 < n ? v.y : kWordNone;
+      w[4 * j + 2] = c + 2 < n ? v.z : kWordNone;
+      w[4 * j + 3] = c + 3 < n ? v.w : kWordNone;
+    }
+  }
+  // f(word, index) over this thread's share (kWordNone for padding)
+  template <class F>
+  __device__ void each(F &&f) const {
+    const int tid = threadIdx.x;
+    if (inreg) {
+#pragma unroll
+      for (int j = 0; j < REG / 4; ++j) {
+        if (j >= chunks) break;  // uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f(w[4 * j + e], 4 * (tid + j * SEL_THREADS) + e);
+      }
+      return;
+    }
+    for (int64_t i = tid; i < n; i += SEL_THREADS) f(W[i], (uint32_t)i);
+  }
+};
+
+template <int REG>
+__global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x;
+  WordList<REG> L;
+  L.load(a.words + (a.wseg ? a.wseg[q] : q * a.wstride), a.cnt ? a.cnt[q] : a.wn);
+  auto each = [&](auto &&f) { L.each(f); };
+  __shared__ WordShared sh;
+  __shared__ int s_cnt;
   // the k-th smallest word (kWordNone: fewer than k words), or a word a
   // little above it: the search stops once the words left in the k-th's
   // bucket span less than 1/64 of the margin (the limit then only grows by
   // that much, and every key it adds is rescored like the others)
   const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
-  uint32_t kth = kWordNone;
-  if (lo != kWordNone) {
-    uint32_t prefix = lo, mask = 0xFFFFFFFFu, need = (uint32_t)a.k;
-    int top = -1;
-    if (lo != hi) {
-      top = 31 - __builtin_clz(lo ^ hi);
-      mask = top == 31 ? 0u : ~((2u << top) - 1u);
-      prefix = lo & mask;
-    }
-    bool first = true, short_list = false;
-    while (top >= 0) {
-      const int width = top + 1 >= 8 ? 8 : top + 1;
-      const int shift = top + 1 - width;
-      const uint32_t dmask = (1u << width) - 1u;
-      for (int i = tid; i < 256 + 32; i += SEL_THREADS) hist[i] = 0;
-      __syncthreads();
-      const uint32_t spare = 256u + (uint32_t)(lane & 31);
-      each([&](uint32_t x, uint32_t) {
-        const bool in = x != kWordNone && (x & mask) == prefix;
-        atomicAdd(&hist[in ? (x >> shift) & dmask : spare], 1u);
-      });
-      __syncthreads();
-      if (tid < 64) {
-        const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
-                       h3 = hist[4 * lane + 3];
-        const uint32_t s4 = h0 + h1 + h2 + h3;
-        uint32_t incl = s4;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t v = __shfl_up(incl, o);
-          if (lane >= o) incl += v;
-        }
-        const uint32_t excl = incl - s4;
-        if (lane == 63) s_total = incl;
-        if (excl < need && need <= incl) {
-          const uint32_t hs[4] = {h0, h1, h2, h3};
-          uint32_t before = excl;
-          int j = 0;
-          while (before + hs[j] < need) {
-            before += hs[j];
-            ++j;
-          }
-          s_bucket = 4 * lane + j;
-          s_before = before;
-        }
-      }
-      __syncthreads();
-      if (first && s_total < need) {
-        short_list = true;  // fewer than k words
-        break;
-      }
-      first = false;
-      need -= s_before;
-      prefix |= s_bucket << shift;
-      mask |= dmask << shift;
-      __syncthreads();  // every thread has read the shared values
-      top = shift - 1;
-      if (top >= 0 && (double)vsk_ord2f(prefix | ~mask) - (double)vsk_ord2f(prefix) <
-                          0x1p-6 * eps) {
-        prefix |= ~mask;  // the bucket's largest word
-        break;
-      }
-    }
-    if (!short_list) kth = prefix;
-  }
+  const uint32_t kth = word_kth(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   // every key when there are fewer than k, else those within the margin
   uint32_t lim_word = kWordNone - 1u;
   if (kth != kWordNone) {
@@ -516,6 +554,79 @@ void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a) {
   KernelTimer t(ctx, "screen_margin");
   k_screen_margin<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   check_launch("screen_margin");
+}
+
+// Exact top k by (word, index), sorted (declared with WordSelectArgs):
+// word_kth finds the k-th smallest word V; every word below V is kept and,
+// of the words equal to V, those with the smallest indices -- a second
+// search over their indices when more are equal than the k still need.
+template <int REG>
+__global__ __launch_bounds__(SEL_THREADS) void k_select_words(WordSelectArgs a) {
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (a.active && !a.active[q]) return;
+  WordList<REG> L;
+  L.load(a.words + a.wseg[q], a.cnt[q]);
+  auto each = [&](auto &&f) { L.each(f); };
+  __shared__ WordShared sh;
+  __shared__ uint64_t sel[VSK_MAX_K];
+  __shared__ uint32_t s_less, s_eq;
+  __shared__ int s_cnt;
+  const uint32_t k = (uint32_t)a.k;
+  const uint32_t V = word_kth(each, k, sh, 0.0);
+  uint32_t I = 0xFFFFFFFFu;  // the largest index kept among words equal to V
+  if (V != kWordNone) {
+    if (tid == 0) {
+      s_less = 0;
+      s_eq = 0;
+    }
+    __syncthreads();
+    uint32_t less = 0, eq = 0;
+    each([&](uint32_t x, uint32_t) {
+      less += x < V ? 1u : 0u;
+      eq += x == V ? 1u : 0u;
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      less += __shfl_xor(less, o);
+      eq += __shfl_xor(eq, o);
+    }
+    if (lane == 0) {
+      atomicAdd(&s_less, less);
+      atomicAdd(&s_eq, eq);
+    }
+    __syncthreads();
+    const uint32_t need_eq = k - s_less;
+    if (s_eq > need_eq) {
+      I = word_kth([&](auto &&f) {
+        L.each([&](uint32_t x, uint32_t i) { f(x == V ? i : kWordNone, i); });
+      }, need_eq, sh, 0.0);
+    }
+  }
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  each([&](uint32_t x, uint32_t i) {
+    const bool keep = x != kWordNone && (V == kWordNone || x < V || (x == V && i <= I));
+    if (keep) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < VSK_MAX_K) sel[slot] = ((uint64_t)x << 32) | i;
+    }
+  });
+  __syncthreads();
+  int m = s_cnt;
+  if (m > (int)k) m = (int)k;  // (exactly k, or fewer words in all)
+  block_sort(sel, m);
+  uint64_t *out = a.best_out + q * (int64_t)k;
+  for (int i = tid; i < (int)k; i += SEL_THREADS) out[i] = i < m ? sel[i] : VSK_KEY_NONE;
+}
+
+void launch_select_words(vsk_ctx *ctx, const WordSelectArgs &a, const char *name) {
+  if (a.nq <= 0) return;
+  if (a.k < 1 || a.k > VSK_MAX_K)
+    fail(VSK_ERR_INVALID_BUFFER_SIZE, "k out of range for selection");
+  KernelTimer t(ctx, name);
+  k_select_words<32><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  check_launch(name);
 }
 
 void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
