@@ -450,8 +450,9 @@ def setup(c, a, ctx, dev):
                     "points centre + 0.5 N(0,I) (seeds 5, 1, 2), centroids centre + "
                     "0.1 N(0,I) (seed 4); torch Philox",
             "dtype": "f32", "nq": nq, "n": n, "d": d,
-            "kernels": [("ivf_list_screen", "k_list_screen<4> (bf16 MFMA screen of the probed "
-                                            "lists, one 8-byte key per pair)", "keys_hbm"),
+            "kernels": [("ivf_list_screen", "k_list_screen<4, false> (bf16 MFMA screen of the "
+                                            "probed lists, one 32-bit word per pair)",
+                         "words_hbm"),
                         ("ivf_list_scan", "k_list_scan<16>", "valu")],
             "keep": (idx, x, q, dist, ids),
         }
@@ -704,14 +705,21 @@ def roofline(spec, stats):
                                      "achieved_GBps": round(4.0 * d * pairs / sec / 1e9, 1),
                                      "frac_of_hbm": round(4.0 * d * pairs / sec / 1e9
                                                           / PEAK_HBM_GBPS, 4)}
-    elif kind == "keys_hbm":
-        # the screened list scan writes one 8-byte (distance, position) key
-        # per (query, candidate) pair; its bf16 products are 2*d FLOP a pair
-        by = 8.0 * pairs
+    elif kind == "words_hbm":
+        # the screened list scan writes one 32-bit screened distance per
+        # (query, candidate) pair and reads the probed lists' bf16 plane
+        # (2 * roundup(d, 64) bytes a row); at this configuration's nq x
+        # nprobe every list is probed, so the plane is read once whole per
+        # launch (a list read by two 128-query groups counts once); its bf16
+        # products are 2*d FLOP a pair
+        ldb = (d + 63) // 64 * 64
+        by = 4.0 * pairs + 2.0 * ldb * spec["n"]
         ach = by / sec / 1e9
         r.update({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
-                  "algorithmic": "8 bytes (one key) written per (query, candidate) pair",
+                  "algorithmic": "4 bytes written per (query, candidate) pair + the bf16 "
+                                 "plane of the probed lists read once (2*roundup(d,64) "
+                                 "bytes per row, every row at this nprobe)",
                   "bf16_mfma_TFLOPs": round(2.0 * d * pairs / sec / 1e12, 2)})
     elif kind == "kpp":
         # per pick every row's distance to the new centroid: 4*d bytes read
