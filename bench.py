@@ -713,7 +713,7 @@ def roofline(spec, stats):
         # launch (a list read by two 128-query groups counts once); its bf16
         # products are 2*d FLOP a pair
         ldb = (d + 63) // 64 * 64
-        by = 4.0 * pairs + 2.0 * ldb * spec["n"]
+        by = 4.0 * pairs + 2.0 * ldb * spec["n"] * launches
         ach = by / sec / 1e9
         r.update({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
