@@ -497,6 +497,29 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
                                                : (f < 0.f ? __float_as_uint(f) + 1u
                                                           : 0x80000001u));
         s_tdot[tid] = f;
+      } else if constexpr (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2) {
+        // L2: a score can pass the exact test (fma(-2, dot, qa + xa), its
+        // max with 0, <= thf) only when dot - xa/2 >= (qa - thf)/2 less a
+        // margin for the roundings of both forms.  A passing row has
+        // (|x| - 1.01|q|)^2 <= 0.03 |q|^2 + thf + 1 (|dot| <= 1.01 |q||x| for
+        // the bf16 products), which bounds its |x|^2 by xq2 below; every
+        // rounding is then within 2^-22 (thf + qa + xq2 + 1), and the margin
+        // takes four times that.
+        const double qa = (double)s_qa[tid], t = (double)thf;
+        float f;
+        if (!ok) {
+          f = __int_as_float(0x7f800000);
+        } else if (th_hi == 0xFFFFFFFFu) {
+          f = -__int_as_float(0x7f800000);
+        } else {
+          const double xq = 1.01 * sqrt(qa) + sqrt(0.03 * qa + fabs(t) + 1.0);
+          const double m = 0.5 * (qa - t) - 0x1p-20 * (fabs(t) + qa + xq * xq + 1.0);
+          f = (float)m;
+          if ((double)f > m) f = __uint_as_float(f > 0.f ? __float_as_uint(f) - 1u
+                                                 : (f < 0.f ? __float_as_uint(f) + 1u
+                                                            : 0x80000001u));
+        }
+        s_tdot[tid] = f;
       } else {
         s_tdot[tid] = -thf;
       }
@@ -751,28 +774,32 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
               m |= (acc[i][j][r] < tdot) ? 0u : (1u << (4 * i + r));
         } else {
           const float th_f = l_thf[16 * j];
-          // the block's smallest distance first, the same expression as the
-          // per-score test below (its max with 0 maps NaN to 0, so the two
-          // agree exactly): when it is above the bound in every lane, no
-          // score of the block can pass
-          float mn = __int_as_float(0x7f800000);
+          // the block's largest dot - |x|^2/2 first, against the query's
+          // bound on it (with its margin, no score whose exact test below
+          // passes is under it): when it is below in every lane, no score of
+          // the block can pass.  A NaN score is dropped by the max; it needs
+          // a non-finite input, whose bound is not finite, so such a query
+          // fails the screen's check and is redone exactly.
+          const float tdot = l_tdot[16 * j];
+          float mx = -__int_as_float(0x7f800000);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              mn = fminf(mn, dist_from_dot<METRIC>(
-                                 acc[i][j][r], qa,
-                                 s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r]));
-          if (!__builtin_amdgcn_ballot_w64(mn <= th_f)) continue;
+              mx = fmaxf(mx, acc[i][j][r] -
+                                 0.5f * s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r]);
+          if (!__builtin_amdgcn_ballot_w64(!(mx < tdot))) continue;
+          // the same bound per score: a superset of the scores whose exact
+          // test below passes (the exact key test then decides each one)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               // (rows past the slice read 0 and are masked off below)
               const float xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r];
-              m |= (dist_from_dot<METRIC>(acc[i][j][r], qa, xa) > th_f)
-                       ? 0u : (1u << (4 * i + r));
+              m |= (acc[i][j][r] - 0.5f * xa < tdot) ? 0u : (1u << (4 * i + r));
             }
+          (void)th_f;
         }
         m &= vmask;
         if (!__builtin_amdgcn_ballot_w64(m != 0)) continue;  // the common case
