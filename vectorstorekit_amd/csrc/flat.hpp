@@ -91,12 +91,15 @@ __device__ inline float f_down(double v) {
 // |q - bf16(q)| = qr against rows whose maxima of |bf16(x)| and |x - bf16(x)|
 // are xh and xr, over d dimensions (the derivation heads flat_screen.hip):
 // every screened distance lies within eps of the reference's fp32 one.
+// With the query as two bf16 planes (q = qh' + ql' + r), qh is |qh'| + |ql'|,
+// qr is |r| and the screen sums nprod = 2d exact products instead of d.
 __device__ inline double screen_eps_of(double qh, double qr, double xh, double xr, int32_t d,
-                                       int32_t metric) {
+                                       int32_t metric, int32_t nprod = 0) {
   const double u = 0x1p-24;
   const double qn = qh + qr, xn = xh + xr, dd = (double)d;
+  const double np = nprod > 0 ? (double)nprod : dd;
   const double e_dot =
-      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
+      qh * xr + qr * xh + qr * xr + 2.0 * (np - 1.0) * u * qh * xh + np * 0x1p-126;
   const double e_ref = 1.01 * dd * u * qn * xn;
   double eps;
   if (metric == VSK_METRIC_DOT)
@@ -128,6 +131,7 @@ struct MarginArgs {
   const float *qnh = nullptr, *qnr = nullptr;  // per query |qh|, |q - qh|
   double xh = 0, xr = 0;
   int32_t d = 0, metric = 0;
+  int32_t nprod = 0;  // products the screen summed (0: d; 2d with a query lo plane)
   uint64_t *out = nullptr;
   int32_t cap = 0;
   int32_t *nout = nullptr;
@@ -225,6 +229,10 @@ struct ArgminQueries {
   const uint16_t *qh = nullptr;
   const float *qnh = nullptr, *qnr = nullptr, *qsq = nullptr;
   int32_t ldb = 0;
+  // a second plane ql = bf16(q - qh) when the screen takes the query as two
+  // planes (then qnh = |qh| + |ql|, qnr = |q - qh - ql|, nprod = 2d)
+  const uint16_t *ql = nullptr;
+  int32_t nprod = 0;
 };
 ArgminQueries argmin_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
                              int32_t ld, const char *slot);

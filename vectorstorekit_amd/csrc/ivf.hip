@@ -483,10 +483,11 @@ struct DenseScreen {
   int32_t nchunks;
 };
 constexpr int kScreenQ = 128;  // queries per screen workgroup: 2 halves of 4 waves
-template <int KS, bool DENSE>
+template <int KS, bool DENSE, int PL>
 __global__ __launch_bounds__(512) void k_list_screen(
     const uint16_t *xplane, const float *xsq, int32_t ldb, const int64_t *list_off,
-    const uint16_t *qplane, const float *qsq, const int32_t *pairs, const int4 *groups,
+    const uint16_t *qplane, const uint16_t *qlo, const float *qsq, const int32_t *pairs,
+    const int4 *groups,
     const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *wseg,
     uint32_t *out, DenseScreen ds) {
   if (!DENSE && blockIdx.x >= *ngroups) return;
@@ -536,6 +537,19 @@ __global__ __launch_bounds__(512) void k_list_screen(
     for (int ks = 0; ks < KS; ++ks)
       qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + q * ldb + 32 * ks + kc);
   }
+  // the lo plane of the group's queries in LDS, rows padded by 16 bytes so
+  // that the 16 lanes reading one fragment (16 queries, one column) touch
+  // distinct banks
+  constexpr int QLP = PL == 2 ? 32 * KS + 8 : 8;  // row pitch in bf16
+  __shared__ __attribute__((aligned(16))) uint16_t s_ql[PL == 2 ? kScreenQ * QLP : 8];
+  if constexpr (PL == 2) {
+    constexpr int CH = 4 * KS;  // 16-byte chunks a row
+    for (int e = threadIdx.x; e < kScreenQ * CH; e += 512) {
+      const int j = e / CH, c = e - j * CH;
+      *reinterpret_cast<bf8v *>(s_ql + j * QLP + 8 * c) =
+          *reinterpret_cast<const bf8v *>(qlo + query(j) * ldb + 8 * c);
+    }
+  }
   __syncthreads();
   if (ntile == 0) return;  // (after the block's only barrier)
   for (int64_t b = v0 + 16 * w; b < v1; b += 64) {
@@ -553,8 +567,14 @@ __global__ __launch_bounds__(512) void k_list_screen(
       if (t >= ntile) break;  // uniform
       f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int ks = 0; ks < KS; ++ks) {
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t][ks], xf[ks], acc, 0, 0, 0);
+        if constexpr (PL == 2) {
+          const bf8v lo = *reinterpret_cast<const bf8v *>(
+              s_ql + (hbase + 16 * t + (lane & 15)) * QLP + 32 * ks + kc);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, xf[ks], acc, 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = hbase + 16 * t + 4 * (lane >> 4) + r;
@@ -694,6 +714,8 @@ static void ivf_assign_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dx,
 
 static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
                             int64_t nq, int32_t np, uint64_t *keys);
+static ArgminQueries screen_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                                    int32_t ld);
 static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int64_t nq,
                          int32_t np, const ArgminQueries &qp, uint64_t *keys);
 
@@ -718,7 +740,7 @@ static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
     if (qp) {
       probe_screen(ctx, ivf, dq, nq, np, *qp, keys);
     } else {
-      const ArgminQueries own = argmin_queries(ctx, dq, nq, ivf->d, ivf->ld, "ivf.sq");
+      const ArgminQueries own = screen_queries(ctx, dq, nq, ivf->d, ivf->ld);
       probe_screen(ctx, ivf, dq, nq, np, own, keys);
     }
   } else {
@@ -751,6 +773,95 @@ static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
     progressive_topk(ctx, nb, ivf->nlist, np, cap, scan, keys + b0 * np,
                      "ivf_probe_select");
   }
+}
+
+// the queries as two bf16 planes for the screens: hi = bf16(q), lo =
+// bf16(q - hi) (ldb columns, zero padded), |hi| + |lo| and |q - hi - lo|
+// (sums of squares in double, square roots rounded up), one wave per query
+__global__ __launch_bounds__(256) void k_query_planes2(const float *Q, int64_t nq, int32_t d,
+                                                       int32_t ld, int32_t ldb, uint16_t *hi,
+                                                       uint16_t *lo, float *nh, float *nr,
+                                                       float *nh1, float *nr1) {
+#pragma clang fp contract(off)
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (q >= nq) return;
+  double sh = 0.0, sl = 0.0, sr = 0.0, s1 = 0.0;
+  for (int c = lane; c < ldb; c += 64) {
+    const float v = c < d ? Q[q * ld + c] : 0.f;
+    const uint16_t h = bf16_rn(v);
+    const float hv = __uint_as_float((uint32_t)h << 16);
+    const float rv = v - hv;  // exact
+    const uint16_t l = bf16_rn(rv);
+    const float lv = __uint_as_float((uint32_t)l << 16);
+    const float r2 = rv - lv;  // exact
+    hi[q * ldb + c] = h;
+    lo[q * ldb + c] = l;
+    sh += (double)hv * (double)hv;
+    sl += (double)lv * (double)lv;
+    sr += (double)r2 * (double)r2;
+    s1 += (double)rv * (double)rv;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    sh += __shfl_xor(sh, o);
+    sl += __shfl_xor(sl, o);
+    sr += __shfl_xor(sr, o);
+    s1 += __shfl_xor(s1, o);
+  }
+  if (lane == 0) {
+    nh[q] = f_up((sqrt(sh) + sqrt(sl)) * (1.0 + 1e-12));
+    nr[q] = f_up(sqrt(sr) * (1.0 + 1e-12));
+    nh1[q] = f_up(sqrt(sh) * (1.0 + 1e-12));
+    nr1[q] = f_up(sqrt(s1) * (1.0 + 1e-12));
+  }
+}
+
+// The screens' query planes.  one: the hi plane with |hi| and |q - hi|;
+// two (d <= 128, the lo plane's fragments fit the list screen's LDS):
+// the same hi plane and a lo plane, with |hi| + |lo| and |q - hi - lo|.  The
+// list scan's rescore reads about half the rows with two planes (the
+// bound's query term shrinks 2^8-fold); the probe, whose margin holds few
+// centroids beyond the nprobe, keeps one plane and its cheaper screen.
+// |q|^2 for both.
+struct ScreenQueries {
+  ArgminQueries one, two;
+};
+static ScreenQueries screen_queries2(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                                     int32_t ld) {
+  ScreenQueries sq;
+  if (d > 128) {
+    sq.one = sq.two = argmin_queries(ctx, dq, nq, d, ld, "ivf.sq");
+    return sq;
+  }
+  ArgminQueries qp;
+  qp.ldb = (d + 63) & ~63;
+  uint16_t *qh = static_cast<uint16_t *>(
+      ctx->scratch_ptr("ivf.sq2.planes", sizeof(uint16_t) * 2 * (size_t)nq * qp.ldb));
+  float *nrm = static_cast<float *>(ctx->scratch_ptr("ivf.sq2.norms", sizeof(float) * 5 * (size_t)nq));
+  {
+    KernelTimer t(ctx, "query_planes");
+    k_query_planes2<<<(unsigned)ceil_div(nq, 4), 256, 0, ctx->stream>>>(
+        dq, nq, d, ld, qp.ldb, qh, qh + (size_t)nq * qp.ldb, nrm, nrm + nq, nrm + 3 * nq,
+        nrm + 4 * nq);
+    check_launch("query_planes");
+  }
+  row_norms(ctx, dq, nq, d, ld, nrm + 2 * nq, nullptr);
+  qp.qh = qh;
+  qp.qsq = nrm + 2 * nq;
+  sq.one = qp;
+  sq.one.qnh = nrm + 3 * nq;
+  sq.one.qnr = nrm + 4 * nq;
+  sq.two = qp;
+  sq.two.ql = qh + (size_t)nq * qp.ldb;
+  sq.two.qnh = nrm;
+  sq.two.qnr = nrm + nq;
+  sq.two.nprod = 2 * d;
+  return sq;
+}
+static ArgminQueries screen_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d,
+                                    int32_t ld) {
+  return screen_queries2(ctx, dq, nq, d, ld).one;
 }
 
 // whether the list scan of kind 0 goes through the bf16 screen: L2 / L2^2,
@@ -1063,16 +1174,16 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     t.device_work(dseg + nb);
     const unsigned gmax =
         (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, kScreenQ));
-#define VSK_LS(KS)                                                                          \
-  k_list_screen<KS, false><<<gmax, 512, 0, ctx->stream>>>(                                 \
+#define VSK_LS(KS, PL)                                                                      \
+  k_list_screen<KS, false, PL><<<gmax, 512, 0, ctx->stream>>>(                             \
       ivf->xplane.as<uint16_t>(), ivf->xsq.as<float>(), ldb, ivf->list_off.as<int64_t>(),   \
-      qp.qh + b0 * qp.ldb, qp.qsq + b0, lg.pairs, lg.groups, lg.gstart + nlist, np, bpos,   \
-      wseg, words, DenseScreen{})
+      qp.qh + b0 * qp.ldb, qp.ql ? qp.ql + b0 * qp.ldb : nullptr, qp.qsq + b0, lg.pairs,    \
+      lg.groups, lg.gstart + nlist, np, bpos, wseg, words, DenseScreen{})
     switch (ldb / 32) {
-    case 2: VSK_LS(2); break;
-    case 4: VSK_LS(4); break;
-    case 6: VSK_LS(6); break;
-    default: VSK_LS(8); break;
+    case 2: if (qp.ql) VSK_LS(2, 2); else VSK_LS(2, 1); break;
+    case 4: if (qp.ql) VSK_LS(4, 2); else VSK_LS(4, 1); break;
+    case 6: VSK_LS(6, 1); break;
+    default: VSK_LS(8, 1); break;
     }
 #undef VSK_LS
     check_launch("ivf_list_screen");
@@ -1100,6 +1211,7 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     ma.xh = ivf->xh_max;
     ma.xr = ivf->xr_max;
     ma.d = ivf->d;
+    ma.nprod = qp.nprod;
     ma.metric = metric;
     ma.out = kept;
     ma.cap = cap;
@@ -1204,15 +1316,16 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
       KernelTimer t(ctx, "ivf_probe_screen", (double)nb * nlist);
       const unsigned grid = (unsigned)(nchunks * ceil_div(nb, kScreenQ));
       const DenseScreen ds{nb, nlist, wstride, nchunks};
-#define VSK_PS(KS)                                                                            \
-  k_list_screen<KS, true><<<grid, 512, 0, ctx->stream>>>(                                    \
+#define VSK_PS(KS, PL)                                                                        \
+  k_list_screen<KS, true, PL><<<grid, 512, 0, ctx->stream>>>(                                \
       cdb->split.as<uint16_t>(), cdb->sqnorm.as<float>(), ldb, nullptr, qp.qh + b0 * qp.ldb, \
-      qp.qsq + b0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, words, ds)
+      qp.ql ? qp.ql + b0 * qp.ldb : nullptr, qp.qsq + b0, nullptr, nullptr, nullptr, 0,      \
+      nullptr, nullptr, words, ds)
       switch (ldb / 32) {
-      case 2: VSK_PS(2); break;
-      case 4: VSK_PS(4); break;
-      case 6: VSK_PS(6); break;
-      default: VSK_PS(8); break;
+      case 2: if (qp.ql) VSK_PS(2, 2); else VSK_PS(2, 1); break;
+      case 4: if (qp.ql) VSK_PS(4, 2); else VSK_PS(4, 1); break;
+      case 6: VSK_PS(6, 1); break;
+      default: VSK_PS(8, 1); break;
       }
 #undef VSK_PS
       check_launch("ivf_probe_screen");
@@ -1228,6 +1341,7 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
     ma.xh = cdb->split_max_hi;
     ma.xr = cdb->split_max_res;
     ma.d = ivf->d;
+    ma.nprod = qp.nprod;
     ma.metric = VSK_METRIC_L2;
     ma.out = kept;
     ma.cap = cap;
@@ -1360,9 +1474,9 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   const bool screen =
       kind == 0 && list_screen_applies(ctx, ivf, metric, k, (double)nq * per_query);
   const bool exact_all = np == ivf->nlist && np > VSK_MAX_K;
-  ArgminQueries qp;
+  ScreenQueries sqp;
   if (screen || (!exact_all && probe_screen_applies(ctx, ivf, nq, np)))
-    qp = argmin_queries(ctx, dq, nq, ivf->d, ld, "ivf.sq");
+    sqp = screen_queries2(ctx, dq, nq, ivf->d, ld);
 
   // 1. probes
   int32_t *probes = static_cast<int32_t *>(
@@ -1378,7 +1492,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     VSK_HIP(hipMemcpyAsync(probes, all.data(), 4 * all.size(),
                            hipMemcpyHostToDevice, ctx->stream));
   } else {
-    ivf_probe_device(ctx, ivf, dq, nq, np, probes, qp.qh ? &qp : nullptr);
+    ivf_probe_device(ctx, ivf, dq, nq, np, probes, sqp.one.qh ? &sqp.one : nullptr);
   }
   // 2. candidate counts and probe position bases
   int64_t *pos_base = static_cast<int64_t *>(
@@ -1454,8 +1568,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     }
     if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     if (screen) {
-      list_screen_batch(ctx, ivf, qp, dq, b0, nb, np, k, metric, probes, pos_base, cnt, dseg,
-                        wseg, lgp, cand, best);
+      list_screen_batch(ctx, ivf, sqp.two, dq, b0, nb, np, k, metric, probes, pos_base, cnt,
+                        dseg, wseg, lgp, cand, best);
       continue;
     }
     const int64_t *ngroups = gstart + nlist;

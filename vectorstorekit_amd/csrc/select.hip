@@ -520,7 +520,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
   // little above it: the search stops once the words left in the k-th's
   // bucket span less than 1/64 of the margin (the limit then only grows by
   // that much, and every key it adds is rescored like the others)
-  const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
+  const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
   const uint32_t kth = word_kth(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   // every key when there are fewer than k, else those within the margin
   uint32_t lim_word = kWordNone - 1u;
