@@ -145,6 +145,26 @@ def test_ivf_probe_screen_overflow():
     sctx.close()
 
 
+def test_ivf_screen_exact_strategy_many_lists():
+    """The screened list scan when every one of more lists than a selection
+    holds is probed (the .exact strategy with 1,100 lists: probes in index
+    order, candidate segments of every row), for both euclidean metrics;
+    bit-exact against the oracle."""
+    x, q, c = _mixture(21, 1100, 9000, 24, 30)
+    sctx = _screen_ctx()
+    idx = _index(sctx, c, x, None, 8)
+    lists = O.ivf_assign(x, c)
+    ids = np.arange(len(x), dtype=np.int64)
+    for metric in ("euclidean", "euclideanSquared"):
+        print(f"ivf screen exact strategy, 1100 lists, {metric}", flush=True)
+        gd, gi = idx.search(q, 12, strategy="exact", metric=metric)
+        od, oi = O.ivf_search(q, x, ids, lists, c, 1100, 12, squared=metric != "euclidean")
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    assert "ivf_list_screen" in sctx.profile_stats()
+    sctx.close()
+
+
 def test_ivf_screen_unclustered_bit_exact():
     """Rows without cluster structure (i.i.d. normal), many probes, so many
     candidates lie within the screen's margin of the k-th.  Bit-exact
