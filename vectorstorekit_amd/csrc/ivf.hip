@@ -528,26 +528,33 @@ __global__ __launch_bounds__(512) void k_list_screen(
   // this half's query tiles: slots 64 half + 16 t
   const int hbase = 64 * half;
   const int ntile = npair - hbase <= 0 ? 0 : (npair - hbase + 15) >> 4;
-  bf8v qf[4][KS];
+  // one plane: the half's query fragments in registers; two planes: both
+  // planes of the group's queries in LDS (the registers of both would halve
+  // the waves a SIMD holds), rows padded by 16 bytes so that the 16 lanes
+  // reading one fragment (16 queries, one column) touch distinct banks
+  bf8v qf[PL == 1 ? 4 : 1][PL == 1 ? KS : 1];
+  if constexpr (PL == 1) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int j = hbase + 16 * t + (lane & 15);
-    const int64_t q = query(j);
+    for (int t = 0; t < 4; ++t) {
+      const int j = hbase + 16 * t + (lane & 15);
+      const int64_t q = query(j);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + q * ldb + 32 * ks + kc);
+      for (int ks = 0; ks < KS; ++ks)
+        qf[t][ks] = *reinterpret_cast<const bf8v *>(qplane + q * ldb + 32 * ks + kc);
+    }
   }
-  // the lo plane of the group's queries in LDS, rows padded by 16 bytes so
-  // that the 16 lanes reading one fragment (16 queries, one column) touch
-  // distinct banks
   constexpr int QLP = PL == 2 ? 32 * KS + 8 : 8;  // row pitch in bf16
+  __shared__ __attribute__((aligned(16))) uint16_t s_qh[PL == 2 ? kScreenQ * QLP : 8];
   __shared__ __attribute__((aligned(16))) uint16_t s_ql[PL == 2 ? kScreenQ * QLP : 8];
   if constexpr (PL == 2) {
     constexpr int CH = 4 * KS;  // 16-byte chunks a row
     for (int e = threadIdx.x; e < kScreenQ * CH; e += 512) {
       const int j = e / CH, c = e - j * CH;
+      const int64_t qo = query(j) * ldb + 8 * c;
+      *reinterpret_cast<bf8v *>(s_qh + j * QLP + 8 * c) =
+          *reinterpret_cast<const bf8v *>(qplane + qo);
       *reinterpret_cast<bf8v *>(s_ql + j * QLP + 8 * c) =
-          *reinterpret_cast<const bf8v *>(qlo + query(j) * ldb + 8 * c);
+          *reinterpret_cast<const bf8v *>(qlo + qo);
     }
   }
   __syncthreads();
@@ -568,10 +575,13 @@ __global__ __launch_bounds__(512) void k_list_screen(
       f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t][ks], xf[ks], acc, 0, 0, 0);
-        if constexpr (PL == 2) {
-          const bf8v lo = *reinterpret_cast<const bf8v *>(
-              s_ql + (hbase + 16 * t + (lane & 15)) * QLP + 32 * ks + kc);
+        if constexpr (PL == 1) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[t][ks], xf[ks], acc, 0, 0, 0);
+        } else {
+          const int off = (hbase + 16 * t + (lane & 15)) * QLP + 32 * ks + kc;
+          const bf8v hi = *reinterpret_cast<const bf8v *>(s_qh + off);
+          const bf8v lo = *reinterpret_cast<const bf8v *>(s_ql + off);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, xf[ks], acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, xf[ks], acc, 0, 0, 0);
         }
       }
