@@ -14,6 +14,8 @@
 // that still match the resolved prefix; it stops early as soon as the bucket
 // holding the k-th key is taken whole.  The <= k winners are gathered into LDS and
 // bitonic-sorted (at most 1024 of them).
+#include <type_traits>
+
 #include "flat.hpp"
 
 namespace vsk {
@@ -507,6 +509,112 @@ struct WordList {
   }
 };
 
+// in-register bitonic sort of R 32-bit values a lane across the wave
+// (value e at lane e / R, register e % R), ascending
+template <int R>
+__device__ void wave_sort_u32(uint32_t (&v)[R]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      if (j < R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r & j) continue;
+          const bool asc = ((lane * R + r) & size) == 0;
+          const uint32_t a = v[r], b = v[r + j];
+          const bool sw = (a > b) == asc;
+          v[r] = sw ? b : a;
+          v[r + j] = sw ? a : b;
+        }
+      } else {
+        const int lj = j / R;
+        const bool lower = (lane & lj) == 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const bool asc = ((lane * R + r) & size) == 0;
+          const uint32_t p = __shfl_xor(v[r], lj);
+          const uint32_t mn = v[r] < p ? v[r] : p, mx = v[r] < p ? p : v[r];
+          v[r] = lower == asc ? mn : mx;
+        }
+      }
+    }
+  }
+}
+
+// The k-th smallest word (ties counted; kWordNone when fewer than k) by a
+// bound first: each wave's k-th smallest per-lane minimum has k words at or
+// below it, so the smallest of those over the waves, T, does too, and the
+// k-th smallest word is among the words at or below T -- usually a few
+// times k of them, gathered into LDS and sorted by one wave.  k <= 64;
+// more than 512 words at or below T (or fewer than k lanes holding words in
+// every wave) falls back to word_kth.  Called by every thread of the block.
+struct KthShared {
+  WordShared w;
+  uint32_t wmin[SEL_THREADS / 64];
+  uint32_t g[512];
+  int cnt;
+  uint32_t kth;
+};
+template <class Each>
+__device__ uint32_t word_kth_fast(Each &&each, uint32_t k, KthShared &sh, double stop_span) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (k == 0 || k > 64) return word_kth(each, k, sh.w, stop_span);
+  uint32_t m = kWordNone;
+  each([&](uint32_t x, uint32_t) { m = x < m ? x : m; });
+  uint32_t v[1] = {m};
+  wave_sort_u32<1>(v);
+  const uint32_t wk = __shfl(v[0], (int)k - 1);
+  if (lane == 0) sh.wmin[wv] = wk;
+  if (tid == 0) sh.cnt = 0;
+  __syncthreads();
+  uint32_t T = sh.wmin[0];
+#pragma unroll
+  for (int i = 1; i < SEL_THREADS / 64; ++i) T = min(T, sh.wmin[i]);
+  if (T == kWordNone) {  // no wave has k lanes holding words
+    __syncthreads();
+    return word_kth(each, k, sh.w, stop_span);
+  }
+  each([&](uint32_t x, uint32_t) {
+    if (x <= T) {
+      const int slot = atomicAdd(&sh.cnt, 1);
+      if (slot < 512) sh.g[slot] = x;
+    }
+  });
+  __syncthreads();
+  const int c = sh.cnt;
+  if (c > 512) {
+    __syncthreads();
+    return word_kth(each, k, sh.w, stop_span);
+  }
+  if (wv == 0) {
+    // c >= k words; sort them in the smallest register width that holds them
+    auto pick = [&](auto rtag) {
+      constexpr int R = decltype(rtag)::value;
+      uint32_t r[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int e = lane * R + i;
+        r[i] = e < c ? sh.g[e] : kWordNone;
+      }
+      wave_sort_u32<R>(r);
+      const int e = (int)k - 1;
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        if (lane * R + i == e) sh.kth = r[i];
+    };
+    if (c <= 64) pick(std::integral_constant<int, 1>{});
+    else if (c <= 128) pick(std::integral_constant<int, 2>{});
+    else if (c <= 256) pick(std::integral_constant<int, 4>{});
+    else pick(std::integral_constant<int, 8>{});
+  }
+  __syncthreads();
+  const uint32_t kth = sh.kth;
+  __syncthreads();  // every thread has read it
+  return kth;
+}
+
 template <int REG>
 __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
   const int64_t q = blockIdx.x;
@@ -514,14 +622,14 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_margin(MarginArgs a) {
   WordList<REG> L;
   L.load(a.words + (a.wseg ? a.wseg[q] : q * a.wstride), a.cnt ? a.cnt[q] : a.wn);
   auto each = [&](auto &&f) { L.each(f); };
-  __shared__ WordShared sh;
+  __shared__ KthShared sh;
   __shared__ int s_cnt;
   // the k-th smallest word (kWordNone: fewer than k words), or a word a
   // little above it: the search stops once the words left in the k-th's
   // bucket span less than 1/64 of the margin (the limit then only grows by
   // that much, and every key it adds is rescored like the others)
   const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
-  const uint32_t kth = word_kth(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
+  const uint32_t kth = word_kth_fast(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   // every key when there are fewer than k, else those within the margin
   uint32_t lim_word = kWordNone - 1u;
   if (kth != kWordNone) {
@@ -568,12 +676,12 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select_words(WordSelectArgs a) 
   WordList<REG> L;
   L.load(a.words + a.wseg[q], a.cnt[q]);
   auto each = [&](auto &&f) { L.each(f); };
-  __shared__ WordShared sh;
+  __shared__ KthShared sh;
   __shared__ uint64_t sel[VSK_MAX_K];
   __shared__ uint32_t s_less, s_eq;
   __shared__ int s_cnt;
   const uint32_t k = (uint32_t)a.k;
-  const uint32_t V = word_kth(each, k, sh, 0.0);
+  const uint32_t V = word_kth_fast(each, k, sh, 0.0);
   uint32_t I = 0xFFFFFFFFu;  // the largest index kept among words equal to V
   if (V != kWordNone) {
     if (tid == 0) {
@@ -600,7 +708,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select_words(WordSelectArgs a) 
     if (s_eq > need_eq) {
       I = word_kth([&](auto &&f) {
         L.each([&](uint32_t x, uint32_t i) { f(x == V ? i : kWordNone, i); });
-      }, need_eq, sh, 0.0);
+      }, need_eq, sh.w, 0.0);
     }
   }
   if (tid == 0) s_cnt = 0;
