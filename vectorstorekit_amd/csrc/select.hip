@@ -181,13 +181,49 @@ __device__ void radix_threshold(EachKey &&each_key, int32_t k, SelShared &sh, ui
   hi_out = hi;
 }
 
+// in-register bitonic sort of R 64-bit keys a lane across the wave (key e
+// at lane e / R, register e % R), ascending
+template <int R>
+__device__ void wave_sort_u64(uint64_t (&v)[R]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64 * R; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      if (j < R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r & j) continue;
+          const bool asc = ((lane * R + r) & size) == 0;
+          const uint64_t a = v[r], b = v[r + j];
+          const bool sw = (a > b) == asc;
+          v[r] = sw ? b : a;
+          v[r + j] = sw ? a : b;
+        }
+      } else {
+        const int lj = j / R;
+        const bool lower = (lane & lj) == 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const bool asc = ((lane * R + r) & size) == 0;
+          const uint64_t p = __shfl_xor(v[r], lj);
+          const uint64_t mn = v[r] < p ? v[r] : p, mx = v[r] < p ? p : v[r];
+          v[r] = lower == asc ? mn : mx;
+        }
+      }
+    }
+  }
+}
+
 // REG: keys per thread held in registers when a query's list fits (REG x
 // SEL_THREADS keys): every pass then reads registers, not the list again.
 // The registers cost occupancy, so only callers whose lists are a few
 // thousand keys (IVF candidate segments, a dense chunk as small as the IVF
 // probe's centroids) take it.
-// W32: the candidates are a.cand32 (no previous list)
-template <int REG, bool W32>
+// W32: the candidates are a.cand32 (no previous list).  FAST: the short
+// cut below for k <= 64 (its registers would slow the radix search of the
+// other instances).
+template <int REG, bool W32, bool FAST = false>
 __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -254,6 +290,62 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   __shared__ SelShared sh;
   __shared__ uint64_t sel[VSK_MAX_K];
   __shared__ int sel_count;
+  // Short cut for k <= 64 over a list in registers, sorted output: each
+  // wave's k-th smallest per-lane minimum has k keys at or below it, so the
+  // smallest of those over the waves, B, does too; the k smallest keys are
+  // among the keys at or below B (usually a few times k), which one wave
+  // sorts.  More than 512 of them, or fewer than k lanes holding keys in
+  // every wave, takes the radix search.
+  if (FAST && REG > 0 && inreg && a.sorted && k <= 64) {
+    uint64_t mn = VSK_KEY_NONE;
+    each_key([&](uint64_t key) { mn = key < mn ? key : mn; });
+    uint64_t v1[1] = {mn};
+    wave_sort_u64<1>(v1);
+    const uint64_t wk = __shfl(v1[0], k - 1);
+    if (lane == 0) sh.lo[tid >> 6] = wk;
+    if (tid == 0) sel_count = 0;
+    __syncthreads();
+    uint64_t B = sh.lo[0];
+#pragma unroll
+    for (int i = 1; i < SEL_THREADS / 64; ++i) B = sh.lo[i] < B ? sh.lo[i] : B;
+    if (B != VSK_KEY_NONE) {
+      each_key([&](uint64_t key) {
+        if (key <= B) {
+          const int slot = atomicAdd(&sel_count, 1);
+          if (slot < 512) sel[slot] = key;
+        }
+      });
+    }
+    __syncthreads();
+    const int c = sel_count;
+    if (B != VSK_KEY_NONE && c <= 512) {
+      if (tid < 64) {
+        uint64_t *out = a.best_out + q * (int64_t)k;
+        auto finish = [&](auto rtag) {
+          constexpr int R = decltype(rtag)::value;
+          uint64_t r[R];
+#pragma unroll
+          for (int i = 0; i < R; ++i) {
+            const int e = lane * R + i;
+            r[i] = e < c ? sel[e] : VSK_KEY_NONE;
+          }
+          wave_sort_u64<R>(r);
+#pragma unroll
+          for (int i = 0; i < R; ++i) {
+            const int e = lane * R + i;
+            if (e < k) out[e] = r[i];
+            if (e == k - 1 && a.thresh) a.thresh[q] = r[i];
+          }
+        };
+        if (c <= 64) finish(std::integral_constant<int, 1>{});
+        else if (c <= 128) finish(std::integral_constant<int, 2>{});
+        else if (c <= 256) finish(std::integral_constant<int, 4>{});
+        else finish(std::integral_constant<int, 8>{});
+      }
+      return;
+    }
+    __syncthreads();  // sel_count and sh.lo are read; the radix search reuses them
+  }
   uint64_t T, hi;
   bool take_all;
   radix_threshold(each_key, k, sh, T, take_all, hi);
@@ -751,15 +843,23 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   }
   // keys per query: the previous list (k) and up to cap candidates
   const int64_t most = a.cap + (a.prev ? a.k : 0);
+  const bool fast = a.k <= 64 && a.sorted && !a.seg_n;
   if (a.cand32) {
     if (a.prev || a.seg_n) fail(VSK_ERR_INVALID_ARGUMENT, "32-bit lists take no previous list or segments");
     k_select<32, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
-  } else if (a.regs && !a.seg_off && most > 32 * SEL_THREADS)
-    k_select<64, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
-  else if (a.seg_off || a.regs)
-    k_select<32, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
-  else
+  } else if (a.regs && !a.seg_off && most > 32 * SEL_THREADS) {
+    if (fast)
+      k_select<64, false, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+    else
+      k_select<64, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  } else if (a.seg_off || a.regs) {
+    if (fast)
+      k_select<32, false, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+    else
+      k_select<32, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  } else {
     k_select<0, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  }
   check_launch(name);
 }
 
