@@ -112,15 +112,15 @@ __global__ void k_probe_bases(const int32_t *probes, int64_t nq, int32_t np,
   cnt[q] = s;
 }
 
-// pair (q, p) -> its slot in the list-grouped pair array
-__global__ void k_group_pairs(const int32_t *probes, int64_t npairs, int32_t np,
-                              int32_t *cursor, int32_t *pairs) {
+// pair (q, p) -> its slot in the list-grouped pair array: its list's
+// first slot plus its rank there
+__global__ void k_group_pairs(const int32_t *probes, int64_t npairs, const int64_t *lstart,
+                              const int32_t *rank, int32_t *pairs) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
        i += (int64_t)gridDim.x * blockDim.x) {
-    int32_t l = probes[i];
+    const int32_t l = probes[i];
     if (l < 0) continue;
-    const int32_t slot = atomicAdd(&cursor[l], 1);
-    pairs[slot] = (int32_t)i;  // i = q * np + p
+    pairs[lstart[l] + rank[i]] = (int32_t)i;  // i = q * np + p
   }
 }
 
@@ -160,8 +160,7 @@ __device__ void block_scan_1024(const int64_t (&v)[NV], int64_t (&out)[NV],
 // seg[i] = cnt[0] + ... + cnt[i-1] for i = 0..m (one block of 1024, each
 // thread a run of consecutive counts, one block scan of the runs' sums);
 // with wseg, the same over the counts rounded up to multiples of 4
-__global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_t m,
-                                                      int64_t *seg, int64_t *wseg) {
+__device__ void seg_offsets(const int64_t *cnt, int64_t m, int64_t *seg, int64_t *wseg) {
   __shared__ int64_t wsum[16][2];
   __shared__ int64_t carry[2];
   if (threadIdx.x < 2) carry[threadIdx.x] = 0;
@@ -189,16 +188,17 @@ __global__ __launch_bounds__(1024) void k_seg_offsets(const int64_t *cnt, int64_
   }
 }
 
-// pairs per list
-__global__ void k_list_pair_counts(const int32_t *probes, int64_t npairs, int32_t *lcnt) {
+// pairs per list, and each pair's rank among its list's pairs
+__global__ void k_list_pair_counts(const int32_t *probes, int64_t npairs, int32_t *lcnt,
+                                   int32_t *rank) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int32_t l = probes[i];
-    if (l >= 0) atomicAdd(&lcnt[l], 1);
+    if (l >= 0) rank[i] = atomicAdd(&lcnt[l], 1);
   }
 }
 
-// per list: its first pair slot (lstart, and cursor for the pair scatter)
+// per list: its first pair slot (lstart)
 // and its first group (gstart; ceil(pairs / G) groups for a list holding
 // rows, none for an empty one); totals at [nlist].  One block of 1024,
 // each thread a run of consecutive lists.
@@ -207,10 +207,8 @@ __device__ inline int64_t list_groups(const int32_t *lcnt, const int64_t *list_o
   const int64_t c = lcnt[l];
   return c > 0 && list_off[l + 1] > list_off[l] ? (c + G - 1) / G : 0;
 }
-__global__ __launch_bounds__(1024) void k_list_offsets(const int32_t *lcnt,
-                                                       const int64_t *list_off, int32_t nlist,
-                                                       int32_t G, int64_t *lstart,
-                                                       int32_t *cursor, int64_t *gstart) {
+__device__ void list_offsets(const int32_t *lcnt, const int64_t *list_off, int32_t nlist,
+                             int32_t G, int64_t *lstart, int64_t *gstart, int4 *groups) {
   __shared__ int64_t wsum[16][2];
   __shared__ int64_t carry[2];
   if (threadIdx.x < 2) carry[threadIdx.x] = 0;
@@ -225,11 +223,15 @@ __global__ __launch_bounds__(1024) void k_list_offsets(const int32_t *lcnt,
   int64_t o[2];
   block_scan_1024<2>(v, o, wsum, carry);
   for (int64_t l = l0; l < l1; ++l) {
+    // the list's groups: (list, first pair slot, pairs, 0), up to G pairs
+    const int32_t c = lcnt[l];
+    const int64_t ng = list_groups(lcnt, list_off, l, G);
+    for (int64_t j = 0; j < ng; ++j)
+      groups[o[1] + j] = int4{(int)l, (int)(o[0] + j * G), (int)min<int64_t>(G, c - j * G), 0};
     lstart[l] = o[0];
-    cursor[l] = (int32_t)o[0];
     gstart[l] = o[1];
-    o[0] += lcnt[l];
-    o[1] += list_groups(lcnt, list_off, l, G);
+    o[0] += c;
+    o[1] += ng;
   }
   if (threadIdx.x == 0) {
     lstart[nlist] = carry[0];
@@ -237,16 +239,18 @@ __global__ __launch_bounds__(1024) void k_list_offsets(const int32_t *lcnt,
   }
 }
 
-// the groups of each list: (list, first pair slot, pairs, 0), up to G pairs
-__global__ void k_make_groups(const int32_t *lcnt, const int64_t *lstart, const int64_t *gstart,
-                              int32_t nlist, int32_t G, int4 *groups) {
-  const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (l >= nlist) return;
-  const int64_t g0 = gstart[l], n = gstart[l + 1] - g0;
-  const int32_t c = lcnt[l];
-  for (int64_t j = 0; j < n; ++j)
-    groups[g0 + j] = int4{(int)l, (int)(lstart[l] + j * G), (int)min<int64_t>(G, c - j * G), 0};
+// block 0: the batch's segment offsets (seg_offsets); block 1 (when there
+// are lists to group): the lists' pair and group offsets and the groups
+__global__ __launch_bounds__(1024) void k_batch_offsets(const int64_t *cnt, int64_t m,
+                                                        int64_t *seg, int64_t *wseg,
+                                                        const int32_t *lcnt,
+                                                        const int64_t *list_off, int32_t nlist,
+                                                        int32_t G, int64_t *lstart,
+                                                        int64_t *gstart, int4 *groups) {
+  if (blockIdx.x == 0) seg_offsets(cnt, m, seg, wseg);
+  else list_offsets(lcnt, list_off, nlist, G, lstart, gstart, groups);
 }
+
 
 struct ListScanArgs {
   const float *rows;     // list rows, ld stride
@@ -1123,37 +1127,37 @@ vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
 struct ListGroups {
   int32_t *lcnt;            // pairs per list
   int64_t *lstart, *gstart;  // nlist + 1 each
-  int32_t *cursor;          // nlist + 1
+  int32_t *rank;            // each pair's rank in its list
   int32_t *pairs;
   int4 *groups;
 };
 
-// the batch's pairs grouped by list, up to G a group; the group count
-// lands in gstart[nlist]
-static void make_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes,
-                        int64_t npairs, int32_t np, int G, const ListGroups &lg) {
+// the batch's pairs grouped by list, up to G a group (the group count in
+// gstart[nlist]), and its candidate segment offsets: counts and ranks, the
+// offsets of both in one launch, then the scatter (pairs null: the offsets
+// only)
+static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes,
+                         int64_t npairs, const int64_t *cnt, int64_t nb, int64_t *dseg,
+                         int64_t *wseg, int G, const ListGroups &lg) {
   const int32_t nlist = ivf->nlist;
-  fill_i32(ctx, lg.lcnt, nlist, 0);
-  {
+  const bool lists = lg.pairs != nullptr;
+  if (lists) {
+    fill_i32(ctx, lg.lcnt, nlist, 0);
     KernelTimer t(ctx, "ivf_pair_counts");
-    k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt);
+    k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt,
+                                                                lg.rank);
     check_launch("ivf_list_pair_counts");
   }
   {
-    KernelTimer t(ctx, "ivf_list_offsets");
-    k_list_offsets<<<1, 1024, 0, ctx->stream>>>(lg.lcnt, ivf->list_off.as<int64_t>(), nlist, G,
-                                                 lg.lstart, lg.cursor, lg.gstart);
-    check_launch("ivf_list_offsets");
+    KernelTimer t(ctx, "ivf_batch_offsets");
+    k_batch_offsets<<<lists ? 2 : 1, 1024, 0, ctx->stream>>>(
+        cnt, nb, dseg, wseg, lg.lcnt, ivf->list_off.as<int64_t>(), nlist, G, lg.lstart,
+        lg.gstart, lg.groups);
+    check_launch("ivf_batch_offsets");
   }
-  {
-    KernelTimer t(ctx, "ivf_make_groups");
-    k_make_groups<<<grid1(nlist), 256, 0, ctx->stream>>>(lg.lcnt, lg.lstart, lg.gstart, nlist,
-                                                         G, lg.groups);
-    check_launch("ivf_make_groups");
-  }
-  {
+  if (lists) {
     KernelTimer t(ctx, "ivf_group_pairs");
-    k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, np, lg.cursor,
+    k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lstart, lg.rank,
                                                           lg.pairs);
     check_launch("ivf_group_pairs");
   }
@@ -1550,9 +1554,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   int64_t *loffs = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
   int64_t *lstart = loffs, *gstart = loffs + 2 * (nlist + 1);
-  int32_t *cursor = reinterpret_cast<int32_t *>(loffs + (nlist + 1));
   int32_t *lcnt = static_cast<int32_t *>(ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * nlist));
-  const ListGroups lg{lcnt, lstart, gstart, cursor, nullptr, nullptr};
+  int32_t *rank = static_cast<int32_t *>(
+      ctx->scratch_ptr("ivf.rank", sizeof(int32_t) * (npmax + 1)));
+  const ListGroups lg{lcnt, lstart, gstart, rank, nullptr, nullptr};
   int32_t *dpairs = static_cast<int32_t *>(
       ctx->scratch_ptr("ivf.pairs", sizeof(int32_t) * (npmax + 1)));
   int4 *dgroups = static_cast<int4 *>(ctx->scratch_ptr("ivf.groups", sizeof(int4) * (gmax + 1)));
@@ -1572,11 +1577,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     const int64_t ng = std::min<int64_t>(nlist, npairs) + ceil_div(npairs, G);
     // 3. segment offsets; pairs grouped by list, groups of up to G pairs
     {
-      KernelTimer t(ctx, "ivf_seg_offsets");
-      k_seg_offsets<<<1, 1024, 0, ctx->stream>>>(cnt + b0, nb, dseg, wseg);
-      check_launch("ivf_seg_offsets");
+      ListGroups g = lgp;
+      if (kind == 2) g.pairs = nullptr;  // the PQ scan walks each query's probes itself
+      batch_groups(ctx, ivf, probes + b0 * np, npairs, cnt + b0, nb, dseg, wseg, G, g);
     }
-    if (kind != 2) make_groups(ctx, ivf, probes + b0 * np, npairs, np, G, lgp);
     if (screen) {
       list_screen_batch(ctx, ivf, sqp.two, dq, b0, nb, np, k, metric, probes, pos_base, cnt,
                         dseg, wseg, lgp, cand, best);
