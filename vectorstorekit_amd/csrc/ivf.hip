@@ -97,19 +97,33 @@ __global__ void k_keys_to_tie(const uint64_t *keys, int64_t total,
     out[i] = keys[i] == VSK_KEY_NONE ? -1 : (int32_t)(uint32_t)keys[i];
 }
 
-// per query: candidate count and the position base of each probe
-__global__ void k_probe_bases(const int32_t *probes, int64_t nq, int32_t np,
-                              const int64_t *list_off, int64_t *pos_base,
-                              int64_t *cnt) {
-  int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+// per query: candidate count and the position base of each probe (the
+// exclusive prefix of its probes' list sizes); one wave per query, 64
+// probes at a time with a shuffle scan
+__global__ __launch_bounds__(256) void k_probe_bases(const int32_t *probes, int64_t nq,
+                                                     int32_t np, const int64_t *list_off,
+                                                     int64_t *pos_base, int64_t *cnt) {
+  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (q >= nq) return;
-  int64_t s = 0;
-  for (int p = 0; p < np; ++p) {
-    int32_t l = probes[q * np + p];
-    pos_base[q * np + p] = s;
-    if (l >= 0) s += list_off[l + 1] - list_off[l];
+  int64_t carry = 0;
+  for (int p0 = 0; p0 < np; p0 += 64) {
+    const int p = p0 + lane;
+    int64_t sz = 0;
+    if (p < np) {
+      const int32_t l = probes[q * np + p];
+      if (l >= 0) sz = list_off[l + 1] - list_off[l];
+    }
+    int64_t incl = sz;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    if (p < np) pos_base[q * np + p] = carry + incl - sz;
+    carry += __shfl(incl, 63);
   }
-  cnt[q] = s;
+  if (lane == 0) cnt[q] = carry;
 }
 
 // pair (q, p) -> its slot in the list-grouped pair array: its list's
@@ -1539,7 +1553,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   if (screen) list_screen_plane(ctx, ivf);
   {
     KernelTimer t(ctx, "ivf_probe_bases");
-    k_probe_bases<<<grid1(nq), 256, 0, ctx->stream>>>(
+    k_probe_bases<<<(unsigned)ceil_div(nq, 4), 256, 0, ctx->stream>>>(
         probes, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt);
     check_launch("ivf_probe_bases");
   }
