@@ -100,9 +100,18 @@ __global__ void k_keys_to_tie(const uint64_t *keys, int64_t total,
 // per query: candidate count and the position base of each probe (the
 // exclusive prefix of its probes' list sizes); one wave per query, 64
 // probes at a time with a shuffle scan
-__global__ __launch_bounds__(256) void k_probe_bases(const int32_t *probes, int64_t nq,
-                                                     int32_t np, const int64_t *list_off,
-                                                     int64_t *pos_base, int64_t *cnt) {
+// With keys, the probes are first taken from the probe's ranked keys
+// (NONE: -1) and written out.  With lcnt, the blocks also clear the nlist
+// per-list pair counters for the first batch's grouping.
+__global__ __launch_bounds__(256) void k_probe_bases(int32_t *probes, const uint64_t *keys,
+                                                     int64_t nq, int32_t np,
+                                                     const int64_t *list_off,
+                                                     int64_t *pos_base, int64_t *cnt,
+                                                     int32_t *lcnt, int32_t nlist) {
+  if (lcnt)
+    for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < nlist;
+         l += (int64_t)gridDim.x * blockDim.x)
+      lcnt[l] = 0;
   const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (q >= nq) return;
@@ -111,7 +120,14 @@ __global__ __launch_bounds__(256) void k_probe_bases(const int32_t *probes, int6
     const int p = p0 + lane;
     int64_t sz = 0;
     if (p < np) {
-      const int32_t l = probes[q * np + p];
+      int32_t l;
+      if (keys) {
+        const uint64_t key = keys[q * np + p];
+        l = key == VSK_KEY_NONE ? -1 : (int32_t)(uint32_t)key;
+        probes[q * np + p] = l;
+      } else {
+        l = probes[q * np + p];
+      }
       if (l >= 0) sz = list_off[l + 1] - list_off[l];
     }
     int64_t incl = sz;
@@ -128,8 +144,14 @@ __global__ __launch_bounds__(256) void k_probe_bases(const int32_t *probes, int6
 
 // pair (q, p) -> its slot in the list-grouped pair array: its list's
 // first slot plus its rank there
+// (lcnt, read by the offsets before this launch, is cleared here for the
+// next batch)
 __global__ void k_group_pairs(const int32_t *probes, int64_t npairs, const int64_t *lstart,
-                              const int32_t *rank, int32_t *pairs) {
+                              const int32_t *rank, int32_t *pairs, int32_t *lcnt,
+                              int32_t nlist) {
+  for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < nlist;
+       l += (int64_t)gridDim.x * blockDim.x)
+    lcnt[l] = 0;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < npairs;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int32_t l = probes[i];
@@ -758,10 +780,13 @@ static bool probe_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t nq, i
 }
 
 // top-nprobe centroids per query (ties by centroid index); qp: the
-// queries' bf16 planes when the caller has them
+// queries' bf16 planes when the caller has them.  With keys_out, the
+// ranked (distance, centroid) keys are left there and probes is not
+// written (the search turns them into ids itself).
 static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
                              int64_t nq, int32_t np, int32_t *probes,
-                             const ArgminQueries *qp = nullptr) {
+                             const ArgminQueries *qp = nullptr,
+                             uint64_t **keys_out = nullptr) {
   uint64_t *keys = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.probe_keys", sizeof(uint64_t) * nq * np));
   if (probe_screen_applies(ctx, ivf, nq, np)) {
@@ -773,6 +798,10 @@ static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
     }
   } else {
     ivf_probe_exact(ctx, ivf, dq, nq, np, keys);
+  }
+  if (keys_out) {
+    *keys_out = keys;
+    return;
   }
   KernelTimer t(ctx, "ivf_probe_ids");
   k_keys_to_tie<<<grid1(nq * np), 256, 0, ctx->stream>>>(keys, nq * np, probes);
@@ -1156,7 +1185,8 @@ static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes
   const int32_t nlist = ivf->nlist;
   const bool lists = lg.pairs != nullptr;
   if (lists) {
-    fill_i32(ctx, lg.lcnt, nlist, 0);
+    // (lcnt starts cleared: by the probe bases for the first batch, by the
+    // previous batch's scatter after it)
     KernelTimer t(ctx, "ivf_pair_counts");
     k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt,
                                                                 lg.rank);
@@ -1172,7 +1202,7 @@ static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes
   if (lists) {
     KernelTimer t(ctx, "ivf_group_pairs");
     k_group_pairs<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lstart, lg.rank,
-                                                          lg.pairs);
+                                                          lg.pairs, lg.lcnt, nlist);
     check_launch("ivf_group_pairs");
   }
 }
@@ -1506,9 +1536,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   if (screen || (!exact_all && probe_screen_applies(ctx, ivf, nq, np)))
     sqp = screen_queries2(ctx, dq, nq, ivf->d, ld);
 
-  // 1. probes
+  // 1. probes (ranked keys, turned into ids by the probe bases below)
   int32_t *probes = static_cast<int32_t *>(
       ctx->scratch_ptr("ivf.probes", sizeof(int32_t) * nq * np));
+  uint64_t *pkeys = nullptr;
   if (exact_all) {
     // .exact with more lists than a selection holds: every list, in index
     // order (the stable sort's order when all lists are kept is by
@@ -1520,7 +1551,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     VSK_HIP(hipMemcpyAsync(probes, all.data(), 4 * all.size(),
                            hipMemcpyHostToDevice, ctx->stream));
   } else {
-    ivf_probe_device(ctx, ivf, dq, nq, np, probes, sqp.one.qh ? &sqp.one : nullptr);
+    ivf_probe_device(ctx, ivf, dq, nq, np, probes, sqp.one.qh ? &sqp.one : nullptr, &pkeys);
   }
   // 2. candidate counts and probe position bases
   int64_t *pos_base = static_cast<int64_t *>(
@@ -1551,10 +1582,14 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   // the screen's groups are up to kScreenQ queries
   const int G = screen ? kScreenQ : QG;
   if (screen) list_screen_plane(ctx, ivf);
+  // the per-list pair counters of the grouping, cleared by the probe bases
+  int32_t *lcnt = kind != 2 ? static_cast<int32_t *>(
+                                  ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * ivf->nlist))
+                            : nullptr;
   {
     KernelTimer t(ctx, "ivf_probe_bases");
     k_probe_bases<<<(unsigned)ceil_div(nq, 4), 256, 0, ctx->stream>>>(
-        probes, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt);
+        probes, pkeys, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt, lcnt, ivf->nlist);
     check_launch("ivf_probe_bases");
   }
   const int64_t nbmax = qb, npmax = nbmax * np;
@@ -1568,7 +1603,6 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   int64_t *loffs = static_cast<int64_t *>(
       ctx->scratch_ptr("ivf.loffs", sizeof(int64_t) * 3 * (nlist + 1)));
   int64_t *lstart = loffs, *gstart = loffs + 2 * (nlist + 1);
-  int32_t *lcnt = static_cast<int32_t *>(ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * nlist));
   int32_t *rank = static_cast<int32_t *>(
       ctx->scratch_ptr("ivf.rank", sizeof(int32_t) * (npmax + 1)));
   const ListGroups lg{lcnt, lstart, gstart, rank, nullptr, nullptr};
