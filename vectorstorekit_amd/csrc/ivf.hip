@@ -588,7 +588,9 @@ __global__ __launch_bounds__(512) void k_list_screen(
   __shared__ __attribute__((aligned(16))) uint16_t s_ql[PL == 2 ? kScreenQ * QLP : 8];
   if constexpr (PL == 2) {
     constexpr int CH = 4 * KS;  // 16-byte chunks a row
-    for (int e = threadIdx.x; e < kScreenQ * CH; e += 512) {
+    // the rows of the group's query tiles (slots past them are never read)
+    const int nrow = (npair + 15) & ~15;
+    for (int e = threadIdx.x; e < nrow * CH; e += 512) {
       const int j = e / CH, c = e - j * CH;
       const int64_t qo = query(j) * ldb + 8 * c;
       *reinterpret_cast<bf8v *>(s_qh + j * QLP + 8 * c) =
