@@ -75,15 +75,18 @@ def _screen_ctx():
                                    (37, 5000, 33, 150, 5, 7, "euclideanSquared"),
                                    (40, 12_000, 160, 90, 40, 100, "euclidean"),
                                    (24, 9000, 256, 70, 6, 64, "euclideanSquared"),
-                                   (16, 3000, 24, 40, 16, 20, "euclidean")])
+                                   (16, 3000, 24, 40, 16, 20, "euclidean"),
+                                   (32, 15_000, 64, 30, 12, 300, "euclidean")])
 def test_ivf_screen_bit_exact(shape):
     """The list scan through the bf16 screen (forced at these sizes): query
     groups of up to 64 per list, the screened keys within the bound's margin
     of the k-th, their exact rescore.  Plane widths of 2, 4, 6 and 8 k-steps,
-    both euclidean metrics, k above 64, every list probed; then rows added
-    (the plane is made again), among them a block of 1,100 identical rows,
-    more than the margin's slots hold, so the queries next to it have their
-    whole candidate set rescored.  Bit-exact against the oracle."""
+    both euclidean metrics, k above 64 and above 256 (where the margin,
+    rescore and selections are launches of their own rather than one fused
+    tail), every list probed; then rows added (the plane is made again),
+    among them a block of identical rows, more than the margin's slots hold
+    (1,024, or 4k above k = 256), so the queries next to it have their whole
+    candidate set rescored.  Bit-exact against the oracle."""
     ncent, n, d, nq, nprobe, k, metric = shape
     print(f"ivf screen ncent={ncent} n={n} d={d} nq={nq} nprobe={nprobe} k={k} {metric}",
           flush=True)
@@ -103,20 +106,22 @@ def test_ivf_screen_bit_exact(shape):
     # rows added after the plane was made, among them 1,100 copies of one
     # row next to the first query
     rng = np.random.default_rng(n)
-    dup = np.repeat(q[:1] + 0.01 * rng.standard_normal((1, d)).astype(np.float32), 1100, 0)
+    ndup = max(1100, 4 * k + 100)
+    dup = np.repeat(q[:1] + 0.01 * rng.standard_normal((1, d)).astype(np.float32), ndup, 0)
     extra = np.concatenate([x[:1000] + 0.1, dup]).astype(np.float32)
     eids = np.arange(n, n + len(extra), dtype=np.int64) * 3 + 7
     idx.insert(extra, eids)
     x2 = np.concatenate([x, extra])
     ids2 = np.concatenate([ids, eids])
     lists2 = O.ivf_assign(x2, c)
-    before = sctx.profile_stats().get("ivf_screen_redo", (0, 0.0, 0.0))[2]
+    fallback = "ivf_screen_tail" if k <= 256 else "ivf_screen_redo"
+    before = sctx.profile_stats().get(fallback, (0, 0.0, 0.0))[2]
     gd, gi = idx.search(q, k, metric=metric)
     od, oi = O.ivf_search(q, x2, ids2, lists2, c, nprobe, k, squared=sq)
     np.testing.assert_array_equal(gi, oi)
     np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
     # the fallback's work count is the number of queries that overflowed
-    assert sctx.profile_stats()["ivf_screen_redo"][2] > before, "no query overflowed"
+    assert sctx.profile_stats()[fallback][2] > before, "no query overflowed"
     sctx.close()
 
 
@@ -136,7 +141,7 @@ def test_ivf_probe_screen_overflow():
     idx = _index(sctx, c, x, None, nprobe)
     np.testing.assert_array_equal(idx.probe(q, nprobe), O.ivf_probe(q, c, nprobe))
     # the fallback's work count is the number of queries that overflowed
-    assert sctx.profile_stats()["ivf_probe_redo"][2] > 0
+    assert sctx.profile_stats()["ivf_probe_tail"][2] > 0
     lists = O.ivf_assign(x, c)
     gd, gi = idx.search(q, k)
     od, oi = O.ivf_search(q, x, np.arange(n, dtype=np.int64), lists, c, nprobe, k)

@@ -140,6 +140,30 @@ struct MarginArgs {
 };
 void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a);
 
+// A screen's whole tail for a query in one workgroup: the margin gather of
+// m (at most m.cap <= 1024 keys, kept in LDS), their exact distances -- the
+// reference's sequential fp32 sum of (q - x)^2 over ld columns, its square
+// root unless squared -- and the top m.k of those, sorted, into best_out.
+// A query with more than m.cap keys in its margin has the exact key of
+// every candidate written to all (at seg_off[q], or q * all_n with all_n
+// candidates) and selected from there instead.  Rows: with list_off, a
+// candidate's position maps to its probe slot (pos_base, probes: np a
+// query) and row as in the IVF candidate segments; without, the position
+// is the row.  m.out, m.nout, m.ok and m.bad are not used.
+struct ScreenTailArgs {
+  MarginArgs m;
+  const float *rows = nullptr, *Q = nullptr;
+  int32_t ld = 0, squared = 0;
+  const int64_t *list_off = nullptr, *pos_base = nullptr;
+  const int32_t *probes = nullptr;
+  int32_t np = 0;
+  uint64_t *all = nullptr;
+  const int64_t *seg_off = nullptr;
+  int64_t all_n = 0;
+  uint64_t *best_out = nullptr;
+};
+void launch_screen_tail(vsk_ctx *ctx, const ScreenTailArgs &a, const char *name);
+
 // Exact top k per query of 32-bit words keyed (word, index), sorted
 // ascending into best_out[q * k ...] (NONE past the words): query q's words
 // are words[wseg[q] + i], i < cnt[q] (wseg a multiple of 4); only queries

@@ -1215,20 +1215,20 @@ static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes
 // (at most cap per query), their exact distances and the top k of those --
 // or, for a query with more than cap keys in the margin, the top k of
 // every candidate's exact distance (in its segment of cand, seg_off) --
-// into best[b0 * k ...].  No read-back: the fallback's launches find no
-// active query when none overflows.
+// into best[b0 * k ...].  Up to k = 256 one launch after the screen does
+// all of that per query (k_screen_tail); above, the margin, rescore and
+// selections are launches of their own, the fallback's finding no active
+// query when none overflows.  No read-back either way.
 static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQueries &qp,
                               const float *dq, int64_t b0, int64_t nb, int32_t np, int32_t k,
                               int32_t metric, const int32_t *probes, const int64_t *pos_base,
                               const int64_t *cnt, const int64_t *dseg, const int64_t *wseg,
-                              const ListGroups &lg, uint64_t *cand, uint64_t *best) {
+                              const ListGroups &lg, uint32_t *words, uint64_t *cand,
+                              uint64_t *best) {
   const int32_t ld = ivf->ld, ldb = ivf->xldb, nlist = ivf->nlist;
   const int64_t npairs = nb * np;
   const int32_t *bprobes = probes + b0 * np;
   const int64_t *bpos = pos_base + b0 * np;
-  // the screened words share cand's memory; the fallback's exact keys
-  // overwrite them after the margin gather has read them
-  uint32_t *words = reinterpret_cast<uint32_t *>(cand);
   {
     KernelTimer t(ctx, "ivf_list_screen");
     t.device_work(dseg + nb);
@@ -1248,7 +1248,48 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
 #undef VSK_LS
     check_launch("ivf_list_screen");
   }
-  const int32_t cap = std::max<int32_t>(1024, 4 * k);
+  const int32_t sq = metric == VSK_METRIC_L2SQ ? 1 : 0;
+  const float *rows = ivf->rows.as<float>();
+  const int64_t *loff = ivf->list_off.as<int64_t>();
+  // the overflowing queries' count as the fallback's work (profiling)
+  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.nbad", 8)) : nullptr;
+  if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
+  MarginArgs ma;
+  ma.nq = nb;
+  ma.k = k;
+  ma.words = words;
+  ma.wseg = wseg;
+  ma.cnt = cnt + b0;
+  ma.qnh = qp.qnh + b0;
+  ma.qnr = qp.qnr + b0;
+  ma.xh = ivf->xh_max;
+  ma.xr = ivf->xr_max;
+  ma.d = ivf->d;
+  ma.nprod = qp.nprod;
+  ma.metric = metric;
+  ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
+  if (k <= 256) {
+    // the margin, its exact rescore and the selection in one launch
+    ScreenTailArgs ta;
+    ta.m = ma;
+    ta.m.cap = 1024;
+    ta.rows = rows;
+    ta.Q = dq + b0 * ld;
+    ta.ld = ld;
+    ta.squared = sq;
+    ta.list_off = loff;
+    ta.pos_base = bpos;
+    ta.probes = bprobes;
+    ta.np = np;
+    ta.all = cand;
+    ta.seg_off = dseg;
+    ta.best_out = best + b0 * k;
+    KernelTimer t(ctx, "ivf_screen_tail");
+    if (nbad) t.device_work(nbad);
+    launch_screen_tail(ctx, ta, "screen_tail");
+    return;
+  }
+  const int32_t cap = 4 * k;
   uint64_t *kept = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.kept", sizeof(uint64_t) * nb * cap));
   uint64_t *exact = static_cast<uint64_t *>(
@@ -1256,34 +1297,12 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
   uint8_t *ok = static_cast<uint8_t *>(ctx->scratch_ptr("ivf.ok", 2 * (size_t)nb));
   uint8_t *bad = ok + nb;
   int32_t *nout = static_cast<int32_t *>(ctx->scratch_ptr("ivf.nout", 4 * (size_t)nb + 8));
-  // the overflowing queries' count as the fallback's work (profiling)
-  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.nbad", 8)) : nullptr;
-  if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
-  {
-    MarginArgs ma;
-    ma.nq = nb;
-    ma.k = k;
-    ma.words = words;
-    ma.wseg = wseg;
-    ma.cnt = cnt + b0;
-    ma.qnh = qp.qnh + b0;
-    ma.qnr = qp.qnr + b0;
-    ma.xh = ivf->xh_max;
-    ma.xr = ivf->xr_max;
-    ma.d = ivf->d;
-    ma.nprod = qp.nprod;
-    ma.metric = metric;
-    ma.out = kept;
-    ma.cap = cap;
-    ma.nout = nout;
-    ma.ok = ok;
-    ma.bad = bad;
-    ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
-    launch_screen_margin(ctx, ma);
-  }
-  const int32_t sq = metric == VSK_METRIC_L2SQ ? 1 : 0;
-  const float *rows = ivf->rows.as<float>();
-  const int64_t *loff = ivf->list_off.as<int64_t>();
+  ma.out = kept;
+  ma.cap = cap;
+  ma.nout = nout;
+  ma.ok = ok;
+  ma.bad = bad;
+  launch_screen_margin(ctx, ma);
   RescoreArgs ra{};
   ra.rows = rows;
   ra.ld = ld;
@@ -1403,13 +1422,30 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
     ma.d = ivf->d;
     ma.nprod = qp.nprod;
     ma.metric = VSK_METRIC_L2;
+    if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
+    ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
+    if (np <= 256) {
+      // the margin, its exact rescore and the selection in one launch
+      ScreenTailArgs ta;
+      ta.m = ma;
+      ta.m.cap = 1024;
+      ta.rows = cdb->x.as<float>();
+      ta.Q = dq + b0 * ld;
+      ta.ld = ld;
+      ta.squared = 0;
+      ta.all = all;
+      ta.all_n = nlist;
+      ta.best_out = keys + b0 * np;
+      KernelTimer t(ctx, "ivf_probe_tail");
+      if (nbad) t.device_work(nbad);
+      launch_screen_tail(ctx, ta, "probe_tail");
+      continue;
+    }
     ma.out = kept;
     ma.cap = cap;
     ma.nout = nout;
     ma.ok = ok;
     ma.bad = bad;
-    if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
-    ma.nbad = reinterpret_cast<unsigned long long *>(nbad);
     launch_screen_margin(ctx, ma);
     RescoreArgs ra{};
     ra.rows = cdb->x.as<float>();
@@ -1620,6 +1656,11 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       "ivf.cand", std::max(sizeof(uint64_t) * (nbmax * ubound + 1),
                            sizeof(uint32_t) * (nbmax * (ubound + 3) + 4))));
   const int64_t *loff = ivf->list_off.as<int64_t>();
+  // the screen's words in memory of their own: the fused tail of one query
+  // writes exact keys into cand while other queries' words are still read
+  uint32_t *swords = screen ? static_cast<uint32_t *>(ctx->scratch_ptr(
+                                  "ivf.words", sizeof(uint32_t) * (nbmax * (ubound + 3) + 4)))
+                            : nullptr;
 
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
@@ -1633,7 +1674,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     }
     if (screen) {
       list_screen_batch(ctx, ivf, sqp.two, dq, b0, nb, np, k, metric, probes, pos_base, cnt,
-                        dseg, wseg, lgp, cand, best);
+                        dseg, wseg, lgp, swords, cand, best);
       continue;
     }
     const int64_t *ngroups = gstart + nlist;

@@ -756,6 +756,155 @@ void launch_screen_margin(vsk_ctx *ctx, const MarginArgs &a) {
   check_launch("screen_margin");
 }
 
+// the screen tail (declared with ScreenTailArgs)
+__device__ inline float tail_exact(const float *x, const float *sq, int32_t ld, int32_t squared) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+  for (int c0 = 0; c0 < ld; c0 += 32) {
+    const int m = ld - c0 < 32 ? (ld - c0) >> 2 : 8;  // ld is a multiple of 4
+    float4 xv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + c0 + 4 * u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < m) {
+        const float4 qv = *reinterpret_cast<const float4 *>(sq + c0 + 4 * u);
+        float t;
+        t = qv.x - xv[u].x;
+        acc = acc + t * t;
+        t = qv.y - xv[u].y;
+        acc = acc + t * t;
+        t = qv.z - xv[u].z;
+        acc = acc + t * t;
+        t = qv.w - xv[u].w;
+        acc = acc + t * t;
+      }
+  }
+  return squared ? acc : sqrtf(acc);
+}
+
+__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p) {
+  if (!t.list_off) return p;
+  const int64_t *pb = t.pos_base + q * t.np;
+  const int32_t *pr = t.probes + q * t.np;
+  int lo = 0, hi = t.np;  // the last slot whose base is at or below p
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (pb[mid] <= p) lo = mid;
+    else hi = mid;
+  }
+  return t.list_off[pr[lo]] + (p - pb[lo]);
+}
+
+template <int REG>
+__global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
+  const MarginArgs &a = t.m;
+  const int64_t q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  WordList<REG> L;
+  L.load(a.words + (a.wseg ? a.wseg[q] : q * a.wstride), a.cnt ? a.cnt[q] : a.wn);
+  auto each = [&](auto &&f) { L.each(f); };
+  __shared__ KthShared sh;
+  __shared__ SelShared ssel;
+  __shared__ uint64_t keys[VSK_MAX_K];
+  __shared__ __attribute__((aligned(16))) float s_q[256];
+  __shared__ int s_cnt;
+  const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
+  const uint32_t kth = word_kth_fast(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
+  uint32_t lim_word = kWordNone - 1u;  // every key when there are fewer than k
+  if (kth != kWordNone) {
+    const double ak = vsk_ord2f(kth);
+    const double lim = a.metric == VSK_METRIC_L2 ? (ak + eps) * (1.0 + 0x1p-20) + eps
+                                                 : ak + 2.0 * eps;
+    lim_word = vsk_f2ord(f_down(lim));
+  }
+  if (tid == 0) s_cnt = 0;
+  for (int c = tid; c < t.ld; c += SEL_THREADS) s_q[c] = t.Q[q * t.ld + c];
+  __syncthreads();
+  each([&](uint32_t x, uint32_t i) {
+    if (x <= lim_word) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < a.cap) keys[slot] = ((uint64_t)x << 32) | i;
+    }
+  });
+  __syncthreads();
+  const int c = s_cnt;
+  const int32_t k = a.k;
+  uint64_t *out = t.best_out + q * (int64_t)k;
+  if (c <= a.cap) {
+    for (int i = tid; i < c; i += SEL_THREADS) {
+      const int64_t p = (int64_t)(uint32_t)keys[i];
+      const float dist = tail_exact(t.rows + tail_row(t, q, p) * t.ld, s_q, t.ld, t.squared);
+      keys[i] = vsk_key(dist, (uint32_t)p);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      for (int i = c + lane; i < k; i += 64) out[i] = VSK_KEY_NONE;
+      auto finish = [&](auto rtag) {
+        constexpr int R = decltype(rtag)::value;
+        uint64_t r[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          const int e = lane * R + i;
+          r[i] = e < c ? keys[e] : VSK_KEY_NONE;
+        }
+        wave_sort_u64<R>(r);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          const int e = lane * R + i;
+          if (e < k && e < c) out[e] = r[i];
+        }
+      };
+      if (c <= 64) finish(std::integral_constant<int, 1>{});
+      else if (c <= 128) finish(std::integral_constant<int, 2>{});
+      else if (c <= 256) finish(std::integral_constant<int, 4>{});
+      else if (c <= 512) finish(std::integral_constant<int, 8>{});
+      else finish(std::integral_constant<int, 16>{});
+    }
+    return;
+  }
+  // more keys in the margin than the slots: every candidate's exact key,
+  // then a radix selection over them
+  if (tid == 0 && a.nbad) atomicAdd(a.nbad, 1ull);
+  const int64_t base = t.seg_off ? t.seg_off[q] : q * t.all_n;
+  const int64_t n = t.seg_off ? t.seg_off[q + 1] - base : t.all_n;
+  uint64_t *A = t.all + base;
+  for (int64_t i = tid; i < n; i += SEL_THREADS)
+    A[i] = vsk_key(tail_exact(t.rows + tail_row(t, q, i) * t.ld, s_q, t.ld, t.squared),
+                   (uint32_t)i);
+  __threadfence_block();
+  __syncthreads();
+  auto each_key = [&](auto &&f) {
+    for (int64_t i = tid; i < n; i += SEL_THREADS) f(A[i]);
+  };
+  uint64_t T, hi;
+  bool take_all;
+  radix_threshold(each_key, k, ssel, T, take_all, hi);
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  each_key([&](uint64_t key) {
+    if (key != VSK_KEY_NONE && (take_all || key <= T)) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < VSK_MAX_K) keys[slot] = key;
+    }
+  });
+  __syncthreads();
+  int m = s_cnt;
+  if (m > k) m = k;
+  block_sort(keys, m);
+  for (int i = tid; i < k; i += SEL_THREADS) out[i] = i < m ? keys[i] : VSK_KEY_NONE;
+}
+
+void launch_screen_tail(vsk_ctx *ctx, const ScreenTailArgs &a, const char *name) {
+  if (a.m.nq <= 0) return;
+  if (a.m.k < 1 || a.m.k > VSK_MAX_K || a.m.cap > VSK_MAX_K || a.ld > 256)
+    fail(VSK_ERR_INVALID_ARGUMENT, "screen tail: k, cap (<= 1024) or ld (<= 256) out of range");
+  KernelTimer t(ctx, name);
+  k_screen_tail<32><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  check_launch(name);
+}
+
 // Exact top k by (word, index), sorted (declared with WordSelectArgs):
 // word_kth finds the k-th smallest word V; every word below V is kept and,
 // of the words equal to V, those with the smallest indices -- a second
