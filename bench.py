@@ -646,8 +646,12 @@ def setup(c, a, ctx, dev):
 
 # ----------------------------------------------------------------- roofline
 
-def roofline(spec, stats):
-    """Dominant kernel's roofline from the library's event timers."""
+def roofline(spec, stats, full=None):
+    """Dominant kernel's roofline from the library's event timers: its
+    launches and time from ``stats`` (the timed steps, where only the
+    candidate kernels carry timers), its work (pairs) per launch from
+    ``full`` (further steps of the same workload under full profiling, which
+    reads the device-side work counts back) when given."""
     d = spec["d"]
     best = None
     for key, label, kind in spec["kernels"]:
@@ -658,6 +662,8 @@ def roofline(spec, stats):
         return None
     key, label, kind = best
     launches, ms, pairs = stats[key]
+    if full is not None and key in full and full[key][0]:
+        pairs = full[key][2] / full[key][0] * launches
     sec = ms * 1e-3
     r = {"kernel": f"{key} ({label})", "launches": launches,
          "avg_launch_ms": round(ms / launches, 4) if launches else None,
@@ -837,6 +843,9 @@ def measure(c, a, ctx, dev):
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
+    # the timed steps carry HIP-event timers on the roofline's candidate
+    # kernels only (two events a launch, no work counts read back)
+    ctx.profile_only([key for key, _, _ in spec["kernels"]])
     ctx.profile(True)
     ctx.profile_reset()
     torch.cuda.synchronize()
@@ -846,8 +855,17 @@ def measure(c, a, ctx, dev):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     stats = ctx.profile_stats()
-    ctx.profile(False)
     progress(f"{c}: {a.steps} steps in {el * 1e3:.1f} ms")
+    # the per-kernel breakdown and the work counts: further steps with every
+    # kernel timed (not part of the value)
+    ctx.profile_only(None)
+    ctx.profile_reset()
+    breakdown_steps = max(1, min(a.steps, 5))
+    for _ in range(breakdown_steps):
+        step()
+    torch.cuda.synchronize()
+    full = ctx.profile_stats()
+    ctx.profile(False)
 
     nq, n = spec["nq"], spec["n"]
     qps = spec.get("units_per_step", nq) * a.steps / el
@@ -866,10 +884,11 @@ def measure(c, a, ctx, dev):
         "data": spec["data"],
         "config": dict({"workload": spec["workload"]}, **spec["config"]),
         "distances_per_s": nq * n * a.steps / el,
-        "roofline": roofline(spec, stats),
+        "roofline": roofline(spec, stats, full),
         "setup_s": round(build_s, 2),
+        "kernels_steps": breakdown_steps,
         "kernels": {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
-                    for k, v in stats.items()},
+                    for k, v in full.items()},
     }
     if host_step is not None and not a.no_host_io:
         # queries read from and results written to pageable host memory:

@@ -135,6 +135,13 @@ vsk_status vsk_last_screen_redo(const vsk_ctx *ctx, int32_t tier, int64_t *out,
                                 int64_t cap, int64_t *count);
 /* Per-kernel event timing (off by default). */
 vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on);
+/* Restricts the timing to the timers named in names (comma-separated;
+ * NULL or "" times every kernel again), so that a run can time its main
+ * kernel with two events a launch and nothing else.  While a restriction
+ * holds, work counts that live on the device (candidate totals, fallback
+ * counts) are not read back: those stats report 0 work.  A profiling
+ * control of this library with no counterpart in the reference. */
+vsk_status vsk_profile_only(vsk_ctx *ctx, const char *names);
 vsk_status vsk_profile_reset(vsk_ctx *ctx);
 int32_t vsk_profile_count(const vsk_ctx *ctx);
 vsk_status vsk_profile_get(const vsk_ctx *ctx, int32_t i, vsk_kernel_stat *out);

@@ -270,6 +270,28 @@ def test_small_problem_exact_scan(ctx, metric):
     np.testing.assert_array_equal(gd, od)
 
 
+def test_profile_only_times_the_named_kernels(ctx):
+    """vsk_profile_only: with a restriction only the named timers record
+    (one launch a call for the small exact scan), results unchanged; the
+    restriction lifted, every kernel is timed again."""
+    x, q = _data(7, 10_000, 100, 128)
+    db = VectorDatabase(ctx, x)
+    ctx.profile(True)
+    ctx.profile_only(["flat_valu_dense"])
+    ctx.profile_reset()
+    gd, gi = db.search(q, 10, METRIC_L2)
+    stats = ctx.profile_stats()
+    assert list(stats) == ["flat_valu_dense"] and stats["flat_valu_dense"][0] == 1
+    ctx.profile_only(None)
+    ctx.profile_reset()
+    gd2, gi2 = db.search(q, 10, METRIC_L2)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    assert "flat_valu_dense" in stats and "flat_select" in stats
+    np.testing.assert_array_equal(gi, gi2)
+    np.testing.assert_array_equal(gd, gd2)
+
+
 def test_upload_read_roundtrip_padded_chunked(ctx):
     """Host rows with a pitch that needs padding (d=129 -> 132) and more than
     one 64 MB staging chunk: upload and read-back are exact, from host and

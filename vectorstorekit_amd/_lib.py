@@ -87,6 +87,7 @@ SIGNATURES = {
     "vsk_last_kernel_ms": (c_float, [P]),
     "vsk_last_screen_redo": (c_int32, [P, c_int32, P, c_int64, P]),
     "vsk_profile_enable": (c_int32, [P, c_int32]),
+    "vsk_profile_only": (c_int32, [P, c_char_p]),
     "vsk_profile_reset": (c_int32, [P]),
     "vsk_profile_count": (c_int32, [P]),
     "vsk_profile_get": (c_int32, [P, c_int32, POINTER(vsk_kernel_stat)]),

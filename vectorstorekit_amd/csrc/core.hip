@@ -70,7 +70,7 @@ void CallScope::finish() {
 
 KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items, hipStream_t s)
     : ctx(c), work(work_items), stream(s ? s : c->stream) {
-  if (!ctx->profile) return;
+  if (!ctx->timed(name)) return;
   auto it = ctx->stat_index.find(name);
   if (it == ctx->stat_index.end()) {
     vsk_kernel_stat s;
@@ -80,15 +80,19 @@ KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items, hipStr
     it = ctx->stat_index.emplace(name, (int)ctx->stats.size() - 1).first;
   }
   stat = it->second;
-  a = ctx->take_event();
+  a = ctx->take_timer_event();
   VSK_HIP(hipEventRecord(a, stream));
 }
 KernelTimer::~KernelTimer() {
   if (stat < 0) return;
-  hipEvent_t b = ctx->take_event();
-  if (hipEventRecord(b, stream) != hipSuccess) return;
+  hipEvent_t b = ctx->take_timer_event();
+  if (hipEventRecord(b, stream) != hipSuccess) {
+    ctx->timer_pool.push_back(a);
+    ctx->timer_pool.push_back(b);
+    return;
+  }
   int slot = -1;
-  if (work_dev) {
+  if (work_dev && ctx->count_work()) {
     if (!ctx->work_pinned &&
         hipHostMalloc(reinterpret_cast<void **>(&ctx->work_pinned),
                       sizeof(int64_t) * vsk_ctx::kWorkSlots, hipHostMallocDefault) != hipSuccess)
@@ -366,6 +370,16 @@ hipEvent_t vsk_ctx::take_event() {
   VSK_HIP(hipEventCreate(&e));
   return e;
 }
+hipEvent_t vsk_ctx::take_timer_event() {
+  if (!timer_pool.empty()) {
+    hipEvent_t e = timer_pool.back();
+    timer_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  VSK_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+  return e;
+}
 void vsk_ctx::resolve_pending() {
   for (auto &p : pending) {
     float ms = 0.f;
@@ -374,8 +388,8 @@ void vsk_ctx::resolve_pending() {
       stats[p.stat].total_ms += ms;
       stats[p.stat].work += p.work_slot >= 0 ? (double)work_pinned[p.work_slot] : p.work;
     }
-    event_pool.push_back(p.a);
-    event_pool.push_back(p.b);
+    timer_pool.push_back(p.a);
+    timer_pool.push_back(p.b);
   }
   pending.clear();
   work_used = 0;
@@ -430,6 +444,7 @@ vsk_status vsk_destroy(vsk_ctx *ctx) {
   if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);
   ctx->resolve_pending();
   for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
+  for (auto e : ctx->timer_pool) (void)hipEventDestroy(e);
   if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
   if (ctx->pinned) (void)hipHostFree(ctx->pinned);
   if (ctx->work_pinned) (void)hipHostFree(ctx->work_pinned);
@@ -480,6 +495,22 @@ vsk_status vsk_device_info(vsk_ctx *ctx, vsk_caps *caps) {
 vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on) {
   if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
   ctx->profile = on != 0;
+  return VSK_OK;
+}
+vsk_status vsk_profile_only(vsk_ctx *ctx, const char *names) {
+  if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
+  ctx->profile_only.clear();
+  if (!names) return VSK_OK;
+  std::string cur;
+  for (const char *p = names;; ++p) {
+    if (*p == ',' || *p == 0) {
+      if (!cur.empty()) ctx->profile_only.push_back(cur);
+      cur.clear();
+      if (*p == 0) break;
+    } else {
+      cur.push_back(*p);
+    }
+  }
   return VSK_OK;
 }
 vsk_status vsk_profile_reset(vsk_ctx *ctx) {

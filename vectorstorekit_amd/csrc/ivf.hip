@@ -1252,7 +1252,8 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
   const float *rows = ivf->rows.as<float>();
   const int64_t *loff = ivf->list_off.as<int64_t>();
   // the overflowing queries' count as the fallback's work (profiling)
-  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.nbad", 8)) : nullptr;
+  int64_t *nbad =
+      ctx->count_work() ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.nbad", 8)) : nullptr;
   if (nbad) fill_i32(ctx, reinterpret_cast<int32_t *>(nbad), 2, 0);
   MarginArgs ma;
   ma.nq = nb;
@@ -1387,7 +1388,8 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
   uint8_t *bad = ok + qb;
   int32_t *nout = static_cast<int32_t *>(ctx->scratch_ptr("ivf.pnout", 4 * (size_t)qb));
   // the overflowing queries' count as the fallback's work (profiling)
-  int64_t *nbad = ctx->profile ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.pnbad", 8)) : nullptr;
+  int64_t *nbad =
+      ctx->count_work() ? static_cast<int64_t *>(ctx->scratch_ptr("ivf.pnbad", 8)) : nullptr;
   const int32_t nchunks = (int32_t)ceil_div(nlist, 256);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;

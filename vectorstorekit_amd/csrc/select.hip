@@ -784,6 +784,57 @@ __device__ inline float tail_exact(const float *x, const float *sq, int32_t ld, 
   return squared ? acc : sqrtf(acc);
 }
 
+__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p);
+
+// The exact keys of keys[0 .. c) in place, L lanes a key (L a power of two,
+// 32 L >= ld): lane s of a group loads columns [32 s, 32 s + 32) of the
+// row, so every load of a round is in flight at once, and the sequential
+// sum passes from lane to lane -- lane s adds its 32 products to what lane
+// s - 1 handed on -- which keeps the order of the one-thread sum.
+__device__ void tail_rescore(uint64_t *keys, int c, const ScreenTailArgs &t, int64_t q,
+                             const float *sq) {
+#pragma clang fp contract(off)
+  const int L = t.ld <= 32 ? 1 : t.ld <= 64 ? 2 : t.ld <= 128 ? 4 : 8;
+  const int tid = threadIdx.x, s = tid & (L - 1);
+  const int c0 = 32 * s;
+  const int m = t.ld - c0 >= 32 ? 8 : (t.ld > c0 ? (t.ld - c0) >> 2 : 0);  // ld: multiple of 4
+  for (int b = 0; b < c; b += SEL_THREADS / L) {  // uniform
+    const int i = b + tid / L;
+    int64_t p = 0;
+    float4 xv[8];
+    if (i < c) {
+      p = (int64_t)(uint32_t)keys[i];
+      const float *x = t.rows + tail_row(t, q, p) * t.ld + c0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + 4 * u);
+    }
+    float acc = 0.f;
+    for (int step = 0; step < L; ++step) {  // uniform
+      const float in = __shfl_up(acc, 1, L);
+      if (s == step) {
+        float a = step == 0 ? 0.f : in;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u < m) {
+            const float4 qv = *reinterpret_cast<const float4 *>(sq + c0 + 4 * u);
+            float d;
+            d = qv.x - xv[u].x;
+            a = a + d * d;
+            d = qv.y - xv[u].y;
+            a = a + d * d;
+            d = qv.z - xv[u].z;
+            a = a + d * d;
+            d = qv.w - xv[u].w;
+            a = a + d * d;
+          }
+        acc = a;
+      }
+    }
+    if (i < c && s == L - 1) keys[i] = vsk_key(t.squared ? acc : sqrtf(acc), (uint32_t)p);
+  }
+}
+
 __device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p) {
   if (!t.list_off) return p;
   const int64_t *pb = t.pos_base + q * t.np;
@@ -833,11 +884,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const int32_t k = a.k;
   uint64_t *out = t.best_out + q * (int64_t)k;
   if (c <= a.cap) {
-    for (int i = tid; i < c; i += SEL_THREADS) {
-      const int64_t p = (int64_t)(uint32_t)keys[i];
-      const float dist = tail_exact(t.rows + tail_row(t, q, p) * t.ld, s_q, t.ld, t.squared);
-      keys[i] = vsk_key(dist, (uint32_t)p);
-    }
+    tail_rescore(keys, c, t, q, s_q);
     __syncthreads();
     if (tid < 64) {
       for (int i = c + lane; i < k; i += 64) out[i] = VSK_KEY_NONE;

@@ -90,6 +90,18 @@ struct vsk_ctx {
 
   // profiling
   bool profile = false;
+  // when not empty, only the timers of these names record (and no work
+  // count is read back from the device)
+  std::vector<std::string> profile_only;
+  bool timed(const char *name) const {
+    if (!profile) return false;
+    if (profile_only.empty()) return true;
+    for (const auto &s : profile_only)
+      if (s == name) return true;
+    return false;
+  }
+  // device-side work counters are kept only under full profiling
+  bool count_work() const { return profile && profile_only.empty(); }
   struct Pending {
     int stat;
     hipEvent_t a, b;
@@ -102,9 +114,14 @@ struct vsk_ctx {
   int work_used = 0;
   std::vector<Pending> pending;
   std::vector<hipEvent_t> event_pool;
+  // the kernel timers' events: timing only, recorded without the system-scope
+  // fence (no cache write-back and invalidation between the timed kernels);
+  // read after the call's stream synchronisation
+  std::vector<hipEvent_t> timer_pool;
   std::vector<vsk_kernel_stat> stats;
   std::map<std::string, int> stat_index;
   hipEvent_t take_event();
+  hipEvent_t take_timer_event();
   void resolve_pending();
 };
 

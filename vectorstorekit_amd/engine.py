@@ -133,6 +133,13 @@ class Context:
     def profile(self, on: bool = True):
         self.check(self.lib.vsk_profile_enable(self.handle, 1 if on else 0))
 
+    def profile_only(self, names=None):
+        """Time only the timers named in ``names`` (an iterable of names;
+        None or empty: all of them again).  Device-side work counts are not
+        read back meanwhile (their stats report 0 work)."""
+        arg = ",".join(names).encode() if names else None
+        self.check(self.lib.vsk_profile_only(self.handle, arg))
+
     def profile_reset(self):
         self.check(self.lib.vsk_profile_reset(self.handle))
 
