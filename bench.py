@@ -55,6 +55,9 @@ PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, datasheet
 PEAK_INT8_MFMA_TOPS = 5000.0  # MI355X dense int8 matrix, datasheet
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, datasheet
 PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
+# the same ceilings re-measured on the device at start (vsk_measure_peaks):
+# each roofline also reports its fraction of these
+MEASURED_PEAKS = {}
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
                  "c3train": (2, 1), "c4bin": (5, 1), "c3sq8": (5, 1), "c3pq": (5, 1),
@@ -646,6 +649,27 @@ def setup(c, a, ctx, dev):
 
 # ----------------------------------------------------------------- roofline
 
+def with_measured_peak(r, kind):
+    """Adds the re-measured ceiling of the roofline's own unit, if one was
+    measured for it (bf16 and int8 matrix cores, HBM copy bandwidth)."""
+    if r is None or not MEASURED_PEAKS:
+        return r
+    m = None
+    if kind == "mfma_bf16":
+        m = MEASURED_PEAKS["bf16_tflops"]
+    elif kind == "mfma":
+        m = MEASURED_PEAKS["bf16_tflops"] / 3
+    elif kind == "int8":
+        m = MEASURED_PEAKS["int8_tops"]
+    elif r.get("bound") == "hbm":
+        # the copy rate: these kernels both read and write
+        m = MEASURED_PEAKS["hbm_gbs"]
+    if m:
+        r["measured_peak"] = round(m, 1)
+        r["frac_of_measured_peak"] = round(r["achieved"] / m, 4)
+    return r
+
+
 def roofline(spec, stats, full=None):
     """Dominant kernel's roofline from the library's event timers: its
     launches and time from ``stats`` (the timed steps, where only the
@@ -802,7 +826,7 @@ def roofline(spec, stats, full=None):
                   "lds_lookup_peak_per_s": PEAK_LDS_LOOKUPS,
                   "lds_lookup_frac": round(M * pairs / sec / PEAK_LDS_LOOKUPS, 4)})
     r["traffic"], r["traffic_source"] = traffic_for(key, spec["workload"])
-    return r
+    return with_measured_peak(r, kind)
 
 
 def traffic_for(kernel_key, workload):
@@ -885,6 +909,7 @@ def measure(c, a, ctx, dev):
         "config": dict({"workload": spec["workload"]}, **spec["config"]),
         "distances_per_s": nq * n * a.steps / el,
         "roofline": roofline(spec, stats, full),
+        "measured_peaks": {k: round(v, 1) for k, v in MEASURED_PEAKS.items()} or None,
         "setup_s": round(build_s, 2),
         "kernels_steps": breakdown_steps,
         "kernels": {k: {"launches": v[0], "ms_total": round(v[1], 3), "pairs": v[2]}
@@ -935,6 +960,8 @@ def main():
 
     dev = torch.device("cuda:0")
     ctx = Context(0)
+    MEASURED_PEAKS.update(ctx.measure_peaks())
+    progress("measured peaks: " + ", ".join(f"{k} {v:.0f}" for k, v in MEASURED_PEAKS.items()))
     if a.config != "all":
         out = measure(a.config, a, ctx, dev)
     else:

@@ -133,6 +133,21 @@ float vsk_last_kernel_ms(const vsk_ctx *ctx);
  * (Acceleration/Metal/MetalProfiler.swift:74-110). */
 vsk_status vsk_last_screen_redo(const vsk_ctx *ctx, int32_t tier, int64_t *out,
                                 int64_t cap, int64_t *count);
+/* Measured ceilings of this GPU, for the rooflines' "fraction of the
+ * measured peak" next to the datasheet one: dense bf16 and int8 matrix-core
+ * rates (register-resident 16x16x32 bf16 and 16x16x64 int8 MFMAs, 32 and 16
+ * independent accumulators per wave, 8 waves per CU), HBM copy bandwidth
+ * (2 GiB, bytes read plus written) and HBM read bandwidth.  Takes about half a second
+ * and 4 GiB of device memory.  No counterpart in the reference: it serves
+ * the benchmark, which reports each kernel against re-measured peaks
+ * beside the datasheet ones. */
+typedef struct {
+  double bf16_tflops;
+  double int8_tops;
+  double hbm_gbs;
+  double hbm_read_gbs;
+} vsk_peaks;
+vsk_status vsk_measure_peaks(vsk_ctx *ctx, vsk_peaks *out);
 /* Per-kernel event timing (off by default). */
 vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on);
 /* Restricts the timing to the timers named in names (comma-separated;

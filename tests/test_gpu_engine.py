@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from vectorstorekit_amd import (HIPAccelerationEngine, HIPAcceleratorStrategy,
+from vectorstorekit_amd import (Context, HIPAccelerationEngine, HIPAcceleratorStrategy,
                                 QuantizationParameters, QuantizationScheme, VectorDatabase,
                                 VSKError)
 
@@ -135,3 +135,19 @@ def test_quantize_vectors_binary_product_none(ctx):
     assert raw[1].codes == x[1].tobytes() and raw[1].metadata.compressionRatio == 1.0
     with pytest.raises(VSKError):
         eng.quantizeVectors(x, QuantizationScheme.product(5))
+
+
+@pytest.mark.gpu
+def test_measure_peaks_plausible():
+    """vsk_measure_peaks: each ceiling is positive and within a factor of
+    the MI355X datasheet figure (bf16 2.5 PFLOP/s, int8 5.0 POP/s, HBM
+    8 TB/s); a measured rate above 1.1x the datasheet would mean the timing
+    or the operation count is wrong."""
+    ctx = Context(0)
+    try:
+        pk = ctx.measure_peaks()
+    finally:
+        ctx.close()
+    for key, sheet in (("bf16_tflops", 2500.0), ("int8_tops", 5000.0), ("hbm_gbs", 8000.0),
+                       ("hbm_read_gbs", 8000.0)):
+        assert 0.25 * sheet < pk[key] < 1.1 * sheet, (key, pk[key])

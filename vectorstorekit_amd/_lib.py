@@ -68,6 +68,11 @@ class vsk_caps(ctypes.Structure):
     ]
 
 
+class vsk_peaks(ctypes.Structure):
+    _fields_ = [("bf16_tflops", c_double), ("int8_tops", c_double), ("hbm_gbs", c_double),
+                ("hbm_read_gbs", c_double)]
+
+
 class vsk_kernel_stat(ctypes.Structure):
     _fields_ = [("name", c_char * 64), ("launches", c_int64), ("total_ms", c_double),
                 ("work", c_double)]
@@ -86,6 +91,7 @@ SIGNATURES = {
     "vsk_stream": (c_void_p, [P]),
     "vsk_last_kernel_ms": (c_float, [P]),
     "vsk_last_screen_redo": (c_int32, [P, c_int32, P, c_int64, P]),
+    "vsk_measure_peaks": (c_int32, [P, POINTER(vsk_peaks)]),
     "vsk_profile_enable": (c_int32, [P, c_int32]),
     "vsk_profile_only": (c_int32, [P, c_char_p]),
     "vsk_profile_reset": (c_int32, [P]),

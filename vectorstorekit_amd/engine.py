@@ -102,6 +102,17 @@ class Context:
     def last_kernel_ms(self) -> float:
         return float(self.lib.vsk_last_kernel_ms(self.handle))
 
+    def measure_peaks(self) -> dict:
+        """Measured ceilings of the device (``vsk_measure_peaks``): dense
+        bf16 TFLOP/s, dense int8 TOP/s, HBM copy GB/s (read plus written)
+        and HBM read GB/s."""
+        from ._lib import vsk_peaks
+
+        pk = vsk_peaks()
+        self.check(self.lib.vsk_measure_peaks(self.handle, ctypes.byref(pk)))
+        return {"bf16_tflops": pk.bf16_tflops, "int8_tops": pk.int8_tops,
+                "hbm_gbs": pk.hbm_gbs, "hbm_read_gbs": pk.hbm_read_gbs}
+
     def last_screen_redo(self, tier: int) -> np.ndarray:
         """Query indices the last flat search redid in the screen's tier 1
         (wider screen) or tier 2 (exact scan over every row)."""
