@@ -24,6 +24,10 @@ struct vsk_sq8 {
   int64_t n = 0;
   int32_t d = 0, ldc = 0;  // ldc: row stride in bytes (multiple of 32)
   vsk::DevBuf codes;
+  // the same codes in 16-row blocks stored in MFMA operand order (see
+  // k_sq8_tile), for the filter scan; tks 64-byte k-steps a row, 0 if none
+  vsk::DevBuf tiles;
+  int32_t tks = 0;
 };
 
 namespace vsk {
@@ -36,6 +40,9 @@ constexpr int SS = SB_K + 16;                     // LDS row stride (bytes)
 struct Sq8Args {
   const int8_t *X;
   int64_t ldx;
+  // tiled copy of X (16-row blocks of tks 1 KB k-steps), or null
+  const int8_t *T;
+  int32_t tks;
   const int8_t *Q;
   int64_t ldq;
   int32_t kbytes;  // padded code length (multiple of 32)
@@ -360,6 +367,27 @@ __device__ __forceinline__ bool sq8_any_pass(const i4 (&acc)[1][QT], const int32
   return any != 0;
 }
 
+// The tiled copy of a code matrix: 16-row block b, k-step ks (64 bytes of
+// each row) is 1 KB at (b * ks_n + ks) KB, whose 16 bytes at 16 l hold row
+// 16 b + (l & 15), bytes 64 ks + 16 (l >> 4): the v_mfma_i32_16x16x64_i8
+// A operand of lane l.  Rows past n and bytes past ldc are zero.  A thread
+// per 16 bytes, grid-stride.
+__global__ __launch_bounds__(256) void k_sq8_tile(const int8_t *X, int64_t n, int32_t ldc,
+                                                  int32_t ks_n, int64_t total, int8_t *T) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {  // 16-byte unit
+    const int l = (int)(i & 63);
+    const int64_t bk = i >> 6;  // block * ks_n + ks
+    const int64_t b = bk / ks_n;
+    const int ks = (int)(bk - b * ks_n);
+    const int64_t row = 16 * b + (l & 15);
+    const int32_t off = 64 * ks + 16 * (l >> 4);
+    i4 v = i4{0, 0, 0, 0};
+    if (row < n && off < ldc) v = *reinterpret_cast<const i4 *>(X + row * ldc + off);
+    reinterpret_cast<i4 *>(T)[i] = v;
+  }
+}
+
 template <int KS, int QT, int NPF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
@@ -398,14 +426,26 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
   }
 
   const int64_t nrows = s1 - s0;
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(a.X + s0 * a.ldx), 0, (int32_t)(nrows * a.ldx), 0x00020000);
-  const int32_t lrow = (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  // Row blocks come from the tiled copy when there is one: block b's k-step
+  // ks is the 1 KB at (b * KS + ks) KB, lane l's 16 bytes at 16 l, so a
+  // wave's load is contiguous (from the row-major codes the 16 lanes of a
+  // quarter-wave touch 16 rows).  s0 is a multiple of 16 (launch_pipe).
+  const bool tiled = a.T != nullptr;
+  const __amdgpu_buffer_rsrc_t rx =
+      tiled ? __builtin_amdgcn_make_buffer_rsrc(
+                  (void *)(a.T + (s0 >> 4) * (KS * 1024)), 0,
+                  (int32_t)(((nrows + 15) >> 4) * (KS * 1024)), 0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc((void *)(a.X + s0 * a.ldx), 0,
+                                                (int32_t)(nrows * a.ldx), 0x00020000);
+  // byte offset of row T's block (T a multiple of 16) and this lane's part
+  const int32_t rstep = tiled ? KS * 64 : (int32_t)a.ldx;
+  const int32_t lrow = tiled ? lane * 16 : (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  const int32_t kstep = tiled ? 1024 : 64;
   i4 ar[NPF][RT][KS];
 #define SP_LOAD(AR, T)                                                          \
   _Pragma("unroll") for (int ks = 0; ks < KS; ++ks) AR[0][ks] = __builtin_bit_cast( \
-      i4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int32_t)(T) * (int32_t)a.ldx + lrow, \
-                                                64 * ks, 0))
+      i4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int32_t)(T) * rstep + lrow, \
+                                                kstep * ks, 0))
   __shared__ uint64_t s_key[4][SQ_WBUF];
   __shared__ int32_t s_q[4][SQ_WBUF];
   int32_t nbuf = 0;  // wave-uniform count of staged candidates
@@ -470,10 +510,13 @@ static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
   if (splits > max_splits) splits = max_splits;
   if (splits < 1) splits = 1;
   Sq8Args b = a;
+  // the tiled copy holds 16-row blocks of this instance's k-steps
+  if ((a.r0 & 15) || a.tks != KS) b.T = nullptr;
   b.rows_per_split = ceil_div(ceil_div(rows, splits), step) * step;
-  // buffer offsets (row * ldx, prefetch up to 2 NPF blocks past the end)
-  // stay within int32
-  const int64_t max_rows = 0x7FFFFFFFll / a.ldx - 2 * step;
+  // buffer offsets (row * ldx, or row * KS * 64 in the tiled copy; prefetch
+  // up to 2 NPF blocks past the end) stay within int32
+  const int64_t stride = b.T ? (int64_t)KS * 64 : a.ldx;
+  const int64_t max_rows = 0x7FFFFFFFll / stride - 2 * step;
   if (b.rows_per_split > max_rows) b.rows_per_split = max_rows / step * step;
   splits = ceil_div(ceil_div(rows, b.rows_per_split), 8) * 8;
   const int64_t spx = splits / 8;
@@ -913,6 +956,19 @@ vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
   if (db->ldc != d)
     fill_i32(ctx, db->codes.as<int32_t>(), n * db->ldc / 4, 0);
   copy_rows(ctx, db->codes.p, db->ldc, codes, d, d, n);
+  // the filter scan's tiled copy (codes of up to 512 bytes, its range), in
+  // the k-steps of the scan instance that takes this width (1, 2, 4 or 8;
+  // the extra ones are zero)
+  int32_t ks_n = 1;
+  while (ks_n * 64 < db->ldc) ks_n <<= 1;
+  if (ks_n <= 8) {
+    const int64_t units = ceil_div(n, 16) * ks_n * 64;
+    db->tiles.reserve((size_t)units * 16);
+    db->tks = ks_n;
+    k_sq8_tile<<<grid1(units), 256, 0, ctx->stream>>>(db->codes.as<int8_t>(), n, db->ldc, ks_n,
+                                                      units, db->tiles.as<int8_t>());
+    check_launch("sq8_tile");
+  }
   cs.finish();
   *out = db.release();
   VSK_API_END(ctx);
@@ -951,6 +1007,8 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
     Sq8Args base{};
     base.X = db->codes.as<int8_t>();
     base.ldx = db->ldc;
+    base.T = db->tks ? db->tiles.as<int8_t>() : nullptr;
+    base.tks = db->tks;
     base.Q = dq + b0 * db->ldc;
     base.ldq = db->ldc;
     base.kbytes = db->ldc;
@@ -1050,6 +1108,8 @@ vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
     Sq8Args a0{};
     a0.X = db->codes.as<int8_t>();
     a0.ldx = db->ldc;
+    a0.T = db->tks ? db->tiles.as<int8_t>() : nullptr;
+    a0.tks = db->tks;
     a0.Q = dq;
     a0.ldq = db->ldc;
     a0.kbytes = db->ldc;
