@@ -574,16 +574,26 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             4, lane * 4, w * 256, 0, 0);
       }
     }
-    uint8_t *bx = lds + dbuf * XS_STAGE + 4 * w * 1024;
     const int32_t kofs = dst * XS_K * 2;
+    // waves 0-3 issue the stage's 64 copies, 16 each: their own units and
+    // those of wave w + 4, 128 rows further (the same swizzle); the other
+    // four waves only multiply (fewer waves issuing memory instructions
+    // measured faster)
+    if (w < 4) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int32_t so = kofs + (u >> 1) * 16 * ldx2;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (__attribute__((address_space(3))) void *)(bx + u * 1024), 16, voff[u & 1], so, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rq, (__attribute__((address_space(3))) void *)(bx + XS_N * XS_R + u * 1024), 16,
-          voff[u & 1], so, 0, 0);
+      for (int h = 0; h < 2; ++h) {
+        uint8_t *bx = lds + dbuf * XS_STAGE + 4 * (w + 4 * h) * 1024;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t so = kofs + (u >> 1) * 16 * ldx2 + h * 128 * ldx2;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rx, (__attribute__((address_space(3))) void *)(bx + u * 1024), 16, voff[u & 1], so,
+              0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rq, (__attribute__((address_space(3))) void *)(bx + XS_N * XS_R + u * 1024), 16,
+              voff[u & 1], so, 0, 0);
+        }
+      }
     }
     dbuf ^= 1;
     if (++dst == nst) {
