@@ -30,9 +30,24 @@ void DevBuf::release() {
   p = nullptr;
   bytes = 0;
 }
+namespace {
+thread_local vsk_ctx *t_fault_ctx = nullptr;
+}
+void set_fault_ctx(vsk_ctx *c) { t_fault_ctx = c; }
+void fault_point(int kind) {
+  vsk_ctx *c = t_fault_ctx;
+  if (!c || c->fault_kind != kind) return;
+  if (++c->fault_seen != c->fault_at) return;
+  static const char *names[] = {"", "allocation", "launch", "synchronisation"};
+  fail(kind == FAULT_ALLOC ? VSK_ERR_OUT_OF_MEMORY : VSK_ERR_EXECUTION_FAILED,
+       std::string("injected fault (VSK_FAULT): ") + names[kind] + " " +
+           std::to_string(c->fault_at));
+}
+
 void DevBuf::reserve(size_t b) {
   if (b <= bytes && p) return;
   release();
+  fault_point(FAULT_ALLOC);
   size_t want = b ? b : 1;
   hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) {
@@ -66,6 +81,7 @@ void CallScope::finish() {
   VSK_HIP(hipEventElapsedTime(&ms, ctx->call_begin, ctx->call_end));
   ctx->last_ms = ms;
   ctx->resolve_pending();
+  fault_point(FAULT_SYNC);
 }
 
 KernelTimer::KernelTimer(vsk_ctx *c, const char *name, double work_items, hipStream_t s)
@@ -110,6 +126,7 @@ void check_launch(const char *name) {
   if (e != hipSuccess)
     fail(VSK_ERR_EXECUTION_FAILED,
          std::string("launch of ") + name + " failed: " + hipGetErrorString(e));
+  fault_point(FAULT_LAUNCH);
 }
 
 const void *input_to_device(vsk_ctx *ctx, const void *p, size_t bytes,
@@ -425,6 +442,19 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
   c->flat_force_screen = fk && strcmp(fk, "screen") == 0;
+  if (const char *ff = getenv("VSK_FAULT")) {
+    const char *colon = strchr(ff, ':');
+    const long long at = colon ? atoll(colon + 1) : 0;
+    const size_t len = colon ? (size_t)(colon - ff) : strlen(ff);
+    int kind = 0;
+    if (len == 5 && strncmp(ff, "alloc", 5) == 0) kind = FAULT_ALLOC;
+    if (len == 6 && strncmp(ff, "launch", 6) == 0) kind = FAULT_LAUNCH;
+    if (len == 4 && strncmp(ff, "sync", 4) == 0) kind = FAULT_SYNC;
+    if (kind && at > 0) {
+      c->fault_kind = kind;
+      c->fault_at = at;
+    }
+  }
   // a blocking stream: it orders itself after work on the null stream, so
   // device buffers produced there (e.g. by torch) are complete when read
   if (hipStreamCreate(&c->stream) != hipSuccess ||
@@ -439,6 +469,7 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
 
 vsk_status vsk_destroy(vsk_ctx *ctx) {
   if (!ctx) return VSK_OK;
+  if (t_fault_ctx == ctx) t_fault_ctx = nullptr;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);

@@ -26,6 +26,19 @@ struct Error {
 
 [[noreturn]] void fail(vsk_status code, const std::string &msg);
 void check_hip(hipError_t e, const char *what, const char *file, int line);
+// Fault injection from the host (VSK_FAULT=alloc:<n>, launch:<n> or
+// sync:<n>, read when a context is created): the n-th device allocation,
+// kernel launch check or end-of-call synchronisation of that context fails
+// as HIP would report it (out of memory; execution failed), once.  The
+// kernels themselves run normally; only the report is forced, so error
+// mapping and recovery can be tested without faulting the GPU.
+enum FaultKind { FAULT_NONE = 0, FAULT_ALLOC = 1, FAULT_LAUNCH = 2, FAULT_SYNC = 3 };
+void fault_point(int kind);
+}  // namespace vsk
+struct vsk_ctx;
+namespace vsk {
+// the context whose API call runs on this thread (fault counting)
+void set_fault_ctx(vsk_ctx *c);
 #define VSK_HIP(expr) ::vsk::check_hip((expr), #expr, __FILE__, __LINE__)
 #define VSK_REQUIRE(cond, code, msg)                                          \
   do {                                                                        \
@@ -82,6 +95,9 @@ struct vsk_ctx {
   bool flat_fp32 = false;
   bool flat_no_screen = false;
   bool flat_force_screen = false;
+  // VSK_FAULT: the kind of event to fail, at which occurrence, seen so far
+  int fault_kind = 0;
+  int64_t fault_at = 0, fault_seen = 0;
 
   // queries the last vsk_search_flat redid in the screen's fallback tiers
   // (indices into that call's queries, ascending): [0] the wider screen,
