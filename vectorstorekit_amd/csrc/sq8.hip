@@ -297,17 +297,24 @@ void k_sq8_reg(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
   }
 
   const int64_t nrows = s1 - s0;
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(a.X + s0 * a.ldx), 0, (int32_t)(nrows * a.ldx), 0x00020000);
-  const int32_t lrow = (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  // the tiled copy when there is one (as in k_sq8_pipe; s0 a multiple of 16)
+  const bool tiled = a.T != nullptr;
+  const __amdgpu_buffer_rsrc_t rx =
+      tiled ? __builtin_amdgcn_make_buffer_rsrc(
+                  (void *)(a.T + (s0 >> 4) * (KS * 1024)), 0,
+                  (int32_t)(((nrows + 15) >> 4) * (KS * 1024)), 0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc((void *)(a.X + s0 * a.ldx), 0,
+                                                (int32_t)(nrows * a.ldx), 0x00020000);
+  const int32_t rstep = tiled ? KS * 64 : (int32_t)a.ldx;
+  const int32_t lrow = tiled ? lane * 16 : (int32_t)(lane & 15) * (int32_t)a.ldx + kc;
+  const int32_t kstep = tiled ? 1024 : 64;
   i4 ar0[RT][KS], ar1[RT][KS];
 #define SR_LOAD(AR, T)                                                       \
   _Pragma("unroll") for (int i = 0; i < RT; ++i)                          \
   _Pragma("unroll") for (int ks = 0; ks < KS; ++ks)                          \
       AR[i][ks] = __builtin_bit_cast(                                        \
           i4, __builtin_amdgcn_raw_buffer_load_b128(                         \
-                  rx, (int32_t)((T) + 16 * i) * (int32_t)a.ldx + lrow,       \
-                  64 * ks, 0))
+                  rx, (int32_t)((T) + 16 * i) * rstep + lrow, kstep * ks, 0))
   i4 acc[RT][QT];
   __shared__ uint64_t s_key[4][DENSE ? 1 : SQ_WBUF];
   __shared__ int32_t s_q[4][DENSE ? 1 : SQ_WBUF];
@@ -537,10 +544,13 @@ static void launch_reg(vsk_ctx *ctx, const Sq8Args &a, bool dense) {
   if (splits > max_splits) splits = max_splits;
   if (splits < 1) splits = 1;
   Sq8Args b = a;
+  // the tiled copy holds 16-row blocks of this instance's k-steps
+  if ((a.r0 & 15) || a.tks != KS) b.T = nullptr;
   b.rows_per_split = ceil_div(ceil_div(rows, splits), 16 * RT) * (16 * RT);
-  // buffer offsets (row * ldx, prefetch up to 4 blocks past the end) stay
-  // within int32
-  const int64_t max_rows = 0x7FFFFFFFll / a.ldx - 4 * 16 * RT;
+  // buffer offsets (row * ldx, or row * KS * 64 in the tiled copy; prefetch
+  // up to 4 blocks past the end) stay within int32
+  const int64_t stride = b.T ? (int64_t)KS * 64 : a.ldx;
+  const int64_t max_rows = 0x7FFFFFFFll / stride - 4 * 16 * RT;
   if (b.rows_per_split > max_rows)
     b.rows_per_split = max_rows / (16 * RT) * (16 * RT);
   splits = ceil_div(ceil_div(rows, b.rows_per_split), 8) * 8;
