@@ -33,7 +33,11 @@ void DevBuf::release() {
 namespace {
 thread_local vsk_ctx *t_fault_ctx = nullptr;
 }
-void set_fault_ctx(vsk_ctx *c) { t_fault_ctx = c; }
+vsk_ctx *set_fault_ctx(vsk_ctx *c) {
+  vsk_ctx *p = t_fault_ctx;
+  t_fault_ctx = c;
+  return p;
+}
 void fault_point(int kind) {
   vsk_ctx *c = t_fault_ctx;
   if (!c || c->fault_kind != kind) return;

@@ -9,7 +9,7 @@
 // context's device is made current and internal errors become status codes.
 #define VSK_API_BEGIN(ctx)                                                    \
   if (!(ctx)) return VSK_ERR_INVALID_ARGUMENT;                                \
-  ::vsk::set_fault_ctx(ctx);                                                  \
+  const ::vsk::FaultCtxScope vsk_fault_scope_(ctx);                           \
   try {                                                                       \
     (ctx)->last_error.clear();                                                \
     VSK_HIP(hipSetDevice((ctx)->device));

@@ -37,8 +37,17 @@ void fault_point(int kind);
 }  // namespace vsk
 struct vsk_ctx;
 namespace vsk {
-// the context whose API call runs on this thread (fault counting)
-void set_fault_ctx(vsk_ctx *c);
+// the context whose API call runs on this thread (fault counting), for the
+// duration of the call: no other code sees a context that may since have
+// been destroyed
+vsk_ctx *set_fault_ctx(vsk_ctx *c);  // returns the previous one
+struct FaultCtxScope {
+  vsk_ctx *prev;  // an enclosing API call's context (nested calls)
+  explicit FaultCtxScope(vsk_ctx *c) : prev(set_fault_ctx(c)) {}
+  ~FaultCtxScope() { set_fault_ctx(prev); }
+  FaultCtxScope(const FaultCtxScope &) = delete;
+  FaultCtxScope &operator=(const FaultCtxScope &) = delete;
+};
 #define VSK_HIP(expr) ::vsk::check_hip((expr), #expr, __FILE__, __LINE__)
 #define VSK_REQUIRE(cond, code, msg)                                          \
   do {                                                                        \
