@@ -319,7 +319,10 @@ vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t 
  * n floats each (may be NULL; the reference keeps them for dequantisation). */
 vsk_status vsk_scalar_quantize_u8(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
                                   int32_t bits, uint8_t *codes, float *scale, float *minv);
-/* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81). */
+/* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81).
+ * Codes of up to 512 bytes are also kept in a tiled copy for the scans
+ * (16-row blocks in the matrix cores' operand order), which doubles the
+ * device memory the database holds. */
 vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
                           int32_t d, vsk_sq8 **out);
 vsk_status vsk_sq8_free(vsk_ctx *ctx, vsk_sq8 *db);

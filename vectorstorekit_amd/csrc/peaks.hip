@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // four 16-byte loads in flight per thread before their stores, both
-// non-temporal (n is a multiple of 4 * 256 * gridDim.x).  Measured on
+// non-temporal (n is a multiple of 4 * 256 * gridDim.x, so every access is
+// in bounds).  Measured on
 // MI355X: 5.1 TB/s; cached accesses reach 4.5 TB/s, with one load in
 // flight per thread or four.
 typedef unsigned pk_u4 __attribute__((ext_vector_type(4)));
@@ -159,18 +160,19 @@ extern "C" vsk_status vsk_measure_peaks(vsk_ctx *ctx, vsk_peaks *out) {
     k_peak_i8<<<blocks, 256, 0, ctx->stream>>>(iters, sink.as<int>());
   });
   out->int8_tops = waves * iters * 16 * (2.0 * 16 * 16 * 64) / (ti * 1e9);
-  const int64_t n16 = copy_bytes / 16;
+  // the copied span: a whole number of the grid's 4-load steps
   const int cgrid = p.multiProcessorCount * 32;
-  VSK_REQUIRE(n16 % (4 * 256 * (int64_t)cgrid) == 0, VSK_ERR_UNSUPPORTED,
-              "copy size not a multiple of the copy grid");
+  const int64_t unit = 4 * 256 * (int64_t)cgrid;
+  const int64_t n16 = copy_bytes / 16 / unit * unit;
+  const double moved = 16.0 * (double)n16;
   const double tc = time_ms([&] {
     k_peak_copy<<<cgrid, 256, 0, ctx->stream>>>(src.as<pk_u4>(), dst.as<pk_u4>(), n16);
   });
-  out->hbm_gbs = 2.0 * (double)copy_bytes / (tc * 1e6);
+  out->hbm_gbs = 2.0 * moved / (tc * 1e6);
   const double tr = time_ms([&] {
     k_peak_read<<<cgrid, 256, 0, ctx->stream>>>(src.as<pk_u4>(), n16, sink.as<unsigned>());
   });
-  out->hbm_read_gbs = (double)copy_bytes / (tr * 1e6);
+  out->hbm_read_gbs = moved / (tr * 1e6);
   check_launch("measure_peaks");
   VSK_API_END(ctx);
 }
