@@ -184,6 +184,18 @@ vsk_status vsk_db_read_f32(vsk_ctx *ctx, const vsk_db *db, int64_t row0,
 vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
                            int64_t nq, int32_t k, int32_t metric,
                            float *out_dist, int64_t *out_ids);
+/* vsk_search_flat over the rows a filter keeps: row r is a candidate when
+ * r < allow_bits and bit r of allow is set (bit r % 32 of allow[r / 32]);
+ * rows past allow_bits are excluded.  The results are those of a search of
+ * the kept rows alone, with the original row ids (ties still go to the lower
+ * row).  Backs VectorIndex.search(query:k:strategy:filter:)
+ * (Core/Protocols.swift:116-121) for a flat index: the reference applies
+ * the filter to the candidates before it ranks them (Indexes/IVFIndex.swift:
+ * 161-176 for IVF).  allow = NULL with allow_bits = 0 is vsk_search_flat. */
+vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                                    int64_t nq, int32_t k, int32_t metric,
+                                    const uint32_t *allow, int64_t allow_bits,
+                                    float *out_dist, int64_t *out_ids);
 /* Full distance matrix out[i*n + j] = dist(q_i, x_j): computeDistances
  * (:76-136, nq = 1) and batchComputeDistances(topK: nil) (:139-204). */
 vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
@@ -222,6 +234,30 @@ vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
 vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                           int64_t nq, int32_t nprobe, int32_t k,
                           int32_t metric, float *out_dist, int64_t *out_ids);
+/* IVFIndex.search with a filter (:124-202): the probed lists' rows are
+ * filtered first (applyFilter, :161-165), then ranked, so a query gets the
+ * k nearest rows that pass among its probed candidates, at any selectivity.
+ * The filter is a bitmap over the stored rows' ids: a row with id i is a
+ * candidate when 0 <= i < allow_bits and bit i % 32 of allow[i / 32] is
+ * set (rows added with ids = NULL have ids 0, 1, 2, ... in insertion
+ * order).  The probes are the unfiltered ones (the reference probes before
+ * it filters).  allow = NULL with allow_bits = 0 is vsk_ivf_search. */
+vsk_status vsk_ivf_search_filtered(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                                   int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
+                                   const uint32_t *allow, int64_t allow_bits, float *out_dist,
+                                   int64_t *out_ids);
+/* IVFIndex.delete(id:) (:210-220): every stored row whose id is one of
+ * ids[0 .. n) leaves its inverted list; the rows after it in the list keep
+ * their order, so later searches rank exactly as the reference's lists do
+ * after remove(at:).  *removed (may be NULL) receives the number of rows
+ * removed.  Codes made by vsk_ivf_encode_* stay valid for the rows kept. */
+vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_t n,
+                          int64_t *removed);
+/* getVectorsFromList for every list at once (:487-490): ids (total, may be
+ * NULL) receives the stored rows' ids in list order and offsets (nlist + 1,
+ * may be NULL) where each list starts; list l holds ids[offsets[l] ..
+ * offsets[l+1]). */
+vsk_status vsk_ivf_list_ids(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t *ids, int64_t *offsets);
 /* sizes[nlist] = rows per inverted list; total = sum */
 vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
                               int64_t *sizes);

@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 import vectorstorekit_amd as vsk
@@ -87,3 +88,18 @@ def test_product_does_not_import_oracle():
                 text = open(os.path.join(dirpath, f), errors="ignore").read()
                 assert "from oracle" not in text and "import oracle" not in text, f
                 assert "libvsk_oracle" not in text, f
+
+
+def test_row_bitmap_layout():
+    """The row filter the C ABI takes: bit i % 32 of word i // 32; from a
+    boolean mask or from allowed indices, padded with zero words."""
+    mask = np.zeros(70, np.bool_)
+    mask[[0, 5, 31, 32, 69]] = True
+    bm = _lib.row_bitmap(mask)
+    assert bm.dtype == np.uint32 and bm.size == 3
+    assert list(bm) == [(1 << 0) | (1 << 5) | (1 << 31), 1, 1 << 5]
+    np.testing.assert_array_equal(_lib.row_bitmap([0, 5, 31, 32, 69]), bm)
+    np.testing.assert_array_equal(_lib.row_bitmap(np.array([], np.int64), 64),
+                                  np.zeros(2, np.uint32))
+    unpacked = np.unpackbits(bm.view(np.uint8), bitorder="little")[:70].astype(bool)
+    np.testing.assert_array_equal(unpacked, mask)

@@ -402,3 +402,41 @@ def test_distance_matrix_symmetric(ctx, metric):
     b = rng.standard_normal((33, 45)).astype(np.float32)
     mb = np.asarray(eng.computeDistanceMatrix(b, a, metric="manhattan"))
     np.testing.assert_array_equal(mb, O.distances(b, a, O.L1))
+
+
+@pytest.mark.parametrize("metric", [METRIC_L2SQ, METRIC_L2, METRIC_COSINE_NORMALIZED,
+                                    METRIC_DOT, METRIC_L1, METRIC_COSINE])
+@pytest.mark.parametrize("shape", [(20_000, 64, 96, 10, 0.005), (5000, 40, 37, 100, 0.4),
+                                   (3000, 300, 768, 50, 0.05), (120_000, 100, 128, 100, 0.5)])
+def test_flat_filtered(ctx, metric, shape):
+    """vsk_search_flat_filtered: the search over the rows the filter keeps,
+    with their own row ids -- the same bar as the unfiltered search (exact
+    metrics bit-exact, the reference's epsilon cosine within the float bar);
+    a filter as allowed ids with a short bitmap; nothing allowed."""
+    n, nq, d, k, frac = shape
+    x, q = _data(7 * n + metric, n, nq, d, normalize=metric == METRIC_COSINE_NORMALIZED)
+    print(f"flat filter metric={metric} n={n} nq={nq} d={d} k={k} keep={frac}", flush=True)
+    db = VectorDatabase(ctx, x)
+    keep = np.random.default_rng(n + k).random(n) < frac
+    sub = np.flatnonzero(keep)
+    gd, gi = db.search(q, k, metric, allow=keep)
+    od, oi = O.search_flat(q, x[sub], k, metric)
+    oi = np.where(oi >= 0, sub[np.maximum(oi, 0)], -1)
+    assert_sorted_unique(gd, gi)
+    if metric == METRIC_COSINE:
+        assert_topk_match(gd, gi, od, oi,
+                          lambda qi, ids: O.distances(q[qi:qi + 1], x[ids], metric)[0])
+    else:
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gd, od)
+    assert set(gi[gi >= 0].tolist()) <= set(sub.tolist())
+    # allowed ids with a bitmap of n // 2 bits: the rows past it are out
+    ids = sub[sub < n // 2]
+    gd2, gi2 = db.search(q, k, metric, allow=ids)
+    od2, oi2 = O.search_flat(q, x[ids], k, metric)
+    oi2 = np.where(oi2 >= 0, ids[np.maximum(oi2, 0)], -1)
+    if metric != METRIC_COSINE:
+        np.testing.assert_array_equal(gi2, oi2)
+        np.testing.assert_array_equal(gd2, od2)
+    gd3, gi3 = db.search(q[:2], k, metric, allow=np.zeros(n, np.bool_))
+    assert (gi3 == -1).all() and np.isinf(gd3).all()

@@ -134,3 +134,91 @@ def test_vector_index_twin_results_filter_delete(ctx):
         np.testing.assert_array_equal(np.array([r.distance for r in res], np.float32),
                                       od[0][:len(want)])
     acc.initialize().close()
+
+
+def test_twin_selective_filter_exact(ctx):
+    """A filter that passes 0.5 % of the rows rejects far more than 1,024
+    probed candidates; the twin still returns the k nearest passing rows of
+    the probed lists (the reference filters before it ranks), for .exact
+    and .approximate, at k = 10 and k = 100."""
+    x, q = _data(5, n=40_000, d=32, ncent=16, nq=4)
+    n, d = x.shape
+    acc = HIPAcceleratorStrategy(0)
+    idx = HIPIVFIndexingStrategy(acc, d, numClusters=16, nprobe=4, trainingSamples=x).createIndex()
+    assert idx.isOptimized
+    idx.insertBatch(VectorEntry(f"vec{i}", x[i], {"i": i, "rare": i % 200 == 7})
+                    for i in range(n))
+    cent = idx.ivf.getCentroids()
+    lists = O.ivf_assign(x, cent)
+    sub = np.flatnonzero(np.arange(n) % 200 == 7)
+    for strategy, probes in ((SearchStrategy.exact, 16), (SearchStrategy.approximate, 4)):
+        for k in (10, 100):
+            for qi in range(q.shape[0]):
+                res = idx.search(q[qi], k, strategy, filter=lambda vid, m: m["rare"])
+                od, oi = O.ivf_search(q[qi:qi + 1], x[sub], sub.astype(np.int64), lists[sub],
+                                      cent, probes, k)
+                want = [f"vec{i}" for i in oi[0] if i >= 0]
+                assert len(want) == min(k, len(res)) and len(want) > 0
+                assert [r.id for r in res] == want
+                np.testing.assert_array_equal(
+                    np.array([r.distance for r in res], np.float32), od[0][:len(want)])
+    with pytest.raises(Exception) as e:
+        idx.search(q[0], 1025)
+    assert getattr(e.value, "kind", "") == "invalidBufferSize"
+
+
+def test_twin_duplicate_ids_delete_contains(ctx):
+    """An id inserted twice is stored twice (the reference appends both):
+    delete removes one copy per call, contains holds while one remains, and
+    a deleted copy never comes back from search."""
+    x, q = _data(6)
+    n, d = x.shape
+    acc = HIPAcceleratorStrategy(0)
+    idx = HIPIVFIndexingStrategy(acc, d, numClusters=16, nprobe=16, trainingSamples=x).createIndex()
+    for i in range(200):
+        idx.insert(VectorEntry(f"vec{i}", x[i], {"i": i}))
+    idx.insert(VectorEntry("vec3", x[3] + 0.5, {"i": "copy"}))  # a second copy of vec3
+    assert idx.count == 201 and idx.contains("vec3")
+    res = idx.search(x[3], 5, SearchStrategy.exact)
+    assert [r.id for r in res][:1] == ["vec3"]
+    assert sum(r.id == "vec3" for r in idx.search(x[3], 201, SearchStrategy.exact)) == 2
+    assert idx.delete("vec3") and idx.contains("vec3") and idx.count == 200
+    assert sum(r.id == "vec3" for r in idx.search(x[3], 200, SearchStrategy.exact)) == 1
+    assert idx.delete("vec3") and not idx.contains("vec3") and idx.count == 199
+    assert not idx.delete("vec3")
+    assert all(r.id != "vec3" for r in idx.search(x[3], 199, SearchStrategy.exact))
+    # the rows left rank as the oracle ranks them
+    rows = np.array([i for i in range(200) if i != 3])
+    res = idx.search(q[0], 20, SearchStrategy.exact)
+    fd, fi = O.search_flat(q[:1], x[rows], 20, O.L2)
+    assert [r.id for r in res] == [f"vec{rows[i]}" for i in fi[0]]
+    np.testing.assert_array_equal(np.array([r.distance for r in res], np.float32), fd[0])
+
+
+def test_twin_export_import_round_trip(ctx):
+    """export() writes the whole index with its VectorIDs and metadata;
+    import_() into a fresh index answers searches, filters and deletes as
+    the original does."""
+    x, q = _data(7)
+    n, d = x.shape
+    acc = HIPAcceleratorStrategy(0)
+    strat = HIPIVFIndexingStrategy(acc, d, numClusters=16, nprobe=4, trainingSamples=x)
+    idx = strat.createIndex()
+    idx.insertBatch(VectorEntry(f"vec{i}", x[i], {"i": i, "odd": i % 2 == 1}) for i in range(n))
+    for i in range(0, 300, 3):
+        assert idx.delete(f"vec{i}")
+    data = idx.export()
+    other = HIPIVFIndexingStrategy(acc, d, numClusters=16, nprobe=4).createIndex()
+    other.import_(data)
+    assert other.count == idx.count == n - 100
+    assert other.contains("vec1") and not other.contains("vec0")
+    for qi in range(q.shape[0]):
+        for flt in (None, lambda vid, m: m["odd"]):
+            for strategy in (SearchStrategy.exact, SearchStrategy.approximate):
+                a = idx.search(q[qi], 12, strategy, filter=flt)
+                b = other.search(q[qi], 12, strategy, filter=flt)
+                assert [(r.id, r.distance, r.metadata) for r in a] == \
+                    [(r.id, r.distance, r.metadata) for r in b]
+    assert other.delete("vec1") and not other.contains("vec1")
+    other.insert(VectorEntry("new", x[1], {"i": -1}))
+    assert [r.id for r in other.search(x[1], 1, SearchStrategy.exact)] == ["new"]

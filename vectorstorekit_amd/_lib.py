@@ -102,6 +102,8 @@ SIGNATURES = {
     "vsk_db_info": (c_int32, [P, POINTER(c_int64), POINTER(c_int32)]),
     "vsk_db_read_f32": (c_int32, [P, P, c_int64, c_int64, P]),
     "vsk_search_flat": (c_int32, [P, P, P, c_int64, c_int32, c_int32, P, P]),
+    "vsk_search_flat_filtered": (c_int32, [P, P, P, c_int64, c_int32, c_int32, P, c_int64, P,
+                                           P]),
     "vsk_distances": (c_int32, [P, P, P, c_int64, c_int32, P]),
     "vsk_ivf_create": (c_int32, [P, P, c_int32, c_int32, PP]),
     "vsk_ivf_free": (c_int32, [P, P]),
@@ -111,6 +113,10 @@ SIGNATURES = {
     "vsk_ivf_search": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P, P]),
     "vsk_ivf_build": (c_int32, [P, P, c_int32, P, P, c_int64, c_int32, PP]),
     "vsk_ivf_list_sizes": (c_int32, [P, P, P]),
+    "vsk_ivf_search_filtered": (c_int32, [P, P, P, c_int64, c_int32, c_int32, c_int32, P,
+                                          c_int64, P, P]),
+    "vsk_ivf_remove": (c_int32, [P, P, P, c_int64, P]),
+    "vsk_ivf_list_ids": (c_int32, [P, P, P, P]),
     "vsk_ivf_encode_sq8": (c_int32, [P, P, c_int32, P, P]),
     "vsk_ivf_encode_pq": (c_int32, [P, P, P]),
     "vsk_ivf_save": (c_int32, [P, P, ctypes.c_char_p]),
@@ -221,6 +227,26 @@ def out_buffer(shape, dtype, like=None):
         return t.data_ptr(), t
     a = np.empty(shape, dtype=dtype)
     return a.ctypes.data, a
+
+
+def row_bitmap(allowed, nbits: int | None = None) -> np.ndarray:
+    """A row filter as the C ABI takes it: bit i (bit i % 32 of word i // 32)
+    is set when row (or id) i may be a candidate.  ``allowed`` is a boolean
+    array over the rows or an iterable of the allowed indices (then nbits
+    gives the bitmap's length)."""
+    a = np.asarray(allowed)
+    if a.dtype == np.bool_:
+        bits = a.reshape(-1)
+    else:
+        n = int(nbits if nbits is not None else (a.max() + 1 if a.size else 0))
+        bits = np.zeros(n, np.bool_)
+        if a.size:
+            bits[a.astype(np.int64)] = True
+    words = np.packbits(bits, bitorder="little")
+    pad = (-words.size) % 4
+    if pad:
+        words = np.concatenate([words, np.zeros(pad, np.uint8)])
+    return words.view(np.uint32)
 
 
 def check(ctx_handle, status: int):

@@ -553,11 +553,103 @@ void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
   }
 }
 
+// a row filter's rows as a database of their own: row t = rows[t] of db,
+// with its norms (the same values, so the filtered search ranks as the
+// whole database does)
+__global__ void k_gather_db_rows(const float *X, const float *sq, const float *nrm, int32_t ld,
+                                 const int32_t *rows, int64_t m, float *out, float *osq,
+                                 float *onrm) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6); t < m; t += (int64_t)gridDim.x * 4) {
+    const int64_t r = rows[t];
+    for (int j = lane; j < ld; j += 64) out[t * ld + j] = X[r * ld + j];
+    if (lane == 0) {
+      osq[t] = sq[r];
+      onrm[t] = nrm[r];
+    }
+  }
+}
+
 }  // namespace vsk
 
 using namespace vsk;
 
 extern "C" {
+
+vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                                    int64_t nq, int32_t k, int32_t metric,
+                                    const uint32_t *allow, int64_t allow_bits,
+                                    float *out_dist, int64_t *out_ids) {
+  if (!allow && allow_bits == 0)
+    return vsk_search_flat(ctx, db, q, nq, k, metric, out_dist, out_ids);
+  VSK_API_BEGIN(ctx);
+  VSK_REQUIRE(db, VSK_ERR_INVALID_ARGUMENT, "db is null");
+  VSK_REQUIRE(metric_valid(metric), VSK_ERR_INVALID_ARGUMENT, "unknown metric");
+  VSK_REQUIRE(nq > 0, VSK_ERR_EMPTY_INPUT, "no queries");
+  VSK_REQUIRE(q && out_dist && out_ids, VSK_ERR_INVALID_ARGUMENT, "null buffer");
+  VSK_REQUIRE(k >= 1, VSK_ERR_INVALID_ARGUMENT, "k must be >= 1");
+  VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE, "k exceeds VSK_MAX_K");
+  VSK_REQUIRE(nq <= 0x7FFFFFFFll, VSK_ERR_INVALID_BUFFER_SIZE, "too many queries");
+  VSK_REQUIRE(allow && allow_bits >= 0, VSK_ERR_INVALID_ARGUMENT,
+              "row filter: null bitmap or negative size");
+  CallScope cs(ctx);
+  for (auto &rec : ctx->screen_redo) rec.clear();
+  // the rows the filter keeps, ascending (so ties still go to the lower row)
+  const int64_t nbits = allow_bits < db->n ? allow_bits : db->n;
+  std::vector<uint32_t> bits((size_t)ceil_div(nbits, 32));
+  if (!bits.empty()) {
+    VSK_HIP(hipMemcpyAsync(bits.data(), allow, sizeof(uint32_t) * bits.size(), hipMemcpyDefault,
+                           ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+  }
+  std::vector<int32_t> rows;
+  for (int64_t r = 0; r < nbits; ++r)
+    if ((bits[(size_t)(r >> 5)] >> (r & 31)) & 1u) rows.push_back((int32_t)r);
+  const int64_t m = (int64_t)rows.size();
+  OutputStage od(ctx, out_dist, sizeof(float) * (size_t)nq * k, "out.dist");
+  OutputStage oi(ctx, out_ids, sizeof(int64_t) * (size_t)nq * k, "out.ids");
+  uint64_t *best = static_cast<uint64_t *>(
+      ctx->scratch_ptr("flat.best", sizeof(uint64_t) * (size_t)nq * k));
+  vsk_db sub;  // (freed after the call's synchronisation below)
+  bool final_keys = true;
+  int64_t *id_map = nullptr;
+  if (m == 0) {
+    fill_u64(ctx, best, nq * (int64_t)k, VSK_KEY_NONE);  // nothing passes
+  } else {
+    sub.n = m;
+    sub.d = db->d;
+    sub.ld = db->ld;
+    sub.x.reserve(sizeof(float) * (size_t)m * db->ld);
+    sub.sqnorm.reserve(sizeof(float) * (size_t)m);
+    sub.norm.reserve(sizeof(float) * (size_t)m);
+    int32_t *drows = static_cast<int32_t *>(
+        ctx->scratch_ptr("flat.frows", sizeof(int32_t) * (size_t)m));
+    id_map = static_cast<int64_t *>(ctx->scratch_ptr("flat.fmap", sizeof(int64_t) * (size_t)m));
+    std::vector<int64_t> map(rows.begin(), rows.end());
+    VSK_HIP(hipMemcpyAsync(drows, rows.data(), sizeof(int32_t) * (size_t)m,
+                           hipMemcpyHostToDevice, ctx->stream));
+    VSK_HIP(hipMemcpyAsync(id_map, map.data(), sizeof(int64_t) * (size_t)m,
+                           hipMemcpyHostToDevice, ctx->stream));
+    {
+      KernelTimer t(ctx, "flat_filter_gather");
+      const int64_t g = ceil_div(m, 4);
+      k_gather_db_rows<<<(unsigned)(g < 65535 * 16 ? g : 65535 * 16), 256, 0, ctx->stream>>>(
+          db->x.as<float>(), db->sqnorm.as<float>(), db->norm.as<float>(), db->ld, drows, m,
+          sub.x.as<float>(), sub.sqnorm.as<float>(), sub.norm.as<float>());
+      check_launch("flat_filter_gather");
+    }
+    const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
+    final_keys = flat_topk_device(ctx, &sub, dq, nq, k, metric, best);
+    // (the host vectors above must outlive their copies)
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+  }
+  decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2 && !final_keys, id_map,
+              od.ptr<float>(), oi.ptr<int64_t>());
+  od.copy_back();
+  oi.copy_back();
+  cs.finish();
+  VSK_API_END(ctx);
+}
 
 vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
                            int64_t nq, int32_t k, int32_t metric,

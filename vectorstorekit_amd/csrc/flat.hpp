@@ -27,6 +27,10 @@ inline int32_t exact_metric(int32_t metric) {
   }
 }
 
+// The 32-bit candidate word that selections skip: the word of a NaN distance
+// and of a candidate a search's row filter excludes.
+constexpr uint32_t kWordNone = 0xFFFFFFFFu;
+
 enum { MODE_DENSE = 0, MODE_FILTER = 1, MODE_MATRIX = 2, MODE_ARGMIN = 3,
        // the screen only: per (query, row split) the smallest key and the
        // second smallest distance (a.cand[q * a.ldm + split] and

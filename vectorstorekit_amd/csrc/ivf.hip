@@ -454,6 +454,67 @@ __global__ __launch_bounds__(256) void k_list_scan_pq_q(ListScanArgs a) {
   }
 }
 
+// A search's row filter in list order: bit v of lmask is set when stored row
+// v may be a candidate, i.e. its id i has 0 <= i < allow_bits and bit i of
+// the caller's bitmap allow (ids the bitmap does not reach are excluded).
+// Each wave writes the two words of its 64 rows.
+__global__ __launch_bounds__(256) void k_allow_list_bits(const int64_t *ids, int64_t total,
+                                                         const uint32_t *allow,
+                                                         int64_t allow_bits, uint32_t *lmask) {
+  const int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  bool ok = false;
+  if (v < total) {
+    const int64_t id = ids[v];
+    ok = id >= 0 && id < allow_bits && ((allow[id >> 5] >> (id & 31)) & 1u);
+  }
+  const uint64_t b = __ballot(ok);
+  const int64_t w0 = v - (threadIdx.x & 63);  // the wave's first row
+  if ((threadIdx.x & 63) == 0 && w0 < total) {
+    lmask[w0 >> 5] = (uint32_t)b;
+    lmask[(w0 >> 5) + 1] = (uint32_t)(b >> 32);
+  }
+}
+
+// Candidates the filter excludes leave their query's ranking: the word at
+// each excluded position becomes kWordNone, which every selection skips
+// (and which the screens' margins never reach).  One workgroup per query
+// walks its probes' lists; the positions are those the list scans write.
+__global__ __launch_bounds__(256) void k_mask_words(const int32_t *probes, int32_t np,
+                                                    const int64_t *pos_base,
+                                                    const int64_t *list_off, const int64_t *wseg,
+                                                    const uint32_t *lmask, uint32_t *words,
+                                                    int64_t nq) {
+  const int64_t q = blockIdx.x;
+  if (q >= nq) return;
+  uint32_t *W = words + wseg[q];
+  for (int p = 0; p < np; ++p) {
+    const int32_t l = probes[q * np + p];
+    if (l < 0) continue;
+    const int64_t v0 = list_off[l], v1 = list_off[l + 1];
+    const int64_t tb = pos_base[q * np + p];
+    for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x)
+      if (!((lmask[v >> 5] >> (v & 31)) & 1u)) W[tb + (v - v0)] = kWordNone;
+  }
+}
+
+// row removal: dst row t = src row idx[t] (ld floats, one wave a row), its
+// id, and (codes non-null) its cstride code bytes (a multiple of 4)
+__global__ void k_gather_stored(const float *src, const int64_t *src_ids, const uint8_t *codes,
+                                int32_t cstride, const int64_t *idx, int64_t n, int32_t ld,
+                                float *dst, int64_t *dst_ids, uint8_t *dst_codes) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6); t < n; t += (int64_t)gridDim.x * 4) {
+    const int64_t s = idx[t];
+    for (int j = lane; j < ld; j += 64) dst[t * ld + j] = src[s * ld + j];
+    if (codes) {
+      const uint32_t *cs = reinterpret_cast<const uint32_t *>(codes + s * cstride);
+      uint32_t *cd = reinterpret_cast<uint32_t *>(dst_codes + t * cstride);
+      for (int j = lane; j < cstride / 4; j += 64) cd[j] = cs[j];
+    }
+    if (lane == 0) dst_ids[t] = src_ids[s];
+  }
+}
+
 // best keys (dist, position) -> (dist, user id)
 __global__ void k_ivf_decode(const uint64_t *best, int64_t nq, int32_t k,
                              const int32_t *probes, int32_t np,
@@ -666,6 +727,11 @@ struct RescoreArgs {
   const uint8_t *active;
   int64_t nq;
   int32_t squared;
+  // every-candidate mode (cnt null): a candidate whose screened word, at
+  // words[wseg[q] + position], is kWordNone (excluded by the row filter)
+  // gets the NONE key (words null: none are excluded)
+  const uint32_t *words;
+  const int64_t *wseg;
 };
 __global__ __launch_bounds__(256) void k_list_rescore(RescoreArgs a) {
 #pragma clang fp contract(off)
@@ -681,8 +747,13 @@ __global__ __launch_bounds__(256) void k_list_rescore(RescoreArgs a) {
   const float *qq = a.Q + q * ld;
   const int64_t *pb = a.list_off ? a.pos_base + q * a.np : nullptr;
   const int32_t *pr = a.list_off ? a.probes + q * a.np : nullptr;
+  const uint32_t *W = !src && a.words ? a.words + a.wseg[q] : nullptr;
   for (int64_t i = lane; i < n; i += 64) {
     const int64_t p = src ? (int64_t)(uint32_t)src[i] : i;
+    if (W && W[p] == kWordNone) {
+      dst[i] = VSK_KEY_NONE;
+      continue;
+    }
     int64_t row = p;
     if (a.list_off) {
       int lo = 0, hi = a.np;
@@ -1209,6 +1280,16 @@ static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes
   }
 }
 
+// the row filter over a batch's candidate words (k_mask_words)
+static void mask_words(vsk_ctx *ctx, const int32_t *probes, int32_t np, const int64_t *pos_base,
+                       const vsk_ivf *ivf, const int64_t *wseg, const uint32_t *lmask,
+                       uint32_t *words, int64_t nb) {
+  KernelTimer t(ctx, "ivf_mask_words");
+  k_mask_words<<<(unsigned)nb, 256, 0, ctx->stream>>>(
+      probes, np, pos_base, ivf->list_off.as<int64_t>(), wseg, lmask, words, nb);
+  check_launch("ivf_mask_words");
+}
+
 // one query batch of the screened list scan: the screened distance of
 // every candidate (a 32-bit word at its position in the query's word
 // segment, wseg), the keys within the margin of the k-th screened distance
@@ -1224,7 +1305,7 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
                               int32_t metric, const int32_t *probes, const int64_t *pos_base,
                               const int64_t *cnt, const int64_t *dseg, const int64_t *wseg,
                               const ListGroups &lg, uint32_t *words, uint64_t *cand,
-                              uint64_t *best) {
+                              uint64_t *best, const uint32_t *lmask) {
   const int32_t ld = ivf->ld, ldb = ivf->xldb, nlist = ivf->nlist;
   const int64_t npairs = nb * np;
   const int32_t *bprobes = probes + b0 * np;
@@ -1248,6 +1329,7 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
 #undef VSK_LS
     check_launch("ivf_list_screen");
   }
+  if (lmask) mask_words(ctx, bprobes, np, bpos, ivf, wseg, lmask, words, nb);
   const int32_t sq = metric == VSK_METRIC_L2SQ ? 1 : 0;
   const float *rows = ivf->rows.as<float>();
   const int64_t *loff = ivf->list_off.as<int64_t>();
@@ -1346,6 +1428,8 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     r.in = cand;
     r.seg_off = dseg;
     r.active = bad;
+    r.words = words;
+    r.wseg = wseg;
     k_list_rescore<<<(unsigned)ceil_div(nb, 4), 256, 0, ctx->stream>>>(r);
     check_launch("ivf_screen_redo");
   }
@@ -1503,10 +1587,13 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
 
 // kind 0: the rows (metric L2 / L2SQ); 1: SQ8 codes, qextra = nq x d int8
 // query codes; 2: PQ codes, qextra = the vsk_pq whose tables score them
+// allow (may be null): the row filter, a bitmap over the stored rows' ids
+// of allow_bits bits (k_allow_list_bits)
 static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                                  const void *qextra, int64_t nq, int32_t nprobe, int32_t k,
                                  int32_t metric, int32_t kind, void *out_dist,
-                                 int64_t *out_ids) {
+                                 int64_t *out_ids, const uint32_t *allow = nullptr,
+                                 int64_t allow_bits = 0) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
   if (kind == 0)
@@ -1538,6 +1625,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   VSK_REQUIRE(k <= VSK_MAX_K, VSK_ERR_INVALID_BUFFER_SIZE,
               "k exceeds VSK_MAX_K");
   VSK_REQUIRE(nprobe >= 1, VSK_ERR_INVALID_ARGUMENT, "nprobe must be >= 1");
+  VSK_REQUIRE(allow_bits >= 0 && (allow || allow_bits == 0), VSK_ERR_INVALID_ARGUMENT,
+              "row filter: null bitmap or negative size");
   const int32_t np = nprobe < ivf->nlist ? nprobe : ivf->nlist;  // .exact
   VSK_REQUIRE(np <= VSK_MAX_K || np == ivf->nlist, VSK_ERR_INVALID_ARGUMENT,
               "nprobe must be <= VSK_MAX_K or cover every list");
@@ -1565,6 +1654,19 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   }
   OutputStage od(ctx, out_dist, sizeof(float) * nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * nq * k, "out.ids");
+  // the row filter in list order (one bit per stored row)
+  uint32_t *lmask = nullptr;
+  if (allow && ivf->total > 0) {
+    const uint32_t *dallow = static_cast<const uint32_t *>(input_to_device(
+        ctx, allow, sizeof(uint32_t) * (size_t)ceil_div(allow_bits, 32), "ivf.allow"));
+    const int64_t blocks = ceil_div(ivf->total, 256);
+    lmask = static_cast<uint32_t *>(
+        ctx->scratch_ptr("ivf.lmask", sizeof(uint32_t) * (size_t)(8 * blocks)));
+    KernelTimer t(ctx, "ivf_allow_bits");
+    k_allow_list_bits<<<(unsigned)blocks, 256, 0, ctx->stream>>>(
+        ivf->ids.as<int64_t>(), ivf->total, dallow, allow_bits, lmask);
+    check_launch("ivf_allow_bits");
+  }
 
   // the bf16 screen of the list scan (kind 0) and of the probe share the
   // queries' bf16 planes
@@ -1676,7 +1778,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     }
     if (screen) {
       list_screen_batch(ctx, ivf, sqp.two, dq, b0, nb, np, k, metric, probes, pos_base, cnt,
-                        dseg, wseg, lgp, swords, cand, best);
+                        dseg, wseg, lgp, swords, cand, best, lmask);
       continue;
     }
     const int64_t *ngroups = gstart + nlist;
@@ -1721,6 +1823,8 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
 #undef VSK_SCAN_QG
       check_launch(names[kind]);
     }
+    if (lmask)
+      mask_words(ctx, la.probes, np, la.pos_base, ivf, wseg, lmask, la.words, nb);
     // 4. selection per query segment
     WordSelectArgs sa;
     sa.nq = nb;
@@ -1777,6 +1881,16 @@ vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
   return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids);
 }
 
+vsk_status vsk_ivf_search_filtered(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                                   int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
+                                   const uint32_t *allow, int64_t allow_bits, float *out_dist,
+                                   int64_t *out_ids) {
+  if (!allow && allow_bits == 0)
+    return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids);
+  return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids,
+                        allow, allow_bits);
+}
+
 vsk_status vsk_ivf_search_sq8(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                               const int8_t *qcodes, int64_t nq, int32_t nprobe, int32_t k,
                               int32_t *out_score, int64_t *out_ids) {
@@ -1787,6 +1901,90 @@ vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
                              const float *q, int64_t nq, int32_t nprobe, int32_t k,
                              float *out_dist, int64_t *out_ids) {
   return ivf_search_any(ctx, ivf, q, pq, nq, nprobe, k, -1, 2, out_dist, out_ids);
+}
+
+vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_t n,
+                          int64_t *removed) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(n >= 0 && (ids || n == 0), VSK_ERR_INVALID_ARGUMENT, "null ids");
+  if (removed) *removed = 0;
+  if (n > 0 && ivf->total > 0) {
+    CallScope cs(ctx);
+    std::vector<int64_t> want((size_t)n), hids((size_t)ivf->total);
+    VSK_HIP(hipMemcpyAsync(want.data(), ids, sizeof(int64_t) * (size_t)n, hipMemcpyDefault,
+                           ctx->stream));
+    VSK_HIP(hipMemcpyAsync(hids.data(), ivf->ids.p, sizeof(int64_t) * hids.size(),
+                           hipMemcpyDeviceToHost, ctx->stream));
+    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    std::sort(want.begin(), want.end());
+    // the rows kept, list by list in their order
+    std::vector<int64_t> keep, off((size_t)ivf->nlist + 1);
+    keep.reserve(hids.size());
+    for (int32_t l = 0; l < ivf->nlist; ++l) {
+      off[(size_t)l] = (int64_t)keep.size();
+      for (int64_t v = ivf->off[(size_t)l]; v < ivf->off[(size_t)l + 1]; ++v)
+        if (!std::binary_search(want.begin(), want.end(), hids[(size_t)v])) keep.push_back(v);
+    }
+    off[(size_t)ivf->nlist] = (int64_t)keep.size();
+    const int64_t m = (int64_t)keep.size(), gone = ivf->total - m;
+    if (gone > 0) {
+      const bool codes = ivf->ckind != 0 && ivf->ctotal == ivf->total;
+      DevBuf rows, nids, ncodes, didx, doff;
+      rows.reserve(sizeof(float) * (size_t)m * ivf->ld);
+      nids.reserve(sizeof(int64_t) * (size_t)m);
+      if (codes) {
+        ncodes.reserve((size_t)m * ivf->cstride + 16);
+        fill_i32(ctx, ncodes.as<int32_t>(), ((int64_t)m * ivf->cstride + 16) / 4, 0);
+      }
+      didx.reserve(sizeof(int64_t) * (size_t)m);
+      doff.reserve(sizeof(int64_t) * off.size());
+      VSK_HIP(hipMemcpyAsync(didx.p, keep.data(), sizeof(int64_t) * (size_t)m,
+                             hipMemcpyHostToDevice, ctx->stream));
+      VSK_HIP(hipMemcpyAsync(doff.p, off.data(), sizeof(int64_t) * off.size(),
+                             hipMemcpyHostToDevice, ctx->stream));
+      if (m > 0) {
+        k_gather_stored<<<grid1(m, 4), 256, 0, ctx->stream>>>(
+            ivf->rows.as<float>(), ivf->ids.as<int64_t>(),
+            codes ? ivf->codes.as<uint8_t>() : nullptr, ivf->cstride, didx.as<int64_t>(), m,
+            ivf->ld, rows.as<float>(), nids.as<int64_t>(), ncodes.as<uint8_t>());
+        check_launch("ivf_remove_gather");
+      }
+      VSK_HIP(hipStreamSynchronize(ctx->stream));
+      std::swap(ivf->rows.p, rows.p);
+      std::swap(ivf->rows.bytes, rows.bytes);
+      std::swap(ivf->ids.p, nids.p);
+      std::swap(ivf->ids.bytes, nids.bytes);
+      std::swap(ivf->list_off.p, doff.p);
+      std::swap(ivf->list_off.bytes, doff.bytes);
+      if (codes) {
+        std::swap(ivf->codes.p, ncodes.p);
+        std::swap(ivf->codes.bytes, ncodes.bytes);
+      }
+      ivf->off.swap(off);
+      ivf->total = m;
+      // codes made before later inserts stay stale (the count must not
+      // come to match again)
+      ivf->ctotal = codes ? m : -1;
+      ++ivf->version;
+    }
+    cs.finish();
+    if (removed) *removed = gone;
+  }
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_list_ids(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t *ids, int64_t *offsets) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  if (offsets) std::memcpy(offsets, ivf->off.data(), sizeof(int64_t) * ivf->off.size());
+  if (ids && ivf->total > 0) {
+    CallScope cs(ctx);
+    VSK_HIP(hipMemcpyAsync(ids, ivf->ids.p, sizeof(int64_t) * (size_t)ivf->total,
+                           hipMemcpyDefault, ctx->stream));
+    cs.finish();
+  }
+  VSK_API_END(ctx);
 }
 
 vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,

@@ -450,7 +450,6 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select_small(SelectArgs a) {
 // outside the prefix counts into one of 32 spare bins).  REG words per
 // thread stay in registers when the list fits, loaded 16 bytes at a time;
 // longer lists are read from memory on every pass.
-constexpr uint32_t kWordNone = 0xFFFFFFFFu;  // no distance has this word
 
 struct WordShared {
   uint32_t hist[256 + 32];
@@ -917,9 +916,13 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const int64_t base = t.seg_off ? t.seg_off[q] : q * t.all_n;
   const int64_t n = t.seg_off ? t.seg_off[q + 1] - base : t.all_n;
   uint64_t *A = t.all + base;
+  // (a candidate the row filter excluded has the word kWordNone: no key)
+  const uint32_t *W = a.words + (a.wseg ? a.wseg[q] : q * a.wstride);
   for (int64_t i = tid; i < n; i += SEL_THREADS)
-    A[i] = vsk_key(tail_exact(t.rows + tail_row(t, q, i) * t.ld, s_q, t.ld, t.squared),
-                   (uint32_t)i);
+    A[i] = W[i] == kWordNone
+               ? VSK_KEY_NONE
+               : vsk_key(tail_exact(t.rows + tail_row(t, q, i) * t.ld, s_q, t.ld, t.squared),
+                         (uint32_t)i);
   __threadfence_block();
   __syncthreads();
   auto each_key = [&](auto &&f) {

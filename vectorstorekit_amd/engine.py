@@ -199,16 +199,26 @@ class VectorDatabase:
                                                     count, out.ctypes.data))
         return out
 
-    def search(self, queries, k: int, metric="euclidean"):
+    def search(self, queries, k: int, metric="euclidean", allow=None):
         """Exact top-k: (distances [nq, k] float32, ids [nq, k] int64),
         ascending (distance, id).  Outputs are torch tensors on the device
-        when ``queries`` is a CUDA tensor, else numpy arrays."""
+        when ``queries`` is a CUDA tensor, else numpy arrays.  ``allow``
+        (optional) keeps only some rows as candidates: a boolean array over
+        the rows or the allowed row indices (``vsk_search_flat_filtered``)."""
         nq = int(queries.shape[0])
         qp, qk = as_buffer(queries, np.float32, (nq, self.d))
         dp, dist = out_buffer((nq, k), np.float32, queries)
         ip, ids = out_buffer((nq, k), np.int64, queries)
-        self.ctx.check(self.ctx.lib.vsk_search_flat(self.ctx.handle, self.handle, qp, nq,
-                                                    k, metric_code(metric), dp, ip))
+        if allow is None:
+            self.ctx.check(self.ctx.lib.vsk_search_flat(self.ctx.handle, self.handle, qp, nq,
+                                                        k, metric_code(metric), dp, ip))
+        else:
+            a = np.asarray(allow)
+            bm = _lib.row_bitmap(a, self.n)
+            nbits = int(a.size) if a.dtype == np.bool_ else self.n
+            self.ctx.check(self.ctx.lib.vsk_search_flat_filtered(
+                self.ctx.handle, self.handle, qp, nq, k, metric_code(metric), bm.ctypes.data,
+                nbits, dp, ip))
         del qk
         return dist, ids
 

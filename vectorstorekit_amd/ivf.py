@@ -17,7 +17,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import VSKError, as_buffer, out_buffer
+from ._lib import VSKError, as_buffer, out_buffer, row_bitmap
 from .clustering import ClusteringResult, KMeansClustering, KMeansClusteringConfiguration
 from .engine import Context, metric_code
 
@@ -52,6 +52,7 @@ class IVFIndex:
         self._centroids = None
         self._sq8 = None  # the quantizers the stored codes were made with
         self._pq = None
+        self.savedExtra = None
 
     @property
     def trained(self) -> bool:
@@ -136,9 +137,12 @@ class IVFIndex:
         return out
 
     def search(self, queries, k: int, strategy: str = "approximate", nprobe=None,
-               metric="euclidean"):
+               metric="euclidean", allow=None, allow_bits=None):
         """Top k by L2 over the probed lists; ``metric`` is "euclidean"
-        (the reference's sqrt distance) or "euclideanSquared"."""
+        (the reference's sqrt distance) or "euclideanSquared".  ``allow``
+        (optional) filters the candidates before they are ranked, as
+        IVFIndex.search's filter does (:161-176): a boolean array over the
+        row ids, or the allowed ids (``vsk_ivf_search_filtered``)."""
         self._need()
         if strategy == "exact":
             nprobe = self.configuration.numberOfCentroids
@@ -150,9 +154,41 @@ class IVFIndex:
         qp, qk = as_buffer(q, np.float32, (nq, self.configuration.dimensions))
         dp, dist = out_buffer((nq, k), np.float32, q)
         ip, ids = out_buffer((nq, k), np.int64, q)
-        self.ctx.check(self.ctx.lib.vsk_ivf_search(self.ctx.handle, self.handle, qp, nq,
-                                                   nprobe, k, metric_code(metric), dp, ip))
+        if allow is None:
+            self.ctx.check(self.ctx.lib.vsk_ivf_search(self.ctx.handle, self.handle, qp, nq,
+                                                       nprobe, k, metric_code(metric), dp, ip))
+        else:
+            bm = row_bitmap(allow, allow_bits)
+            nbits = (int(np.asarray(allow).size) if np.asarray(allow).dtype == np.bool_
+                     else int(bm.size * 32))
+            self.ctx.check(self.ctx.lib.vsk_ivf_search_filtered(
+                self.ctx.handle, self.handle, qp, nq, nprobe, k, metric_code(metric),
+                bm.ctypes.data, nbits, dp, ip))
         return dist, ids
+
+    def remove(self, ids) -> int:
+        """IVFIndex.delete(id:) for device ids (:210-220): every stored row
+        with one of these ids leaves its list (``vsk_ivf_remove``); returns
+        how many rows were removed."""
+        self._need()
+        a = np.ascontiguousarray(np.asarray(ids, np.int64).reshape(-1))
+        out = ctypes.c_int64(0)
+        self.ctx.check(self.ctx.lib.vsk_ivf_remove(self.ctx.handle, self.handle, a.ctypes.data,
+                                                   a.size, ctypes.byref(out)))
+        return int(out.value)
+
+    def listIds(self):
+        """getVectorsFromList for every list (:487-490): (ids in list
+        order, offsets[nlist + 1])."""
+        self._need()
+        off = np.empty(self.configuration.numberOfCentroids + 1, np.int64)
+        self.ctx.check(self.ctx.lib.vsk_ivf_list_ids(self.ctx.handle, self.handle, None,
+                                                     off.ctypes.data))
+        ids = np.empty(int(off[-1]), np.int64)
+        if ids.size:
+            self.ctx.check(self.ctx.lib.vsk_ivf_list_ids(self.ctx.handle, self.handle,
+                                                         ids.ctypes.data, None))
+        return ids, off
 
     # ---- quantized lists (IVFConfiguration's declared quantization,
     # Config/Indexes/IVFConfiguration.swift:13,18-21, which IVFIndex leaves
@@ -218,12 +254,14 @@ class IVFIndex:
 
     # ---- index file (the whole index; the reference's persistence keeps
     # only the configuration and centroids, Indexes/IVFIndex.swift:297-328)
-    def save(self, path: str):
+    def save(self, path: str, extra=None):
         """The index, its codes and quantizer parameters, and this
-        configuration (as JSON in the file's metadata) in one file."""
+        configuration (as JSON in the file's metadata) in one file.
+        ``extra`` (JSON-serialisable, optional) is kept with it and comes
+        back as ``savedExtra`` of the loaded index."""
         self._need()
         cfg = self.configuration
-        meta = json.dumps({
+        meta = json.dumps({"extra": extra,
             "dimensions": cfg.dimensions, "numberOfCentroids": cfg.numberOfCentroids,
             "numberOfProbes": cfg.numberOfProbes,
             "clusteringConfig": {"maxIterations": cfg.clusteringConfig.maxIterations,
@@ -286,6 +324,7 @@ class IVFIndex:
         idx = cls(ctx, cfg)
         idx.handle = h
         idx._centroids = cent
+        idx.savedExtra = meta.get("extra")
         if kind.value == 1:
             idx._sq8 = sq
         elif kind.value == 2:
