@@ -124,6 +124,12 @@ void *vsk_stream(vsk_ctx *ctx);
  * MetalProfiler.recordOperation (Acceleration/Metal/MetalProfiler.swift:
  * 74-110). */
 float vsk_last_kernel_ms(const vsk_ctx *ctx);
+/* How often the last API call on ctx waited on the host for its stream
+ * (the call's final synchronisation included).  A search is queued whole
+ * and waits once; more waits mean a rare path ran (a query whose top-k
+ * candidates overflowed, or that failed the screen's bound) or a buffer
+ * grew.  A diagnostic with no counterpart in the reference. */
+int32_t vsk_last_sync_count(const vsk_ctx *ctx);
 /* Which queries of the last vsk_search_flat call on ctx the exact screen
  * redid: tier 1 = screened again keeping 1024 candidates, tier 2 = the
  * exact scan over every row (queries whose bound test failed; see
@@ -369,15 +375,17 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
                           int32_t *out_score, int64_t *out_ids);
 
 /* No counterpart in the reference: vsk_sq8_search without any device
- * allocation, for callers that cannot allocate (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments and results as vsk_sq8_search, bit for bit, but qcodes,
- * out_score and out_ids must be device memory, and the working buffers
- * (candidate keys, thresholds, counters, padded query codes) live in one
- * static 64 MiB device array per GPU, held until the process ends.  Queries
- * run in batches that fit it; a (k, d) whose single query does not fit
- * returns VSK_ERR_INVALID_BUFFER_SIZE.  Every call on one GPU shares that
- * array: calls that overlap on one GPU (several contexts or threads) race. */
+ * allocation, for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * vsk_sq8_search, bit for bit, but qcodes, out_score and out_ids must be
+ * device memory, and the working buffers (candidate keys, thresholds,
+ * counters, padded query codes) live in one static 64 MiB device array per
+ * GPU, held until the process ends.  Queries run in batches that fit it; a
+ * (k, d) whose single query does not fit returns
+ * VSK_ERR_INVALID_BUFFER_SIZE.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (several contexts or threads) race.  The
+ * call waits for the context's own stream before it returns (as every call
+ * does), so it cannot be captured into a HIP graph. */
 vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
                                   const int8_t *qcodes, int64_t nq, int32_t k,
                                   int32_t *out_score, int64_t *out_ids);

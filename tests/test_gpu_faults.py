@@ -73,3 +73,32 @@ def test_unarmed_and_malformed_specs_do_nothing():
         np.testing.assert_array_equal(gi, oi)
         db.free()
         ctx.close()
+
+
+@pytest.mark.parametrize("spec", ["launch:3", "sync:2"])
+def test_profile_reset_after_failed_profiled_call(spec):
+    """With per-kernel timing on, a call that fails after some of its
+    timers closed leaves no pending timings behind: vsk_profile_reset and
+    the next call see clean statistics (the next call's timings name only
+    statistics that exist)."""
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((4000, 32)).astype(np.float32)
+    q = rng.standard_normal((30, 32)).astype(np.float32)
+    ctx = _armed(spec)
+    ctx.profile(True)
+    db = VectorDatabase(ctx, x)
+    raised = None
+    try:
+        for _ in range(3):
+            db.search(q, 10, "euclideanSquared")
+    except VSKError as e:
+        raised = e
+    assert raised is not None, "the armed fault did not fire"
+    ctx.profile_reset()
+    gd, gi = db.search(q, 10, "euclideanSquared")
+    od, oi = O.search_flat(q, x, 10, O.L2SQ)
+    np.testing.assert_array_equal(gi, oi)
+    stats = ctx.profile_stats()
+    assert stats and all(v[0] >= 1 for v in stats.values())
+    db.free()
+    ctx.close()

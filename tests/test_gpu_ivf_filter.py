@@ -233,3 +233,41 @@ def test_config3_filter_and_delete(ctx):
     gd, gi = idx.search(qh[:4], 100)
     for i in range(4):
         assert not set(gi[i].tolist()) & set(near[i].tolist())
+
+
+def test_exact_strategy_ties_follow_probe_order(ctx):
+    """.exact over more lists than a selection holds (1,100 > 1,024): the
+    reference concatenates the lists in findNearestCentroids' order (by
+    distance, then centroid index) and stable-sorts, so of two rows at
+    exactly the same distance the one in the nearer list comes first even
+    when its centroid index is higher.  Rows +-delta*e0 around the query
+    (distance delta both) sit in list 5 (far) and list 900 (near)."""
+    d, nlist = 8, 1100
+    rng = np.random.default_rng(17)
+    c = (100.0 + 10.0 * rng.standard_normal((nlist, d))).astype(np.float32)
+    delta = np.float32(0.25)
+    c[5] = 0
+    c[5, 0] = 2 * delta          # nearest to +delta e0; 2 delta from the query
+    c[900] = 0
+    c[900, 0] = -1.5 * delta     # nearest to -delta e0; 1.5 delta from the query
+    x = (100.0 + 10.0 * rng.standard_normal((3000, d))).astype(np.float32)
+    a = np.zeros(d, np.float32)
+    a[0] = delta
+    x[100], x[2000] = a, -a       # row 100 in list 5, row 2000 in list 900
+    q = np.zeros((1, d), np.float32)
+    idx = _index(ctx, c, x, 8)
+    lists = O.ivf_assign(x, c)
+    assert lists[100] == 5 and lists[2000] == 900
+    gd, gi = idx.search(q, 2, strategy="exact")
+    od, oi = O.ivf_search(q, x, np.arange(len(x)), lists, c, nlist, 2)
+    assert list(oi[0]) == [2000, 100]
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+    # and with more queries and rows, every result
+    q2 = (100.0 + 10.0 * rng.standard_normal((40, d))).astype(np.float32)
+    x2 = np.concatenate([x, x[:500]])  # exact duplicates in the same lists
+    idx2 = _index(ctx, c, x2, 8)
+    gd, gi = idx2.search(q2, 20, strategy="exact")
+    od, oi = O.ivf_search(q2, x2, np.arange(len(x2)), O.ivf_assign(x2, c), c, nlist, 20)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)

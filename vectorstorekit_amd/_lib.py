@@ -90,6 +90,7 @@ SIGNATURES = {
     "vsk_last_error": (c_char_p, [P]),
     "vsk_stream": (c_void_p, [P]),
     "vsk_last_kernel_ms": (c_float, [P]),
+    "vsk_last_sync_count": (c_int32, [P]),
     "vsk_last_screen_redo": (c_int32, [P, c_int32, P, c_int64, P]),
     "vsk_measure_peaks": (c_int32, [P, POINTER(vsk_peaks)]),
     "vsk_profile_enable": (c_int32, [P, c_int32]),

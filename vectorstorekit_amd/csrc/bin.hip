@@ -549,12 +549,12 @@ vsk_status vsk_bin_upload(vsk_ctx *ctx, const uint8_t *codes, int64_t n, int32_t
 
 vsk_status vsk_bin_free(vsk_ctx *ctx, vsk_bin *bin) {
   VSK_API_BEGIN(ctx);
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   delete bin;
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
+static vsk_status bin_search_body(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
                           int64_t nq, int32_t k, int32_t *out_dist, int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
   VSK_REQUIRE(bin, VSK_ERR_INVALID_ARGUMENT, "bin is null");
@@ -629,6 +629,12 @@ vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcode
   oi.copy_back();
   cs.finish();
   VSK_API_END(ctx);
+}
+
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_bin_search(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,
+                          int64_t nq, int32_t k, int32_t *out_dist, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return bin_search_body(ctx, bin, qcodes, nq, k, out_dist, out_ids); });
 }
 
 vsk_status vsk_bin_distances(vsk_ctx *ctx, const vsk_bin *bin, const uint8_t *qcodes,

@@ -77,10 +77,24 @@ bool is_device_ptr(const void *p) {
 CallScope::CallScope(vsk_ctx *c) : ctx(c) {
   VSK_HIP(hipEventRecord(ctx->call_begin, ctx->stream));
 }
+void stream_sync(vsk_ctx *ctx) {
+  ++ctx->sync_count;
+  VSK_HIP(hipStreamSynchronize(ctx->stream));
+}
+
 void CallScope::finish() {
   if (ctx->aux) VSK_HIP(hipStreamSynchronize(ctx->aux));
+  // the deferred top-k overflow count comes back with the final sync
+  const bool armed = ctx->ovf_armed;
+  if (armed)
+    VSK_HIP(hipMemcpyAsync(ctx->ovf_host, ctx->ovf_dev, sizeof(int32_t),
+                           hipMemcpyDeviceToHost, ctx->stream));
   VSK_HIP(hipEventRecord(ctx->call_end, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
+  if (armed) {
+    ctx->ovf_armed = false;
+    if (ctx->ovf_host[0] > 0) ctx->topk_overflowed = true;
+  }
   float ms = 0.f;
   VSK_HIP(hipEventElapsedTime(&ms, ctx->call_begin, ctx->call_end));
   ctx->last_ms = ms;
@@ -357,6 +371,7 @@ void *vsk_ctx::scratch_ptr(const std::string &key, size_t bytes) {
   if (!b) b.reset(new vsk::DevBuf());
   if (b->bytes < bytes || !b->p) {
     // a buffer in use by queued work must not be freed under it
+    ++sync_count;
     VSK_HIP(hipStreamSynchronize(stream));
     if (aux) VSK_HIP(hipStreamSynchronize(aux));
     b->reserve(bytes + bytes / 8);
@@ -370,6 +385,7 @@ hipStream_t vsk_ctx::aux_stream() {
 void *vsk_ctx::pinned_ptr(size_t bytes) {
   if (pinned_bytes < bytes) {
     if (pinned) {
+      ++sync_count;
       VSK_HIP(hipStreamSynchronize(stream));
       if (aux) VSK_HIP(hipStreamSynchronize(aux));
       (void)hipHostFree(pinned);
@@ -401,10 +417,19 @@ hipEvent_t vsk_ctx::take_timer_event() {
   VSK_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
   return e;
 }
+void vsk_ctx::drop_pending() {
+  for (auto &p : pending) {
+    timer_pool.push_back(p.a);
+    timer_pool.push_back(p.b);
+  }
+  pending.clear();
+  work_used = 0;
+}
+
 void vsk_ctx::resolve_pending() {
   for (auto &p : pending) {
     float ms = 0.f;
-    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+    if (p.stat < (int)stats.size() && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
       stats[p.stat].launches += 1;
       stats[p.stat].total_ms += ms;
       stats[p.stat].work += p.work_slot >= 0 ? (double)work_pinned[p.work_slot] : p.work;
@@ -463,7 +488,15 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   // device buffers produced there (e.g. by torch) are complete when read
   if (hipStreamCreate(&c->stream) != hipSuccess ||
       hipEventCreate(&c->call_begin) != hipSuccess ||
-      hipEventCreate(&c->call_end) != hipSuccess) {
+      hipEventCreate(&c->call_end) != hipSuccess ||
+      hipMalloc(reinterpret_cast<void **>(&c->ovf_dev), 256) != hipSuccess ||
+      hipHostMalloc(reinterpret_cast<void **>(&c->ovf_host), 8 * sizeof(int32_t),
+                    hipHostMallocDefault) != hipSuccess) {
+    (void)hipGetLastError();
+    if (c->ovf_dev) (void)hipFree(c->ovf_dev);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->call_begin) (void)hipEventDestroy(c->call_begin);
+    if (c->call_end) (void)hipEventDestroy(c->call_end);
     delete c;
     return VSK_ERR_DEVICE_NOT_AVAILABLE;
   }
@@ -483,6 +516,8 @@ vsk_status vsk_destroy(vsk_ctx *ctx) {
   if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
   if (ctx->pinned) (void)hipHostFree(ctx->pinned);
   if (ctx->work_pinned) (void)hipHostFree(ctx->work_pinned);
+  if (ctx->ovf_host) (void)hipHostFree(ctx->ovf_host);
+  if (ctx->ovf_dev) (void)hipFree(ctx->ovf_dev);
   ctx->scratch.clear();
   (void)hipEventDestroy(ctx->call_begin);
   (void)hipEventDestroy(ctx->call_end);
@@ -496,6 +531,7 @@ const char *vsk_last_error(const vsk_ctx *ctx) {
 }
 void *vsk_stream(vsk_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 float vsk_last_kernel_ms(const vsk_ctx *ctx) { return ctx ? ctx->last_ms : 0.f; }
+int32_t vsk_last_sync_count(const vsk_ctx *ctx) { return ctx ? ctx->sync_count : 0; }
 
 vsk_status vsk_last_screen_redo(const vsk_ctx *ctx, int32_t tier, int64_t *out,
                                 int64_t cap, int64_t *count) {
@@ -550,6 +586,11 @@ vsk_status vsk_profile_only(vsk_ctx *ctx, const char *names) {
 }
 vsk_status vsk_profile_reset(vsk_ctx *ctx) {
   if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
+  // timings of a failed call that were never resolved name stats that are
+  // about to go
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  ctx->drop_pending();
   ctx->stats.clear();
   ctx->stat_index.clear();
   return VSK_OK;

@@ -467,7 +467,7 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                h + (size_t)db->n * ldb, ldb, nullptr, nullptr, mb);
     uint32_t hb[2];
     VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
     std::memcpy(&db->split_max_hi, &hb[0], sizeof(float));
     std::memcpy(&db->split_max_res, &hb[1], sizeof(float));
   }
@@ -488,7 +488,8 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
 
 // top-k over a resident database for queries already on the device
 bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
-                      int64_t nq, int32_t k, int32_t metric, uint64_t *best) {
+                      int64_t nq, int32_t k, int32_t metric, uint64_t *best,
+                      ScreenDeferred *defer) {
   // a small problem (at most 2^28 query x row x dimension terms, some 20 us
   // of exact VALU work) is cheaper by the exact sequential scan alone than
   // by the screen's fixed chain of launches and its check read-back
@@ -498,7 +499,7 @@ bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
     return true;
   }
   if (!ctx->flat_no_screen && screen_applies(metric, k)) {
-    screen_topk(ctx, db, dq, nq, k, metric, best);
+    screen_topk(ctx, db, dq, nq, k, metric, best, defer);
     return true;
   }
   approx_topk(ctx, db, dq, nq, k, metric, best, 3);
@@ -576,7 +577,7 @@ using namespace vsk;
 
 extern "C" {
 
-vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float *q,
+static vsk_status search_flat_filtered_body(vsk_ctx *ctx, const vsk_db *db, const float *q,
                                     int64_t nq, int32_t k, int32_t metric,
                                     const uint32_t *allow, int64_t allow_bits,
                                     float *out_dist, int64_t *out_ids) {
@@ -600,7 +601,7 @@ vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float 
   if (!bits.empty()) {
     VSK_HIP(hipMemcpyAsync(bits.data(), allow, sizeof(uint32_t) * bits.size(), hipMemcpyDefault,
                            ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
   }
   std::vector<int32_t> rows;
   for (int64_t r = 0; r < nbits; ++r)
@@ -641,7 +642,7 @@ vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float 
     const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
     final_keys = flat_topk_device(ctx, &sub, dq, nq, k, metric, best);
     // (the host vectors above must outlive their copies)
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
   }
   decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2 && !final_keys, id_map,
               od.ptr<float>(), oi.ptr<int64_t>());
@@ -651,7 +652,15 @@ vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float 
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                                    int64_t nq, int32_t k, int32_t metric,
+                                    const uint32_t *allow, int64_t allow_bits,
+                                    float *out_dist, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return search_flat_filtered_body(ctx, db, q, nq, k, metric, allow, allow_bits, out_dist, out_ids); });
+}
+
+static vsk_status search_flat_body(vsk_ctx *ctx, const vsk_db *db, const float *q,
                            int64_t nq, int32_t k, int32_t metric,
                            float *out_dist, int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
@@ -671,7 +680,9 @@ vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
   const float *dq = rows_to_device_padded(ctx, q, nq, db->d, db->ld, "flat.q");
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("flat.best", sizeof(uint64_t) * (size_t)nq * k));
-  const bool final_keys = flat_topk_device(ctx, db, dq, nq, k, metric, best);
+  // the screen's bound check is read with the call's synchronisation
+  ScreenDeferred defer;
+  const bool final_keys = flat_topk_device(ctx, db, dq, nq, k, metric, best, &defer);
   OutputStage od(ctx, out_dist, sizeof(float) * (size_t)nq * k, "out.dist");
   OutputStage oi(ctx, out_ids, sizeof(int64_t) * (size_t)nq * k, "out.ids");
   decode_keys(ctx, best, nq * (int64_t)k, metric == VSK_METRIC_L2 && !final_keys,
@@ -679,7 +690,23 @@ vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
   od.copy_back();
   oi.copy_back();
   cs.finish();
+  // queries that failed the bound (near ties) are redone now and the
+  // results written again; an overflowed top-k reruns the whole call
+  if (!ctx->topk_overflowed && screen_finish(ctx, db, dq, k, metric, best, defer)) {
+    decode_keys(ctx, best, nq * (int64_t)k, false, nullptr, od.ptr<float>(),
+                oi.ptr<int64_t>());
+    od.copy_back();
+    oi.copy_back();
+    cs.finish();
+  }
   VSK_API_END(ctx);
+}
+
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
+                           int64_t nq, int32_t k, int32_t metric,
+                           float *out_dist, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return search_flat_body(ctx, db, q, nq, k, metric, out_dist, out_ids); });
 }
 
 vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,

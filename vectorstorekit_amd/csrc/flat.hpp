@@ -216,8 +216,10 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin);
 // best: nq*k keys.  Returns true when the keys hold the final distances
 // (the screen path: exact fp32, sqrt applied for L2), false when they hold
 // the kernel's distances (squared for L2).
+struct ScreenDeferred;
 bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
-                      int64_t nq, int32_t k, int32_t metric, uint64_t *best);
+                      int64_t nq, int32_t k, int32_t metric, uint64_t *best,
+                      ScreenDeferred *defer = nullptr);
 // progressive top-k on the bf16 kernel with the given passes (3: fp32-level
 // distances; 1: the screen's hi products) or, for L1, the exact VALU kernel;
 // qnh/qnr (optional): per-query |hi| and |q - hi| of the split;
@@ -284,8 +286,31 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
 // scan); best: final keys (exact distances)
 bool screen_applies(int32_t metric, int32_t k);
 int32_t screen_keep(int32_t k);
+// With defer, screen_topk queues every batch without waiting for the bound
+// check: each batch's count of failing queries goes to pinned memory with
+// the stream, and screen_finish, called after the caller's synchronisation,
+// redoes the failing queries (rare) -- true when it redid any (best then
+// holds their new keys).
+struct ScreenDeferred {
+  struct Batch {
+    int64_t b0, nb;
+  };
+  std::vector<Batch> batches;
+  int32_t *fails_host = nullptr;  // pinned, one count per batch
+  uint8_t *ok = nullptr;          // device, per query
+  int32_t kc = 0;
+  bool active = false;
+};
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
-                 int32_t k, int32_t metric, uint64_t *best);
+                 int32_t k, int32_t metric, uint64_t *best,
+                 ScreenDeferred *defer = nullptr);
+bool screen_finish(vsk_ctx *ctx, const vsk_db *db, const float *dq, int32_t k,
+                   int32_t metric, uint64_t *best, ScreenDeferred &defer);
+
+// out[s * len ...] = the keys of in[s * len ...] sorted ascending, for
+// each of nseg segments of len keys (at most 2^31 - 1 keys in all)
+void segmented_sort_u64(vsk_ctx *ctx, const uint64_t *in, uint64_t *out, int64_t nseg,
+                        int64_t len);
 
 // a PQ quantizer's shape for other translation units: returns d
 int32_t pq_shape(const vsk_pq *pq, int32_t *M, int32_t *ksub);

@@ -261,18 +261,25 @@ static void rescore_select(vsk_ctx *ctx, const vsk_db *db, const float *dq,
 // bound test, exact rescore and select into best (nb x k; rows of failing
 // queries are written too but must be redone).  Returns the failing query
 // indices.
+// With fail_host (pinned), the tier does not wait for the check: ok_out
+// (nb bytes of device memory) keeps each query's result and the failing
+// count goes to *fail_host with the stream; the caller redoes the failing
+// queries after its synchronisation (screen_finish).
 static std::vector<int32_t> screen_tier(vsk_ctx *ctx, const vsk_db *db,
                                         const float *qbat, int64_t nb, int32_t k,
                                         int32_t kc, int32_t metric,
-                                        uint64_t *best, const char *tag) {
+                                        uint64_t *best, const char *tag,
+                                        uint8_t *ok_out = nullptr,
+                                        int32_t *fail_host = nullptr) {
   uint64_t *cand = static_cast<uint64_t *>(ctx->scratch_ptr(
       std::string("screen.cand") + tag, sizeof(uint64_t) * (size_t)nb * kc));
   float *qn = static_cast<float *>(ctx->scratch_ptr(
       std::string("screen.qnorm") + tag, sizeof(float) * 2 * (size_t)nb));
   approx_topk(ctx, db, qbat, nb, kc, metric, cand, 1, qn, qn + nb, 8);
 
-  uint8_t *ok = static_cast<uint8_t *>(
-      ctx->scratch_ptr(std::string("screen.ok") + tag, (size_t)nb));
+  uint8_t *ok = ok_out ? ok_out
+                      : static_cast<uint8_t *>(
+                            ctx->scratch_ptr(std::string("screen.ok") + tag, (size_t)nb));
   int32_t *nvalid = static_cast<int32_t *>(ctx->scratch_ptr(
       std::string("screen.nvalid") + tag, sizeof(int32_t) * (size_t)nb));
   int32_t *fails = static_cast<int32_t *>(
@@ -300,16 +307,21 @@ static std::vector<int32_t> screen_tier(vsk_ctx *ctx, const vsk_db *db,
   }
   rescore_select(ctx, db, qbat, nb, k, kc, metric, cand, nvalid, best);
 
+  if (fail_host) {
+    VSK_HIP(hipMemcpyAsync(fail_host, fails, sizeof(int32_t), hipMemcpyDeviceToHost,
+                           ctx->stream));
+    return {};
+  }
   int32_t nfail = 0;
   VSK_HIP(hipMemcpyAsync(&nfail, fails, sizeof(int32_t), hipMemcpyDeviceToHost,
                          ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   std::vector<int32_t> idx;
   if (nfail == 0) return idx;
   std::vector<uint8_t> hok((size_t)nb);
   VSK_HIP(hipMemcpyAsync(hok.data(), ok, (size_t)nb, hipMemcpyDeviceToHost,
                          ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   for (int64_t i = 0; i < nb; ++i)
     if (!hok[(size_t)i]) idx.push_back((int32_t)i);
   return idx;
@@ -631,7 +643,7 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
   }
   int32_t hf = 0;
   VSK_HIP(hipMemcpyAsync(&hf, nfail, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   if (hf == 0) return;
   // Undecided queries (near ties).  A second screen pass over them keeps
   // every row whose screened distance is within their limit (at most
@@ -686,7 +698,7 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
   check_launch("screen_argmin_collect");
   int32_t hr = 0;
   VSK_HIP(hipMemcpyAsync(&hr, nredo, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   if (hr == 0) return;
   // overflowing candidate lists: the exact VALU argmin over every row
   KernelTimer tv(ctx, "screen_argmin_fallback", (double)hr);
@@ -723,9 +735,26 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
 }
 
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
-                 int32_t k, int32_t metric, uint64_t *best) {
+                 int32_t k, int32_t metric, uint64_t *best, ScreenDeferred *defer) {
   const int32_t kc = screen_keep(k);
   const int64_t qb = query_batch(nq, screen_cap(kc));
+  if (defer) {
+    // every batch enqueued; the failing counts come back with the call's
+    // synchronisation (pinned slots taken before any work is queued)
+    const int64_t nbat = ceil_div(nq, qb);
+    defer->fails_host = static_cast<int32_t *>(ctx->pinned_ptr(sizeof(int32_t) * nbat));
+    defer->ok = static_cast<uint8_t *>(ctx->scratch_ptr("screen.okall", (size_t)nq));
+    defer->batches.clear();
+    defer->active = true;
+    defer->kc = kc;
+    for (int64_t b0 = 0, i = 0; b0 < nq; b0 += qb, ++i) {
+      const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+      screen_tier(ctx, db, dq + b0 * db->ld, nb, k, kc, metric, best + b0 * k, "",
+                  defer->ok + b0, defer->fails_host + i);
+      defer->batches.push_back({b0, nb});
+    }
+    return;
+  }
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     const float *qbat = dq + b0 * db->ld;
@@ -738,6 +767,32 @@ void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  kc >= VSK_MAX_K, gidx);
   }
   for (auto &rec : ctx->screen_redo) std::sort(rec.begin(), rec.end());
+}
+
+bool screen_finish(vsk_ctx *ctx, const vsk_db *db, const float *dq, int32_t k,
+                   int32_t metric, uint64_t *best, ScreenDeferred &defer) {
+  bool any = false;
+  if (!defer.active) return false;
+  for (size_t i = 0; i < defer.batches.size(); ++i) {
+    if (defer.fails_host[i] <= 0) continue;
+    const int64_t b0 = defer.batches[i].b0, nb = defer.batches[i].nb;
+    std::vector<uint8_t> hok((size_t)nb);
+    VSK_HIP(hipMemcpyAsync(hok.data(), defer.ok + b0, (size_t)nb, hipMemcpyDeviceToHost,
+                           ctx->stream));
+    stream_sync(ctx);
+    std::vector<int32_t> idx;
+    for (int64_t j = 0; j < nb; ++j)
+      if (!hok[(size_t)j]) idx.push_back((int32_t)j);
+    if (idx.empty()) continue;
+    std::vector<int64_t> gidx((size_t)nb);
+    for (int64_t j = 0; j < nb; ++j) gidx[(size_t)j] = b0 + j;
+    redo_queries(ctx, db, dq + b0 * db->ld, idx, k, metric, best + b0 * k,
+                 defer.kc >= VSK_MAX_K, gidx);
+    any = true;
+  }
+  defer.active = false;
+  for (auto &rec : ctx->screen_redo) std::sort(rec.begin(), rec.end());
+  return any;
 }
 
 }  // namespace vsk

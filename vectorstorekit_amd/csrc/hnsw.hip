@@ -154,7 +154,7 @@ vsk_status vsk_hnsw_distances(vsk_ctx *ctx, const vsk_db *db, const float *q, in
   if (is_device_ptr(offsets)) {
     VSK_HIP(hipMemcpyAsync(hoff.data(), offsets, sizeof(int64_t) * hoff.size(),
                            hipMemcpyDeviceToHost, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
   } else {
     std::copy(offsets, offsets + nq + 1, hoff.begin());
   }

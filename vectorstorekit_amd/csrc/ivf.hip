@@ -905,6 +905,30 @@ static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
   }
 }
 
+// every centroid of each query ranked by (exact sqrt-L2, centroid): the
+// exact VALU scan's dense keys, sorted per query (batches of at most 2^26
+// keys), written as the probe list probes[nq][nlist]
+static void ivf_rank_all(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int64_t nq,
+                         int32_t *probes) {
+  const int64_t nl = ivf->nlist;
+  const int64_t qb = std::max<int64_t>(1, std::min<int64_t>(nq, (1ll << 26) / nl));
+  uint64_t *k0 = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.rank0", sizeof(uint64_t) * (size_t)(qb * nl)));
+  uint64_t *k1 = static_cast<uint64_t *>(
+      ctx->scratch_ptr("ivf.rank1", sizeof(uint64_t) * (size_t)(qb * nl)));
+  for (int64_t b0 = 0; b0 < nq; b0 += qb) {
+    const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
+    FlatArgs a = centroid_args(ivf, dq + b0 * ivf->ld, nb);
+    a.cand = k0;
+    a.cap = nl;
+    launch_flat(ctx, a, MODE_DENSE, nullptr);
+    segmented_sort_u64(ctx, k0, k1, nb, nl);
+    KernelTimer t(ctx, "ivf_probe_ids");
+    k_keys_to_tie<<<grid1(nb * nl), 256, 0, ctx->stream>>>(k1, nb * nl, probes + b0 * nl);
+    check_launch("ivf_probe_ids");
+  }
+}
+
 // the queries as two bf16 planes for the screens: hi = bf16(q), lo =
 // bf16(q - hi) (ldb columns, zero padded), |hi| + |lo| and |q - hi - lo|
 // (sums of squares in double, square roots rounded up), one wave per query
@@ -1034,7 +1058,7 @@ static void list_screen_plane(vsk_ctx *ctx, const vsk_ivf *ivf) {
             nullptr);
   uint32_t hb[2];
   VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   ivf->xh_max = __builtin_bit_cast(float, hb[0]);
   ivf->xr_max = __builtin_bit_cast(float, hb[1]);
   ivf->xldb = ldb;
@@ -1155,7 +1179,7 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
   std::vector<int32_t> h_assign(n);
   VSK_HIP(hipMemcpyAsync(h_assign.data(), assign, 4 * n, hipMemcpyDeviceToHost,
                          ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
 
   // new CSR: old lists keep their order, new rows follow in call order
   std::vector<int64_t> add(nlist, 0);
@@ -1186,7 +1210,7 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
         ivf->rows.as<float>(), ivf->ids.as<int64_t>(), 0, ddest, ivf->total,
         ld, rows2->as<float>(), ids2->as<int64_t>());
     check_launch("ivf_scatter_old");
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
   }
   VSK_HIP(hipMemcpyAsync(ddest, dest_new.data(), 8 * n, hipMemcpyHostToDevice,
                          ctx->stream));
@@ -1197,7 +1221,7 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
   VSK_HIP(hipMemcpyAsync(ivf->list_off.p, noff.data(),
                          sizeof(int64_t) * (nlist + 1), hipMemcpyHostToDevice,
                          ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   std::swap(ivf->rows.p, rows2->p);
   std::swap(ivf->rows.bytes, rows2->bytes);
   ++ivf->version;
@@ -1210,7 +1234,7 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+static vsk_status ivf_probe_body(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                          int64_t nq, int32_t nprobe, int32_t *out_lists) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
@@ -1225,6 +1249,12 @@ vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
   o.copy_back();
   cs.finish();
   VSK_API_END(ctx);
+}
+
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_ivf_probe(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
+                         int64_t nq, int32_t nprobe, int32_t *out_lists) {
+  return topk_call(ctx, [&] { return ivf_probe_body(ctx, ivf, q, nq, nprobe, out_lists); });
 }
 
 vsk_status vsk_ivf_list_sizes(vsk_ctx *ctx, const vsk_ivf *ivf,
@@ -1683,15 +1713,10 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
       ctx->scratch_ptr("ivf.probes", sizeof(int32_t) * nq * np));
   uint64_t *pkeys = nullptr;
   if (exact_all) {
-    // .exact with more lists than a selection holds: every list, in index
-    // order (the stable sort's order when all lists are kept is by
-    // distance, but the candidate set -- and so the result -- is the same
-    // up to the position tie key)
-    std::vector<int32_t> all((size_t)nq * np);
-    for (int64_t i = 0; i < nq; ++i)
-      std::iota(all.begin() + i * np, all.begin() + (i + 1) * np, 0);
-    VSK_HIP(hipMemcpyAsync(probes, all.data(), 4 * all.size(),
-                           hipMemcpyHostToDevice, ctx->stream));
+    // .exact with more lists than a selection holds: every list, ranked by
+    // (exact distance, centroid) as findNearestCentroids sorts them, so
+    // that candidates tied on distance keep the reference's order
+    ivf_rank_all(ctx, ivf, dq, nq, probes);
   } else {
     ivf_probe_device(ctx, ivf, dq, nq, np, probes, sqp.one.qh ? &sqp.one : nullptr, &pkeys);
   }
@@ -1865,7 +1890,7 @@ static void ivf_store_codes(vsk_ctx *ctx, vsk_ivf *ivf, const void *dense, int32
   fill_i32(ctx, buf->as<int32_t>(), ((int64_t)ivf->total * stride + 16) / 4, 0);
   VSK_HIP(hipMemcpy2DAsync(buf->p, stride, dense, w, w, ivf->total, hipMemcpyDeviceToDevice,
                            ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   std::swap(ivf->codes.p, buf->p);
   std::swap(ivf->codes.bytes, buf->bytes);
   ivf->ckind = kind;
@@ -1878,7 +1903,7 @@ extern "C" {
 vsk_status vsk_ivf_search(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                           int64_t nq, int32_t nprobe, int32_t k, int32_t metric,
                           float *out_dist, int64_t *out_ids) {
-  return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids);
+  return topk_call(ctx, [&] { return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids); });
 }
 
 vsk_status vsk_ivf_search_filtered(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
@@ -1886,21 +1911,21 @@ vsk_status vsk_ivf_search_filtered(vsk_ctx *ctx, const vsk_ivf *ivf, const float
                                    const uint32_t *allow, int64_t allow_bits, float *out_dist,
                                    int64_t *out_ids) {
   if (!allow && allow_bits == 0)
-    return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids);
-  return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids,
-                        allow, allow_bits);
+    return topk_call(ctx, [&] { return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids); });
+  return topk_call(ctx, [&] { return ivf_search_any(ctx, ivf, q, nullptr, nq, nprobe, k, metric, 0, out_dist, out_ids,
+                        allow, allow_bits); });
 }
 
 vsk_status vsk_ivf_search_sq8(vsk_ctx *ctx, const vsk_ivf *ivf, const float *q,
                               const int8_t *qcodes, int64_t nq, int32_t nprobe, int32_t k,
                               int32_t *out_score, int64_t *out_ids) {
-  return ivf_search_any(ctx, ivf, q, qcodes, nq, nprobe, k, -1, 1, out_score, out_ids);
+  return topk_call(ctx, [&] { return ivf_search_any(ctx, ivf, q, qcodes, nq, nprobe, k, -1, 1, out_score, out_ids); });
 }
 
 vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
                              const float *q, int64_t nq, int32_t nprobe, int32_t k,
                              float *out_dist, int64_t *out_ids) {
-  return ivf_search_any(ctx, ivf, q, pq, nq, nprobe, k, -1, 2, out_dist, out_ids);
+  return topk_call(ctx, [&] { return ivf_search_any(ctx, ivf, q, pq, nq, nprobe, k, -1, 2, out_dist, out_ids); });
 }
 
 vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_t n,
@@ -1916,7 +1941,7 @@ vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_
                            ctx->stream));
     VSK_HIP(hipMemcpyAsync(hids.data(), ivf->ids.p, sizeof(int64_t) * hids.size(),
                            hipMemcpyDeviceToHost, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
     std::sort(want.begin(), want.end());
     // the rows kept, list by list in their order
     std::vector<int64_t> keep, off((size_t)ivf->nlist + 1);
@@ -1950,7 +1975,7 @@ vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_
             ivf->ld, rows.as<float>(), nids.as<int64_t>(), ncodes.as<uint8_t>());
         check_launch("ivf_remove_gather");
       }
-      VSK_HIP(hipStreamSynchronize(ctx->stream));
+      stream_sync(ctx);
       std::swap(ivf->rows.p, rows.p);
       std::swap(ivf->rows.bytes, rows.bytes);
       std::swap(ivf->ids.p, nids.p);
@@ -2129,7 +2154,7 @@ void put_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, const void *dev, int64_t rows, si
     const int64_t cnt = std::min(per, rows - r);
     VSK_HIP(hipMemcpy2DAsync(buf.data(), w, static_cast<const uint8_t *>(dev) + r * pitch,
                              pitch, w, cnt, hipMemcpyDeviceToHost, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
     put(f, h, buf.data(), (size_t)cnt * w);
   }
 }
@@ -2147,7 +2172,7 @@ void get_rows(vsk_ctx *ctx, FILE *f, Fnv1a &h, void *dev, int64_t rows, size_t p
     if (check && !check(buf.data(), cnt)) fail(VSK_ERR_IO, "index file: bad code values");
     VSK_HIP(hipMemcpy2DAsync(static_cast<uint8_t *>(dev) + r * pitch, pitch, buf.data(), w, w,
                              cnt, hipMemcpyHostToDevice, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
   }
 }
 
@@ -2165,7 +2190,7 @@ vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
   VSK_REQUIRE(path, VSK_ERR_INVALID_ARGUMENT, "path is null");
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   File f(fopen(path, "wb"));
   VSK_REQUIRE(f, VSK_ERR_IO, std::string("cannot open for writing: ") + path);
   Fnv1a h;
@@ -2290,7 +2315,7 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
               "index file: checksum mismatch");
   VSK_HIP(hipMemcpyAsync(ivf->list_off.p, off.data(), sizeof(int64_t) * (nlist + 1),
                          hipMemcpyHostToDevice, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   ivf->off = off;
   ivf->total = total;
   ivf->next_id = next_id;

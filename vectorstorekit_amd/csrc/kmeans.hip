@@ -740,7 +740,7 @@ static bool init_plusplus(vsk_ctx *ctx, const float *dx, int64_t n, int32_t d,
   std::vector<int64_t> h((size_t)k);
   VSK_HIP(hipMemcpyAsync(h.data(), chosen, sizeof(int64_t) * k, hipMemcpyDeviceToHost,
                          ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   for (int64_t v : h)
     if (v < 0 || v >= n) return false;
   return true;
@@ -791,7 +791,7 @@ vsk_status vsk_kmeans(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
       std::vector<int64_t> h = init_random_rows(n, k, seed);
       VSK_HIP(hipMemcpyAsync(rows, h.data(), sizeof(int64_t) * k, hipMemcpyHostToDevice,
                              ctx->stream));
-      VSK_HIP(hipStreamSynchronize(ctx->stream));  // h goes out of scope
+      stream_sync(ctx);  // h goes out of scope
     } else {
       VSK_REQUIRE(init_plusplus(ctx, dx, n, d, ld, k, seed, rows),
                   VSK_ERR_INVALID_ARGUMENT,

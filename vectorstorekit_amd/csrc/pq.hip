@@ -796,7 +796,7 @@ static void pq_screen_plane(vsk_ctx *ctx, const vsk_pq *pq) {
   }
   uint32_t hb[2];
   VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
-  VSK_HIP(hipStreamSynchronize(ctx->stream));
+  stream_sync(ctx);
   pq->xh_max = __builtin_bit_cast(float, hb[0]);
   pq->xr_max = __builtin_bit_cast(float, hb[1]);
   pq->xldb = ldb;
@@ -1111,7 +1111,7 @@ vsk_status vsk_pq_add_codes(vsk_ctx *ctx, vsk_pq *pq, const uint8_t *codes,
     if (pq->n > 0)
       VSK_HIP(hipMemcpyAsync(nb->p, pq->codes.p, (size_t)pq->n * pq->M,
                              hipMemcpyDeviceToDevice, ctx->stream));
-    VSK_HIP(hipStreamSynchronize(ctx->stream));
+    stream_sync(ctx);
     std::swap(pq->codes.p, nb->p);
     std::swap(pq->codes.bytes, nb->bytes);
     pq->cap_rows = cap;
@@ -1138,7 +1138,7 @@ vsk_status vsk_pq_lut(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+static vsk_status pq_search_body(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
                          int64_t nq, int32_t k_adc, int32_t k,
                          int32_t rerank_metric, const vsk_db *rerank_db,
                          float *out_dist, int64_t *out_ids) {
@@ -1308,6 +1308,14 @@ vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
   oi.copy_back();
   cs.finish();
   VSK_API_END(ctx);
+}
+
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_pq_search(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
+                         int64_t nq, int32_t k_adc, int32_t k,
+                         int32_t rerank_metric, const vsk_db *rerank_db,
+                         float *out_dist, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return pq_search_body(ctx, pq, q, nq, k_adc, k, rerank_metric, rerank_db, out_dist, out_ids); });
 }
 
 }  // extern "C"

@@ -1112,6 +1112,14 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
   uint64_t *thresh = w.thresh, *cand = w.cand;
   int32_t *counts = w.counts, *seg_n = w.seg_n, *ovf_count = w.ovf_count;
   uint8_t *ovf_mask = w.ovf_mask;
+  // Without topk_sync no chunk is checked from the host: an overflow only
+  // counts into the context's call counter, which the call's final
+  // synchronisation reads back (then the call runs again with checks).
+  const bool defer = !ctx->topk_sync;
+  if (defer && !ctx->ovf_armed) {
+    fill_i32(ctx, ctx->ovf_dev, 1, 0);
+    ctx->ovf_armed = true;
+  }
 
   int64_t r0 = 0;
   bool first = true;
@@ -1156,10 +1164,15 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     // are read into registers once
     sa.regs = dense && cap <= 64 * SEL_THREADS;  // (no previous list)
     if (!dense) {
-      fill_i32(ctx, ovf_count, 1, 0);
-      fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
+      if (defer) {
+        // (the mask is written, never read)
+        sa.overflow_count = ctx->ovf_dev;
+      } else {
+        fill_i32(ctx, ovf_count, 1, 0);
+        fill_i32(ctx, reinterpret_cast<int32_t *>(ovf_mask), (nq + 3) / 4, 0);
+        sa.overflow_count = ovf_count;
+      }
       sa.overflow_mask = ovf_mask;
-      sa.overflow_count = ovf_count;
       if (nseg > 0) {
         sa.seg_n = seg_n;
         sa.nseg = nseg;
@@ -1167,11 +1180,11 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
       }
     }
     launch_select(ctx, sa, select_name);
-    if (!dense) {
+    if (!dense && !defer) {
       int32_t h_ovf = 0;
       VSK_HIP(hipMemcpyAsync(&h_ovf, ovf_count, 4, hipMemcpyDeviceToHost,
                              ctx->stream));
-      VSK_HIP(hipStreamSynchronize(ctx->stream));
+      stream_sync(ctx);
       if (h_ovf > 0) {
         // queries whose survivors did not fit re-scan this chunk in
         // sub-chunks of cap rows, each kept whole

@@ -993,7 +993,7 @@ vsk_status vsk_sq8_free(vsk_ctx *ctx, vsk_sq8 *db) {
   return VSK_OK;
 }
 
-vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
+static vsk_status sq8_search_body(vsk_ctx *ctx, const vsk_sq8 *db,
                           const int8_t *qcodes, int64_t nq, int32_t k,
                           int32_t *out_score, int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
@@ -1053,7 +1053,14 @@ vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
   VSK_API_END(ctx);
 }
 
-vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_sq8_search(vsk_ctx *ctx, const vsk_sq8 *db,
+                          const int8_t *qcodes, int64_t nq, int32_t k,
+                          int32_t *out_score, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return sq8_search_body(ctx, db, qcodes, nq, k, out_score, out_ids); });
+}
+
+static vsk_status sq8_search_noalloc_body(vsk_ctx *ctx, const vsk_sq8 *db,
                                   const int8_t *qcodes, int64_t nq, int32_t k,
                                   int32_t *out_score, int64_t *out_ids) {
   VSK_API_BEGIN(ctx);
@@ -1143,6 +1150,13 @@ vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
   }
   cs.finish();
   VSK_API_END(ctx);
+}
+
+// top-k overflow is checked at the call's end (topk_call)
+vsk_status vsk_sq8_search_noalloc(vsk_ctx *ctx, const vsk_sq8 *db,
+                                  const int8_t *qcodes, int64_t nq, int32_t k,
+                                  int32_t *out_score, int64_t *out_ids) {
+  return topk_call(ctx, [&] { return sq8_search_noalloc_body(ctx, db, qcodes, nq, k, out_score, out_ids); });
 }
 
 }  // extern "C"

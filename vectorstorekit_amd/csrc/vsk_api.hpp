@@ -10,6 +10,7 @@
 #define VSK_API_BEGIN(ctx)                                                    \
   if (!(ctx)) return VSK_ERR_INVALID_ARGUMENT;                                \
   const ::vsk::FaultCtxScope vsk_fault_scope_(ctx);                           \
+  if (!vsk_fault_scope_.prev) (ctx)->sync_count = 0;                          \
   try {                                                                       \
     (ctx)->last_error.clear();                                                \
     VSK_HIP(hipSetDevice((ctx)->device));
@@ -18,13 +19,18 @@
   }                                                                           \
   catch (const ::vsk::Error &e) {                                             \
     (ctx)->last_error = e.msg;                                                \
+    (ctx)->ovf_armed = false;                                                 \
     (void)hipStreamSynchronize((ctx)->stream);                                \
     if ((ctx)->aux) (void)hipStreamSynchronize((ctx)->aux);                   \
     (void)hipGetLastError();                                                  \
+    (ctx)->drop_pending();                                                    \
     return e.code;                                                            \
   }                                                                           \
   catch (const std::exception &e) {                                           \
     (ctx)->last_error = e.what();                                             \
+    (ctx)->ovf_armed = false;                                                 \
+    (void)hipStreamSynchronize((ctx)->stream);                                \
+    (ctx)->drop_pending();                                                    \
     return VSK_ERR_EXECUTION_FAILED;                                          \
   }                                                                           \
   return VSK_OK;

@@ -108,6 +108,22 @@ struct vsk_ctx {
   int fault_kind = 0;
   int64_t fault_at = 0, fault_seen = 0;
 
+  // Top-k overflow without a read-back per chunk (progressive_topk): unless
+  // topk_sync is set, a filtered chunk whose survivors overflow a query's
+  // slots only counts into ovf_dev (the query keeps its earlier list, so
+  // later work stays well defined); CallScope::finish reads the count with
+  // the call's final synchronisation into topk_overflowed, and the entry
+  // point then runs the call again with topk_sync (a check after each
+  // chunk, and the overflowing queries re-scan it in sub-chunks).  Both
+  // buffers are made with the context, so no call allocates them.
+  int32_t *ovf_dev = nullptr;   // device counter
+  int32_t *ovf_host = nullptr;  // pinned copy (8 ints: [0] the count)
+  bool ovf_armed = false;       // ovf_dev cleared for this call
+  bool topk_sync = false;
+  bool topk_overflowed = false;
+  // host waits for the stream in the current (outermost) API call
+  int32_t sync_count = 0;
+
   // queries the last vsk_search_flat redid in the screen's fallback tiers
   // (indices into that call's queries, ascending): [0] the wider screen,
   // [1] the exact scan over every row
@@ -148,6 +164,9 @@ struct vsk_ctx {
   hipEvent_t take_event();
   hipEvent_t take_timer_event();
   void resolve_pending();
+  // the pending timings of a call that failed: their events back to the
+  // pool, unread
+  void drop_pending();
 };
 
 struct vsk_db {
@@ -174,6 +193,27 @@ struct CallScope {
   void finish();  // sync + timing; call before returning results
 };
 
+// Runs an API entry point's body with deferred top-k overflow checks (see
+// vsk_ctx::topk_sync); when a query overflowed, the body runs once more
+// with a check after every chunk.  Nested calls leave the decision to the
+// outermost one.
+template <class F> vsk_status topk_call(vsk_ctx *ctx, F &&body) {
+  if (!ctx) return VSK_ERR_INVALID_ARGUMENT;
+  if (ctx->topk_sync) return body();
+  ctx->topk_overflowed = false;
+  vsk_status st = body();
+  if (st == VSK_OK && ctx->topk_overflowed) {
+    const int32_t waits = ctx->sync_count;  // (the second run counts afresh)
+    ctx->topk_overflowed = false;
+    ctx->topk_sync = true;
+    st = body();
+    ctx->topk_sync = false;
+    ctx->sync_count += waits;
+  }
+  ctx->topk_overflowed = false;
+  return st;
+}
+
 // Times one kernel launch when profiling is on.
 struct KernelTimer {
   vsk_ctx *ctx;
@@ -191,6 +231,8 @@ struct KernelTimer {
 
 // check the last launch on the stream
 void check_launch(const char *name);
+// the host waits for the context's stream (counted per API call)
+void stream_sync(vsk_ctx *ctx);
 
 // staging of caller buffers: a device pointer is used as is, a host
 // pointer is copied through a scratch slot.

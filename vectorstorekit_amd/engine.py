@@ -102,6 +102,10 @@ class Context:
     def last_kernel_ms(self) -> float:
         return float(self.lib.vsk_last_kernel_ms(self.handle))
 
+    def last_sync_count(self) -> int:
+        """Host waits for the stream in the last call (``vsk_last_sync_count``)."""
+        return int(self.lib.vsk_last_sync_count(self.handle))
+
     def measure_peaks(self) -> dict:
         """Measured ceilings of the device (``vsk_measure_peaks``): dense
         bf16 TFLOP/s, dense int8 TOP/s, HBM copy GB/s (read plus written)
