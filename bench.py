@@ -221,6 +221,15 @@ def exact_check(gd, gi, od, oi, m):
             "distances_bitwise_equal": bool(same_d.all())}
 
 
+def probed_pairs(idx, q, nprobe):
+    """(query, row) pairs an IVF search scores: the sizes of each query's
+    probed lists, summed over the queries."""
+    sizes = idx.list_sizes()
+    probes = idx.probe(q, nprobe)
+    probes = probes.cpu().numpy() if hasattr(probes, "cpu") else np.asarray(probes)
+    return int(sizes[probes[probes >= 0]].sum())
+
+
 def setup(c, a, ctx, dev):
     """Builds the resident index for config c; returns (spec, step, cpu_leg,
     host_step): cpu_leg(target_s) gives (baseline dict, agreement), and
@@ -453,6 +462,7 @@ def setup(c, a, ctx, dev):
                     "points centre + 0.5 N(0,I) (seeds 5, 1, 2), centroids centre + "
                     "0.1 N(0,I) (seed 4); torch Philox",
             "dtype": "f32", "nq": nq, "n": n, "d": d,
+            "pairs_per_step": probed_pairs(idx, q, nprobe),
             "kernels": [("ivf_list_screen", "k_list_screen<4, false> (bf16 MFMA screen of the "
                                             "probed lists, one 32-bit word per pair)",
                          "words_hbm"),
@@ -531,6 +541,7 @@ def setup(c, a, ctx, dev):
                                       "segments"),
             "dtype": "i8 codes, i32 scores" if sq8 else "u8 codes, f32 LUT",
             "nq": nq, "n": n, "d": d, "M": M,
+            "pairs_per_step": probed_pairs(idx, q, nprobe),
             "kernels": [("ivf_sq8_list_scan", "k_list_scan_sq8<16>", "valu_dot4")] if sq8
                        else [("ivf_pq_list_scan", "k_list_scan_pq_q (one workgroup per query)", "lds_pq")],
             "keep": (idx, x, q, ids, sq if sq8 else pq),
@@ -907,7 +918,7 @@ def measure(c, a, ctx, dev):
         "dtype": spec["dtype"],
         "data": spec["data"],
         "config": dict({"workload": spec["workload"]}, **spec["config"]),
-        "distances_per_s": nq * n * a.steps / el,
+        "distances_per_s": spec.get("pairs_per_step", nq * n) * a.steps / el,
         "roofline": roofline(spec, stats, full),
         "measured_peaks": {k: round(v, 1) for k, v in MEASURED_PEAKS.items()} or None,
         "setup_s": round(build_s, 2),
