@@ -60,10 +60,14 @@ PEAK_LDS_LOOKUPS = 256 * 64 * 2.4e9  # 4-byte LDS reads/s, 64 banks x 256 CUs
 MEASURED_PEAKS = {}
 
 DEFAULT_STEPS = {"c1": (200, 20), "c2": (5, 1), "c3": (5, 1), "c4": (5, 1), "c5": (5, 1),
+                 "c5lut": (3, 1),
                  "c3train": (2, 1), "c4bin": (5, 1), "c3sq8": (5, 1), "c3pq": (5, 1),
                  "all": (20, 5)}
 # the BASELINE configs the default run measures; the first is the headline
 BASELINE_CONFIGS = ("c2", "c1", "c3", "c4", "c5")
+# measured after them in the default run: config 5 through the LUT scan over
+# the codes alone (no decoded plane), beside the screened line
+EXTRA_CONFIGS = ("c5lut",)
 
 
 def parse():
@@ -600,7 +604,7 @@ def setup(c, a, ctx, dev):
         }
         return spec, step, cpu_leg, host_step
 
-    # c5
+    # c5 / c5lut
     n, d, nq, M, ksub, k_adc, k = 10_000_000, 128, 1000, 16, 256, 1000, 100
     x, q, _ = gen_mixture(n, d, 1024, nq, dev, jitter=False)
     pq = ProductQuantizer.train(ctx, x[:65536], M, ksub, iterations=8, seed=0)
@@ -610,17 +614,32 @@ def setup(c, a, ctx, dev):
     dist = torch.empty(nq, k, device=dev)
     ids = torch.empty(nq, k, dtype=torch.int64, device=dev)
     l1 = L.METRIC_L1
+    lut = c == "c5lut"
+    sctx = ctx
+    if lut:
+        # codes only: a context without the bf16 screen (VSK_FLAT_KERNEL=
+        # exact) scans the codes with the LDS tables, no decoded plane
+        from vectorstorekit_amd import Context
+        old = os.environ.get("VSK_FLAT_KERNEL")
+        os.environ["VSK_FLAT_KERNEL"] = "exact"
+        try:
+            sctx = Context(0)
+        finally:
+            if old is None:
+                del os.environ["VSK_FLAT_KERNEL"]
+            else:
+                os.environ["VSK_FLAT_KERNEL"] = old
 
     def step():
-        ctx.check(lib.vsk_pq_search(ctx.handle, pq.handle, q.data_ptr(), nq, k_adc, k, l1,
-                                    db.handle, dist.data_ptr(), ids.data_ptr()))
+        sctx.check(lib.vsk_pq_search(sctx.handle, pq.handle, q.data_ptr(), nq, k_adc, k, l1,
+                                     db.handle, dist.data_ptr(), ids.data_ptr()))
 
     qhost = q.cpu().numpy()
     hd, hi = np.empty((nq, k), np.float32), np.empty((nq, k), np.int64)
 
     def host_step():
-        ctx.check(lib.vsk_pq_search(ctx.handle, pq.handle, qhost.ctypes.data, nq, k_adc, k, l1,
-                                    db.handle, hd.ctypes.data, hi.ctypes.data))
+        sctx.check(lib.vsk_pq_search(sctx.handle, pq.handle, qhost.ctypes.data, nq, k_adc, k,
+                                     l1, db.handle, hd.ctypes.data, hi.ctypes.data))
 
     def cpu_leg(target_s):
         from oracle import oracle as O
@@ -637,9 +656,19 @@ def setup(c, a, ctx, dev):
                  "exact_oracle_check": exact_check(gd, gi, od, oi, m)},
                 id_agreement(gi[:m], oi))
 
+    code_bytes = n * M
+    plane_bytes = 0 if lut else n * ((d + 63) // 64 * 64) * 2
     spec = {
         "metric": "QPS @k=100, PQ M16x256 ADC 10M x 128, top-1000 L1 re-rank",
-        "workload": "pq-adc-10Mx128-m16-q1000-kadc1000-l1rerank-k100 (BASELINE config 5)",
+        "workload": ("pq-adc-10Mx128-m16-q1000-kadc1000-l1rerank-k100 (BASELINE config 5)"
+                     if not lut else
+                     "pq-adc-codes-only-10Mx128-m16-q1000-kadc1000-l1rerank-k100 (BASELINE "
+                     "config 5, LUT scan over the codes, no decoded plane)"),
+        "ctx": sctx,
+        "device_bytes": {"codes": code_bytes, "decoded_bf16_plane": plane_bytes,
+                         "note": "the search's index memory besides the fp32 rows the "
+                                 "re-rank reads" + ("" if lut else
+                                 "; the screen's decoded plane is 16x the codes")},
         "config": {"n": n, "d": d, "M": M, "ksub": ksub, "nq": nq, "k_adc": k_adc, "k": k,
                    "metric": "ADC sum of LUT[m][code_m]; re-rank sum |q-x|"},
         "data": "synthetic: 1,024-Gaussian mixture, centres 2 N(0,I) (seed 3), points "
@@ -649,11 +678,11 @@ def setup(c, a, ctx, dev):
         # filtered chunks: the bf16 screen over the decoded rows (one bf16
         # product per pair), then the survivors' exact ADC sums; the dense
         # first chunk: the LUT scan
-        "kernels": [("flat_screen_filter", "k_flat_screen<FILTER> over the decoded PQ rows",
-                     "mfma_bf16"),
-                    ("pq_adc_filter", "k_pq_adc16<FILTER> (8 queries per workgroup)", "lds_pq"),
+        "kernels": ([("flat_screen_filter", "k_flat_screen<FILTER> over the decoded PQ rows",
+                      "mfma_bf16")] if not lut else []) +
+                   [("pq_adc_filter", "k_pq_adc16<FILTER> (8 queries per workgroup)", "lds_pq"),
                     ("pq_adc_dense", "k_pq_adc16<DENSE> (8 queries per workgroup)", "lds_pq")],
-        "keep": (pq, db, x, q, codes, dist, ids),
+        "keep": (pq, db, x, q, codes, dist, ids, sctx),
     }
     return spec, step, cpu_leg, host_step
 
@@ -878,6 +907,8 @@ def measure(c, a, ctx, dev):
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
+    # (a workload may run on a context of its own)
+    ctx = spec.get("ctx", ctx)
     # the timed steps carry HIP-event timers on the roofline's candidate
     # kernels only (two events a launch, no work counts read back)
     ctx.profile_only([key for key, _, _ in spec["kernels"]])
@@ -920,6 +951,7 @@ def measure(c, a, ctx, dev):
         "config": dict({"workload": spec["workload"]}, **spec["config"]),
         "distances_per_s": spec.get("pairs_per_step", nq * n) * a.steps / el,
         "roofline": roofline(spec, stats, full),
+        "device_bytes": spec.get("device_bytes"),
         "measured_peaks": {k: round(v, 1) for k, v in MEASURED_PEAKS.items()} or None,
         "setup_s": round(build_s, 2),
         "kernels_steps": breakdown_steps,
@@ -983,7 +1015,7 @@ def main():
         # configs under "configs", each measured the same way
         out = None
         others = {}
-        for c in BASELINE_CONFIGS:
+        for c in BASELINE_CONFIGS + EXTRA_CONFIGS:
             r = measure(c, a, ctx, dev)
             gc.collect()
             torch.cuda.empty_cache()

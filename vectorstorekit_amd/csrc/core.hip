@@ -471,6 +471,7 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   c->flat_fp32 = fk && strcmp(fk, "fp32") == 0;
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
   c->flat_force_screen = fk && strcmp(fk, "screen") == 0;
+  c->exact_only = fk && strcmp(fk, "exact") == 0;
   if (const char *ff = getenv("VSK_FAULT")) {
     const char *colon = strchr(ff, ':');
     const long long at = colon ? atoll(colon + 1) : 0;

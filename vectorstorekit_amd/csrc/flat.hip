@@ -457,19 +457,26 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
   // whole 64-dimension stages of the screen (zero padding)
   const int32_t ldb = (db->d + 63) & ~63;
   if (!db->split.p) {
-    db->split.reserve(sizeof(uint16_t) * 2 * (size_t)db->n * ldb);
+    // the hi plane (all the screen reads) and the maxima of its bound
+    db->split.reserve(sizeof(uint16_t) * (size_t)db->n * ldb);
     db->ldb = ldb;
-    uint16_t *h = db->split.as<uint16_t>();
     uint32_t *mb =
         static_cast<uint32_t *>(ctx->scratch_ptr("flat.splitmax", 2 * sizeof(uint32_t)));
     fill_i32(ctx, reinterpret_cast<int32_t *>(mb), 2, 0);
-    split_bf16(ctx, db->x.as<float>(), db->n, db->d, db->ld, h,
-               h + (size_t)db->n * ldb, ldb, nullptr, nullptr, mb);
+    split_bf16(ctx, db->x.as<float>(), db->n, db->d, db->ld, db->split.as<uint16_t>(), nullptr,
+               ldb, nullptr, nullptr, mb);
     uint32_t hb[2];
     VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
     stream_sync(ctx);
     std::memcpy(&db->split_max_hi, &hb[0], sizeof(float));
     std::memcpy(&db->split_max_res, &hb[1], sizeof(float));
+  }
+  if (qlo && !db->split_lo.p) {
+    // the lo plane only for the bf16x3 kernel (hi is written again, the
+    // same values)
+    db->split_lo.reserve(sizeof(uint16_t) * (size_t)db->n * ldb);
+    split_bf16(ctx, db->x.as<float>(), db->n, db->d, db->ld, db->split.as<uint16_t>(),
+               db->split_lo.as<uint16_t>(), ldb, nullptr, nullptr, nullptr);
   }
   uint16_t *qs = static_cast<uint16_t *>(ctx->scratch_ptr(
       "flat.qsplit", sizeof(uint16_t) * (qlo ? 2 : 1) * (size_t)nq * ldb));
@@ -477,7 +484,7 @@ SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
              ldb, qnh, qnr, nullptr);
   SplitPtrs s;
   s.xh = db->split.as<uint16_t>();
-  s.xl = s.xh + (size_t)db->n * ldb;
+  s.xl = db->split_lo.as<uint16_t>();  // (null until a bf16x3 call made it)
   s.qh = qs;
   s.ql = qlo ? qs + (size_t)nq * ldb : nullptr;
   s.ldxb = ldb;
@@ -494,7 +501,7 @@ bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
   // of exact VALU work) is cheaper by the exact sequential scan alone than
   // by the screen's fixed chain of launches and its check read-back
   if (!ctx->flat_no_screen && !ctx->flat_force_screen && screen_applies(metric, k) &&
-      (double)nq * (double)db->n * (double)db->d <= 268435456.0) {
+      (ctx->exact_only || (double)nq * (double)db->n * (double)db->d <= 268435456.0)) {
     approx_topk(ctx, db, dq, nq, k, exact_metric(metric), best, 3);
     return true;
   }

@@ -565,7 +565,7 @@ ArgminQueries argmin_queries(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t 
 }
 
 bool screen_argmin_applies(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t d) {
-  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (ctx->flat_no_screen || ctx->flat_fp32 || ctx->exact_only) return false;
   if (n >= 0x7FFFFFFFll || d < 32) return false;  // narrow rows: the padding to 64 dims costs
   // small problems take the exact scan alone (the screen's fixed launches)
   return ctx->flat_force_screen || (double)nq * (double)n * d >= (double)(1ll << 30);

@@ -846,7 +846,7 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
 // most 256 dims, enough work (forced by VSK_FLAT_KERNEL=screen, off by
 // =exact / =bf16x3 / =fp32)
 static bool probe_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t nq, int32_t np) {
-  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (ctx->flat_no_screen || ctx->flat_fp32 || ctx->exact_only) return false;
   if (ivf->d > 256 || np > VSK_MAX_K) return false;
   return ctx->flat_force_screen ||
          (double)nq * (double)ivf->nlist * (double)ivf->d >= (double)(1ll << 30);
@@ -1024,7 +1024,7 @@ static ArgminQueries screen_queries(vsk_ctx *ctx, const float *dq, int64_t nq, i
 // launches (forced by VSK_FLAT_KERNEL=screen, off by =exact / =bf16x3)
 static bool list_screen_applies(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t metric, int32_t k,
                                 double ncand) {
-  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (ctx->flat_no_screen || ctx->flat_fp32 || ctx->exact_only) return false;
   if (metric != VSK_METRIC_L2 && metric != VSK_METRIC_L2SQ) return false;
   if (ivf->d > 256) return false;
   return ctx->flat_force_screen || ncand * ivf->d >= (double)(1ll << 30);

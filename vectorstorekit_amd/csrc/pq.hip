@@ -807,7 +807,7 @@ static void pq_screen_plane(vsk_ctx *ctx, const vsk_pq *pq) {
 // whose count divides a wave, and a problem large enough that the screen's
 // fixed launches pay (forced by VSK_FLAT_KERNEL=screen, off by =exact)
 static bool pq_screen_applies(const vsk_ctx *ctx, const vsk_pq *pq, int64_t nq) {
-  if (ctx->flat_no_screen || ctx->flat_fp32) return false;
+  if (ctx->flat_no_screen || ctx->flat_fp32 || ctx->exact_only) return false;
   if (pq->M < 1 || pq->M > 64 || (64 % pq->M) != 0) return false;
   if (pq->dsub != 1 && pq->dsub != 2 && pq->dsub != 4 && pq->dsub != 8 && pq->dsub != 16 &&
       pq->dsub != 32)

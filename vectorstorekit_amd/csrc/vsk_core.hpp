@@ -104,6 +104,10 @@ struct vsk_ctx {
   bool flat_fp32 = false;
   bool flat_no_screen = false;
   bool flat_force_screen = false;
+  // "exact": no bf16 screen anywhere -- the exact scans alone (flat search
+  // on the exact VALU kernel for its screenable metrics, IVF's exact probe
+  // and list scans, PQ's LUT scan over the codes, the exact argmin)
+  bool exact_only = false;
   // VSK_FAULT: the kind of event to fail, at which occurrence, seen so far
   int fault_kind = 0;
   int64_t fault_at = 0, fault_seen = 0;
@@ -176,9 +180,10 @@ struct vsk_db {
   vsk::DevBuf x;       // n x ld fp32
   vsk::DevBuf sqnorm;  // n: sum x^2 (fp32)
   vsk::DevBuf norm;    // n: sqrt(sum x^2)
-  // bf16 hi/lo planes for the bf16 MFMA kernels, built on first use, and
+  // bf16 hi/lo planes for the bf16 MFMA kernels, built on first use (the
+  // lo plane only for the bf16x3 kernel; the screen reads hi alone), and
   // the maxima over the rows of |hi| and |x - hi| (the screen's bound)
-  mutable vsk::DevBuf split;
+  mutable vsk::DevBuf split, split_lo;
   mutable int32_t ldb = 0;
   mutable float split_max_hi = 0.f, split_max_res = 0.f;
 };
