@@ -154,6 +154,29 @@ typedef struct {
   double hbm_read_gbs;
 } vsk_peaks;
 vsk_status vsk_measure_peaks(vsk_ctx *ctx, vsk_peaks *out);
+/* ---- configuration ----------------------------------------------------------
+ * HIPAccelerationConfiguration, the HIP counterpart of MetalComputeConfiguration
+ * (Config/Acceleration/MetalComputeConfiguration.swift:8-46) and of the
+ * store's DistanceComputeBackend choice (Config/Core/StoreConfiguration.swift:
+ * 145-166).  A context starts from the environment (VSK_FLAT_KERNEL,
+ * VSK_MAX_TILE_BYTES); vsk_configure replaces those settings for later
+ * calls on ctx. */
+#define VSK_KERNEL_AUTO 0   /* the bf16 screen where it is exact and pays, else exact scans */
+#define VSK_KERNEL_EXACT 1  /* no screen: the exact scans alone (flat, IVF, PQ LUT, argmin) */
+#define VSK_KERNEL_SCREEN 2 /* the screen at every size (where the metric allows it) */
+#define VSK_KERNEL_BF16X3 3 /* flat search on the bf16x3 kernel (tolerance path) */
+#define VSK_KERNEL_FP32 4   /* flat search on the fp32 MFMA kernel (tolerance path) */
+typedef struct {
+  int32_t kernel;           /* VSK_KERNEL_* */
+  int32_t enable_profiling; /* per-kernel event timing (MetalComputeConfiguration.enableProfiling) */
+  int64_t max_tile_bytes;   /* largest working buffer of a query batch; 0 = 2 GiB of
+                               candidate keys.  Searches split their queries into
+                               batches under it, as MetalDistanceCompute chunks queries
+                               under its buffer limit (Acceleration/Metal/
+                               MetalDistanceCompute.swift:371-380,450-473) */
+} vsk_config;
+vsk_status vsk_configure(vsk_ctx *ctx, const vsk_config *cfg);
+vsk_status vsk_get_config(const vsk_ctx *ctx, vsk_config *cfg);
 /* Per-kernel event timing (off by default). */
 vsk_status vsk_profile_enable(vsk_ctx *ctx, int32_t on);
 /* Restricts the timing to the timers named in names (comma-separated;

@@ -103,3 +103,23 @@ def test_row_bitmap_layout():
                                   np.zeros(2, np.uint32))
     unpacked = np.unpackbits(bm.view(np.uint8), bitorder="little")[:70].astype(bool)
     np.testing.assert_array_equal(unpacked, mask)
+
+
+def test_acceleration_configuration_host_side():
+    """HIPAccelerationConfiguration validates on the host; the backend
+    choice takes the HIP device for .auto and keeps explicit choices."""
+    from vectorstorekit_amd import DistanceComputeBackend, HIPAccelerationConfiguration
+
+    HIPAccelerationConfiguration().validate()
+    HIPAccelerationConfiguration.research().validate()
+    with pytest.raises(vsk.VSKError):
+        HIPAccelerationConfiguration(kernel="fast").validate()
+    with pytest.raises(vsk.VSKError):
+        HIPAccelerationConfiguration(maxTileBytes=-1).validate()
+    B = DistanceComputeBackend
+    assert B.auto.selectOptimal(128, 10) == B.hip
+    assert B.auto.selectOptimal(512, 10, hipAvailable=False) == B.simd
+    assert B.auto.selectOptimal(128, 5000, hipAvailable=False) == B.metal
+    assert B.accelerate.selectOptimal(128, 5000) == B.accelerate
+    lib = vsk.load_library()
+    assert lib.vsk_configure(None, None) == -2

@@ -332,10 +332,10 @@ def test_device_tensors(ctx):
 def test_config2_cosine_full_size(ctx):
     """BASELINE config 2 at full size: 1,000,000 x 768 unit-norm rows, 10,000
     queries, k = 100.  Bit-exact against the oracle (distances bit for bit,
-    ids equal) on the first 1,000 queries plus every query the screen redid
-    (tier 1: the wider screen; tier 2: the exact scan), whose numbers must
-    equal the screen_retry / screen_fallback work counters; size-independent
-    properties over all 10,000."""
+    ids equal) on all 10,000 queries; the queries the screen redid (tier 1:
+    the wider screen; tier 2: the exact scan) must number as the
+    screen_retry / screen_fallback work counters say (printed: none on this
+    data)."""
     import torch
 
     n, d, nq, k = 1_000_000, 768, 10_000, 100
@@ -365,16 +365,56 @@ def test_config2_cosine_full_size(ctx):
     assert (gi >= 0).all() and (gi < n).all()
     xh, qh = x.cpu().numpy(), q.cpu().numpy()
     del x
-    check = np.union1d(np.union1d(np.arange(1000), tier1), tier2)
-    od, oi = O.search_flat(qh[check], xh, k, METRIC_COSINE_NORMALIZED)
-    np.testing.assert_array_equal(gi[check], oi)
-    np.testing.assert_array_equal(gd[check].view(np.uint32), od.view(np.uint32))
-    # over all queries: the distances are 1 - q.x of the returned rows
-    # within fp32 rounding (each row a unit vector)
+    od, oi = O.search_flat(qh, xh, k, METRIC_COSINE_NORMALIZED)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    # the distances are 1 - q.x of the returned rows within fp32 rounding
+    # (each row a unit vector)
     some = np.random.default_rng(0).choice(nq, 64, replace=False)
     for qi in some:
         ref = 1.0 - xh[gi[qi]].astype(np.float64) @ qh[qi].astype(np.float64)
         np.testing.assert_allclose(gd[qi], ref, rtol=0, atol=2e-6)
+
+
+def test_config2_planted_near_ties(ctx):
+    """Config 2's database and queries with near-duplicate clusters planted
+    around three queries: 600 rows (more than the 364 the screen keeps, fewer
+    than the 1,024 of its second tier) around query 0 and 1,600 rows (more
+    than both) around queries 1 and 2, all within the screen's error bound of
+    each other.  Those queries fail the bound: query 0 is settled by the
+    wider screen (tier 1), queries 1 and 2 by the exact scan over every row
+    (tier 2).  All 10,000 queries bit-exact against the oracle."""
+    import torch
+
+    n, d, nq, k = 1_000_000, 768, 10_000, 100
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    x = torch.randn(n, d, generator=g, device="cuda")
+    x /= x.norm(dim=1, keepdim=True)
+    g.manual_seed(2)
+    q = torch.randn(nq, d, generator=g, device="cuda")
+    q /= q.norm(dim=1, keepdim=True)
+    g.manual_seed(9)
+    at = 0
+    for qi, m in ((0, 600), (1, 1600), (2, 1600)):
+        rows = q[qi] + 0.01 * torch.randn(m, d, generator=g, device="cuda")
+        x[at:at + m] = rows / rows.norm(dim=1, keepdim=True)
+        at += m
+    print("config2 planted near ties 1Mx768 q10000 k100", flush=True)
+    db = VectorDatabase(ctx, x)
+    gd, gi = db.search(q, k, METRIC_COSINE_NORMALIZED)
+    tier1, tier2 = ctx.last_screen_redo(1), ctx.last_screen_redo(2)
+    print(f"screen redo: tier 1 {tier1.tolist()[:10]} ({len(tier1)}), "
+          f"tier 2 {tier2.tolist()[:10]} ({len(tier2)})", flush=True)
+    assert {0, 1, 2} <= set(tier1.tolist())
+    assert {1, 2} <= set(tier2.tolist()) and 0 not in set(tier2.tolist())
+    gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
+    xh, qh = x.cpu().numpy(), q.cpu().numpy()
+    del x
+    od, oi = O.search_flat(qh, xh, k, METRIC_COSINE_NORMALIZED)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    assert set(gi[1].tolist()) <= set(range(600, 2200))
 
 
 @pytest.mark.parametrize("metric", ["euclidean", "manhattan", "cosine", "hamming"])
@@ -440,3 +480,44 @@ def test_flat_filtered(ctx, metric, shape):
         np.testing.assert_array_equal(gd2, od2)
     gd3, gi3 = db.search(q[:2], k, metric, allow=np.zeros(n, np.bool_))
     assert (gi3 == -1).all() and np.isinf(gd3).all()
+
+
+def test_screen_segment_overflow_rescan(ctx):
+    """A filtered chunk of the screen whose survivors overflow a query's
+    per-split segment: 900 near-copies of query 0 placed after the first
+    dense chunk (2,048 rows) all beat its running threshold, more than a
+    split's segment holds.  The call notices at its end and runs again with
+    a check per chunk; the overflowing query re-scans that chunk in dense
+    sub-chunks, whose keys the selection must read as dense lists (not in
+    the filtered chunk's segmented layout).  Bit-exact for every query."""
+    import os
+
+    from vectorstorekit_amd import Context
+
+    rng = np.random.default_rng(41)
+    n, nq, d, k = 60_000, 300, 64, 100
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    near = q[0] + 0.05 * rng.standard_normal((900, d)).astype(np.float32)
+    x[3000:3900] = near / np.linalg.norm(near, axis=1, keepdims=True)
+    old = os.environ.get("VSK_FLAT_KERNEL")
+    os.environ["VSK_FLAT_KERNEL"] = "screen"
+    try:
+        sctx = Context(0)
+    finally:
+        if old is None:
+            del os.environ["VSK_FLAT_KERNEL"]
+        else:
+            os.environ["VSK_FLAT_KERNEL"] = old
+    db = VectorDatabase(sctx, x)
+    gd, gi = db.search(q, k, METRIC_COSINE_NORMALIZED)
+    waits = sctx.last_sync_count()
+    od, oi = O.search_flat(q, x, k, METRIC_COSINE_NORMALIZED)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+    print(f"segment overflow: {waits} host waits", flush=True)
+    assert waits > 2, "no chunk overflowed"
+    db.free()
+    sctx.close()

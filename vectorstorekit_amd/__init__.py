@@ -7,7 +7,9 @@ accelerator, index and quantizer interfaces on top.
 from ._lib import VSKError, library_path, load_library  # noqa: F401
 from .engine import (  # noqa: F401
     Context,
+    DistanceComputeBackend,
     DistanceMetric,
+    HIPAccelerationConfiguration,
     HIPAccelerationEngine,
     HIPAcceleratorStrategy,
     QuantizationMetadata,

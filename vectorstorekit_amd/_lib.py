@@ -78,6 +78,12 @@ class vsk_kernel_stat(ctypes.Structure):
                 ("work", c_double)]
 
 
+class vsk_config(ctypes.Structure):
+    _fields_ = [("kernel", c_int32), ("enable_profiling", c_int32), ("max_tile_bytes", c_int64)]
+
+
+KERNEL_AUTO, KERNEL_EXACT, KERNEL_SCREEN, KERNEL_BF16X3, KERNEL_FP32 = 0, 1, 2, 3, 4
+
 P = c_void_p  # every buffer argument is passed as a raw address
 PP = POINTER(c_void_p)
 
@@ -93,6 +99,8 @@ SIGNATURES = {
     "vsk_last_sync_count": (c_int32, [P]),
     "vsk_last_screen_redo": (c_int32, [P, c_int32, P, c_int64, P]),
     "vsk_measure_peaks": (c_int32, [P, POINTER(vsk_peaks)]),
+    "vsk_configure": (c_int32, [P, POINTER(vsk_config)]),
+    "vsk_get_config": (c_int32, [P, POINTER(vsk_config)]),
     "vsk_profile_enable": (c_int32, [P, c_int32]),
     "vsk_profile_only": (c_int32, [P, c_char_p]),
     "vsk_profile_reset": (c_int32, [P]),

@@ -577,7 +577,7 @@ static vsk_status bin_search_body(vsk_ctx *ctx, const vsk_bin *bin, const uint8_
     check_launch("bin_popcount");
   }
   const int64_t cap = default_cap(k);
-  const int64_t qb = query_batch(nq, cap);
+  const int64_t qb = query_batch(ctx, nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     BinArgs base{};

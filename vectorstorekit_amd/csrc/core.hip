@@ -472,6 +472,10 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
   c->flat_force_screen = fk && strcmp(fk, "screen") == 0;
   c->exact_only = fk && strcmp(fk, "exact") == 0;
+  if (const char *tb = getenv("VSK_MAX_TILE_BYTES")) {
+    const long long v = atoll(tb);
+    if (v > 0) c->max_tile_bytes = v;
+  }
   if (const char *ff = getenv("VSK_FAULT")) {
     const char *colon = strchr(ff, ':');
     const long long at = colon ? atoll(colon + 1) : 0;
@@ -524,6 +528,33 @@ vsk_status vsk_destroy(vsk_ctx *ctx) {
   (void)hipEventDestroy(ctx->call_end);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
+  return VSK_OK;
+}
+
+vsk_status vsk_configure(vsk_ctx *ctx, const vsk_config *cfg) {
+  if (!ctx || !cfg) return VSK_ERR_INVALID_ARGUMENT;
+  if (cfg->kernel < VSK_KERNEL_AUTO || cfg->kernel > VSK_KERNEL_FP32 || cfg->max_tile_bytes < 0) {
+    ctx->last_error = "invalid configuration";
+    return VSK_ERR_INVALID_ARGUMENT;
+  }
+  ctx->flat_fp32 = cfg->kernel == VSK_KERNEL_FP32;
+  ctx->flat_no_screen = cfg->kernel == VSK_KERNEL_FP32 || cfg->kernel == VSK_KERNEL_BF16X3;
+  ctx->flat_force_screen = cfg->kernel == VSK_KERNEL_SCREEN;
+  ctx->exact_only = cfg->kernel == VSK_KERNEL_EXACT;
+  ctx->profile = cfg->enable_profiling != 0;
+  ctx->max_tile_bytes = cfg->max_tile_bytes;
+  return VSK_OK;
+}
+
+vsk_status vsk_get_config(const vsk_ctx *ctx, vsk_config *cfg) {
+  if (!ctx || !cfg) return VSK_ERR_INVALID_ARGUMENT;
+  cfg->kernel = ctx->flat_fp32           ? VSK_KERNEL_FP32
+                : ctx->flat_no_screen    ? VSK_KERNEL_BF16X3
+                : ctx->flat_force_screen ? VSK_KERNEL_SCREEN
+                : ctx->exact_only        ? VSK_KERNEL_EXACT
+                                         : VSK_KERNEL_AUTO;
+  cfg->enable_profiling = ctx->profile ? 1 : 0;
+  cfg->max_tile_bytes = ctx->max_tile_bytes;
   return VSK_OK;
 }
 

@@ -517,7 +517,7 @@ void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  int32_t k, int32_t metric, uint64_t *best, int passes,
                  float *qnh, float *qnr, int64_t max_growth) {
   const int64_t cap = passes == 1 ? screen_cap(k) : default_cap(k);
-  const int64_t qb = query_batch(nq, cap);
+  const int64_t qb = query_batch(ctx, nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     const float *qbat = dq + b0 * db->ld;

@@ -737,7 +737,7 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
 void screen_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
                  int32_t k, int32_t metric, uint64_t *best, ScreenDeferred *defer) {
   const int32_t kc = screen_keep(k);
-  const int64_t qb = query_batch(nq, screen_cap(kc));
+  const int64_t qb = query_batch(ctx, nq, screen_cap(kc));
   if (defer) {
     // every batch enqueued; the failing counts come back with the call's
     // synchronisation (pinned slots taken before any work is queued)

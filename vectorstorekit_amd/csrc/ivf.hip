@@ -885,7 +885,7 @@ static void ivf_probe_device(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
 static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
                             int64_t nq, int32_t np, uint64_t *keys) {
   const int64_t cap = ivf->nlist;  // one dense chunk
-  const int64_t qb = query_batch(nq, cap);
+  const int64_t qb = query_batch(ctx, nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     FlatArgs base = centroid_args(ivf, dq + b0 * ivf->ld, nb);
@@ -911,7 +911,7 @@ static void ivf_probe_exact(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq,
 static void ivf_rank_all(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int64_t nq,
                          int32_t *probes) {
   const int64_t nl = ivf->nlist;
-  const int64_t qb = std::max<int64_t>(1, std::min<int64_t>(nq, (1ll << 26) / nl));
+  const int64_t qb = std::max<int64_t>(1, std::min<int64_t>(nq, tile_keys(ctx, 1ll << 26, 16) / nl));
   uint64_t *k0 = static_cast<uint64_t *>(
       ctx->scratch_ptr("ivf.rank0", sizeof(uint64_t) * (size_t)(qb * nl)));
   uint64_t *k1 = static_cast<uint64_t *>(
@@ -1488,7 +1488,8 @@ static void probe_screen(vsk_ctx *ctx, const vsk_ivf *ivf, const float *dq, int6
   const int32_t nlist = ivf->nlist, ld = ivf->ld, ldb = cdb->ldb;
   const int64_t wstride = ceil_div(nlist, 4) * 4;
   // batches whose words and fallback keys stay under 1 GiB
-  const int64_t qb = std::max<int64_t>(1, std::min<int64_t>(nq, (1ll << 27) / wstride));
+  const int64_t qb =
+      std::max<int64_t>(1, std::min<int64_t>(nq, tile_keys(ctx, 1ll << 27, 12) / wstride));
   const int32_t cap = std::max<int32_t>(1024, 4 * np);
   uint32_t *words = static_cast<uint32_t *>(
       ctx->scratch_ptr("ivf.pwords", sizeof(uint32_t) * qb * wstride));
@@ -1744,7 +1745,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   const int64_t ubound = probe_bound(ivf, np);
   // (pair ids q * np + p are 32-bit)
   const int64_t qb = std::max<int64_t>(
-      1, std::min<int64_t>({nq, (1ll << 27) / std::max<int64_t>(ubound, 1),
+      1, std::min<int64_t>({nq, tile_keys(ctx, 1ll << 27, 12) / std::max<int64_t>(ubound, 1),
                             (int64_t)INT32_MAX / np}));
   // the screen's groups are up to kScreenQ queries
   const int G = screen ? kScreenQ : QG;

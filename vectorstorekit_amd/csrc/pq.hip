@@ -1181,7 +1181,7 @@ static vsk_status pq_search_body(vsk_ctx *ctx, const vsk_pq *pq, const float *q,
   const bool screen = pq_screen_applies(ctx, pq, nq);
   const int64_t cap = screen ? std::max<int64_t>(default_cap(k_adc) / 2, 4 * (int64_t)k_adc)
                              : default_cap(k_adc);
-  const int64_t qb = query_batch(nq, cap);
+  const int64_t qb = query_batch(ctx, nq, cap);
   ArgminQueries qp;
   uint64_t *sthr = nullptr;
   if (screen) {

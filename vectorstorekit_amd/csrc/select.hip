@@ -1074,12 +1074,21 @@ int64_t screen_cap(int32_t k) {
   return c;
 }
 
-int64_t query_batch(int64_t nq, int64_t cap) {
-  // candidate buffers of one batch stay under ~2 GiB of HBM
-  const int64_t budget = 2ll << 30;
+int64_t query_batch(const vsk_ctx *ctx, int64_t nq, int64_t cap) {
+  // candidate buffers of one batch stay under the context's tile budget
+  // (2 GiB of HBM, at least 64 queries; VSK_MAX_TILE_BYTES sets it, down to
+  // one query a batch)
+  const int64_t budget = ctx->max_tile_bytes > 0 ? ctx->max_tile_bytes : 2ll << 30;
   int64_t b = budget / (cap * (int64_t)sizeof(uint64_t));
-  if (b < 64) b = 64;
+  const int64_t least = ctx->max_tile_bytes > 0 ? 1 : 64;
+  if (b < least) b = least;
   return nq < b ? nq : b;
+}
+
+int64_t tile_keys(const vsk_ctx *ctx, int64_t keys, int64_t bytes_per_key) {
+  if (ctx->max_tile_bytes <= 0) return keys;
+  const int64_t k = ctx->max_tile_bytes / bytes_per_key;
+  return k < keys ? (k > 0 ? k : 1) : keys;
 }
 
 void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
@@ -1196,6 +1205,11 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
           sb.active = ovf_mask;
           sb.overflow_mask = nullptr;
           sb.overflow_count = nullptr;
+          // a sub-chunk's keys are dense (cap a query), whatever the
+          // filtered chunk's layout was
+          sb.seg_n = nullptr;
+          sb.nseg = 0;
+          sb.seg_stride = 0;
           launch_select(ctx, sb, select_name);
         }
       }

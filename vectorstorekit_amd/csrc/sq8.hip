@@ -1011,7 +1011,7 @@ static vsk_status sq8_search_body(vsk_ctx *ctx, const vsk_sq8 *db,
   uint64_t *best = static_cast<uint64_t *>(
       ctx->scratch_ptr("sq8.best", sizeof(uint64_t) * nq * k));
   const int64_t cap = default_cap(k);
-  const int64_t qb = query_batch(nq, cap);
+  const int64_t qb = query_batch(ctx, nq, cap);
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     Sq8Args base{};

@@ -142,8 +142,12 @@ int64_t default_cap(int32_t k);
 // chunk and its selection, at a few more launches; measured at 1M x 768 with
 // 10,000 queries and k = 100 (kept 364): 5% faster than default_cap
 int64_t screen_cap(int32_t k);
-// largest query batch whose candidate buffers fit the scratch budget
-int64_t query_batch(int64_t nq, int64_t cap);
+// largest query batch whose candidate buffers (cap keys a query) fit the
+// context's tile budget
+int64_t query_batch(const vsk_ctx *ctx, int64_t nq, int64_t cap);
+// keys of bytes_per_key bytes a batch may hold: at most keys, and under
+// VSK_MAX_TILE_BYTES when it is set
+int64_t tile_keys(const vsk_ctx *ctx, int64_t keys, int64_t bytes_per_key);
 
 // decode keys: dist = float of the key (sqrt when sqrt_out), id =
 // id_map ? id_map[tie] : tie; VSK_KEY_NONE -> (+inf, -1)

@@ -104,6 +104,12 @@ struct vsk_ctx {
   bool flat_fp32 = false;
   bool flat_no_screen = false;
   bool flat_force_screen = false;
+  // VSK_MAX_TILE_BYTES: the largest working buffer a query batch may take
+  // (candidate keys and words); searches split their queries into batches
+  // under it, as MetalDistanceCompute chunks queries under its buffer limit
+  // (Acceleration/Metal/MetalDistanceCompute.swift:371-380, 450-473).  0:
+  // the defaults (2 GiB of candidate keys, at least 64 queries a batch)
+  int64_t max_tile_bytes = 0;
   // "exact": no bf16 screen anywhere -- the exact scans alone (flat search
   // on the exact VALU kernel for its screenable metrics, IVF's exact probe
   // and list scans, PQ's LUT scan over the codes, the exact argmin)

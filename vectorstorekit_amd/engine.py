@@ -68,10 +68,74 @@ def metric_code(metric) -> int:
     return DistanceMetric(metric).code
 
 
+class DistanceComputeBackend(str, enum.Enum):
+    """``DistanceComputeBackend`` (Config/Core/StoreConfiguration.swift:145-166)
+    with the ``hip`` case this build adds.  ``selectOptimal`` keeps the
+    reference's heuristics for its own backends and takes ``hip`` whenever a
+    HIP device serves the store: this build has no CPU product path, so small
+    batches run on the GPU too (the reference sends them to Accelerate)."""
+
+    metal = "metal"
+    accelerate = "accelerate"
+    simd = "simd"
+    auto = "auto"
+    hip = "hip"
+
+    def selectOptimal(self, dimension: int, candidateCount: int,
+                      hipAvailable: bool = True) -> "DistanceComputeBackend":
+        if self != DistanceComputeBackend.auto:
+            return self
+        if hipAvailable:
+            return DistanceComputeBackend.hip
+        if candidateCount > 1000:
+            return DistanceComputeBackend.metal
+        return (DistanceComputeBackend.simd if dimension == 512
+                else DistanceComputeBackend.accelerate)
+
+
+@dataclass(frozen=True)
+class HIPAccelerationConfiguration:
+    """``MetalComputeConfiguration`` (Config/Acceleration/
+    MetalComputeConfiguration.swift:8-46) for the HIP device, applied to a
+    context by ``vsk_configure``.
+
+    * ``kernel``: "auto" (the bf16 screen where it is exact and pays),
+      "exact" (exact scans only), "screen" (the screen at every size),
+      "bf16x3" / "fp32" (tolerance-path flat kernels);
+    * ``enableProfiling``: per-kernel HIP-event timing;
+    * ``maxTileBytes``: the working-buffer limit a query batch stays under
+      (0: the default, 2 GiB of candidate keys); searches chunk their
+      queries under it, as MetalDistanceCompute chunks under its buffer
+      limit (Acceleration/Metal/MetalDistanceCompute.swift:371-380);
+    * ``minBatchSizeForGPU``: kept for the reference's API; nothing is routed
+      to a CPU path by it here."""
+
+    kernel: str = "auto"
+    enableProfiling: bool = False
+    maxTileBytes: int = 0
+    minBatchSizeForGPU: int = 1000
+
+    _KERNELS = {"auto": 0, "exact": 1, "screen": 2, "bf16x3": 3, "fp32": 4}
+
+    def validate(self):
+        if self.kernel not in self._KERNELS:
+            raise VSKError(-2, f"unknown kernel choice {self.kernel!r}")
+        if self.maxTileBytes < 0 or self.minBatchSizeForGPU <= 0:
+            raise VSKError(-2, "maxTileBytes must be >= 0 and minBatchSizeForGPU positive")
+
+    @classmethod
+    def research(cls):
+        return cls(enableProfiling=True, minBatchSizeForGPU=500)
+
+    @classmethod
+    def efficient(cls):
+        return cls(enableProfiling=False, minBatchSizeForGPU=2000)
+
+
 class Context:
     """One ``vsk_ctx``: a device and the HIP stream every call runs on."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, configuration: HIPAccelerationConfiguration | None = None):
         self.lib = load_library()
         h = ctypes.c_void_p()
         st = self.lib.vsk_create(device, ctypes.byref(h))
@@ -79,6 +143,24 @@ class Context:
             raise VSKError(st, f"cannot open HIP device {device}")
         self.handle = h
         self.device = device
+        if configuration is not None:
+            self.configure(configuration)
+
+    def configure(self, configuration: HIPAccelerationConfiguration):
+        """Apply a configuration to later calls (``vsk_configure``)."""
+        configuration.validate()
+        cfg = _lib.vsk_config(configuration._KERNELS[configuration.kernel],
+                              1 if configuration.enableProfiling else 0,
+                              int(configuration.maxTileBytes))
+        self.check(self.lib.vsk_configure(self.handle, ctypes.byref(cfg)))
+
+    def configuration(self) -> HIPAccelerationConfiguration:
+        cfg = _lib.vsk_config()
+        self.check(self.lib.vsk_get_config(self.handle, ctypes.byref(cfg)))
+        names = {v: k for k, v in HIPAccelerationConfiguration._KERNELS.items()}
+        return HIPAccelerationConfiguration(kernel=names[cfg.kernel],
+                                            enableProfiling=bool(cfg.enable_profiling),
+                                            maxTileBytes=int(cfg.max_tile_bytes))
 
     def close(self):
         if getattr(self, "handle", None):
@@ -254,13 +336,15 @@ class HIPAcceleratorStrategy:
     identifier = "hip-gfx950"
     requirements = HardwareRequirements()
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0,
+                 configuration: HIPAccelerationConfiguration | None = None):
         self.device = device
+        self.configuration = configuration
         self._ctx: Context | None = None
 
     def initialize(self) -> Context:
         if self._ctx is None:
-            self._ctx = Context(self.device)
+            self._ctx = Context(self.device, self.configuration)
         return self._ctx
 
     def capabilities(self) -> dict:
