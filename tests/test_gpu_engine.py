@@ -43,12 +43,15 @@ def test_compute_distances_exact(ctx, metric, code):
 
 
 @pytest.mark.parametrize("metric,code", [("cosine", O.COSINE), ("dotProduct", O.DOT)])
-def test_compute_distances_float_bar(ctx, metric, code):
+def test_compute_distances_cosine_dot_exact(ctx, metric, code):
+    """cosine (the reference's epsilon form) and dot: the oracle's
+    sequential fp32 values bit for bit."""
     rng = np.random.default_rng(2)
     cand = rng.standard_normal((2000, 64)).astype(np.float32)
     q = rng.standard_normal(64).astype(np.float32)
     got = np.asarray(HIPAccelerationEngine(ctx).computeDistances(q, cand, metric))
-    np.testing.assert_allclose(got, O.distances(q[None], cand, code)[0], rtol=1e-4, atol=1e-4)
+    want = O.distances(q[None], cand, code)[0]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_batch_compute_distances(ctx):

@@ -12,7 +12,8 @@ import pytest
 from oracle import oracle as O
 from vectorstorekit_amd import (BinaryDatabase, BinaryQuantizer, IVFConfiguration, IVFIndex,
                                 ProductQuantizer, SQ8Database, VectorDatabase)
-from vectorstorekit_amd._lib import METRIC_COSINE_NORMALIZED, METRIC_L1, METRIC_L2SQ
+from vectorstorekit_amd._lib import (METRIC_COSINE, METRIC_COSINE_NORMALIZED, METRIC_L1,
+                                     METRIC_L2SQ)
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +40,15 @@ def test_flat_screen_one_wait(ctx):
     np.testing.assert_array_equal(gi, oi)
     np.testing.assert_array_equal(gd, od)
     assert waits == 1, f"{waits} host waits"
+    # the epsilon cosine: its relative bound is made once per database (one
+    # more wait in the first call), then one wait a call
+    xs = x * rng.uniform(0.5, 4.0, (n, 1)).astype(np.float32)
+    db2 = VectorDatabase(ctx, xs)
+    (gd, gi), waits = _twice(ctx, lambda: db2.search(q, k, METRIC_COSINE))
+    od, oi = O.search_flat(q, xs, k, METRIC_COSINE)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd, od)
+    assert waits == 1, f"{waits} host waits (cosine)"
 
 
 def test_sq8_one_wait(ctx):

@@ -297,8 +297,12 @@ void row_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
 // per row keeps the sequential sum; each wave stages 64 rows x 32 columns
 // at a time through LDS so the row reads stay coalesced.
 constexpr int NRM_COLS = 32;
+// With norms, the same sequential sums give norms[row] = sqrt(sum x_i^2)
+// and the rows are left as they are: the reference's |x| (cosine,
+// Acceleration/AccelerateOptimizer.swift:305-316 restated sequentially).
 __global__ __launch_bounds__(256) void k_normalize_rows(float *x, int64_t n,
-                                                       int32_t d, int32_t ld) {
+                                                       int32_t d, int32_t ld,
+                                                       float *norms) {
 #pragma clang fp contract(off)
   __shared__ float tile[4][64][NRM_COLS + 1];
   __shared__ float mag[4][64];
@@ -322,6 +326,10 @@ __global__ __launch_bounds__(256) void k_normalize_rows(float *x, int64_t n,
     }
     __syncthreads();
   }
+  if (norms) {
+    if (lane < rows) norms[row0 + lane] = sqrtf(s);
+    return;
+  }
   mag[w][lane] = sqrtf(s) + 1e-8f;
   __syncthreads();
   if (rows == 0) return;
@@ -330,6 +338,14 @@ __global__ __launch_bounds__(256) void k_normalize_rows(float *x, int64_t n,
     float *xr = x + (row0 + r) * ld;
     for (int32_t c = lane; c < d; c += 64) xr[c] = xr[c] / m;
   }
+}
+
+void seq_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
+               float *norms) {
+  if (n <= 0) return;
+  k_normalize_rows<<<(unsigned)ceil_div(n, 256), 256, 0, ctx->stream>>>(
+      const_cast<float *>(x), n, d, ld, norms);
+  check_launch("seq_norms");
 }
 
 // decode composite keys into (distance, id) outputs
@@ -663,7 +679,7 @@ vsk_status vsk_db_upload_f32(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
             sizeof(float) * d, n);
   if (flags & VSK_DB_NORMALIZE) {
     k_normalize_rows<<<(unsigned)ceil_div(n, 256), 256, 0, ctx->stream>>>(
-        db->x.as<float>(), n, d, db->ld);
+        db->x.as<float>(), n, d, db->ld, nullptr);
     check_launch("normalize_rows");
   }
   db->sqnorm.reserve(sizeof(float) * n);

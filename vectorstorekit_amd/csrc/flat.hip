@@ -186,7 +186,10 @@ __global__ __launch_bounds__(256) void k_flat_mfma(FlatArgs a) {
 constexpr int LS = FB_K + 1;  // odd stride: conflict-free column reads
 // sequential (dimension-order, no FMA) terms and final transforms of the
 // exact VALU kernel, one per metric of the CPU reference
-enum { OP_L1 = 0, OP_L2SEQ = 1, OP_L2SQSEQ = 2, OP_CNSEQ = 3, OP_DOTSEQ = 4, OP_HAM = 5 };
+//  OP_COSSEQ 1 - (sum q x)/(|q| |x| + 1e-8) with the norms the reference
+//           computes (AccelerateOptimizer.swift:285-320, sums sequential)
+enum { OP_L1 = 0, OP_L2SEQ = 1, OP_L2SQSEQ = 2, OP_CNSEQ = 3, OP_DOTSEQ = 4, OP_HAM = 5,
+       OP_COSSEQ = 6 };
 
 __device__ inline uint64_t shfl_xor_u64(uint64_t v, int m) {
   uint32_t lo = __shfl_xor((uint32_t)v, m);
@@ -238,10 +241,12 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
   bool qok[V];
   uint64_t th[V];
   uint64_t best[V];
+  float qn[V];  // OP_COSSEQ: the queries' norms
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     qi[v] = q0 + qsub + 8 * v;
     qok[v] = qi[v] < a.nq && (!a.active || a.active[qi[v]]);
+    qn[v] = (OP == OP_COSSEQ && qi[v] < a.nq) ? a.qaux[qi[v]] : 0.f;
     th[v] = (MODE == MODE_FILTER && qok[v]) ? a.thresh[qi[v]] : 0;
     best[v] = VSK_KEY_NONE;
   }
@@ -299,10 +304,12 @@ __global__ __launch_bounds__(256) void k_flat_valu(FlatArgs a, int32_t *argmin) 
     for (int u = 0; u < U; ++u) {
       const int64_t row = t0 + rsub + 32 * u;
       if (row >= s1) continue;
+      const float xn = OP == OP_COSSEQ ? a.xaux[row] : 0.f;
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         if (!qok[v]) continue;
-        const float dist = valu_final<OP>(acc[u][v]);
+        const float dist = OP == OP_COSSEQ ? 1.0f - acc[u][v] / (qn[v] * xn + 1e-8f)
+                                           : valu_final<OP>(acc[u][v]);
         if constexpr (MODE == MODE_ARGMIN) {
           uint64_t key = vsk_key(dist, (uint32_t)row);
           best[v] = key < best[v] ? key : best[v];
@@ -409,6 +416,7 @@ void launch_flat(vsk_ctx *ctx, FlatArgs a, int mode, int32_t *argmin) {
     case METRIC_L2SQ_EXACT: launch_valu_sized<OP_L2SQSEQ>(ctx, a, mode, argmin, small); break;
     case METRIC_CN_EXACT: launch_valu_sized<OP_CNSEQ>(ctx, a, mode, argmin, small); break;
     case METRIC_DOT_EXACT: launch_valu_sized<OP_DOTSEQ>(ctx, a, mode, argmin, small); break;
+    case METRIC_COS_EXACT: launch_valu_sized<OP_COSSEQ>(ctx, a, mode, argmin, small); break;
     default: fail(VSK_ERR_INVALID_ARGUMENT, "no exact kernel for this metric");
     }
   } else {
@@ -431,16 +439,28 @@ const float *x_aux(const vsk_db *db, int32_t metric) {
   if (metric == VSK_METRIC_L2SQ || metric == VSK_METRIC_L2)
     return db->sqnorm.as<float>();
   if (metric == VSK_METRIC_COSINE) return db->norm.as<float>();
+  if (metric == METRIC_COS_EXACT) {
+    if (!db->seqnorm.p) fail(VSK_ERR_EXECUTION_FAILED, "exact cosine norms not made");
+    return db->seqnorm.as<float>();
+  }
   return nullptr;
+}
+
+void ensure_seq_norms(vsk_ctx *ctx, const vsk_db *db) {
+  if (db->seqnorm.p) return;
+  db->seqnorm.reserve(sizeof(float) * (size_t)db->n);
+  seq_norms(ctx, db->x.as<float>(), db->n, db->d, db->ld, db->seqnorm.as<float>());
 }
 
 float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
              int32_t metric) {
   if (metric != VSK_METRIC_L2SQ && metric != VSK_METRIC_L2 &&
-      metric != VSK_METRIC_COSINE)
+      metric != VSK_METRIC_COSINE && metric != METRIC_COS_EXACT)
     return nullptr;
   float *aux = static_cast<float *>(ctx->scratch_ptr("flat.qaux", 4 * nq));
-  if (metric == VSK_METRIC_COSINE)
+  if (metric == METRIC_COS_EXACT)
+    seq_norms(ctx, dq, nq, d, ld, aux);
+  else if (metric == VSK_METRIC_COSINE)
     row_norms(ctx, dq, nq, d, ld, nullptr, aux);
   else
     row_norms(ctx, dq, nq, d, ld, aux, nullptr);
@@ -500,13 +520,20 @@ bool flat_topk_device(vsk_ctx *ctx, const vsk_db *db, const float *dq,
   // a small problem (at most 2^28 query x row x dimension terms, some 20 us
   // of exact VALU work) is cheaper by the exact sequential scan alone than
   // by the screen's fixed chain of launches and its check read-back
-  if (!ctx->flat_no_screen && !ctx->flat_force_screen && screen_applies(metric, k) &&
+  const bool screen = !ctx->flat_no_screen && screen_applies(metric, k);
+  if (screen && !ctx->flat_force_screen &&
       (ctx->exact_only || (double)nq * (double)db->n * (double)db->d <= 268435456.0)) {
     approx_topk(ctx, db, dq, nq, k, exact_metric(metric), best, 3);
     return true;
   }
-  if (!ctx->flat_no_screen && screen_applies(metric, k)) {
+  if (screen && (metric != VSK_METRIC_COSINE || cosine_screen_ok(ctx, db))) {
     screen_topk(ctx, db, dq, nq, k, metric, best, defer);
+    return true;
+  }
+  if (screen) {
+    // cosine over rows whose norms the screen's bound cannot cover: the
+    // exact scan
+    approx_topk(ctx, db, dq, nq, k, exact_metric(metric), best, 3);
     return true;
   }
   approx_topk(ctx, db, dq, nq, k, metric, best, 3);
@@ -521,6 +548,7 @@ void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     const float *qbat = dq + b0 * db->ld;
+    if (metric == METRIC_COS_EXACT) ensure_seq_norms(ctx, db);
     float *qa = q_aux(ctx, qbat, nb, db->d, db->ld, metric);
     FlatArgs base{};
     base.X = db->x.as<float>();
@@ -743,13 +771,22 @@ vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
   a.metric = metric;
   a.mat = om.ptr<float>();
   a.ldm = db->n;
-  // L2 and L2^2 sum (q - x)^2 in dimension order, as the reference does: the
-  // norm expansion |q|^2 + |x|^2 - 2 q.x of the MFMA path cancels for close
-  // pairs (a duplicate row gets sqrt of the rounding error, not 0)
-  if (metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ) {
+  // Every metric of the reference's CPU path is evaluated as it evaluates
+  // it, on the exact VALU kernel: L2 and L2^2 sum (q - x)^2 in dimension
+  // order (the norm expansion |q|^2 + |x|^2 - 2 q.x of an MFMA path cancels
+  // for close pairs: a duplicate row would get sqrt of the rounding error,
+  // not 0); cosine, normalised cosine and dot sum q.x in dimension order,
+  // cosine with the sequential norms.  The matrix is then the reference's
+  // bit for bit, and exactly symmetric when the rows are the queries.
+  if (exact_metric(metric) >= 0) {
     a.metric = exact_metric(metric);
     a.xaux = nullptr;
     a.qaux = nullptr;
+    if (metric == VSK_METRIC_COSINE) {
+      ensure_seq_norms(ctx, db);
+      a.xaux = x_aux(db, METRIC_COS_EXACT);
+      a.qaux = q_aux(ctx, dq, nq, db->d, db->ld, METRIC_COS_EXACT);
+    }
   }
   if (use_bf16x3(ctx, a.metric))
     launch_flat_bf16x3(ctx, a, make_split(ctx, db, dq, nq, true, nullptr, nullptr),

@@ -13,6 +13,9 @@ constexpr int32_t METRIC_L2_EXACT = 100;
 constexpr int32_t METRIC_L2SQ_EXACT = 101;
 constexpr int32_t METRIC_CN_EXACT = 102;
 constexpr int32_t METRIC_DOT_EXACT = 103;
+// the reference's cosine 1 - q.x/(|q||x| + 1e-8): the dot product summed in
+// dimension order, with the norms of seq_norms (a.qaux, a.xaux)
+constexpr int32_t METRIC_COS_EXACT = 104;
 // the exact VALU metric that computes a public metric as the CPU reference
 // does (-1 if none)
 inline int32_t exact_metric(int32_t metric) {
@@ -21,6 +24,7 @@ inline int32_t exact_metric(int32_t metric) {
   case VSK_METRIC_L2: return METRIC_L2_EXACT;
   case VSK_METRIC_COSINE_NORMALIZED: return METRIC_CN_EXACT;
   case VSK_METRIC_DOT: return METRIC_DOT_EXACT;
+  case VSK_METRIC_COSINE: return METRIC_COS_EXACT;
   case VSK_METRIC_L1: return VSK_METRIC_L1;
   case VSK_METRIC_HAMMING: return VSK_METRIC_HAMMING;
   default: return -1;
@@ -97,11 +101,28 @@ __device__ inline float f_down(double v) {
 // every screened distance lies within eps of the reference's fp32 one.
 // With the query as two bf16 planes (q = qh' + ql' + r), qh is |qh'| + |ql'|,
 // qr is |r| and the screen sums nprod = 2d exact products instead of d.
+// Cosine with the reference's epsilon (1 - q.x/(|q||x| + 1e-8)): xh and xr
+// are then the maxima over the rows of |bf16(x)| / |x| and |x - bf16(x)| /
+// |x| (|x| the fp32 norm the screen divides by, rows of norm 0 excluded:
+// both forms give exactly 1 there) and qnorm the query's fp32 norm.  The dot
+// product's error is then at most |x| (qh xr + qr xh + qr xr + 2(d-1)u qh xh)
+// and its quotient by |q||x| + 1e-8 at most that over |q| (times 1 + (d+8)u
+// for the norms' roundings); the reference's own sums, norms, quotient and
+// subtraction err by at most (2.1 d + 11) u and the screen's fp32 norms and
+// last operations by (1.1 d + 9) u.  A zero query gives 1 for every row in
+// both forms (no error); a query of tiny or non-finite norm gets no bound
+// (it fails the check and is redone exactly).
 __device__ inline double screen_eps_of(double qh, double qr, double xh, double xr, int32_t d,
-                                       int32_t metric, int32_t nprod = 0) {
+                                       int32_t metric, int32_t nprod = 0, double qnorm = 0.0) {
   const double u = 0x1p-24;
   const double qn = qh + qr, xn = xh + xr, dd = (double)d;
   const double np = nprod > 0 ? (double)nprod : dd;
+  if (metric == VSK_METRIC_COSINE) {
+    if (qh == 0.0 && qr == 0.0) return 4.0 * u;
+    if (!(qnorm >= 0x1p-60) || !(qnorm <= 0x1p60)) return __builtin_inf();
+    const double x = qh * xr + qr * xh + qr * xr + 2.0 * (np - 1.0) * u * qh * xh;
+    return (x / qnorm * (1.0 + (dd + 8.0) * u) + (3.2 * dd + 20.0) * u + 0x1p-80) * 1.01;
+  }
   const double e_dot =
       qh * xr + qr * xh + qr * xr + 2.0 * (np - 1.0) * u * qh * xh + np * 0x1p-126;
   const double e_ref = 1.01 * dd * u * qn * xn;
@@ -233,8 +254,11 @@ void approx_topk(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
 // |hi| into qnh and |q - hi| into qnr when given)
 SplitPtrs make_split(vsk_ctx *ctx, const vsk_db *db, const float *dq,
                      int64_t nq, bool qlo, float *qnh, float *qnr);
-// |x|^2 (L2 metrics) or |x| (cosine) of the rows / of a query batch
+// |x|^2 (L2 metrics) or |x| (cosine) of the rows / of a query batch; for
+// METRIC_COS_EXACT the reference's sequential norms (ensure_seq_norms makes
+// the rows' first)
 const float *x_aux(const vsk_db *db, int32_t metric);
+void ensure_seq_norms(vsk_ctx *ctx, const vsk_db *db);
 float *q_aux(vsk_ctx *ctx, const float *dq, int64_t nq, int32_t d, int32_t ld,
              int32_t metric);
 // bf16 planes and norms of a query batch for screen_argmin: hi plane
@@ -247,7 +271,8 @@ struct CheckArgs {
   int64_t nq;
   int32_t k, kc, d, metric;
   const float *qnh, *qnr;  // per query |qh|, |q - qh|
-  double xh, xr;           // maxima over the rows of |xh|, |x - xh|
+  double xh, xr;           // maxima over the rows of |xh|, |x - xh| (cosine: relative)
+  const float *qn = nullptr;  // cosine: per query |q| (fp32, as the screen divides)
   uint8_t *ok;
   int32_t *nvalid;
   int32_t *fails;
@@ -285,6 +310,10 @@ void screen_argmin(vsk_ctx *ctx, const float *X, const float *xsq, int64_t n,
 // order ranks them (a query failing the bound is redone by the exact VALU
 // scan); best: final keys (exact distances)
 bool screen_applies(int32_t metric, int32_t k);
+// cosine through the screen needs the rows' relative residual maxima (made
+// here once per database); false when a row's norm is too small or not
+// finite for the bound (cosine then takes the exact scan)
+bool cosine_screen_ok(vsk_ctx *ctx, const vsk_db *db);
 int32_t screen_keep(int32_t k);
 // With defer, screen_topk queues every batch without waiting for the bound
 // check: each batch's count of failing queries goes to pinned memory with

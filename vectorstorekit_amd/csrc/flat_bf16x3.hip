@@ -393,7 +393,8 @@ constexpr int XS_LDS_XA = XS_LDS + 4 * XS_N * 4;
 template <int MODE, int METRIC>
 constexpr bool xs_norms_in_lds() {
   return MODE == MODE_TOP2 ||
-         (MODE == MODE_FILTER && (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2));
+         (MODE == MODE_FILTER && (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2 ||
+                                  METRIC == VSK_METRIC_COSINE));
 }
 
 __device__ __forceinline__ float top2_keydist(uint64_t k) {
@@ -514,6 +515,26 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         } else {
           const double xq = 1.01 * sqrt(qa) + sqrt(0.03 * qa + fabs(t) + 1.0);
           const double m = 0.5 * (qa - t) - 0x1p-20 * (fabs(t) + qa + xq * xq + 1.0);
+          f = (float)m;
+          if ((double)f > m) f = __uint_as_float(f > 0.f ? __float_as_uint(f) - 1u
+                                                 : (f < 0.f ? __float_as_uint(f) + 1u
+                                                            : 0x80000001u));
+        }
+        s_tdot[tid] = f;
+      } else if constexpr (METRIC == VSK_METRIC_COSINE) {
+        // cosine (with the reference's epsilon): a <= thf is
+        // dot >= (1 - thf) den, den = |q||x| + 1e-8 > 0; the bound t2 on
+        // dot / den sits 2^-20 (1 + |1 - thf|) below 1 - thf, more than
+        // the roundings of either form, so no score whose exact test below
+        // passes is under it
+        float f;
+        if (!ok) {
+          f = __int_as_float(0x7f800000);
+        } else if (th_hi == 0xFFFFFFFFu) {
+          f = -__int_as_float(0x7f800000);
+        } else {
+          const double t = 1.0 - (double)thf;
+          const double m = t - 0x1p-20 * (1.0 + fabs(t));
           f = (float)m;
           if ((double)f > m) f = __uint_as_float(f > 0.f ? __float_as_uint(f) - 1u
                                                  : (f < 0.f ? __float_as_uint(f) + 1u
@@ -782,6 +803,29 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               m |= (acc[i][j][r] < tdot) ? 0u : (1u << (4 * i + r));
+        } else if constexpr (METRIC == VSK_METRIC_COSINE) {
+          // dot - t2 (|q||x| + 1e-8) >= 0 with the row norms from LDS; the
+          // block's largest first (a NaN score is dropped by the max: it
+          // needs a non-finite input, whose query fails the screen's check)
+          const float t2 = l_tdot[16 * j];
+          float mx = -__int_as_float(0x7f800000);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float xn = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r];
+              mx = fmaxf(mx, __builtin_fmaf(-t2, __builtin_fmaf(qa, xn, 1e-8f), acc[i][j][r]));
+            }
+          if (!__builtin_amdgcn_ballot_w64(!(mx < 0.f))) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float xn = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * i + r];
+              m |= (__builtin_fmaf(-t2, __builtin_fmaf(qa, xn, 1e-8f), acc[i][j][r]) < 0.f)
+                       ? 0u
+                       : (1u << (4 * i + r));
+            }
         } else {
           const float th_f = l_thf[16 * j];
           // the block's largest dot - |x|^2/2 first, against the query's
@@ -937,6 +981,12 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
         reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_DOT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
+        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_COSINE>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    VSK_HIP(hipFuncSetAttribute(
+        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_COSINE>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
+    VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_DOT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
@@ -1018,6 +1068,7 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     launch_s<VSK_METRIC_COSINE_NORMALIZED>(ctx, (unsigned)nblocks, a, s, mode);
     break;
   case VSK_METRIC_DOT: launch_s<VSK_METRIC_DOT>(ctx, (unsigned)nblocks, a, s, mode); break;
+  case VSK_METRIC_COSINE: launch_s<VSK_METRIC_COSINE>(ctx, (unsigned)nblocks, a, s, mode); break;
   default: fail(VSK_ERR_UNSUPPORTED, "metric without a one-pass screen");
   }
   check_launch(names[mode]);

@@ -33,6 +33,7 @@
 // Acceleration/AccelerateOptimizer.swift:251-383 restated sequentially), so
 // the returned distances are bit-identical to it and the order is (distance,
 // row id) over exact fp32 distances.
+#include <cstring>
 #include <vector>
 
 #include "flat.hpp"
@@ -41,9 +42,72 @@ namespace vsk {
 
 bool screen_applies(int32_t metric, int32_t k) {
   if (metric != VSK_METRIC_L2SQ && metric != VSK_METRIC_L2 &&
-      metric != VSK_METRIC_COSINE_NORMALIZED && metric != VSK_METRIC_DOT)
+      metric != VSK_METRIC_COSINE_NORMALIZED && metric != VSK_METRIC_DOT &&
+      metric != VSK_METRIC_COSINE)
     return false;
   return screen_keep(k) <= VSK_MAX_K;
+}
+
+// per row (one wave): |bf16(x)| and |x - bf16(x)| (sums of squares in
+// double, square roots rounded up) over the fp32 norm |x| the screen
+// divides by, their maxima over the rows with |x| > 0 as float bits
+// (atomic max, ratios rounded up) in rel[0..1]; rel[2] = 1 when a row with
+// a nonzero component has a norm below 2^-60 or not finite
+__global__ __launch_bounds__(256) void k_cos_rel(const float *x, int64_t n, int32_t d,
+                                                 int32_t ld, const float *norm, uint32_t *rel) {
+  const int lane = threadIdx.x & 63;
+  uint32_t mh = 0, mr = 0, bad = 0;
+  for (int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += (int64_t)gridDim.x * 4) {
+    double sh = 0.0, sr = 0.0;
+    for (int32_t c = lane; c < d; c += 64) {
+      const float v = x[r * ld + c];
+      const float hv = __uint_as_float((uint32_t)bf16_rn(v) << 16);
+      const float rv = v - hv;  // exact
+      sh += (double)hv * (double)hv;
+      sr += (double)rv * (double)rv;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      sh += __shfl_xor(sh, o);
+      sr += __shfl_xor(sr, o);
+    }
+    const double nx = (double)norm[r];
+    if (sh == 0.0 && sr == 0.0) continue;  // a zero row: exactly 1 either way
+    if (!(nx >= 0x1p-60) || !(nx <= 0x1p60)) {
+      bad = 1;
+      continue;
+    }
+    const float a = f_up(sqrt(sh) / nx * (1.0 + 1e-12));
+    const float b = f_up(sqrt(sr) / nx * (1.0 + 1e-12));
+    mh = __float_as_uint(a) > mh ? __float_as_uint(a) : mh;
+    mr = __float_as_uint(b) > mr ? __float_as_uint(b) : mr;
+  }
+  if (lane == 0) {
+    if (mh | mr) {
+      atomicMax(&rel[0], mh);
+      atomicMax(&rel[1], mr);
+    }
+    if (bad) atomicMax(&rel[2], 1u);
+  }
+}
+
+bool cosine_screen_ok(vsk_ctx *ctx, const vsk_db *db) {
+  if (db->cos_state == 0) {
+    uint32_t *rel = static_cast<uint32_t *>(ctx->scratch_ptr("screen.cosrel", 16));
+    fill_i32(ctx, reinterpret_cast<int32_t *>(rel), 4, 0);
+    int64_t g = ceil_div(db->n, 4);
+    if (g > 16384) g = 16384;
+    k_cos_rel<<<(unsigned)g, 256, 0, ctx->stream>>>(db->x.as<float>(), db->n, db->d, db->ld,
+                                                    db->norm.as<float>(), rel);
+    check_launch("cos_rel");
+    uint32_t h[3];
+    VSK_HIP(hipMemcpyAsync(h, rel, sizeof(h), hipMemcpyDeviceToHost, ctx->stream));
+    stream_sync(ctx);
+    std::memcpy(&db->cos_rel_hi, &h[0], sizeof(float));
+    std::memcpy(&db->cos_rel_res, &h[1], sizeof(float));
+    db->cos_state = h[2] ? -1 : 1;
+  }
+  return db->cos_state > 0;
 }
 
 // candidates kept per query: on config 2 (k = 100) some 200-250 rows fall
@@ -100,7 +164,7 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
 #pragma unroll
     for (int i = 0; i < 16; ++i) buf[i] = *reinterpret_cast<const rs_f4 *>(src[i] + col);
   }
-  float s = 0.f;
+  float s = 0.f, sq = 0.f, sx = 0.f;  // (cosine: the two norms' sums)
   for (int32_t j0 = 0; j0 < d; j0 += RS_W) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -125,6 +189,10 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
         s = s + tt * tt;
       } else {
         s = s + qv * xv;
+        if constexpr (METRIC == VSK_METRIC_COSINE) {
+          sq = sq + qv * qv;
+          sx = sx + xv * xv;
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -140,13 +208,16 @@ __global__ __launch_bounds__(256) void k_rescore(const float *X, int64_t ldx,
   if constexpr (METRIC == VSK_METRIC_L2SQ) dist = s;
   else if constexpr (METRIC == VSK_METRIC_L2) dist = sqrtf(s);
   else if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED) dist = 1.0f - s;
+  else if constexpr (METRIC == VSK_METRIC_COSINE)
+    dist = 1.0f - s / (sqrtf(sq) * sqrtf(sx) + 1e-8f);  // the reference's formula
   else dist = -s;
   out[q * kc + c] = vsk_key(dist, row);
 }
 
 // the screen's error bound eps(q) for the metric (see the file comment)
 __device__ double screen_eps(const CheckArgs &a, int64_t q) {
-  return screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric);
+  return screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, 0,
+                       a.qn ? (double)a.qn[q] : 0.0);
 }
 
 __global__ void k_screen_check(CheckArgs a) {
@@ -231,6 +302,10 @@ static void rescore(vsk_ctx *ctx, const vsk_db *db, const float *dq, int64_t nq,
     k_rescore<VSK_METRIC_COSINE_NORMALIZED><<<grid, 256, 0, ctx->stream>>>(
         X, db->ld, dq, db->ld, db->d, cand, kc, nvalid, out);
     break;
+  case VSK_METRIC_COSINE:
+    k_rescore<VSK_METRIC_COSINE><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld, db->d,
+                                                                cand, kc, nvalid, out);
+    break;
   default:
     k_rescore<VSK_METRIC_DOT><<<grid, 256, 0, ctx->stream>>>(X, db->ld, dq, db->ld,
                                                              db->d, cand, kc, nvalid, out);
@@ -296,6 +371,15 @@ static std::vector<int32_t> screen_tier(vsk_ctx *ctx, const vsk_db *db,
   ca.qnr = qn + nb;
   ca.xh = db->split_max_hi;
   ca.xr = db->split_max_res;
+  if (metric == VSK_METRIC_COSINE) {
+    // relative maxima and the queries' fp32 norms (those the screen divided by)
+    ca.xh = db->cos_rel_hi;
+    ca.xr = db->cos_rel_res;
+    float *qnorm = static_cast<float *>(ctx->scratch_ptr(
+        std::string("screen.qn") + tag, sizeof(float) * (size_t)nb));
+    row_norms(ctx, qbat, nb, db->d, db->ld, nullptr, qnorm);
+    ca.qn = qnorm;
+  }
   ca.ok = ok;
   ca.nvalid = nvalid;
   ca.fails = fails;

@@ -190,6 +190,15 @@ struct vsk_db {
   // lo plane only for the bf16x3 kernel; the screen reads hi alone), and
   // the maxima over the rows of |hi| and |x - hi| (the screen's bound)
   mutable vsk::DevBuf split, split_lo;
+  // the reference's |x| per row (seq_norms), built when the exact cosine
+  // first needs it
+  mutable vsk::DevBuf seqnorm;
+  // the screen's bound for cosine: maxima over the rows with 0 < |x| of
+  // |bf16(x)| / |x| and |x - bf16(x)| / |x| (|x| the fp32 norm above);
+  // cos_state 0 = not made, 1 = made, -1 = a row's norm is too small or not
+  // finite for the bound (cosine then takes the exact scan)
+  mutable int32_t cos_state = 0;
+  mutable float cos_rel_hi = 0.f, cos_rel_res = 0.f;
   mutable int32_t ldb = 0;
   mutable float split_max_hi = 0.f, split_max_res = 0.f;
 };
@@ -287,6 +296,10 @@ void fill_i32(vsk_ctx *ctx, int32_t *p, int64_t n, int32_t v);
 // sq[i] = sum x^2 (fp32), nrm[i] = sqrt(sq[i]); either may be null.
 void row_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
                float *sq, float *nrm);
+// norms[i] = sqrtf of the squares of row i summed in dimension order without
+// FMA: the |x| of the reference's cosine, bit for bit
+void seq_norms(vsk_ctx *ctx, const float *x, int64_t n, int32_t d, int32_t ld,
+               float *norms);
 
 }  // namespace vsk
 

@@ -536,9 +536,8 @@ class HIPAccelerationEngine:
         MetalDistanceMatrix.swift:49-120): the |A| x |B| distance matrix;
         vectorsB None is the symmetric matrix of A, whose upper triangle
         (i <= j) is mirrored below the diagonal as the reference does
-        (:340-385): the split-bf16 products add their two cross terms in
-        opposite orders for (i, j) and (j, i), so only the mirror is exactly
-        symmetric."""
+        (:340-385).  Every metric is summed in the reference's order on the
+        exact kernel, so (i, j) and (j, i) are equal already."""
         b = vectorsA if vectorsB is None else vectorsB
         m = self._with_db(b, lambda db: db.distances(vectorsA, metric))
         if vectorsB is None:
