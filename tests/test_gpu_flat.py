@@ -173,12 +173,14 @@ def sctx():
 @pytest.mark.parametrize("metric", SCREEN)
 @pytest.mark.parametrize("shape", [(3000, 20, 128, 10), (40_000, 64, 100, 50),
                                    (20_000, 33, 37, 100), (25_000, 10, 768, 320),
-                                   (6000, 12, 96, 20)])
+                                   (6000, 12, 96, 20), (30_000, 6, 64, 700),
+                                   (4000, 5, 48, 1024), (900, 3, 16, 1024)])
 def test_screen_bit_exact(sctx, metric, shape):
     """The screened metrics (one-pass bf16 screen, proven bound, fp32
     rescore) return the CPU reference's sequential fp32 distances and its
     (distance, id) order exactly: one dense chunk, filtered chunks, odd d,
-    and the largest k the screen takes."""
+    k above 320 (the screen keeps VSK_MAX_K candidates, a narrower margin),
+    k = VSK_MAX_K (no margin: the exact scan unless every row is kept)."""
     n, nq, d, k = shape
     x, q = _data(n + d + metric, n, nq, d, normalize=metric == METRIC_COSINE_NORMALIZED)
     print(f"screen metric={metric} n={n} nq={nq} d={d} k={k}", flush=True)

@@ -45,7 +45,7 @@ bool screen_applies(int32_t metric, int32_t k) {
       metric != VSK_METRIC_COSINE_NORMALIZED && metric != VSK_METRIC_DOT &&
       metric != VSK_METRIC_COSINE)
     return false;
-  return screen_keep(k) <= VSK_MAX_K;
+  return k <= VSK_MAX_K;
 }
 
 // per row (one wave): |bf16(x)| and |x - bf16(x)| (sums of squares in
@@ -114,8 +114,11 @@ bool cosine_screen_ok(vsk_ctx *ctx, const vsk_db *db) {
 // within the bound's margin of the k-th, so 3k + 64 makes the second,
 // wider screen rare
 int32_t screen_keep(int32_t k) {
+  // 3k + 64, at least 256, at most the selection's VSK_MAX_K: above k = 320
+  // the margin narrows (k = VSK_MAX_K keeps none, so only a database of at
+  // most VSK_MAX_K rows passes the check; the others go to the exact scan)
   const int32_t kc = 3 * k + 64;
-  return kc < 256 ? 256 : kc;
+  return kc < 256 ? 256 : (kc > VSK_MAX_K ? VSK_MAX_K : kc);
 }
 
 // Exact distance of each screened candidate, summed in dimension order
