@@ -61,6 +61,26 @@ def test_metrics_shapes(ctx, metric, shape):
     _check(ctx, x, q, k, metric, exact=True)
 
 
+@pytest.mark.parametrize("kernel", ["bf16x3", "fp32"])
+def test_named_kernels_float_bar(ctx, kernel):
+    """The tolerance-path kernels a configuration selects by name (bf16x3,
+    fp32 MFMA) for every metric: distances within 1e-4 relative of the
+    oracle's, id sets equal except ties within that tolerance; Manhattan
+    stays on the exact VALU scan (bit-exact) under either."""
+    from vectorstorekit_amd.engine import Context, HIPAccelerationConfiguration
+
+    c = Context(0, configuration=HIPAccelerationConfiguration(kernel=kernel))
+    try:
+        assert c.configuration().kernel == kernel
+        for metric in ALL:
+            x, q = _data(300 + metric, 20_000, 37, 96,
+                         normalize=metric == METRIC_COSINE_NORMALIZED)
+            print(f"kernel={kernel} metric={metric}", flush=True)
+            _check(c, x, q, 50, metric, exact=metric == METRIC_L1)
+    finally:
+        c.close()
+
+
 def test_chunked_path_large_n(ctx):
     """n well above the first chunk: exercises the filtered, atomic-append
     pass and the running thresholds."""
