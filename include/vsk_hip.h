@@ -229,6 +229,14 @@ vsk_status vsk_search_flat_filtered(vsk_ctx *ctx, const vsk_db *db, const float 
  * (:76-136, nq = 1) and batchComputeDistances(topK: nil) (:139-204). */
 vsk_status vsk_distances(vsk_ctx *ctx, const vsk_db *db, const float *q,
                          int64_t nq, int32_t metric, float *out);
+/* MetalAccelerationEngine.matrixMultiply(matrixA:matrixB:)
+ * (Acceleration/MetalAccelerationEngine.swift:209-229): c (m x n) =
+ * a (m x k) . b (k x n), row-major fp32.  Every entry is summed over the k
+ * products in order from 0, a product and then a sum (no FMA), as the
+ * reference's CPU loop adds it (Acceleration/Metal/MetalMatrixCompute.swift:
+ * 791-806).  Pointers may be host or device memory. */
+vsk_status vsk_matrix_multiply(vsk_ctx *ctx, const float *a, int64_t m, int32_t k,
+                               const float *b, int64_t n, float *c);
 
 /* ---- IVF-Flat ------------------------------------------------------------
  * IVFIndex (Indexes/IVFIndex.swift).  The coarse centroids come from

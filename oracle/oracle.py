@@ -39,6 +39,7 @@ def lib():
             "vsko_l1": (c_float, [P, P, c_int32]),
             "vsko_distance": (c_float, [P, P, c_int32, c_int32]),
             "vsko_normalize": (None, [P, c_int64, c_int32, P]),
+            "vsko_matmul": (None, [P, c_int64, c_int32, P, c_int64, P]),
             "vsko_hnsw_distance": (c_float, [P, P, c_int32, c_int32]),
             "vsko_hnsw_distances": (None, [P, c_int64, P, c_int32, P, P, c_int32, P]),
             "vsko_scalar_quantize_u8": (None, [P, c_int64, c_int32, c_int32, P, P, P]),
@@ -137,6 +138,17 @@ def normalize(x):
     x, xp = _c(x, np.float32)
     out = np.empty_like(x)
     lib().vsko_normalize(xp, x.shape[0], x.shape[1], out.ctypes.data)
+    return out
+
+
+def matmul(a, b):
+    """matrixMultiply: a (m x k) times b (k x n), each entry summed over k in
+    order from 0, a product then a sum (MetalMatrixCompute.swift:791-806)."""
+    a, ap = _c(a, np.float32)
+    b, bp = _c(b, np.float32)
+    assert a.ndim == 2 and b.ndim == 2 and a.shape[1] == b.shape[0]
+    out = np.empty((a.shape[0], b.shape[1]), np.float32)
+    lib().vsko_matmul(ap, a.shape[0], a.shape[1], bp, b.shape[1], out.ctypes.data)
     return out
 
 

@@ -214,6 +214,19 @@ void vsko_normalize(const float *x, int64_t n, int32_t d, float *out) {
   }
 }
 
+/* matrixMultiply's CPU loop (Acceleration/Metal/MetalMatrixCompute.swift:
+ * 791-806): result[i][j] starts at 0 and adds a[i][t] * b[t][j] for t in
+ * order (a product, then a sum).  a is m x k, b is k x n, c is m x n, all
+ * row-major. */
+void vsko_matmul(const float *a, int64_t m, int32_t k, const float *b, int64_t n, float *c) {
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      float s = 0.0f;
+      for (int32_t t = 0; t < k; ++t) s += a[i * k + t] * b[(int64_t)t * n + j];
+      c[i * n + j] = s;
+    }
+}
+
 /* 16 independent accumulators: what a SIMD library loop does.  Used only by
  * the CPU-baseline timing (fast != 0), never by parity checks. */
 static float dot16(const float *a, const float *b, int32_t d) {

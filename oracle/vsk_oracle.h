@@ -54,6 +54,8 @@ void vsko_hnsw_distances(const float *q, int64_t nq, const float *x, int32_t d,
                          float *out);
 /* normalizeVectors: out = x / (sqrt(sum x^2) + 1e-8) per row */
 void vsko_normalize(const float *x, int64_t n, int32_t d, float *out);
+/* matrixMultiply: c (m x n) = a (m x k) . b (k x n), sequential sums */
+void vsko_matmul(const float *a, int64_t m, int32_t k, const float *b, int64_t n, float *c);
 /* out[i*n + j] = distance(q_i, x_j) */
 void vsko_distances(const float *q, int64_t nq, const float *x, int64_t n,
                     int32_t d, int32_t metric, float *out, int32_t nthreads);

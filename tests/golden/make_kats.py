@@ -52,6 +52,14 @@ KATS = {
         "clusters": 32, "per_cluster": 20, "dim": 128, "inserted": 100,
         "query_row": 50, "k": 10,
     },
+    "matrix_multiply": {
+        "_cite": "MetalComponentTests.swift:244-271 and MetalComputeIntegrationTests.swift:"
+                 "105-121: [[1,2,3],[4,5,6]] x [[7,8],[9,10],[11,12]] = [[58,64],[139,154]]",
+        "a": [[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]],
+        "b": [[7.0, 8.0], [9.0, 10.0], [11.0, 12.0]],
+        "c": [[58.0, 64.0], [139.0, 154.0]],
+        "tolerance": 0.001,
+    },
     "sq8_roundtrip": {
         "_cite": "ScalarQuantizerTests.swift:55-74: int8 round trip of "
                  "[-1,-0.5,0,0.5,1] within 0.1",

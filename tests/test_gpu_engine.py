@@ -154,3 +154,38 @@ def test_measure_peaks_plausible():
     for key, sheet in (("bf16_tflops", 2500.0), ("int8_tops", 5000.0), ("hbm_gbs", 8000.0),
                        ("hbm_read_gbs", 8000.0)):
         assert 0.25 * sheet < pk[key] < 1.1 * sheet, (key, pk[key])
+
+
+def test_matrix_multiply_bit_exact(ctx):
+    """matrixMultiply (MetalAccelerationEngine.swift:209-229): the
+    reference test's known answer (MetalComponentTests.swift:244-271), then
+    ragged shapes (partial tiles in every dimension, k past one inner step,
+    single rows and columns) and device tensors, each entry the oracle's
+    in-order sum bit for bit; a dimension mismatch and an empty matrix
+    raise."""
+    import json
+    import os
+
+    eng = HIPAccelerationEngine(ctx)
+    kat = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                      "reference_kats.json")))["matrix_multiply"]
+    c = np.asarray(eng.matrixMultiply(kat["a"], kat["b"]))
+    np.testing.assert_array_equal(c, np.array(kat["c"], np.float32))
+    rng = np.random.default_rng(11)
+    for m, k, n in ((1, 1, 1), (67, 33, 130), (64, 32, 64), (5, 1000, 3), (300, 768, 257)):
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        print(f"matmul {m}x{k}x{n}", flush=True)
+        got = np.asarray(eng.matrixMultiply(a, b))
+        np.testing.assert_array_equal(got.view(np.uint32), O.matmul(a, b).view(np.uint32))
+    import torch
+
+    a = rng.standard_normal((129, 70)).astype(np.float32)
+    b = rng.standard_normal((70, 65)).astype(np.float32)
+    got = eng.matrixMultiply(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda())
+    assert got.is_cuda
+    np.testing.assert_array_equal(got.cpu().numpy(), O.matmul(a, b))
+    with pytest.raises(VSKError):
+        eng.matrixMultiply(a, a)
+    with pytest.raises(VSKError):
+        eng.matrixMultiply(np.empty((0, 4), np.float32), np.ones((4, 2), np.float32))

@@ -548,3 +548,29 @@ class HIPAccelerationEngine:
             else:
                 m = np.triu(m) + np.triu(m, 1).T
         return m
+
+    def matrixMultiply(self, matrixA, matrixB):
+        """MetalAccelerationEngine.matrixMultiply(matrixA:matrixB:)
+        (Acceleration/MetalAccelerationEngine.swift:209-229): A (m x k) times
+        B (k x n) as an m x n fp32 matrix (``vsk_matrix_multiply``).  Each
+        entry is summed over k in order from 0, a product and then a sum, as
+        the reference's CPU loop adds it (Acceleration/Metal/
+        MetalMatrixCompute.swift:791-806).  A column count of A that differs
+        from B's row count raises (the reference's
+        MetalMatrixError.dimensionMismatch, MetalAccelerationEngine.swift:
+        491-496)."""
+        a = matrixA if _lib._is_torch(matrixA) else np.asarray(matrixA, np.float32)
+        b = matrixB if _lib._is_torch(matrixB) else np.asarray(matrixB, np.float32)
+        if a.ndim != 2 or b.ndim != 2:
+            raise VSKError(-2, "matrixMultiply takes two 2-d matrices")
+        m, k = int(a.shape[0]), int(a.shape[1])
+        if int(b.shape[0]) != k:
+            raise VSKError(-4, f"dimension mismatch: a is {m} x {k}, b is "
+                               f"{int(b.shape[0])} x {int(b.shape[1])}")
+        n = int(b.shape[1])
+        ap, ak = as_buffer(a, np.float32, (m, k))
+        bp, bk = as_buffer(b, np.float32, (k, n))
+        cp, c = out_buffer((m, n), np.float32, a)
+        self.ctx.check(self.ctx.lib.vsk_matrix_multiply(self.ctx.handle, ap, m, k, bp, n, cp))
+        del ak, bk
+        return c
