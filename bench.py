@@ -531,6 +531,11 @@ def setup(c, a, ctx, dev):
                                f"timing), {reps} pass(es) ({el:.1f} s)"},
                     id_agreement(ids.cpu().numpy()[:m], oi))
 
+        # the quantized index keeps its codes only (vsk_ivf_drop_rows): the
+        # searches read nothing else
+        _, with_rows = idx.storage()
+        idx.dropRows()
+        _, codes_only = idx.storage()
         sq8 = c == "c3sq8"
         spec = {
             "metric": ("QPS @k=10, IVF-SQ8 (per-dim int8) 1M x 128, nlist 4096, nprobe 32" if sq8
@@ -548,6 +553,7 @@ def setup(c, a, ctx, dev):
             "pairs_per_step": probed_pairs(idx, q, nprobe),
             "kernels": [("ivf_sq8_list_scan", "k_list_scan_sq8<16>", "valu_dot4")] if sq8
                        else [("ivf_pq_list_scan", "k_list_scan_pq_q (one workgroup per query)", "lds_pq")],
+            "device_bytes": {"index_codes_only": codes_only, "index_with_fp32_rows": with_rows},
             "keep": (idx, x, q, ids, sq if sq8 else pq),
         }
         return spec, step, cpu_leg, None

@@ -335,7 +335,8 @@ vsk_status vsk_ivf_search_pq(vsk_ctx *ctx, const vsk_ivf *ivf, const vsk_pq *pq,
  * This file holds the whole index, little-endian:
  *   "VSKIVF02"; int32 nlist, d; int64 total, next_id;
  *   int32 code_kind, code_stride, pq_M, pq_ksub, sq8_per_dim, pq_dsub
- *   (code_kind 0 = none, 1 = SQ8, 2 = PQ); int64 meta_bytes;
+ *   (code_kind 0 = none, 1 = SQ8, 2 = PQ; 17 / 18 = SQ8 / PQ codes only,
+ *   without the rows section); int64 meta_bytes;
  *   float centroids[nlist][d]; int64 list_off[nlist + 1]; int64 ids[total];
  *   float rows[total][d] (list order); uint8 codes[total][code_stride];
  *   float quantizer[] (SQ8: scale then offset, d each when per-dimension,
@@ -364,6 +365,23 @@ vsk_status vsk_ivf_centroids(vsk_ctx *ctx, const vsk_ivf *ivf, float *out);
  * (VSK_ERR_DIMENSION_MISMATCH). */
 vsk_status vsk_ivf_sq8_params(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *per_dim,
                               float *scale, float *offset);
+/* A quantized index that keeps only its codes: IVFConfiguration's
+ * quantization (Config/Indexes/IVFConfiguration.swift:13,18-21) is there to
+ * shrink the index, which the reference declares but never builds.  After
+ * vsk_ivf_encode_sq8 / _pq, the fp32 rows (total x d x 4 bytes) and their
+ * screen plane are freed; ids, lists, codes and the quantizer stay.  Then
+ * vsk_ivf_search_sq8 / _pq answer exactly as before, vsk_ivf_add encodes the
+ * new rows with the stored quantizer (their codes are what vsk_sq8_encode /
+ * vsk_pq_encode give), vsk_ivf_remove and vsk_ivf_save / load keep codes
+ * only, and the calls that read rows (vsk_ivf_search, _filtered,
+ * vsk_ivf_encode_*) return VSK_ERR_UNSUPPORTED.  VSK_ERR_NOT_TRAINED
+ * without current codes. */
+vsk_status vsk_ivf_drop_rows(vsk_ctx *ctx, vsk_ivf *ivf);
+/* *codes_only (may be NULL): 1 after vsk_ivf_drop_rows; *device_bytes (may
+ * be NULL): the device memory the index holds (centroids and their planes,
+ * rows, ids, list offsets, codes, the list screen's plane). */
+vsk_status vsk_ivf_storage(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *codes_only,
+                           int64_t *device_bytes);
 /* nlist, d, total rows and code kind (0 none, 1 SQ8, 2 PQ) of an index */
 vsk_status vsk_ivf_info(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *nlist, int32_t *d,
                         int64_t *total, int32_t *code_kind);

@@ -232,3 +232,76 @@ def test_ivf_index_file_damage(ctx, tmp_path):
         assert e.value.status == -10, name
     with pytest.raises(VSKError):
         IVFIndex.load(ctx, str(tmp_path / "missing.vsk"))
+
+
+@pytest.mark.parametrize("kind", ["sq8", "pq"])
+def test_ivf_codes_only(ctx, tmp_path, kind):
+    """vsk_ivf_drop_rows: the index keeps its codes and frees its fp32 rows.
+    Searches answer exactly as before (and as the oracle); the index's
+    device memory shrinks by the rows; inserts after it are encoded with the
+    stored quantizer and rank as the oracle over all rows; removes keep the
+    remaining codes; the codes-only file has no rows section and loads back
+    to the same answers; the calls that need rows raise."""
+    nlist, n, d, nq, nprobe, k = 32, 12_000, 64, 60, 6, 20
+    x, q, c = _mixture(77 if kind == "sq8" else 78, nlist, n, d, nq)
+    idx = _index(ctx, c, x[:10_000], nprobe)
+    if kind == "sq8":
+        sq = ScalarQuantizer(ctx, per_dim=True)
+        sq.train(x)
+        idx.encodeSQ8(sq)
+        run = lambda ix: ix.searchSQ8(q, k)
+        codes = O.sq8_encode(x, sq.scale, sq.offset)
+        qc = O.sq8_encode(q, sq.scale, sq.offset)
+        want = lambda keep: O.ivf_sq8_search(q, qc, codes[keep], keep, O.ivf_assign(x[keep], c),
+                                             c, nprobe, k)
+    else:
+        rng = np.random.default_rng(3)
+        cb = x[rng.choice(n, 256, replace=False)].reshape(256, 16, 4).transpose(1, 0, 2).copy()
+        pq = ProductQuantizer(ctx, cb)
+        idx.encodePQ(pq)
+        run = lambda ix: ix.searchPQ(q, k)
+        codes = O.pq_encode(x, cb)
+        want = lambda keep: O.ivf_pq_search(q, cb, codes[keep], keep, O.ivf_assign(x[keep], c),
+                                            c, nprobe, k)
+    s0, i0 = run(idx)
+    co, before = idx.storage()
+    assert not co
+    idx.dropRows()
+    co, after = idx.storage()
+    assert co and idx.codesOnly
+    assert before - after >= 10_000 * d * 4  # the rows (and any plane) are gone
+    s1, i1 = run(idx)
+    np.testing.assert_array_equal(s1, s0)
+    np.testing.assert_array_equal(i1, i0)
+    with pytest.raises(VSKError):
+        idx.search(q, k)
+    with pytest.raises(VSKError):
+        if kind == "sq8":
+            idx.encodeSQ8(sq)
+        else:
+            idx.encodePQ(pq)
+    # inserts are encoded with the stored quantizer
+    idx.insert(x[10_000:])
+    s2, i2 = run(idx)
+    es, ei = want(np.arange(n))
+    np.testing.assert_array_equal(s2, es)
+    np.testing.assert_array_equal(i2, ei)
+    # removes keep the other rows' codes
+    gone = np.arange(0, n, 3)
+    assert idx.remove(gone) == gone.size
+    keep = np.setdiff1d(np.arange(n), gone)
+    s3, i3 = run(idx)
+    es, ei = want(keep)
+    np.testing.assert_array_equal(s3, es)
+    np.testing.assert_array_equal(i3, ei)
+    # the file has no rows section and answers the same after loading
+    path = str(tmp_path / f"codes_only_{kind}.ivf")
+    idx.save(path)
+    import os
+
+    assert os.path.getsize(path) < keep.size * d * 4  # smaller than the rows alone
+    back = IVFIndex.load(ctx, path, pq=None if kind == "sq8" else pq)
+    assert back.codesOnly
+    s4, i4 = run(back)
+    np.testing.assert_array_equal(s4, s3)
+    np.testing.assert_array_equal(i4, i3)

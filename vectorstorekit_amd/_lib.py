@@ -115,6 +115,8 @@ SIGNATURES = {
                                            P]),
     "vsk_distances": (c_int32, [P, P, P, c_int64, c_int32, P]),
     "vsk_matrix_multiply": (c_int32, [P, P, c_int64, c_int32, P, c_int64, P]),
+    "vsk_ivf_drop_rows": (c_int32, [P, P]),
+    "vsk_ivf_storage": (c_int32, [P, P, P, P]),
     "vsk_ivf_create": (c_int32, [P, P, c_int32, c_int32, PP]),
     "vsk_ivf_free": (c_int32, [P, P]),
     "vsk_ivf_add": (c_int32, [P, P, P, P, c_int64]),

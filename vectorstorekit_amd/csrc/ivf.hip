@@ -56,6 +56,9 @@ struct vsk_ivf {
   // each when cper_dim, else 1), or the PQ codebooks (cM x cksub x cdsub)
   std::vector<float> cparams;
   int32_t cper_dim = 0, cdsub = 0;
+  // codes only (vsk_ivf_drop_rows): the fp32 rows are gone, the codes stay
+  // current (inserts are encoded with the stored quantizer)
+  bool codes_only = false;
   // caller bytes stored with the index file (e.g. the index configuration)
   std::vector<uint8_t> meta;
   // the bf16 screen of the list scan: the stored rows as a bf16 plane of
@@ -505,13 +508,31 @@ __global__ void k_gather_stored(const float *src, const int64_t *src_ids, const 
   const int lane = threadIdx.x & 63;
   for (int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6); t < n; t += (int64_t)gridDim.x * 4) {
     const int64_t s = idx[t];
-    for (int j = lane; j < ld; j += 64) dst[t * ld + j] = src[s * ld + j];
+    if (src)  // (a codes-only index has no rows)
+      for (int j = lane; j < ld; j += 64) dst[t * ld + j] = src[s * ld + j];
     if (codes) {
       const uint32_t *cs = reinterpret_cast<const uint32_t *>(codes + s * cstride);
       uint32_t *cd = reinterpret_cast<uint32_t *>(dst_codes + t * cstride);
       for (int j = lane; j < cstride / 4; j += 64) cd[j] = cs[j];
     }
     if (lane == 0) dst_ids[t] = src_ids[s];
+  }
+}
+
+// code rows to their list positions (a codes-only index's insert): row r
+// of src (w bytes at src_stride; null: left as is) goes to dest[r] of dst
+// (cstride bytes a row, zero padded beforehand), its id with it (src_ids
+// null: id_base + r).  One wave per row, byte copies (w is a few hundred
+// bytes at most).
+__global__ void k_scatter_codes(const uint8_t *src, int32_t src_stride, int32_t w,
+                                const int64_t *src_ids, int64_t id_base, const int64_t *dest,
+                                int64_t n, int32_t cstride, uint8_t *dst, int64_t *dst_ids) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += (int64_t)gridDim.x * 4) {
+    const int64_t t = dest[r];
+    if (src)
+      for (int j = lane; j < w; j += 64) dst[t * cstride + j] = src[r * src_stride + j];
+    if (lane == 0) dst_ids[t] = src_ids ? src_ids[r] : id_base + r;
   }
 }
 
@@ -1069,6 +1090,33 @@ static void require_ivf(const vsk_ivf *ivf) {
   VSK_REQUIRE(ivf, VSK_ERR_INVALID_ARGUMENT, "ivf is null");
 }
 
+// the calls that read the fp32 rows
+static void require_rows(const vsk_ivf *ivf) {
+  VSK_REQUIRE(!ivf->codes_only, VSK_ERR_UNSUPPORTED,
+              "the index holds codes only (vsk_ivf_drop_rows): search it with "
+              "vsk_ivf_search_sq8 / vsk_ivf_search_pq");
+}
+
+// codes of n rows x (n x d, dense, host or device) with the index's stored
+// quantizer, n x w bytes dense into out (w = d for SQ8, M for PQ)
+static void encode_with_stored(vsk_ctx *ctx, const vsk_ivf *ivf, const float *x, int64_t n,
+                               uint8_t *out) {
+  vsk_status st = VSK_OK;
+  if (ivf->ckind == 1) {
+    const size_t ns = ivf->cper_dim ? (size_t)ivf->d : 1;
+    st = vsk_sq8_encode(ctx, x, n, ivf->d, ivf->cper_dim, ivf->cparams.data(),
+                        ivf->cparams.data() + ns, reinterpret_cast<int8_t *>(out));
+  } else {
+    vsk_pq *pq = nullptr;
+    st = vsk_pq_create(ctx, ivf->cparams.data(), ivf->cM, ivf->cksub, ivf->cdsub, &pq);
+    if (st == VSK_OK) {
+      st = vsk_pq_encode(ctx, pq, x, n, out);
+      vsk_pq_free(ctx, pq);
+    }
+  }
+  if (st != VSK_OK) fail(st, "encoding the inserted rows with the index's quantizer failed");
+}
+
 }  // namespace vsk
 
 using namespace vsk;
@@ -1197,12 +1245,51 @@ vsk_status vsk_ivf_add(vsk_ctx *ctx, vsk_ivf *ivf, const float *x,
     cursor[l] = noff[l] + (ivf->off[l + 1] - ivf->off[l]);
   for (int64_t i = 0; i < n; ++i) dest_new[i] = cursor[h_assign[i]]++;
 
+  int64_t *ddest = static_cast<int64_t *>(
+      ctx->scratch_ptr("ivf.dest", sizeof(int64_t) * std::max(ivf->total, n)));
+  if (ivf->codes_only) {
+    // the new rows' codes with the index's own quantizer, then old and new
+    // codes (and ids) to their places in the new list order
+    const int32_t w = ivf->ckind == 1 ? ivf->d : ivf->cM;
+    uint8_t *fresh = static_cast<uint8_t *>(ctx->scratch_ptr("ivf.newcodes", (size_t)n * w));
+    encode_with_stored(ctx, ivf, x, n, fresh);
+    DevBuf codes2, ids2;
+    codes2.reserve((size_t)total * ivf->cstride + 16);
+    fill_i32(ctx, codes2.as<int32_t>(), ((int64_t)total * ivf->cstride + 16) / 4, 0);
+    ids2.reserve(sizeof(int64_t) * total);
+    if (ivf->total > 0) {
+      VSK_HIP(hipMemcpyAsync(ddest, dest_old.data(), 8 * ivf->total, hipMemcpyHostToDevice,
+                             ctx->stream));
+      k_scatter_codes<<<grid1(ivf->total, 4), 256, 0, ctx->stream>>>(
+          ivf->codes.as<uint8_t>(), ivf->cstride, ivf->cstride, ivf->ids.as<int64_t>(), 0,
+          ddest, ivf->total, ivf->cstride, codes2.as<uint8_t>(), ids2.as<int64_t>());
+      check_launch("ivf_scatter_old_codes");
+      stream_sync(ctx);
+    }
+    VSK_HIP(hipMemcpyAsync(ddest, dest_new.data(), 8 * n, hipMemcpyHostToDevice, ctx->stream));
+    k_scatter_codes<<<grid1(n, 4), 256, 0, ctx->stream>>>(
+        fresh, w, w, did, ivf->next_id, ddest, n, ivf->cstride, codes2.as<uint8_t>(),
+        ids2.as<int64_t>());
+    check_launch("ivf_scatter_new_codes");
+    VSK_HIP(hipMemcpyAsync(ivf->list_off.p, noff.data(), sizeof(int64_t) * (nlist + 1),
+                           hipMemcpyHostToDevice, ctx->stream));
+    stream_sync(ctx);
+    std::swap(ivf->codes.p, codes2.p);
+    std::swap(ivf->codes.bytes, codes2.bytes);
+    std::swap(ivf->ids.p, ids2.p);
+    std::swap(ivf->ids.bytes, ids2.bytes);
+    ++ivf->version;
+    ivf->off = noff;
+    ivf->total = total;
+    ivf->ctotal = total;
+    ivf->next_id += n;
+    cs.finish();
+    return VSK_OK;
+  }
   auto rows2 = std::make_unique<DevBuf>();
   auto ids2 = std::make_unique<DevBuf>();
   rows2->reserve(sizeof(float) * (size_t)total * ld);
   ids2->reserve(sizeof(int64_t) * total);
-  int64_t *ddest = static_cast<int64_t *>(
-      ctx->scratch_ptr("ivf.dest", sizeof(int64_t) * std::max(ivf->total, n)));
   if (ivf->total > 0) {
     VSK_HIP(hipMemcpyAsync(ddest, dest_old.data(), 8 * ivf->total,
                            hipMemcpyHostToDevice, ctx->stream));
@@ -1627,6 +1714,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
                                  int64_t allow_bits = 0) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
+  if (kind == 0) require_rows(ivf);
   if (kind == 0)
     VSK_REQUIRE(metric == VSK_METRIC_L2 || metric == VSK_METRIC_L2SQ,
                 VSK_ERR_UNSUPPORTED,
@@ -1957,7 +2045,7 @@ vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_
     if (gone > 0) {
       const bool codes = ivf->ckind != 0 && ivf->ctotal == ivf->total;
       DevBuf rows, nids, ncodes, didx, doff;
-      rows.reserve(sizeof(float) * (size_t)m * ivf->ld);
+      if (!ivf->codes_only) rows.reserve(sizeof(float) * (size_t)m * ivf->ld);
       nids.reserve(sizeof(int64_t) * (size_t)m);
       if (codes) {
         ncodes.reserve((size_t)m * ivf->cstride + 16);
@@ -1971,7 +2059,7 @@ vsk_status vsk_ivf_remove(vsk_ctx *ctx, vsk_ivf *ivf, const int64_t *ids, int64_
                              hipMemcpyHostToDevice, ctx->stream));
       if (m > 0) {
         k_gather_stored<<<grid1(m, 4), 256, 0, ctx->stream>>>(
-            ivf->rows.as<float>(), ivf->ids.as<int64_t>(),
+            ivf->codes_only ? nullptr : ivf->rows.as<float>(), ivf->ids.as<int64_t>(),
             codes ? ivf->codes.as<uint8_t>() : nullptr, ivf->cstride, didx.as<int64_t>(), m,
             ivf->ld, rows.as<float>(), nids.as<int64_t>(), ncodes.as<uint8_t>());
         check_launch("ivf_remove_gather");
@@ -2013,10 +2101,41 @@ vsk_status vsk_ivf_list_ids(vsk_ctx *ctx, const vsk_ivf *ivf, int64_t *ids, int6
   VSK_API_END(ctx);
 }
 
+vsk_status vsk_ivf_drop_rows(vsk_ctx *ctx, vsk_ivf *ivf) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  VSK_REQUIRE(ivf->ckind != 0 && ivf->ctotal == ivf->total, VSK_ERR_NOT_TRAINED,
+              "the index holds no current codes (vsk_ivf_encode_sq8 / vsk_ivf_encode_pq)");
+  if (!ivf->codes_only) {
+    stream_sync(ctx);  // (nothing queued may still read the rows)
+    ivf->rows.release();
+    ivf->xplane.release();
+    ivf->xsq.release();
+    ivf->xversion = -1;
+    ivf->codes_only = true;
+  }
+  VSK_API_END(ctx);
+}
+
+vsk_status vsk_ivf_storage(vsk_ctx *ctx, const vsk_ivf *ivf, int32_t *codes_only,
+                           int64_t *device_bytes) {
+  VSK_API_BEGIN(ctx);
+  require_ivf(ivf);
+  if (codes_only) *codes_only = ivf->codes_only ? 1 : 0;
+  if (device_bytes)
+    *device_bytes = (int64_t)(ivf->centroids.x.bytes + ivf->centroids.sqnorm.bytes +
+                              ivf->centroids.norm.bytes + ivf->centroids.split.bytes +
+                              ivf->centroids.split_lo.bytes + ivf->centroids.seqnorm.bytes +
+                              ivf->rows.bytes + ivf->ids.bytes + ivf->list_off.bytes +
+                              ivf->codes.bytes + ivf->xplane.bytes + ivf->xsq.bytes);
+  VSK_API_END(ctx);
+}
+
 vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,
                               const float *scale, const float *offset) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
+  require_rows(ivf);
   VSK_REQUIRE(ivf->total > 0, VSK_ERR_EMPTY_INPUT, "the index holds no rows");
   VSK_REQUIRE(scale && offset, VSK_ERR_INVALID_ARGUMENT, "null buffer");
   DevBuf dense, codes;
@@ -2040,6 +2159,7 @@ vsk_status vsk_ivf_encode_sq8(vsk_ctx *ctx, vsk_ivf *ivf, int32_t per_dim,
 vsk_status vsk_ivf_encode_pq(vsk_ctx *ctx, vsk_ivf *ivf, const vsk_pq *pq) {
   VSK_API_BEGIN(ctx);
   require_ivf(ivf);
+  require_rows(ivf);
   VSK_REQUIRE(ivf->total > 0, VSK_ERR_EMPTY_INPUT, "the index holds no rows");
   VSK_REQUIRE(pq, VSK_ERR_INVALID_ARGUMENT, "pq is null");
   int32_t M = 0, ksub = 0;
@@ -2196,9 +2316,10 @@ vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path) {
   VSK_REQUIRE(f, VSK_ERR_IO, std::string("cannot open for writing: ") + path);
   Fnv1a h;
   const bool coded = ivf->ckind != 0 && ivf->ctotal == ivf->total;
+  // a codes-only index (no rows section) marks its code kind with 16
   const int32_t hdr32[8] = {ivf->nlist,
                             ivf->d,
-                            coded ? ivf->ckind : 0,
+                            coded ? ivf->ckind | (ivf->codes_only ? 16 : 0) : 0,
                             coded ? ivf->cstride : 0,
                             coded ? ivf->cM : 0,
                             coded ? ivf->cksub : 0,
@@ -2215,7 +2336,7 @@ vsk_status vsk_ivf_save(vsk_ctx *ctx, const vsk_ivf *ivf, const char *path) {
   put_rows(ctx, f.get(), h, ivf->centroids.x.p, ivf->nlist, ldb, db);
   put(f.get(), h, ivf->off.data(), sizeof(int64_t) * (ivf->nlist + 1));
   put_rows(ctx, f.get(), h, ivf->ids.p, ivf->total, 8, 8);
-  put_rows(ctx, f.get(), h, ivf->rows.p, ivf->total, ldb, db);
+  if (!ivf->codes_only) put_rows(ctx, f.get(), h, ivf->rows.p, ivf->total, ldb, db);
   if (coded) {
     put_rows(ctx, f.get(), h, ivf->codes.p, ivf->total, ivf->cstride, ivf->cstride);
     put(f.get(), h, ivf->cparams.data(), sizeof(float) * ivf->cparams.size());
@@ -2253,6 +2374,9 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
               VSK_ERR_IO, "index file: bad header");
   int64_t nparams = 0;  // floats of quantizer parameters
   bool kind_ok = false;
+  // code kind 17 / 18: SQ8 / PQ codes without the rows (vsk_ivf_drop_rows)
+  const bool codes_only = ck[0] == 17 || ck[0] == 18;
+  if (codes_only) ck[0] -= 16;
   if (ck[0] == 0) kind_ok = ck[1] == 0 && ck[2] == 0 && ck[3] == 0 && ck[4] == 0 && ck[5] == 0;
   if (ck[0] == 1) {
     kind_ok = ck[1] == (d + 15) / 16 * 16 && ck[2] == 0 && ck[3] == 0 &&
@@ -2268,7 +2392,8 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   // the file's length must be exactly what the header describes (bounded
   // sizes: no product below can overflow int64)
   const int64_t body = kHeaderBytes + 4ll * nlist * d + 8ll * (nlist + 1) + 8 * total +
-                       4 * total * d + (int64_t)ck[1] * total + 4 * nparams + meta_n + 8;
+                       (codes_only ? 0 : 4 * total * d) + (int64_t)ck[1] * total +
+                       4 * nparams + meta_n + 8;
   VSK_REQUIRE(fseek(f.get(), 0, SEEK_END) == 0 && ftell(f.get()) == body &&
                   fseek(f.get(), kHeaderBytes, SEEK_SET) == 0,
               VSK_ERR_IO, "index file: length does not match its header");
@@ -2284,11 +2409,13 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   if (st != VSK_OK) return st;
   std::unique_ptr<vsk_ivf, IvfDeleter> ivf(raw, IvfDeleter{ctx});
   const int32_t ld = ivf->ld;
-  ivf->rows.reserve(sizeof(float) * (size_t)std::max<int64_t>(total, 1) * ld);
   ivf->ids.reserve(sizeof(int64_t) * (size_t)std::max<int64_t>(total, 1));
-  fill_i32(ctx, ivf->rows.as<int32_t>(), std::max<int64_t>(total, 1) * ld, 0);
   get_rows(ctx, f.get(), h, ivf->ids.p, total, 8, 8);
-  get_rows(ctx, f.get(), h, ivf->rows.p, total, sizeof(float) * ld, sizeof(float) * d);
+  if (!codes_only) {
+    ivf->rows.reserve(sizeof(float) * (size_t)std::max<int64_t>(total, 1) * ld);
+    fill_i32(ctx, ivf->rows.as<int32_t>(), std::max<int64_t>(total, 1) * ld, 0);
+    get_rows(ctx, f.get(), h, ivf->rows.p, total, sizeof(float) * ld, sizeof(float) * d);
+  }
   ++ivf->version;
   if (ck[0] != 0) {
     ivf->codes.reserve((size_t)total * ck[1] + 16);
@@ -2327,6 +2454,7 @@ vsk_status vsk_ivf_load(vsk_ctx *ctx, const char *path, vsk_ivf **out) {
   ivf->cper_dim = ck[4];
   ivf->cdsub = ck[5];
   ivf->ctotal = ck[0] ? total : -1;
+  ivf->codes_only = codes_only;
   *out = ivf.release();
   VSK_API_END(ctx);
 }

@@ -209,6 +209,26 @@ class IVFIndex:
         self.ctx.check(self.ctx.lib.vsk_ivf_encode_pq(self.ctx.handle, self.handle, pq.handle))
         self._sq8, self._pq = None, pq
 
+    def dropRows(self):
+        """Keep only the codes (``vsk_ivf_drop_rows``): the fp32 rows and
+        their screen plane are freed.  ``searchSQ8`` / ``searchPQ`` answer as
+        before; ``insert`` encodes new rows with the quantizer the codes were
+        made with; ``search`` and ``encodeSQ8`` / ``encodePQ`` raise."""
+        self._need()
+        self.ctx.check(self.ctx.lib.vsk_ivf_drop_rows(self.ctx.handle, self.handle))
+
+    @property
+    def codesOnly(self) -> bool:
+        return self.storage()[0]
+
+    def storage(self):
+        """(codes only, device bytes the index holds) (``vsk_ivf_storage``)."""
+        self._need()
+        co, nb = ctypes.c_int32(0), ctypes.c_int64(0)
+        self.ctx.check(self.ctx.lib.vsk_ivf_storage(self.ctx.handle, self.handle,
+                                                    ctypes.byref(co), ctypes.byref(nb)))
+        return bool(co.value), int(nb.value)
+
     def _queries(self, queries):
         q = queries
         if not hasattr(q, "shape") or len(q.shape) == 1:
