@@ -132,7 +132,11 @@ __device__ inline double screen_eps_of(double qh, double qr, double xh, double x
   else if (metric == VSK_METRIC_COSINE_NORMALIZED)
     eps = e_dot + e_ref + 2.02 * u * (1.0 + qn * xn + e_dot);
   else
-    eps = 2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05;
+    // (the last term: the filter pass accumulates dot - |x|^2/2 from
+    // -|x|^2/2, so its partial sums carry |x|^2/2 more: 2 np u |x|^2/2 more
+    // on the dot, twice that on the distance, plus a rounding of each)
+    eps = 2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05 +
+          (2.0 * np + 4.0) * u * xn * xn * 1.01;
   return eps * 1.0001;
 }
 

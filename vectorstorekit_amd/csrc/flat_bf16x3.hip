@@ -468,6 +468,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   // [4][XS_N]: |x|^2 of row tile t in slot t & 3
   float *s_xa = MODE == MODE_TOP2 ? s_t2 + 4 * XS_Q : reinterpret_cast<float *>(lds + XS_LDS);
   constexpr bool XA = xs_norms_in_lds<MODE, METRIC>();
+  constexpr bool XS_SHIFT =
+      MODE == MODE_FILTER && (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2);
   if constexpr (MODE == MODE_TOP2) {
     for (int i = tid; i < 4 * XS_Q; i += 512) {
       s_t1[i] = VSK_KEY_NONE;
@@ -647,11 +649,21 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     // the tile's first operands are read here rather than before the
     // previous epilogue, which then has the registers to itself
     read_ops(lds + (g & 1) * XS_STAGE, 0, 0);
+    // the accumulators start at zero, or in filter mode on L2 and L2^2 at
+    // -|x|^2/2 of the lane's rows (the tile's norms reached LDS with its
+    // first stage): acc is then dot - |x|^2/2, the quantity the filter's
+    // bound is on
     f4 acc[4][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      f4 init = f4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (XS_SHIFT)
+        init = *reinterpret_cast<const f4 *>(s_xa + (tcur & 3) * XS_N + wr * 64 + 4 * cl +
+                                             16 * i) *
+               -0.5f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 8; ++j) acc[i][j] = init;
+    }
 #define XS_MMA(N)                                                               \
   do {                                                                          \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                             \
@@ -682,7 +694,11 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       // stage g+1 (at a tile's last stage the next tile's first one, read
       // again at its start: unconditional, so the reads can interleave)
       read_ops(lds + ((g + 1) & 1) * XS_STAGE, 0, 0);
-      copy_next();  // stage g+2 into cur
+      // stage g+2 into cur; in filter mode on L2 the next tile's second
+      // stage waits until after the epilogue: with a copy in flight the
+      // epilogue's first LDS atomic waits for it (measured at config 5:
+      // 6 % faster launches; slower for the other metrics)
+      if (!XS_SHIFT || st + 1 < nst) copy_next();
       XS_MMA(1);
       __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // the copies first
 #pragma unroll
@@ -785,7 +801,9 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         // may pass (NaN included); rows past the slice masked off
         uint32_t m = 0;
         if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED ||
-                      METRIC == VSK_METRIC_DOT) {
+                      METRIC == VSK_METRIC_DOT || XS_SHIFT) {
+          // (L2: acc already holds dot - |x|^2/2, the quantity the bound
+          // below is on)
           const float tdot = l_tdot[16 * j];
           // the block's largest dot first: when it is below the bound in
           // every lane, no score of the block can pass (one compare and a
@@ -884,12 +902,19 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             const float w0 = b2 ? u1 : u0, w1 = b2 ? u3 : u2;
             const float dot = (b & 8) ? w1 : w0;
             const int64_t row = rbase + 16 * (b >> 2) + (b & 3);
-            float xa = 0.f;
-            if constexpr (XA)
-              xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * (b >> 2) + (b & 3)];
-            else if (a.xaux)
-              xa = a.xaux[row];
-            const uint64_t key = vsk_key(dist_from_dot<METRIC>(dot, qa, xa), (uint32_t)row);
+            float dist;
+            if constexpr (XS_SHIFT) {
+              // |q|^2 - 2 (dot - |x|^2/2), one rounding
+              dist = fmaxf(__builtin_fmaf(-2.0f, dot, qa), 0.0f);
+            } else {
+              float xa = 0.f;
+              if constexpr (XA)
+                xa = s_xa[(tcur & 3) * XS_N + wr * 64 + 4 * cl + 16 * (b >> 2) + (b & 3)];
+              else if (a.xaux)
+                xa = a.xaux[row];
+              dist = dist_from_dot<METRIC>(dot, qa, xa);
+            }
+            const uint64_t key = vsk_key(dist, (uint32_t)row);
             if (key <= th) {
               const int pos = atomicAdd(&l_cnt[16 * j], 1);
               if (pos < l_lim[16 * j]) a.cand[l_pb[16 * j] + pos] = key;
@@ -898,6 +923,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         }
       }
     }
+    if constexpr (XS_SHIFT) copy_next();  // (deferred from the tile's last stage)
   }
   // the copies issued past the slice end land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt(kWaitAll);

@@ -1,6 +1,7 @@
-// flat_screen.hip -- exact flat top-k for L2^2, L2, normalised cosine and
-// dot: a one-pass bf16 MFMA screen, a proven bound on its error, and an fp32
-// rescore of the survivors in the CPU reference's own summation order.
+// flat_screen.hip -- exact flat top-k for L2^2, L2, cosine (the reference's
+// epsilon form), normalised cosine and dot: a one-pass bf16 MFMA screen, a
+// proven bound on its error, and an fp32 rescore of the survivors in the CPU
+// reference's own summation order.
 //
 // Bound.  With qh = bf16(q), xh = bf16(x) and the exact residuals
 // dq = q - qh, dx = x - xh, Cauchy-Schwarz gives
@@ -9,7 +10,10 @@
 // summation of d of them, in any order and with round-to-nearest or
 // truncation, errs by at most 2(d-1)u sum|qh_i xh_i| <= 2(d-1)u |qh||xh|,
 // u = 2^-24.  Taking the maxima of |xh| and |dx| over the rows bounds every
-// pair of one query: eps_dot(q).  The screen's distance a(x) of each metric
+// pair of one query: eps_dot(q).  (The filter pass on L2 and L2^2 starts
+// its sums at -|x|^2/2 instead of 0: that adds 2 d u |x|^2/2 to the sum's
+// error, which screen_eps_of adds for those metrics.)  The screen's distance
+// a(x) of each metric
 // is then within eps(q) of the distance d(x) the rescore computes; eps adds
 // the error of the reference's sequential fp32 sum and of the metric's last
 // operations (norms and the final subtraction for L2^2, 1 - s for cosine).
@@ -20,10 +24,11 @@
 // while the k rows with a <= A_k have d <= A_k + eps: y is strictly beaten
 // by k rows.  For L2 the ranking distance is sqrt(d), and the test asks for
 // a relative gap of 2^-20 so that rounding of the square root cannot tie
-// them.  A query failing the test (about 1 in 100 on config 2, where some
-// 2k rows fall within the margin of 2^-8 of the norms) is screened again
-// keeping 1024 candidates, and one failing that too is redone by the exact
-// VALU scan, which evaluates the reference's formula for every row.
+// them.  A query failing the test (rows closer to each other than the
+// bound: none of config 2's queries, but planted near-duplicates do it) is
+// screened again keeping 1024 candidates, and one failing that too is redone
+// by the exact VALU scan, which evaluates the reference's formula for every
+// row.  The epsilon cosine's bound is relative to the norms (screen_eps_of).
 //
 // Kept rows above that limit are beaten the same way, so only the rows of
 // a within 2 eps of A_k are rescored.

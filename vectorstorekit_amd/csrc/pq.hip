@@ -696,11 +696,7 @@ __global__ void k_pq_screen_thresh(const uint64_t *thresh, int64_t nq, const flo
     out[q] = VSK_KEY_NONE;
     return;
   }
-  const double u = 0x1p-24, dd = (double)d;
-  const double qh = qnh[q], qr = qnr[q], qn = qh + qr, xn = xh + xr;
-  const double e_dot =
-      qh * xr + qr * xh + qr * xr + 2.0 * (dd - 1.0) * u * qh * xh + dd * 0x1p-126;
-  const double eps = (2.0 * e_dot + (2.0 * dd + 8.0) * u * (qn + xn) * (qn + xn) * 1.05) * 1.0001;
+  const double eps = screen_eps_of(qnh[q], qnr[q], xh, xr, d, VSK_METRIC_L2SQ);
   const double lim = (double)vsk_ord2f((uint32_t)(t >> 32)) + eps;
   out[q] = vsk_key(f_up(lim), 0xFFFFFFFFu);
 }
