@@ -209,6 +209,10 @@ vsk_status vsk_db_read_f32(vsk_ctx *ctx, const vsk_db *db, int64_t row0,
  * fused on the device and ids returned (the reference returns distances
  * only, after a CPU sort of the full matrix, :457-477).  Also the exact
  * path of VectorIndex.search (Core/Protocols.swift:116-121).
+ * Every metric returns the reference CPU path's fp32 distances (sums in
+ * dimension order, its own formulas) and its (distance, row) order bit for
+ * bit, for every k <= VSK_MAX_K; only VSK_KERNEL_BF16X3 / _FP32
+ * (vsk_configure) trade that for a tolerance-path kernel.
  * q: nq x d fp32; out_dist: nq x k fp32; out_ids: nq x k int64. */
 vsk_status vsk_search_flat(vsk_ctx *ctx, const vsk_db *db, const float *q,
                            int64_t nq, int32_t k, int32_t metric,
