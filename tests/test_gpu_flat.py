@@ -574,3 +574,39 @@ def test_screen_segment_overflow_rescan(ctx):
     assert waits > 2, "no chunk overflowed"
     db.free()
     sctx.close()
+
+
+def test_epsilon_cosine_rows_outside_the_bound(sctx):
+    """Rows the epsilon-cosine screen's relative bound cannot cover: a row
+    whose squares underflow (norm 0 in fp32, components not zero) and a row
+    of norm above 2^60.  The database then takes the exact scan, bit for bit
+    the oracle's; a database without them takes the screen again.  (Rows
+    with non-finite components are refused by the same test, but their NaN
+    distances have no order the oracle's heap keeps, so no parity is
+    claimed for them.)"""
+    rng = np.random.default_rng(55)
+    x = rng.standard_normal((6000, 48)).astype(np.float32)
+    q = rng.standard_normal((9, 48)).astype(np.float32)
+    x[10] = 1e-30
+    x[11] = 3e18
+    print("cosine rows outside the bound", flush=True)
+    sctx.profile(True)
+    sctx.profile_reset()
+    gd, gi = VectorDatabase(sctx, x).search(q, 40, METRIC_COSINE)
+    stats = sctx.profile_stats()
+    sctx.profile(False)
+    assert "flat_screen_dense" not in stats and "screen_rescore" not in stats
+    od, oi = O.search_flat(q, x, 40, METRIC_COSINE)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+    # the same rows without the two: the screen runs, still exact
+    y = np.delete(x, [10, 11], axis=0)
+    sctx.profile(True)
+    sctx.profile_reset()
+    gd, gi = VectorDatabase(sctx, y).search(q, 40, METRIC_COSINE)
+    stats = sctx.profile_stats()
+    sctx.profile(False)
+    assert "screen_rescore" in stats
+    od, oi = O.search_flat(q, y, 40, METRIC_COSINE)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
