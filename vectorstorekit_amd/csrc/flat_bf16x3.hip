@@ -369,10 +369,13 @@ void k_flat_bf16x3(FlatArgs a, SplitPtrs s) {
 // chunks, chunk c of row r stored at position c ^ ((r >> 1) & 7): the 16
 // lanes of one ds_read_b128 phase (rows r..r+15, one chunk) and of one
 // staging write (rows r, r+1, all chunks) then touch 16 distinct bank
-// quads.  Two stage buffers (128 KB); the stage after next is loaded into
-// registers while the current one is multiplied.  Filtered candidates go
-// through per-wave LDS lists (24 KB).  Per MFMA this moves half
-// the global bytes and two thirds of the LDS bytes of the 128 x 128 tile.
+// quads.  Two stage buffers (128 KB); the next stage is copied into the
+// other one by buffer loads that write LDS directly while the current one
+// is multiplied.  Filter mode appends each query's surviving keys to its
+// slots of the candidate array; on L2 and L2^2 the blocks of scores that
+// may pass wait in a per-wave LDS queue (17 KB) and are tested in batches.
+// Per MFMA this moves half the global bytes and two thirds of the LDS bytes
+// of the 128 x 128 tile.
 constexpr int XS_N = 256, XS_Q = 256, XS_K = 64, XS_R = 128;
 // query tiles per XCD group: the 32 workgroups resident on an XCD then hold
 // 4 query tiles (1.5 MB of bf16 queries at d = 768) and 8 row slices
@@ -390,6 +393,12 @@ static_assert(XS_LDS_TOP2 <= 160 * 1024, "LDS of one workgroup");
 // filter mode on L2 and L2^2: the row norms of four row tiles in LDS too (a
 // global load in the epilogue would wait for every stage copy in flight)
 constexpr int XS_LDS_XA = XS_LDS + 4 * XS_N * 4;
+// filter mode on L2 and L2^2: after the row norms, a queue per wave of up to
+// XS_QCAP blocks (a lane's 16 scores of one query, 64 bytes) and a position
+// word for each
+constexpr int XS_QCAP = 32;
+constexpr int XS_LDS_QUEUE = XS_LDS_XA + 8 * XS_QCAP * (64 + 4);
+static_assert(XS_LDS_QUEUE <= 160 * 1024, "LDS of one workgroup");
 template <int MODE, int METRIC>
 constexpr bool xs_norms_in_lds() {
   return MODE == MODE_TOP2 ||
@@ -406,6 +415,15 @@ __device__ __forceinline__ void top2_merge(uint64_t &k, float &m2, uint64_t ko, 
   const uint64_t hi = ko < k ? k : ko;
   k = ko < k ? ko : k;
   m2 = fminf(fminf(m2, mo), top2_keydist(hi));
+}
+
+// The lane index, computed where it is used and opaque to the compiler:
+// kept live from a kernel's start under register pressure it is spilled,
+// and its reload waits for every stage copy in flight.
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 __device__ __forceinline__ int swz8(int r, int c) {
@@ -643,6 +661,54 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   copy_next();
   __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this wave's copies of stage 0
   __builtin_amdgcn_s_barrier();
+  // L2 filter: a lane whose block of 16 scores may pass (its largest
+  // score clears the query's bound) puts the block in its wave's queue,
+  // with the block's position (tile, query column, lane).  The queue is
+  // drained, one block a lane, when full and at the end of the slice: the
+  // per-score test and the exact keys then run once for up to XS_QCAP
+  // blocks instead of once per flagged block.  (Rows per split stay below
+  // 2^31, so the tile index fits in 23 bits.)
+  int qn = 0;  // blocks in the queue (wave-uniform)
+  float *q_val = reinterpret_cast<float *>(lds + XS_LDS_XA) + w * XS_QCAP * 16;
+  int32_t *q_pos = reinterpret_cast<int32_t *>(lds + XS_LDS_XA + 8 * XS_QCAP * 64) + w * XS_QCAP;
+  auto drain = [&]() {
+    const int ln = lane_here();
+    if (ln < qn) {
+      const int pw = q_pos[ln];
+      const int jj = (pw >> 6) & 7, sl = pw & 63;
+      const int lq = wq * 128 + 16 * jj + (sl & 15);
+      const f4 *src = reinterpret_cast<const f4 *>(q_val + ln * 16);
+      const f4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+      const bool ok = s_ok[lq] != 0;
+      const float td = s_tdot[lq];
+      const float qa = a.qaux ? s_qa[lq] : 0.f;
+      const uint64_t th = s_th[lq];
+      uint32_t m = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        m |= (v0[r] < td) ? 0u : (1u << r);
+        m |= (v1[r] < td) ? 0u : (1u << (4 + r));
+        m |= (v2[r] < td) ? 0u : (1u << (8 + r));
+        m |= (v3[r] < td) ? 0u : (1u << (12 + r));
+      }
+      if (!ok) m = 0;
+      const int64_t rb = s0 + (int64_t)(pw >> 9) * XS_N + wr * 64 + 4 * (sl >> 4);
+      while (m) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1;
+        const int64_t row = rb + 16 * (b >> 2) + (b & 3);
+        if (row >= s1) continue;  // past the slice
+        // |q|^2 - 2 (dot - |x|^2/2), one rounding
+        const float dist = fmaxf(__builtin_fmaf(-2.0f, q_val[ln * 16 + b], qa), 0.0f);
+        const uint64_t key = vsk_key(dist, (uint32_t)row);
+        if (key <= th) {
+          const int pos = atomicAdd(&s_cnt[lq], 1);
+          if (pos < s_lim[lq]) a.cand[s_pb[lq] + pos] = key;
+        }
+      }
+    }
+    qn = 0;
+  };
   int g = 0;  // stage of the sequence being multiplied
   int tcur = 0;  // index of the tile being multiplied
   for (int64_t t0 = s0; t0 < s1; t0 += XS_N, ++tcur) {
@@ -654,12 +720,13 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     // first stage): acc is then dot - |x|^2/2, the quantity the filter's
     // bound is on
     f4 acc[4][8];
+    const int xl = XS_SHIFT ? lane_here() : lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f4 init = f4{0.f, 0.f, 0.f, 0.f};
       if constexpr (XS_SHIFT)
-        init = *reinterpret_cast<const f4 *>(s_xa + (tcur & 3) * XS_N + wr * 64 + 4 * cl +
-                                             16 * i) *
+        init = *reinterpret_cast<const f4 *>(s_xa + (tcur & 3) * XS_N + wr * 64 +
+                                             4 * (xl >> 4) + 16 * i) *
                -0.5f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = init;
@@ -731,6 +798,13 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     const int64_t *l_pb = s_pb + lq0;
     uint64_t *l_t1 = s_t1 + wr * XS_Q + lq0;
     float *l_t2 = s_t2 + wr * XS_Q + lq0;
+    // L2 filter: the eight query columns' bounds read at once (read one at
+    // a time, each test waits for its read)
+    float tdv[8];
+    if constexpr (MODE == MODE_FILTER && XS_SHIFT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tdv[j] = l_tdot[16 * j];
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t qi = q0 + lq0 + 16 * j;
@@ -799,11 +873,38 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         // exact test only in the (row block, r) steps where a lane passes
         // fast test, one compare per score: bit 4i+r of m for a score that
         // may pass (NaN included); rows past the slice masked off
+        if constexpr (XS_SHIFT) {
+          // acc holds dot - |x|^2/2, the quantity the bound is on; the
+          // block's largest score first (a NaN score is dropped by the max:
+          // it needs a non-finite input, whose bound is not finite, so such
+          // a query fails the screen's check and is redone exactly)
+          const float tdot = tdv[j];
+          float mx = acc[0][j][0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, acc[i][j][r]);
+          uint64_t bal = __builtin_amdgcn_ballot_w64(!(mx < tdot));
+          while (bal) {  // (the common case skips it)
+            if (qn == XS_QCAP) drain();
+            const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            const int ln = lane_here();
+            const bool mine = ((bal >> ln) & 1u) && (int)pos < XS_QCAP - qn;
+            if (mine) {
+              f4 *dst = reinterpret_cast<f4 *>(q_val + (qn + (int)pos) * 16);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) dst[i] = acc[i][j];
+              q_pos[qn + (int)pos] = (tcur << 9) | (j << 6) | ln;
+            }
+            const uint64_t took = __builtin_amdgcn_ballot_w64(mine);
+            qn = __builtin_amdgcn_readfirstlane(qn + __builtin_popcountll(took));
+            bal &= ~took;
+          }
+          continue;
+        }
         uint32_t m = 0;
-        if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED ||
-                      METRIC == VSK_METRIC_DOT || XS_SHIFT) {
-          // (L2: acc already holds dot - |x|^2/2, the quantity the bound
-          // below is on)
+        if constexpr (METRIC == VSK_METRIC_COSINE_NORMALIZED || METRIC == VSK_METRIC_DOT) {
           const float tdot = l_tdot[16 * j];
           // the block's largest dot first: when it is below the bound in
           // every lane, no score of the block can pass (one compare and a
@@ -927,6 +1028,9 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   }
   // the copies issued past the slice end land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt(kWaitAll);
+  if constexpr (MODE == MODE_FILTER && XS_SHIFT) {
+    if (qn) drain();
+  }
   if constexpr (MODE == MODE_TOP2) {
     __syncthreads();
     if (tid < XS_Q && s_ok[tid]) {
@@ -970,7 +1074,10 @@ static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a,
     k_flat_screen<MODE_DENSE, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
   else
     k_flat_screen<MODE_FILTER, METRIC><<<grid, 512,
-                                         xs_norms_in_lds<MODE_FILTER, METRIC>() ? XS_LDS_XA : lds,
+                                         (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2)
+                                             ? XS_LDS_QUEUE
+                                             : (xs_norms_in_lds<MODE_FILTER, METRIC>() ? XS_LDS_XA
+                                                                                        : lds),
                                          ctx->stream>>>(a, s);
 }
 
@@ -990,13 +1097,13 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2SQ>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_QUEUE));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_L2>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
+        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_QUEUE));
     VSK_HIP(hipFuncSetAttribute(
         reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_COSINE_NORMALIZED>),
         hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
