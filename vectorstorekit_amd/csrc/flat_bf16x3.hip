@@ -430,7 +430,11 @@ __device__ __forceinline__ int swz8(int r, int c) {
   return r * XS_R + ((c ^ ((r >> 1) & 7)) << 4);
 }
 
-template <int MODE, int METRIC>
+// QR (planes of at most 128 dims, two stages a tile): the workgroup's
+// queries are copied into LDS once and stay there (64 KB where the second
+// stage buffer's query half was), and each stage copies only its 256 rows,
+// into one of two 32 KB row buffers: half the copies per stage.
+template <int MODE, int METRIC, bool QR = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_flat_screen(FlatArgs a, SplitPtrs s) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -616,23 +620,24 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       }
     }
     const int32_t kofs = dst * XS_K * 2;
-    // waves 0-3 issue the stage's 64 copies, 16 each: their own units and
-    // those of wave w + 4, 128 rows further (the same swizzle); the other
-    // four waves only multiply (fewer waves issuing memory instructions
-    // measured faster)
+    // waves 0-3 issue the stage's 64 copies (QR: 32), 16 (8) each: their
+    // own units and those of wave w + 4, 128 rows further (the same
+    // swizzle); the other four waves only multiply (fewer waves issuing
+    // memory instructions measured faster)
     if (w < 4) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        uint8_t *bx = lds + dbuf * XS_STAGE + 4 * (w + 4 * h) * 1024;
+        uint8_t *bx = lds + dbuf * (QR ? XS_N * XS_R : XS_STAGE) + 4 * (w + 4 * h) * 1024;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int32_t so = kofs + (u >> 1) * 16 * ldx2 + h * 128 * ldx2;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               rx, (__attribute__((address_space(3))) void *)(bx + u * 1024), 16, voff[u & 1], so,
               0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rq, (__attribute__((address_space(3))) void *)(bx + XS_N * XS_R + u * 1024), 16,
-              voff[u & 1], so, 0, 0);
+          if constexpr (!QR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rq, (__attribute__((address_space(3))) void *)(bx + XS_N * XS_R + u * 1024), 16,
+                voff[u & 1], so, 0, 0);
         }
       }
     }
@@ -643,20 +648,49 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       ++dtile;
     }
   };
+  // the rows and the queries of stage g
+  auto rows_of = [&](int gg) -> const uint8_t * {
+    return lds + (gg & 1) * (QR ? XS_N * XS_R : XS_STAGE);
+  };
+  auto queries_of = [&](int gg) -> const uint8_t * {
+    if constexpr (QR)
+      return lds + 2 * XS_N * XS_R + (nst == 2 ? (gg & 1) : 0) * XS_Q * XS_R;
+    else
+      return lds + (gg & 1) * XS_STAGE + XS_N * XS_R;
+  };
   // operands: two sets, this step's and the next one's (read one step ahead)
   bf8 ra[2][4], rb[2][8];
-  auto read_ops = [&](const uint8_t *buf, int kk, int n) {
+  auto read_ops = [&](int gg, int kk, int n) {
+    const uint8_t *bq = queries_of(gg), *bx = rows_of(gg);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       rb[n][j] = __builtin_bit_cast(
           bf8, *reinterpret_cast<const uint4 *>(
-                   buf + XS_N * XS_R + swz8(wq * 128 + j * 16 + (lane & 15), kk * 4 + cl)));
+                   bq + swz8(wq * 128 + j * 16 + (lane & 15), kk * 4 + cl)));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ra[n][i] = __builtin_bit_cast(
           bf8, *reinterpret_cast<const uint4 *>(
-                   buf + swz8(wr * 64 + i * 16 + (lane & 15), kk * 4 + cl)));
+                   bx + swz8(wr * 64 + i * 16 + (lane & 15), kk * 4 + cl)));
   };
+  if constexpr (QR) {
+    // the queries' stages, once (in the layout of a stage's query half)
+    if (w < 4) {
+      for (int hh = 0; hh < nst; ++hh) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint8_t *bq = lds + 2 * XS_N * XS_R + hh * XS_Q * XS_R + 4 * (w + 4 * h) * 1024;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int32_t so = hh * XS_K * 2 + (u >> 1) * 16 * ldx2 + h * 128 * ldx2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rq, (__attribute__((address_space(3))) void *)(bq + u * 1024), 16, voff[u & 1],
+                so, 0, 0);
+          }
+        }
+      }
+    }
+  }
   copy_next();
   copy_next();
   __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this wave's copies of stage 0
@@ -714,7 +748,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   for (int64_t t0 = s0; t0 < s1; t0 += XS_N, ++tcur) {
     // the tile's first operands are read here rather than before the
     // previous epilogue, which then has the registers to itself
-    read_ops(lds + (g & 1) * XS_STAGE, 0, 0);
+    read_ops(g, 0, 0);
     // the accumulators start at zero, or in filter mode on L2 and L2^2 at
     // -|x|^2/2 of the lane's rows (the tile's norms reached LDS with its
     // first stage): acc is then dot - |x|^2/2, the quantity the filter's
@@ -741,8 +775,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
     // (the operand reads are spread over the MFMAs: as a block, the eight
     // waves' reads fill the LDS queue and hold up the MFMA issue)
     for (int st = 0; st < nst; ++st, ++g) {
-      const uint8_t *cur = lds + (g & 1) * XS_STAGE;
-      read_ops(cur, 1, 1);
+      read_ops(g, 1, 1);
       XS_MMA(0);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -760,7 +793,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       __builtin_amdgcn_sched_barrier(0);
       // stage g+1 (at a tile's last stage the next tile's first one, read
       // again at its start: unconditional, so the reads can interleave)
-      read_ops(lds + ((g + 1) & 1) * XS_STAGE, 0, 0);
+      read_ops(g + 1, 0, 0);
       // stage g+2 into cur; in filter mode on L2 the next tile's second
       // stage waits until after the epilogue: with a copy in flight the
       // epilogue's first LDS atomic waits for it (measured at config 5:
@@ -1059,26 +1092,59 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   }
 }
 
-template <int METRIC>
+// dynamic LDS of each mode: the stage buffers and the queries' state, then
+// the row norms (filter mode on L2, L2^2 and cosine) and the candidate
+// queue (filter mode on L2 and L2^2), or the argmin's slots
+template <int MODE, int METRIC>
+constexpr int xs_lds_bytes() {
+  if constexpr (MODE == MODE_TOP2) return XS_LDS_TOP2;
+  if constexpr (MODE == MODE_FILTER && (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2))
+    return XS_LDS_QUEUE;
+  if constexpr (xs_norms_in_lds<MODE, METRIC>()) return XS_LDS_XA;
+  return XS_LDS;
+}
+
+template <int MODE, int METRIC, bool QR>
+static void set_lds() {
+  VSK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(k_flat_screen<MODE, METRIC, QR>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              xs_lds_bytes<MODE, METRIC>()));
+}
+
+template <int METRIC, bool QR>
+static void set_lds_metric() {
+  set_lds<MODE_DENSE, METRIC, QR>();
+  set_lds<MODE_FILTER, METRIC, QR>();
+  if constexpr (METRIC == VSK_METRIC_L2SQ) set_lds<MODE_TOP2, METRIC, QR>();
+}
+
+template <int METRIC, bool QR>
 static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a,
                      const SplitPtrs &s, int mode) {
-  const size_t lds = XS_LDS;
   if constexpr (METRIC == VSK_METRIC_L2SQ) {
     if (mode == MODE_TOP2) {
-      k_flat_screen<MODE_TOP2, METRIC><<<grid, 512, XS_LDS_TOP2, ctx->stream>>>(a, s);
+      k_flat_screen<MODE_TOP2, METRIC, QR>
+          <<<grid, 512, xs_lds_bytes<MODE_TOP2, METRIC>(), ctx->stream>>>(a, s);
       return;
     }
   }
   if (mode == MODE_TOP2) fail(VSK_ERR_UNSUPPORTED, "the screen's argmin mode is L2^2 only");
   if (mode == MODE_DENSE)
-    k_flat_screen<MODE_DENSE, METRIC><<<grid, 512, lds, ctx->stream>>>(a, s);
+    k_flat_screen<MODE_DENSE, METRIC, QR>
+        <<<grid, 512, xs_lds_bytes<MODE_DENSE, METRIC>(), ctx->stream>>>(a, s);
   else
-    k_flat_screen<MODE_FILTER, METRIC><<<grid, 512,
-                                         (METRIC == VSK_METRIC_L2SQ || METRIC == VSK_METRIC_L2)
-                                             ? XS_LDS_QUEUE
-                                             : (xs_norms_in_lds<MODE_FILTER, METRIC>() ? XS_LDS_XA
-                                                                                        : lds),
-                                         ctx->stream>>>(a, s);
+    k_flat_screen<MODE_FILTER, METRIC, QR>
+        <<<grid, 512, xs_lds_bytes<MODE_FILTER, METRIC>(), ctx->stream>>>(a, s);
+}
+
+// planes of at most 128 dims (two stages a tile) keep the queries in LDS
+template <int METRIC>
+static void launch_s(vsk_ctx *ctx, unsigned grid, const FlatArgs &a, const SplitPtrs &s,
+                     int mode) {
+  if (s.kb <= 2 * XS_K)
+    launch_s<METRIC, true>(ctx, grid, a, s, mode);
+  else
+    launch_s<METRIC, false>(ctx, grid, a, s, mode);
 }
 
 void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
@@ -1091,40 +1157,16 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
     fail(VSK_ERR_INVALID_ARGUMENT, "screen planes need one pitch and a padded dimension");
   static bool lds_set = false;
   if (!lds_set) {
-    const int bytes = XS_LDS;
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_L2SQ>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2SQ>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_QUEUE));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_L2>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_L2>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_QUEUE));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_COSINE_NORMALIZED>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_COSINE_NORMALIZED>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_DOT>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_DENSE, VSK_METRIC_COSINE>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_COSINE>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_XA));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_FILTER, VSK_METRIC_DOT>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
-    VSK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void *>(k_flat_screen<MODE_TOP2, VSK_METRIC_L2SQ>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, XS_LDS_TOP2));
+    set_lds_metric<VSK_METRIC_L2SQ, false>();
+    set_lds_metric<VSK_METRIC_L2SQ, true>();
+    set_lds_metric<VSK_METRIC_L2, false>();
+    set_lds_metric<VSK_METRIC_L2, true>();
+    set_lds_metric<VSK_METRIC_COSINE_NORMALIZED, false>();
+    set_lds_metric<VSK_METRIC_COSINE_NORMALIZED, true>();
+    set_lds_metric<VSK_METRIC_DOT, false>();
+    set_lds_metric<VSK_METRIC_DOT, true>();
+    set_lds_metric<VSK_METRIC_COSINE, false>();
+    set_lds_metric<VSK_METRIC_COSINE, true>();
     lds_set = true;
   }
   const int64_t qt = ceil_div(a.nq, XS_Q);
