@@ -794,11 +794,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
       // stage g+1 (at a tile's last stage the next tile's first one, read
       // again at its start: unconditional, so the reads can interleave)
       read_ops(g + 1, 0, 0);
-      // stage g+2 into cur; in filter mode on L2 the next tile's second
-      // stage waits until after the epilogue: with a copy in flight the
-      // epilogue's first LDS atomic waits for it (measured at config 5:
-      // 6 % faster launches; slower for the other metrics)
-      if (!XS_SHIFT || st + 1 < nst) copy_next();
+      // stage g+2 into cur
+      copy_next();
       XS_MMA(1);
       __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // the copies first
 #pragma unroll
@@ -1057,7 +1054,6 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         }
       }
     }
-    if constexpr (XS_SHIFT) copy_next();  // (deferred from the tile's last stage)
   }
   // the copies issued past the slice end land before the workgroup's LDS is released
   __builtin_amdgcn_s_waitcnt(kWaitAll);
