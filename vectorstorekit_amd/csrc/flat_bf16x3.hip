@@ -1009,6 +1009,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
         if (m && l_ok[16 * j]) {
           // the few candidates of this lane: exact key test
           const uint64_t th = l_th[16 * j];
+          const int32_t lim = l_lim[16 * j];
+          const int64_t pb = l_pb[16 * j];
           // this query's 16 scores of the lane as named values behind an
           // empty asm: a select between two loads of one array would be
           // folded into one dynamically indexed load, which sends the array
@@ -1048,7 +1050,7 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
             const uint64_t key = vsk_key(dist, (uint32_t)row);
             if (key <= th) {
               const int pos = atomicAdd(&l_cnt[16 * j], 1);
-              if (pos < l_lim[16 * j]) a.cand[l_pb[16 * j] + pos] = key;
+              if (pos < lim) a.cand[pb + pos] = key;
             }
           }
         }
