@@ -222,8 +222,12 @@ __device__ void wave_sort_u64(uint64_t (&v)[R]) {
 // probe's centroids) take it.
 // W32: the candidates are a.cand32 (no previous list).  FAST: the short
 // cut below for k <= 64 (its registers would slow the radix search of the
-// other instances).
-template <int REG, bool W32, bool FAST = false>
+// other instances).  SEGB: a segmented list is read SEGB segments a wave
+// at a time, one key a lane from each, every load issued before the first
+// is used: with few queries a launch (a workgroup or two a CU) each pass
+// otherwise waits on the memory latency once per segment.  The loads' registers
+// cost occupancy, which launches of many queries need more.
+template <int REG, bool W32, bool FAST = false, int SEGB = 0>
 __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -280,6 +284,29 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
       return;
     }
     for (int64_t i = tid; i < np; i += SEL_THREADS) f(P[i]);
+    if constexpr (SEGB > 0) {
+      // keys past a segment's first 64 follow the batch
+      const uint64_t *cq = a.cand + q * a.cap;
+      for (int s0 = tid >> 6; s0 < a.nseg; s0 += SEGB * (SEL_THREADS / 64)) {
+        uint64_t v[SEGB];
+#pragma unroll
+        for (int u = 0; u < SEGB; ++u) {
+          const int s = s0 + u * (SEL_THREADS / 64);
+          const int32_t ns = s < a.nseg ? seg_cnt[s] : 0;
+          v[u] = lane < ns ? cq[(int64_t)s * a.seg_stride + lane] : VSK_KEY_NONE;
+        }
+#pragma unroll
+        for (int u = 0; u < SEGB; ++u)
+          if (v[u] != VSK_KEY_NONE) f(v[u]);
+#pragma unroll
+        for (int u = 0; u < SEGB; ++u) {
+          const int s = s0 + u * (SEL_THREADS / 64);
+          const int32_t ns = s < a.nseg ? seg_cnt[s] : 0;
+          for (int32_t j = lane + 64; j < ns; j += 64) f(cq[(int64_t)s * a.seg_stride + j]);
+        }
+      }
+      return;
+    }
     for (int s = tid >> 6; s < a.nseg; s += SEL_THREADS / 64) {
       const uint64_t *cs = a.cand + q * a.cap + (int64_t)s * a.seg_stride;
       const int32_t ns = seg_cnt[s];
@@ -1056,6 +1083,8 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
       k_select<32, false, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
     else
       k_select<32, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  } else if (a.seg_n && a.nq < 4 * (int64_t)ctx->cu_count) {
+    k_select<0, false, false, 8><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   } else {
     k_select<0, false><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   }
