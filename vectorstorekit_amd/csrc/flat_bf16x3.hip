@@ -1211,6 +1211,9 @@ void launch_flat_screen(vsk_ctx *ctx, FlatArgs a, const SplitPtrs &s, int mode,
   // reserved slots per (workgroup, query), all splits within cap
   a.sub = 0;
   if (mode == MODE_FILTER) {
+    // (the filter queue keeps a block's tile index in 23 bits)
+    if (a.rows_per_split >= (int64_t)1 << 31)
+      fail(VSK_ERR_INVALID_BUFFER_SIZE, "row split too long for the screen's filter");
     const int64_t sub = a.cap / splits < 256 ? a.cap / splits : 256;
     if (sub < 1) fail(VSK_ERR_INVALID_BUFFER_SIZE, "candidate capacity too small");
     a.sub = (int32_t)sub;
