@@ -458,6 +458,75 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
   int32_t nbuf = 0;  // wave-uniform count of staged candidates
   constexpr int32_t RB = 16;
   const int32_t nr = (int32_t)nrows;
+  // A lane whose 4 scores of a query tile may pass (their largest reaches
+  // the query's floor) queues them with their place (16-row block, tile,
+  // lane) and the query's floor and threshold row; the queue is tested, a
+  // block a lane, when full and at the end of the split, so the exact test
+  // leaves the multiply pipeline once per SQ_QC blocks instead of once per
+  // block that holds a candidate.
+  constexpr int SQ_QC = 64;
+  __shared__ i4 s_qv[4][SQ_QC];
+  __shared__ int32_t s_qm[4][SQ_QC];
+  __shared__ int2 s_qt[4][SQ_QC];
+  int32_t qn = 0;  // queued blocks (wave-uniform)
+  auto drain = [&]() {
+    if (nbuf > SQ_WBUF - 4 * SQ_QC) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
+    const bool has = lane < qn;
+    const i4 v = has ? s_qv[w][lane] : i4{0, 0, 0, 0};
+    const int32_t pw = has ? s_qm[w][lane] : 0;
+    const int2 st = has ? s_qt[w][lane] : int2{0x7FFFFFFF, 0};
+    const int jj = (pw >> 6) & 7, sl = pw & 63;
+    const int32_t q = (int32_t)(qw0 + 16 * jj + (sl & 15));
+    const int64_t rb = s0 + (int64_t)(pw >> 9) * RB + 4 * (sl >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = rb + r;
+      const bool p = has && row < s1 &&
+                     (v[r] > st.x || (v[r] == st.x && (uint32_t)row <= (uint32_t)st.y));
+      const uint64_t m = __builtin_amdgcn_ballot_w64(p);
+      if (!m) continue;
+      if (p) {
+        const int32_t pos = nbuf + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                                       (uint32_t)(m >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        s_key[w][pos] = vsk_key_i32(-v[r], (uint32_t)row);
+        s_q[w][pos] = q;
+      }
+      nbuf += __builtin_popcountll(m);
+    }
+    qn = 0;
+  };
+  // block blk (16 rows from s0 + 16 blk) of accumulator set ac
+  auto push = [&](const i4 (&ac)[1][QT], int32_t blk) {
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const i4 v = ac[0][j];
+      const int32_t m01 = v[0] > v[1] ? v[0] : v[1];
+      const int32_t m23 = v[2] > v[3] ? v[2] : v[3];
+      bool f = (m01 > m23 ? m01 : m23) >= smin[j];
+      uint64_t bal = __builtin_amdgcn_ballot_w64(f);
+      while (bal) {  // one pass unless the queue fills
+        if (qn == SQ_QC) drain();
+        const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        const int room = SQ_QC - qn;
+        if (f && (int)pos < room) {
+          const int e = qn + (int)pos;
+          s_qv[w][e] = v;
+          s_qm[w][e] = (blk << 9) | (j << 6) | lane;
+          s_qt[w][e] = int2{smin[j], (int32_t)(uint32_t)th[j]};
+        }
+        const int n = __builtin_popcountll(bal);
+        if (n <= room) {
+          qn += n;
+          break;
+        }
+        qn = SQ_QC;
+        f = f && (int)pos >= room;
+        bal = __builtin_amdgcn_ballot_w64(f);
+      }
+    }
+  };
   i4 acc[2][RT][QT];
   // the "previous block" of the first: scores that pass no floor
 #pragma unroll
@@ -485,9 +554,7 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
     __builtin_amdgcn_sched_barrier(0);                                          \
     SP_LOAD(ar[P], t + ((P) + NPF) * RB);                                       \
     __builtin_amdgcn_sched_barrier(0);                                          \
-    if (hit)                                                                    \
-      sq8_epilogue<RT, QT, false>(a, acc[Y], s0 + t + ((P) - 1) * RB, s1, lane, qw0, qok, \
-                                  smin, th, s_key[w], s_q[w], nbuf);           \
+    if (hit) push(acc[Y], (t + ((P) - 1) * RB) >> 4);                          \
   } while (0)
   static_assert(NPF == 4, "four blocks per step: the register sets are fixed per position");
   for (int32_t t = 0; t < nr; t += NPF * RB) {
@@ -500,8 +567,8 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
 #undef SP_LOAD
   // the last block (set 1: NPF is even)
   if (sq8_any_pass<QT>(acc[1], smin))
-    sq8_epilogue<RT, QT, false>(a, acc[1], s0 + ((nr + NPF * RB - 1) / (NPF * RB)) * NPF * RB - RB,
-                                s1, lane, qw0, qok, smin, th, s_key[w], s_q[w], nbuf);
+    push(acc[1], (((nr + NPF * RB - 1) / (NPF * RB)) * NPF * RB - RB) >> 4);
+  if (qn) drain();
   if (nbuf > 0) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
 }
 
