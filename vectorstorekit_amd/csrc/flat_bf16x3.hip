@@ -708,8 +708,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
   auto drain = [&]() {
     const int ln = lane_here();
     if (ln < qn) {
-      const int pw = q_pos[ln];
-      const int jj = (pw >> 6) & 7, sl = pw & 63;
+      const uint32_t pw = (uint32_t)q_pos[ln];
+      const int jj = (int)((pw >> 6) & 7u), sl = (int)(pw & 63u);
       const int lq = wq * 128 + 16 * jj + (sl & 15);
       const f4 *src = reinterpret_cast<const f4 *>(q_val + ln * 16);
       const f4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
@@ -925,7 +925,8 @@ void k_flat_screen(FlatArgs a, SplitPtrs s) {
               f4 *dst = reinterpret_cast<f4 *>(q_val + (qn + (int)pos) * 16);
 #pragma unroll
               for (int i = 0; i < 4; ++i) dst[i] = acc[i][j];
-              q_pos[qn + (int)pos] = (tcur << 9) | (j << 6) | ln;
+              q_pos[qn + (int)pos] =
+                  (int32_t)(((uint32_t)tcur << 9) | ((uint32_t)j << 6) | (uint32_t)ln);
             }
             const uint64_t took = __builtin_amdgcn_ballot_w64(mine);
             qn = __builtin_amdgcn_readfirstlane(qn + __builtin_popcountll(took));

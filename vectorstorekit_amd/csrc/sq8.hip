@@ -473,9 +473,9 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
     if (nbuf > SQ_WBUF - 4 * SQ_QC) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
     const bool has = lane < qn;
     const i4 v = has ? s_qv[w][lane] : i4{0, 0, 0, 0};
-    const int32_t pw = has ? s_qm[w][lane] : 0;
+    const uint32_t pw = has ? (uint32_t)s_qm[w][lane] : 0u;
     const int2 st = has ? s_qt[w][lane] : int2{0x7FFFFFFF, 0};
-    const int jj = (pw >> 6) & 7, sl = pw & 63;
+    const int jj = (int)((pw >> 6) & 7u), sl = (int)(pw & 63u);
     const int32_t q = (int32_t)(qw0 + 16 * jj + (sl & 15));
     const int64_t rb = s0 + (int64_t)(pw >> 9) * RB + 4 * (sl >> 4);
 #pragma unroll
@@ -590,7 +590,10 @@ static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
   // buffer offsets (row * ldx, or row * KS * 64 in the tiled copy; prefetch
   // up to 2 NPF blocks past the end) stay within int32
   const int64_t stride = b.T ? (int64_t)KS * 64 : a.ldx;
-  const int64_t max_rows = 0x7FFFFFFFll / stride - 2 * step;
+  // (and the filter queue's position word holds a 16-row block index of
+  // 23 bits)
+  const int64_t max_rows =
+      std::min<int64_t>(0x7FFFFFFFll / stride - 2 * step, (int64_t)1 << 26);
   if (b.rows_per_split > max_rows) b.rows_per_split = max_rows / step * step;
   splits = ceil_div(ceil_div(rows, b.rows_per_split), 8) * 8;
   const int64_t spx = splits / 8;
