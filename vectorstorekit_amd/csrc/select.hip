@@ -1153,11 +1153,9 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
   // Without topk_sync no chunk is checked from the host: an overflow only
   // counts into the context's call counter, which the call's final
   // synchronisation reads back (then the call runs again with checks).
+  // (armed before the first filtered chunk: a search that is one dense
+  // chunk has nothing to count, nor to read back)
   const bool defer = !ctx->topk_sync;
-  if (defer && !ctx->ovf_armed) {
-    fill_i32(ctx, ctx->ovf_dev, 1, 0);
-    ctx->ovf_armed = true;
-  }
 
   int64_t r0 = 0;
   bool first = true;
@@ -1176,6 +1174,10 @@ void progressive_topk(vsk_ctx *ctx, int64_t nq, int64_t n, int32_t k,
     }
     const bool dense = first;
     if (!dense) fill_i32(ctx, counts, nq, 0);
+    if (!dense && defer && !ctx->ovf_armed) {
+      fill_i32(ctx, ctx->ovf_dev, 1, 0);
+      ctx->ovf_armed = true;
+    }
     int32_t nseg = 0;
     int64_t seg_stride = 0;
     {
