@@ -221,7 +221,7 @@ __device__ void wave_sort_u64(uint64_t (&v)[R]) {
 // thousand keys (IVF candidate segments, a dense chunk as small as the IVF
 // probe's centroids) take it.
 // W32: the candidates are a.cand32 (no previous list).  FAST: the short
-// cut below for k <= 64 (its registers would slow the radix search of the
+// cut below for k <= 128 (its registers would slow the radix search of the
 // other instances).  SEGB: a segmented list is read SEGB segments a wave
 // at a time, one key a lane from each, every load issued before the first
 // is used: with few queries a launch (a workgroup or two a CU) each pass
@@ -317,18 +317,34 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
   __shared__ SelShared sh;
   __shared__ uint64_t sel[VSK_MAX_K];
   __shared__ int sel_count;
-  // Short cut for k <= 64 over a list in registers, sorted output: each
-  // wave's k-th smallest per-lane minimum has k keys at or below it, so the
-  // smallest of those over the waves, B, does too; the k smallest keys are
-  // among the keys at or below B (usually a few times k), which one wave
-  // sorts.  More than 512 of them, or fewer than k lanes holding keys in
-  // every wave, takes the radix search.
-  if (FAST && REG > 0 && inreg && a.sorted && k <= 64) {
-    uint64_t mn = VSK_KEY_NONE;
-    each_key([&](uint64_t key) { mn = key < mn ? key : mn; });
-    uint64_t v1[1] = {mn};
-    wave_sort_u64<1>(v1);
-    const uint64_t wk = __shfl(v1[0], k - 1);
+  // Short cut for k <= 128 over a list in registers: each wave's k-th
+  // smallest of its lanes' smallest keys (k <= 64) or of their two smallest
+  // keys (k <= 128) has k keys at or below it, so the smallest of those
+  // over the waves, B, does too; the k smallest keys are among the keys at
+  // or below B (a few times k), which are sorted: by one wave in registers
+  // (at most 512 of them), else by the block in LDS (at most 1,024).  More
+  // of them, or fewer than k values in every wave, takes the radix search.
+  // The output is sorted whether or not it was asked for.
+  if (FAST && REG > 0 && inreg && k <= 128) {
+    uint64_t wk;
+    if (k <= 64) {
+      uint64_t mn = VSK_KEY_NONE;
+      each_key([&](uint64_t key) { mn = key < mn ? key : mn; });
+      uint64_t v1[1] = {mn};
+      wave_sort_u64<1>(v1);
+      wk = __shfl(v1[0], k - 1);
+    } else {
+      uint64_t m1 = VSK_KEY_NONE, m2 = VSK_KEY_NONE;  // m1 <= m2
+      each_key([&](uint64_t key) {
+        const uint64_t lo = key < m1 ? key : m1, up = key < m1 ? m1 : key;
+        m2 = up < m2 ? up : m2;
+        m1 = lo;
+      });
+      uint64_t v2[2] = {m1, m2};
+      wave_sort_u64<2>(v2);  // element e at lane e / 2, register e % 2
+      const uint64_t c0 = __shfl(v2[0], (k - 1) >> 1), c1 = __shfl(v2[1], (k - 1) >> 1);
+      wk = ((k - 1) & 1) ? c1 : c0;
+    }
     if (lane == 0) sh.lo[tid >> 6] = wk;
     if (tid == 0) sel_count = 0;
     __syncthreads();
@@ -339,12 +355,19 @@ __global__ __launch_bounds__(SEL_THREADS) void k_select(SelectArgs a) {
       each_key([&](uint64_t key) {
         if (key <= B) {
           const int slot = atomicAdd(&sel_count, 1);
-          if (slot < 512) sel[slot] = key;
+          if (slot < VSK_MAX_K) sel[slot] = key;
         }
       });
     }
     __syncthreads();
     const int c = sel_count;
+    if (B != VSK_KEY_NONE && c > 512 && c <= VSK_MAX_K) {
+      block_sort(sel, c);
+      uint64_t *out = a.best_out + q * (int64_t)k;
+      for (int i = tid; i < k; i += SEL_THREADS) out[i] = sel[i];
+      if (tid == 0 && a.thresh) a.thresh[q] = sel[k - 1];
+      return;
+    }
     if (B != VSK_KEY_NONE && c <= 512) {
       if (tid < 64) {
         uint64_t *out = a.best_out + q * (int64_t)k;
@@ -1069,7 +1092,7 @@ void launch_select(vsk_ctx *ctx, const SelectArgs &a, const char *name) {
   }
   // keys per query: the previous list (k) and up to cap candidates
   const int64_t most = a.cap + (a.prev ? a.k : 0);
-  const bool fast = a.k <= 64 && a.sorted && !a.seg_n;
+  const bool fast = a.k <= 128 && !a.seg_n;
   if (a.cand32) {
     if (a.prev || a.seg_n) fail(VSK_ERR_INVALID_ARGUMENT, "32-bit lists take no previous list or segments");
     k_select<32, true><<<(unsigned)a.nq, SEL_THREADS, 0, ctx->stream>>>(a);
