@@ -833,7 +833,8 @@ __device__ inline float tail_exact(const float *x, const float *sq, int32_t ld, 
   return squared ? acc : sqrtf(acc);
 }
 
-__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p);
+__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p,
+                                   const int64_t *lpb, const int64_t *llr);
 
 // The exact keys of keys[0 .. c) in place, L lanes a key (L a power of two,
 // 32 L >= ld): lane s of a group loads columns [32 s, 32 s + 32) of the
@@ -841,7 +842,7 @@ __device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p
 // sum passes from lane to lane -- lane s adds its 32 products to what lane
 // s - 1 handed on -- which keeps the order of the one-thread sum.
 __device__ void tail_rescore(uint64_t *keys, int c, const ScreenTailArgs &t, int64_t q,
-                             const float *sq) {
+                             const float *sq, const int64_t *lpb, const int64_t *llr) {
 #pragma clang fp contract(off)
   const int L = t.ld <= 32 ? 1 : t.ld <= 64 ? 2 : t.ld <= 128 ? 4 : 8;
   const int tid = threadIdx.x, s = tid & (L - 1);
@@ -853,7 +854,7 @@ __device__ void tail_rescore(uint64_t *keys, int c, const ScreenTailArgs &t, int
     float4 xv[8];
     if (i < c) {
       p = (int64_t)(uint32_t)keys[i];
-      const float *x = t.rows + tail_row(t, q, p) * t.ld + c0;
+      const float *x = t.rows + tail_row(t, q, p, lpb, llr) * t.ld + c0;
 #pragma unroll
       for (int u = 0; u < 8; ++u)
         if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + 4 * u);
@@ -884,8 +885,20 @@ __device__ void tail_rescore(uint64_t *keys, int c, const ScreenTailArgs &t, int
   }
 }
 
-__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p) {
+// (lpb, llr: the query's probe bases and their lists' first rows, in LDS,
+// or null to read them from memory)
+__device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p,
+                                   const int64_t *lpb, const int64_t *llr) {
   if (!t.list_off) return p;
+  if (lpb) {
+    int lo = 0, hi = t.np;  // the last slot whose base is at or below p
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (lpb[mid] <= p) lo = mid;
+      else hi = mid;
+    }
+    return llr[lo] + (p - lpb[lo]);
+  }
   const int64_t *pb = t.pos_base + q * t.np;
   const int32_t *pr = t.probes + q * t.np;
   int lo = 0, hi = t.np;  // the last slot whose base is at or below p
@@ -910,6 +923,17 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   __shared__ uint64_t keys[VSK_MAX_K];
   __shared__ __attribute__((aligned(16))) float s_q[256];
   __shared__ int s_cnt;
+  // the query's probe bases and their lists' first rows (a candidate's
+  // row is found by a search over the bases: in LDS, not 7 dependent
+  // global loads)
+  __shared__ int64_t s_pb[256], s_lr[256];
+  const bool lcache = t.list_off && t.np <= 256;
+  if (lcache)
+    for (int i = tid; i < t.np; i += SEL_THREADS) {
+      s_pb[i] = t.pos_base[q * t.np + i];
+      s_lr[i] = t.list_off[t.probes[q * t.np + i]];
+    }
+  const int64_t *lpb = lcache ? s_pb : nullptr, *llr = lcache ? s_lr : nullptr;
   const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
   const uint32_t kth = word_kth_fast(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   uint32_t lim_word = kWordNone - 1u;  // every key when there are fewer than k
@@ -933,7 +957,7 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const int32_t k = a.k;
   uint64_t *out = t.best_out + q * (int64_t)k;
   if (c <= a.cap) {
-    tail_rescore(keys, c, t, q, s_q);
+    tail_rescore(keys, c, t, q, s_q, lpb, llr);
     __syncthreads();
     if (tid < 64) {
       for (int i = c + lane; i < k; i += 64) out[i] = VSK_KEY_NONE;
@@ -971,7 +995,8 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   for (int64_t i = tid; i < n; i += SEL_THREADS)
     A[i] = W[i] == kWordNone
                ? VSK_KEY_NONE
-               : vsk_key(tail_exact(t.rows + tail_row(t, q, i) * t.ld, s_q, t.ld, t.squared),
+               : vsk_key(tail_exact(t.rows + tail_row(t, q, i, lpb, llr) * t.ld, s_q, t.ld,
+                                    t.squared),
                          (uint32_t)i);
   __threadfence_block();
   __syncthreads();
