@@ -934,6 +934,8 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
       s_lr[i] = t.list_off[t.probes[q * t.np + i]];
     }
   const int64_t *lpb = lcache ? s_pb : nullptr, *llr = lcache ? s_lr : nullptr;
+  // the query too, read while the k-th word is found
+  for (int c = tid; c < t.ld; c += SEL_THREADS) s_q[c] = t.Q[q * t.ld + c];
   const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
   const uint32_t kth = word_kth_fast(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   uint32_t lim_word = kWordNone - 1u;  // every key when there are fewer than k
@@ -944,7 +946,6 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
     lim_word = vsk_f2ord(f_down(lim));
   }
   if (tid == 0) s_cnt = 0;
-  for (int c = tid; c < t.ld; c += SEL_THREADS) s_q[c] = t.Q[q * t.ld + c];
   __syncthreads();
   each([&](uint32_t x, uint32_t i) {
     if (x <= lim_word) {
