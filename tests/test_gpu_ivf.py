@@ -193,6 +193,59 @@ def test_ivf_screen_unclustered_bit_exact():
     sctx.close()
 
 
+def _screen_ctx_keep_all():
+    """A screen context whose list scan keeps every candidate's word
+    (VSK_IVF_COMPACT=0) instead of those under each query's bound."""
+    old = os.environ.get("VSK_IVF_COMPACT")
+    os.environ["VSK_IVF_COMPACT"] = "0"
+    try:
+        return _screen_ctx()
+    finally:
+        if old is None:
+            del os.environ["VSK_IVF_COMPACT"]
+        else:
+            os.environ["VSK_IVF_COMPACT"] = old
+
+
+@pytest.mark.parametrize("nprobe,k", [(6, 25), (2, 25), (12, 1), (8, 64)])
+def test_ivf_screen_compact_bound(nprobe, k):
+    """The screened list scan keeps only the candidates under each query's
+    bound: the smallest d + R (centroid distance plus list radius) at which
+    the probed lists hold k rows.  Lists of about 10 rows, so the bound
+    comes from several lists (k = 25), from none (nprobe 2: fewer candidates
+    than k, every one kept, results padded), k = 1 and k = 64; both
+    euclidean metrics, then rows added (the radii are made again with the
+    plane).  Bit-identical to the scan that keeps every candidate and to
+    the oracle."""
+    x, q, c = _mixture(31, 300, 3000, 32, 60)
+    ids = np.arange(len(x), dtype=np.int64) * 2 + 1
+    sctx, actx = _screen_ctx(), _screen_ctx_keep_all()
+    a, b = _index(sctx, c, x, ids, nprobe), _index(actx, c, x, ids, nprobe)
+    lists = O.ivf_assign(x, c)
+    for step in range(2):
+        for metric in ("euclidean", "euclideanSquared"):
+            print(f"ivf screen compact nprobe={nprobe} k={k} {metric} step={step}", flush=True)
+            gd, gi = a.search(q, k, metric=metric)
+            hd, hi = b.search(q, k, metric=metric)
+            np.testing.assert_array_equal(gi, hi)
+            np.testing.assert_array_equal(gd.view(np.uint32), hd.view(np.uint32))
+            od, oi = O.ivf_search(q, x, ids, lists, c, nprobe, k,
+                                  squared=metric != "euclidean")
+            np.testing.assert_array_equal(gi, oi)
+            np.testing.assert_array_equal(gd.view(np.uint32), od.view(np.uint32))
+        # rows next to the queries, added after the plane and radii were made
+        extra = (q[:20] + 0.05).astype(np.float32)
+        eids = np.arange(len(x), len(x) + len(extra), dtype=np.int64) * 2 + 1
+        a.insert(extra, eids)
+        b.insert(extra, eids)
+        x = np.concatenate([x, extra])
+        ids = np.concatenate([ids, eids])
+        lists = O.ivf_assign(x, c)
+    assert "ivf_list_screen" in sctx.profile_stats()
+    sctx.close()
+    actx.close()
+
+
 def test_ivf_build_one_call_matches_create_add(ctx):
     x, q, c = _mixture(11, 32, 6000, 40, 25)
     ids = np.arange(len(x), dtype=np.int64) * 5 + 1

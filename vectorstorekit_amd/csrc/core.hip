@@ -488,6 +488,8 @@ vsk_status vsk_create(int32_t device, vsk_ctx **out) {
   c->flat_no_screen = fk && (c->flat_fp32 || strcmp(fk, "bf16x3") == 0);
   c->flat_force_screen = fk && strcmp(fk, "screen") == 0;
   c->exact_only = fk && strcmp(fk, "exact") == 0;
+  const char *ic = getenv("VSK_IVF_COMPACT");
+  c->ivf_no_compact = ic && strcmp(ic, "0") == 0;
   if (const char *tb = getenv("VSK_MAX_TILE_BYTES")) {
     const long long v = atoll(tb);
     if (v > 0) c->max_tile_bytes = v;

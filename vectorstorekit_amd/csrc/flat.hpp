@@ -190,6 +190,16 @@ struct ScreenTailArgs {
   const int64_t *seg_off = nullptr;
   int64_t all_n = 0;
   uint64_t *best_out = nullptr;
+  // compact candidates (the IVF list scan under a per-query bound, list_off
+  // set, np <= 256): probe slot p's kept candidates are the first
+  // pcnt[q * np + p] words from its base, m.words[wseg[q] + pos_base], and
+  // at the same places of prow their rows' offsets in the list (the
+  // candidate's position is the base plus that offset); a slot whose list
+  // is empty has none.  Null: every candidate's word at its position.
+  const int32_t *pcnt = nullptr;
+  const uint32_t *prow = nullptr;
+  // only the queries with active[q] (all when null)
+  const uint8_t *active = nullptr;
 };
 void launch_screen_tail(vsk_ctx *ctx, const ScreenTailArgs &a, const char *name);
 

@@ -70,6 +70,9 @@ struct vsk_ivf {
   mutable vsk::DevBuf xplane, xsq;
   mutable int32_t xldb = 0;
   mutable double xh_max = 0, xr_max = 0;
+  // per list the largest fp32 distance of its rows from its centroid (the
+  // list scan's per-query bound), valid with the plane
+  mutable vsk::DevBuf xrad;
 };
 
 namespace vsk {
@@ -106,11 +109,31 @@ __global__ void k_keys_to_tie(const uint64_t *keys, int64_t total,
 // With keys, the probes are first taken from the probe's ranked keys
 // (NONE: -1) and written out.  With lcnt, the blocks also clear the nlist
 // per-list pair counters for the first batch's grouping.
+// With bound.qlim (and keys), each query's bound on the screened words the
+// list scan keeps.  The rows of a list whose centroid lies at exact
+// distance d from the query are within d + R of it (R: the list's radius,
+// the largest exact distance of its rows from the centroid), so the
+// smallest V for which the lists with d + R <= V hold k rows bounds the k-th
+// exact distance.  Each fp32 distance lies within 2^-16 of the real one
+// relatively, so V (1 + 2^-10) still bounds it, and a candidate whose
+// screened squared distance is above that squared (times 1 + 2^-10) plus
+// 2 eps -- eps the screen's bound -- is farther than k others: it cannot be
+// among the k nearest.  From the first 64 probes; none that hold k rows
+// (or a bound that is not finite): every candidate is kept.
+struct ProbeBound {
+  uint32_t *qlim = nullptr;
+  const float *rad = nullptr;   // per list R
+  int32_t k = 0;
+  const float *qnh = nullptr, *qnr = nullptr;  // the queries' plane norms
+  double xh = 0, xr = 0;
+  int32_t d = 0, metric = 0, nprod = 0;
+};
 __global__ __launch_bounds__(256) void k_probe_bases(int32_t *probes, const uint64_t *keys,
                                                      int64_t nq, int32_t np,
                                                      const int64_t *list_off,
                                                      int64_t *pos_base, int64_t *cnt,
-                                                     int32_t *lcnt, int32_t nlist) {
+                                                     int32_t *lcnt, int32_t nlist,
+                                                     ProbeBound bound = ProbeBound{}) {
   if (lcnt)
     for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < nlist;
          l += (int64_t)gridDim.x * blockDim.x)
@@ -141,6 +164,39 @@ __global__ __launch_bounds__(256) void k_probe_bases(int32_t *probes, const uint
     }
     if (p < np) pos_base[q * np + p] = carry + incl - sz;
     carry += __shfl(incl, 63);
+    if (bound.qlim && keys && p0 == 0) {
+      float v = __int_as_float(0x7f800000);  // this probe's d + R
+      if (p < np && sz > 0) {
+        const uint64_t key = keys[q * np + p];
+        const int32_t l = (int32_t)(uint32_t)key;
+        v = vsk_ord2f((uint32_t)(key >> 32)) + bound.rad[l];
+        if (!(v < __int_as_float(0x7f800000))) v = __int_as_float(0x7f800000);
+      }
+      // the rows of the probes whose d + R is at most this one's (each
+      // probe's value and size read out of its lane into scalars)
+      const int32_t sz32 = (int32_t)min<int64_t>(sz, 0x7FFFFFFF);
+      const int npl = np < 64 ? np : 64;
+      int64_t rows = 0;
+      for (int i = 0; i < npl; ++i) {
+        const float vi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+        const int32_t si = __builtin_amdgcn_readlane(sz32, i);
+        if (vi <= v) rows += si;
+      }
+      float V = rows >= bound.k ? v : __int_as_float(0x7f800000);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) V = fminf(V, __shfl_xor(V, o));
+      if (lane == 0) {
+        uint32_t lim = kWordNone - 1u;  // every candidate
+        if (V < __int_as_float(0x7f800000)) {
+          const double u = (double)V * (1.0 + 0x1p-10);
+          const double eps = screen_eps_of(bound.qnh[q], bound.qnr[q], bound.xh, bound.xr,
+                                           bound.d, bound.metric, bound.nprod);
+          const double w = u * u * (1.0 + 0x1p-10) + 2.0 * eps;
+          if (w < 0x1p127) lim = vsk_f2ord(f_down(w));
+        }
+        bound.qlim[q] = lim;
+      }
+    }
   }
   if (lane == 0) cnt[q] = carry;
 }
@@ -604,17 +660,31 @@ struct DenseScreen {
   int64_t nq, nrows, wstride;
   int32_t nchunks;
 };
+// CMP: only the candidates whose word is at most the query's bound qlim[q]
+// are kept, compactly: a pair's first pcnt[pair] words from the start of
+// its place in the query's word segment, with their rows' offsets in the
+// list at the same places of prow (the order is that of the workgroup's
+// atomics; the tail's keys carry the positions)
+struct ScreenKeep {
+  const uint32_t *qlim = nullptr;
+  int32_t *pcnt = nullptr;
+  uint32_t *prow = nullptr;
+};
 constexpr int kScreenQ = 128;  // queries per screen workgroup: 2 halves of 4 waves
-template <int KS, bool DENSE, int PL>
+template <int KS, bool DENSE, int PL, bool CMP = false>
 __global__ __launch_bounds__(512) void k_list_screen(
     const uint16_t *xplane, const float *xsq, int32_t ldb, const int64_t *list_off,
     const uint16_t *qplane, const uint16_t *qlo, const float *qsq, const int32_t *pairs,
     const int4 *groups,
     const int64_t *ngroups, int32_t np, const int64_t *pos_base, const int64_t *wseg,
-    uint32_t *out, DenseScreen ds) {
+    uint32_t *out, DenseScreen ds, ScreenKeep keep = ScreenKeep{}) {
+  static_assert(!(CMP && DENSE), "the probe's screen keeps every word");
   if (!DENSE && blockIdx.x >= *ngroups) return;
   __shared__ int64_t s_out[kScreenQ];  // value address of the list's first row (-1: none)
   __shared__ float s_qa[kScreenQ];     // |q|^2
+  // CMP: per slot, the query's bound, the pair and its kept count
+  __shared__ uint32_t s_lim[CMP ? kScreenQ : 1];
+  __shared__ int32_t s_pid[CMP ? kScreenQ : 1], s_n[CMP ? kScreenQ : 1];
   const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3, half = threadIdx.x >> 8;
   int64_t v0, v1, q0 = 0;
   int npair;
@@ -643,6 +713,11 @@ __global__ __launch_bounds__(512) void k_list_screen(
     } else {
       const int32_t pid = pairs[g.y + (j < npair ? j : 0)];
       s_out[j] = j < npair ? wseg[q] + pos_base[pid] : -1;
+      if constexpr (CMP) {
+        s_lim[j] = keep.qlim[q];
+        s_pid[j] = pid;
+        s_n[j] = 0;
+      }
     }
     s_qa[j] = qsq[q];
   }
@@ -682,8 +757,8 @@ __global__ __launch_bounds__(512) void k_list_screen(
     }
   }
   __syncthreads();
-  if (ntile == 0) return;  // (after the block's only barrier)
-  for (int64_t b = v0 + 16 * w; b < v1; b += 64) {
+  if (!CMP && ntile == 0) return;  // (after the block's only barrier)
+  for (int64_t b = v0 + 16 * w; ntile > 0 && b < v1; b += 64) {
     const int64_t row = b + (lane & 15);
     const bool live = row < v1;
     bf8v xf[KS];
@@ -713,9 +788,22 @@ __global__ __launch_bounds__(512) void k_list_screen(
       for (int r = 0; r < 4; ++r) {
         const int j = hbase + 16 * t + 4 * (lane >> 4) + r;
         const int64_t o = s_out[j];
-        if (live && o >= 0) out[o + i] = vsk_f2ord(fmaxf(s_qa[j] + xa - 2.0f * acc[r], 0.0f));
+        const uint32_t word = vsk_f2ord(fmaxf(s_qa[j] + xa - 2.0f * acc[r], 0.0f));
+        if constexpr (CMP) {
+          if (live && o >= 0 && word <= s_lim[j]) {
+            const int slot = atomicAdd(&s_n[j], 1);  // < the list's rows
+            out[o + slot] = word;
+            keep.prow[o + slot] = (uint32_t)i;
+          }
+        } else {
+          if (live && o >= 0) out[o + i] = word;
+        }
       }
     }
+  }
+  if constexpr (CMP) {
+    __syncthreads();
+    if (threadIdx.x < npair) keep.pcnt[s_pid[threadIdx.x]] = s_n[threadIdx.x];
   }
 }
 
@@ -1065,6 +1153,32 @@ static int64_t probe_bound(const vsk_ivf *ivf, int32_t np) {
 
 // the stored rows' bf16 plane (roundup(d, 64) columns), |x|^2 per row and
 // the maxima of |bf16(x)| and |x - bf16(x)|, rebuilt after the rows change
+// per list l, the largest sqrt of the sequential fp32 sum of (x - c_l)^2
+// over its rows (0 for an empty list): one workgroup a list
+__global__ __launch_bounds__(256) void k_list_radius(const float *rows, int32_t ld, int32_t d,
+                                                    const int64_t *list_off, const float *cent,
+                                                    int32_t cld, float *rad) {
+#pragma clang fp contract(off)
+  const int64_t l = blockIdx.x;
+  const float *c = cent + l * cld;
+  float m = 0.f;
+  for (int64_t r = list_off[l] + threadIdx.x; r < list_off[l + 1]; r += 256) {
+    const float *x = rows + r * ld;
+    float acc = 0.f;
+    for (int j = 0; j < d; ++j) {
+      const float t = x[j] - c[j];
+      acc = acc + t * t;
+    }
+    // (a NaN row leaves the bound unset: its list bounds nothing)
+    m = acc == acc ? fmaxf(m, sqrtf(acc)) : __int_as_float(0x7f800000);
+  }
+  __shared__ float s_m[4];
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) rad[l] = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+}
+
 static void list_screen_plane(vsk_ctx *ctx, const vsk_ivf *ivf) {
   if (ivf->xversion == ivf->version) return;
   const int32_t ldb = (ivf->d + 63) & ~63;
@@ -1077,6 +1191,14 @@ static void list_screen_plane(vsk_ctx *ctx, const vsk_ivf *ivf) {
              ivf->xplane.as<uint16_t>(), nullptr, ldb, nullptr, nullptr, mb);
   row_norms(ctx, ivf->rows.as<float>(), ivf->total, ivf->d, ivf->ld, ivf->xsq.as<float>(),
             nullptr);
+  ivf->xrad.reserve(sizeof(float) * (size_t)std::max<int32_t>(ivf->nlist, 1));
+  if (ivf->nlist > 0) {
+    KernelTimer t(ctx, "ivf_list_radius");
+    k_list_radius<<<(unsigned)ivf->nlist, 256, 0, ctx->stream>>>(
+        ivf->rows.as<float>(), ivf->ld, ivf->d, ivf->list_off.as<int64_t>(),
+        ivf->centroids.x.as<float>(), ivf->centroids.ld, ivf->xrad.as<float>());
+    check_launch("ivf_list_radius");
+  }
   uint32_t hb[2];
   VSK_HIP(hipMemcpyAsync(hb, mb, sizeof(hb), hipMemcpyDeviceToHost, ctx->stream));
   stream_sync(ctx);
@@ -1422,7 +1544,8 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
                               int32_t metric, const int32_t *probes, const int64_t *pos_base,
                               const int64_t *cnt, const int64_t *dseg, const int64_t *wseg,
                               const ListGroups &lg, uint32_t *words, uint64_t *cand,
-                              uint64_t *best, const uint32_t *lmask) {
+                              uint64_t *best, const uint32_t *lmask,
+                              const ScreenKeep *keep) {
   const int32_t ld = ivf->ld, ldb = ivf->xldb, nlist = ivf->nlist;
   const int64_t npairs = nb * np;
   const int32_t *bprobes = probes + b0 * np;
@@ -1432,11 +1555,21 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     t.device_work(dseg + nb);
     const unsigned gmax =
         (unsigned)(std::min<int64_t>(nlist, npairs) + ceil_div(npairs, kScreenQ));
-#define VSK_LS(KS, PL)                                                                      \
-  k_list_screen<KS, false, PL><<<gmax, 512, 0, ctx->stream>>>(                             \
+    // (compact: the batch's bounds, the pair counts and row offsets)
+    ScreenKeep kb;
+    if (keep) kb = ScreenKeep{keep->qlim + b0, keep->pcnt, keep->prow};
+#define VSK_LS1(KS, PL, CMP)                                                                \
+  k_list_screen<KS, false, PL, CMP><<<gmax, 512, 0, ctx->stream>>>(                        \
       ivf->xplane.as<uint16_t>(), ivf->xsq.as<float>(), ldb, ivf->list_off.as<int64_t>(),   \
       qp.qh + b0 * qp.ldb, qp.ql ? qp.ql + b0 * qp.ldb : nullptr, qp.qsq + b0, lg.pairs,    \
-      lg.groups, lg.gstart + nlist, np, bpos, wseg, words, DenseScreen{})
+      lg.groups, lg.gstart + nlist, np, bpos, wseg, words, DenseScreen{}, kb)
+#define VSK_LS(KS, PL)         \
+  do {                         \
+    if (keep)                  \
+      VSK_LS1(KS, PL, true);   \
+    else                       \
+      VSK_LS1(KS, PL, false);  \
+  } while (0)
     switch (ldb / 32) {
     case 2: if (qp.ql) VSK_LS(2, 2); else VSK_LS(2, 1); break;
     case 4: if (qp.ql) VSK_LS(4, 2); else VSK_LS(4, 1); break;
@@ -1444,6 +1577,7 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     default: VSK_LS(8, 1); break;
     }
 #undef VSK_LS
+#undef VSK_LS1
     check_launch("ivf_list_screen");
   }
   if (lmask) mask_words(ctx, bprobes, np, bpos, ivf, wseg, lmask, words, nb);
@@ -1484,6 +1618,10 @@ static void list_screen_batch(vsk_ctx *ctx, const vsk_ivf *ivf, const ArgminQuer
     ta.all = cand;
     ta.seg_off = dseg;
     ta.best_out = best + b0 * k;
+    if (keep) {
+      ta.pcnt = keep->pcnt;
+      ta.prow = keep->prow;
+    }
     KernelTimer t(ctx, "ivf_screen_tail");
     if (nbad) t.device_work(nbad);
     launch_screen_tail(ctx, ta, "screen_tail");
@@ -1842,10 +1980,29 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   int32_t *lcnt = kind != 2 ? static_cast<int32_t *>(
                                   ctx->scratch_ptr("ivf.lcnt", sizeof(int32_t) * ivf->nlist))
                             : nullptr;
+  // the screened list scan keeps only the candidates under each query's
+  // bound, from the probe's exact centroid distances (not with a row
+  // filter, whose excluded rows may be the ones that make the bound)
+  const bool compact =
+      screen && !lmask && pkeys && np <= 256 && k <= 256 && !ctx->ivf_no_compact;
+  ProbeBound pbd;
+  if (compact) {
+    pbd.qlim = static_cast<uint32_t *>(ctx->scratch_ptr("ivf.qlim", sizeof(uint32_t) * nq));
+    pbd.rad = ivf->xrad.as<float>();
+    pbd.k = k;
+    pbd.qnh = sqp.two.qnh;
+    pbd.qnr = sqp.two.qnr;
+    pbd.xh = ivf->xh_max;
+    pbd.xr = ivf->xr_max;
+    pbd.d = ivf->d;
+    pbd.metric = metric;
+    pbd.nprod = sqp.two.nprod;
+  }
   {
     KernelTimer t(ctx, "ivf_probe_bases");
     k_probe_bases<<<(unsigned)ceil_div(nq, 4), 256, 0, ctx->stream>>>(
-        probes, pkeys, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt, lcnt, ivf->nlist);
+        probes, pkeys, nq, np, ivf->list_off.as<int64_t>(), pos_base, cnt, lcnt, ivf->nlist,
+        pbd);
     check_launch("ivf_probe_bases");
   }
   const int64_t nbmax = qb, npmax = nbmax * np;
@@ -1879,6 +2036,14 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
   uint32_t *swords = screen ? static_cast<uint32_t *>(ctx->scratch_ptr(
                                   "ivf.words", sizeof(uint32_t) * (nbmax * (ubound + 3) + 4)))
                             : nullptr;
+  ScreenKeep keep;
+  if (compact) {
+    keep.qlim = pbd.qlim;
+    keep.pcnt = static_cast<int32_t *>(
+        ctx->scratch_ptr("ivf.pcnt", sizeof(int32_t) * (npmax + 1)));
+    keep.prow = static_cast<uint32_t *>(ctx->scratch_ptr(
+        "ivf.prow", sizeof(uint32_t) * (nbmax * (ubound + 3) + 4)));
+  }
 
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
@@ -1892,7 +2057,7 @@ static vsk_status ivf_search_any(vsk_ctx *ctx, const vsk_ivf *ivf, const float *
     }
     if (screen) {
       list_screen_batch(ctx, ivf, sqp.two, dq, b0, nb, np, k, metric, probes, pos_base, cnt,
-                        dseg, wseg, lgp, swords, cand, best, lmask);
+                        dseg, wseg, lgp, swords, cand, best, lmask, compact ? &keep : nullptr);
       continue;
     }
     const int64_t *ngroups = gstart + nlist;

@@ -650,6 +650,70 @@ struct WordList {
   }
 };
 
+// One query's compact candidates (ScreenTailArgs::pcnt): probe slot p's are
+// entries pre[p] .. pre[p + 1] - 1, stored from the slot's base pb[p] of the
+// query's word segment W, with their rows' offsets in the list at the same
+// places of R; an entry's position is pb[p] plus that offset.  pb and pre
+// (np + 1 values) sit in LDS.  REG entries a thread in registers when they
+// fit, else read from memory on each pass.
+template <int REG>
+struct CompactList {
+  const uint32_t *W, *R;
+  const int64_t *pb;
+  const int32_t *pre;
+  int np, n;
+  bool inreg;
+  uint32_t w[REG], pos[REG];
+  __device__ void at(int e, uint32_t &x, uint32_t &i) const {
+    int lo = 0, hi = np;  // the last slot whose first entry is at or below e
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pre[mid] <= e) lo = mid;
+      else hi = mid;
+    }
+    const int64_t o = pb[lo] + (e - pre[lo]);
+    x = W[o];
+    i = (uint32_t)(pb[lo] + R[o]);
+  }
+  __device__ void load(const uint32_t *W_, const uint32_t *R_, const int64_t *pb_,
+                       const int32_t *pre_, int np_) {
+    W = W_;
+    R = R_;
+    pb = pb_;
+    pre = pre_;
+    np = np_;
+    n = pre[np];
+    inreg = n <= REG * SEL_THREADS;  // uniform
+    if (!inreg) return;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < REG; ++j) {
+      const int e = tid + j * SEL_THREADS;
+      w[j] = kWordNone;
+      pos[j] = 0;
+      if (e < n) at(e, w[j], pos[j]);
+    }
+  }
+  // f(word, position) over this thread's share (kWordNone for padding)
+  template <class F>
+  __device__ void each(F &&f) const {
+    const int tid = threadIdx.x;
+    if (inreg) {
+#pragma unroll
+      for (int j = 0; j < REG; ++j) {
+        if (j * SEL_THREADS >= n) break;  // uniform
+        f(w[j], pos[j]);
+      }
+      return;
+    }
+    for (int e = tid; e < n; e += SEL_THREADS) {
+      uint32_t x, i;
+      at(e, x, i);
+      f(x, i);
+    }
+  }
+};
+
 // in-register bitonic sort of R 32-bit values a lane across the wave
 // (value e at lane e / R, register e % R), ascending
 template <int R>
@@ -910,14 +974,21 @@ __device__ inline int64_t tail_row(const ScreenTailArgs &t, int64_t q, int64_t p
   return t.list_off[pr[lo]] + (p - pb[lo]);
 }
 
-template <int REG>
+// CMP: compact candidates (t.pcnt), 8 a thread in registers
+template <int REG, bool CMP>
 __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const MarginArgs &a = t.m;
   const int64_t q = blockIdx.x;
+  if (t.active && !t.active[q]) return;
   const int tid = threadIdx.x, lane = tid & 63;
-  WordList<REG> L;
-  L.load(a.words + (a.wseg ? a.wseg[q] : q * a.wstride), a.cnt ? a.cnt[q] : a.wn);
-  auto each = [&](auto &&f) { L.each(f); };
+  const int64_t wbase = a.wseg ? a.wseg[q] : q * a.wstride;
+  WordList<CMP ? 1 : REG> L;
+  CompactList<CMP ? 8 : 1> C;
+  if constexpr (!CMP) L.load(a.words + wbase, a.cnt ? a.cnt[q] : a.wn);
+  auto each = [&](auto &&f) {
+    if constexpr (CMP) C.each(f);
+    else L.each(f);
+  };
   __shared__ KthShared sh;
   __shared__ SelShared ssel;
   __shared__ uint64_t keys[VSK_MAX_K];
@@ -936,6 +1007,41 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const int64_t *lpb = lcache ? s_pb : nullptr, *llr = lcache ? s_lr : nullptr;
   // the query too, read while the k-th word is found
   for (int c = tid; c < t.ld; c += SEL_THREADS) s_q[c] = t.Q[q * t.ld + c];
+  if constexpr (CMP) {
+    // the probe slots' first entries (an exclusive scan of their kept
+    // counts by wave 0, four slots a lane; np <= 256) and the total
+    __shared__ int32_t s_pre[257];
+    if (tid < 64) {
+      const int64_t *pb = t.pos_base + q * t.np;
+      int32_t v[4], sum = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = 4 * lane + u;
+        v[u] = 0;
+        if (p < t.np) {
+          const int64_t size = (p + 1 < t.np ? pb[p + 1] : a.cnt[q]) - pb[p];
+          v[u] = size > 0 ? t.pcnt[q * t.np + p] : 0;
+        }
+        sum += v[u];
+      }
+      int32_t incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      int32_t run = incl - sum;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = 4 * lane + u;
+        if (p < t.np) s_pre[p] = run;
+        run += v[u];
+      }
+      if (lane == 63) s_pre[t.np] = incl;
+    }
+    __syncthreads();
+    C.load(a.words + wbase, t.prow + wbase, s_pb, s_pre, t.np);
+  }
   const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
   const uint32_t kth = word_kth_fast(each, (uint32_t)a.k, sh, 0x1p-6 * eps);
   uint32_t lim_word = kWordNone - 1u;  // every key when there are fewer than k
@@ -991,10 +1097,11 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   const int64_t base = t.seg_off ? t.seg_off[q] : q * t.all_n;
   const int64_t n = t.seg_off ? t.seg_off[q + 1] - base : t.all_n;
   uint64_t *A = t.all + base;
-  // (a candidate the row filter excluded has the word kWordNone: no key)
-  const uint32_t *W = a.words + (a.wseg ? a.wseg[q] : q * a.wstride);
+  // (a candidate the row filter excluded has the word kWordNone: no key;
+  // compact candidates come from searches without a row filter)
+  const uint32_t *W = a.words + wbase;
   for (int64_t i = tid; i < n; i += SEL_THREADS)
-    A[i] = W[i] == kWordNone
+    A[i] = !CMP && W[i] == kWordNone
                ? VSK_KEY_NONE
                : vsk_key(tail_exact(t.rows + tail_row(t, q, i, lpb, llr) * t.ld, s_q, t.ld,
                                     t.squared),
@@ -1022,12 +1129,205 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   for (int i = tid; i < k; i += SEL_THREADS) out[i] = i < m ? keys[i] : VSK_KEY_NONE;
 }
 
+// The tail over compact candidates with a wave per query, for the common
+// case: np <= 64, k <= 64, at most 512 kept candidates, at most 128 of them
+// within the margin of the k-th (the k-th found from the per-lane minima
+// with at most 64 words at or below their k-th).  A query outside that is
+// marked in redo and left to k_screen_tail; every query's flag is written.
+// The same margin, exact sums and keys as k_screen_tail, so the results are
+// the same.  Four queries a workgroup, no block barrier.
+constexpr int kTailWaveR = 8;  // kept candidates a lane
+__global__ __launch_bounds__(256) void k_screen_tail_wave(ScreenTailArgs t, uint8_t *redo) {
+#pragma clang fp contract(off)
+  const MarginArgs &a = t.m;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t q = (int64_t)blockIdx.x * 4 + wv;
+  if (q >= a.nq) return;
+  __shared__ __attribute__((aligned(16))) float s_q[4][256];
+  __shared__ uint64_t s_g[4][128];
+  __shared__ uint8_t s_map[4][64 * kTailWaveR];
+  const int np = t.np;
+  const int64_t wbase = a.wseg[q];
+  // lane p: probe slot p's base, its list's first row and its kept count
+  int64_t pb = 0, lr = 0;
+  int32_t cp = 0;
+  if (lane < np) {
+    pb = t.pos_base[q * np + lane];
+    const int32_t l = t.probes[q * np + lane];
+    lr = l >= 0 ? t.list_off[l] : 0;
+  }
+  const int64_t pnext = __shfl_down(pb, 1);
+  if (lane < np) {
+    const int64_t size = (lane + 1 < np ? pnext : a.cnt[q]) - pb;
+    cp = size > 0 ? t.pcnt[q * np + lane] : 0;
+  }
+  int32_t incl = cp;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  const int32_t excl = incl - cp;
+  const int32_t n = __shfl(incl, 63);
+  if (n > 64 * kTailWaveR) {
+    if (lane == 0) redo[q] = 1;
+    return;
+  }
+  for (int c = lane; c < t.ld; c += 64) s_q[wv][c] = t.Q[q * t.ld + c];
+  // entry e's probe slot: slot p marks entries excl .. incl - 1
+  for (int p = 0; p < np; ++p) {
+    const int32_t b = __builtin_amdgcn_readlane(excl, p), c = __builtin_amdgcn_readlane(cp, p);
+    for (int i = lane; i < c; i += 64) s_map[wv][b + i] = (uint8_t)p;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t *W = a.words + wbase, *R = t.prow + wbase;
+  uint32_t w[kTailWaveR], ps[kTailWaveR];
+  int sl[kTailWaveR];
+#pragma unroll
+  for (int r = 0; r < kTailWaveR; ++r) {
+    const int e = lane + 64 * r;
+    const int p = e < n ? s_map[wv][e] : 0;
+    const int32_t pe = __shfl(excl, p);
+    const int64_t pbp = __shfl(pb, p);
+    w[r] = kWordNone;
+    ps[r] = 0;
+    sl[r] = p;
+    if (e < n) {
+      const int64_t o = pbp + (e - pe);
+      w[r] = W[o];
+      ps[r] = (uint32_t)(pbp + R[o]);
+    }
+  }
+  // the k-th smallest word: at least k words are at or below the k-th
+  // smallest per-lane minimum T, and it is among them
+  const int32_t k = a.k;
+  uint32_t kth = kWordNone;
+  {
+    uint32_t m = kWordNone;
+#pragma unroll
+    for (int r = 0; r < kTailWaveR; ++r) m = w[r] < m ? w[r] : m;
+    uint32_t v[1] = {m};
+    wave_sort_u32<1>(v);
+    const uint32_t T = __shfl(v[0], k - 1);
+    if (T != kWordNone) {
+      int32_t c = 0;
+#pragma unroll
+      for (int r = 0; r < kTailWaveR; ++r) {
+        const bool in = w[r] <= T;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+        const int32_t at = c + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                                   (uint32_t)(bal >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (in && at < 64) s_g[wv][at] = w[r];
+        c += __builtin_popcountll(bal);
+      }
+      if (c > 64) {
+        if (lane == 0) redo[q] = 1;
+        return;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      v[0] = lane < c ? (uint32_t)s_g[wv][lane] : kWordNone;
+      wave_sort_u32<1>(v);
+      kth = __shfl(v[0], k - 1);
+    }
+  }
+  uint32_t lim_word = kWordNone - 1u;  // every key when there are fewer than k
+  if (kth != kWordNone) {
+    const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
+    const double ak = vsk_ord2f(kth);
+    const double lim = a.metric == VSK_METRIC_L2 ? (ak + eps) * (1.0 + 0x1p-20) + eps
+                                                 : ak + 2.0 * eps;
+    lim_word = vsk_f2ord(f_down(lim));
+  }
+  // the margin: up to 128 keys (probe slot, position), one or two a lane
+  __builtin_amdgcn_wave_barrier();
+  int32_t c = 0;
+#pragma unroll
+  for (int r = 0; r < kTailWaveR; ++r) {
+    const bool in = w[r] <= lim_word;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+    const int32_t at = c + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                               (uint32_t)(bal >> 32),
+                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    if (in && at < 128) s_g[wv][at] = ((uint64_t)(uint32_t)sl[r] << 32) | ps[r];
+    c += __builtin_popcountll(bal);
+  }
+  if (c > 128) {
+    if (lane == 0) redo[q] = 1;
+    return;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  // key e (lane e, then lane e - 64): its exact distance
+  auto exact_key = [&](int e) -> uint64_t {
+    const uint64_t g = e < c ? s_g[wv][e] : 0;
+    const int gp = (int)(g >> 32);
+    const uint32_t pos = (uint32_t)g;
+    const int64_t gpb = __shfl(pb, gp), glr = __shfl(lr, gp);
+    if (e >= c) return VSK_KEY_NONE;
+    // the reference's sequential fp32 sum of (q - x)^2 over the row
+    const float *x = t.rows + (glr + ((int64_t)pos - gpb)) * t.ld;
+    const float *sq = s_q[wv];
+    float acc = 0.f;
+    for (int c0 = 0; c0 < t.ld; c0 += 64) {
+      const int m = t.ld - c0 < 64 ? (t.ld - c0) >> 2 : 16;  // ld: multiple of 4
+      float4 xv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + c0 + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) {
+          const float4 qv = *reinterpret_cast<const float4 *>(sq + c0 + 4 * u);
+          float d;
+          d = qv.x - xv[u].x;
+          acc = acc + d * d;
+          d = qv.y - xv[u].y;
+          acc = acc + d * d;
+          d = qv.z - xv[u].z;
+          acc = acc + d * d;
+          d = qv.w - xv[u].w;
+          acc = acc + d * d;
+        }
+    }
+    return vsk_key(t.squared ? acc : sqrtf(acc), pos);
+  };
+  uint64_t *out = t.best_out + q * (int64_t)k;
+  if (c <= 64) {
+    uint64_t key[1] = {exact_key(lane)};
+    wave_sort_u64<1>(key);
+    if (lane < k) out[lane] = key[0];
+  } else {
+    const uint64_t k0 = exact_key(lane), k1 = exact_key(lane + 64);
+    uint64_t key[2] = {k0, k1};  // (any order: sorted next)
+    wave_sort_u64<2>(key);       // element e at lane e / 2, register e % 2
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (2 * lane + r < k) out[2 * lane + r] = key[r];
+  }
+  if (lane == 0) redo[q] = 0;
+}
+
 void launch_screen_tail(vsk_ctx *ctx, const ScreenTailArgs &a, const char *name) {
   if (a.m.nq <= 0) return;
   if (a.m.k < 1 || a.m.k > VSK_MAX_K || a.m.cap > VSK_MAX_K || a.ld > 256)
     fail(VSK_ERR_INVALID_ARGUMENT, "screen tail: k, cap (<= 1024) or ld (<= 256) out of range");
+  if (a.pcnt && (!a.list_off || a.np > 256 || !a.prow || !a.m.wseg || !a.m.cnt))
+    fail(VSK_ERR_INVALID_ARGUMENT, "screen tail: compact candidates need list slots (np <= 256)");
   KernelTimer t(ctx, name);
-  k_screen_tail<32><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  if (a.pcnt && a.np <= 64 && a.m.k <= 64) {
+    // a wave per query, the block tail for the queries it leaves
+    uint8_t *redo = static_cast<uint8_t *>(ctx->scratch_ptr("tail.redo", a.m.nq + 64));
+    k_screen_tail_wave<<<(unsigned)ceil_div(a.m.nq, 4), 256, 0, ctx->stream>>>(a, redo);
+    ScreenTailArgs b = a;
+    b.active = redo;
+    k_screen_tail<32, true><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(b);
+  } else if (a.pcnt)
+    k_screen_tail<32, true><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(a);
+  else
+    k_screen_tail<32, false><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   check_launch(name);
 }
 

@@ -114,6 +114,10 @@ struct vsk_ctx {
   // on the exact VALU kernel for its screenable metrics, IVF's exact probe
   // and list scans, PQ's LUT scan over the codes, the exact argmin)
   bool exact_only = false;
+  // VSK_IVF_COMPACT=0: the screened IVF list scan keeps every candidate's
+  // word at its position instead of the candidates under each query's
+  // bound, compacted (the two give the same results)
+  bool ivf_no_compact = false;
   // VSK_FAULT: the kind of event to fail, at which occurrence, seen so far
   int fault_kind = 0;
   int64_t fault_at = 0, fault_seen = 0;
