@@ -70,7 +70,7 @@ struct vsk_ivf {
   mutable vsk::DevBuf xplane, xsq;
   mutable int32_t xldb = 0;
   mutable double xh_max = 0, xr_max = 0;
-  // per list the largest fp32 distance of its rows from its centroid (the
+  // per list the largest distance of its rows from its centroid (for the
   // list scan's per-query bound), valid with the plane
   mutable vsk::DevBuf xrad;
 };
@@ -110,12 +110,12 @@ __global__ void k_keys_to_tie(const uint64_t *keys, int64_t total,
 // (NONE: -1) and written out.  With lcnt, the blocks also clear the nlist
 // per-list pair counters for the first batch's grouping.
 // With bound.qlim (and keys), each query's bound on the screened words the
-// list scan keeps.  The rows of a list whose centroid lies at exact
-// distance d from the query are within d + R of it (R: the list's radius,
-// the largest exact distance of its rows from the centroid), so the
-// smallest V for which the lists with d + R <= V hold k rows bounds the k-th
-// exact distance.  Each fp32 distance lies within 2^-16 of the real one
-// relatively, so V (1 + 2^-10) still bounds it, and a candidate whose
+// list scan keeps.  The rows of a list whose centroid lies at distance d
+// from the query are within d + R of it (R: the list's radius, the largest
+// distance of its rows from the centroid), so the smallest V for which the
+// lists with d + R <= V hold k rows bounds the k-th distance.  d, R and the
+// exact distances are fp32 sums, each within 2^-16 of the real distance
+// relatively, so V (1 + 2^-10) bounds the k-th exact one, and a candidate whose
 // screened squared distance is above that squared (times 1 + 2^-10) plus
 // 2 eps -- eps the screen's bound -- is farther than k others: it cannot be
 // among the k nearest.  From the first 64 probes; none that hold k rows
@@ -1153,28 +1153,31 @@ static int64_t probe_bound(const vsk_ivf *ivf, int32_t np) {
 
 // the stored rows' bf16 plane (roundup(d, 64) columns), |x|^2 per row and
 // the maxima of |bf16(x)| and |x - bf16(x)|, rebuilt after the rows change
-// per list l, the largest sqrt of the sequential fp32 sum of (x - c_l)^2
-// over its rows (0 for an empty list): one workgroup a list
+// per list l, the largest fp32 distance of its rows from its centroid c_l
+// (0 for an empty list; infinite when a row gives NaN): one workgroup a
+// list, a wave a row at a time with the dimensions over its lanes.  The sum
+// is a tree, not the reference's sequential order: any order lies within
+// (d + 2) u of the real distance, which the bound's slack covers.
 __global__ __launch_bounds__(256) void k_list_radius(const float *rows, int32_t ld, int32_t d,
                                                     const int64_t *list_off, const float *cent,
                                                     int32_t cld, float *rad) {
-#pragma clang fp contract(off)
   const int64_t l = blockIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const float *c = cent + l * cld;
   float m = 0.f;
-  for (int64_t r = list_off[l] + threadIdx.x; r < list_off[l + 1]; r += 256) {
+  for (int64_t r = list_off[l] + wv; r < list_off[l + 1]; r += 4) {
     const float *x = rows + r * ld;
     float acc = 0.f;
-    for (int j = 0; j < d; ++j) {
+    for (int j = lane; j < d; j += 64) {
       const float t = x[j] - c[j];
-      acc = acc + t * t;
+      acc = __builtin_fmaf(t, t, acc);
     }
-    // (a NaN row leaves the bound unset: its list bounds nothing)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     m = acc == acc ? fmaxf(m, sqrtf(acc)) : __int_as_float(0x7f800000);
   }
   __shared__ float s_m[4];
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  if (lane == 0) s_m[wv] = m;
   __syncthreads();
   if (threadIdx.x == 0) rad[l] = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
 }
