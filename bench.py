@@ -786,10 +786,12 @@ def roofline(spec, stats, full=None):
         # (2 * roundup(d, 64) bytes a row): at this configuration's nq x
         # nprobe every list is probed, so the plane is read once whole per
         # launch (a list read by two 128-query groups counts once).  That
-        # is the algorithmic traffic.  The 32-bit screened distance it
-        # writes per (query, candidate) pair is an intermediate the tail
-        # reads back: reported beside it, not counted.  Its bf16 products
-        # are 2*d FLOP a pair.
+        # is the algorithmic traffic.  The 32-bit screened distances it
+        # writes (by default only the candidates under each query's bound,
+        # compacted; with VSK_IVF_COMPACT=0 one per (query, candidate)
+        # pair) are an intermediate the tail reads back: the every-pair
+        # figure is reported beside it as an upper bound, not counted.  Its
+        # bf16 products are 2*d FLOP a pair.
         ldb = (d + 63) // 64 * 64
         plane = 2.0 * ldb * spec["n"] * launches
         by = plane
@@ -798,11 +800,13 @@ def roofline(spec, stats, full=None):
                   "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4),
                   "algorithmic": "the bf16 plane of the probed lists read once per launch "
                                  "(2*roundup(d,64) bytes per row, every row at this nprobe)",
-                  "with_words": {"bytes_per_launch": (4.0 * pairs + plane) / launches,
-                                 "achieved_GBps": round((4.0 * pairs + plane) / sec / 1e9, 1),
-                                 "note": "plus the 4-byte screened word written per (query, "
-                                         "candidate) pair (an intermediate the tail reads "
-                                         "back)"},
+                  "with_every_word": {"bytes_per_launch": (4.0 * pairs + plane) / launches,
+                                      "achieved_GBps": round((4.0 * pairs + plane) / sec / 1e9,
+                                                             1),
+                                      "note": "plus a 4-byte screened word per (query, "
+                                              "candidate) pair, the most the scan writes (by "
+                                              "default it writes only the candidates under "
+                                              "each query's bound)"},
                   "bf16_mfma_TFLOPs": round(2.0 * d * pairs / sec / 1e12, 2)})
     elif kind == "kpp":
         # per pick every row's distance to the new centroid: 4*d bytes read
