@@ -1129,6 +1129,68 @@ __global__ __launch_bounds__(SEL_THREADS) void k_screen_tail(ScreenTailArgs t) {
   for (int i = tid; i < k; i += SEL_THREADS) out[i] = i < m ? keys[i] : VSK_KEY_NONE;
 }
 
+// The end of a wave's tail: the exact keys of the c <= 128 margin entries
+// g[0 .. c) (position in the low 32 bits; row_of maps an entry to its row,
+// called by every lane) -- the reference's sequential fp32 sum of (q - x)^2
+// over the row, its square root unless squared -- one or two a lane, and
+// the k smallest of them sorted into best_out[q]
+template <class RowOf>
+__device__ inline void wave_tail_finish(const ScreenTailArgs &t, int64_t q, const uint64_t *g,
+                                        int32_t c, int32_t k, const float *sq, RowOf row_of) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  auto exact_key = [&](int e) -> uint64_t {
+    const uint64_t ge = e < c ? g[e] : 0;
+    const int64_t row = row_of(ge);
+    if (e >= c) return VSK_KEY_NONE;
+    const float *x = t.rows + row * t.ld;
+    float acc = 0.f;
+    for (int c0 = 0; c0 < t.ld; c0 += 64) {
+      const int m = t.ld - c0 < 64 ? (t.ld - c0) >> 2 : 16;  // ld: multiple of 4
+      float4 xv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + c0 + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < m) {
+          const float4 qv = *reinterpret_cast<const float4 *>(sq + c0 + 4 * u);
+          float d;
+          d = qv.x - xv[u].x;
+          acc = acc + d * d;
+          d = qv.y - xv[u].y;
+          acc = acc + d * d;
+          d = qv.z - xv[u].z;
+          acc = acc + d * d;
+          d = qv.w - xv[u].w;
+          acc = acc + d * d;
+        }
+    }
+    return vsk_key(t.squared ? acc : sqrtf(acc), (uint32_t)ge);
+  };
+  uint64_t *out = t.best_out + q * (int64_t)k;
+  if (c <= 64) {
+    uint64_t key[1] = {exact_key(lane)};
+    wave_sort_u64<1>(key);
+    if (lane < k) out[lane] = key[0];
+  } else {
+    const uint64_t k0 = exact_key(lane), k1 = exact_key(lane + 64);
+    uint64_t key[2] = {k0, k1};  // (any order: sorted next)
+    wave_sort_u64<2>(key);       // element e at lane e / 2, register e % 2
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (2 * lane + r < k) out[2 * lane + r] = key[r];
+  }
+}
+
+// the margin limit of a k-th screened word (kWordNone: every word)
+__device__ inline uint32_t tail_limit(uint32_t kth, double eps, int32_t metric) {
+  if (kth == kWordNone) return kWordNone - 1u;
+  const double ak = vsk_ord2f(kth);
+  const double lim = metric == VSK_METRIC_L2 ? (ak + eps) * (1.0 + 0x1p-20) + eps : ak + 2.0 * eps;
+  return vsk_f2ord(f_down(lim));
+}
+
 // The tail over compact candidates with a wave per query, for the common
 // case: np <= 64, k <= 64, at most 512 kept candidates, at most 128 of them
 // within the margin of the k-th (the k-th found from the per-lane minima
@@ -1260,53 +1322,98 @@ __global__ __launch_bounds__(256) void k_screen_tail_wave(ScreenTailArgs t, uint
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  // key e (lane e, then lane e - 64): its exact distance
-  auto exact_key = [&](int e) -> uint64_t {
-    const uint64_t g = e < c ? s_g[wv][e] : 0;
+  wave_tail_finish(t, q, s_g[wv], c, k, s_q[wv], [&](uint64_t g) -> int64_t {
+    // (every lane takes part in the shuffles)
     const int gp = (int)(g >> 32);
-    const uint32_t pos = (uint32_t)g;
     const int64_t gpb = __shfl(pb, gp), glr = __shfl(lr, gp);
-    if (e >= c) return VSK_KEY_NONE;
-    // the reference's sequential fp32 sum of (q - x)^2 over the row
-    const float *x = t.rows + (glr + ((int64_t)pos - gpb)) * t.ld;
-    const float *sq = s_q[wv];
-    float acc = 0.f;
-    for (int c0 = 0; c0 < t.ld; c0 += 64) {
-      const int m = t.ld - c0 < 64 ? (t.ld - c0) >> 2 : 16;  // ld: multiple of 4
-      float4 xv[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (u < m) xv[u] = *reinterpret_cast<const float4 *>(x + c0 + 4 * u);
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (u < m) {
-          const float4 qv = *reinterpret_cast<const float4 *>(sq + c0 + 4 * u);
-          float d;
-          d = qv.x - xv[u].x;
-          acc = acc + d * d;
-          d = qv.y - xv[u].y;
-          acc = acc + d * d;
-          d = qv.z - xv[u].z;
-          acc = acc + d * d;
-          d = qv.w - xv[u].w;
-          acc = acc + d * d;
-        }
+    return glr + ((int64_t)(uint32_t)g - gpb);
+  });
+  if (lane == 0) redo[q] = 0;
+}
+
+// The tail of positional words without list slots (the probe's centroid
+// words) with a wave per query, for k <= 64 and at most 4,096 words: the
+// words are read in three passes (from cache after the first) rather than
+// held.  Pass 1 takes each lane's minimum; T, the k-th smallest of those,
+// has k words at or below it.  Pass 2 gathers every word within the margin
+// of T (at most 128, with its position): they include the k smallest, so
+// sorted they give the k-th word A_k, and those within the margin of A_k,
+// a prefix of them, get their exact keys.  A query with more is marked in
+// redo and left to k_screen_tail; every query's flag is written.
+__global__ __launch_bounds__(256) void k_screen_tail_dense(ScreenTailArgs t, uint8_t *redo) {
+  const MarginArgs &a = t.m;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t q = (int64_t)blockIdx.x * 4 + wv;
+  if (q >= a.nq) return;
+  __shared__ __attribute__((aligned(16))) float s_q[4][256];
+  __shared__ uint64_t s_g[4][128];
+  const uint32_t *W = a.words + q * a.wstride;
+  const int n = (int)a.wn;
+  for (int c = lane; c < t.ld; c += 64) s_q[wv][c] = t.Q[q * t.ld + c];
+  // word 256 j + 4 lane + e of a pass (rows padded to 4 words)
+  auto each = [&](auto &&f) {
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+      const int e0 = 256 * j + 4 * lane;
+      uint4 v = make_uint4(kWordNone, kWordNone, kWordNone, kWordNone);
+      if (e0 < n) v = *reinterpret_cast<const uint4 *>(W + e0);
+      f(e0 < n ? v.x : kWordNone, e0);
+      f(e0 + 1 < n ? v.y : kWordNone, e0 + 1);
+      f(e0 + 2 < n ? v.z : kWordNone, e0 + 2);
+      f(e0 + 3 < n ? v.w : kWordNone, e0 + 3);
     }
-    return vsk_key(t.squared ? acc : sqrtf(acc), pos);
   };
-  uint64_t *out = t.best_out + q * (int64_t)k;
-  if (c <= 64) {
-    uint64_t key[1] = {exact_key(lane)};
-    wave_sort_u64<1>(key);
-    if (lane < k) out[lane] = key[0];
-  } else {
-    const uint64_t k0 = exact_key(lane), k1 = exact_key(lane + 64);
-    uint64_t key[2] = {k0, k1};  // (any order: sorted next)
-    wave_sort_u64<2>(key);       // element e at lane e / 2, register e % 2
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-      if (2 * lane + r < k) out[2 * lane + r] = key[r];
+  uint32_t m = kWordNone;
+  each([&](uint32_t x, int) { m = x < m ? x : m; });
+  const int32_t k = a.k;
+  uint32_t v[1] = {m};
+  wave_sort_u32<1>(v);
+  const uint32_t T = __shfl(v[0], k - 1);
+  const double eps = screen_eps_of(a.qnh[q], a.qnr[q], a.xh, a.xr, a.d, a.metric, a.nprod);
+  const uint32_t limT = tail_limit(T, eps, a.metric);
+  int32_t c = 0;
+  each([&](uint32_t x, int e) {
+    const bool in = x <= limT;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+    const int32_t at = c + (int32_t)__builtin_amdgcn_mbcnt_hi(
+                               (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    if (in && at < 128) s_g[wv][at] = ((uint64_t)x << 32) | (uint32_t)e;
+    c += __builtin_popcountll(bal);
+  });
+  if (c > 128) {
+    if (lane == 0) redo[q] = 1;
+    return;
   }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  // sorted by (word, position): the k-th word, and the margin a prefix
+  uint32_t kth = kWordNone;
+  if (c <= 64) {
+    uint64_t r[1] = {lane < c ? s_g[wv][lane] : VSK_KEY_NONE};
+    wave_sort_u64<1>(r);
+    if (c >= k) kth = (uint32_t)(__shfl(r[0], k - 1) >> 32);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < c) s_g[wv][lane] = r[0];
+  } else {
+    uint64_t r[2] = {s_g[wv][lane], lane + 64 < c ? s_g[wv][lane + 64] : VSK_KEY_NONE};
+    wave_sort_u64<2>(r);  // element e at lane e / 2, register e % 2
+    const uint64_t kk = __shfl(r[(k - 1) & 1], (k - 1) >> 1);
+    kth = (uint32_t)(kk >> 32);
+    __builtin_amdgcn_wave_barrier();
+    if (2 * lane < c) s_g[wv][2 * lane] = r[0];
+    if (2 * lane + 1 < c) s_g[wv][2 * lane + 1] = r[1];
+  }
+  const uint32_t lim = tail_limit(kth, eps, a.metric);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  int32_t cm = 0;  // the margin: the sorted entries whose word is within it
+  for (int b = 0; b < c; b += 64) {
+    const bool in = b + lane < c && (uint32_t)(s_g[wv][b + lane] >> 32) <= lim;
+    cm += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
+  }
+  // (keys carry the position; the exact key replaces the word)
+  wave_tail_finish(t, q, s_g[wv], cm, k, s_q[wv],
+                   [&](uint64_t g) -> int64_t { return (int64_t)(uint32_t)g; });
   if (lane == 0) redo[q] = 0;
 }
 
@@ -1317,13 +1424,21 @@ void launch_screen_tail(vsk_ctx *ctx, const ScreenTailArgs &a, const char *name)
   if (a.pcnt && (!a.list_off || a.np > 256 || !a.prow || !a.m.wseg || !a.m.cnt))
     fail(VSK_ERR_INVALID_ARGUMENT, "screen tail: compact candidates need list slots (np <= 256)");
   KernelTimer t(ctx, name);
-  if (a.pcnt && a.np <= 64 && a.m.k <= 64) {
+  if (a.pcnt && a.np <= 64 && a.m.k <= 64 && !a.active) {
     // a wave per query, the block tail for the queries it leaves
     uint8_t *redo = static_cast<uint8_t *>(ctx->scratch_ptr("tail.redo", a.m.nq + 64));
     k_screen_tail_wave<<<(unsigned)ceil_div(a.m.nq, 4), 256, 0, ctx->stream>>>(a, redo);
     ScreenTailArgs b = a;
     b.active = redo;
     k_screen_tail<32, true><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(b);
+  } else if (!a.pcnt && !a.list_off && !a.m.wseg && !a.m.cnt && a.m.wn <= 4096 &&
+             a.m.wstride % 4 == 0 && a.m.k <= 64 && !a.active) {
+    // positional words (the probe's): the same, over three passes
+    uint8_t *redo = static_cast<uint8_t *>(ctx->scratch_ptr("tail.redo", a.m.nq + 64));
+    k_screen_tail_dense<<<(unsigned)ceil_div(a.m.nq, 4), 256, 0, ctx->stream>>>(a, redo);
+    ScreenTailArgs b = a;
+    b.active = redo;
+    k_screen_tail<32, false><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(b);
   } else if (a.pcnt)
     k_screen_tail<32, true><<<(unsigned)a.m.nq, SEL_THREADS, 0, ctx->stream>>>(a);
   else
