@@ -293,6 +293,52 @@ __global__ void k_list_pair_counts(const int32_t *probes, int64_t npairs, int32_
   }
 }
 
+// The same with the counting in LDS: workgroup b takes pairs [b per,
+// (b + 1) per), ranks them within its share of each list by LDS atomics,
+// takes its base in each list it touches with one device atomic, and adds
+// it.  Device atomics drop from one a pair to one a (workgroup, list).
+// Dynamic LDS: nlist counters.
+__global__ __launch_bounds__(1024) void k_list_pair_counts_lds(const int32_t *probes,
+                                                               int64_t npairs, int64_t per,
+                                                               int32_t *lcnt, int32_t *rank,
+                                                               int32_t nlist) {
+  extern __shared__ int32_t s_cnt[];
+  for (int l = threadIdx.x; l < nlist; l += blockDim.x) s_cnt[l] = 0;
+  __syncthreads();
+  const int64_t i0 = blockIdx.x * per, i1 = i0 + per < npairs ? i0 + per : npairs;
+  // eight pairs a thread at a time, their loads issued together
+  constexpr int U = 8;
+  for (int64_t b = i0 + threadIdx.x; b < i1; b += U * (int64_t)blockDim.x) {
+    int32_t l[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = b + u * (int64_t)blockDim.x;
+      l[u] = i < i1 ? probes[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (l[u] >= 0) rank[b + u * (int64_t)blockDim.x] = atomicAdd(&s_cnt[l[u]], 1);
+  }
+  __syncthreads();
+  for (int l = threadIdx.x; l < nlist; l += blockDim.x) {
+    const int32_t c = s_cnt[l];
+    if (c > 0) s_cnt[l] = atomicAdd(&lcnt[l], c);
+  }
+  __syncthreads();
+  for (int64_t b = i0 + threadIdx.x; b < i1; b += U * (int64_t)blockDim.x) {
+    int32_t l[U], r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = b + u * (int64_t)blockDim.x;
+      l[u] = i < i1 ? probes[i] : -1;
+      r[u] = l[u] >= 0 ? rank[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (l[u] >= 0) rank[b + u * (int64_t)blockDim.x] = r[u] + s_cnt[l[u]];
+  }
+}
+
 // per list: its first pair slot (lstart)
 // and its first group (gstart; ceil(pairs / G) groups for a list holding
 // rows, none for an empty one); totals at [nlist].  One block of 1024,
@@ -1503,8 +1549,15 @@ static void batch_groups(vsk_ctx *ctx, const vsk_ivf *ivf, const int32_t *probes
     // (lcnt starts cleared: by the probe bases for the first batch, by the
     // previous batch's scatter after it)
     KernelTimer t(ctx, "ivf_pair_counts");
-    k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt,
-                                                                lg.rank);
+    if ((int64_t)nlist * 4 <= 64 * 1024 && npairs >= 8192) {
+      // about 16 workgroups, each with at least 4,096 pairs
+      const int64_t per = std::max<int64_t>(4096, ceil_div(ceil_div(npairs, 16), 1024) * 1024);
+      k_list_pair_counts_lds<<<(unsigned)ceil_div(npairs, per), 1024, sizeof(int32_t) * nlist,
+                               ctx->stream>>>(probes, npairs, per, lg.lcnt, lg.rank, nlist);
+    } else {
+      k_list_pair_counts<<<grid1(npairs), 256, 0, ctx->stream>>>(probes, npairs, lg.lcnt,
+                                                                  lg.rank);
+    }
     check_launch("ivf_list_pair_counts");
   }
   {
