@@ -263,19 +263,44 @@ __device__ void seg_offsets(const int64_t *cnt, int64_t m, int64_t *seg, int64_t
   const int64_t run = (m + 1023) / 1024;
   const int64_t i0 = threadIdx.x * run, i1 = i0 + run < m ? i0 + run : m;
   int64_t v[2] = {0, 0};
-  for (int64_t i = i0; i < i1; ++i) {
-    const int64_t c = cnt[i];
-    v[0] += c;
-    v[1] += (c + 3) & ~3ll;
+  // runs of up to 16 are read into registers at once (a loop that waits
+  // for each load took most of the launch)
+  constexpr int RUN = 16;
+  int64_t cr[RUN];
+  if (run <= RUN) {
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) cr[u] = i0 + u < i1 ? cnt[i0 + u] : 0;
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      v[0] += cr[u];
+      v[1] += (cr[u] + 3) & ~3ll;
+    }
+  } else {
+    for (int64_t i = i0; i < i1; ++i) {
+      const int64_t c = cnt[i];
+      v[0] += c;
+      v[1] += (c + 3) & ~3ll;
+    }
   }
   int64_t o[2];
   block_scan_1024<2>(v, o, wsum, carry);
-  for (int64_t i = i0; i < i1; ++i) {
-    const int64_t c = cnt[i];
-    seg[i] = o[0];
-    if (wseg) wseg[i] = o[1];
-    o[0] += c;
-    o[1] += (c + 3) & ~3ll;
+  if (run <= RUN) {
+#pragma unroll
+    for (int u = 0; u < RUN; ++u)
+      if (i0 + u < i1) {
+        seg[i0 + u] = o[0];
+        if (wseg) wseg[i0 + u] = o[1];
+        o[0] += cr[u];
+        o[1] += (cr[u] + 3) & ~3ll;
+      }
+  } else {
+    for (int64_t i = i0; i < i1; ++i) {
+      const int64_t c = cnt[i];
+      seg[i] = o[0];
+      if (wseg) wseg[i] = o[1];
+      o[0] += c;
+      o[1] += (c + 3) & ~3ll;
+    }
   }
   if (threadIdx.x == 0) {
     seg[m] = carry[0];
@@ -357,22 +382,42 @@ __device__ void list_offsets(const int32_t *lcnt, const int64_t *list_off, int32
   const int64_t run = (nlist + 1023) / 1024;
   const int64_t l0 = threadIdx.x * run, l1 = l0 + run < nlist ? l0 + run : nlist;
   int64_t v[2] = {0, 0};
-  for (int64_t l = l0; l < l1; ++l) {
-    v[0] += lcnt[l];
-    v[1] += list_groups(lcnt, list_off, l, G);
-  }
-  int64_t o[2];
-  block_scan_1024<2>(v, o, wsum, carry);
-  for (int64_t l = l0; l < l1; ++l) {
-    // the list's groups: (list, first pair slot, pairs, 0), up to G pairs
-    const int32_t c = lcnt[l];
-    const int64_t ng = list_groups(lcnt, list_off, l, G);
+  // the list's groups: (list, first pair slot, pairs, 0), up to G pairs
+  auto emit = [&](int64_t l, int32_t c, int64_t ng, int64_t (&o)[2]) {
     for (int64_t j = 0; j < ng; ++j)
       groups[o[1] + j] = int4{(int)l, (int)(o[0] + j * G), (int)min<int64_t>(G, c - j * G), 0};
     lstart[l] = o[0];
     gstart[l] = o[1];
     o[0] += c;
     o[1] += ng;
+  };
+  // runs of up to 8 lists are read into registers at once
+  constexpr int RUN = 8;
+  int32_t cr[RUN];
+  int64_t gr[RUN];
+  int64_t o[2];
+  if (run <= RUN) {
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      cr[u] = l0 + u < l1 ? lcnt[l0 + u] : 0;
+      gr[u] = l0 + u < l1 ? list_groups(lcnt, list_off, l0 + u, G) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      v[0] += cr[u];
+      v[1] += gr[u];
+    }
+    block_scan_1024<2>(v, o, wsum, carry);
+#pragma unroll
+    for (int u = 0; u < RUN; ++u)
+      if (l0 + u < l1) emit(l0 + u, cr[u], gr[u], o);
+  } else {
+    for (int64_t l = l0; l < l1; ++l) {
+      v[0] += lcnt[l];
+      v[1] += list_groups(lcnt, list_off, l, G);
+    }
+    block_scan_1024<2>(v, o, wsum, carry);
+    for (int64_t l = l0; l < l1; ++l) emit(l, lcnt[l], list_groups(lcnt, list_off, l, G), o);
   }
   if (threadIdx.x == 0) {
     lstart[nlist] = carry[0];
