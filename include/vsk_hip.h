@@ -415,9 +415,10 @@ vsk_status vsk_sq8_decode(vsk_ctx *ctx, const int8_t *codes, int64_t n, int32_t 
 vsk_status vsk_scalar_quantize_u8(vsk_ctx *ctx, const float *x, int64_t n, int32_t d,
                                   int32_t bits, uint8_t *codes, float *scale, float *minv);
 /* Resident database of n x d int8 codes (QuantizedVectorStore, :68-81).
- * Codes of up to 512 bytes are also kept in a tiled copy for the scans
- * (16-row blocks in the matrix cores' operand order), which doubles the
- * device memory the database holds. */
+ * Codes of up to 512 bytes are held only in a tiled layout (16-row blocks
+ * in the matrix cores' operand order, rows padded to 64-byte k-steps),
+ * which every scan reads; wider codes stay row-major.  The upload holds
+ * both for the moment it converts. */
 vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
                           int32_t d, vsk_sq8 **out);
 vsk_status vsk_sq8_free(vsk_ctx *ctx, vsk_sq8 *db);

@@ -23,9 +23,11 @@
 struct vsk_sq8 {
   int64_t n = 0;
   int32_t d = 0, ldc = 0;  // ldc: row stride in bytes (multiple of 32)
+  // row-major codes: kept only when there is no tiled copy (rows over 512
+  // bytes); the tiled copy is then the one layout the scans read
   vsk::DevBuf codes;
-  // the same codes in 16-row blocks stored in MFMA operand order (see
-  // k_sq8_tile), for the filter scan; tks 64-byte k-steps a row, 0 if none
+  // the codes in 16-row blocks stored in MFMA operand order (see
+  // k_sq8_tile); tks 64-byte k-steps a row, 0 if none
   vsk::DevBuf tiles;
   int32_t tks = 0;
 };
@@ -586,6 +588,8 @@ static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
   Sq8Args b = a;
   // the tiled copy holds 16-row blocks of this instance's k-steps
   if ((a.r0 & 15) || a.tks != KS) b.T = nullptr;
+  if (!b.T && !b.X)
+    fail(VSK_ERR_INVALID_ARGUMENT, "SQ8 scan: a chunk the tiled codes do not cover");
   b.rows_per_split = ceil_div(ceil_div(rows, splits), step) * step;
   // buffer offsets (row * ldx, or row * KS * 64 in the tiled copy; prefetch
   // up to 2 NPF blocks past the end) stay within int32
@@ -616,6 +620,8 @@ static void launch_reg(vsk_ctx *ctx, const Sq8Args &a, bool dense) {
   Sq8Args b = a;
   // the tiled copy holds 16-row blocks of this instance's k-steps
   if ((a.r0 & 15) || a.tks != KS) b.T = nullptr;
+  if (!b.T && !b.X)
+    fail(VSK_ERR_INVALID_ARGUMENT, "SQ8 scan: a chunk the tiled codes do not cover");
   b.rows_per_split = ceil_div(ceil_div(rows, splits), 16 * RT) * (16 * RT);
   // buffer offsets (row * ldx, or row * KS * 64 in the tiled copy; prefetch
   // up to 4 blocks past the end) stay within int32
@@ -1050,6 +1056,10 @@ vsk_status vsk_sq8_upload(vsk_ctx *ctx, const int8_t *codes, int64_t n,
     check_launch("sq8_tile");
   }
   cs.finish();
+  // one layout in memory: every chunk a search scans starts on a 16-row
+  // boundary (the chunk sizes are multiples of 16), so the tiled copy
+  // serves every scan and the row-major codes go
+  if (db->tks) db->codes.release();
   *out = db.release();
   VSK_API_END(ctx);
 }
@@ -1085,7 +1095,7 @@ static vsk_status sq8_search_body(vsk_ctx *ctx, const vsk_sq8 *db,
   for (int64_t b0 = 0; b0 < nq; b0 += qb) {
     const int64_t nb = nq - b0 < qb ? nq - b0 : qb;
     Sq8Args base{};
-    base.X = db->codes.as<int8_t>();
+    base.X = db->codes.p ? db->codes.as<int8_t>() : nullptr;
     base.ldx = db->ldc;
     base.T = db->tks ? db->tiles.as<int8_t>() : nullptr;
     base.tks = db->tks;
@@ -1193,7 +1203,7 @@ static vsk_status sq8_search_noalloc_body(vsk_ctx *ctx, const vsk_sq8 *db,
       dq = qpad;
     }
     Sq8Args a0{};
-    a0.X = db->codes.as<int8_t>();
+    a0.X = db->codes.p ? db->codes.as<int8_t>() : nullptr;
     a0.ldx = db->ldc;
     a0.T = db->tks ? db->tiles.as<int8_t>() : nullptr;
     a0.tks = db->tks;
