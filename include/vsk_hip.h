@@ -160,7 +160,9 @@ vsk_status vsk_measure_peaks(vsk_ctx *ctx, vsk_peaks *out);
  * store's DistanceComputeBackend choice (Config/Core/StoreConfiguration.swift:
  * 145-166).  A context starts from the environment (VSK_FLAT_KERNEL,
  * VSK_MAX_TILE_BYTES); vsk_configure replaces those settings for later
- * calls on ctx. */
+ * calls on ctx.  VSK_IVF_COMPACT=0, read at creation only, makes the
+ * screened IVF list scan keep every candidate's word instead of those under
+ * each query's bound (same results; for comparison and tests). */
 #define VSK_KERNEL_AUTO 0   /* the bf16 screen where it is exact and pays, else exact scans */
 #define VSK_KERNEL_EXACT 1  /* no screen: the exact scans alone (flat, IVF, PQ LUT, argmin) */
 #define VSK_KERNEL_SCREEN 2 /* the screen at every size (where the metric allows it) */
