@@ -813,9 +813,16 @@ __global__ __launch_bounds__(512) void k_list_screen(
     s_qa[j] = qsq[q];
   }
   const int kc = 8 * (lane >> 4);  // this lane's 8 dims of a k-step
-  // this half's query tiles: slots 64 half + 16 t
-  const int hbase = 64 * half;
+  // ALLQ (the query planes in LDS, the list scan): each of the 8 waves
+  // takes every query tile of the group for its row blocks (a row block
+  // loaded once a workgroup, half as many a wave); otherwise each half's 4
+  // waves take its 64 queries, slots 64 half + 16 t
+  constexpr bool ALLQ = PL == 2 && !DENSE;
+  constexpr int TPW = ALLQ ? 8 : 4;  // query tiles a wave
+  const int hbase = ALLQ ? 0 : 64 * half;
   const int ntile = npair - hbase <= 0 ? 0 : (npair - hbase + 15) >> 4;
+  const int wrow = ALLQ ? (int)(threadIdx.x >> 6) : w;  // the wave's first row block
+  constexpr int RSTEP = ALLQ ? 128 : 64;
   // one plane: the half's query fragments in registers; two planes: both
   // planes of the group's queries in LDS (the registers of both would halve
   // the waves a SIMD holds), rows padded by 16 bytes so that the 16 lanes
@@ -849,7 +856,7 @@ __global__ __launch_bounds__(512) void k_list_screen(
   }
   __syncthreads();
   if (!CMP && ntile == 0) return;  // (after the block's only barrier)
-  for (int64_t b = v0 + 16 * w; ntile > 0 && b < v1; b += 64) {
+  for (int64_t b = v0 + 16 * wrow; ntile > 0 && b < v1; b += RSTEP) {
     const int64_t row = b + (lane & 15);
     const bool live = row < v1;
     bf8v xf[KS];
@@ -860,7 +867,7 @@ __global__ __launch_bounds__(512) void k_list_screen(
     const float xa = live ? xsq[row] : 0.f;
     const int64_t i = row - v0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TPW; ++t) {
       if (t >= ntile) break;  // uniform
       f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
