@@ -207,16 +207,18 @@ def _screen_ctx_keep_all():
             os.environ["VSK_IVF_COMPACT"] = old
 
 
-@pytest.mark.parametrize("nprobe,k", [(6, 25), (2, 25), (12, 1), (8, 64)])
+@pytest.mark.parametrize("nprobe,k", [(6, 25), (2, 25), (12, 1), (8, 64), (100, 10),
+                                     (20, 100)])
 def test_ivf_screen_compact_bound(nprobe, k):
     """The screened list scan keeps only the candidates under each query's
     bound: the smallest d + R (centroid distance plus list radius) at which
     the probed lists hold k rows.  Lists of about 10 rows, so the bound
     comes from several lists (k = 25), from none (nprobe 2: fewer candidates
-    than k, every one kept, results padded), k = 1 and k = 64; both
-    euclidean metrics, then rows added (the radii are made again with the
-    plane).  Bit-identical to the scan that keeps every candidate and to
-    the oracle."""
+    than k, every one kept, results padded), k = 1 and k = 64 (the tail a
+    wave per query), nprobe 100 and k = 100 (the tail a workgroup per
+    query over the compact candidates); both euclidean metrics, then rows
+    added (the radii are made again with the plane).  Bit-identical to the
+    scan that keeps every candidate and to the oracle."""
     x, q, c = _mixture(31, 300, 3000, 32, 60)
     ids = np.arange(len(x), dtype=np.int64) * 2 + 1
     sctx, actx = _screen_ctx(), _screen_ctx_keep_all()
