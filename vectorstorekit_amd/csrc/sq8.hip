@@ -397,8 +397,9 @@ __global__ __launch_bounds__(256) void k_sq8_tile(const int8_t *X, int64_t n, in
   }
 }
 
-template <int KS, int QT, int NPF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WPE: waves a SIMD holds (the register budget per wave)
+template <int KS, int QT, int NPF, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
   constexpr int RT = 1;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -574,7 +575,7 @@ void k_sq8_pipe(Sq8Args a, int32_t groups, int32_t splits_per_xcd) {
   if (nbuf > 0) sq8_flush(a, s_key[w], s_q[w], nbuf, lane);
 }
 
-template <int KS, int QT, int NPF>
+template <int KS, int QT, int NPF, int WPE = 2>
 static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
   const int64_t rows = a.r1 - a.r0;
   const int64_t qpg = 4 * QT * 16;  // queries per workgroup
@@ -603,7 +604,7 @@ static void launch_pipe(vsk_ctx *ctx, const Sq8Args &a) {
   const int64_t spx = splits / 8;
   const int64_t nblocks = 8 * spx * groups;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
-  k_sq8_pipe<KS, QT, NPF><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
+  k_sq8_pipe<KS, QT, NPF, WPE><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
                                                                       (int32_t)spx);
 }
 
@@ -662,7 +663,10 @@ static void launch_sq8(vsk_ctx *ctx, Sq8Args a, bool dense) {
     if (ksteps <= 1)
       launch_pipe<1, 8, 4>(ctx, a);
     else if (ksteps <= 2)
-      launch_pipe<2, 8, 4>(ctx, a);
+      // 64 queries a wave and three waves a SIMD: 4 % faster than 128 and
+      // two at config 4 (the test's VALU work overlaps more MFMAs); 32
+      // queries a wave read each row block too often
+      launch_pipe<2, 4, 4, 3>(ctx, a);
     else if (ksteps <= 4)
       launch_pipe<4, 4, 4>(ctx, a);
     else
