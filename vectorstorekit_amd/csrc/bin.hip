@@ -224,8 +224,9 @@ __device__ __forceinline__ void bm_flush(const BinMArgs &a, const uint64_t *lkey
   nbuf = 0;
 }
 
-template <int RT, int KS, int QT, bool DENSE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WPE: waves a SIMD holds (the register budget per wave)
+template <int RT, int KS, int QT, bool DENSE, int WPE = 2>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void k_bin_mfma(BinMArgs a, int32_t groups, int32_t splits_per_xcd) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
@@ -372,7 +373,7 @@ void k_bin_mfma(BinMArgs a, int32_t groups, int32_t splits_per_xcd) {
 #undef BM_LOAD
 }
 
-template <int RT, int KS, int QT>
+template <int RT, int KS, int QT, int WPE = 2>
 static void launch_bm(vsk_ctx *ctx, const BinMArgs &a, bool dense) {
   const int64_t rows = a.r1 - a.r0;
   const int64_t qpg = 4 * QT * 16;  // queries per workgroup
@@ -392,10 +393,10 @@ static void launch_bm(vsk_ctx *ctx, const BinMArgs &a, bool dense) {
   const int64_t nblocks = 8 * spx * groups;
   if (nblocks > 0x7FFFFFFF) fail(VSK_ERR_INVALID_BUFFER_SIZE, "grid too large");
   if (dense)
-    k_bin_mfma<RT, KS, QT, true><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
+    k_bin_mfma<RT, KS, QT, true, WPE><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
                                                                             (int32_t)spx);
   else
-    k_bin_mfma<RT, KS, QT, false><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
+    k_bin_mfma<RT, KS, QT, false, WPE><<<(unsigned)nblocks, 256, 0, ctx->stream>>>(b, (int32_t)groups,
                                                                              (int32_t)spx);
 }
 
@@ -405,7 +406,9 @@ static void launch_bin_mfma(vsk_ctx *ctx, const BinMArgs &a, bool dense) {
   static const char *names[2] = {"bin_mfma_filter", "bin_mfma_dense"};
   KernelTimer t(ctx, names[dense ? 1 : 0], (double)a.nq * (double)rows);
   switch (a.words) {
-  case 4: launch_bm<2, 2, 8>(ctx, a, dense); break;
+  // 128-bit codes: 64 queries a wave and three waves a SIMD (9 % faster
+  // than 128 and two at 10M rows, 1,000 queries)
+  case 4: launch_bm<2, 2, 4, 3>(ctx, a, dense); break;
   case 8: launch_bm<2, 4, 4>(ctx, a, dense); break;
   case 16: launch_bm<1, 8, 2>(ctx, a, dense); break;
   case 32: launch_bm<1, 16, 1>(ctx, a, dense); break;
