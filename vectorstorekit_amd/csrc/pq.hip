@@ -748,18 +748,30 @@ __global__ __launch_bounds__(256) void k_pq_rescore_keys(
     const uint64_t ek = vsk_key(s, row);
     key = ek <= th ? ek : VSK_KEY_NONE;
   };
+  // four keys a lane at a time: their loads (key, then code row) in
+  // flight together rather than one key's chain after another's
+  auto rescore4 = [&](uint64_t *p, int64_t i, int64_t n, int64_t step) {
+    uint64_t k4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) k4[u] = i + u * step < n ? p[i + u * step] : VSK_KEY_NONE;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rescore(k4[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * step < n) p[i + u * step] = k4[u];
+  };
   uint64_t *base = cand + q * cap;
   if (seg_n) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int sgi = w; sgi < nseg; sgi += 4) {
       const int32_t ns = seg_n[q * nseg + sgi];
       uint64_t *cs = base + (int64_t)sgi * seg_stride;
-      for (int32_t i = lane; i < ns; i += 64) rescore(cs[i]);
+      for (int32_t i = lane; i < ns; i += 256) rescore4(cs, i, ns, 64);
     }
   } else {
     int64_t cnt = counts[q];
     if (cnt > cap) return;  // overflowed: the chunk is re-scanned whole
-    for (int64_t i = threadIdx.x; i < cnt; i += 256) rescore(base[i]);
+    for (int64_t i = threadIdx.x; i < cnt; i += 1024) rescore4(base, i, cnt, 256);
   }
 }
 
